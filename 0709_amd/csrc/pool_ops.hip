@@ -1,0 +1,244 @@
+// Page-pool bookkeeping kernels: reachability prune with an ascending
+// free-list compaction, page ownership marking, paged-metadata compression of
+// slot paths, and the decode / extend slot assignment of the paged allocator.
+#include "common.hpp"
+
+namespace atlas {
+namespace {
+
+constexpr int kSweepThreads = 1024;
+
+__global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t value) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x)
+    p[i] = value;
+}
+
+__global__ void mark_pages_kernel(uint32_t* bitmap, int64_t num_pages, const int64_t* slots, int64_t n,
+                                  int64_t page_size) {
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += int64_t(gridDim.x) * blockDim.x) {
+    const int64_t s = slots[i];
+    if (s < 0) continue;
+    const int64_t page = s / page_size;
+    if (page >= num_pages) continue;
+    atomicOr(&bitmap[page >> 5], 1u << (page & 31));
+  }
+}
+
+// One workgroup: free = owned & ~live in ascending page order, owned &= live.
+// Each thread owns a contiguous run of words; a block-wide exclusive scan of
+// the per-thread counts gives every thread its output offset.
+__global__ __launch_bounds__(kSweepThreads) void sweep_kernel(uint32_t* owned, const uint32_t* live,
+                                                              int64_t num_words,
+                                                              int64_t* free_pages,
+                                                              int64_t* free_count) {
+  __shared__ int64_t scan[kSweepThreads];
+  const int tid = threadIdx.x;
+  const int64_t per = (num_words + kSweepThreads - 1) / kSweepThreads;
+  const int64_t w0 = min(num_words, int64_t(tid) * per);
+  const int64_t w1 = min(num_words, w0 + per);
+  int64_t cnt = 0;
+  for (int64_t w = w0; w < w1; ++w) cnt += __popc(owned[w] & ~live[w]);
+  scan[tid] = cnt;
+  __syncthreads();
+  for (int off = 1; off < kSweepThreads; off <<= 1) {
+    const int64_t add = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  int64_t pos = scan[tid] - cnt;
+  for (int64_t w = w0; w < w1; ++w) {
+    const uint32_t ow = owned[w];
+    const uint32_t lv = live[w];
+    uint32_t rel = ow & ~lv;
+    while (rel) {
+      const int b = __ffs(rel) - 1;
+      free_pages[pos++] = w * 32 + b;
+      rel &= rel - 1;
+    }
+    owned[w] = ow & lv;
+  }
+  if (tid == kSweepThreads - 1) *free_count = scan[tid];
+}
+
+// Page tables from concatenated slot paths.  Thread per page: the page id is
+// the slot of the page's first token divided by page_size; the layout check
+// requires that first slot to be page-aligned and every later slot of the page
+// (within the path length) to follow it contiguously.
+__global__ void paged_metadata_kernel(const int64_t* slots, const int64_t* path_offsets,
+                                      const int64_t* page_offsets, int num_paths, int64_t total_pages,
+                                      int64_t page_size, int validate, int32_t* page_indices,
+                                      int32_t* layout_ok) {
+  for (int64_t pg = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; pg < total_pages;
+       pg += int64_t(gridDim.x) * blockDim.x) {
+    // Binary search for the path owning this page.
+    int lo = 0, hi = num_paths - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (page_offsets[mid] <= pg) lo = mid; else hi = mid - 1;
+    }
+    const int64_t local = pg - page_offsets[lo];
+    const int64_t begin = path_offsets[lo] + local * page_size;
+    const int64_t end = min(path_offsets[lo + 1], begin + page_size);
+    const int64_t first = slots[begin];
+    page_indices[pg] = static_cast<int32_t>(first >= 0 ? first / page_size : -((-first + page_size - 1) / page_size));
+    if (validate) {
+      bool ok = (((first % page_size) + page_size) % page_size) == 0;
+      for (int64_t i = begin + 1; ok && i < end; ++i) ok = slots[i] == first + (i - begin);
+      if (!ok) *layout_ok = 0;
+    }
+  }
+}
+
+// Decode slots: request i continues its tail page when (seq_len - 1) is not a
+// page boundary, else takes the next page of the free list (in request order).
+__global__ __launch_bounds__(1024) void alloc_decode_kernel(const int64_t* seq_lens, const int64_t* last_loc,
+                                                            const int64_t* free_pages, int64_t page_size,
+                                                            int bs, int64_t* out) {
+  __shared__ int scan[1024];
+  const int tid = threadIdx.x;
+  int base = 0;
+  for (int c0 = 0; c0 < bs; c0 += 1024) {
+    const int i = c0 + tid;
+    const int need = (i < bs && ((seq_lens[i] - 1) % page_size) == 0) ? 1 : 0;
+    scan[tid] = need;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int add = tid >= off ? scan[tid - off] : 0;
+      __syncthreads();
+      scan[tid] += add;
+      __syncthreads();
+    }
+    if (i < bs) out[i] = need ? free_pages[base + scan[tid] - 1] * page_size : last_loc[i] + 1;
+    base += scan[1023];
+    __syncthreads();
+  }
+}
+
+// Extend slots: request i appends seq_lens[i] - prefix_lens[i] tokens; it first
+// fills the free tail of its current page (continuing last_loc), then takes
+// new pages from the free list in request order.  Output tokens are packed in
+// request order.  Offsets come from block-wide scans of the per-request token
+// and new-page counts, so the host uploads nothing.
+__global__ __launch_bounds__(1024) void alloc_extend_kernel(const int64_t* prefix_lens, const int64_t* seq_lens,
+                                                            const int64_t* last_loc, const int64_t* free_pages,
+                                                            int64_t page_size, int bs, int64_t* out) {
+  __shared__ int64_t scan_tok[1024];
+  __shared__ int64_t scan_pg[1024];
+  const int tid = threadIdx.x;
+  int64_t tok_base = 0, pg_base = 0;
+  for (int c0 = 0; c0 < bs; c0 += 1024) {
+    const int i = c0 + tid;
+    int64_t ntok = 0, npg = 0, pre = 0, seq = 0;
+    if (i < bs) {
+      pre = prefix_lens[i];
+      seq = seq_lens[i];
+      ntok = seq - pre;
+      npg = (seq + page_size - 1) / page_size - (pre + page_size - 1) / page_size;
+    }
+    scan_tok[tid] = ntok;
+    scan_pg[tid] = npg;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int64_t at = tid >= off ? scan_tok[tid - off] : 0;
+      const int64_t ap = tid >= off ? scan_pg[tid - off] : 0;
+      __syncthreads();
+      scan_tok[tid] += at;
+      scan_pg[tid] += ap;
+      __syncthreads();
+    }
+    if (i < bs) {
+      int64_t o = tok_base + scan_tok[tid] - ntok;
+      int64_t pg = pg_base + scan_pg[tid] - npg;
+      int64_t cur = last_loc[i];
+      for (int64_t t = pre; t < seq; ++t) {
+        const int64_t slot = (t % page_size == 0) ? free_pages[pg++] * page_size : cur + 1;
+        out[o++] = slot;
+        cur = slot;
+      }
+    }
+    tok_base += scan_tok[1023];
+    pg_base += scan_pg[1023];
+    __syncthreads();
+  }
+}
+
+}  // namespace
+}  // namespace atlas
+
+using namespace atlas;
+
+extern "C" int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev,
+                                int64_t n, int64_t page_size, void* stream) {
+  ATLAS_REQUIRE(bitmap_dev && num_pages > 0 && page_size > 0, "bad bitmap / page arguments");
+  if (n <= 0) return ATLAS_OK;
+  ATLAS_REQUIRE(slots_dev, "slots must not be NULL");
+  const int blocks = static_cast<int>(std::min<int64_t>((n + 255) / 256, 1024));
+  hipLaunchKernelGGL(mark_pages_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     bitmap_dev, num_pages, slots_dev, n, page_size);
+  return launch_status("mark_pages_kernel");
+}
+
+extern "C" int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                                 const int64_t* live_slots_dev, int64_t n_live_slots, int64_t page_size,
+                                 int64_t* free_pages_dev, int64_t* free_count_dev, void* stream) {
+  ATLAS_REQUIRE(owned_bitmap_dev && live_bitmap_dev && free_pages_dev && free_count_dev,
+                "prune buffers must not be NULL");
+  ATLAS_REQUIRE(num_pages > 0 && page_size > 0, "num_pages and page_size must be positive");
+  ATLAS_REQUIRE(n_live_slots == 0 || live_slots_dev, "live slots must not be NULL");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t words = (num_pages + 31) / 32;
+  const int fill_blocks = static_cast<int>(std::min<int64_t>((words + 255) / 256, 1024));
+  hipLaunchKernelGGL(fill_u32_kernel, dim3(fill_blocks), dim3(256), 0, s, live_bitmap_dev, words, 0u);
+  int rc = launch_status("fill_u32_kernel");
+  if (rc) return rc;
+  if (n_live_slots > 0) {
+    const int blocks = static_cast<int>(std::min<int64_t>((n_live_slots + 255) / 256, 1024));
+    hipLaunchKernelGGL(mark_pages_kernel, dim3(blocks), dim3(256), 0, s, live_bitmap_dev, num_pages,
+                       live_slots_dev, n_live_slots, page_size);
+    if ((rc = launch_status("mark_pages_kernel"))) return rc;
+  }
+  hipLaunchKernelGGL(sweep_kernel, dim3(1), dim3(kSweepThreads), 0, s, owned_bitmap_dev, live_bitmap_dev,
+                     words, free_pages_dev, free_count_dev);
+  return launch_status("sweep_kernel");
+}
+
+extern "C" int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_dev,
+                                    const int64_t* page_offsets_dev, int num_paths, int64_t total_pages,
+                                    int64_t page_size, int validate, int32_t* kv_page_indices_dev,
+                                    int32_t* layout_ok_dev, void* stream) {
+  ATLAS_REQUIRE(num_paths > 0 && page_size > 0, "num_paths and page_size must be positive");
+  ATLAS_REQUIRE(slots_dev && path_offsets_dev && page_offsets_dev && kv_page_indices_dev,
+                "metadata buffers must not be NULL");
+  ATLAS_REQUIRE(!validate || layout_ok_dev, "validation needs a layout flag");
+  if (total_pages <= 0) return ATLAS_OK;
+  const int blocks = static_cast<int>(std::min<int64_t>((total_pages + 255) / 256, 2048));
+  hipLaunchKernelGGL(paged_metadata_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream),
+                     slots_dev, path_offsets_dev, page_offsets_dev, num_paths, total_pages, page_size,
+                     validate, kv_page_indices_dev, layout_ok_dev);
+  return launch_status("paged_metadata_kernel");
+}
+
+extern "C" int atlas_alloc_decode_slots(const int64_t* seq_lens_dev, const int64_t* last_loc_dev,
+                                        const int64_t* free_pages_dev, int64_t page_size, int bs,
+                                        int64_t* out_dev, void* stream) {
+  ATLAS_REQUIRE(bs >= 0 && page_size > 0, "bad batch / page size");
+  if (bs == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(seq_lens_dev && last_loc_dev && free_pages_dev && out_dev, "NULL buffer");
+  hipLaunchKernelGGL(alloc_decode_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream), seq_lens_dev,
+                     last_loc_dev, free_pages_dev, page_size, bs, out_dev);
+  return launch_status("alloc_decode_kernel");
+}
+
+extern "C" int atlas_alloc_extend_slots(const int64_t* prefix_lens_dev, const int64_t* seq_lens_dev,
+                                        const int64_t* last_loc_dev, const int64_t* free_pages_dev,
+                                        int64_t page_size, int bs, int64_t* out_dev, void* stream) {
+  ATLAS_REQUIRE(bs >= 0 && page_size > 0, "bad batch / page size");
+  if (bs == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(prefix_lens_dev && seq_lens_dev && last_loc_dev && free_pages_dev && out_dev, "NULL buffer");
+  hipLaunchKernelGGL(alloc_extend_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
+                     prefix_lens_dev, seq_lens_dev, last_loc_dev, free_pages_dev, page_size, bs, out_dev);
+  return launch_status("alloc_extend_kernel");
+}

@@ -1,0 +1,366 @@
+"""Target-side tree construction and paged-KV helpers (drop-in for the
+reference module ``atlas_0709.flashinfer_full_verify``).
+
+Same names, keyword-only arguments, return types and exceptions as the
+reference's tree / paged-KV functions.  Differences are in where the work runs:
+
+* the ancestor mask is derived once on the host as one 64-bit bitmask per tree
+  node (``TreeSpec.tree_mask``); the dense bool mask the reference builds with
+  a Python double loop of single-element device writes
+  (``flashinfer_full_verify.py:719-723``) is expanded from it with a handful
+  of tensor ops, and the attention kernel consumes the bitmask directly;
+* ``write_suffix_kv`` and ``prefix_layer_to_paged_kv`` write through the gfx950
+  append kernel instead of ``index_put``.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+from . import kv_ops
+from .tree_attention import BatchPrefillWithPagedKVCacheWrapper
+
+
+@dataclass(frozen=True)
+class TreeSpec:
+    """Reference ``TreeSpec`` (``flashinfer_full_verify.py:136-149``) plus the
+    compact ancestor bitmask: ``tree_mask[i]`` has bit ``j`` set iff tree node
+    ``j`` is an ancestor-or-self of node ``i``; tree node ``j`` sits at key
+    position ``mask_col_start + j``."""
+
+    flat_token_ids: torch.Tensor
+    parent_indices: list[int]
+    depths: torch.Tensor
+    packed_mask: torch.Tensor
+    bool_mask: torch.Tensor
+    qo_indptr: torch.Tensor
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    kv_last_page_len: torch.Tensor
+    total_pages: int
+    node_count: int
+    kv_len: int
+    tree_mask: torch.Tensor | None = None
+    mask_col_start: int = 0
+
+
+@dataclass
+class FullVerifyState:
+    tree: TreeSpec
+    paged_prefix_kv: list[torch.Tensor]
+
+
+def ceil_div(value: int, divisor: int) -> int:
+    return (int(value) + int(divisor) - 1) // int(divisor)
+
+
+def last_page_len(length: int, page_size: int) -> int:
+    rem = int(length) % int(page_size)
+    return int(page_size) if rem == 0 else rem
+
+
+def packbits(mask: torch.Tensor, bitorder: str = "big") -> torch.Tensor:
+    """numpy.packbits semantics (FlashInfer's ``packbits`` default, big bit
+    order) on the tensor's device."""
+    if bitorder not in ("big", "little"):
+        raise ValueError("bitorder must be 'big' or 'little'")
+    flat = mask.reshape(-1).to(torch.uint8)
+    pad = (-int(flat.numel())) % 8
+    if pad:
+        flat = torch.cat((flat, torch.zeros(pad, dtype=torch.uint8, device=flat.device)))
+    shifts = torch.arange(8, dtype=torch.uint8, device=flat.device)
+    if bitorder == "big":
+        shifts = 7 - shifts
+    return (flat.view(-1, 8) << shifts).sum(dim=1, dtype=torch.int32).to(torch.uint8)
+
+
+def _validate_paths(paths: Sequence[Sequence[int]]) -> int:
+    if not paths:
+        raise ValueError("paths must not be empty")
+    path_lengths = {len(path) for path in paths}
+    if len(path_lengths) != 1:
+        raise ValueError(f"all paths must have the same length, got {sorted(path_lengths)}")
+    depth = next(iter(path_lengths))
+    if depth <= 0:
+        raise ValueError("paths must contain at least one token")
+    return depth
+
+
+def build_path_tree_tokens_from_paths(
+    paths: Sequence[Sequence[int]],
+    *,
+    device: torch.device | str,
+) -> tuple[torch.Tensor, list[int], torch.Tensor]:
+    """One node per path position, no sharing
+    (``flashinfer_full_verify.py:541-567``)."""
+    _validate_paths(paths)
+    token_ids: list[int] = []
+    parent_indices: list[int] = []
+    depths: list[int] = []
+    for path in paths:
+        parent = -1
+        for depth_idx, token_id in enumerate(path):
+            token_ids.append(int(token_id))
+            parent_indices.append(parent)
+            depths.append(depth_idx)
+            parent = len(token_ids) - 1
+    return (
+        torch.tensor(token_ids, dtype=torch.long, device=device),
+        parent_indices,
+        torch.tensor(depths, dtype=torch.long, device=device),
+    )
+
+
+def build_deduplicated_path_tree_tokens(
+    paths: Sequence[Sequence[int]],
+    *,
+    device: torch.device | str,
+) -> tuple[torch.Tensor, list[int], torch.Tensor, list[list[int]]]:
+    """Prefix trie over the routes: one node per unique token prefix, numbered
+    in insertion order (route by route, depth by depth), and the route -> node
+    paths (``flashinfer_full_verify.py:570-616``)."""
+    _validate_paths(paths)
+    token_ids: list[int] = []
+    parent_indices: list[int] = []
+    depths: list[int] = []
+    # children[(parent_node, token)] -> node; parent -1 is the root.
+    children: dict[tuple[int, int], int] = {}
+    route_nodes: list[list[int]] = []
+    for path in paths:
+        parent = -1
+        nodes: list[int] = []
+        for depth_idx, raw in enumerate(path):
+            token = int(raw)
+            node = children.get((parent, token))
+            if node is None:
+                node = len(token_ids)
+                children[(parent, token)] = node
+                token_ids.append(token)
+                parent_indices.append(parent)
+                depths.append(depth_idx)
+            nodes.append(node)
+            parent = node
+        route_nodes.append(nodes)
+    return (
+        torch.tensor(token_ids, dtype=torch.long, device=device),
+        parent_indices,
+        torch.tensor(depths, dtype=torch.long, device=device),
+        route_nodes,
+    )
+
+
+def ancestors_inclusive(node_idx: int, parent_indices: Sequence[int]) -> list[int]:
+    out: list[int] = []
+    cur = int(node_idx)
+    while cur >= 0:
+        out.append(cur)
+        cur = int(parent_indices[cur])
+    return out
+
+
+def ancestor_bitmasks(parent_indices: Sequence[int]) -> list[int]:
+    """bits[i] = OR of 1 << a over the ancestors-or-self a of node i.  Parents
+    precede children in the trie numbering, so one forward pass suffices."""
+    bits: list[int] = []
+    for i, parent in enumerate(parent_indices):
+        parent = int(parent)
+        if parent >= i:
+            # Arbitrary parent order: walk the chain.
+            value = 0
+            for a in ancestors_inclusive(i, parent_indices):
+                value |= 1 << a
+            bits.append(value)
+        else:
+            bits.append((bits[parent] if parent >= 0 else 0) | (1 << i))
+    return bits
+
+
+def _signed64(value: int) -> int:
+    value &= (1 << 64) - 1
+    return value - (1 << 64) if value >= 1 << 63 else value
+
+
+def _tree_spec(
+    *,
+    flat_token_ids: torch.Tensor,
+    parent_indices: list[int],
+    depths: torch.Tensor,
+    prefix_len: int,
+    page_size: int,
+    device: torch.device | str,
+) -> TreeSpec:
+    node_count = int(flat_token_ids.numel())
+    kv_len = int(prefix_len) + node_count
+    total_pages = ceil_div(kv_len, page_size)
+    bits = ancestor_bitmasks(parent_indices)
+    device = torch.device(device)
+    # Dense mask [node, prefix + node]: prefix columns all visible, tree column
+    # j visible iff bit j of the row's ancestor bitmask.
+    mask = torch.zeros((node_count, kv_len), dtype=torch.bool, device=device)
+    mask[:, : int(prefix_len)] = True
+    tree_mask = None
+    if node_count <= 64:
+        tree_mask = torch.tensor([_signed64(b) for b in bits], dtype=torch.int64, device=device)
+        shifts = torch.arange(node_count, dtype=torch.int64, device=device)
+        mask[:, int(prefix_len) :] = ((tree_mask[:, None] >> shifts[None, :]) & 1).to(torch.bool)
+    else:
+        rows = [[(b >> j) & 1 for j in range(node_count)] for b in bits]
+        mask[:, int(prefix_len) :] = torch.tensor(rows, dtype=torch.bool, device=device)
+    flat_mask = mask.flatten()
+    if tree_mask is not None:
+        # Lets the attention plan skip re-deriving the bitmask from the mask.
+        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask)
+    return TreeSpec(
+        flat_token_ids=flat_token_ids,
+        parent_indices=list(parent_indices),
+        depths=depths,
+        packed_mask=packbits(flat_mask),
+        bool_mask=flat_mask,
+        qo_indptr=torch.tensor([0, node_count], dtype=torch.int32, device=device),
+        kv_indptr=torch.tensor([0, total_pages], dtype=torch.int32, device=device),
+        kv_indices=torch.arange(total_pages, dtype=torch.int32, device=device),
+        kv_last_page_len=torch.tensor([last_page_len(kv_len, page_size)], dtype=torch.int32, device=device),
+        total_pages=total_pages,
+        node_count=node_count,
+        kv_len=kv_len,
+        tree_mask=tree_mask,
+        mask_col_start=int(prefix_len),
+    )
+
+
+def build_tree_spec_from_paths(
+    *,
+    paths: Sequence[Sequence[int]],
+    prefix_len: int,
+    page_size: int,
+    device: torch.device | str,
+) -> TreeSpec:
+    """Undeduplicated tree (``flashinfer_full_verify.py:655-701``)."""
+    flat, parents, depths = build_path_tree_tokens_from_paths(paths, device=device)
+    return _tree_spec(flat_token_ids=flat, parent_indices=parents, depths=depths, prefix_len=prefix_len,
+                      page_size=page_size, device=device)
+
+
+def build_deduplicated_tree_spec_from_paths(
+    *,
+    paths: Sequence[Sequence[int]],
+    prefix_len: int,
+    page_size: int,
+    device: torch.device | str,
+) -> tuple[TreeSpec, list[list[int]]]:
+    """Deduplicated tree and its route -> node paths
+    (``flashinfer_full_verify.py:704-739``)."""
+    flat, parents, depths, route_nodes = build_deduplicated_path_tree_tokens(paths, device=device)
+    spec = _tree_spec(flat_token_ids=flat, parent_indices=parents, depths=depths, prefix_len=prefix_len,
+                      page_size=page_size, device=device)
+    return spec, route_nodes
+
+
+def prefix_layer_to_paged_kv(
+    *,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    prefix_len: int,
+    node_count: int,
+    page_size: int,
+    total_pages: int | None = None,
+) -> torch.Tensor:
+    """HF ``[1, Hkv, T, D]`` prefix K/V -> zero-initialised paged layer
+    ``[pages, 2, page_size, Hkv, D]`` with token t at page t // page_size,
+    offset t % page_size (``flashinfer_full_verify.py:814-849``)."""
+    if key.shape[0] != 1 or value.shape[0] != 1:
+        raise ValueError("full masked verify expects batch-1 prefix KV")
+    if key.ndim != 4 or value.ndim != 4:
+        raise ValueError(f"expected key/value shape [1, H, T, D], got {tuple(key.shape)} and {tuple(value.shape)}")
+    _, kv_heads, key_len, head_dim = key.shape
+    if int(key_len) != int(prefix_len):
+        raise ValueError(f"prefix cache length mismatch: expected {prefix_len}, got {key_len}")
+    if total_pages is None:
+        total_pages = ceil_div(int(prefix_len) + int(node_count), int(page_size))
+    kv_cache = torch.zeros(
+        int(total_pages), 2, int(page_size), int(kv_heads), int(head_dim), dtype=key.dtype, device=key.device
+    )
+    if int(prefix_len) > 0:
+        key_tokens = key[0].permute(1, 0, 2).contiguous()
+        value_tokens = value[0].permute(1, 0, 2).contiguous()
+        kv_ops.append_paged([kv_cache], [key_tokens], [value_tokens], start_pos=0)
+    return kv_cache
+
+
+def write_suffix_kv(
+    kv_cache: torch.Tensor,
+    *,
+    key_states: torch.Tensor,
+    value_states: torch.Tensor,
+    prefix_len: int,
+    page_size: int,
+    start_pos: int | None = None,
+) -> None:
+    """Write node K/V ``[n, Hkv, D]`` at positions ``start + i`` of one paged
+    layer (``flashinfer_full_verify.py:1027-1042``)."""
+    if int(kv_cache.shape[2]) != int(page_size):
+        raise ValueError(f"page_size {page_size} does not match the cache's {int(kv_cache.shape[2])}")
+    start = int(prefix_len) if start_pos is None else int(start_pos)
+    node_count = int(key_states.shape[0])
+    if start < 0 or start + node_count > int(kv_cache.shape[0]) * int(page_size):
+        raise IndexError(
+            f"positions [{start}, {start + node_count}) exceed the cache's "
+            f"{int(kv_cache.shape[0]) * int(page_size)} slots"
+        )
+    kv_ops.append_paged([kv_cache], [key_states], [value_states], start_pos=start)
+
+
+def first_tensor(value) -> torch.Tensor:
+    if isinstance(value, torch.Tensor):
+        return value
+    if isinstance(value, (tuple, list)):
+        for item in value:
+            if isinstance(item, torch.Tensor):
+                return item
+    raise TypeError(f"expected tensor output, got {type(value).__name__}")
+
+
+def make_prefill_wrapper(*, args, flashinfer=None) -> BatchPrefillWithPagedKVCacheWrapper:
+    """Workspace-backed wrapper (``flashinfer_full_verify.py:877-879``)."""
+    workspace = torch.empty(int(args.workspace_mb) * 1024 * 1024, dtype=torch.uint8, device=args.device)
+    return BatchPrefillWithPagedKVCacheWrapper(workspace, "NHD", backend=getattr(args, "flashinfer_backend", "auto"))
+
+
+def plan_prefill_wrapper(wrapper, tree: TreeSpec, *, args, config, dtype: torch.dtype) -> None:
+    """Masked, non-causal plan with the reference's keyword retry ladder
+    (``flashinfer_full_verify.py:953-985``)."""
+    head_dim = getattr(config, "head_dim", int(config.hidden_size) // int(config.num_attention_heads))
+    attempts = [
+        {"q_data_type": dtype, "kv_data_type": dtype},
+        {"q_data_type": str(dtype).replace("torch.", ""), "kv_data_type": str(dtype).replace("torch.", "")},
+        {},
+    ]
+    last_error: Exception | None = None
+    for kwargs in attempts:
+        try:
+            mask_kwargs = (
+                {"packed_custom_mask": tree.packed_mask}
+                if getattr(args, "use_packed_custom_mask", False)
+                else {"custom_mask": tree.bool_mask}
+            )
+            wrapper.plan(
+                tree.qo_indptr,
+                tree.kv_indptr,
+                tree.kv_indices,
+                tree.kv_last_page_len,
+                int(config.num_attention_heads),
+                int(config.num_key_value_heads),
+                int(head_dim),
+                int(args.page_size),
+                causal=False,
+                pos_encoding_mode="NONE",
+                **mask_kwargs,
+                **kwargs,
+            )
+            return
+        except (AttributeError, TypeError) as exc:
+            last_error = exc
+    raise RuntimeError(f"BatchPrefillWithPagedKVCacheWrapper.plan failed: {last_error!r}")

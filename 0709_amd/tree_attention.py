@@ -1,0 +1,386 @@
+"""Ancestor-masked paged tree / forest verify attention (FlashInfer-shaped API).
+
+``BatchPrefillWithPagedKVCacheWrapper`` keeps the plan/run protocol the
+reference drives (``flashinfer_full_verify.py:877-879``, ``:953-985``,
+``:1223``): ``plan`` receives the page-table metadata, head counts, page size,
+``causal`` and ``custom_mask`` / ``packed_custom_mask``; ``run(q, kv_cache)``
+returns ``[nnz, Hq, D]`` (optionally with the LSE).  ``plan`` does the host
+work once per verify (the reference re-plans per verify and runs per layer):
+it reads the index arrays, derives a per-query 64-bit ancestor bitmask for the
+tree columns, splits every (request, KV head, row block) along its keys so a
+launch fills the 256 CUs, and uploads the work list in one copy.  ``run`` is a
+single kernel launch (plus a merge launch when rows are split).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+
+TILE_KEYS = 64
+MAX_ROWS_PER_ITEM = 192  # 4 waves x 3 row tiles of 16
+MAX_TREE_WIDTH = 64
+DEFAULT_CU_COUNT = 256
+
+
+@dataclass
+class AttentionPlan:
+    batch: int
+    num_qo_heads: int
+    num_kv_heads: int
+    head_dim: int
+    page_size: int
+    sm_scale: float
+    q_dtype: torch.dtype
+    kv_dtype: torch.dtype
+    nnz: int
+    mask_mode: int
+    qo_indptr: torch.Tensor
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    tree_mask: torch.Tensor | None
+    meta: torch.Tensor  # int32: [work | merge | kv_len | mask_col_start]
+    num_work: int
+    num_merge: int
+    work_offset: int
+    merge_offset: int
+    kv_len_offset: int
+    col_offset: int
+    max_rows: int
+    partial_rows: int
+    kv_lens: list[int]
+    qo_lens: list[int]
+    tiles_per_split: int
+
+    def device_view(self, offset: int) -> int:
+        return int(self.meta.data_ptr()) + 4 * offset
+
+
+def _to_host_list(t: torch.Tensor | list | tuple) -> list[int]:
+    if isinstance(t, torch.Tensor):
+        return [int(x) for x in t.detach().cpu().reshape(-1).tolist()]
+    return [int(x) for x in t]
+
+
+def _dtype_from(value, default: torch.dtype) -> torch.dtype:
+    if value is None:
+        return default
+    if isinstance(value, torch.dtype):
+        return value
+    name = str(value).replace("torch.", "")
+    table = {"float16": torch.float16, "half": torch.float16, "bfloat16": torch.bfloat16}
+    if name not in table:
+        raise TypeError(f"unsupported data type {value!r}")
+    return table[name]
+
+
+def tree_mask_from_dense(mask2d: torch.Tensor) -> tuple[int, torch.Tensor] | None:
+    """(col0, bits) such that columns < col0 are visible to every row and row
+    q sees column col0 + j iff bit j of bits[q]; None if no window of at most
+    64 columns describes the mask."""
+    qo, kv = (int(x) for x in mask2d.shape)
+    if qo == 0:
+        return kv, torch.zeros(0, dtype=torch.int64, device=mask2d.device)
+    m = mask2d.to(torch.bool)
+    all_true = m.all(dim=0)
+    # col0 = first column that is not visible to every row.
+    false_cols = torch.nonzero(~all_true)
+    col0 = kv if false_cols.numel() == 0 else int(false_cols[0])
+    if kv - col0 > MAX_TREE_WIDTH:
+        return None
+    window = m[:, col0:kv].to(torch.int64)
+    shifts = torch.arange(kv - col0, device=m.device, dtype=torch.int64)
+    bits = (window << shifts).sum(dim=1) if kv > col0 else torch.zeros(qo, dtype=torch.int64, device=m.device)
+    return col0, bits
+
+
+def unpack_bits_little(packed: torch.Tensor, count: int) -> torch.Tensor:
+    """Inverse of a little-bit-order packbits over ``count`` booleans."""
+    b = packed.to(torch.uint8).reshape(-1).to(torch.int32)
+    bits = (b[:, None] >> torch.arange(8, device=b.device, dtype=torch.int32)) & 1
+    return bits.reshape(-1)[:count].to(torch.bool)
+
+
+class BatchPrefillWithPagedKVCacheWrapper:
+    """Paged prefill attention with a custom (tree) mask on the gfx950 kernel.
+
+    ``float_workspace_buffer`` holds the fp32 split-KV partial states (like
+    FlashInfer's workspace); its size bounds how finely keys are split.
+    """
+
+    def __init__(
+        self,
+        float_workspace_buffer: torch.Tensor,
+        kv_layout: str = "NHD",
+        backend: str = "auto",
+        **_unused,
+    ) -> None:
+        if kv_layout != "NHD":
+            raise NotImplementedError("only the NHD paged layout is supported")
+        self._workspace = float_workspace_buffer
+        self._kv_layout = kv_layout
+        self._backend = backend
+        self._plan: AttentionPlan | None = None
+        self.split_target_items = 2 * DEFAULT_CU_COUNT
+        self.min_tiles_per_split = 1
+
+    @property
+    def device(self) -> torch.device:
+        return self._workspace.device
+
+    # ------------------------------------------------------------------ plan
+    def plan(
+        self,
+        qo_indptr: torch.Tensor,
+        paged_kv_indptr: torch.Tensor,
+        paged_kv_indices: torch.Tensor,
+        paged_kv_last_page_len: torch.Tensor,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim_qk: int,
+        page_size: int,
+        head_dim_vo: int | None = None,
+        custom_mask: torch.Tensor | None = None,
+        packed_custom_mask: torch.Tensor | None = None,
+        causal: bool = False,
+        pos_encoding_mode: str = "NONE",
+        use_fp16_qk_reduction: bool = False,
+        sm_scale: float | None = None,
+        window_left: int = -1,
+        logits_soft_cap: float | None = None,
+        rope_scale: float | None = None,
+        rope_theta: float | None = None,
+        q_data_type=torch.float16,
+        kv_data_type=None,
+        non_blocking: bool = True,
+    ) -> None:
+        device = self.device
+        _lib.require_device(self._workspace, what="BatchPrefillWithPagedKVCacheWrapper")
+        if pos_encoding_mode != "NONE":
+            raise NotImplementedError("only pos_encoding_mode='NONE' is supported (RoPE is applied by the caller)")
+        if head_dim_vo is not None and int(head_dim_vo) != int(head_dim_qk):
+            raise NotImplementedError("head_dim_vo must equal head_dim_qk")
+        if window_left != -1 or logits_soft_cap not in (None, 0.0):
+            raise NotImplementedError("sliding windows and logit soft-capping are not supported")
+        hq, hkv, d, ps = int(num_qo_heads), int(num_kv_heads), int(head_dim_qk), int(page_size)
+        if hq <= 0 or hkv <= 0 or hq % hkv != 0:
+            raise ValueError("num_qo_heads must be a positive multiple of num_kv_heads")
+        if d not in (64, 128):
+            raise NotImplementedError(f"head_dim {d} is not supported (64 or 128)")
+        if ps <= 0:
+            raise ValueError("page_size must be positive")
+        q_dtype = _dtype_from(q_data_type, torch.float16)
+        kv_dtype = _dtype_from(kv_data_type, q_dtype)
+        if q_dtype != kv_dtype:
+            raise NotImplementedError("q and kv data types must match")
+
+        qo = _to_host_list(qo_indptr)
+        kvp = _to_host_list(paged_kv_indptr)
+        last = _to_host_list(paged_kv_last_page_len)
+        batch = len(qo) - 1
+        if batch <= 0 or len(kvp) != batch + 1 or len(last) != batch:
+            raise ValueError("qo_indptr / kv_indptr / kv_last_page_len sizes are inconsistent")
+        qo_lens = [qo[b + 1] - qo[b] for b in range(batch)]
+        pages = [kvp[b + 1] - kvp[b] for b in range(batch)]
+        if any(x < 0 for x in qo_lens) or any(x < 0 for x in pages):
+            raise ValueError("indptr arrays must be non-decreasing")
+        kv_lens = [0 if pages[b] == 0 else (pages[b] - 1) * ps + last[b] for b in range(batch)]
+        for b in range(batch):
+            if pages[b] and not (1 <= last[b] <= ps):
+                raise ValueError(f"kv_last_page_len[{b}]={last[b]} outside [1, page_size]")
+
+        # ---- mask ----
+        mask_mode = _lib.MASK_CAUSAL if causal else _lib.MASK_NONE
+        tree_bits = None
+        cols = [0] * batch
+        if custom_mask is not None or packed_custom_mask is not None:
+            if causal:
+                raise ValueError("custom masks require causal=False")
+            mask_mode = _lib.MASK_TREE
+            cached = getattr(custom_mask, "_atlas_tree_window", None) if custom_mask is not None else None
+            if cached is not None and batch == 1:
+                col0, bits = cached
+                cols = [int(col0)]
+                tree_bits = bits.to(device=device, dtype=torch.int64)
+            else:
+                total = sum(qo_lens[b] * kv_lens[b] for b in range(batch))
+                if custom_mask is not None:
+                    flat = custom_mask.reshape(-1).to(device=device, dtype=torch.bool)
+                else:
+                    flat = self._unpack_segments(packed_custom_mask.to(device), qo_lens, kv_lens)
+                if int(flat.numel()) != total:
+                    raise ValueError(f"custom mask has {int(flat.numel())} entries, expected {total}")
+                parts = []
+                off = 0
+                for b in range(batch):
+                    seg = flat[off : off + qo_lens[b] * kv_lens[b]].view(qo_lens[b], kv_lens[b])
+                    off += qo_lens[b] * kv_lens[b]
+                    res = tree_mask_from_dense(seg)
+                    if res is None:
+                        raise NotImplementedError(
+                            f"request {b}: the mask's non-visible region spans more than "
+                            f"{MAX_TREE_WIDTH} key columns; only prefix + tree masks are supported"
+                        )
+                    cols[b] = res[0]
+                    parts.append(res[1])
+                tree_bits = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.int64, device=device)
+
+        # ---- work decomposition ----
+        group = hq // hkv
+        blocks = []  # (req, row_start, num_rows)
+        for b in range(batch):
+            rows = qo_lens[b] * group
+            for r0 in range(0, rows, MAX_ROWS_PER_ITEM):
+                blocks.append((b, r0, min(MAX_ROWS_PER_ITEM, rows - r0)))
+        unit_tiles = sum(hkv * math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks)
+        tiles_per_split = max(self.min_tiles_per_split, math.ceil(unit_tiles / max(1, self.split_target_items)))
+        ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // (4 * (d + 1))
+        while True:
+            work, merge = [], []
+            partial_rows = 0
+            for (b, r0, nr) in blocks:
+                tiles = math.ceil(kv_lens[b] / TILE_KEYS)
+                splits = max(1, math.ceil(tiles / tiles_per_split))
+                for h in range(hkv):
+                    if splits == 1:
+                        work.append((b, h, r0, nr, 0, kv_lens[b], -1, 0))
+                        continue
+                    base = partial_rows
+                    for s in range(splits):
+                        k0 = s * tiles_per_split * TILE_KEYS
+                        k1 = min(kv_lens[b], (s + 1) * tiles_per_split * TILE_KEYS)
+                        work.append((b, h, r0, nr, k0, k1, base + s * nr, 0))
+                    merge.append((b, h, r0, nr, base, splits, 0, 0))
+                    partial_rows += splits * nr
+            if partial_rows <= ws_rows_cap:
+                break
+            tiles_per_split *= 2
+        max_rows = max((nr for (_, _, nr) in blocks), default=1)
+
+        # Interleave work items so consecutive workgroups (spread round-robin
+        # over the XCDs) come from different KV heads and splits.
+        meta_vals: list[int] = []
+        for item in work:
+            meta_vals.extend(item)
+        merge_off = len(meta_vals)
+        for item in merge:
+            meta_vals.extend(item)
+        kvlen_off = len(meta_vals)
+        meta_vals.extend(kv_lens)
+        col_off = len(meta_vals)
+        meta_vals.extend(cols)
+        meta = torch.tensor(meta_vals, dtype=torch.int32).to(device, non_blocking=non_blocking)
+
+        self._plan = AttentionPlan(
+            batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,
+            sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
+            q_dtype=q_dtype, kv_dtype=kv_dtype, nnz=qo[-1] - qo[0] if batch else 0, mask_mode=mask_mode,
+            qo_indptr=qo_indptr.to(device=device, dtype=torch.int32).contiguous()
+            if isinstance(qo_indptr, torch.Tensor) else torch.tensor(qo, dtype=torch.int32, device=device),
+            kv_indptr=paged_kv_indptr.to(device=device, dtype=torch.int32).contiguous()
+            if isinstance(paged_kv_indptr, torch.Tensor) else torch.tensor(kvp, dtype=torch.int32, device=device),
+            kv_indices=paged_kv_indices.to(device=device, dtype=torch.int32).contiguous(),
+            tree_mask=tree_bits, meta=meta, num_work=len(work), num_merge=len(merge), work_offset=0,
+            merge_offset=merge_off, kv_len_offset=kvlen_off, col_offset=col_off, max_rows=max_rows,
+            partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=tiles_per_split,
+        )
+
+    @staticmethod
+    def _unpack_segments(packed: torch.Tensor, qo_lens: list[int], kv_lens: list[int]) -> torch.Tensor:
+        # Each request's segment is packed separately and padded to whole bytes.
+        parts = []
+        byte_off = 0
+        for ql, kl in zip(qo_lens, kv_lens):
+            count = ql * kl
+            nbytes = (count + 7) // 8
+            parts.append(unpack_bits_little(packed[byte_off : byte_off + nbytes], count))
+            byte_off += nbytes
+        return torch.cat(parts) if parts else torch.zeros(0, dtype=torch.bool, device=packed.device)
+
+    begin_forward = plan
+
+    # ------------------------------------------------------------------- run
+    def run(
+        self,
+        q: torch.Tensor,
+        paged_kv_cache,
+        *args,
+        out: torch.Tensor | None = None,
+        lse: torch.Tensor | None = None,
+        return_lse: bool = False,
+    ):
+        plan = self._plan
+        if plan is None:
+            raise RuntimeError("plan() must be called before run()")
+        if isinstance(paged_kv_cache, (tuple, list)):
+            k_cache, v_cache = paged_kv_cache
+            if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+                raise ValueError("K and V caches must have the same shape and strides")
+            if k_cache.ndim != 4:
+                raise ValueError("tuple KV caches must be [pages, page_size, Hkv, D]")
+            base = k_cache
+            es = k_cache.element_size()
+            page_stride = k_cache.stride(0) * es
+            token_stride = k_cache.stride(1) * es
+            v_offset = int(v_cache.data_ptr()) - int(k_cache.data_ptr())
+            shape_tail = tuple(k_cache.shape[1:])
+        else:
+            kv = paged_kv_cache
+            if kv.ndim != 5 or int(kv.shape[1]) != 2:
+                raise ValueError(f"kv cache must be [pages, 2, page_size, Hkv, D], got {tuple(kv.shape)}")
+            base = kv
+            es = kv.element_size()
+            page_stride = kv.stride(0) * es
+            token_stride = kv.stride(2) * es
+            v_offset = kv.stride(1) * es
+            shape_tail = (int(kv.shape[2]), int(kv.shape[3]), int(kv.shape[4]))
+        device = _lib.require_device(q, base, what="tree verify attention")
+        if shape_tail != (plan.page_size, plan.num_kv_heads, plan.head_dim):
+            raise ValueError(
+                f"kv cache page shape {shape_tail} does not match the plan "
+                f"({plan.page_size}, {plan.num_kv_heads}, {plan.head_dim})"
+            )
+        if base.stride(-1) != 1 or (plan.num_kv_heads > 1 and base.stride(-2) != plan.head_dim):
+            raise ValueError("kv cache rows (Hkv, D) must be contiguous")
+        if q.dtype != plan.q_dtype or base.dtype != plan.kv_dtype:
+            raise TypeError(f"dtype mismatch: q {q.dtype}, kv {base.dtype}, planned {plan.q_dtype}")
+        if q.ndim != 3 or tuple(q.shape[1:]) != (plan.num_qo_heads, plan.head_dim) or int(q.shape[0]) < plan.nnz:
+            raise ValueError(f"q must be [nnz, {plan.num_qo_heads}, {plan.head_dim}], got {tuple(q.shape)}")
+        if q.stride(-1) != 1:
+            raise ValueError("q rows must be contiguous")
+        if out is None:
+            out = torch.empty((int(q.shape[0]), plan.num_qo_heads, plan.head_dim), dtype=q.dtype, device=device)
+        if out.stride(-1) != 1 or out.dtype != q.dtype:
+            raise ValueError("out must have q's dtype and contiguous rows")
+        want_lse = return_lse or lse is not None
+        if want_lse and lse is None:
+            lse = torch.empty((int(q.shape[0]), plan.num_qo_heads), dtype=torch.float32, device=device)
+        if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()):
+            raise ValueError("lse must be a contiguous float32 tensor")
+        ws_bytes = plan.partial_rows * (plan.head_dim + 1) * 4
+        lib = _lib.load()
+        rc = lib.atlas_tree_verify_attn(
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride,
+            _lib.ptr(plan.qo_indptr), _lib.ptr(plan.kv_indptr), _lib.ptr(plan.kv_indices),
+            plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
+            plan.device_view(plan.col_offset), plan.device_view(plan.work_offset), plan.num_work,
+            plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge, plan.max_rows,
+            plan.num_qo_heads, plan.num_kv_heads, plan.head_dim, plan.page_size, plan.sm_scale,
+            _lib.dtype_code(q.dtype), _lib.ptr(out), out.stride(0), out.stride(1),
+            _lib.ptr(lse) if lse is not None else None, _lib.ptr(self._workspace) if ws_bytes else None,
+            ws_bytes, _lib.stream_of(device),
+        )
+        _lib.check(rc, "atlas_tree_verify_attn")
+        if want_lse:
+            return out, lse
+        return out
+
+    forward = run
+
+    @property
+    def current_plan(self) -> AttentionPlan | None:
+        return self._plan

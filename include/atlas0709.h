@@ -1,0 +1,252 @@
+/*
+ * atlas0709.h -- C ABI of the MI355X (gfx950) paged-KV tree path.
+ *
+ * One shared library (0709_amd/_lib/libatlas0709_hip.so) exports these entry
+ * points.  Conventions shared by every call:
+ *   - all pointers named *_dev are device (HBM) addresses; arrays named *_host
+ *     are host memory that is copied into the kernel argument block;
+ *   - memory is owned by the caller; no entry point allocates device memory;
+ *   - work is enqueued on `stream` (a hipStream_t passed as void*) and the call
+ *     returns without synchronising;
+ *   - the return value is 0 on success, ATLAS_EINVAL for an argument error,
+ *     ATLAS_EUNSUPPORTED for a configuration the kernels do not cover, and
+ *     ATLAS_EHIP_BASE - hipError_t for a HIP runtime error.  atlas_last_error()
+ *     returns a message for the last failing call on the calling thread.
+ *
+ * KV layouts.  A layer's K (or V) row for one token is `row_bytes` contiguous
+ * bytes (num_kv_heads * head_dim * element size).  A physical slot id s lives at
+ *     base + (s / page_size) * page_stride + (s % page_size) * token_stride
+ * where base is the layer's K or V base address.  This covers
+ *   - FlashInfer NHD pages [pages, 2, page_size, Hkv, D] (V base = K base +
+ *     page_size*token_stride, page_stride = 2*page_size*token_stride), and
+ *   - SGLang's flat token pool [slots, Hkv, D] per layer (page_size = 1,
+ *     separate K and V bases, page_stride = token_stride = row_bytes).
+ */
+#ifndef ATLAS0709_H
+#define ATLAS0709_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ATLAS_OK 0
+#define ATLAS_EINVAL (-1)
+#define ATLAS_EUNSUPPORTED (-2)
+#define ATLAS_EHIP_BASE (-1000)
+
+/* Data types of KV / query / output elements. */
+#define ATLAS_DTYPE_F16 0
+#define ATLAS_DTYPE_BF16 1
+
+/* Largest layer count one KV call carries in its argument block; larger pools
+ * are processed in several launches by the same call. */
+#define ATLAS_MAX_LAYERS_PER_LAUNCH 64
+/* Largest item count for the *_host index variants (indices in kernarg). */
+#define ATLAS_MAX_INLINE_ITEMS 64
+
+const char* atlas_last_error(void);
+int atlas_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * KV movement.  All three are HBM-bound 16-byte-vector gathers/scatters over
+ * every layer in one launch.  row_bytes must be a multiple of 16 and every
+ * base / stride a multiple of 16.
+ * ---------------------------------------------------------------------- */
+
+/* K[dst[i]] <- K[src[i]] and V[dst[i]] <- V[src[i]] for every layer.
+ * Replaces SGLang MHATokenToKVPool.move_kv_cache(tgt_loc, src_loc) as called
+ * by SGLangRoutePoolBridge._copy_kv_slots
+ * (src/atlas_0709/flashinfer_paged/sglang_runtime.py:686-695), whose
+ * semantics the reference pins as values[dst] = values[src]
+ * (tests/test_tail_page_cow.py:14-16).  dst and src must be disjoint sets
+ * (tail-page copy-on-write copies into freshly allocated pages). */
+int atlas_kv_move_slots(const void* const* k_layers, const void* const* v_layers, int num_layers,
+                        int64_t page_size, int64_t page_stride, int64_t token_stride,
+                        int64_t row_bytes, const int64_t* dst_slots_dev,
+                        const int64_t* src_slots_dev, int64_t n, void* stream);
+
+/* Append: write dense per-layer source rows into slots.
+ * K[slot_i] <- k_src_l[i], V[slot_i] <- v_src_l[i] for every layer l, where
+ * slot_i = dst_slots_dev[i] when dst_slots_dev != NULL, else dst_start + i.
+ * Source row i of layer l lives at k_src[l] + i * src_token_stride.
+ * Replaces write_suffix_kv (src/atlas_0709/flashinfer_full_verify.py:1027-1042,
+ * one layer, contiguous positions through the identity page table) and
+ * SGLang set_kv_buffer as used by the Drafter decode
+ * (src/atlas_0709/flashinfer_paged/sglang_page_attention.py:187-194). */
+int atlas_kv_append(const void* const* k_layers, const void* const* v_layers, int num_layers,
+                    int64_t page_size, int64_t page_stride, int64_t token_stride,
+                    int64_t row_bytes, const void* const* k_src, const void* const* v_src,
+                    int64_t src_token_stride, const int64_t* dst_slots_dev, int64_t dst_start,
+                    int64_t n, void* stream);
+
+/* Route-commit compaction through a page table.  For item i (request
+ * item_req[i], or 0 when item_req is NULL) the logical positions src_pos[i]
+ * and dst_pos[i] are mapped through that request's pages
+ * kv_indices[kv_indptr[req] + pos / page_size] (identity when kv_indices is
+ * NULL) and the row is copied for every layer.  The call is a gather followed
+ * by a scatter, like the reference's clone-then-index_put: when some
+ * destination equals another item's source it stages through `workspace_dev`
+ * (needs n * 2 * num_layers * row_bytes bytes), otherwise it copies in place.
+ * Replaces DirectFlashInferMaskedTreeVerifyBackend._commit_selected_path
+ * (src/atlas_0709/target_runtime.py:873-920). */
+int atlas_kv_commit_paged(const void* const* k_layers, const void* const* v_layers, int num_layers,
+                          int64_t page_size, int64_t page_stride, int64_t token_stride,
+                          int64_t row_bytes, const int32_t* kv_indptr_dev,
+                          const int32_t* kv_indices_dev, const int32_t* item_req_dev,
+                          const int64_t* src_pos_dev, const int64_t* dst_pos_dev, int64_t n,
+                          int needs_staging, void* workspace_dev, size_t workspace_bytes,
+                          void* stream);
+
+/* Same as atlas_kv_commit_paged for up to ATLAS_MAX_INLINE_ITEMS items whose
+ * request ids and positions are host arrays: they travel in the kernel
+ * argument block, so the commit costs no host-to-device copy. */
+int atlas_kv_commit_paged_host(const void* const* k_layers, const void* const* v_layers,
+                               int num_layers, int64_t page_size, int64_t page_stride,
+                               int64_t token_stride, int64_t row_bytes,
+                               const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
+                               const int32_t* item_req_host, const int64_t* src_pos_host,
+                               const int64_t* dst_pos_host, int64_t n, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Ancestor-masked paged tree / forest verify attention.
+ * ---------------------------------------------------------------------- */
+
+/* Work item of one attention workgroup (filled by the host planner). */
+typedef struct {
+  int32_t req;          /* request index */
+  int32_t kv_head;      /* KV head */
+  int32_t row_start;    /* first packed query row (node * group + head_in_group) */
+  int32_t num_rows;     /* packed rows handled (<= 16 * 4 * row tiles per wave) */
+  int32_t kv_start;     /* first key position (multiple of 64) */
+  int32_t kv_end;       /* one past the last key position of this split */
+  int32_t partial_row;  /* first row in the partial buffers, or -1 when the item
+                           is the only split and writes the final output */
+  int32_t pad;
+} atlas_attn_work_t;
+
+/* Merge item: combines `num_splits` partial states of one row block. */
+typedef struct {
+  int32_t req;
+  int32_t kv_head;
+  int32_t row_start;
+  int32_t num_rows;
+  int32_t partial_row;  /* partial row of split 0; split s row r lives at
+                           partial_row + s * num_rows + r */
+  int32_t num_splits;
+  int32_t pad0;
+  int32_t pad1;
+} atlas_attn_merge_t;
+
+/* Mask modes. */
+#define ATLAS_MASK_NONE 0   /* every key < kv_len visible */
+#define ATLAS_MASK_TREE 1   /* keys < mask_col_start[req] visible; key p >= that
+                               visible iff bit (p - start) of tree_mask[q] */
+#define ATLAS_MASK_CAUSAL 2 /* key p visible iff p <= kv_len - qo_len + q */
+
+/* O = softmax(Q K^T * sm_scale + M) V over paged KV, GQA (num_qo_heads a
+ * multiple of num_kv_heads), one launch for all requests plus a merge launch
+ * when a row block is split along the keys.  q: [nnz, Hq, D]; kv_cache:
+ * FlashInfer NHD pages [pages, 2, page_size, Hkv, D] addressed with the
+ * strides above; out: [nnz, Hq, D] in the input dtype; lse (optional, may be
+ * NULL): [nnz, Hq] fp32, natural-log log-sum-exp of the scaled scores.
+ * workspace_dev holds fp32 partial states: partial_rows * (D + 1) * 4 bytes.
+ * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with
+ * causal=False and custom_mask as used by run_flashinfer_full_verify
+ * (src/atlas_0709/flashinfer_full_verify.py:953-985, :1223). */
+int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stride_head,
+                           const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
+                           int64_t token_stride, const int32_t* qo_indptr_dev,
+                           const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
+                           const int32_t* kv_len_dev, int mask_mode,
+                           const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                           const atlas_attn_work_t* work_dev, int num_work,
+                           const atlas_attn_merge_t* merge_dev, int num_merge,
+                           int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                           int head_dim, int page_size, float sm_scale, int dtype, void* out,
+                           int64_t out_stride_token, int64_t out_stride_head, float* lse,
+                           void* workspace_dev, size_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Reachability prune and free-list return.
+ * ---------------------------------------------------------------------- */
+
+/* Mark-and-sweep over a page pool of num_pages pages held as bitmaps
+ * (bit p of word p/32).  live_slots_dev lists slot ids of every live path (the
+ * committed prefix and each retained route); their pages are marked live in
+ * live_bitmap_dev (cleared first).  Every page set in owned_bitmap_dev but not
+ * live is cleared from owned_bitmap_dev and written to free_pages_dev in
+ * ascending order; the count goes to free_count_dev.
+ * Replaces SGLangRoutePoolBridge.release_unreferenced_node_slots
+ * (src/atlas_0709/flashinfer_paged/sglang_runtime.py:507-539):
+ * releasable = sorted(owned - live). */
+int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                      const int64_t* live_slots_dev, int64_t n_live_slots, int64_t page_size,
+                      int64_t* free_pages_dev, int64_t* free_count_dev, void* stream);
+
+/* Set the owned bit of the pages of `n` slot ids (pages newly handed out). */
+int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev, int64_t n,
+                     int64_t page_size, void* stream);
+
+/* Paged allocator slot assignment (the free list is a device int64 array of
+ * page ids whose head the host advances by the number of pages consumed).
+ * Decode: request i writes out[i] = last_loc[i] + 1 when seq_lens[i] - 1 is not
+ * a multiple of page_size, else free_pages[j] * page_size where j counts the
+ * earlier requests that also start a page.  Replaces SGLang
+ * PagedTokenToKVPoolAllocator.alloc_decode as called by
+ * SGLangRoutePoolBridge.allocate_decode_slots
+ * (src/atlas_0709/flashinfer_paged/sglang_runtime.py:636-659). */
+int atlas_alloc_decode_slots(const int64_t* seq_lens_dev, const int64_t* last_loc_dev,
+                             const int64_t* free_pages_dev, int64_t page_size, int bs,
+                             int64_t* out_dev, void* stream);
+
+/* Extend: request i appends tokens prefix_lens[i] .. seq_lens[i]-1, first
+ * continuing its partial tail page after last_loc[i], then opening pages from
+ * the free list in request order; slots are packed in request order.
+ * Replaces PagedTokenToKVPoolAllocator.alloc_extend as called by
+ * SGLangRoutePoolBridge.allocate_extend_slots
+ * (src/atlas_0709/flashinfer_paged/sglang_runtime.py:595-634). */
+int atlas_alloc_extend_slots(const int64_t* prefix_lens_dev, const int64_t* seq_lens_dev,
+                             const int64_t* last_loc_dev, const int64_t* free_pages_dev,
+                             int64_t page_size, int bs, int64_t* out_dev, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Paged metadata.
+ * ---------------------------------------------------------------------- */
+
+/* Compress concatenated token-slot paths into page tables.  Path b occupies
+ * slots_dev[path_offsets_host[b] .. path_offsets_host[b+1]).  Writes
+ * kv_page_indices (int32, one per page, page b's run starting at
+ * page_offsets_host[b]) and, when validate != 0, sets *layout_ok_dev to 0 if
+ * any page of any path is not page-aligned and contiguous (it must hold 1
+ * before the call).  Replaces the per-route loop of
+ * build_flashinfer_paged_kv_metadata
+ * (src/atlas_0709/flashinfer_paged/paged_metadata.py:64-102). */
+int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_dev,
+                         const int64_t* page_offsets_dev, int num_paths, int64_t total_pages,
+                         int64_t page_size, int validate, int32_t* kv_page_indices_dev,
+                         int32_t* layout_ok_dev, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Route scoring.
+ * ---------------------------------------------------------------------- */
+
+/* out[i] = log_softmax(logits[row[i]])[token[i]] in fp32 for n gathers over
+ * rows of `vocab` logits (dtype fp16, bf16, or ATLAS_DTYPE_F32 = 2).  Row
+ * log-sum-exps are computed once per distinct row.  Replaces the two
+ * full-vocab log_softmax calls and the per-token gathers of
+ * DirectFlashInferMaskedTreeVerifyBackend._score_routes
+ * (src/atlas_0709/target_runtime.py:732-742). */
+#define ATLAS_DTYPE_F32 2
+int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows,
+                          int64_t vocab, int dtype, const int32_t* row_dev,
+                          const int64_t* token_dev, int64_t n, float* row_lse_dev,
+                          float* out_dev, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ATLAS0709_H */

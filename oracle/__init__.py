@@ -1,0 +1,29 @@
+"""CPU restatement of the reference's paged-KV tree path -- TEST INFRASTRUCTURE.
+
+This package is the checker, never the product: only ``tests/``,
+``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
+it.  Every function cites the reference file:line it restates (paths relative
+to the reference's ``src/atlas_0709/``).  Integer and byte work is numpy;
+attention is the closed form ``softmax(Q K^T * scale + M) V`` in float64 (or
+float32 when timed as the CPU baseline).
+
+Pinning (what each function is checked against in ``tests/``):
+
+* ``paged_metadata``      -- reference literals (test_paged_attention_metadata.py:24-67)
+* ``dedup_tree``          -- reference literals (test_tree_dedup.py:6-35) + brute force
+* ``ancestor_mask``       -- closed form from parents + brute-force ancestor walk
+* ``masked_attention``    -- torch SDPA with a bool mask, page-permutation
+                             invariance, one-node = decode, uniform-V identity
+* ``write_suffix`` / ``commit`` / ``grow_capacity``
+                          -- reference literals (test_target_kv_commit.py:28-73)
+* ``move_kv``             -- reference FakeKVCache semantics and move lists
+                             (test_tail_page_cow.py:14-16, :77-79, :111-113, :193-195)
+* ``prune``               -- reference literals (test_tail_page_cow.py:241-293)
+* ``PagedAllocator``      -- documented SGLang paged-allocator policy; decode /
+                             extend slot rules checked against brute force.
+                             SGLang's own allocator is absent: parity unpinned
+                             against it (only against this restated policy).
+* ``scoring``             -- reference literals (test_target_kv_commit.py:76-367)
+* ``RoutePool``           -- reference literals (test_tail_page_cow.py,
+                             test_req_row_incremental.py)
+"""

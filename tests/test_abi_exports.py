@@ -1,0 +1,63 @@
+"""The C-ABI library loads and exports every entry point include/*.h declares
+(no compute calls: runs without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+from helpers import ROOT, pkg
+
+
+def _declared_symbols() -> set[str]:
+    names = set()
+    for header in (ROOT / "include").glob("*.h"):
+        text = header.read_text()
+        names.update(re.findall(r"^\s*(?:int|const char\*)\s+(atlas_\w+)\s*\(", text, flags=re.M))
+    return names
+
+
+def test_header_declares_entry_points():
+    names = _declared_symbols()
+    assert {"atlas_tree_verify_attn", "atlas_kv_move_slots", "atlas_kv_commit_paged", "atlas_prune_pages"} <= names
+
+
+def test_library_exports_every_declared_symbol():
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    for name in sorted(_declared_symbols()):
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+    # The ctypes signature table covers the same set.
+    assert set(lib_mod.exported_symbols()) == _declared_symbols()
+
+
+def test_abi_version_and_error_string():
+    lib = pkg("_lib").load()
+    assert lib.atlas_abi_version() == 1
+    assert isinstance(lib.atlas_last_error(), bytes)
+
+
+def test_argument_errors_are_reported_without_device_work():
+    """Invalid arguments are rejected before any launch (no GPU needed)."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    rc = lib.atlas_kv_move_slots(None, None, 0, 1, 16, 16, 16, None, None, 4, None)
+    assert rc == lib_mod.ATLAS_EINVAL
+    assert b"" != lib.atlas_last_error()
+    rc = lib.atlas_tree_verify_attn(
+        None, 0, 0,            # q, strides
+        None, 0, 0, 0,         # kv cache, page stride, V offset, token stride
+        None, None, None, None,  # qo_indptr, kv_indptr, kv_indices, kv_len
+        0, None, None,         # mask mode, tree mask, mask column start
+        None, 0, None, 0,      # work, merge lists
+        1, 32, 8, 96, 16,      # rows per item, Hq, Hkv, head_dim (unsupported), page size
+        ctypes.c_float(0.1), 0,
+        None, 0, 0, None,      # out, out strides, lse
+        None, 0, None,         # workspace, bytes, stream
+    )
+    assert rc == lib_mod.ATLAS_EINVAL
+    try:
+        lib_mod.check(rc, "probe")
+    except ValueError as exc:
+        assert "probe" in str(exc)
+    else:
+        raise AssertionError("check() did not raise")

@@ -1,0 +1,183 @@
+"""KV append / move / commit kernels vs the oracle: bit-exact."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits16, pkg
+from oracle import paged_kv as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand(gen, shape, dtype):
+    return (torch.randn(shape, generator=gen) * 0.5).to(dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("layers,heads,dim", [(2, 8, 64), (3, 8, 128), (1, 2, 64)])
+def test_move_slots_matches_values_dst_eq_src(dev, dtype, layers, heads, dim):
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(1)
+    slots = 512
+    k_cpu = [_rand(gen, (slots, heads, dim), dtype) for _ in range(layers)]
+    v_cpu = [_rand(gen, (slots, heads, dim), dtype) for _ in range(layers)]
+    perm = torch.randperm(slots, generator=gen)
+    src = perm[:40]
+    dst = perm[100:140]
+    k_dev = [t.to(dev) for t in k_cpu]
+    v_dev = [t.to(dev) for t in v_cpu]
+    kv.move_slots(k_dev, v_dev, dst.to(dev), src.to(dev))
+    torch.cuda.synchronize()
+    k_np = [bits16(t) for t in k_cpu]
+    v_np = [bits16(t) for t in v_cpu]
+    ref.move_kv(k_np, v_np, dst.tolist(), src.tolist())
+    for a, b in zip(k_dev + v_dev, k_np + v_np):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
+def test_move_slots_empty_and_reference_move_list(dev):
+    kv = pkg("kv_ops")
+    # tests/test_tail_page_cow.py:77-79: one COW move ([40, 41, 42] <- [0, 1, 2]).
+    k = torch.arange(512 * 8, dtype=torch.float16).reshape(512, 1, 8).to(dev)
+    v = (-torch.arange(512 * 8, dtype=torch.float16)).reshape(512, 1, 8).to(dev)
+    kv.move_slots([k], [v], torch.tensor([], dtype=torch.long, device=dev), torch.tensor([], dtype=torch.long, device=dev))
+    kv.move_slots([k], [v], torch.tensor([40, 41, 42], device=dev), torch.tensor([0, 1, 2], device=dev))
+    torch.cuda.synchronize()
+    assert torch.equal(k[40:43].cpu(), k[0:3].cpu())
+    assert torch.equal(v[40:43].cpu(), v[0:3].cpu())
+    assert torch.equal(k[43].cpu(), torch.arange(43 * 8, 44 * 8, dtype=torch.float16).reshape(1, 8))
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_append_paged_write_suffix_matches_oracle(dev, dtype):
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(2)
+    pages, ps, h, d = 9, 16, 8, 128
+    cache_cpu = _rand(gen, (pages, 2, ps, h, d), dtype)
+    key = _rand(gen, (13, h, d), dtype)
+    val = _rand(gen, (13, h, d), dtype)
+    cache = cache_cpu.to(dev)
+    ffv.write_suffix_kv(cache, key_states=key.to(dev), value_states=val.to(dev), prefix_len=101, page_size=ps)
+    torch.cuda.synchronize()
+    expect = bits16(cache_cpu).copy()
+    ref.write_suffix(expect, bits16(key), bits16(val), 101)
+    np.testing.assert_array_equal(bits16(cache), expect)
+
+
+def test_prefix_layer_to_paged_kv_reference_literal(dev):
+    # tests/test_target_kv_commit.py:58-73 (float32 literal rows, here fp16).
+    ffv = pkg("flashinfer_full_verify")
+    key = torch.arange(5, dtype=torch.float16).reshape(1, 1, 5, 1).repeat(1, 1, 1, 8).to(dev)
+    value = (100 + torch.arange(5, dtype=torch.float16)).reshape(1, 1, 5, 1).repeat(1, 1, 1, 8).to(dev)
+    cache = ffv.prefix_layer_to_paged_kv(key=key, value=value, prefix_len=5, node_count=2, page_size=4)
+    torch.cuda.synchronize()
+    c = cache.cpu()
+    assert c.shape == (2, 2, 4, 1, 8)
+    assert [c[p // 4, 0, p % 4, 0, 0].item() for p in range(5)] == [0, 1, 2, 3, 4]
+    assert [c[p // 4, 1, p % 4, 0, 0].item() for p in range(5)] == [100, 101, 102, 103, 104]
+    assert float(c[1, :, 1:].abs().sum()) == 0.0
+
+
+@pytest.mark.parametrize("node_ids", [(0, 2), (0, 1, 4, 5), (6, 7, 8, 9), (0, 1, 2, 3)])
+@pytest.mark.parametrize("permuted", [False, True])
+def test_commit_matches_gather_clone_scatter(dev, node_ids, permuted):
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(3)
+    layers, pages, ps, h, d = 4, 12, 16, 8, 128
+    cpu = [_rand(gen, (pages, 2, ps, h, d), torch.float16) for _ in range(layers)]
+    prefix_len = 150
+    indices = torch.randperm(pages, generator=gen).to(torch.int32) if permuted else None
+    devs = [t.to(dev) for t in cpu]
+    src = [prefix_len + n for n in node_ids]
+    dst = list(range(prefix_len, prefix_len + len(node_ids)))
+    kv.commit_paged(
+        devs, src, dst,
+        kv_indptr=None if indices is None else torch.tensor([0, pages], dtype=torch.int32, device=dev),
+        kv_indices=None if indices is None else indices.to(dev),
+    )
+    torch.cuda.synchronize()
+    expect = [bits16(t).copy() for t in cpu]
+    ref.commit(expect, prefix_len, node_ids, None if indices is None else indices.tolist())
+    for a, b in zip(devs, expect):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
+def test_commit_aliasing_uses_staging(dev):
+    kv = pkg("kv_ops")
+    assert kv.commit_positions_need_staging([10, 12], [9, 10])
+    assert not kv.commit_positions_need_staging([10, 12], [10, 11])
+    gen = torch.Generator().manual_seed(4)
+    cpu = [_rand(gen, (6, 2, 4, 2, 64), torch.float16) for _ in range(3)]
+    devs = [t.to(dev) for t in cpu]
+    # dst 5 is the source of item 1: a one-pass copy would race.
+    src, dst = [7, 5, 9], [4, 5, 6]
+    src2, dst2 = [5, 9, 2], [8, 5, 7]
+    kv.commit_paged(devs, src2, dst2)
+    kv.commit_paged(devs, src, dst)
+    torch.cuda.synchronize()
+    expect = [bits16(t).copy() for t in cpu]
+    for layer in expect:
+        for s_list, d_list in ((src2, dst2), (src, dst)):
+            rows = [layer[s // 4, :, s % 4].copy() for s in s_list]
+            for r, d_ in zip(rows, d_list):
+                layer[d_ // 4, :, d_ % 4] = r
+    for a, b in zip(devs, expect):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
+def test_batched_commit_device_positions(dev):
+    """Several requests with their own page tables in one launch."""
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(5)
+    layers, pool, ps, h, d = 3, 64, 16, 8, 64
+    cpu = [_rand(gen, (pool, 2, ps, h, d), torch.bfloat16) for _ in range(layers)]
+    perm = torch.randperm(pool, generator=gen).to(torch.int32)
+    indptr = torch.tensor([0, 20, 41, 64], dtype=torch.int32)
+    prefixes = [300, 17, 320]
+    nodes = [(0, 2, 5), (1, 3), (0, 1, 2, 3)]
+    req, src, dst = [], [], []
+    for b, (p, ns) in enumerate(zip(prefixes, nodes)):
+        for i, n in enumerate(ns):
+            req.append(b)
+            src.append(p + n)
+            dst.append(p + i)
+    devs = [t.to(dev) for t in cpu]
+    kv.commit_paged(
+        devs, torch.tensor(src, device=dev), torch.tensor(dst, device=dev), kv_indptr=indptr.to(dev),
+        kv_indices=perm.to(dev), item_req=torch.tensor(req, dtype=torch.int32, device=dev),
+    )
+    torch.cuda.synchronize()
+    expect = [bits16(t).copy() for t in cpu]
+    for b, (p, ns) in enumerate(zip(prefixes, nodes)):
+        pt = perm[int(indptr[b]) : int(indptr[b + 1])].tolist()
+        ref.commit(expect, p, ns, pt)
+    for a, e in zip(devs, expect):
+        np.testing.assert_array_equal(bits16(a), e)
+
+
+def test_append_token_pool_set_kv_buffer(dev):
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(6)
+    layers, slots, h, d = 4, 256, 8, 64
+    k_cpu = [_rand(gen, (slots, h, d), torch.float16) for _ in range(layers)]
+    v_cpu = [_rand(gen, (slots, h, d), torch.float16) for _ in range(layers)]
+    rows_k = [_rand(gen, (9, h, d), torch.float16) for _ in range(layers)]
+    rows_v = [_rand(gen, (9, h, d), torch.float16) for _ in range(layers)]
+    loc = torch.randperm(slots, generator=gen)[:9]
+    k_dev = [t.to(dev) for t in k_cpu]
+    v_dev = [t.to(dev) for t in v_cpu]
+    kv.append_token_pool(k_dev, v_dev, [t.to(dev) for t in rows_k], [t.to(dev) for t in rows_v], loc.to(dev))
+    torch.cuda.synchronize()
+    k_np = [bits16(t).copy() for t in k_cpu]
+    v_np = [bits16(t).copy() for t in v_cpu]
+    ref.set_kv(k_np, v_np, loc.tolist(), [bits16(t) for t in rows_k], [bits16(t) for t in rows_v])
+    for a, b in zip(k_dev + v_dev, k_np + v_np):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
+def test_kv_ops_reject_cpu_tensors():
+    kv = pkg("kv_ops")
+    k = torch.zeros(4, 1, 8, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="HIP device"):
+        kv.move_slots([k], [k], torch.tensor([1]), torch.tensor([0]))

@@ -1,0 +1,275 @@
+"""Ancestor-masked paged tree attention vs the oracle's closed form.
+
+Tolerance: 2e-3 absolute on O and LSE (fp16 / bf16), the bound the path is
+specified with.  V is always drawn as N(0,1) * 0.1 (the configs' scale), which
+keeps |O| below ~0.5 where one bf16 output rounding stays under 2e-3; Q and K
+vary in scale.  Cases are built so that a wrong mask bit, page or split merge
+moves the output by far more than the tolerance: short prefixes (the tree keys
+carry a large share of the softmax mass), and long prefixes whose keys are
+pushed far below the tree keys ("dominant tree"), so every query's output is
+the softmax over exactly its visible ancestors.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import pkg
+from oracle import attention as oatt
+from oracle import paged_kv as ref
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-3
+
+
+def _routes(gen, k, depth, share):
+    routes = []
+    for r in range(k):
+        if routes and share:
+            keep = int(torch.randint(0, depth, (1,), generator=gen))
+            base = list(routes[-1][:keep])
+        else:
+            base = []
+        while len(base) < depth:
+            base.append(int(torch.randint(0, 128256, (1,), generator=gen)))
+        routes.append(tuple(base))
+    return routes
+
+
+def _build(dev, *, seed, prefix_len, routes, hq=32, hkv=8, d=128, ps=16, dtype=torch.float16, spare_pages=7,
+           scale=1.0, dominant_tree=False, permute=True):
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(seed)
+    spec, route_nodes = ffv.build_deduplicated_tree_spec_from_paths(
+        paths=routes, prefix_len=prefix_len, page_size=ps, device=dev
+    )
+    n = spec.node_count
+    kv_len = prefix_len + n
+    pages = math.ceil(kv_len / ps)
+    pool = pages + spare_pages
+    order = torch.randperm(pool, generator=gen)[:pages] if permute else torch.arange(pages)
+    kv = torch.randn((pool, 2, ps, hkv, d), generator=gen) * scale
+    kv[:, 1] = torch.randn((pool, ps, hkv, d), generator=gen) * 0.1
+    q = torch.randn((n, hq, d), generator=gen) * scale
+    if dominant_tree:
+        # All queries near u; prefix keys near -u, tree keys near +u.  With
+        # |u| = 12 a prefix key scores ~25 (natural log) below a tree key, so
+        # 16k prefix keys hold < 1e-6 of the softmax mass.
+        u = torch.randn(d, generator=gen)
+        u = u / u.norm() * 12.0
+        q = u + 0.3 * torch.randn((n, hq, d), generator=gen)
+        flat_k = kv[order, 0].reshape(pages * ps, hkv, d)
+        flat_k[:prefix_len] = -u + 0.3 * torch.randn((prefix_len, hkv, d), generator=gen)
+        flat_k[prefix_len:kv_len] = u + 0.3 * torch.randn((n, hkv, d), generator=gen)
+        kv[order, 0] = flat_k.reshape(pages, ps, hkv, d)
+    kv = kv.to(dtype)
+    q = q.to(dtype)
+    _, parents, _, _ = ref.dedup_tree(routes)
+    mask = ref.ancestor_mask(parents, prefix_len)
+    return dict(spec=spec, q=q, kv=kv, order=order.to(torch.int32), pages=pages, kv_len=kv_len, n=n, mask=mask,
+                hq=hq, hkv=hkv, d=d, ps=ps, dtype=dtype, route_nodes=route_nodes)
+
+
+def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL):
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    ws = torch.empty(128 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    if split_target is not None:
+        w.split_target_items = split_target
+    last = ffv.last_page_len(c["kv_len"], c["ps"])
+    mask_kw = (
+        {"packed_custom_mask": ffv.packbits(c["spec"].bool_mask, bitorder="little")}
+        if use_packed else {"custom_mask": c["spec"].bool_mask}
+    )
+    w.plan(
+        torch.tensor([0, c["n"]], dtype=torch.int32, device=dev),
+        torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev),
+        c["order"].to(dev),
+        torch.tensor([last], dtype=torch.int32, device=dev),
+        c["hq"], c["hkv"], c["d"], c["ps"], causal=False, pos_encoding_mode="NONE",
+        q_data_type=c["dtype"], kv_data_type=c["dtype"], **mask_kw,
+    )
+    out, lse = w.run(c["q"].to(dev), c["kv"].to(dev), return_lse=True)
+    torch.cuda.synchronize()
+    ro, rl = oatt.masked_attention(
+        c["q"].float().numpy().astype(np.float64), c["kv"].float().numpy().astype(np.float64),
+        [0, c["n"]], [0, c["pages"]], c["order"].tolist(), [last], masks=[c["mask"]],
+    )
+    o = out.float().cpu().numpy()
+    l = lse.cpu().numpy()
+    err_o = float(np.abs(o - ro).max())
+    err_l = float(np.abs(l - rl).max())
+    assert err_o <= atol, f"max |O - ref| = {err_o}"
+    assert err_l <= atol, f"max |lse - ref| = {err_l}"
+    return w, o, ro
+
+
+@pytest.mark.parametrize("prefix_len", [0, 1, 5, 16, 61, 64, 100, 257])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_tree_short_prefix(dev, prefix_len, dtype):
+    gen = torch.Generator().manual_seed(prefix_len)
+    routes = _routes(gen, 3, 4, share=True)
+    c = _build(dev, seed=10 + prefix_len, prefix_len=prefix_len, routes=routes, dtype=dtype)
+    _run_and_check(dev, c)
+    c = _build(dev, seed=20 + prefix_len, prefix_len=prefix_len, routes=routes, dtype=dtype, dominant_tree=True)
+    _run_and_check(dev, c)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_config2_geometry_4096_prefix_no_shared_prefix(dev, dtype):
+    """8B attention geometry, prefix 4096 in permuted pages, k=3 d=4 (12 nodes)."""
+    gen = torch.Generator().manual_seed(0)
+    routes = _routes(gen, 3, 4, share=False)
+    c = _build(dev, seed=0, prefix_len=4096, routes=routes, dtype=dtype, scale=0.1, spare_pages=300)
+    assert c["n"] == 12
+    _run_and_check(dev, c)
+    c = _build(dev, seed=1, prefix_len=4096, routes=routes, dtype=dtype, dominant_tree=True, spare_pages=300)
+    _run_and_check(dev, c)
+
+
+@pytest.mark.parametrize("split_target", [1, 64, 512, 4096])
+def test_forest_16k_prefix_dominant_tree_all_split_levels(dev, split_target):
+    """Forest of 9 routes (shared prefixes, <= 36 nodes) over a 16k prefix; the
+    tree keys dominate so mask, paging and split-merge errors are visible."""
+    gen = torch.Generator().manual_seed(3)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=3, prefix_len=16384, routes=routes, dominant_tree=True, spare_pages=50)
+    assert c["n"] <= 36
+    w, o, ro = _run_and_check(dev, c, split_target=split_target)
+    plan = w.current_plan
+    if split_target == 1:
+        assert plan.num_merge == 0
+    if split_target >= 512:
+        assert plan.num_merge > 0
+
+
+def test_forest_16k_unit_scale(dev):
+    gen = torch.Generator().manual_seed(4)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=4, prefix_len=16384, routes=routes, spare_pages=11)
+    _run_and_check(dev, c)
+
+
+def test_packed_mask_little_bit_order(dev):
+    gen = torch.Generator().manual_seed(5)
+    routes = _routes(gen, 3, 4, share=True)
+    c = _build(dev, seed=5, prefix_len=77, routes=routes)
+    _run_and_check(dev, c, use_packed=True)
+
+
+def test_identical_routes_and_single_node(dev):
+    c = _build(dev, seed=6, prefix_len=33, routes=[(7, 8), (7, 8)])
+    assert c["n"] == 2
+    _run_and_check(dev, c)
+    c = _build(dev, seed=7, prefix_len=500, routes=[(9,)], dominant_tree=True)
+    _run_and_check(dev, c)
+
+
+@pytest.mark.parametrize("hq,hkv,d,ps", [(32, 8, 64, 16), (32, 8, 128, 64), (8, 8, 128, 16), (16, 2, 64, 32)])
+def test_geometry_variants(dev, hq, hkv, d, ps):
+    gen = torch.Generator().manual_seed(hq + d + ps)
+    routes = _routes(gen, 3, 4, share=True)
+    c = _build(dev, seed=8, prefix_len=300, routes=routes, hq=hq, hkv=hkv, d=d, ps=ps)
+    _run_and_check(dev, c)
+    c = _build(dev, seed=9, prefix_len=3000, routes=routes, hq=hq, hkv=hkv, d=d, ps=ps, dominant_tree=True)
+    _run_and_check(dev, c)
+
+
+def test_batched_ragged_requests_mixed_masks(dev):
+    """Several requests (ragged prefixes, scattered pages) in one plan: tree
+    masks per request, compared against the oracle request by request."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(11)
+    hq, hkv, d, ps = 32, 8, 128, 16
+    prefixes = [1024, 37, 5000, 16, 2048]
+    specs, qs, masks = [], [], []
+    pages_per, lasts, kv_lens = [], [], []
+    for i, p in enumerate(prefixes):
+        routes = _routes(gen, 3, 4, share=bool(i % 2))
+        spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=routes, prefix_len=p, page_size=ps, device=dev)
+        _, parents, _, _ = ref.dedup_tree(routes)
+        specs.append(spec)
+        masks.append(ref.ancestor_mask(parents, p))
+        qs.append(torch.randn((spec.node_count, hq, d), generator=gen))
+        kv_lens.append(p + spec.node_count)
+        pages_per.append(math.ceil(kv_lens[-1] / ps))
+        lasts.append(ffv.last_page_len(kv_lens[-1], ps))
+    total_pages = sum(pages_per)
+    pool = total_pages + 40
+    perm = torch.randperm(pool, generator=gen)[:total_pages].to(torch.int32)
+    kv = torch.randn((pool, 2, ps, hkv, d), generator=gen)
+    kv[:, 1] *= 0.1
+    kv = kv.to(torch.float16)
+    q = torch.cat(qs).to(torch.float16)
+    qo = [0]
+    for s in specs:
+        qo.append(qo[-1] + s.node_count)
+    kvp = [0]
+    for p in pages_per:
+        kvp.append(kvp[-1] + p)
+    flat_mask = torch.cat([torch.from_numpy(m.reshape(-1)) for m in masks]).to(dev)
+    ws = torch.empty(64 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32, device=dev), torch.tensor(kvp, dtype=torch.int32, device=dev),
+           perm.to(dev), torch.tensor(lasts, dtype=torch.int32, device=dev), hq, hkv, d, ps,
+           custom_mask=flat_mask, q_data_type=torch.float16)
+    out, lse = w.run(q.to(dev), kv.to(dev), return_lse=True)
+    torch.cuda.synchronize()
+    ro, rl = oatt.masked_attention(q.float().numpy().astype(np.float64), kv.float().numpy().astype(np.float64),
+                                   qo, kvp, perm.tolist(), lasts, masks=masks)
+    assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+    assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL
+
+
+def test_causal_and_unmasked_modes(dev):
+    ta = pkg("tree_attention")
+    gen = torch.Generator().manual_seed(12)
+    hq, hkv, d, ps = 16, 4, 128, 16
+    qo_len, kv_len = 20, 700
+    pages = math.ceil(kv_len / ps)
+    kv = torch.randn((pages + 3, 2, ps, hkv, d), generator=gen)
+    kv[:, 1] *= 0.1
+    kv = kv.to(torch.float16)
+    q = torch.randn((qo_len, hq, d), generator=gen).to(torch.float16)
+    perm = torch.randperm(pages + 3, generator=gen)[:pages].to(torch.int32)
+    last = kv_len - (pages - 1) * ps
+    ws = torch.empty(16 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    for causal in (False, True):
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        w.plan(torch.tensor([0, qo_len], dtype=torch.int32), torch.tensor([0, pages], dtype=torch.int32),
+               perm.to(dev), torch.tensor([last], dtype=torch.int32), hq, hkv, d, ps, causal=causal)
+        out, lse = w.run(q.to(dev), kv.to(dev), return_lse=True)
+        torch.cuda.synchronize()
+        ro, rl = oatt.masked_attention(q.float().numpy().astype(np.float64), kv.float().numpy().astype(np.float64),
+                                       [0, qo_len], [0, pages], perm.tolist(), [last], causal=causal)
+        assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+        assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL
+
+
+def test_reference_plan_helper_and_kv_tuple(dev):
+    """plan_prefill_wrapper's keyword ladder drives the wrapper; run accepts a
+    (K, V) tuple of [pages, page_size, Hkv, D] caches."""
+    ffv = pkg("flashinfer_full_verify")
+    from types import SimpleNamespace
+
+    gen = torch.Generator().manual_seed(13)
+    routes = _routes(gen, 3, 4, share=True)
+    c = _build(dev, seed=13, prefix_len=160, routes=routes, permute=False, spare_pages=0)
+    args = SimpleNamespace(workspace_mb=8, device=dev, page_size=16, use_packed_custom_mask=False)
+    cfg = SimpleNamespace(num_attention_heads=32, num_key_value_heads=8, head_dim=128, hidden_size=4096)
+    w = ffv.make_prefill_wrapper(args=args)
+    ffv.plan_prefill_wrapper(w, c["spec"], args=args, config=cfg, dtype=torch.float16)
+    kvd = c["kv"].to(dev)
+    out = ffv.first_tensor(w.run(c["q"].to(dev), kvd))
+    out2 = w.run(c["q"].to(dev), (kvd[:, 0], kvd[:, 1]))
+    torch.cuda.synchronize()
+    ro, _ = oatt.masked_attention(c["q"].float().numpy().astype(np.float64), c["kv"].float().numpy().astype(np.float64),
+                                  [0, c["n"]], [0, c["pages"]], list(range(c["pages"])), [ffv.last_page_len(c["kv_len"], 16)],
+                                  masks=[c["mask"]])
+    assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+    assert torch.equal(out, out2)

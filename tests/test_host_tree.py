@@ -1,0 +1,107 @@
+"""Host-side tree construction of the product (trie, TreeSpec, bitmasks, plan
+helpers) against the reference literals and the oracle.  CPU only."""
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import pkg
+from oracle import paged_kv as ref
+
+
+def test_dedup_literals():
+    # tests/test_tree_dedup.py:6-35
+    ffv = pkg("flashinfer_full_verify")
+    tokens, parents, depths, routes = ffv.build_deduplicated_path_tree_tokens(
+        [(10, 20, 30, 40), (10, 20, 31, 41), (11, 21, 32, 42)], device="cpu"
+    )
+    assert tokens.tolist() == [10, 20, 30, 40, 31, 41, 11, 21, 32, 42]
+    assert parents == [-1, 0, 1, 2, 1, 4, -1, 6, 7, 8]
+    assert depths.tolist() == [0, 1, 2, 3, 2, 3, 0, 1, 2, 3]
+    assert routes == [[0, 1, 2, 3], [0, 1, 4, 5], [6, 7, 8, 9]]
+    tokens, parents, depths, routes = ffv.build_deduplicated_path_tree_tokens([(7, 8), (7, 8)], device="cpu")
+    assert tokens.tolist() == [7, 8] and parents == [-1, 0] and routes == [[0, 1], [0, 1]]
+
+
+@pytest.mark.parametrize("bad", [[], [(1, 2), (3,)], [()]])
+def test_dedup_rejects_bad_paths(bad):
+    ffv = pkg("flashinfer_full_verify")
+    with pytest.raises(ValueError):
+        ffv.build_deduplicated_path_tree_tokens(bad, device="cpu")
+
+
+def test_tree_spec_matches_oracle_mask_and_metadata():
+    ffv = pkg("flashinfer_full_verify")
+    rng = np.random.default_rng(0)
+    for trial in range(20):
+        k = int(rng.integers(1, 10))
+        depth = int(rng.integers(1, 5))
+        paths = [tuple(int(x) for x in rng.integers(0, 3, size=depth)) for _ in range(k)]
+        prefix = int(rng.integers(0, 70))
+        spec, routes = ffv.build_deduplicated_tree_spec_from_paths(paths=paths, prefix_len=prefix, page_size=16,
+                                                                   device="cpu")
+        tokens, parents, _, oroutes = ref.dedup_tree(paths)
+        mask = ref.ancestor_mask(parents, prefix)
+        assert routes == oroutes
+        assert spec.bool_mask.numpy().tolist() == mask.reshape(-1).tolist()
+        assert spec.packed_mask.numpy().tolist() == ref.packbits(mask).tolist()
+        n = len(tokens)
+        assert spec.kv_len == prefix + n and spec.node_count == n
+        assert spec.total_pages == (prefix + n + 15) // 16
+        assert spec.kv_last_page_len.tolist() == [ffv.last_page_len(prefix + n, 16)]
+        assert spec.kv_indices.tolist() == list(range(spec.total_pages))
+        # compact bitmask agrees with the dense mask's tree columns
+        bits = spec.tree_mask.numpy().astype(np.uint64)
+        for i in range(n):
+            row = [(int(bits[i]) >> j) & 1 for j in range(n)]
+            assert row == mask[i, prefix:].astype(int).tolist()
+
+
+def test_undeduplicated_tree_spec():
+    ffv = pkg("flashinfer_full_verify")
+    spec = ffv.build_tree_spec_from_paths(paths=[(1, 2), (1, 3)], prefix_len=3, page_size=4, device="cpu")
+    assert spec.node_count == 4 and spec.parent_indices == [-1, 0, -1, 2]
+
+
+def test_tree_mask_from_dense_window_detection():
+    ta = pkg("tree_attention")
+    _, parents, _, _ = ref.dedup_tree([(1, 2, 3), (1, 5, 6), (9, 9, 9)])
+    mask = torch.from_numpy(ref.ancestor_mask(parents, 40))
+    col0, bits = ta.tree_mask_from_dense(mask)
+    assert col0 == 40
+    for i in range(mask.shape[0]):
+        assert [(int(bits[i]) >> j) & 1 for j in range(mask.shape[1] - 40)] == mask[i, 40:].int().tolist()
+    # A mask whose hidden region spans more than 64 columns is not a tree window.
+    wide = torch.ones((2, 200), dtype=torch.bool)
+    wide[0, 10] = False
+    assert ta.tree_mask_from_dense(wide) is None
+    # all-visible mask
+    col0, bits = ta.tree_mask_from_dense(torch.ones((3, 50), dtype=torch.bool))
+    assert col0 == 50
+
+
+def test_packbits_and_unpack_roundtrip():
+    ffv = pkg("flashinfer_full_verify")
+    ta = pkg("tree_attention")
+    rng = np.random.default_rng(1)
+    x = torch.from_numpy(rng.random(101) > 0.4)
+    assert ffv.packbits(x).tolist() == np.packbits(x.numpy()).tolist()
+    little = ffv.packbits(x, bitorder="little")
+    assert ta.unpack_bits_little(little, 101).tolist() == x.tolist()
+
+
+def test_ancestor_bitmasks_arbitrary_order():
+    ffv = pkg("flashinfer_full_verify")
+    # parent after child: bitmask still the ancestor closure
+    parents = [2, -1, 1]
+    bits = ffv.ancestor_bitmasks(parents)
+    assert bits == [0b111, 0b010, 0b110]
+
+
+def test_plan_argument_validation_without_gpu():
+    ta = pkg("tree_attention")
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "NHD")
+    with pytest.raises(RuntimeError, match="HIP device"):
+        w.plan(torch.tensor([0, 1]), torch.tensor([0, 1]), torch.tensor([0]), torch.tensor([1]), 4, 2, 64, 16)
+    with pytest.raises(NotImplementedError):
+        ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "HND")

@@ -1,0 +1,369 @@
+"""Pin the oracle: reference test literals, closed forms, brute force and
+library routines that a plausible mistake in the oracle would fail."""
+
+import hashlib
+import itertools
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as oatt
+from oracle import paged_kv as ref
+from oracle import scoring as osc
+
+
+# ---------------------------------------------------------------- a1 metadata
+def _slot_path(page_ids, length, page_size=16):
+    slots = [p * page_size + o for p in page_ids for o in range(page_size)]
+    return slots[:length]
+
+
+def test_metadata_reference_literals():
+    # tests/test_paged_attention_metadata.py:24-42
+    lengths = [1, 15, 16, 17, 31, 32]
+    paths = [_slot_path([11 + 3 * i, 31 + 5 * i], n) for i, n in enumerate(lengths)]
+    md = ref.paged_metadata(paths, 16)
+    counts = [(n + 15) // 16 for n in lengths]
+    assert md.kv_indptr == list(itertools.accumulate([0] + counts))
+    assert md.kv_last_page_len == [1, 15, 16, 1, 15, 16]
+    assert md.seq_lens == lengths
+    assert md.token_index_count == sum(lengths)
+    assert len(md.kv_page_indices) == sum(counts)
+    assert md.layout_ok
+    # page ids are the physical pages of each path
+    flat = [p for i, n in enumerate(lengths) for p in [11 + 3 * i, 31 + 5 * i][: counts[i]]]
+    assert md.kv_page_indices == flat
+
+
+def test_metadata_long_prefix_literal():
+    # tests/test_paged_attention_metadata.py:45-52
+    md = ref.paged_metadata([_slot_path(list(range(100, 612)), 8192)], 16)
+    assert md.token_index_count == 8192 and len(md.kv_page_indices) == 512
+    assert md.kv_indptr == [0, 512] and md.kv_last_page_len == [16]
+
+
+@pytest.mark.parametrize("path", [[161, 162, 163], [160, 161, 165], list(range(160, 176)) + [193]])
+def test_metadata_rejects_invalid_layouts(path):
+    # tests/test_paged_attention_metadata.py:55-67
+    assert not ref.paged_metadata([path], 16).layout_ok
+
+
+def test_metadata_errors():
+    with pytest.raises(ValueError):
+        ref.paged_metadata([[1]], 0)
+    with pytest.raises(ValueError):
+        ref.paged_metadata([], 16)
+    with pytest.raises(ValueError):
+        ref.paged_metadata([[]], 16)
+
+
+# ---------------------------------------------------------------- a2 dedup
+def test_dedup_reference_literals():
+    # tests/test_tree_dedup.py:6-25
+    tokens, parents, depths, routes = ref.dedup_tree([(10, 20, 30, 40), (10, 20, 31, 41), (11, 21, 32, 42)])
+    assert tokens == [10, 20, 30, 40, 31, 41, 11, 21, 32, 42]
+    assert parents == [-1, 0, 1, 2, 1, 4, -1, 6, 7, 8]
+    assert depths == [0, 1, 2, 3, 2, 3, 0, 1, 2, 3]
+    assert routes == [[0, 1, 2, 3], [0, 1, 4, 5], [6, 7, 8, 9]]
+
+
+def test_dedup_identical_routes_literal():
+    # tests/test_tree_dedup.py:28-35
+    tokens, parents, depths, routes = ref.dedup_tree([(7, 8), (7, 8)])
+    assert tokens == [7, 8] and parents == [-1, 0] and depths == [0, 1] and routes == [[0, 1], [0, 1]]
+
+
+def test_dedup_brute_force_unique_prefixes():
+    rng = np.random.default_rng(0)
+    for _ in range(50):
+        paths = [tuple(int(x) for x in rng.integers(0, 3, size=4)) for _ in range(9)]
+        tokens, parents, depths, routes = ref.dedup_tree(paths)
+        prefixes = {p[: i + 1] for p in paths for i in range(4)}
+        assert len(tokens) == len(prefixes)
+        for path, nodes in zip(paths, routes):
+            for i, node in enumerate(nodes):
+                # reconstruct the prefix through parents
+                chain, cur = [], node
+                while cur >= 0:
+                    chain.append(tokens[cur])
+                    cur = parents[cur]
+                assert tuple(reversed(chain)) == path[: i + 1]
+                assert depths[node] == i
+        # insertion order: a node's parent precedes it
+        assert all(p < i for i, p in enumerate(parents))
+        # commit aliasing argument: node_ids[j] < depth implies node_ids[j] == j
+        for nodes in routes:
+            for j, nid in enumerate(nodes):
+                if nid < 4:
+                    assert nid == j
+
+
+# ---------------------------------------------------------------- a3 mask
+def test_ancestor_mask_closed_form():
+    _, parents, _, _ = ref.dedup_tree([(10, 20, 30, 40), (10, 20, 31, 41), (11, 21, 32, 42)])
+    m = ref.ancestor_mask(parents, 5)
+    assert m.shape == (10, 15)
+    assert m[:, :5].all()
+    tree = m[:, 5:]
+    # node 5 (41) sees 0, 1, 4, 5; node 6 (11) sees only itself
+    assert np.flatnonzero(tree[5]).tolist() == [0, 1, 4, 5]
+    assert np.flatnonzero(tree[6]).tolist() == [6]
+    # reflexive, and transitive: a visible column's own visible set is a subset
+    for i in range(10):
+        assert tree[i, i]
+        for j in np.flatnonzero(tree[i]):
+            assert (tree[j] <= tree[i]).all()
+
+
+def test_packbits_matches_numpy_orders():
+    rng = np.random.default_rng(1)
+    x = rng.random(77) > 0.5
+    assert ref.packbits(x).tolist() == np.packbits(x).tolist()
+    little = ref.packbits(x, "little")
+    assert np.unpackbits(little, bitorder="little")[:77].astype(bool).tolist() == x.tolist()
+
+
+# ---------------------------------------------------------------- a4 attention
+def _sdpa_reference(q, k, v, mask, scale):
+    qt = torch.from_numpy(q).permute(1, 0, 2)  # [H, n, D]
+    kt = torch.from_numpy(k).permute(1, 0, 2)
+    vt = torch.from_numpy(v).permute(1, 0, 2)
+    out = torch.nn.functional.scaled_dot_product_attention(
+        qt, kt, vt, attn_mask=torch.from_numpy(mask)[None], scale=scale
+    )
+    return out.permute(1, 0, 2).numpy()
+
+
+def test_attention_matches_torch_sdpa_and_is_page_permutation_invariant():
+    rng = np.random.default_rng(2)
+    hq, hkv, d, ps = 8, 2, 32, 4
+    prefix = 13
+    _, parents, _, _ = ref.dedup_tree([(1, 2, 3), (1, 4, 5)])
+    n = len(parents)
+    kv_len = prefix + n
+    pages = math.ceil(kv_len / ps)
+    kv = rng.standard_normal((pages + 3, 2, ps, hkv, d))
+    q = rng.standard_normal((n, hq, d))
+    mask = ref.ancestor_mask(parents, prefix)
+    last = kv_len - (pages - 1) * ps
+    perm = list(rng.permutation(pages + 3)[:pages])
+    o1, l1 = oatt.masked_attention(q, kv, [0, n], [0, pages], perm, [last], masks=[mask])
+    # contiguous copy of the same pages
+    kv2 = kv[perm]
+    o2, l2 = oatt.masked_attention(q, kv2, [0, n], [0, pages], list(range(pages)), [last], masks=[mask])
+    np.testing.assert_allclose(o1, o2, atol=1e-12)
+    np.testing.assert_allclose(l1, l2, atol=1e-12)
+    k = kv2[:, 0].reshape(-1, hkv, d)[:kv_len].repeat(hq // hkv, axis=1)
+    v = kv2[:, 1].reshape(-1, hkv, d)[:kv_len].repeat(hq // hkv, axis=1)
+    # the GQA repeat must map q head h to kv head h // group
+    k = np.concatenate([np.repeat(kv2[:, 0].reshape(-1, hkv, d)[:kv_len, h : h + 1], hq // hkv, axis=1)
+                        for h in range(hkv)], axis=1)
+    v = np.concatenate([np.repeat(kv2[:, 1].reshape(-1, hkv, d)[:kv_len, h : h + 1], hq // hkv, axis=1)
+                        for h in range(hkv)], axis=1)
+    sd = _sdpa_reference(q, k, v, mask, 1 / math.sqrt(d))
+    np.testing.assert_allclose(o1, sd, atol=1e-10)
+    # lse closed form
+    s = np.einsum("nhd,khd->nhk", q, k) / math.sqrt(d)
+    s = np.where(mask[:, None, :], s, -np.inf)
+    np.testing.assert_allclose(l1, np.log(np.exp(s).sum(-1)), atol=1e-10)
+
+
+def test_attention_special_cases():
+    rng = np.random.default_rng(3)
+    hq, hkv, d, ps = 4, 4, 16, 8
+    kv = rng.standard_normal((5, 2, ps, hkv, d))
+    # uniform V rows -> output equals that row regardless of scores
+    kv[:, 1] = rng.standard_normal((hkv, d))[None, None]
+    q = rng.standard_normal((3, hq, d))
+    o, _ = oatt.masked_attention(q, kv, [0, 3], [0, 5], [0, 1, 2, 3, 4], [8])
+    np.testing.assert_allclose(o, np.broadcast_to(kv[0, 1, 0][None], o.shape), atol=1e-12)
+    # one visible key -> output is that key's V, lse is its score
+    mask = np.zeros((1, 40), dtype=bool)
+    mask[0, 17] = True
+    kv = rng.standard_normal((5, 2, ps, hkv, d))
+    q1 = rng.standard_normal((1, hq, d))
+    o, l = oatt.masked_attention(q1, kv, [0, 1], [0, 5], [0, 1, 2, 3, 4], [8], masks=[mask])
+    np.testing.assert_allclose(o[0], kv[2, 1, 1], atol=1e-12)
+    np.testing.assert_allclose(l[0], (q1[0] * kv[2, 0, 1]).sum(-1) / 4.0, atol=1e-12)
+    # fully masked row
+    o, l = oatt.masked_attention(q1, kv, [0, 1], [0, 5], [0, 1, 2, 3, 4], [8], masks=[np.zeros((1, 40), bool)])
+    assert (o == 0).all() and np.isneginf(l).all()
+    # causal: last query sees everything, first sees kv_len - qo_len + 1 keys
+    qc = rng.standard_normal((2, hq, d))
+    oc, _ = oatt.masked_attention(qc, kv, [0, 2], [0, 5], [0, 1, 2, 3, 4], [8], causal=True)
+    om, _ = oatt.masked_attention(qc, kv, [0, 2], [0, 5], [0, 1, 2, 3, 4], [8])
+    np.testing.assert_allclose(oc[1], om[1], atol=1e-12)
+    m0 = np.zeros((2, 40), bool)
+    m0[0, :39] = True
+    m0[1] = True
+    o0, _ = oatt.masked_attention(qc, kv, [0, 2], [0, 5], [0, 1, 2, 3, 4], [8], masks=[m0])
+    np.testing.assert_allclose(oc, o0, atol=1e-12)
+
+
+# ---------------------------------------------------------------- a5/a6/a7
+def _commit_cache():
+    # tests/test_target_kv_commit.py:13-25
+    cache = np.zeros((2, 2, 4, 1, 1), dtype=np.float32)
+    for pos in range(8):
+        page, off = divmod(pos, 4)
+        cache[page, 0, off, 0, 0] = 100 + pos
+        cache[page, 1, off, 0, 0] = 200 + pos
+    return cache
+
+
+def test_commit_reference_literals():
+    # tests/test_target_kv_commit.py:28-45
+    cache = _commit_cache()
+    ref.commit([cache], 3, (0, 2))
+    assert cache[0, 0, 3, 0, 0] == 103 and cache[1, 0, 0, 0, 0] == 105
+    assert cache[0, 1, 3, 0, 0] == 203 and cache[1, 1, 0, 0, 0] == 205
+
+
+def test_commit_clone_semantics_brute_force():
+    rng = np.random.default_rng(4)
+    for _ in range(20):
+        cache = rng.standard_normal((6, 2, 4, 1, 2))
+        nodes = sorted(rng.choice(10, size=3, replace=False).tolist())
+        before = cache.copy()
+        ref.commit([cache], 5, nodes)
+        for i, nid in enumerate(nodes):
+            s, d_ = 5 + nid, 5 + i
+            np.testing.assert_array_equal(cache[d_ // 4, :, d_ % 4], before[s // 4, :, s % 4])
+
+
+def test_capacity_growth_literal():
+    # tests/test_target_kv_commit.py:48-55
+    cache = _commit_cache()
+    (grown,) = ref.grow_capacity([cache], 4)
+    assert grown.shape[0] == 4 and np.array_equal(grown[:2], cache) and not grown[2:].any()
+
+
+def test_prefix_to_paged_literal():
+    # tests/test_target_kv_commit.py:58-73
+    key = np.arange(5, dtype=np.float32).reshape(1, 1, 5, 1)
+    value = (100 + np.arange(5, dtype=np.float32)).reshape(1, 1, 5, 1)
+    cache = ref.prefix_to_paged(key, value, 5, 2, 4)
+    assert [cache[p // 4, 0, p % 4, 0, 0] for p in range(5)] == [0, 1, 2, 3, 4]
+    assert [cache[p // 4, 1, p % 4, 0, 0] for p in range(5)] == [100, 101, 102, 103, 104]
+
+
+# ---------------------------------------------------------------- a9 / a13
+def test_move_kv_reference_fake_semantics():
+    # tests/test_tail_page_cow.py:9-16, :77-79
+    values = [np.arange(512, dtype=np.float32)]
+    ref.move_kv(values, [np.zeros(512)], [40, 41, 42], [0, 1, 2])
+    assert values[0][40:43].tolist() == [0.0, 1.0, 2.0]
+
+
+def test_prune_reference_literals():
+    # tests/test_tail_page_cow.py:241-277: prefix [0, 1, 40] after promotion,
+    # retained route 2 [0, 1, 40, 41], owned {0, 10, 11} -> free [11] (slot 44).
+    released, owned = ref.prune({0, 10, 11}, [0, 1, 40], [[0, 1, 40, 41]], 4)
+    assert released == [11] and owned == {0, 10}
+    assert [p * 4 for p in released] == [44]
+    # tests/test_tail_page_cow.py:280-293
+    released, owned = ref.prune({0, 10, 11}, [0, 1], [[0, 1, 40]], 4)
+    assert released == [11] and owned == {0, 10}
+    assert ref.prune(owned, [0, 1], [[0, 1, 40]], 4)[0] == []
+
+
+def test_prune_brute_force_sorted_difference():
+    rng = np.random.default_rng(5)
+    for _ in range(30):
+        ps = int(rng.choice([1, 4, 16]))
+        owned = set(rng.choice(200, size=60, replace=False).tolist())
+        paths = []
+        for _ in range(3):
+            pages = rng.choice(200, size=4, replace=False)
+            length = int(rng.integers(1, 4 * ps + 1))
+            paths.append([int(pages[i // ps]) * ps + i % ps for i in range(length)])
+        released, left = ref.prune(owned, None, paths, ps)
+        live = {s // ps for p in paths for s in p}
+        assert released == sorted(owned - live) and left == owned & live
+
+
+def test_allocator_policy_brute_force():
+    ps = 4
+    a = ref.PagedAllocator(num_pages=20, page_size=ps)
+    assert a.alloc(8) == [4, 5, 6, 7, 8, 9, 10, 11]
+    a.free([9, 5, 40])
+    assert a.free_pages[:3] == [1, 2, 10]
+    # decode: request 0 continues slot 41 (seq 7 -> pre 6 not a boundary),
+    # request 1 opens a page (seq 5 -> pre 4 boundary)
+    out = a.alloc_decode([7, 5], [41, 99])
+    assert out == [42, 4]
+    # extend: prefix 6 -> 11 with last 45: slots 46, 47, then new pages
+    a2 = ref.PagedAllocator(num_pages=20, page_size=ps)
+    out = a2.alloc_extend([6, 0], [11, 3], [45, -1])
+    assert out == [46, 47, 4, 5, 6, 8, 9, 10]
+    # brute force: every extended slot sits at offset t % ps of its page
+    a3 = ref.PagedAllocator(num_pages=100, page_size=ps)
+    pre, seq = [3, 9, 0, 12], [10, 10, 5, 30]
+    last = [2 * ps + 2, 5 * ps + 0, -1, 7 * ps + 3]
+    slots = a3.alloc_extend(pre, seq, last)
+    k = 0
+    for p, s in zip(pre, seq):
+        for t in range(p, s):
+            assert slots[k] % ps == t % ps
+            k += 1
+
+
+# ---------------------------------------------------------------- a8 scoring
+def test_scoring_reference_literal():
+    # tests/test_target_kv_commit.py:76-103
+    prefix = np.array([0.0, 3.0, 0.0, 0.0])
+    verify = np.array([[0.0, 0.0, 4.0, 2.0], [0, 0, 0, 0], [0, 0, 0, 0]])
+    lps = osc.route_token_logprobs([(1, 2), (1, 3)], [[0, 1], [0, 2]], prefix, verify)
+    plp = float(torch.log_softmax(torch.tensor(prefix), -1)[1])
+    vlp = torch.log_softmax(torch.tensor(verify[0]), -1)
+    assert abs(sum(lps[0]) - (plp + float(vlp[2]))) < 1e-9
+    assert abs(sum(lps[1]) - (plp + float(vlp[3]))) < 1e-9
+
+
+def test_selection_literals():
+    # target_best tie-break, tests/test_target_kv_commit.py:128-147, :311-331
+    a = dict(route_id=9, selection_score=-1.0, draft_path_logprob=-2.0, token_ids=(11,))
+    b = dict(route_id=4, selection_score=-1.0, draft_path_logprob=-1.0, token_ids=(12,))
+    assert osc.select_best([a, b])["route_id"] == 4
+    c = dict(route_id=1, selection_score=-1.0, draft_path_logprob=-0.3, token_ids=(10, 11))
+    d = dict(route_id=2, selection_score=-1.0, draft_path_logprob=-2.0, token_ids=(20, 21))
+    assert osc.select_best([d, c])["route_id"] == 1
+    # identical scores: lowest route id wins
+    e = dict(route_id=3, selection_score=-1.0, draft_path_logprob=-1.0, token_ids=(1,))
+    f = dict(route_id=5, selection_score=-1.0, draft_path_logprob=-1.0, token_ids=(2,))
+    assert osc.select_best([f, e])["route_id"] == 3
+
+
+def test_sampling_draw_closed_form_and_order_independence():
+    # target_runtime.py:507-511 draw; tests/test_target_kv_commit.py:167-219
+    scores = [
+        dict(route_id=8, token_ids=(30, 31), selection_score=-1.0, draft_path_logprob=-0.8),
+        dict(route_id=2, token_ids=(10, 11), selection_score=-1.4, draft_path_logprob=-0.2),
+        dict(route_id=5, token_ids=(20, 21), selection_score=-0.7, draft_path_logprob=-0.5),
+    ]
+    sa, da = osc.sample_route(scores, 1234, 7)
+    sb, db = osc.sample_route(list(reversed(scores)), 1234, 7)
+    _, dn = osc.sample_route(scores, 1234, 8)
+    assert sa["token_ids"] == sb["token_ids"] and da == db and da != dn
+    bits = int.from_bytes(hashlib.sha256(b"atlas0709-target-route-sample-v1:1234:7").digest()[:8], "big")
+    assert da == (bits + 0.5) / 2.0**64
+    # inverse CDF over the canonical (token-sorted) order
+    ordered = sorted(scores, key=lambda s: s["token_ids"])
+    w = np.exp(np.array([s["selection_score"] for s in ordered]) - max(s["selection_score"] for s in ordered))
+    cdf = np.cumsum(w / w.sum())
+    assert ordered[int(np.searchsorted(cdf, da, side="right"))]["route_id"] == sa["route_id"]
+
+
+def test_truncation_literals():
+    # tests/test_target_kv_commit.py:345-367
+    assert osc.truncate_path((10, 11, 12, 13), (20, 21, 22, 23), 3, 11) == ((10, 11), (20, 21))
+    with pytest.raises(ValueError, match="must be positive"):
+        osc.truncate_path((10,), (20,), 0, None)
+
+
+def test_weights_normalised():
+    assert osc.normalise_weights([1.0, 3.0]) == (0.25, 0.75)
+    with pytest.raises(ValueError):
+        osc.normalise_weights([-1.0])
