@@ -30,6 +30,7 @@ constexpr int kThreads = kWaves * 64;
 constexpr int kTileKeys = 64;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleLog2 = 8.0f;
 
 struct AttnArgs {
   const char* q;
@@ -60,9 +61,16 @@ struct AttnArgs {
   int page_shift;
 };
 
+typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 half2v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+
 template <bool BF16>
 struct Mfma;
 
+// P is converted two values at a time; fp16 uses round-toward-zero packing
+// (one instruction), bf16 round-to-nearest-even.  The row sum of the
+// softmax is accumulated from the same packed values the P.V MFMA consumes.
 template <>
 struct Mfma<false> {
   typedef f16x8 frag;
@@ -72,6 +80,13 @@ struct Mfma<false> {
   static __device__ __forceinline__ uint16_t from_float(float x) {
     _Float16 h = static_cast<_Float16>(x);
     return __builtin_bit_cast(uint16_t, h);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(a, b));
+  }
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, packed), half2v{(_Float16)1.0f, (_Float16)1.0f}, acc,
+                                  false);
   }
 };
 
@@ -85,6 +100,13 @@ struct Mfma<true> {
     __bf16 h = static_cast<__bf16>(x);
     return __builtin_bit_cast(uint16_t, h);
   }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, bf16x2v{static_cast<__bf16>(a), static_cast<__bf16>(b)});
+  }
+  static __device__ __forceinline__ float sum2(uint32_t packed, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, packed),
+                                           bf16x2v{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
+  }
 };
 
 // Position inside a 32-key block of V^T at which key k (0..31) is stored.  The
@@ -95,30 +117,70 @@ __device__ __forceinline__ int vt_position(int k) {
   return ((k & 15) >> 2) * 8 + ((k >> 4) << 2) + (k & 3);
 }
 
-__device__ __forceinline__ float wave_max_across_groups(float v) {
-  v = fmaxf(v, __shfl_xor(v, 16));
-  v = fmaxf(v, __shfl_xor(v, 32));
-  return v;
+// Reductions across the four 16-lane rows of a wave (lanes l, l^16, l^32,
+// l^48) with the gfx950 row-swap permutes: swapping a register with itself
+// yields each lane's value and its partner's, so no selection is needed.
+__device__ __forceinline__ float xor32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
-
-__device__ __forceinline__ float wave_sum_across_groups(float v) {
-  v += __shfl_xor(v, 16);
-  v += __shfl_xor(v, 32);
-  return v;
+__device__ __forceinline__ float xor16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float wave_max_across_groups(float v) { return xor32_max(xor16_max(v)); }
+__device__ __forceinline__ float wave_sum_across_groups(float v) { return xor32_sum(xor16_sum(v)); }
 
-template <int D, bool BF16, int RT>
-__global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
+// V^T row d stores its 16-byte granules XOR-swizzled by vt_swizzle(d): the
+// eight rows one MFMA A-read touches per LDS cycle land in eight different
+// granules, and the writers (rows 8c + e, c = 0..15) collide at most 2-way.
+__device__ __forceinline__ int vt_swizzle(int d) { return (d ^ (d >> 3)) & 7; }
+
+// Page-table walk of one thread's keys: key (t + key0) clamped to the split's
+// last key, mapped to its physical page and in-page offset.
+struct PageWalk {
+  const int32_t* pages;
+  int page_size;
+  int page_shift;
+  int last_key;
+  int key0;
+
+  __device__ __forceinline__ int clamp(int t) const { return min(t + key0, last_key); }
+  __device__ __forceinline__ int page(int t) const {
+    const int p = clamp(t);
+    return pages[page_shift >= 0 ? (p >> page_shift) : (p / page_size)];
+  }
+  __device__ __forceinline__ const char* row(const char* base, int64_t page_stride, int64_t token_stride, int t,
+                                             int phys_page) const {
+    const int p = clamp(t);
+    const int off = page_shift >= 0 ? (p & (page_size - 1)) : (p % page_size);
+    return base + int64_t(phys_page) * page_stride + int64_t(off) * token_stride;
+  }
+};
+
+// NWC waves compute, each owning RT row tiles of 16 rows (tile = wave +
+// NWC * rt); all 4 waves load.  Rows beyond num_rows carry zero queries, so
+// every MFMA runs unconditionally.
+template <int D, bool BF16, int RT, int NWC>
+__global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(AttnArgs a) {
   typedef Mfma<BF16> M;
   typedef typename M::frag frag;
   constexpr int KS = D / 32;           // k-steps of the score MFMA
   constexpr int DT = D / 16;           // 16-dim output tiles
   constexpr int CH = D / 8;            // 16-byte chunks per key row
   constexpr int KROW = D + 8;          // K row stride in LDS (elements)
-  constexpr int VROW = kTileKeys + 8;  // V^T row stride in LDS (elements)
-  constexpr int NKV = kTileKeys * CH / kThreads;  // K vectors per thread
-  constexpr int KPT = NKV;                        // keys per thread for V (same count)
-  static_assert(NKV == 2 || NKV == 4, "head_dim must be 64 or 128");
+  constexpr int VROW = kTileKeys;      // V^T row stride in LDS (elements), swizzled granules
+  constexpr int KPT = kTileKeys * CH / kThreads;  // consecutive keys per thread
+  static_assert(KPT == 2 || KPT == 4, "head_dim must be 64 or 128");
+  static_assert(NWC >= 1 && NWC <= kWaves, "compute waves");
 
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kTileKeys * KROW];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
@@ -126,7 +188,7 @@ __global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
   const atlas_attn_work_t w = a.work[blockIdx.x];
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int grp = lane >> 4;
   const int r16 = lane & 15;
 
@@ -140,7 +202,7 @@ __global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
   const int G = a.group;
   const int64_t head_off = int64_t(kvh) * D * 2;
 
-  // Mask window: keys < vis_all are visible to every row.
+  // Keys < vis_all are visible to every row.
   int vis_all = kv_end;
   int col0 = 0;
   if (a.mask_mode == ATLAS_MASK_TREE) {
@@ -150,6 +212,7 @@ __global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
     vis_all = min(vis_all, kv_len - qo_len + 1);
   }
 
+  const bool computes = wave < NWC;
   frag qf[RT][KS];
   f32x4 o[RT][DT];
   float m_run[RT];
@@ -162,99 +225,119 @@ __global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
 
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int lr = (wave + kWaves * rt) * 16 + r16;
-    row_ok[rt] = lr < w.num_rows;
-    const int prow = w.row_start + lr;
+    const int lr = (wave + NWC * rt) * 16 + r16;
+    row_ok[rt] = computes && lr < w.num_rows;
+    const int prow = w.row_start + (row_ok[rt] ? lr : 0);
     node_of[rt] = prow / G;
     head_of[rt] = kvh * G + (prow - node_of[rt] * G);
     m_run[rt] = -INFINITY;
     l_run[rt] = 0.f;
-    tbits[rt] = 0;
-    climit[rt] = 0;
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (row_ok[rt]) {
-      const char* qrow = a.q + ((int64_t(qo_start + node_of[rt]) * a.q_stride_token +
-                                 int64_t(head_of[rt]) * a.q_stride_head) * 2);
+    const char* qrow = a.q + ((int64_t(qo_start + node_of[rt]) * a.q_stride_token +
+                               int64_t(head_of[rt]) * a.q_stride_head) * 2);
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 v = *reinterpret_cast<const uint4*>(qrow + (ks * 32 + grp * 8) * 2);
-        qf[rt][ks] = __builtin_bit_cast(frag, v);
-      }
-      if (a.mask_mode == ATLAS_MASK_TREE) tbits[rt] = a.tree_mask[qo_start + node_of[rt]];
-      if (a.mask_mode == ATLAS_MASK_CAUSAL) climit[rt] = kv_len - qo_len + node_of[rt];
-    } else {
-#pragma unroll
-      for (int ks = 0; ks < KS; ++ks) qf[rt][ks] = __builtin_bit_cast(frag, uint4{0, 0, 0, 0});
+    for (int ks = 0; ks < KS; ++ks) {
+      uint4 v = *reinterpret_cast<const uint4*>(qrow + (ks * 32 + grp * 8) * 2);
+      if (!row_ok[rt]) v = uint4{0, 0, 0, 0};
+      qf[rt][ks] = __builtin_bit_cast(frag, v);
     }
+    tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && row_ok[rt]) ? a.tree_mask[qo_start + node_of[rt]] : 0ull;
+    climit[rt] = kv_len - qo_len + node_of[rt];
   }
 
-  // Global -> register staging of one key tile.
-  uint4 kreg[NKV];
-  uint4 vreg[KPT];
-  const int v_chunk = tid % CH;
-  const int v_key0 = (tid / CH) * KPT;
+  // Each thread stages KPT consecutive keys x one 16-byte chunk of K and V.
+  const int chunk = tid % CH;
+  const int key0 = (tid / CH) * KPT;
+  const int last_key = kv_end - 1;
+  const char* kv_head_base = a.kv + head_off + chunk * 16;
 
-  auto key_addr = [&](int p) -> const char* {
-    const int lp = a.page_shift >= 0 ? (p >> a.page_shift) : (p / a.page_size);
-    const int off = p - lp * a.page_size;
-    const int64_t page = a.kv_indices[pt_base + lp];
-    return a.kv + page * a.page_stride + int64_t(off) * a.token_stride + head_off;
-  };
-
-  auto load_tile = [&](int t0) {
+  const PageWalk pw{a.kv_indices + pt_base, a.page_size, a.page_shift, last_key, key0};
+  // Empty splits (only for requests without keys) load nothing: the loop
+  // below is skipped and the rows get O = 0, lse = -inf.
+  const int t_first = w.kv_start < kv_end ? w.kv_start : kv_end;
+  // A thread's KPT keys share one page whenever page_size is a multiple of
+  // KPT (tiles start on multiples of 64): one page-table read per tile.
+  const bool one_page = (a.page_size % KPT) == 0;
+  int idx_cur = 0, idx_next = 0;
+  uint4 kreg[KPT], vreg[KPT];
 #pragma unroll
-    for (int j = 0; j < NKV; ++j) {
-      const int v = tid + kThreads * j;
-      const int kk = v / CH;
-      const int c = v % CH;
-      const int p = t0 + kk;
-      kreg[j] = uint4{0, 0, 0, 0};
-      if (p < kv_end) kreg[j] = *reinterpret_cast<const uint4*>(key_addr(p) + c * 16);
-    }
+  for (int j = 0; j < KPT; ++j) {
+    kreg[j] = uint4{0, 0, 0, 0};
+    vreg[j] = uint4{0, 0, 0, 0};
+  }
+  // Stage tile t: full tiles read KPT consecutive rows of one page; the
+  // split's last partial tile clamps every key to the last valid key (rows of
+  // valid memory and finite values; masked out of the softmax).
+  auto stage = [](const PageWalk& pw, const char* base, int64_t page_stride, int64_t token_stride, int64_t v_off,
+                  int t, int page0, bool full, bool one_page, uint4 (&kr)[KPT], uint4 (&vr)[KPT]) {
+    if (full && one_page) {
+      const int p = t + pw.key0;
+      const int off = pw.page_shift >= 0 ? (p & (pw.page_size - 1)) : (p % pw.page_size);
+      const char* r0 = base + int64_t(page0) * page_stride + int64_t(off) * token_stride;
 #pragma unroll
-    for (int j = 0; j < KPT; ++j) {
-      const int p = t0 + v_key0 + j;
-      vreg[j] = uint4{0, 0, 0, 0};
-      if (p < kv_end)
-        vreg[j] = *reinterpret_cast<const uint4*>(key_addr(p) + a.v_offset + v_chunk * 16);
-    }
-  };
-
-  auto store_tile = [&]() {
+      for (int j = 0; j < KPT; ++j) {
+        kr[j] = *reinterpret_cast<const uint4*>(r0 + j * token_stride);
+        vr[j] = *reinterpret_cast<const uint4*>(r0 + j * token_stride + v_off);
+      }
+    } else {
 #pragma unroll
-    for (int j = 0; j < NKV; ++j) {
-      const int v = tid + kThreads * j;
-      const int kk = v / CH;
-      const int c = v % CH;
-      *reinterpret_cast<uint4*>(&k_lds[kk * KROW + c * 8]) = kreg[j];
-    }
-    // Transpose KPT keys x 8 dims into 8 dim rows of KPT keys.
-    const int pos = (v_key0 >> 5) * 32 + vt_position(v_key0 & 31);
-    const uint16_t* e[KPT];
-#pragma unroll
-    for (int j = 0; j < KPT; ++j) e[j] = reinterpret_cast<const uint16_t*>(&vreg[j]);
-#pragma unroll
-    for (int d = 0; d < 8; ++d) {
-      uint16_t* dst = &vt_lds[(v_chunk * 8 + d) * VROW + pos];
-      if constexpr (KPT == 4) {
-        const uint32_t lo = uint32_t(e[0][d]) | (uint32_t(e[1][d]) << 16);
-        const uint32_t hi = uint32_t(e[2][d]) | (uint32_t(e[3][d]) << 16);
-        *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
-      } else {
-        *reinterpret_cast<uint32_t*>(dst) = uint32_t(e[0][d]) | (uint32_t(e[1][d]) << 16);
+      for (int j = 0; j < KPT; ++j) {
+        const char* rj = pw.row(base, page_stride, token_stride, t + j, pw.page(t + j));
+        kr[j] = *reinterpret_cast<const uint4*>(rj);
+        vr[j] = *reinterpret_cast<const uint4*>(rj + v_off);
       }
     }
   };
+  if (t_first < kv_end) {
+    idx_cur = pw.page(t_first);
+    idx_next = pw.page(t_first + kTileKeys);
+    stage(pw, kv_head_base, a.page_stride, a.token_stride, a.v_offset, t_first, idx_cur,
+          t_first + kTileKeys <= kv_end, one_page, kreg, vreg);
+  }
 
-  int t0 = w.kv_start;
-  if (t0 < kv_end) load_tile(t0);
+  const int vt_pos = (key0 >> 5) * 32 + vt_position(key0 & 31);
 
-  for (; t0 < kv_end; t0 += kTileKeys) {
+  for (int t0 = t_first; t0 < kv_end; t0 += kTileKeys) {
     __syncthreads();  // previous tile's LDS reads are done
-    store_tile();
+#pragma unroll
+    for (int j = 0; j < KPT; ++j)
+      *reinterpret_cast<uint4*>(&k_lds[(key0 + j) * KROW + chunk * 8]) = kreg[j];
+    {
+      // Transpose KPT keys x 8 dims into 8 dim rows of KPT keys: byte
+      // permutes pair the low (even dim) or high (odd dim) halves of two keys.
+      constexpr uint32_t kLoLo = 0x05040100u, kHiHi = 0x07060302u;
+#pragma unroll
+      for (int d = 0; d < 8; ++d) {
+        const int word = d >> 1;
+        const uint32_t sel = (d & 1) ? kHiHi : kLoLo;
+        const int row = chunk * 8 + d;
+        uint16_t* dst = &vt_lds[row * VROW + (((vt_pos >> 3) ^ vt_swizzle(row)) << 3) + (vt_pos & 7)];
+        auto w4 = [&](int j) -> uint32_t {
+          return word == 0 ? vreg[j].x : word == 1 ? vreg[j].y : word == 2 ? vreg[j].z : vreg[j].w;
+        };
+        if constexpr (KPT == 4) {
+          *reinterpret_cast<uint2*>(dst) =
+              uint2{__builtin_amdgcn_perm(w4(1), w4(0), sel), __builtin_amdgcn_perm(w4(3), w4(2), sel)};
+        } else {
+          *reinterpret_cast<uint32_t*>(dst) = __builtin_amdgcn_perm(w4(1), w4(0), sel);
+        }
+      }
+    }
     __syncthreads();
-    if (t0 + kTileKeys < kv_end) load_tile(t0 + kTileKeys);
+
+    // Prefetch: the next tile's K/V with the page id fetched one tile
+    // earlier, and the page id of the tile after it.
+    {
+      const int tn = t0 + kTileKeys;
+      idx_cur = idx_next;
+      idx_next = pw.page(tn + kTileKeys);
+      if (tn < kv_end)
+        stage(pw, kv_head_base, a.page_stride, a.token_stride, a.v_offset, tn, idx_cur, tn + kTileKeys <= kv_end,
+              one_page, kreg, vreg);
+    }
+
+    if (!computes) continue;
 
     // ---- scores S^T = K Q^T ----
     f32x4 s[RT][4];
@@ -264,108 +347,98 @@ __global__ __launch_bounds__(kThreads) void tree_attn_kernel(AttnArgs a) {
       for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kt = 0; kt < 4; ++kt) {
+      frag af[KS];
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks) {
-        const uint4 av = *reinterpret_cast<const uint4*>(&k_lds[(kt * 16 + r16) * KROW + ks * 32 + grp * 8]);
-        const frag af = __builtin_bit_cast(frag, av);
+      for (int ks = 0; ks < KS; ++ks)
+        af[ks] = __builtin_bit_cast(
+            frag, *reinterpret_cast<const uint4*>(&k_lds[(kt * 16 + r16) * KROW + ks * 32 + grp * 8]));
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          if ((wave + kWaves * rt) * 16 < w.num_rows) s[rt][kt] = M::run(af, qf[rt][ks], s[rt][kt]);
-        }
-      }
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) s[rt][kt] = M::run(af[ks], qf[rt][ks], s[rt][kt]);
     }
 
-    // ---- online softmax, P^T fragments ----
+    // ---- online softmax (lazy rescale), P^T fragments ----
+    // Scores stay raw (unscaled) until exp2(fma(s, scale*log2e, -m)).
     const bool need_mask = (t0 + kTileKeys) > vis_all;
     frag pf[RT][2];
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
-      if ((wave + kWaves * rt) * 16 >= w.num_rows) {
-        pf[rt][0] = pf[rt][1] = __builtin_bit_cast(frag, uint4{0, 0, 0, 0});
-        continue;
-      }
-      float x[4][4];
-      float mx = -INFINITY;
+      if (need_mask) {
 #pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
+        for (int kt = 0; kt < 4; ++kt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float v = s[rt][kt][i] * a.scale_log2;
-          if (need_mask) {
+          for (int i = 0; i < 4; ++i) {
             const int p = t0 + kt * 16 + grp * 4 + i;
             bool vis = p < kv_end;
-            if (vis && p >= vis_all) {
-              if (a.mask_mode == ATLAS_MASK_TREE) {
-                const int b = p - col0;
-                vis = b < 64 && ((tbits[rt] >> b) & 1ull);
-              } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
-                vis = p <= climit[rt];
-              }
+            if (a.mask_mode == ATLAS_MASK_TREE) {
+              const int b = p - col0;
+              vis = vis && (p < col0 || (b < 64 && ((tbits[rt] >> (b & 63)) & 1ull)));
+            } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
+              vis = vis && p <= climit[rt];
             }
-            v = vis ? v : -INFINITY;
+            s[rt][kt][i] = vis ? s[rt][kt][i] : -INFINITY;
           }
-          x[kt][i] = v;
-          mx = fmaxf(mx, v);
         }
       }
-      mx = wave_max_across_groups(mx);
-      const float m_new = fmaxf(m_run[rt], mx);
-      const bool dead = m_new == -INFINITY;
-      const float alpha = dead ? 1.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
-      float psum = 0.f;
-      uint16_t ph[4][4];
+      float mx = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
+                       fmaxf(fmaxf(s[rt][1][0], s[rt][1][1]), fmaxf(s[rt][1][2], s[rt][1][3])));
+      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[rt][2][0], s[rt][2][1]), fmaxf(s[rt][2][2], s[rt][2][3])),
+                           fmaxf(fmaxf(s[rt][3][0], s[rt][3][1]), fmaxf(s[rt][3][2], s[rt][3][3]))));
+      mx = wave_max_across_groups(mx) * a.scale_log2;
+      // Lazy rescale: keep the running reference max until a row's max grows
+      // by more than kRescaleLog2 (P stays below 2^kRescaleLog2), so most
+      // tiles skip the O rescale.
+      if (__builtin_amdgcn_ballot_w64(mx > m_run[rt] + kRescaleLog2) != 0) {
+        const float m_new = fmaxf(m_run[rt], mx);
+        const float alpha = (m_run[rt] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run[rt] - m_new);
+        l_run[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) o[rt][dt] *= alpha;
+        m_run[rt] = m_new;
+      }
+      // A row with every key masked so far has m = -inf and only -inf scores.
+      const float neg_m = m_run[rt] == -INFINITY ? 0.f : -m_run[rt];
+      uint32_t pk[4][2];
 #pragma unroll
       for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pe = dead ? 0.f : __builtin_amdgcn_exp2f(x[kt][i] - m_new);
-          psum += pe;
-          ph[kt][i] = M::from_float(pe);
-        }
+        const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][0], a.scale_log2, neg_m));
+        const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][1], a.scale_log2, neg_m));
+        const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][2], a.scale_log2, neg_m));
+        const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][3], a.scale_log2, neg_m));
+        pk[kt][0] = M::pack2(p0, p1);
+        pk[kt][1] = M::pack2(p2, p3);
+        l_run[rt] = M::sum2(pk[kt][1], M::sum2(pk[kt][0], l_run[rt]));
       }
-      l_run[rt] = l_run[rt] * alpha + psum;
-      m_run[rt] = m_new;
-#pragma unroll
-      for (int dt = 0; dt < DT; ++dt) o[rt][dt] *= alpha;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        u16x8 u;
-        u[0] = ph[2 * kk][0];
-        u[1] = ph[2 * kk][1];
-        u[2] = ph[2 * kk][2];
-        u[3] = ph[2 * kk][3];
-        u[4] = ph[2 * kk + 1][0];
-        u[5] = ph[2 * kk + 1][1];
-        u[6] = ph[2 * kk + 1][2];
-        u[7] = ph[2 * kk + 1][3];
-        pf[rt][kk] = __builtin_bit_cast(frag, u);
-      }
+      pf[rt][0] = __builtin_bit_cast(frag, uint4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]});
+      pf[rt][1] = __builtin_bit_cast(frag, uint4{pk[2][0], pk[2][1], pk[3][0], pk[3][1]});
     }
 
     // ---- O^T += V^T P^T ----
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt) {
+      frag av[2];
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const uint4 av = *reinterpret_cast<const uint4*>(&vt_lds[(dt * 16 + r16) * VROW + kk * 32 + grp * 8]);
-        const frag af = __builtin_bit_cast(frag, av);
+      for (int kk = 0; kk < 2; ++kk)
+        av[kk] = __builtin_bit_cast(
+            frag, *reinterpret_cast<const uint4*>(
+                      &vt_lds[(dt * 16 + r16) * VROW + (((kk * 4 + grp) ^ vt_swizzle(dt * 16 + r16)) << 3)]));
 #pragma unroll
-        for (int rt = 0; rt < RT; ++rt) {
-          if ((wave + kWaves * rt) * 16 < w.num_rows) o[rt][dt] = M::run(af, pf[rt][kk], o[rt][dt]);
-        }
-      }
+      for (int kk = 0; kk < 2; ++kk)
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) o[rt][dt] = M::run(av[kk], pf[rt][kk], o[rt][dt]);
     }
   }
 
+  if (!computes) return;
   // ---- epilogue ----
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    if ((wave + kWaves * rt) * 16 >= w.num_rows) continue;
     const float l_tot = wave_sum_across_groups(l_run[rt]);
     if (!row_ok[rt]) continue;
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const float lse2 = l_tot > 0.f ? m_run[rt] + __builtin_log2f(l_tot) : -INFINITY;
-    const int lr = (wave + kWaves * rt) * 16 + r16;
+    const int lr = (wave + NWC * rt) * 16 + r16;
     if (w.partial_row < 0) {
       char* orow = a.out + ((int64_t(qo_start + node_of[rt]) * a.out_stride_token +
                              int64_t(head_of[rt]) * a.out_stride_head) * 2);
@@ -405,68 +478,135 @@ struct MergeArgs {
   int num_qo_heads;
 };
 
-// One wave per packed row: combine the row's split states.
+// One workgroup per packed row: the split LSEs give weights
+// w_s = exp2(lse_s - max) (kept in LDS), then threads sweep (split, 16-byte
+// dim chunk) pairs with independent loads and reduce the per-thread sums
+// through LDS.
+constexpr int kMergeThreads = 256;
+
 template <int D, bool BF16>
-__global__ __launch_bounds__(256) void tree_attn_merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArgs a) {
   typedef Mfma<BF16> M;
-  constexpr int PER = D / 64;
+  constexpr int CHUNKS = D / 4;                       // float4 chunks per row
+  constexpr int SPLIT_LANES = kMergeThreads / CHUNKS;  // splits read in parallel
+  __shared__ float w_sh[1024];
+  __shared__ float red[kMergeThreads / 64];
+  __shared__ f32x4 acc_sh[SPLIT_LANES][CHUNKS];
   const atlas_attn_merge_t mi = a.merge[blockIdx.x];
-  const int lane = threadIdx.x & 63;
-  const int row = blockIdx.y * 4 + (threadIdx.x >> 6);
+  const int row = blockIdx.y;
   if (row >= mi.num_rows) return;
+  const int tid = threadIdx.x;
+  const int ns = min(mi.num_splits, 1024);
+  const int64_t base = int64_t(mi.partial_row) + row;
+
   float mx = -INFINITY;
-  for (int s = 0; s < mi.num_splits; ++s)
-    mx = fmaxf(mx, a.part_lse[int64_t(mi.partial_row) + int64_t(s) * mi.num_rows + row]);
-  float acc[PER];
+  for (int sp = tid; sp < ns; sp += kMergeThreads) {
+    const float l = a.part_lse[base + int64_t(sp) * mi.num_rows];
+    w_sh[sp] = l;
+    mx = fmaxf(mx, l);
+  }
+  mx = wave_max_across_groups(mx);
+  mx = fmaxf(mx, __shfl_xor(mx, 8));
+  mx = fmaxf(mx, __shfl_xor(mx, 4));
+  mx = fmaxf(mx, __shfl_xor(mx, 2));
+  mx = fmaxf(mx, __shfl_xor(mx, 1));
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  float wpart = 0.f;
+  for (int sp = tid; sp < ns; sp += kMergeThreads) {
+    const float wv = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(w_sh[sp] - mx);
+    w_sh[sp] = wv;
+    wpart += wv;
+  }
+  __syncthreads();
+  const int chunk = tid % CHUNKS;
+  const int lane_split = tid / CHUNKS;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int sp = lane_split; sp < ns; sp += SPLIT_LANES) {
+    const float wv = w_sh[sp];
+    const f32x4 v =
+        *reinterpret_cast<const f32x4*>(a.part_o + (base + int64_t(sp) * mi.num_rows) * D + chunk * 4);
+    acc += wv * v;
+  }
+  acc_sh[lane_split][chunk] = acc;
+  // total weight
+  wpart = wave_sum_across_groups(wpart);
+  wpart += __shfl_xor(wpart, 8);
+  wpart += __shfl_xor(wpart, 4);
+  wpart += __shfl_xor(wpart, 2);
+  wpart += __shfl_xor(wpart, 1);
+  __syncthreads();
+  if ((tid & 63) == 0) red[tid >> 6] = wpart;
+  __syncthreads();
+  const float wsum = red[0] + red[1] + red[2] + red[3];
+  if (tid < CHUNKS) {
+    f32x4 tot = acc_sh[0][tid];
 #pragma unroll
-  for (int i = 0; i < PER; ++i) acc[i] = 0.f;
-  float wsum = 0.f;
-  if (mx != -INFINITY) {
-    for (int s = 0; s < mi.num_splits; ++s) {
-      const int64_t prow = int64_t(mi.partial_row) + int64_t(s) * mi.num_rows + row;
-      const float ws = __builtin_amdgcn_exp2f(a.part_lse[prow] - mx);
-      wsum += ws;
-      const float* po = a.part_o + prow * D + lane * PER;
-#pragma unroll
-      for (int i = 0; i < PER; ++i) acc[i] += ws * po[i];
+    for (int k = 1; k < SPLIT_LANES; ++k) tot += acc_sh[k][tid];
+    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+    const int prow_q = mi.row_start + row;
+    const int node = prow_q / a.group;
+    const int head = mi.kv_head * a.group + (prow_q - node * a.group);
+    const int qo_start = a.qo_indptr[mi.req];
+    char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
+    const uint32_t lo = uint32_t(M::from_float(tot[0] * inv)) | (uint32_t(M::from_float(tot[1] * inv)) << 16);
+    const uint32_t hi = uint32_t(M::from_float(tot[2] * inv)) | (uint32_t(M::from_float(tot[3] * inv)) << 16);
+    *reinterpret_cast<uint2*>(orow + tid * 8) = uint2{lo, hi};
+    if (tid == 0 && a.lse != nullptr)
+      a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] =
+          wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
+  }
+}
+
+// Work-shape choice: the fewest (compute waves x row tiles) slots that cover
+// the row tiles, preferring more waves (fewer tiles per wave).
+inline void choose_shape(int row_tiles, int& nwc, int& rt) {
+  int best = 1 << 30;
+  nwc = 4;
+  rt = 3;
+  for (int r = 1; r <= 3; ++r) {
+    for (int nw = 1; nw <= kWaves; ++nw) {
+      if (nw * r < row_tiles) continue;
+      const int slots = nw * r;
+      if (slots < best || (slots == best && r < rt)) {
+        best = slots;
+        nwc = nw;
+        rt = r;
+      }
     }
   }
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const int prow_q = mi.row_start + row;
-  const int node = prow_q / a.group;
-  const int head = mi.kv_head * a.group + (prow_q - node * a.group);
-  const int qo_start = a.qo_indptr[mi.req];
-  uint16_t* orow = reinterpret_cast<uint16_t*>(
-      a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2));
-#pragma unroll
-  for (int i = 0; i < PER; ++i) orow[lane * PER + i] = M::from_float(acc[i] * inv);
-  if (a.lse != nullptr && lane == 0)
-    a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] =
-        wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
+}
+
+template <int D, bool BF16, int RT, int NWC>
+void launch_shape(const AttnArgs& args, int num_work, hipStream_t stream) {
+  hipLaunchKernelGGL((tree_attn_kernel<D, BF16, RT, NWC>), dim3(num_work), dim3(kThreads), 0, stream, args);
 }
 
 template <int D, bool BF16>
-int launch_attn(const AttnArgs& args, int num_work, int rt, const MergeArgs& margs, int num_merge,
+int launch_attn(const AttnArgs& args, int num_work, int row_tiles, const MergeArgs& margs, int num_merge,
                 int max_rows, hipStream_t stream) {
   int rc;
-  switch (rt) {
-    case 1:
-      hipLaunchKernelGGL((tree_attn_kernel<D, BF16, 1>), dim3(num_work), dim3(kThreads), 0, stream, args);
-      break;
-    case 2:
-      hipLaunchKernelGGL((tree_attn_kernel<D, BF16, 2>), dim3(num_work), dim3(kThreads), 0, stream, args);
-      break;
-    case 3:
-      hipLaunchKernelGGL((tree_attn_kernel<D, BF16, 3>), dim3(num_work), dim3(kThreads), 0, stream, args);
-      break;
+  int nwc, rt;
+  choose_shape(row_tiles, nwc, rt);
+  switch (rt * 10 + nwc) {
+    case 11: launch_shape<D, BF16, 1, 1>(args, num_work, stream); break;
+    case 12: launch_shape<D, BF16, 1, 2>(args, num_work, stream); break;
+    case 13: launch_shape<D, BF16, 1, 3>(args, num_work, stream); break;
+    case 14: launch_shape<D, BF16, 1, 4>(args, num_work, stream); break;
+    case 22: launch_shape<D, BF16, 2, 2>(args, num_work, stream); break;
+    case 23: launch_shape<D, BF16, 2, 3>(args, num_work, stream); break;
+    case 24: launch_shape<D, BF16, 2, 4>(args, num_work, stream); break;
+    case 33: launch_shape<D, BF16, 3, 3>(args, num_work, stream); break;
+    case 34: launch_shape<D, BF16, 3, 4>(args, num_work, stream); break;
     default:
-      set_error("unsupported row tiles per wave %d", rt);
+      set_error("no kernel shape for %d row tiles (rt=%d, waves=%d)", row_tiles, rt, nwc);
       return ATLAS_EUNSUPPORTED;
   }
   if ((rc = launch_status("tree_attn_kernel"))) return rc;
   if (num_merge > 0) {
-    const dim3 grid(num_merge, (max_rows + 3) / 4);
-    hipLaunchKernelGGL((tree_attn_merge_kernel<D, BF16>), grid, dim3(256), 0, stream, margs);
+    const dim3 grid(num_merge, max_rows);
+    hipLaunchKernelGGL((tree_attn_merge_kernel<D, BF16>), grid, dim3(kMergeThreads), 0, stream, margs);
     if ((rc = launch_status("tree_attn_merge_kernel"))) return rc;
   }
   return ATLAS_OK;
@@ -513,8 +653,6 @@ extern "C" int atlas_tree_verify_attn(
   if (num_work == 0) return ATLAS_OK;
   ATLAS_REQUIRE(work_dev != nullptr, "work list must not be NULL");
   const int row_tiles = (max_rows_per_item + 15) / 16;
-  const int rt = (row_tiles + kWaves - 1) / kWaves;
-  ATLAS_REQUIRE(rt >= 1 && rt <= 3, "rows per item %d exceeds %d", max_rows_per_item, 3 * kWaves * 16);
 
   AttnArgs args{};
   args.q = static_cast<const char*>(q);
@@ -566,8 +704,8 @@ extern "C" int atlas_tree_verify_attn(
   hipStream_t s = static_cast<hipStream_t>(stream);
   const bool bf16 = dtype == ATLAS_DTYPE_BF16;
   if (head_dim == 128)
-    return bf16 ? launch_attn<128, true>(args, num_work, rt, margs, num_merge, max_rows_per_item, s)
-                : launch_attn<128, false>(args, num_work, rt, margs, num_merge, max_rows_per_item, s);
-  return bf16 ? launch_attn<64, true>(args, num_work, rt, margs, num_merge, max_rows_per_item, s)
-              : launch_attn<64, false>(args, num_work, rt, margs, num_merge, max_rows_per_item, s);
+    return bf16 ? launch_attn<128, true>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s)
+                : launch_attn<128, false>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s);
+  return bf16 ? launch_attn<64, true>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s)
+              : launch_attn<64, false>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s);
 }

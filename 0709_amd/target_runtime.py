@@ -1,0 +1,566 @@
+"""Target-side persistent tree verifier (drop-in for the reference's
+``atlas_0709.target_runtime``).
+
+``DirectFlashInferMaskedTreeVerifyBackend`` keeps the reference's method
+names, arguments, metadata and exceptions (``target_runtime.py:41-920``).  The
+work that touches KV or logits runs on the gfx950 kernels:
+
+* ``_commit_selected_path`` -- one all-layer commit launch whose positions
+  travel in the kernel arguments (the reference issues gather + clone +
+  index_put per layer, ``:885-912``);
+* ``_score_routes`` -- one log-sum-exp + gather launch per logits tensor and a
+  single device-to-host copy of the k*d log-probs (the reference converts each
+  token's log-prob with ``.cpu()``, ``:742``);
+* the masked verify forward uses ``write_suffix_kv`` and the tree attention
+  wrapper of this package.
+
+Model compute (embedding, projections, MLP, lm_head) stays in the caller's
+torch model; ``run_full_verify`` drives a Hugging Face Llama-layout module the
+way ``flashinfer_full_verify.run_flashinfer_full_verify`` does (``:1182-1231``).
+"""
+
+from __future__ import annotations
+
+import hashlib
+import json
+import math
+import time
+from dataclasses import dataclass
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib, kv_ops
+from .flashinfer_full_verify import (
+    FullVerifyState,
+    build_deduplicated_tree_spec_from_paths,
+    ceil_div,
+    first_tensor,
+    make_prefill_wrapper,
+    plan_prefill_wrapper,
+    prefix_layer_to_paged_kv,
+    write_suffix_kv,
+)
+from .types import TargetRouteScore, TargetVerifyResult
+
+ROUTE_POLICIES = ("target_best", "target_sample", "first_route")
+
+
+@dataclass(frozen=True)
+class VerifyRoutePayload:
+    route_id: int
+    token_ids: tuple[int, ...]
+    draft_logprob: float
+    draft_token_logprobs: tuple[float, ...] = ()
+
+
+def verify_payload_from_mapping(item: dict) -> VerifyRoutePayload:
+    """``target_runtime.py:922-935``."""
+    raw = item.get("draft_token_logprobs")
+    if raw is None:
+        draft_token_logprobs: tuple[float, ...] = ()
+    elif isinstance(raw, (list, tuple)):
+        draft_token_logprobs = tuple(float(v) for v in raw)
+    else:
+        raise ValueError("draft_token_logprobs must be a list of numbers when provided")
+    return VerifyRoutePayload(
+        route_id=int(item["route_id"]),
+        token_ids=tuple(int(t) for t in item["token_ids"]),
+        draft_logprob=float(item.get("draft_logprob", 0.0)),
+        draft_token_logprobs=draft_token_logprobs,
+    )
+
+
+def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Sequence[int]) -> torch.Tensor:
+    """fp32 ``log_softmax(logits[row])[token]`` for each (row, token) pair,
+    computed on the device in one launch.  ``logits``: [rows, vocab] or [vocab]."""
+    device = _lib.require_device(logits, what="route scoring")
+    lg = logits.reshape(1, -1) if logits.ndim == 1 else logits
+    if lg.ndim != 2 or lg.stride(-1) != 1:
+        raise ValueError("logits must be [rows, vocab] with contiguous rows")
+    n = len(rows)
+    out = torch.empty(n, dtype=torch.float32, device=device)
+    if n == 0:
+        return out
+    if len(tokens) != n:
+        raise ValueError("rows and tokens must have equal length")
+    idx = torch.tensor([*map(int, tokens), *map(int, rows)], dtype=torch.int64).to(device, non_blocking=True)
+    tok = idx[:n]
+    row = idx[n:].to(torch.int32)
+    lib = _lib.load()
+    rc = lib.atlas_gather_logprobs(
+        _lib.ptr(lg), lg.stride(0), int(lg.shape[0]), int(lg.shape[1]), _lib.dtype_code(lg.dtype),
+        _lib.ptr(row), _lib.ptr(tok), n, None, _lib.ptr(out), _lib.stream_of(device),
+    )
+    _lib.check(rc, "atlas_gather_logprobs")
+    return out
+
+
+def rotate_half(hidden_states: torch.Tensor) -> torch.Tensor:
+    first, second = hidden_states.chunk(2, dim=-1)
+    return torch.cat((-second, first), dim=-1)
+
+
+def rope_cos_sin(model, positions: torch.Tensor, head_dim: int, dtype: torch.dtype, device) -> tuple:
+    """cos/sin at the given positions from the model's rotary module, else the
+    default theta schedule (``flashinfer_full_verify.py:231-297``)."""
+    positions = positions.to(device=device, dtype=torch.long).reshape(-1)
+    rotary = getattr(getattr(model, "model", None), "rotary_emb", None)
+    if rotary is not None:
+        hidden = int(getattr(model.config, "hidden_size", head_dim))
+        dummy = torch.empty((1, int(positions.numel()), hidden), dtype=dtype, device=device)
+        cos, sin = rotary(dummy, positions.reshape(1, -1))
+        return cos.to(dtype).reshape(-1, head_dim), sin.to(dtype).reshape(-1, head_dim)
+    theta = float(getattr(model.config, "rope_theta", 10000.0))
+    inv = 1.0 / (theta ** (torch.arange(0, head_dim, 2, device=device, dtype=torch.float32) / head_dim))
+    emb = torch.outer(positions.float(), inv)
+    emb = torch.cat((emb, emb), dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+@torch.inference_mode()
+def run_full_verify(*, model, wrapper, state: FullVerifyState, prefix_len: int, page_size: int) -> torch.Tensor:
+    """Masked tree forward of a Llama-layout model: per layer RMSNorm, QKV,
+    RoPE at prefix_len + depth, ``write_suffix_kv`` then tree attention
+    (append before attention, as ``flashinfer_full_verify.py:1207-1223``)."""
+    cfg = model.config
+    base = model.model
+    head_dim = getattr(cfg, "head_dim", None) or int(cfg.hidden_size) // int(cfg.num_attention_heads)
+    hq, hkv = int(cfg.num_attention_heads), int(cfg.num_key_value_heads)
+    n = state.tree.node_count
+    hidden = base.embed_tokens(state.tree.flat_token_ids)
+    positions = int(prefix_len) + state.tree.depths.to(device=hidden.device, dtype=torch.long)
+    cos, sin = rope_cos_sin(model, positions, head_dim, hidden.dtype, hidden.device)
+    cos, sin = cos[:, None, :], sin[:, None, :]
+    for layer_idx, layer in enumerate(base.layers):
+        residual = hidden
+        normed = layer.input_layernorm(hidden)
+        q = layer.self_attn.q_proj(normed).reshape(n, hq, head_dim)
+        k = layer.self_attn.k_proj(normed).reshape(n, hkv, head_dim)
+        v = layer.self_attn.v_proj(normed).reshape(n, hkv, head_dim).contiguous()
+        q = (q * cos + rotate_half(q) * sin).contiguous()
+        k = (k * cos + rotate_half(k) * sin).contiguous()
+        kv_cache = state.paged_prefix_kv[layer_idx]
+        write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size)
+        attn = first_tensor(wrapper.run(q, kv_cache)).reshape(n, hq * head_dim)
+        hidden = residual + layer.self_attn.o_proj(attn)
+        residual = hidden
+        hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
+    return model.lm_head(base.norm(hidden))
+
+
+class DirectFlashInferMaskedTreeVerifyBackend:
+    """Persistent Target: committed prefix KV, masked tree verify, route
+    scoring / selection and in-place commit of the selected path."""
+
+    def __init__(
+        self,
+        *,
+        model_path: str | None = None,
+        config,
+        model=None,
+        tokenizer=None,
+        score_weights: Sequence[float] | None = None,
+        fallback_threshold: float | None = None,
+        first_token_threshold: float | None = None,
+        fallback_ar_tokens: int = 4,
+        profile_fallback_ar: bool = False,
+        route_selection_policy: str = "target_best",
+        route_sampling_temperature: float = 1.0,
+    ) -> None:
+        validate = getattr(config, "validate", None)
+        if callable(validate):
+            validate()
+        self.model_path = model_path
+        self.config = config
+        self.score_weights = self._validate_score_weights(score_weights)
+        self.fallback_threshold = None if fallback_threshold is None else float(fallback_threshold)
+        self.first_token_threshold = None if first_token_threshold is None else float(first_token_threshold)
+        self.fallback_ar_tokens = int(fallback_ar_tokens)
+        self.profile_fallback_ar = bool(profile_fallback_ar)
+        self.route_selection_policy = self._validate_route_selection_policy(route_selection_policy)
+        self.route_sampling_temperature = self._validate_route_sampling_temperature(route_sampling_temperature)
+        if self.fallback_ar_tokens <= 0:
+            raise ValueError("fallback_ar_tokens must be positive")
+        if self.route_selection_policy == "first_route" and (
+            self.fallback_threshold is not None or self.first_token_threshold is not None
+        ):
+            raise ValueError(
+                "first_route is a strict diagnostic policy and requires fallback thresholds to be disabled"
+            )
+        if model is None and model_path is not None:
+            from transformers import AutoModelForCausalLM, AutoTokenizer
+
+            dtype = getattr(torch, str(getattr(config, "dtype", "float16")))
+            tokenizer = AutoTokenizer.from_pretrained(model_path)
+            model = AutoModelForCausalLM.from_pretrained(model_path, torch_dtype=dtype).to(config.device).eval()
+        self.model = model
+        self.tokenizer = tokenizer
+        self.dtype = next(model.parameters()).dtype if model is not None else torch.float16
+        self._wrapper = make_prefill_wrapper(args=config) if model is not None else None
+        self.prefix_token_ids: tuple[int, ...] = ()
+        self._paged_prefix_kv: list[torch.Tensor] | None = None
+        self._prefix_logits: torch.Tensor | None = None
+        self._committed_verify_rounds = 0
+        self._last_fallback_ar_profile = None
+        self.match_logits_dtype_rounding = True
+
+    # ------------------------------------------------------------ prefill
+    @torch.inference_mode()
+    def prefill(self, prompt_token_ids: Sequence[int]):
+        token_ids = tuple(int(t) for t in prompt_token_ids)
+        if not token_ids:
+            raise ValueError("target prefill requires a non-empty prompt")
+        if self.model is None:
+            raise RuntimeError("target prefill needs a model")
+        ids = torch.tensor([token_ids], dtype=torch.long, device=self.config.device)
+        out = self.model(input_ids=ids, use_cache=True)
+        past = out.past_key_values
+        layers = []
+        for layer_idx in range(len(self.model.model.layers)):
+            key, value = _legacy_layer_kv(past, layer_idx)
+            layers.append(prefix_layer_to_paged_kv(key=key, value=value, prefix_len=len(token_ids), node_count=0,
+                                                   page_size=self.config.page_size))
+        self.prefix_token_ids = token_ids
+        self._paged_prefix_kv = layers
+        self._prefix_logits = out.logits[:, -1, :].detach()
+        self._committed_verify_rounds = 0
+        return self._prefix_logits[0]
+
+    # ------------------------------------------------------------ verify
+    @torch.inference_mode()
+    def verify_payloads(
+        self,
+        *,
+        prefix_token_ids: Sequence[int],
+        routes: Sequence[VerifyRoutePayload],
+        fallback_max_tokens: int | None = None,
+        selected_path_max_tokens: int | None = None,
+        eos_token_id: int | None = None,
+        route_sampling_seed: int | None = None,
+        route_sampling_round: int | None = None,
+    ) -> TargetVerifyResult:
+        prefix = tuple(int(t) for t in prefix_token_ids)
+        if self._paged_prefix_kv is None or self._prefix_logits is None:
+            self.prefill(prefix)
+        elif prefix != self.prefix_token_ids:
+            raise RuntimeError(
+                "target committed prefix mismatch; incremental verify cannot silently rebuild KV: "
+                f"request_len={len(prefix)}, target_len={len(self.prefix_token_ids)}"
+            )
+        if not routes:
+            raise ValueError("verify requires at least one route")
+        if len(routes) != int(self.config.k):
+            raise ValueError(f"verify route count does not match configured k: routes={len(routes)}, k={int(self.config.k)}")
+        route_ids = [int(r.route_id) for r in routes]
+        if len(set(route_ids)) != len(route_ids):
+            raise ValueError("verify route ids must be unique")
+        paths = [tuple(int(t) for t in r.token_ids) for r in routes]
+        for r, p in zip(routes, paths):
+            if r.draft_token_logprobs and len(r.draft_token_logprobs) != len(p):
+                raise ValueError(
+                    "draft_token_logprobs must be empty or match route depth: "
+                    f"route_id={int(r.route_id)}, values={len(r.draft_token_logprobs)}, depth={len(p)}"
+                )
+        depths = {len(p) for p in paths}
+        if len(depths) != 1:
+            raise ValueError(f"all verify routes must have the same depth, got {sorted(depths)}")
+        depth = next(iter(depths))
+        if depth <= 0:
+            raise ValueError("verify routes must contain at least one token")
+        if int(depth) != int(self.config.d):
+            raise ValueError(f"verify route depth does not match configured d: depth={int(depth)}, d={int(self.config.d)}")
+        tree, route_nodes = build_deduplicated_tree_spec_from_paths(
+            paths=paths, prefix_len=len(prefix), page_size=self.config.page_size, device=self.config.device
+        )
+        self._ensure_page_capacity(tree.total_pages)
+        state = FullVerifyState(tree=tree, paged_prefix_kv=self._paged_prefix_kv)
+        plan_prefill_wrapper(self._wrapper, tree, args=self.config, config=self.model.config, dtype=self.dtype)
+        logits = run_full_verify(model=self.model, wrapper=self._wrapper, state=state, prefix_len=len(prefix),
+                                 page_size=self.config.page_size)
+        scores = self._score_routes(routes=routes, paths=paths, prefix_logits=self._prefix_logits[0],
+                                    verify_logits=logits, route_to_node_paths=route_nodes)
+        selected, sampling_meta = self._select_route_with_metadata(
+            scores, route_sampling_seed=route_sampling_seed, route_sampling_round=route_sampling_round
+        )
+        best = max(scores, key=lambda s: (self._selection_score(s), s.draft_path_logprob, -s.route_id))
+        reason = self._fallback_reason(selected)
+        common = {
+            "route_count": len(routes),
+            "path_depth": int(depth),
+            "node_count": int(tree.node_count),
+            "unmerged_path_node_count": int(len(routes) * depth),
+            "kv_len": int(tree.kv_len),
+            "prefix_len_before": len(self.prefix_token_ids),
+            "selection_policy": self._selection_policy_name(),
+            "best_route_id": int(best.route_id),
+            **sampling_meta,
+        }
+        if reason is not None:
+            raise NotImplementedError(
+                f"fallback AR ({reason}) needs paged decode attention, which this package does not provide"
+            )
+        idx = next(i for i, r in enumerate(routes) if int(r.route_id) == int(selected.route_id))
+        path, nodes = self._truncate_selected_path(token_ids=paths[idx], node_ids=route_nodes[idx],
+                                                   max_tokens=selected_path_max_tokens, eos_token_id=eos_token_id)
+        self._commit_selected_path(token_ids=path, node_ids=nodes, verify_logits=logits)
+        return TargetVerifyResult(
+            selected_route_id=selected.route_id,
+            scores=scores,
+            metadata={
+                **common,
+                "prefix_len_after": len(self.prefix_token_ids),
+                "target_kv_commit": "selected_tree_path_in_place",
+                "target_reprefill_after_verify": False,
+                "fallback_triggered": False,
+                "selected_route_id": int(selected.route_id),
+                "selected_path_committed_tokens": len(path),
+                "selected_path_was_truncated": len(path) != len(paths[idx]),
+            },
+        )
+
+    # ------------------------------------------------------------ policies
+    @staticmethod
+    def _validate_score_weights(weights: Sequence[float] | None) -> tuple[float, ...] | None:
+        if weights is None:
+            return None
+        values = tuple(float(v) for v in weights)
+        if not values:
+            return None
+        if any(v < 0.0 for v in values):
+            raise ValueError("score weights must be non-negative")
+        total = sum(values)
+        if total <= 0.0:
+            raise ValueError("at least one score weight must be positive")
+        return tuple(v / total for v in values)
+
+    def _weights_for_depth(self, depth: int) -> tuple[float, ...] | None:
+        if self.score_weights is None:
+            return None
+        if len(self.score_weights) != int(depth):
+            raise ValueError(
+                f"score weights must match verify route depth: weights={len(self.score_weights)}, depth={int(depth)}"
+            )
+        return self.score_weights
+
+    def _selection_policy_name(self) -> str:
+        if self.route_selection_policy == "first_route":
+            return "diagnostic_first_payload_route"
+        weighted = self.score_weights is not None
+        if self.route_selection_policy == "target_sample":
+            return "sample_weighted_target_route_score_distribution" if weighted else "sample_target_route_logprob_distribution"
+        return "best_of_n_weighted_target_path_logprob" if weighted else "best_of_n_target_path_logprob"
+
+    @staticmethod
+    def _validate_route_selection_policy(policy: str) -> str:
+        value = str(policy).strip().lower()
+        if value not in ROUTE_POLICIES:
+            raise ValueError("route_selection_policy must be one of: target_best, target_sample, first_route")
+        return value
+
+    @staticmethod
+    def _validate_route_sampling_temperature(temperature: float) -> float:
+        value = float(temperature)
+        if not math.isfinite(value) or value <= 0.0:
+            raise ValueError("route_sampling_temperature must be finite and positive")
+        return value
+
+    @staticmethod
+    def _selection_score(score: TargetRouteScore) -> float:
+        return float(score.target_logprob if score.selection_score is None else score.selection_score)
+
+    def _select_route(self, scores, *, route_sampling_seed=None, route_sampling_round=None) -> TargetRouteScore:
+        return self._select_route_with_metadata(
+            scores, route_sampling_seed=route_sampling_seed, route_sampling_round=route_sampling_round
+        )[0]
+
+    def _select_route_with_metadata(self, scores, *, route_sampling_seed=None, route_sampling_round=None):
+        if not scores:
+            raise ValueError("cannot select from an empty route score list")
+        if self.route_selection_policy == "first_route":
+            return scores[0], self._route_sampling_disabled_metadata()
+        if self.route_selection_policy == "target_sample":
+            return self._sample_target_route(scores, route_sampling_seed=route_sampling_seed,
+                                             route_sampling_round=route_sampling_round)
+        best = max(scores, key=lambda s: (self._selection_score(s), s.draft_path_logprob, -s.route_id))
+        return best, self._route_sampling_disabled_metadata()
+
+    def _route_sampling_disabled_metadata(self) -> dict:
+        return {
+            "route_sampling_enabled": False,
+            "route_sampling_scope": "verified_route_level_only",
+            "route_sampling_seed": None,
+            "route_sampling_round": None,
+            "route_sampling_temperature": float(getattr(self, "route_sampling_temperature", 1.0)),
+        }
+
+    @staticmethod
+    def _token_path_hash(token_ids: Sequence[int]) -> str:
+        return hashlib.sha256(json.dumps([int(t) for t in token_ids], separators=(",", ":")).encode("utf-8")).hexdigest()
+
+    def _sample_target_route(self, scores, *, route_sampling_seed, route_sampling_round):
+        """Seeded route draw (``target_runtime.py:454-546``): canonical
+        semantic order, softmax of score / temperature, SHA-256 uniform,
+        inverse CDF."""
+        if route_sampling_seed is None or route_sampling_round is None:
+            raise ValueError(
+                "target_sample requires explicit route_sampling_seed and route_sampling_round on every verify request"
+            )
+        rnd = int(route_sampling_round)
+        if rnd < 0:
+            raise ValueError("route_sampling_round must be non-negative")
+        seed = int(route_sampling_seed)
+        ordered = sorted(
+            scores,
+            key=lambda s: (tuple(int(t) for t in s.token_ids), float(s.draft_path_logprob), self._selection_score(s),
+                           int(s.route_id)),
+        )
+        temp = float(getattr(self, "route_sampling_temperature", 1.0))
+        logits = [self._selection_score(s) / temp for s in ordered]
+        if any(math.isnan(v) for v in logits):
+            raise ValueError("cannot sample a route from NaN target scores")
+        pos_inf = [math.isinf(v) and v > 0.0 for v in logits]
+        if any(pos_inf):
+            probs = [1.0 / sum(pos_inf) if f else 0.0 for f in pos_inf]
+        else:
+            finite = [v for v in logits if math.isfinite(v)]
+            if not finite:
+                probs = [1.0 / len(ordered)] * len(ordered)
+            else:
+                top = max(finite)
+                w = [0.0 if v == -math.inf else math.exp(v - top) for v in logits]
+                probs = [x / sum(w) for x in w]
+        material = f"atlas0709-target-route-sample-v1:{seed}:{rnd}".encode("utf-8")
+        draw = (int.from_bytes(hashlib.sha256(material).digest()[:8], "big") + 0.5) / float(1 << 64)
+        last = len(ordered) - 1
+        idx, lo, hi, cum = last, 0.0, 1.0, 0.0
+        for i, p in enumerate(probs):
+            nxt = cum + p
+            if draw < nxt or i == last:
+                idx, lo, hi = i, cum, (nxt if i < last else 1.0)
+                break
+            cum = nxt
+        chosen = ordered[idx]
+        return chosen, {
+            "route_sampling_enabled": True,
+            "route_sampling_scope": "verified_route_level_only",
+            "route_sampling_seed": seed,
+            "route_sampling_round": rnd,
+            "route_sampling_temperature": temp,
+            "route_sampling_uniform": float(draw),
+            "route_sampling_selected_probability": float(probs[idx]),
+            "route_sampling_selected_cdf_low": float(lo),
+            "route_sampling_selected_cdf_high": float(hi),
+            "route_sampling_boundary_margin": float(min(draw - lo, hi - draw)),
+            "route_sampling_ordered_candidates": [
+                {"route_id": int(s.route_id), "token_path_hash": self._token_path_hash(s.token_ids),
+                 "probability": float(p)}
+                for s, p in zip(ordered, probs)
+            ],
+        }
+
+    @staticmethod
+    def _truncate_selected_path(*, token_ids, node_ids, max_tokens, eos_token_id):
+        if len(token_ids) != len(node_ids) or not token_ids:
+            raise ValueError("selected path tokens and node ids must have equal non-zero length")
+        limit = len(token_ids) if max_tokens is None else min(len(token_ids), int(max_tokens))
+        if limit <= 0:
+            raise ValueError("selected_path_max_tokens must be positive")
+        toks = [int(t) for t in token_ids[:limit]]
+        if eos_token_id is not None and int(eos_token_id) in toks:
+            toks = toks[: toks.index(int(eos_token_id)) + 1]
+        return tuple(toks), tuple(int(n) for n in node_ids[: len(toks)])
+
+    def _fallback_reason(self, selected: TargetRouteScore) -> str | None:
+        if (self.first_token_threshold is not None and selected.first_token_logprob is not None
+                and float(selected.first_token_logprob) < float(self.first_token_threshold)):
+            return "first_token_below_threshold"
+        if self.fallback_threshold is not None and self._selection_score(selected) < float(self.fallback_threshold):
+            return "path_score_below_threshold"
+        return None
+
+    # ------------------------------------------------------------ scoring
+    def _score_routes(self, *, routes, paths, prefix_logits, verify_logits, route_to_node_paths):
+        """Per-token target log-probs: token 0 of a route reads the prefix
+        logits, token t > 0 the verify row of the route's node t - 1
+        (``target_runtime.py:722-765``).  One device launch per logits tensor
+        and one device-to-host copy for all routes."""
+        first_rows, first_toks, rows, toks = [], [], [], []
+        for path, nodes in zip(paths, route_to_node_paths):
+            first_rows.append(0)
+            first_toks.append(int(path[0]))
+            for off in range(1, len(path)):
+                rows.append(int(nodes[off - 1]))
+                toks.append(int(path[off]))
+        a = gather_token_logprobs(prefix_logits, first_rows, first_toks)
+        b = gather_token_logprobs(verify_logits, rows, toks)
+        values = torch.cat((a, b)).cpu().numpy()
+        if self.match_logits_dtype_rounding and verify_logits.dtype in (torch.float16, torch.bfloat16):
+            # The reference reads log_softmax outputs in the logits dtype.
+            values = torch.from_numpy(values).to(verify_logits.dtype).float().numpy()
+        first_vals = values[: len(paths)]
+        rest = values[len(paths):]
+        scores, k = [], 0
+        for i, (route, path) in enumerate(zip(routes, paths)):
+            lps = [float(first_vals[i])]
+            for _ in range(1, len(path)):
+                lps.append(float(rest[k]))
+                k += 1
+            target = sum(lps)
+            weights = self._weights_for_depth(len(lps))
+            sel = target if weights is None else sum(w * v for w, v in zip(weights, lps))
+            scores.append(TargetRouteScore(
+                route_id=int(route.route_id), token_ids=tuple(int(t) for t in path), target_logprob=target,
+                draft_logprob=float(route.draft_logprob), token_logprobs=tuple(lps), first_token_logprob=lps[0],
+                selection_score=sel, score_weights=() if weights is None else tuple(weights),
+                draft_token_logprobs=tuple(float(v) for v in route.draft_token_logprobs),
+            ))
+        return scores
+
+    # ------------------------------------------------------------ KV state
+    def _ensure_page_capacity(self, required_pages: int) -> None:
+        """Grow every layer to ``required_pages`` pages, keeping the existing
+        pages (``target_runtime.py:858-871``)."""
+        if self._paged_prefix_kv is None:
+            raise RuntimeError("target prefill must initialize paged prefix KV")
+        required_pages = int(required_pages)
+        grown = []
+        for layer_kv in self._paged_prefix_kv:
+            if int(layer_kv.shape[0]) >= required_pages:
+                grown.append(layer_kv)
+                continue
+            expanded = torch.zeros((required_pages, *layer_kv.shape[1:]), dtype=layer_kv.dtype, device=layer_kv.device)
+            expanded[: int(layer_kv.shape[0])].copy_(layer_kv)
+            grown.append(expanded)
+        self._paged_prefix_kv = grown
+
+    def _commit_selected_path(self, *, token_ids, node_ids, verify_logits) -> None:
+        """Compact the selected nodes' KV into the committed prefix (every
+        layer, one launch), extend the prefix and keep the last node's logits
+        as the next prefix logits (``target_runtime.py:873-920``)."""
+        if self._paged_prefix_kv is None:
+            raise RuntimeError("target paged prefix KV is not initialized")
+        if len(token_ids) != len(node_ids) or not node_ids:
+            raise ValueError("selected path tokens and node ids must have equal non-zero length")
+        prefix_len = len(self.prefix_token_ids)
+        src = [prefix_len + int(n) for n in node_ids]
+        dst = list(range(prefix_len, prefix_len + len(node_ids)))
+        kv_ops.commit_paged(self._paged_prefix_kv, src, dst)
+        self.prefix_token_ids = (*self.prefix_token_ids, *(int(t) for t in token_ids))
+        self._prefix_logits = verify_logits[int(node_ids[-1])].detach().unsqueeze(0)
+        self._committed_verify_rounds += 1
+
+
+def _legacy_layer_kv(past, layer_idx: int):
+    if hasattr(past, "layers"):
+        layer = past.layers[layer_idx]
+        for kn, vn in (("keys", "values"), ("key_cache", "value_cache")):
+            if hasattr(layer, kn):
+                return getattr(layer, kn), getattr(layer, vn)
+    if hasattr(past, "key_cache"):
+        return past.key_cache[layer_idx], past.value_cache[layer_idx]
+    if hasattr(past, "to_legacy_cache"):
+        legacy = past.to_legacy_cache()
+        return legacy[layer_idx][0], legacy[layer_idx][1]
+    return past[layer_idx][0], past[layer_idx][1]

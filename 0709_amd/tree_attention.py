@@ -23,7 +23,9 @@ from . import _lib
 
 TILE_KEYS = 64
 MAX_ROWS_PER_ITEM = 192  # 4 waves x 3 row tiles of 16
+DEFAULT_ROWS_PER_ITEM = 64  # 4 waves x 1 row tile: 3 workgroups per CU
 MAX_TREE_WIDTH = 64
+MAX_SPLITS = 1024
 DEFAULT_CU_COUNT = 256
 
 
@@ -127,6 +129,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._plan: AttentionPlan | None = None
         self.split_target_items = 2 * DEFAULT_CU_COUNT
         self.min_tiles_per_split = 1
+        self.max_rows_per_item = DEFAULT_ROWS_PER_ITEM
+        self._meta_buf: torch.Tensor | None = None
+        self._indices_buf: torch.Tensor | None = None
+        self._bits_buf: torch.Tensor | None = None
 
     @property
     def device(self) -> torch.device:
@@ -231,13 +237,22 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
         # ---- work decomposition ----
         group = hq // hkv
+        row_block = max(16, min(MAX_ROWS_PER_ITEM, int(self.max_rows_per_item)))
         blocks = []  # (req, row_start, num_rows)
         for b in range(batch):
             rows = qo_lens[b] * group
-            for r0 in range(0, rows, MAX_ROWS_PER_ITEM):
-                blocks.append((b, r0, min(MAX_ROWS_PER_ITEM, rows - r0)))
+            nblk = max(1, math.ceil(rows / row_block))
+            # equal-sized blocks, each a multiple of 16 rows where possible
+            size = min(row_block, 16 * math.ceil(math.ceil(rows / nblk) / 16)) if rows else 0
+            for r0 in range(0, rows, max(size, 1)):
+                blocks.append((b, r0, min(size, rows - r0)))
+            if rows == 0:
+                blocks.append((b, 0, 0))
         unit_tiles = sum(hkv * math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks)
         tiles_per_split = max(self.min_tiles_per_split, math.ceil(unit_tiles / max(1, self.split_target_items)))
+        # the merge kernel combines at most MAX_SPLITS states per row
+        max_tiles = max((math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks), default=0)
+        tiles_per_split = max(tiles_per_split, math.ceil(max_tiles / MAX_SPLITS))
         ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // (4 * (d + 1))
         while True:
             work, merge = [], []
@@ -261,8 +276,6 @@ class BatchPrefillWithPagedKVCacheWrapper:
             tiles_per_split *= 2
         max_rows = max((nr for (_, _, nr) in blocks), default=1)
 
-        # Interleave work items so consecutive workgroups (spread round-robin
-        # over the XCDs) come from different KV heads and splits.
         meta_vals: list[int] = []
         for item in work:
             meta_vals.extend(item)
@@ -273,21 +286,43 @@ class BatchPrefillWithPagedKVCacheWrapper:
         meta_vals.extend(kv_lens)
         col_off = len(meta_vals)
         meta_vals.extend(cols)
-        meta = torch.tensor(meta_vals, dtype=torch.int32).to(device, non_blocking=non_blocking)
+        qo_off = len(meta_vals)
+        meta_vals.extend(qo)
+        kvp_off = len(meta_vals)
+        meta_vals.extend(kvp)
+        # Persistent device buffers keep their addresses across plans, so a
+        # HIP graph captured over run() stays valid after a re-plan of the
+        # same (or a smaller) shape.
+        meta = self._persistent("_meta_buf", len(meta_vals), torch.int32)
+        meta[: len(meta_vals)].copy_(torch.tensor(meta_vals, dtype=torch.int32), non_blocking=non_blocking)
+        indices_src = paged_kv_indices.reshape(-1)
+        n_idx = int(indices_src.numel())
+        indices = self._persistent("_indices_buf", n_idx, torch.int32)
+        if n_idx:
+            indices[:n_idx].copy_(indices_src.to(device=device, dtype=torch.int32), non_blocking=non_blocking)
+        bits_buf = None
+        if tree_bits is not None:
+            nb = int(tree_bits.numel())
+            bits_buf = self._persistent("_bits_buf", nb, torch.int64)
+            if nb:
+                bits_buf[:nb].copy_(tree_bits, non_blocking=non_blocking)
 
         self._plan = AttentionPlan(
             batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,
             sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
             q_dtype=q_dtype, kv_dtype=kv_dtype, nnz=qo[-1] - qo[0] if batch else 0, mask_mode=mask_mode,
-            qo_indptr=qo_indptr.to(device=device, dtype=torch.int32).contiguous()
-            if isinstance(qo_indptr, torch.Tensor) else torch.tensor(qo, dtype=torch.int32, device=device),
-            kv_indptr=paged_kv_indptr.to(device=device, dtype=torch.int32).contiguous()
-            if isinstance(paged_kv_indptr, torch.Tensor) else torch.tensor(kvp, dtype=torch.int32, device=device),
-            kv_indices=paged_kv_indices.to(device=device, dtype=torch.int32).contiguous(),
-            tree_mask=tree_bits, meta=meta, num_work=len(work), num_merge=len(merge), work_offset=0,
+            qo_indptr=meta[qo_off:], kv_indptr=meta[kvp_off:], kv_indices=indices,
+            tree_mask=bits_buf, meta=meta, num_work=len(work), num_merge=len(merge), work_offset=0,
             merge_offset=merge_off, kv_len_offset=kvlen_off, col_offset=col_off, max_rows=max_rows,
             partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=tiles_per_split,
         )
+
+    def _persistent(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:
+        buf = getattr(self, name, None)
+        if buf is None or int(buf.numel()) < count or buf.dtype != dtype:
+            buf = torch.empty(max(count, 1024), dtype=dtype, device=self.device)
+            setattr(self, name, buf)
+        return buf
 
     @staticmethod
     def _unpack_segments(packed: torch.Tensor, qo_lens: list[int], kv_lens: list[int]) -> torch.Tensor:

@@ -1,0 +1,122 @@
+"""Seeded synthetic inputs of the paged-KV tree path's benchmark configurations.
+
+Every generator draws from ``torch.Generator`` seeds so the HIP path and the
+CPU checker see identical inputs.  Geometry names:
+
+* ``LLAMA_8B``  -- 32 layers, 32 query heads, 8 KV heads, head_dim 128;
+* ``LLAMA_1B``  -- 16 layers, 32 query heads, 8 KV heads, head_dim 64.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+from typing import Sequence
+
+import torch
+
+VOCAB = 128256
+
+
+@dataclass(frozen=True)
+class Geometry:
+    layers: int
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+
+    @property
+    def group(self) -> int:
+        return self.q_heads // self.kv_heads
+
+    def token_bytes(self, elem: int = 2) -> int:
+        """K + V bytes of one token in one layer."""
+        return 2 * self.kv_heads * self.head_dim * elem
+
+
+LLAMA_8B = Geometry(32, 32, 8, 128)
+LLAMA_1B = Geometry(16, 32, 8, 64)
+
+
+def tree_routes(seed: int, k: int = 3, depth: int = 4) -> list[tuple[int, ...]]:
+    """k independent routes of ``depth`` random token ids (no shared prefix)."""
+    gen = torch.Generator().manual_seed(seed)
+    return [tuple(int(x) for x in torch.randint(0, VOCAB, (depth,), generator=gen)) for _ in range(k)]
+
+
+def forest_routes(seed: int, k: int = 3, depth: int = 4) -> list[tuple[int, ...]]:
+    """k * k routes by seeded branching: k stage-1 roots, each forking into k
+    routes that share a random-length prefix (0 .. depth-1 tokens) with their
+    root.  Deduplication leaves at most k * k * depth nodes."""
+    gen = torch.Generator().manual_seed(seed)
+    roots = [[int(x) for x in torch.randint(0, VOCAB, (depth,), generator=gen)] for _ in range(k)]
+    routes = []
+    for i in range(k):
+        for _ in range(k):
+            shared = int(torch.randint(0, depth, (1,), generator=gen))
+            tail = [int(x) for x in torch.randint(0, VOCAB, (depth - shared,), generator=gen)]
+            routes.append(tuple(roots[i][:shared] + tail))
+    return routes
+
+
+@dataclass
+class PagedTargetKV:
+    """One request's Target KV in a paged pool, all layers in one allocation.
+
+    ``pool[l]`` is layer l's ``[pool_pages, 2, page_size, Hkv, D]`` view; the
+    request's pages are ``kv_indices`` (a random permutation of pool pages).
+    """
+
+    pool: torch.Tensor  # [L, pool_pages, 2, ps, Hkv, D]
+    kv_indices: torch.Tensor  # int32 [pages]
+    page_size: int
+
+    @property
+    def layers(self) -> list[torch.Tensor]:
+        return list(self.pool.unbind(0))
+
+
+def make_paged_target_kv(
+    geom: Geometry,
+    *,
+    kv_len: int,
+    page_size: int,
+    dtype: torch.dtype,
+    device: torch.device,
+    seed: int = 0,
+    spare_pages: int = 0,
+    scale: float = 0.1,
+) -> PagedTargetKV:
+    pages = math.ceil(kv_len / page_size)
+    pool_pages = pages + spare_pages
+    gen = torch.Generator(device=device).manual_seed(seed)
+    pool = torch.empty((geom.layers, pool_pages, 2, page_size, geom.kv_heads, geom.head_dim), dtype=dtype,
+                       device=device)
+    for l in range(geom.layers):
+        pool[l].copy_(torch.randn(pool[l].shape, generator=gen, device=device, dtype=torch.float32) * scale)
+    perm_gen = torch.Generator().manual_seed(seed + 1)
+    kv_indices = torch.randperm(pool_pages, generator=perm_gen)[:pages].to(torch.int32).to(device)
+    return PagedTargetKV(pool=pool, kv_indices=kv_indices, page_size=page_size)
+
+
+def random_queries(geom: Geometry, n: int, *, dtype: torch.dtype, device: torch.device, seed: int,
+                   scale: float = 0.1) -> list[torch.Tensor]:
+    gen = torch.Generator(device=device).manual_seed(seed)
+    return [
+        (torch.randn((n, geom.q_heads, geom.head_dim), generator=gen, device=device) * scale).to(dtype)
+        for _ in range(geom.layers)
+    ]
+
+
+def verify_attention_bytes(geom: Geometry, *, kv_len: int, nodes: int, page_size: int, elem: int = 2) -> int:
+    """Algorithmic HBM bytes of one layer's verify attention: K and V of every
+    key once, Q read and O written once, fp32 LSE, page indices, one 64-bit
+    ancestor mask word per node."""
+    kv = kv_len * geom.kv_heads * geom.head_dim * elem * 2
+    qo = 2 * nodes * geom.q_heads * geom.head_dim * elem
+    return kv + qo + nodes * geom.q_heads * 4 + 4 * math.ceil(kv_len / page_size) + 8 * nodes
+
+
+def verify_attention_flops(geom: Geometry, visible_keys: Sequence[int]) -> int:
+    """4 * Hq * D flops per visible (query, key) pair (QK^T and PV)."""
+    return 4 * geom.q_heads * geom.head_dim * int(sum(visible_keys))

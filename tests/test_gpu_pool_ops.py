@@ -1,0 +1,193 @@
+"""Prune / ownership / allocator-slot / paged-metadata kernels vs the oracle
+(bit-exact integer results)."""
+
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import pkg
+from oracle import paged_kv as ref
+
+pytestmark = pytest.mark.gpu
+
+
+def _lib():
+    return pkg("_lib")
+
+
+def _bitmap(pages_set, num_pages, dev):
+    words = np.zeros((num_pages + 31) // 32, dtype=np.uint32)
+    for p in pages_set:
+        words[p >> 5] |= np.uint32(1 << (p & 31))
+    return torch.from_numpy(words.view(np.int32)).to(dev)
+
+
+def _set_from_bitmap(bm):
+    w = bm.cpu().numpy().view(np.uint32)
+    return {i * 32 + b for i, x in enumerate(w) for b in range(32) if (int(x) >> b) & 1}
+
+
+def _prune(dev, owned, live_slots, num_pages, ps):
+    lib = _lib()
+    owned_bm = _bitmap(owned, num_pages, dev)
+    live_bm = torch.zeros_like(owned_bm)
+    free = torch.full((num_pages,), -1, dtype=torch.int64, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+    slots = torch.tensor(live_slots, dtype=torch.int64, device=dev)
+    rc = lib.load().atlas_prune_pages(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, lib.ptr(slots),
+                                      len(live_slots), ps, lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev))
+    lib.check(rc, "prune")
+    torch.cuda.synchronize()
+    n = int(cnt.item())
+    return free[:n].cpu().tolist(), _set_from_bitmap(owned_bm)
+
+
+def test_prune_reference_literal(dev):
+    # tests/test_tail_page_cow.py:241-277 -> freed page 11 (slot 44), owned {0, 10}
+    prefix = [0, 1, 40]
+    route = [0, 1, 40, 41]
+    sampled = prefix[::4] + route[::4] + route[-1:]
+    freed, owned = _prune(dev, {0, 10, 11}, sampled, 64, 4)
+    assert freed == [11] and owned == {0, 10}
+    assert [p * 4 for p in freed] == [44]
+
+
+@pytest.mark.parametrize("num_pages", [1, 31, 32, 33, 4096, 95367])
+def test_prune_random_matches_oracle(dev, num_pages):
+    rng = np.random.default_rng(num_pages)
+    ps = 16
+    owned = set(rng.choice(num_pages, size=min(num_pages, 3000), replace=False).tolist())
+    paths = []
+    for _ in range(9):
+        pages = rng.choice(num_pages, size=min(num_pages, 8), replace=False)
+        length = int(rng.integers(1, len(pages) * ps + 1))
+        paths.append([int(pages[i // ps]) * ps + i % ps for i in range(length)])
+    sampled = [s for p in paths for s in (p[::ps] + p[-1:])]
+    freed, left = _prune(dev, owned, sampled, num_pages, ps)
+    exp_freed, exp_left = ref.prune(owned, None, paths, ps)
+    assert freed == exp_freed and left == exp_left
+
+
+def test_prune_empty_live_frees_everything_ascending(dev):
+    owned = {5, 3, 900, 64, 31, 32}
+    freed, left = _prune(dev, owned, [], 1000, 16)
+    assert freed == sorted(owned) and left == set()
+
+
+def test_mark_pages(dev):
+    lib = _lib()
+    bm = torch.zeros(4, dtype=torch.int32, device=dev)
+    slots = torch.tensor([0, 17, 18, 127, 64, -1, 5000], dtype=torch.int64, device=dev)
+    rc = lib.load().atlas_mark_pages(lib.ptr(bm), 120, lib.ptr(slots), 7, 16, lib.stream_of(dev))
+    lib.check(rc, "mark")
+    torch.cuda.synchronize()
+    # slot -> page: 0, 1, 1, 7, 4; -1 and page 312 (>= 120) are ignored
+    assert _set_from_bitmap(bm) == {0, 1, 4, 7}
+
+
+def test_alloc_decode_and_extend_match_allocator_policy(dev):
+    lib = _lib()
+    ps = 16
+    rng = np.random.default_rng(7)
+    free_pages = [int(x) for x in rng.permutation(np.arange(1, 200))]
+    alloc = ref.PagedAllocator(num_pages=199, page_size=ps)
+    alloc.free_pages = list(free_pages)
+    seq = [int(x) for x in rng.integers(1, 300, size=70)]
+    last = [int(x) for x in rng.integers(0, 4000, size=70)]
+    expect = alloc.alloc_decode(seq, last)
+    fp = torch.tensor(free_pages, dtype=torch.int64, device=dev)
+    out = torch.empty(70, dtype=torch.int64, device=dev)
+    # Keep every argument tensor referenced until the launch is enqueued: a
+    # temporary freed earlier can be handed to the next upload.
+    seq_t = torch.tensor(seq, device=dev)
+    last_t = torch.tensor(last, device=dev)
+    rc = lib.load().atlas_alloc_decode_slots(lib.ptr(seq_t), lib.ptr(last_t), lib.ptr(fp), ps, 70, lib.ptr(out),
+                                             lib.stream_of(dev))
+    lib.check(rc, "alloc_decode")
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == expect
+    # extend
+    alloc2 = ref.PagedAllocator(num_pages=199, page_size=ps)
+    alloc2.free_pages = list(free_pages)
+    pre = [int(x) for x in rng.integers(0, 100, size=9)]
+    seqe = [p + int(x) for p, x in zip(pre, rng.integers(1, 70, size=9))]
+    laste = [int(rng.integers(1, 100)) * ps + (p - 1) % ps if p else -1 for p in pre]
+    expect = alloc2.alloc_extend(pre, seqe, laste)
+    n = sum(s - p for p, s in zip(pre, seqe))
+    out = torch.empty(n, dtype=torch.int64, device=dev)
+    pre_t = torch.tensor(pre, device=dev)
+    seqe_t = torch.tensor(seqe, device=dev)
+    laste_t = torch.tensor(laste, device=dev)
+    rc = lib.load().atlas_alloc_extend_slots(lib.ptr(pre_t), lib.ptr(seqe_t), lib.ptr(laste_t), lib.ptr(fp), ps, 9,
+                                             lib.ptr(out), lib.stream_of(dev))
+    lib.check(rc, "alloc_extend")
+    torch.cuda.synchronize()
+    assert out.cpu().tolist() == expect
+
+
+def _slot_path(page_ids, length, page_size=16):
+    return [p * page_size + o for p in page_ids for o in range(page_size)][:length]
+
+
+def test_paged_metadata_reference_literals(dev):
+    # tests/test_paged_attention_metadata.py:24-52
+    pm = pkg("flashinfer_paged.paged_metadata")
+    lengths = [1, 15, 16, 17, 31, 32]
+    paths = [torch.tensor(_slot_path([11 + 3 * i, 31 + 5 * i], n), device=dev) for i, n in enumerate(lengths)]
+    md = pm.build_flashinfer_paged_kv_metadata(paths, page_size=16)
+    counts = [(n + 15) // 16 for n in lengths]
+    assert md.kv_indptr.tolist() == list(itertools.accumulate([0] + counts))
+    assert md.kv_last_page_len.tolist() == [1, 15, 16, 1, 15, 16]
+    assert md.seq_lens.tolist() == lengths
+    assert md.token_index_count == sum(lengths) and md.page_index_count == sum(counts)
+    assert md.layout_validated
+    md.assert_layout_valid()
+    exp = ref.paged_metadata([p.tolist() for p in paths], 16)
+    assert md.kv_page_indices.tolist() == exp.kv_page_indices
+    long = torch.tensor(_slot_path(list(range(100, 612)), 8192), device=dev)
+    md = pm.build_flashinfer_paged_kv_metadata([long], page_size=16, sync_check=True)
+    assert md.token_index_count == 8192 and md.page_index_count == 512
+    assert md.kv_indptr.tolist() == [0, 512] and md.kv_last_page_len.tolist() == [16]
+
+
+@pytest.mark.parametrize("bad", [[161, 162, 163], [160, 161, 165], list(range(160, 176)) + [193]])
+def test_paged_metadata_invalid_layout_raises_on_check(dev, bad):
+    # tests/test_paged_attention_metadata.py:55-67 (raised on the host, no device assert)
+    pm = pkg("flashinfer_paged.paged_metadata")
+    md = pm.build_flashinfer_paged_kv_metadata([torch.tensor(bad, device=dev)], page_size=16)
+    with pytest.raises(RuntimeError, match="page-aligned"):
+        md.assert_layout_valid()
+    with pytest.raises(RuntimeError):
+        pm.build_flashinfer_paged_kv_metadata([torch.tensor(bad, device=dev)], page_size=16, sync_check=True)
+
+
+def test_paged_metadata_random_paths_match_oracle(dev):
+    pm = pkg("flashinfer_paged.paged_metadata")
+    rng = np.random.default_rng(9)
+    for ps in (1, 4, 16, 64):
+        paths = []
+        for _ in range(72):
+            pages = rng.choice(5000, size=6, replace=False)
+            length = int(rng.integers(1, 6 * ps + 1))
+            paths.append(_slot_path([int(x) for x in pages], length, ps))
+        md = pm.build_flashinfer_paged_kv_metadata([torch.tensor(p, device=dev) for p in paths], page_size=ps,
+                                                   sync_check=True)
+        exp = ref.paged_metadata(paths, ps)
+        assert md.kv_page_indices.tolist() == exp.kv_page_indices
+        assert md.kv_indptr.tolist() == exp.kv_indptr
+        assert md.kv_last_page_len.tolist() == exp.kv_last_page_len
+        assert md.seq_lens.tolist() == exp.seq_lens
+
+
+def test_paged_metadata_argument_errors(dev):
+    pm = pkg("flashinfer_paged.paged_metadata")
+    with pytest.raises(ValueError):
+        pm.build_flashinfer_paged_kv_metadata([torch.tensor([0], device=dev)], page_size=0)
+    with pytest.raises(ValueError):
+        pm.build_flashinfer_paged_kv_metadata([], page_size=16)
+    with pytest.raises(TypeError):
+        pm.build_flashinfer_paged_kv_metadata([torch.tensor([0.0], device=dev)], page_size=16)
+    with pytest.raises(ValueError):
+        pm.build_flashinfer_paged_kv_metadata([torch.zeros(0, dtype=torch.long, device=dev)], page_size=16)

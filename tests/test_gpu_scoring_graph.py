@@ -1,0 +1,171 @@
+"""Route scoring kernel vs the oracle, Target commit/scoring drop-in methods,
+and HIP-graph replays of the verify forward vs its eager result."""
+
+import math
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import bits16, pkg
+from oracle import paged_kv as ref
+from oracle import scoring as osc
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_gather_logprobs_matches_oracle(dev, dtype):
+    tr = pkg("target_runtime")
+    gen = torch.Generator().manual_seed(0)
+    logits = (torch.randn((36, 128256), generator=gen) * 3).to(dtype)
+    rows = [int(x) for x in torch.randint(0, 36, (40,), generator=gen)]
+    toks = [int(x) for x in torch.randint(0, 128256, (40,), generator=gen)]
+    out = tr.gather_token_logprobs(logits.to(dev), rows, toks).cpu().numpy()
+    lp = osc.log_softmax(logits.double().numpy())
+    exp = np.array([lp[r, t] for r, t in zip(rows, toks)])
+    assert np.abs(out - exp).max() <= 2e-4  # fp32 accumulation over 128256 logits
+
+
+def _backend(tr, **attrs):
+    b = object.__new__(tr.DirectFlashInferMaskedTreeVerifyBackend)
+    b.score_weights = None
+    b.route_selection_policy = "target_best"
+    b.route_sampling_temperature = 1.0
+    b.match_logits_dtype_rounding = True
+    for k, v in attrs.items():
+        setattr(b, k, v)
+    return b
+
+
+def test_score_routes_reference_literal(dev):
+    # tests/test_target_kv_commit.py:76-103 (float32 logits)
+    tr = pkg("target_runtime")
+    b = _backend(tr)
+    prefix = torch.tensor([0.0, 3.0, 0.0, 0.0], device=dev)
+    verify = torch.tensor([[0.0, 0.0, 4.0, 2.0], [0, 0, 0, 0], [0, 0, 0, 0]], device=dev)
+    routes = [tr.VerifyRoutePayload(1, (1, 2), -1.0), tr.VerifyRoutePayload(2, (1, 3), -2.0)]
+    scores = b._score_routes(routes=routes, paths=[r.token_ids for r in routes], prefix_logits=prefix,
+                             verify_logits=verify, route_to_node_paths=[[0, 1], [0, 2]])
+    plp = torch.log_softmax(prefix.cpu(), -1)[1].item()
+    vlp = torch.log_softmax(verify[0].cpu(), -1)
+    assert abs(scores[0].target_logprob - (plp + vlp[2].item())) < 1e-6
+    assert abs(scores[1].target_logprob - (plp + vlp[3].item())) < 1e-6
+    assert b._select_route(scores).route_id == 1
+
+
+def test_score_routes_forest_matches_oracle_and_selection(dev):
+    tr = pkg("target_runtime")
+    wl = pkg("workloads")
+    b = _backend(tr)
+    routes = wl.forest_routes(3)
+    _, _, _, nodes = ref.dedup_tree(routes)
+    n = max(max(x) for x in nodes) + 1
+    gen = torch.Generator().manual_seed(1)
+    verify = (torch.randn((n, 128256), generator=gen) * 2).half()
+    prefix = (torch.randn((128256,), generator=gen) * 2).half()
+    # plant the scored tokens so the routes differ clearly
+    payloads = [tr.VerifyRoutePayload(i, r, -float(i)) for i, r in enumerate(routes)]
+    scores = b._score_routes(routes=payloads, paths=routes, prefix_logits=prefix.to(dev), verify_logits=verify.to(dev),
+                             route_to_node_paths=nodes)
+    # the reference reads fp16 log_softmax outputs: compare to the oracle rounded the same way
+    lps = osc.route_token_logprobs(routes, nodes, prefix.double().numpy(), verify.double().numpy())
+    for s, exact in zip(scores, lps):
+        rounded = np.array(exact, dtype=np.float16).astype(np.float64)
+        assert np.abs(np.array(s.token_logprobs) - rounded).max() <= 2e-3
+        assert np.abs(np.array(s.token_logprobs) - np.array(exact)).max() <= 2e-3 + 2 ** -7
+    best = osc.select_best([dict(route_id=s.route_id, selection_score=s.selection_score,
+                                 draft_path_logprob=s.draft_path_logprob, token_ids=s.token_ids) for s in scores])
+    assert b._select_route(scores).route_id == best["route_id"]
+
+
+def test_commit_selected_path_reference_literal(dev):
+    # tests/test_target_kv_commit.py:13-45 on fp16 rows (D = 8 for 16-byte rows)
+    tr = pkg("target_runtime")
+    b = _backend(tr)
+    b.config = SimpleNamespace(page_size=4)
+    b.prefix_token_ids = (1, 2, 3)
+    b._prefix_logits = torch.zeros((1, 8), device=dev)
+    b._committed_verify_rounds = 0
+    cache = torch.zeros((2, 2, 4, 1, 8), dtype=torch.float16)
+    for pos in range(8):
+        page, off = divmod(pos, 4)
+        cache[page, 0, off] = 100 + pos
+        cache[page, 1, off] = 200 + pos
+    b._paged_prefix_kv = [cache.to(dev)]
+    logits = torch.arange(32, dtype=torch.float32, device=dev).reshape(4, 8)
+    b._commit_selected_path(token_ids=(9, 10), node_ids=(0, 2), verify_logits=logits)
+    c = b._paged_prefix_kv[0].cpu()
+    assert c[0, 0, 3, 0, 0].item() == 103 and c[1, 0, 0, 0, 0].item() == 105
+    assert c[0, 1, 3, 0, 0].item() == 203 and c[1, 1, 0, 0, 0].item() == 205
+    assert b.prefix_token_ids == (1, 2, 3, 9, 10)
+    assert torch.equal(b._prefix_logits, logits[2].unsqueeze(0))
+    assert b._committed_verify_rounds == 1
+    b._ensure_page_capacity(4)
+    assert b._paged_prefix_kv[0].shape[0] == 4 and torch.equal(b._paged_prefix_kv[0][:2].cpu(), c)
+    with pytest.raises(ValueError):
+        b._commit_selected_path(token_ids=(1,), node_ids=(), verify_logits=logits)
+
+
+def test_graph_replays_match_eager_forward(dev):
+    """Capture append + attention over 4 layers, replay it several times with
+    eager work and synchronisations in between; every replay equals eager."""
+    ffv = pkg("flashinfer_full_verify")
+    kv_ops = pkg("kv_ops")
+    wl = pkg("workloads")
+    geom = wl.Geometry(4, 32, 8, 128)
+    routes = wl.forest_routes(1)
+    prefix_len, ps = 3000, 16
+    spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=routes, prefix_len=prefix_len, page_size=ps, device=dev)
+    n = spec.node_count
+    kv = wl.make_paged_target_kv(geom, kv_len=prefix_len + n, page_size=ps, dtype=torch.float16, device=dev,
+                                 seed=3, spare_pages=9)
+    layers = kv.layers
+    q = wl.random_queries(geom, n, dtype=torch.float16, device=dev, seed=4)
+    g = torch.Generator(device=dev).manual_seed(5)
+    kn = [(torch.randn((n, 8, 128), generator=g, device=dev) * 0.1).half() for _ in range(4)]
+    vn = [(torch.randn((n, 8, 128), generator=g, device=dev) * 0.1).half() for _ in range(4)]
+    pages = math.ceil((prefix_len + n) / ps)
+    idx = kv.kv_indices.cpu().long()
+    pos = torch.arange(prefix_len, prefix_len + n)
+    slots = (idx[pos // ps] * ps + pos % ps).to(dev)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    w = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+
+    def plan():
+        w.plan(spec.qo_indptr, torch.tensor([0, pages], dtype=torch.int32, device=dev), kv.kv_indices,
+               torch.tensor([prefix_len + n - (pages - 1) * ps], dtype=torch.int32, device=dev), 32, 8, 128, ps,
+               custom_mask=spec.bool_mask, q_data_type=torch.float16)
+
+    outs = [torch.empty_like(x) for x in q]
+
+    def forward():
+        for l in range(4):
+            kv_ops.append_paged([layers[l]], [kn[l]], [vn[l]], dst_slots=slots)
+            w.run(q[l], layers[l], out=outs[l])
+
+    plan()
+    forward()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    eager_kv = kv.pool.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        forward()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        forward()
+    for rep in range(4):
+        for o in outs:
+            o.zero_()
+        plan()  # re-plan into the persistent buffers between replays
+        scratch = torch.randn(1 << 20, device=dev).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float(scratch) == float(scratch)
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), f"replay {rep} differs from eager"
+        assert torch.equal(kv.pool, eager_kv)

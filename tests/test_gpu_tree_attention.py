@@ -73,13 +73,15 @@ def _build(dev, *, seed, prefix_len, routes, hq=32, hkv=8, d=128, ps=16, dtype=t
                 hq=hq, hkv=hkv, d=d, ps=ps, dtype=dtype, route_nodes=route_nodes)
 
 
-def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL):
+def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL, max_rows=None):
     ta = pkg("tree_attention")
     ffv = pkg("flashinfer_full_verify")
     ws = torch.empty(128 * 1024 * 1024, dtype=torch.uint8, device=dev)
     w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
     if split_target is not None:
         w.split_target_items = split_target
+    if max_rows is not None:
+        w.max_rows_per_item = max_rows
     last = ffv.last_page_len(c["kv_len"], c["ps"])
     mask_kw = (
         {"packed_custom_mask": ffv.packbits(c["spec"].bool_mask, bitorder="little")}
@@ -145,6 +147,17 @@ def test_forest_16k_prefix_dominant_tree_all_split_levels(dev, split_target):
         assert plan.num_merge == 0
     if split_target >= 512:
         assert plan.num_merge > 0
+
+
+@pytest.mark.parametrize("max_rows", [16, 48, 64, 100, 192])
+def test_row_blocking_variants(dev, max_rows):
+    """Rows of a KV head split over several work items (each re-reading the
+    keys) give the same result as one block."""
+    gen = torch.Generator().manual_seed(21)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=21, prefix_len=2000, routes=routes, dominant_tree=True)
+    w, _, _ = _run_and_check(dev, c, max_rows=max_rows)
+    assert w.current_plan.max_rows <= max(16, max_rows)
 
 
 def test_forest_16k_unit_scale(dev):
