@@ -1,0 +1,264 @@
+"""Drafter route-pool fork workload: seeded fork / decode / promote / prune /
+fallback-EXTEND sequences driven through the route-pool bridge.
+
+One request = one ``KVTreeStore`` + one ``SGLangRoutePoolBridge`` + one
+frontier backend; all requests share one allocator, KV pool and request-row
+pool, as the Drafter's requests share SGLang's pools.  The model is replaced
+by an executor that writes, for every new token, a K/V row pattern derived
+from a value id (``kv_pattern``), so the KV content of every slot is known
+exactly: slot s holds the pattern of the value id last written or moved to it.
+
+The sequence per request (``run``):
+
+1. prefill ``prefix_len`` tokens (``alloc_extend`` from an empty prefix);
+2. ``steps`` frontier decode steps; before step t every active route forks
+   into ``forks[t]`` children (forks happen at arbitrary fill levels of the
+   shared tail page, so the children's first frontier copies the tail);
+3. commit a route (an ancestor of a random final route at depth
+   ``commit_depth``), keep its descendants, promote, prune;
+4. ``post_steps`` decode steps of the kept routes;
+5. fallback EXTEND: drop every route, prune, append ``extend_tokens``
+   known tokens to the prefix with one EXTEND, then decode ``post_steps``
+   steps from a fresh root.
+"""
+
+from __future__ import annotations
+
+import random
+from dataclasses import dataclass, field
+from typing import Any, Callable, Sequence
+
+import torch
+
+from .flashinfer_paged.kv import KVTreeStore
+from .flashinfer_paged.sglang_runtime import SGLangFlashInferFrontierModelBackend, SGLangRoutePoolBridge
+from .flashinfer_paged.types import DecodePhase, RouteState
+
+VOCAB = 128256
+
+
+def kv_pattern(value_ids: torch.Tensor, layer: int, kv: int, heads: int, head_dim: int) -> torch.Tensor:
+    """int16 row pattern [n, heads, head_dim] of each value id (a 64-bit
+    multiply-xorshift hash; identical on every device)."""
+    v = value_ids.to(torch.int64).reshape(-1, 1, 1)
+    h = torch.arange(heads, dtype=torch.int64, device=v.device).reshape(1, -1, 1)
+    d = torch.arange(head_dim, dtype=torch.int64, device=v.device).reshape(1, 1, -1)
+    x = v * 0x9E3779B1 + (layer * 2 + kv) * 0x85EBCA77 + h * 0xC2B2AE3D + d * 0x27D4EB2F
+    x = x ^ (x >> 15)
+    x = x * 0x2C1B3C6D
+    x = x ^ (x >> 12)
+    x = x & 0xFFFF
+    return (x - ((x >> 15) << 16)).to(torch.int16)
+
+
+@dataclass(frozen=True)
+class ForkPlan:
+    prefix_len: int
+    steps: int
+    forks: dict[int, int]
+    commit_depth: int
+    post_steps: int
+    extend_tokens: tuple[int, ...]
+    seed: int
+
+
+def config1_plans(seed: int = 0) -> list[ForkPlan]:
+    """1000-token prefix (tail page holds 8 at page 16), k=3 routes of depth 4
+    forking at the prefix; commit one whole route, keep it."""
+    rng = random.Random(seed)
+    return [ForkPlan(prefix_len=1000, steps=4, forks={0: 3}, commit_depth=4, post_steps=1,
+                     extend_tokens=tuple(rng.randrange(VOCAB) for _ in range(4)), seed=seed)]
+
+
+def config5_plans(n_requests: int = 8, page_size: int = 64, seed: int = 0) -> list[ForkPlan]:
+    """8 requests, 9 routes each from two 3-way forks at random depths, 8
+    decode steps; commit the second-level fork point, keep its 3 children."""
+    rng = random.Random(seed)
+    plans = []
+    for r in range(n_requests):
+        prefix = rng.randrange(2 * page_size, 16 * page_size)
+        if prefix % page_size == 0:
+            prefix += 1 + rng.randrange(page_size - 1)
+        a = rng.randrange(1, 4)
+        b = rng.randrange(1, 4)
+        plans.append(ForkPlan(prefix_len=prefix, steps=8, forks={a: 3, a + b: 3}, commit_depth=a + b, post_steps=1,
+                              extend_tokens=tuple(rng.randrange(VOCAB) for _ in range(4)), seed=seed * 1000 + r))
+    return plans
+
+
+class PatternExecutor:
+    """Stands in for the Drafter model: writes each new token's K/V pattern
+    and returns zero logits.  ``writer(slots, value_ids)`` stores the rows."""
+
+    def __init__(self, writer: Callable[[torch.Tensor, torch.Tensor], None], ids: "ValueIds", vocab: int = 8) -> None:
+        self.writer = writer
+        self.ids = ids
+        self.vocab = vocab
+
+    def _write(self, slots: torch.Tensor) -> torch.Tensor:
+        vids = self.ids.take(int(slots.numel()))
+        self.writer(slots, vids)
+        return torch.zeros((int(slots.numel()), self.vocab), dtype=torch.float32, device=slots.device)
+
+    def forward_frontier(self, *, input_ids, route_kv_metadata):
+        return self._write(route_kv_metadata.out_cache_loc)
+
+    def forward_extend(self, *, input_ids, out_cache_loc, positions, req_pool_indices, seq_lens_cpu):
+        return self._write(out_cache_loc)
+
+
+class ValueIds:
+    def __init__(self) -> None:
+        self.next = 1
+        self.log: list[tuple[int, int]] = []
+
+    def take(self, n: int) -> torch.Tensor:
+        out = torch.arange(self.next, self.next + n, dtype=torch.int64)
+        self.log.append((self.next, n))
+        self.next += n
+        return out
+
+
+@dataclass
+class RequestState:
+    plan: ForkPlan
+    store: KVTreeStore
+    bridge: SGLangRoutePoolBridge
+    backend: SGLangFlashInferFrontierModelBackend
+    rng: random.Random
+    active: list[RouteState] = field(default_factory=list)
+    prefix_value_ids: list[int] = field(default_factory=list)
+    node_value_ids: dict[int, int] = field(default_factory=dict)
+    stats: list[dict[str, int]] = field(default_factory=list)
+
+
+class DrafterForkWorkload:
+    """Runs ``ForkPlan``s through bridges over shared pools.
+
+    ``writer(slots, value_ids)`` writes KV rows; ``on_phase(name)`` is
+    called after every phase (for state comparison or timing)."""
+
+    def __init__(self, *, plans: Sequence[ForkPlan], req_pool: Any, allocator: Any, page_size: int,
+                 device, writer: Callable[[torch.Tensor, torch.Tensor], None],
+                 use_page_attention_metadata: bool = True) -> None:
+        self.page_size = int(page_size)
+        self.device = torch.device(device)
+        self.allocator = allocator
+        self.req_pool = req_pool
+        self.ids = ValueIds()
+        self.writer = writer
+        self.requests: list[RequestState] = []
+        for plan in plans:
+            store = KVTreeStore()
+            bridge = SGLangRoutePoolBridge(req_to_token_pool=req_pool, token_to_kv_pool_allocator=allocator,
+                                           page_size=page_size, device=self.device,
+                                           use_page_attention_metadata=use_page_attention_metadata)
+            executor = PatternExecutor(self._record_writer, self.ids)
+            backend = SGLangFlashInferFrontierModelBackend(route_store=store, executor=executor, route_pool=bridge)
+            self.requests.append(RequestState(plan, store, bridge, backend, random.Random(plan.seed)))
+        self._last_write: tuple[torch.Tensor, torch.Tensor] | None = None
+
+    def _record_writer(self, slots: torch.Tensor, vids: torch.Tensor) -> None:
+        self._last_write = (slots, vids)
+        self.writer(slots, vids)
+
+    # ------------------------------------------------------------ phases
+    def prefill(self) -> None:
+        for req in self.requests:
+            n = req.plan.prefix_len
+            dev = self.device
+            zero = torch.zeros(1, dtype=torch.int64)
+            slots = self.allocator.alloc_extend(zero.to(dev), zero, torch.tensor([n], device=dev),
+                                                torch.tensor([n]), torch.full((1,), -1, dtype=torch.int64, device=dev),
+                                                n)
+            if slots is None:
+                raise RuntimeError("pool too small for the prefill")
+            vids = self.ids.take(n)
+            self.writer(slots, vids)
+            req.prefix_value_ids = vids.tolist()
+            tokens = [req.rng.randrange(VOCAB) for _ in range(n)]
+            req.backend.attach_prefilled_prefix(prompt_token_ids=tokens, prefix_slot_ids=slots,
+                                                next_token_logits=torch.zeros(8, device=dev))
+            req.active = [req.store.new_root_route(req.rng.randrange(VOCAB), req.store.prefix_view(n))]
+
+    def _fork(self, req: RequestState, fanout: int) -> None:
+        children = []
+        for parent in req.active:
+            for _ in range(fanout):
+                children.append(req.store.clone_route_with_new_pending(parent, req.rng.randrange(VOCAB)))
+        req.store.release_routes_without_descendants(req.active, children)
+        req.active = children
+
+    def decode_step(self, req: RequestState, step: int | None = None) -> None:
+        if step is not None and step in req.plan.forks:
+            self._fork(req, req.plan.forks[step])
+        out = req.backend.decode_frontier_one_token(req.active)
+        slots, vids = self._last_write
+        for nid, v in zip(out.new_node_ids, vids.tolist()):
+            req.node_value_ids[int(nid)] = int(v)
+        req.store.mark_routes_materialized(req.active, out.new_node_ids, DecodePhase.STAGE1)
+        for r in req.active:
+            r.pending_token_id = req.rng.randrange(VOCAB)
+
+    def stage1(self, on_step: Callable[[str], None] | None = None) -> None:
+        steps = max(r.plan.steps for r in self.requests)
+        for t in range(steps):
+            for req in self.requests:
+                if t < req.plan.steps:
+                    self.decode_step(req, t)
+            if on_step is not None:
+                on_step(f"decode{t}")
+
+    def commit(self) -> None:
+        for req in self.requests:
+            final = req.rng.choice(req.active)
+            committed = final
+            while committed.total_materialized_depth() > req.plan.commit_depth:
+                committed = req.store.routes[int(committed.parent_route_id)]
+            nodes = committed.kv_view.node_ids
+            keep = [r for r in req.active if r.kv_view.node_ids[: len(nodes)] == nodes]
+            req.prefix_value_ids = req.prefix_value_ids + [req.node_value_ids[int(n)] for n in nodes]
+            promoted, stats = req.backend.commit_stage1_and_promote(committed_route=committed, retained_routes=keep)
+            req.active = promoted
+            req.stats.append(stats)
+
+    def post_decode(self) -> None:
+        for req in self.requests:
+            for _ in range(req.plan.post_steps):
+                self.decode_step(req)
+
+    def fallback_extend(self) -> None:
+        for req in self.requests:
+            b = req.bridge
+            b.retain_route_rows([])
+            req.stats.append({"released_kv_pages": b.release_unreferenced_node_slots([])})
+            before = self.ids.next
+            req.backend.append_known_tokens_as_prefix(req.plan.extend_tokens)
+            n = len(req.plan.extend_tokens)
+            req.prefix_value_ids = req.prefix_value_ids + list(range(before, before + n))
+            req.active = [req.store.new_root_route(req.rng.randrange(VOCAB),
+                                                   req.store.prefix_view(len(req.backend.prefix_token_ids)))]
+        for req in self.requests:
+            # The logical store's committed tokens lag the EXTEND suffix; the
+            # root's prefix view carries the true committed length.
+            for _ in range(req.plan.post_steps):
+                self.decode_step(req)
+
+    def run(self, on_phase: Callable[[str], None] | None = None) -> None:
+        cb = on_phase or (lambda _name: None)
+        self.prefill()
+        cb("prefill")
+        self.stage1(cb)
+        self.commit()
+        cb("commit")
+        self.post_decode()
+        cb("post_decode")
+        self.fallback_extend()
+        cb("extend")
+
+    # ------------------------------------------------------------ expected content
+    def expected_path_values(self, req: RequestState, route: RouteState) -> list[int]:
+        """Value ids a route's slot path must hold: the committed prefix's,
+        then one per materialized node."""
+        n = int(route.kv_view.prefix.committed_length)
+        return req.prefix_value_ids[:n] + [req.node_value_ids[int(x)] for x in route.kv_view.node_ids]

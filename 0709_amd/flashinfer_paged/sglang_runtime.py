@@ -1,0 +1,1177 @@
+"""Drafter route pool: logical routes bound to request rows and physical KV
+slots (drop-in for ``SGLangRoutePoolBridge``, reference
+``flashinfer_paged/sglang_runtime.py:89-1117``).
+
+Same fields, methods, counters, exceptions and copy-on-write rules as the
+reference.  Differences (all leave the KV bytes, slot paths, request rows and
+freed-page order identical):
+
+* tail-page copy-on-write issues ONE ``move_kv_cache`` for all copied pages of
+  a frontier (destinations are freshly allocated, disjoint pages), where the
+  reference calls it once per copied page (``:783-797``);
+* with the native allocator (``native_pool.NativePagedAllocator``) page
+  ownership is a bitmap in HBM: newly handed-out pages are marked by a kernel
+  at once (no deferred device-to-host flush), and ``release_unreferenced_
+  node_slots`` is a mark/sweep kernel that returns the releasable pages in
+  ascending order straight to the device free list.  With any other
+  allocator the reference's host-set bookkeeping is kept.
+"""
+
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Any, Sequence
+
+import numpy as np
+import torch
+
+from .. import _lib
+from .paged_metadata import build_flashinfer_paged_kv_metadata
+from .kv import KVTreeStore
+from .types import DraftPrefixState, FrontierDecodeOutput, PrefixKVView, RouteState
+
+
+@dataclass(frozen=True)
+class AtlasPagedDecodeSpec:
+    """Page metadata carried to paged decode (``sglang_page_attention.py:10-17``)."""
+
+    kv_indptr: torch.Tensor
+    kv_indices: torch.Tensor
+    kv_last_page_len: torch.Tensor
+    page_size: int
+
+
+@dataclass(frozen=True)
+class SGLangRouteKVMetadata:
+    """Per-frontier decode metadata (``flashinfer_backends.py:12-32``)."""
+
+    req_pool_indices: torch.Tensor
+    seq_lens: torch.Tensor
+    out_cache_loc: torch.Tensor
+    positions: torch.Tensor
+    seq_lens_sum: int
+    seq_lens_cpu: torch.Tensor
+    orig_seq_lens: torch.Tensor | None = None
+    attention_page_size: int = 1
+    token_index_count: int = 0
+    page_index_count: int = 0
+    paged_decode_spec: AtlasPagedDecodeSpec | None = None
+
+
+@dataclass
+class SGLangRouteRow:
+    route_id: int
+    req_pool_index: int
+    handle: Any
+    written_length: int = 0
+    pending_dirty_start: int | None = None
+
+
+@dataclass
+class _PoolReqHandle:
+    rid: str
+    req_pool_idx: int | None = None
+
+
+class DeviceOwnedPages:
+    """Set of owned page ids held as a bitmap in HBM (bit p of word p // 32).
+
+    Supports the set operations the bridge and its callers use; reading it as
+    a Python set copies the bitmap to the host (diagnostics only)."""
+
+    def __init__(self, num_pages: int, page_size: int, device: torch.device) -> None:
+        self.num_pages = int(num_pages)
+        self.page_size = int(page_size)
+        self.device = device
+        words = (self.num_pages + 31) // 32
+        self.bitmap = torch.zeros(words, dtype=torch.int32, device=device)
+        self.live = torch.zeros(words, dtype=torch.int32, device=device)
+        self.free_pages = torch.zeros(self.num_pages, dtype=torch.int64, device=device)
+        self.free_count = torch.zeros(1, dtype=torch.int64, device=device)
+
+    # -- device operations ---------------------------------------------
+    def mark_slots(self, slots: torch.Tensor) -> None:
+        s = slots.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
+        if int(s.numel()) == 0:
+            return
+        lib = _lib.load()
+        rc = lib.atlas_mark_pages(_lib.ptr(self.bitmap), self.num_pages, _lib.ptr(s), int(s.numel()), self.page_size,
+                                  _lib.stream_of(self.device))
+        _lib.check(rc, "atlas_mark_pages")
+
+    def sweep(self, live_slots: torch.Tensor) -> torch.Tensor:
+        """owned -= pages not reachable from live_slots; returns the released
+        pages (ascending, on the device)."""
+        s = live_slots.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
+        lib = _lib.load()
+        rc = lib.atlas_prune_pages(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, _lib.ptr(s),
+                                   int(s.numel()), self.page_size, _lib.ptr(self.free_pages),
+                                   _lib.ptr(self.free_count), _lib.stream_of(self.device))
+        _lib.check(rc, "atlas_prune_pages")
+        n = int(self.free_count.item())
+        return self.free_pages[:n]
+
+    # -- set protocol -----------------------------------------------------
+    def to_set(self) -> set[int]:
+        words = self.bitmap.cpu().numpy().view(np.uint32)
+        out = set()
+        for i in np.flatnonzero(words):
+            w = int(words[i])
+            while w:
+                b = (w & -w).bit_length() - 1
+                out.add(int(i) * 32 + b)
+                w &= w - 1
+        return out
+
+    def _set_pages(self, pages, value: bool) -> None:
+        pages = sorted({int(p) for p in pages})
+        if not pages:
+            return
+        if pages[0] < 0 or pages[-1] >= self.num_pages:
+            raise ValueError("page id outside the pool")
+        words = self.bitmap.cpu().numpy().view(np.uint32).copy()
+        for p in pages:
+            bit = np.uint32(1 << (p % 32))
+            if value:
+                words[p // 32] |= bit
+            else:
+                words[p // 32] &= ~bit
+        self.bitmap.copy_(torch.from_numpy(words.view(np.int32)))
+
+    def update(self, pages) -> None:
+        self._set_pages(pages, True)
+
+    def add(self, page: int) -> None:
+        self._set_pages([page], True)
+
+    def difference_update(self, pages) -> None:
+        self._set_pages(pages, False)
+
+    def remove(self, page: int) -> None:
+        if int(page) not in self:
+            raise KeyError(page)
+        self._set_pages([page], False)
+
+    def clear(self) -> None:
+        self.bitmap.zero_()
+
+    def __contains__(self, page) -> bool:
+        p = int(page)
+        if not 0 <= p < self.num_pages:
+            return False
+        return bool((int(self.bitmap[p // 32].item()) >> (p % 32)) & 1)
+
+    def __iter__(self):
+        return iter(sorted(self.to_set()))
+
+    def __len__(self) -> int:
+        return len(self.to_set())
+
+    def __eq__(self, other) -> bool:
+        return self.to_set() == set(other)
+
+    def __sub__(self, other):
+        return self.to_set() - set(other)
+
+    def __rsub__(self, other):
+        return set(other) - self.to_set()
+
+    def __repr__(self) -> str:
+        return f"DeviceOwnedPages({sorted(self.to_set())})"
+
+
+@dataclass
+class SGLangRoutePoolBridge:
+    """Bind logical routes to request rows and physical KV slots."""
+
+    req_to_token_pool: Any
+    token_to_kv_pool_allocator: Any
+    page_size: int
+    max_context_len: int | None = None
+    device: str | torch.device = "cuda"
+    prefix_slot_ids: torch.Tensor | None = None
+    prefix_slot_count: int = 0
+    prefix_page_ids: set[int] = field(default_factory=set)
+    route_rows: dict[int, SGLangRouteRow] = field(default_factory=dict)
+    node_slot_ids: dict[int, int | torch.Tensor] = field(default_factory=dict)
+    route_slot_paths: dict[int, torch.Tensor] = field(default_factory=dict)
+    route_tail_page_keys: dict[int, int] = field(default_factory=dict)
+    prefix_tail_page_key: int | None = None
+    prefix_partial_tail_keys: dict[int, int] = field(default_factory=dict)
+    next_tail_page_key: int = 1
+    owned_page_ids: Any = field(default_factory=set)
+    pending_owned_slot_tensors: list[torch.Tensor] = field(default_factory=list)
+    cow_pages_copied: int = 0
+    cow_tokens_copied: int = 0
+    attention_metadata_builds: int = 0
+    attention_metadata_token_indices: int = 0
+    attention_metadata_page_indices: int = 0
+    req_row_write_calls: int = 0
+    req_row_elements_written: int = 0
+    req_row_full_rewrite_calls: int = 0
+    req_row_full_rewrite_elements: int = 0
+    req_row_full_init_calls: int = 0
+    req_row_full_init_elements: int = 0
+    req_row_append_calls: int = 0
+    req_row_append_elements: int = 0
+    req_row_cow_patch_calls: int = 0
+    req_row_cow_patch_elements: int = 0
+    hot_path_host_transfer_batches: int = 0
+    hot_path_host_transfer_elements: int = 0
+    use_page_attention_metadata: bool = True
+    validate_page_layout: bool = True
+    pending_device_checks: list[Any] = field(default_factory=list)
+
+    def __post_init__(self) -> None:
+        alloc = self.token_to_kv_pool_allocator
+        num_pages = getattr(alloc, "num_pages", None)
+        alloc_device = getattr(alloc, "device", None)
+        if (
+            isinstance(self.owned_page_ids, set)
+            and not self.owned_page_ids
+            and num_pages is not None
+            and isinstance(alloc_device, torch.device)
+            and alloc_device.type == "cuda"
+            and callable(getattr(alloc, "free_pages_prepend", None))
+        ):
+            # Native pool: ownership in HBM (pages 0..num_pages, page 0 = padding).
+            self.owned_page_ids = DeviceOwnedPages(int(num_pages) + 1, self.page_size, alloc_device)
+
+    @property
+    def _device_ownership(self) -> bool:
+        return isinstance(self.owned_page_ids, DeviceOwnedPages)
+
+    @classmethod
+    def from_runner(cls, model_runner: Any, *, page_size: int, device: str | torch.device = "cuda"):
+        """``sglang_runtime.py:130-171``."""
+        req_pool = getattr(model_runner, "req_to_token_pool", None)
+        allocator = None
+        for name in ("token_to_kv_pool_allocator", "token_to_kv_pool_alloc", "kv_pool_allocator"):
+            allocator = getattr(model_runner, name, None)
+            if allocator is not None:
+                break
+        if req_pool is None:
+            raise RuntimeError("SGLang ModelRunner does not expose req_to_token_pool")
+        if allocator is None:
+            raise RuntimeError("SGLang ModelRunner does not expose token_to_kv_pool_allocator")
+        actual = getattr(model_runner, "atlas_pool_page_size", None)
+        if actual is None:
+            for name in ("token_to_kv_pool", "kv_pool", "kvcache"):
+                pool = getattr(model_runner, name, None)
+                if pool is not None:
+                    actual = getattr(pool, "page_size", None)
+                    break
+        if actual is not None and int(actual) != int(page_size):
+            raise RuntimeError(
+                "ATLAS page-size argument does not match the physical SGLang KV pool: "
+                f"requested={int(page_size)}, physical={int(actual)}"
+            )
+        max_ctx = getattr(model_runner, "atlas_max_context_len", None)
+        if max_ctx is None:
+            max_ctx = _req_pool_capacity(req_pool)
+        return cls(
+            req_to_token_pool=req_pool,
+            token_to_kv_pool_allocator=allocator,
+            page_size=page_size,
+            max_context_len=int(max_ctx) if max_ctx is not None else None,
+            device=device,
+            use_page_attention_metadata=bool(getattr(model_runner, "atlas_use_page_attention_metadata", True)),
+            validate_page_layout=bool(getattr(model_runner, "atlas_validate_page_layout", True)),
+        )
+
+    # ------------------------------------------------------------ prefix
+    def set_prefix_slots(self, slot_ids: Sequence[int] | torch.Tensor) -> None:
+        """``sglang_runtime.py:173-187``."""
+        self.prefix_slot_ids = _as_long(slot_ids, self.device)
+        self._refresh_prefix_cpu_metadata()
+        if self._device_ownership:
+            self.owned_page_ids.clear()
+            if self.prefix_slot_count:
+                self.owned_page_ids.mark_slots(self.prefix_slot_ids[:: self.page_size])
+        else:
+            self.owned_page_ids = set(self.prefix_page_ids)
+        self.pending_owned_slot_tensors.clear()
+        self.prefix_partial_tail_keys.clear()
+        partial = self.prefix_slot_count and self.prefix_slot_count % self.page_size
+        self.prefix_tail_page_key = self._new_tail_page_key() if partial else None
+        if self.prefix_tail_page_key is not None:
+            self.prefix_partial_tail_keys[(self.prefix_slot_count - 1) // self.page_size] = self.prefix_tail_page_key
+
+    def _refresh_prefix_cpu_metadata(self) -> None:
+        if self.prefix_slot_ids is None or int(self.prefix_slot_ids.numel()) == 0:
+            self.prefix_slot_count = 0
+            self.prefix_page_ids.clear()
+            return
+        self.prefix_slot_count = int(self.prefix_slot_ids.numel())
+        starts = torch.div(self.prefix_slot_ids[:: self.page_size], self.page_size, rounding_mode="floor")
+        self.prefix_page_ids = set(_int_list(starts))
+
+    def _new_tail_page_key(self) -> int:
+        # Lease keys are negative, so they never equal a physical page id.
+        key = -int(self.next_tail_page_key)
+        self.next_tail_page_key += 1
+        return key
+
+    # ------------------------------------------------------------ ownership
+    def _record_pending_owned_slots(self, slot_ids: torch.Tensor) -> None:
+        if int(slot_ids.numel()) == 0:
+            return
+        if self._device_ownership:
+            self.owned_page_ids.mark_slots(slot_ids.detach())
+        else:
+            self.pending_owned_slot_tensors.append(slot_ids.detach().reshape(-1))
+
+    def _materialize_pending_owned_pages(self) -> None:
+        """Host-set mode: fold the pending slots into ``owned_page_ids`` with
+        one batched copy (``sglang_runtime.py:216-233``).  Device mode marks
+        pages as they are handed out, so there is nothing pending."""
+        if not self.pending_owned_slot_tensors:
+            return
+        slots = torch.cat(self.pending_owned_slot_tensors, dim=0)
+        self.owned_page_ids.update(s // self.page_size for s in _int_list(slots))
+        self.pending_owned_slot_tensors.clear()
+
+    def owned_page_count(self) -> int:
+        self._materialize_pending_owned_pages()
+        return len(self.owned_page_ids)
+
+    # ------------------------------------------------------------ rows
+    def bind_existing_route_row(self, route_id: int, req_pool_index: int, handle: Any | None = None, *,
+                                written_length: int = 0) -> None:
+        if int(written_length) < 0:
+            raise ValueError("written_length must be non-negative")
+        if handle is None:
+            handle = _PoolReqHandle(rid=f"atlas-{int(route_id)}", req_pool_idx=int(req_pool_index))
+        self.route_rows[int(route_id)] = SGLangRouteRow(int(route_id), int(req_pool_index), handle,
+                                                        written_length=int(written_length))
+
+    def ensure_route_rows(self, routes: Sequence[RouteState]) -> torch.Tensor:
+        missing = [r for r in routes if int(r.route_id) not in self.route_rows]
+        if missing:
+            handles = [_PoolReqHandle(rid=f"atlas-{int(r.route_id)}") for r in missing]
+            indices = self.req_to_token_pool.alloc(handles)
+            if indices is None:
+                raise RuntimeError("SGLang ReqToTokenPool.alloc returned None")
+            rows = _int_list(indices)
+            if len(rows) != len(missing):
+                raise RuntimeError("SGLang ReqToTokenPool.alloc returned the wrong number of rows")
+            for route, handle, row in zip(missing, handles, rows):
+                handle.req_pool_idx = int(row)
+                self.bind_existing_route_row(route.route_id, int(row), handle=handle)
+        return torch.tensor([self.route_rows[int(r.route_id)].req_pool_index for r in routes], dtype=torch.long,
+                            device=self.device)
+
+    def release_route_rows(self, route_ids: Sequence[int]) -> None:
+        for route_id in route_ids:
+            row = self.route_rows.pop(int(route_id), None)
+            if row is not None and hasattr(self.req_to_token_pool, "free"):
+                self.req_to_token_pool.free(row.handle)
+
+    def retain_route_rows(self, route_ids: Sequence[int]) -> int:
+        """Keep only the given routes' rows, slot paths and leases
+        (``sglang_runtime.py:284-302``); returns the number of released rows."""
+        keep = {int(r) for r in route_ids}
+        released = [int(r) for r in self.route_rows if int(r) not in keep]
+        self.release_route_rows(released)
+        self.route_slot_paths = {r: p for r, p in self.route_slot_paths.items() if r in keep}
+        self.route_tail_page_keys = {r: k for r, k in self.route_tail_page_keys.items() if r in keep}
+        return len(released)
+
+    def register_node_slots(self, node_ids, slot_ids) -> None:
+        nodes = _int_list(node_ids)
+        if isinstance(slot_ids, torch.Tensor):
+            flat = slot_ids.reshape(-1)
+            values: list[Any] = [flat[i] for i in range(int(flat.numel()))]
+        else:
+            values = [int(s) for s in slot_ids]
+        if len(nodes) != len(values):
+            raise ValueError("node_ids and slot_ids must have the same length")
+        for n, s in zip(nodes, values):
+            self.node_slot_ids[int(n)] = s
+
+    def reconcile_route_rows(self, previous_routes: Sequence[RouteState], next_routes: Sequence[RouteState]) -> None:
+        """Children inherit the parent's slot path and lease; the first child
+        takes over the parent's row, other rows are freed
+        (``sglang_runtime.py:318-355``)."""
+        children: dict[int, list[RouteState]] = {}
+        for child in next_routes:
+            if child.parent_route_id is not None:
+                children.setdefault(int(child.parent_route_id), []).append(child)
+        for parent in previous_routes:
+            pid = int(parent.route_id)
+            row = self.route_rows.pop(pid, None)
+            kids = children.get(pid, [])
+            path = self.route_slot_paths.get(pid)
+            if path is not None:
+                for child in kids:
+                    self.route_slot_paths[int(child.route_id)] = path
+                    key = self.route_tail_page_keys.get(pid)
+                    if key is not None:
+                        self.route_tail_page_keys[int(child.route_id)] = key
+            if row is None:
+                continue
+            if kids:
+                first = kids[0]
+                self.route_rows[int(first.route_id)] = SGLangRouteRow(
+                    route_id=int(first.route_id), req_pool_index=row.req_pool_index, handle=row.handle,
+                    written_length=row.written_length, pending_dirty_start=row.pending_dirty_start,
+                )
+            elif hasattr(self.req_to_token_pool, "free"):
+                self.req_to_token_pool.free(row.handle)
+
+    # ------------------------------------------------------------ promote / prune
+    def commit_route_as_prefix(self, route: RouteState) -> torch.Tensor:
+        """Zero-copy promotion: the route's slot path becomes the prefix and
+        its tail lease carries over (``sglang_runtime.py:357-378``)."""
+        old_len = 0 if self.prefix_slot_ids is None else int(self.prefix_slot_ids.numel())
+        path = self._slot_path_for_route(route)
+        expected = old_len + len(route.kv_view.node_ids)
+        if int(path.numel()) != expected:
+            raise RuntimeError(
+                f"cannot promote route KV to prefix: slot_path_len={int(path.numel())}, expected={expected}"
+            )
+        self.prefix_slot_ids = path
+        self._refresh_prefix_cpu_metadata()
+        self.prefix_partial_tail_keys.clear()
+        n = int(path.numel())
+        self.prefix_tail_page_key = self.route_tail_page_keys.get(int(route.route_id)) if n % self.page_size else None
+        if self.prefix_tail_page_key is not None:
+            self.prefix_partial_tail_keys[(n - 1) // self.page_size] = self.prefix_tail_page_key
+        return path
+
+    def page_reference_counts(self) -> dict[int, int]:
+        """One reference per path view reaching a page (prefix + each route),
+        ``sglang_runtime.py:380-396``."""
+        counts: dict[int, int] = {}
+        for pages in self._page_id_sets_for_paths([self.prefix_slot_ids, *self.route_slot_paths.values()]):
+            for p in pages:
+                counts[p] = counts.get(p, 0) + 1
+        return dict(sorted(counts.items()))
+
+    def _page_id_sets_for_paths(self, paths: Sequence[torch.Tensor | None]) -> list[set[int]]:
+        """Pages of each path from its page-start slots plus its last slot,
+        fetched in one batch (``sglang_runtime.py:479-505``)."""
+        counts: list[int] = []
+        parts: list[torch.Tensor] = []
+        for path in paths:
+            if path is None or int(path.numel()) == 0:
+                counts.append(0)
+                continue
+            sampled = torch.cat((path[:: self.page_size], path[-1:]))
+            parts.append(torch.div(sampled, self.page_size, rounding_mode="floor").to(torch.long))
+            counts.append(int(parts[-1].numel()))
+        flat = _int_list(torch.cat(parts)) if parts else []
+        out, off = [], 0
+        for c in counts:
+            out.append(set(flat[off : off + c]))
+            off += c
+        return out
+
+    def validate_route_physical_state(self, route: RouteState) -> None:
+        """``sglang_runtime.py:398-477``."""
+        rid = int(route.route_id)
+        path = self.route_slot_paths.get(rid)
+        if path is None:
+            raise RuntimeError(f"Drafter route {rid} has no physical slot path")
+        committed = int(route.kv_view.prefix.committed_length)
+        expected = committed + len(route.kv_view.node_ids)
+        slots = _int_list(path)
+        if len(slots) != expected:
+            raise RuntimeError(
+                f"Drafter route {rid} physical length does not match logical KV: physical={len(slots)}, "
+                f"committed={committed}, nodes={len(route.kv_view.node_ids)}"
+            )
+        missing = [int(n) for n in route.kv_view.node_ids if int(n) not in self.node_slot_ids]
+        if missing:
+            raise RuntimeError(f"Drafter route {rid} has logical nodes without materialized KV: node_ids={missing}")
+        ps = int(self.page_size)
+        for pos, slot in enumerate(slots):
+            off = pos % ps
+            if slot % ps != off:
+                raise RuntimeError(
+                    f"Drafter route {rid} physical page layout is invalid: logical_position={pos}, slot_id={slot}, "
+                    f"expected_page_offset={off}"
+                )
+            if off and slot != slots[pos - 1] + 1:
+                raise RuntimeError(
+                    f"Drafter route {rid} physical page is not contiguous: logical_position={pos}, "
+                    f"previous_slot={slots[pos - 1]}, slot_id={slot}"
+                )
+        self._materialize_pending_owned_pages()
+        owned = self.owned_page_ids.to_set() if self._device_ownership else self.owned_page_ids
+        unowned = sorted({s // ps for s in slots} - owned)
+        if unowned:
+            raise RuntimeError(f"Drafter route {rid} references unowned KV pages: page_ids={unowned}")
+        row = self.route_rows.get(rid)
+        if row is None:
+            return
+        if int(row.written_length) != len(slots):
+            raise RuntimeError(
+                f"Drafter route {rid} req-row length is inconsistent: row={int(row.written_length)}, slots={len(slots)}"
+            )
+        table = getattr(self.req_to_token_pool, "req_to_token", None)
+        if isinstance(table, torch.Tensor) and _int_list(table[int(row.req_pool_index), : len(slots)]) != slots:
+            raise RuntimeError(f"Drafter route {rid} req-row slots do not match its physical path")
+
+    def release_unreferenced_node_slots(self, live_node_ids: Sequence[int]) -> int:
+        """Return every owned page that neither the committed prefix nor a
+        retained route reaches, in ascending page order; forget dead node
+        mappings (``sglang_runtime.py:507-539``).  Returns the page count."""
+        self.check_pending_device_checks()
+        live_nodes = {int(n) for n in live_node_ids}
+        if self._device_ownership:
+            parts = []
+            if self.prefix_slot_ids is not None and int(self.prefix_slot_ids.numel()):
+                parts.append(self.prefix_slot_ids[:: self.page_size])
+            for path in self.route_slot_paths.values():
+                if int(path.numel()):
+                    parts.append(path[:: self.page_size])
+                    parts.append(path[-1:])
+            live = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.long, device=self.device)
+            released = self.owned_page_ids.sweep(live)
+            count = int(released.numel())
+        else:
+            self._materialize_pending_owned_pages()
+            live_pages = set(self.prefix_page_ids)
+            for pages in self._page_id_sets_for_paths(list(self.route_slot_paths.values())):
+                live_pages.update(pages)
+            releasable = sorted(self.owned_page_ids - live_pages)
+            count = len(releasable)
+        for node in list(self.node_slot_ids):
+            if int(node) not in live_nodes:
+                self.node_slot_ids.pop(int(node), None)
+        if count:
+            free = getattr(self.token_to_kv_pool_allocator, "free", None)
+            if not callable(free):
+                raise RuntimeError("SGLang token-to-KV allocator does not expose free()")
+            if self._device_ownership:
+                self.token_to_kv_pool_allocator.free_pages_prepend(released.clone())
+            else:
+                free(torch.tensor([p * self.page_size for p in releasable], dtype=torch.long, device=self.device))
+                self.owned_page_ids.difference_update(releasable)
+        return count
+
+    def clear_physical_state(self) -> None:
+        """``sglang_runtime.py:541-576``."""
+        self.prefix_slot_ids = None
+        self.prefix_slot_count = 0
+        self.prefix_page_ids.clear()
+        self.prefix_tail_page_key = None
+        self.prefix_partial_tail_keys.clear()
+        self.route_rows.clear()
+        self.node_slot_ids.clear()
+        self.route_slot_paths.clear()
+        self.route_tail_page_keys.clear()
+        self.next_tail_page_key = 1
+        self.owned_page_ids.clear()
+        self.pending_owned_slot_tensors.clear()
+        self.pending_device_checks.clear()
+        for name in _COUNTERS:
+            setattr(self, name, 0)
+        for target in (self.req_to_token_pool, self.token_to_kv_pool_allocator):
+            clear = getattr(target, "clear", None)
+            if callable(clear):
+                clear()
+
+    # ------------------------------------------------------------ allocation
+    def allocate_token_slots(self, count: int, *, mode: str = "decode") -> torch.Tensor:
+        if count <= 0:
+            raise ValueError("count must be positive")
+        result = _allocate_kv_slots(self.token_to_kv_pool_allocator, int(count), mode=mode)
+        slots = _slot_tensor(result, self.device)
+        if int(slots.numel()) < int(count):
+            raise RuntimeError(
+                "SGLang token slot allocator returned too few slots: "
+                f"needed={int(count)}, got_shape={tuple(slots.shape)}, mode={mode}, result_type={type(result).__name__}"
+            )
+        return slots[: int(count)]
+
+    def allocate_extend_slots(self, *, prefix_lens: Sequence[int], seq_lens: Sequence[int],
+                              last_locs: Sequence[int] | torch.Tensor) -> torch.Tensor:
+        pre_cpu = torch.tensor(list(prefix_lens), dtype=torch.long)
+        seq_cpu = torch.tensor(list(seq_lens), dtype=torch.long)
+        pre = pre_cpu.to(self.device)
+        seq = seq_cpu.to(self.device)
+        last = _as_long(last_locs, self.device)
+        if not (pre.numel() == seq.numel() == last.numel()):
+            raise ValueError("prefix_lens, seq_lens, and last_locs must have the same length")
+        n = sum(int(s) - int(p) for p, s in zip(prefix_lens, seq_lens))
+        if n <= 0:
+            raise ValueError("extend_num_tokens must be positive")
+        fn = getattr(self.token_to_kv_pool_allocator, "alloc_extend", None)
+        if callable(fn):
+            result = fn(pre, pre_cpu, seq, seq_cpu, last, n)
+            if result is not None:
+                slots = _slot_tensor(result, self.device)
+                if int(slots.numel()) >= n:
+                    return slots[:n]
+        return self.allocate_token_slots(n, mode="extend")
+
+    def allocate_decode_slots(self, *, seq_lens: Sequence[int], last_locs: Sequence[int] | torch.Tensor) -> torch.Tensor:
+        seq_cpu = torch.tensor(list(seq_lens), dtype=torch.long)
+        seq = seq_cpu.to(self.device)
+        last = _as_long(last_locs, self.device)
+        if seq.numel() != last.numel():
+            raise ValueError("seq_lens and last_locs must have the same length")
+        fn = getattr(self.token_to_kv_pool_allocator, "alloc_decode", None)
+        if callable(fn):
+            result = fn(seq, seq_cpu, last)
+            if result is not None:
+                slots = _slot_tensor(result, self.device)
+                if int(slots.numel()) >= int(seq.numel()):
+                    return slots[: int(seq.numel())]
+        return self.allocate_token_slots(int(seq.numel()), mode="decode")
+
+    def _allocate_full_pages(self, count: int) -> torch.Tensor:
+        """``count`` whole pages as a [count, page_size] slot tensor
+        (``sglang_runtime.py:661-684``)."""
+        if count <= 0:
+            return torch.empty((0, self.page_size), dtype=torch.long, device=self.device)
+        alloc = getattr(self.token_to_kv_pool_allocator, "alloc", None)
+        if not callable(alloc):
+            raise RuntimeError("SGLang token-to-KV allocator does not expose alloc()")
+        result = alloc(int(count) * self.page_size)
+        if result is None:
+            raise RuntimeError(f"SGLang KV pool cannot allocate {int(count)} COW pages")
+        slots = _slot_tensor(result, self.device)
+        expected = int(count) * self.page_size
+        if int(slots.numel()) != expected:
+            raise RuntimeError(
+                f"SGLang full-page allocation returned the wrong number of slots: expected={expected}, "
+                f"got={int(slots.numel())}"
+            )
+        pages = slots.reshape(int(count), self.page_size)
+        if not self._device_ownership:
+            # Foreign allocators: confirm each returned page is contiguous.
+            ids = torch.div(pages, self.page_size, rounding_mode="floor")
+            self._check_or_defer(ids.eq(ids[:, :1]).all(), "SGLang allocator returned a non-contiguous COW page")
+        self._record_pending_owned_slots(pages[:, 0])
+        return pages
+
+    def _copy_kv_slots(self, destination: torch.Tensor, source: torch.Tensor) -> None:
+        get_kvcache = getattr(self.token_to_kv_pool_allocator, "get_kvcache", None)
+        kv_cache = get_kvcache() if callable(get_kvcache) else None
+        move = getattr(kv_cache, "move_kv_cache", None)
+        if not callable(move):
+            raise RuntimeError(
+                "SGLang KV pool does not expose move_kv_cache(); tail-page copy-on-write cannot be performed"
+            )
+        move(destination.to(dtype=torch.long), source.to(dtype=torch.long))
+
+    # ------------------------------------------------------------ copy-on-write
+    def _copy_partial_tail_pages(self, routes: Sequence[RouteState], slot_paths: Sequence[torch.Tensor]):
+        return self._copy_partial_tail_pages_with_dirty_starts(routes, slot_paths)[0]
+
+    def _copy_partial_tail_pages_with_dirty_starts(self, routes: Sequence[RouteState],
+                                                   slot_paths: Sequence[torch.Tensor]):
+        """Tail-page copy-on-write (``sglang_runtime.py:708-798``).
+
+        Active writers whose slot paths end inside the same partial page
+        (same lease key) form a group; the first keeps the page, every other
+        gets a fresh page holding a copy of its valid tail, a new lease, and a
+        dirty start at the copied tail.  All copies go in one move call.
+        Returns the new paths and {route position: dirty start}.
+        """
+        if len(routes) != len(slot_paths):
+            raise ValueError("routes and slot_paths must have the same length")
+        result = list(slot_paths)
+        if len(routes) <= 1:
+            return result, {}
+        groups: dict[int, list[tuple[int, torch.Tensor, int]]] = {}
+        unkeyed: list[tuple[int, torch.Tensor, int, int, torch.Tensor]] = []
+        for index, path in enumerate(slot_paths):
+            tail = int(path.numel()) % self.page_size
+            if not tail:
+                continue
+            rid = int(routes[index].route_id)
+            key = self.route_tail_page_keys.get(rid)
+            if key is None:
+                # Paths injected without a lease: key them by their physical
+                # tail page (one batched device-to-host read).
+                src = path[-tail:]
+                pages = torch.div(src, self.page_size, rounding_mode="floor")
+                self._check_or_defer(pages.eq(pages[:1]).all(), "route partial tail spans multiple physical pages")
+                unkeyed.append((index, path, tail, rid, pages[:1]))
+                continue
+            groups.setdefault(key, []).append((index, path, tail))
+        if unkeyed:
+            keys = _int_list(torch.cat([e[4] for e in unkeyed]))
+            self.hot_path_host_transfer_batches += 1
+            self.hot_path_host_transfer_elements += len(keys)
+            for (index, path, tail, rid, _), key in zip(unkeyed, keys):
+                self.route_tail_page_keys[rid] = int(key)
+                groups.setdefault(int(key), []).append((index, path, tail))
+        plan = [entry for group in groups.values() for entry in group[1:]]
+        if not plan:
+            return result, {}
+        dest_pages = self._allocate_full_pages(len(plan))
+        dirty: dict[int, int] = {}
+        dst_parts, src_parts = [], []
+        for page, (index, path, tail) in zip(dest_pages, plan):
+            src = path[-tail:]
+            dst = page[:tail]
+            dst_parts.append(dst)
+            src_parts.append(src)
+            new_path = torch.cat((path[:-tail], dst))
+            rid = int(routes[index].route_id)
+            self.route_slot_paths[rid] = new_path
+            self.route_tail_page_keys[rid] = self._new_tail_page_key()
+            result[index] = new_path
+            dirty[index] = int(path.numel()) - tail
+            self.cow_pages_copied += 1
+            self.cow_tokens_copied += tail
+        self._copy_kv_slots(torch.cat(dst_parts), torch.cat(src_parts))
+        return result, dirty
+
+    # ------------------------------------------------------------ frontier
+    def prepare_frontier(self, active_routes: Sequence[RouteState], *,
+                         output_slot_ids: torch.Tensor | None = None):
+        """Rows, copy-on-write, decode slots, incremental request-row writes
+        and page metadata for one decode step (``sglang_runtime.py:800-959``)."""
+        if not active_routes:
+            raise ValueError("active_routes cannot be empty")
+        req_indices = self.ensure_route_rows(active_routes)
+        input_ids = torch.tensor([int(r.pending_token_id) for r in active_routes], dtype=torch.long,
+                                 device=self.device)
+        paths = [self._slot_path_for_route(r) for r in active_routes]
+        paths, dirty = self._copy_partial_tail_pages_with_dirty_starts(active_routes, paths)
+        for index, start in dirty.items():
+            row = self.route_rows[int(active_routes[index].route_id)]
+            if int(row.written_length) > 0:
+                row.pending_dirty_start = int(start) if row.pending_dirty_start is None else min(
+                    int(row.pending_dirty_start), int(start))
+        seq_lens = [int(p.numel()) + 1 for p in paths]
+        last_locs = torch.cat([
+            p[-1:].to(torch.long) if int(p.numel()) else torch.full((1,), -1, dtype=torch.long, device=self.device)
+            for p in paths
+        ])
+        if output_slot_ids is None:
+            output_slot_ids = self.allocate_decode_slots(seq_lens=seq_lens, last_locs=last_locs)
+        else:
+            output_slot_ids = _as_long(output_slot_ids, self.device)
+        if int(output_slot_ids.numel()) != len(active_routes):
+            raise ValueError("output_slot_ids must have one slot per active route")
+        if len(active_routes) > 1:
+            dup = output_slot_ids[:, None].eq(output_slot_ids[None, :])
+            dup.fill_diagonal_(False)
+            self._check_or_defer(dup.logical_not().all(),
+                                 "SGLang allocated duplicate output KV slots across forked routes; "
+                                 "tail-page copy-on-write is not active")
+        self._record_pending_owned_slots(output_slot_ids)
+
+        positions: list[int] = []
+        full_paths: list[torch.Tensor] = []
+        for i, (route, path) in enumerate(zip(active_routes, paths)):
+            rid = int(route.route_id)
+            row = self.route_rows[rid]
+            full = torch.cat([path, output_slot_ids[i : i + 1]])
+            prev = int(path.numel())
+            if int(row.written_length) == 0:
+                start, values, kind = 0, full, "full_init"
+            else:
+                if int(row.written_length) != prev:
+                    raise RuntimeError(
+                        "SGLang route-row state does not match its physical KV path: "
+                        f"route_id={rid}, written_length={int(row.written_length)}, physical_path_length={prev}"
+                    )
+                if row.pending_dirty_start is None:
+                    start, values, kind = prev, full[prev:], "append"
+                else:
+                    start = int(row.pending_dirty_start)
+                    values, kind = full[start:], "cow_patch"
+            self._write_req_token_slice(int(row.req_pool_index), start, values, write_kind=kind)
+            row.written_length = int(full.numel())
+            row.pending_dirty_start = None
+            self.route_slot_paths[rid] = full
+            if prev % self.page_size == 0 or rid not in self.route_tail_page_keys:
+                self.route_tail_page_keys[rid] = self._new_tail_page_key()
+            positions.append(int(full.numel()) - 1)
+            full_paths.append(full)
+
+        seq_cpu = torch.tensor(seq_lens, dtype=torch.long)
+        seq_dev = seq_cpu.to(self.device)
+        tokens = int(sum(seq_lens))
+        spec = None
+        attn_ps = 1
+        page_indices = tokens
+        if self.use_page_attention_metadata:
+            md = build_flashinfer_paged_kv_metadata(full_paths, page_size=self.page_size,
+                                                    validate_layout=self.validate_page_layout)
+            if md.layout_flag is not None:
+                self.pending_device_checks.append(md.assert_layout_valid)
+            spec = AtlasPagedDecodeSpec(md.kv_indptr, md.kv_page_indices, md.kv_last_page_len, int(md.page_size))
+            attn_ps = int(md.page_size)
+            page_indices = int(md.page_index_count)
+        self.attention_metadata_builds += 1
+        self.attention_metadata_token_indices += tokens
+        self.attention_metadata_page_indices += page_indices
+        meta = SGLangRouteKVMetadata(
+            req_pool_indices=req_indices, seq_lens=seq_dev, out_cache_loc=output_slot_ids,
+            positions=torch.tensor(positions, dtype=torch.long, device=self.device), orig_seq_lens=seq_dev,
+            seq_lens_sum=tokens, seq_lens_cpu=seq_cpu, attention_page_size=attn_ps, token_index_count=tokens,
+            page_index_count=page_indices, paged_decode_spec=spec,
+        )
+        return input_ids, meta
+
+    def _check_or_defer(self, ok: torch.Tensor, message: str) -> None:
+        """A device-computed condition is checked at the next report boundary
+        (prune), so the decode step does not wait on it; a host condition is
+        checked now."""
+        if ok.device.type == "cpu":
+            _assert_true(ok, message)
+        else:
+            self.pending_device_checks.append(lambda: _assert_true(ok, message))
+
+    def check_pending_device_checks(self) -> None:
+        """Raise the first failed deferred condition (layout of frontier page
+        metadata, distinct output slots) recorded since the last check."""
+        pending, self.pending_device_checks = self.pending_device_checks, []
+        for check in pending:
+            check()
+
+    def _slot_path_for_route(self, route: RouteState) -> torch.Tensor:
+        """Existing path, else the parent's (inheriting its lease), else a
+        committed-prefix slice keyed by the prefix's partial-tail lease
+        (``sglang_runtime.py:961-1021``)."""
+        rid = int(route.route_id)
+        expected = int(route.kv_view.prefix.committed_length) + len(route.kv_view.node_ids)
+        existing = self.route_slot_paths.get(rid)
+        if existing is not None:
+            if int(existing.numel()) != expected:
+                raise RuntimeError(
+                    "route-specific physical path length does not match logical KV: "
+                    f"route_id={rid}, physical={int(existing.numel())}, logical={expected}"
+                )
+            return existing
+        if route.parent_route_id is not None:
+            pid = int(route.parent_route_id)
+            parent = self.route_slot_paths.get(pid)
+            if parent is not None:
+                if int(parent.numel()) != expected:
+                    raise RuntimeError(
+                        "inherited physical path length does not match logical KV: "
+                        f"route_id={rid}, physical={int(parent.numel())}, logical={expected}"
+                    )
+                self.route_slot_paths[rid] = parent
+                key = self.route_tail_page_keys.get(pid)
+                if key is not None:
+                    self.route_tail_page_keys[rid] = key
+                return parent
+        committed = int(route.kv_view.prefix.committed_length)
+        if committed:
+            if self.prefix_slot_ids is None:
+                raise RuntimeError("prefix_slot_ids must be set before decoding non-empty prefixes")
+            if int(self.prefix_slot_ids.numel()) < committed:
+                raise RuntimeError(
+                    f"prefix_slot_ids has length {int(self.prefix_slot_ids.numel())}, "
+                    f"but route requires committed_length={committed}"
+                )
+            prefix = self.prefix_slot_ids[:committed]
+        else:
+            prefix = torch.empty((0,), dtype=torch.long, device=self.device)
+        if route.kv_view.node_ids:
+            raise RuntimeError(
+                "route has materialized logical KV nodes but no route-specific physical slot path: "
+                f"route_id={rid}"
+            )
+        self.route_slot_paths[rid] = prefix
+        if committed % self.page_size:
+            tail_index = (committed - 1) // self.page_size
+            key = self.prefix_partial_tail_keys.get(tail_index)
+            if key is None:
+                key = self._new_tail_page_key()
+                self.prefix_partial_tail_keys[tail_index] = key
+            if committed == self.prefix_slot_count:
+                self.prefix_tail_page_key = key
+            self.route_tail_page_keys[rid] = key
+        return prefix
+
+    # ------------------------------------------------------------ request rows
+    def _write_req_token_row(self, req_pool_index: int, slot_path: torch.Tensor) -> None:
+        self._write_req_token_slice(req_pool_index, 0, slot_path, write_kind="full_init")
+
+    def _write_req_token_slice(self, req_pool_index: int, start: int, slot_ids: torch.Tensor, *,
+                               write_kind: str) -> None:
+        """Write ``slot_ids`` into a request row at ``start`` (slice API, then
+        the tensor-index form); counters count successful writes only
+        (``sglang_runtime.py:1031-1092``)."""
+        if write_kind not in {"full_init", "append", "cow_patch"}:
+            raise ValueError(f"unknown req-row write kind: {write_kind}")
+        start = int(start)
+        if start < 0:
+            raise ValueError("req-row write start must be non-negative")
+        values = _as_long(slot_ids, self.device)
+        n = int(values.numel())
+        if n <= 0:
+            raise ValueError("req-row write cannot be empty")
+        end = start + n
+        cap = _req_pool_capacity(self.req_to_token_pool)
+        if cap is None:
+            cap = self.max_context_len
+        if cap is not None and end > int(cap):
+            raise RuntimeError(
+                "SGLang req_to_token_pool row is too short for the requested prefix. "
+                f"write_end={end}, req_pool_context_capacity={int(cap)}, req_pool_index={int(req_pool_index)}. "
+                "Increase --context-length or recreate the runner with a larger ReqToTokenPool."
+            )
+        try:
+            self.req_to_token_pool.write((int(req_pool_index), slice(start, end)), values)
+        except Exception:
+            pos = torch.arange(start, end, dtype=torch.long, device=values.device)
+            rows = torch.full_like(pos, int(req_pool_index))
+            try:
+                self.req_to_token_pool.write((rows, pos), values)
+            except Exception as exc:
+                raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
+        self.req_row_write_calls += 1
+        self.req_row_elements_written += n
+        if write_kind == "full_init":
+            self.req_row_full_init_calls += 1
+            self.req_row_full_init_elements += n
+            self.req_row_full_rewrite_calls += 1
+            self.req_row_full_rewrite_elements += n
+        elif write_kind == "append":
+            self.req_row_append_calls += 1
+            self.req_row_append_elements += n
+        else:
+            self.req_row_cow_patch_calls += 1
+            self.req_row_cow_patch_elements += n
+
+    def hot_path_counters(self) -> dict[str, int]:
+        return {name: int(getattr(self, name)) for name in _COUNTERS}
+
+
+class SGLangFlashInferFrontierModelBackend:
+    """Drafter frontier backend over the route pool
+    (``sglang_runtime.py:1120-1346``).
+
+    ``executor`` runs the Drafter model and must write each new token's K/V
+    into the slots it is given (the model itself is outside this path):
+
+    * ``forward_frontier(input_ids=, route_kv_metadata=) -> logits [B, V]``
+      (one DECODE step: K/V of route i go to ``out_cache_loc[i]``);
+    * ``forward_extend(input_ids=, out_cache_loc=, positions=,
+      req_pool_indices=, seq_lens_cpu=) -> logits [n, V] or [V]``
+      (one EXTEND of a known causal suffix).
+    """
+
+    def __init__(self, *, route_store: KVTreeStore, executor: Any, route_pool: SGLangRoutePoolBridge) -> None:
+        self.route_store = route_store
+        self.executor = executor
+        self.route_pool = route_pool
+        self.prefix_token_ids: tuple[int, ...] = ()
+        self.prefix_next_token_logits: torch.Tensor | None = None
+        hook = getattr(route_store, "add_route_release_hook", None)
+        if callable(hook):
+            hook(route_pool.reconcile_route_rows)
+
+    def attach_prefilled_prefix(self, *, prompt_token_ids: Sequence[int], prefix_slot_ids,
+                                next_token_logits: torch.Tensor) -> DraftPrefixState:
+        self.prefix_token_ids = tuple(int(t) for t in prompt_token_ids)
+        self.prefix_next_token_logits = next_token_logits
+        self.route_pool.set_prefix_slots(prefix_slot_ids)
+        n = len(self.prefix_token_ids)
+        return DraftPrefixState(
+            token_ids=torch.tensor(self.prefix_token_ids, dtype=torch.long, device=next_token_logits.device),
+            prefix_kv_view=PrefixKVView(committed_length=n), next_token_logits=next_token_logits,
+            committed_length=n)
+
+    def set_prefix(self, token_ids: Sequence[int]) -> None:
+        self.prefix_token_ids = tuple(int(t) for t in token_ids)
+
+    @torch.inference_mode()
+    def append_known_tokens_as_prefix(self, token_ids: Sequence[int]) -> torch.Tensor:
+        """Fallback EXTEND: slots continuing the prefix's partial tail page,
+        one request-row write, one EXTEND forward, then the extended path
+        becomes the prefix with a fresh tail lease (``:1171-1251``)."""
+        suffix = tuple(int(t) for t in token_ids)
+        if not suffix:
+            raise ValueError("known prefix extension cannot be empty")
+        pool = self.route_pool
+        prefix_slots = pool.prefix_slot_ids
+        if prefix_slots is None or int(prefix_slots.numel()) != len(self.prefix_token_ids):
+            raise RuntimeError("persistent Drafter prefix slots are not initialized")
+        device = pool.device
+        prefix_len = len(self.prefix_token_ids)
+        seq_len = prefix_len + len(suffix)
+        handle = _PoolReqHandle(rid="atlas-known-prefix-extend")
+        indices = pool.req_to_token_pool.alloc([handle])
+        if indices is None:
+            raise RuntimeError("SGLang ReqToTokenPool.alloc returned None for known-token extend")
+        row = int(_int_list(indices)[0])
+        handle.req_pool_idx = row
+        try:
+            last = prefix_slots[-1:].to(torch.long) if prefix_len else torch.full((1,), -1, dtype=torch.long,
+                                                                                 device=device)
+            suffix_slots = pool.allocate_extend_slots(prefix_lens=[prefix_len], seq_lens=[seq_len], last_locs=last)
+            full = torch.cat([prefix_slots, suffix_slots])
+            pool._write_req_token_row(row, full)
+            logits = self.executor.forward_extend(
+                input_ids=torch.tensor(suffix, dtype=torch.long, device=device), out_cache_loc=suffix_slots,
+                positions=torch.arange(prefix_len, seq_len, dtype=torch.long, device=device),
+                req_pool_indices=torch.tensor([row], dtype=torch.long, device=device),
+                seq_lens_cpu=torch.tensor([seq_len], dtype=torch.long))
+        finally:
+            if hasattr(pool.req_to_token_pool, "free"):
+                pool.req_to_token_pool.free(handle)
+        pool.set_prefix_slots(full)
+        self.prefix_token_ids = (*self.prefix_token_ids, *suffix)
+        return logits if logits.ndim == 1 else logits[-1]
+
+    def commit_stage1_and_promote(self, *, committed_route: RouteState, retained_routes: Sequence[RouteState]):
+        """Promote the committed route's path to the prefix (no KV copy),
+        rebase the retained routes, free the other rows, prune
+        (``:1256-1297``)."""
+        nodes = self.route_store.node_path_for_route(committed_route)
+        if not nodes:
+            raise ValueError("cannot commit a stage-1 route with no materialized nodes")
+        tokens = self.route_store.tokens_for_node_ids(nodes)
+        self.route_pool.commit_route_as_prefix(committed_route)
+        stored = self.route_store.commit_route(committed_route)
+        if stored != tokens:
+            raise RuntimeError("logical committed tokens changed during route promotion")
+        self.prefix_token_ids = (*self.prefix_token_ids, *tokens)
+        promoted = self.route_store.promote_routes_after_commit(
+            committed_route, retained_routes, PrefixKVView(committed_length=len(self.prefix_token_ids)))
+        released_rows = self.route_pool.retain_route_rows([r.route_id for r in promoted])
+        live = sorted({int(n) for r in promoted for n in r.kv_view.node_ids})
+        released_pages = self.route_pool.release_unreferenced_node_slots(live)
+        return promoted, {
+            "committed_kv_tokens": len(nodes),
+            "retained_routes": len(promoted),
+            "released_route_rows": released_rows,
+            "released_kv_pages": released_pages,
+        }
+
+    @torch.inference_mode()
+    def decode_frontier_one_token(self, active_routes: Sequence[RouteState],
+                                  attention_backend: object = None) -> FrontierDecodeOutput:
+        start = time.perf_counter()
+        before = self.route_pool.hot_path_counters()
+        new_nodes = self.route_store.reserve_node_ids(len(active_routes))
+        input_ids, metadata = self.route_pool.prepare_frontier(active_routes)
+        logits = self.executor.forward_frontier(input_ids=input_ids, route_kv_metadata=metadata)
+        self.route_pool.register_node_slots(new_nodes, metadata.out_cache_loc)
+        after = self.route_pool.hot_path_counters()
+        return FrontierDecodeOutput(
+            route_ids=torch.tensor([int(r.route_id) for r in active_routes], dtype=torch.long,
+                                   device=input_ids.device),
+            next_token_logits=logits, new_node_ids=tuple(new_nodes), new_node_ids_cpu=tuple(new_nodes),
+            model_ms=(time.perf_counter() - start) * 1000.0,
+            metadata={
+                "backend": "atlas_hip_paged_decode",
+                "paged_kv": True,
+                "route_tail_page_cow": True,
+                "cow_pages_copied_total": int(self.route_pool.cow_pages_copied),
+                "cow_tokens_copied_total": int(self.route_pool.cow_tokens_copied),
+                "attention_metadata_page_size": int(metadata.attention_page_size),
+                "attention_metadata_token_indices_step": int(metadata.token_index_count),
+                "attention_metadata_page_indices_step": int(metadata.page_index_count),
+                "hot_path_counter_delta": {k: int(after[k] - before.get(k, 0)) for k in after},
+                "hot_path_counters_total": after,
+                "attention_backend": str(attention_backend),
+            },
+        )
+
+
+_COUNTERS = (
+    "attention_metadata_builds",
+    "attention_metadata_token_indices",
+    "attention_metadata_page_indices",
+    "cow_pages_copied",
+    "cow_tokens_copied",
+    "req_row_write_calls",
+    "req_row_elements_written",
+    "req_row_full_rewrite_calls",
+    "req_row_full_rewrite_elements",
+    "req_row_full_init_calls",
+    "req_row_full_init_elements",
+    "req_row_append_calls",
+    "req_row_append_elements",
+    "req_row_cow_patch_calls",
+    "req_row_cow_patch_elements",
+    "hot_path_host_transfer_batches",
+    "hot_path_host_transfer_elements",
+)
+
+
+def _allocate_kv_slots(allocator: Any, count: int, *, mode: str) -> Any:
+    names = {"extend": ["alloc_extend", "alloc"], "decode": ["alloc_decode", "alloc"]}.get(mode, ["alloc"])
+    errors: list[str] = []
+    for name in names:
+        fn = getattr(allocator, name, None)
+        if not callable(fn):
+            continue
+        try:
+            result = fn(int(count))
+        except Exception as exc:
+            errors.append(f"{name}({int(count)},): {exc!r}")
+            continue
+        if result is not None:
+            return result
+        errors.append(f"{name}({int(count)},): returned None")
+    raise RuntimeError(
+        "SGLang token_to_kv_pool_allocator could not allocate slots. "
+        + ("; ".join(errors) if errors else "no supported allocation method")
+    )
+
+
+def _slot_tensor(result: Any, device) -> torch.Tensor:
+    if isinstance(result, torch.Tensor):
+        return _as_long(result, device)
+    if isinstance(result, (list, tuple)):
+        tensors = [x for x in result if isinstance(x, torch.Tensor)]
+        if tensors:
+            return _as_long(tensors[0], device)
+        flat: list[int] = []
+        for item in result:
+            if isinstance(item, int):
+                flat.append(int(item))
+            elif isinstance(item, (list, tuple)) and all(isinstance(v, int) for v in item):
+                flat.extend(int(v) for v in item)
+        if flat:
+            return _as_long(flat, device)
+    return _as_long(result, device)
+
+
+def _req_pool_capacity(req_pool: Any) -> int | None:
+    if req_pool is None:
+        return None
+    for name in ("req_to_token", "req_to_token_pool", "req_to_token_table", "pool", "data"):
+        value = getattr(req_pool, name, None)
+        if isinstance(value, torch.Tensor) and value.ndim >= 2:
+            return int(value.shape[1])
+    try:
+        attrs = vars(req_pool)
+    except TypeError:
+        return None
+    for value in attrs.values():
+        if isinstance(value, torch.Tensor) and value.ndim >= 2:
+            return int(value.shape[1])
+    return None
+
+
+def _as_long(value, device) -> torch.Tensor:
+    t = value if isinstance(value, torch.Tensor) else torch.tensor(list(value), dtype=torch.long)
+    t = t.to(device=device, dtype=torch.long)
+    if t.ndim != 1:
+        raise ValueError(f"expected a 1D tensor, got shape {tuple(t.shape)}")
+    return t
+
+
+def _assert_true(condition: torch.Tensor, message: str) -> None:
+    """Host check of a scalar tensor.  (The reference uses a device-side
+    assertion on GPU tensors; a device trap is avoided here, so a GPU
+    condition is read back, which synchronises -- this check runs only on
+    foreign-allocator and lease-less compatibility paths.)"""
+    if condition.numel() != 1:
+        raise ValueError("device assertion condition must be scalar")
+    if not bool(condition.item()):
+        raise RuntimeError(message)
+
+
+def _int_list(value) -> list[int]:
+    if isinstance(value, torch.Tensor):
+        return [int(x) for x in value.detach().cpu().reshape(-1).tolist()]
+    return [int(x) for x in value]

@@ -24,6 +24,14 @@ Pinning (what each function is checked against in ``tests/``):
                              SGLang's own allocator is absent: parity unpinned
                              against it (only against this restated policy).
 * ``scoring``             -- reference literals (test_target_kv_commit.py:76-367)
-* ``RoutePool``           -- reference literals (test_tail_page_cow.py,
-                             test_req_row_incremental.py)
+* ``route_pool``          -- host pools for the route-pool trace: the
+                             ``PagedAllocator`` policy above, slot contents as
+                             value ids with ``move_kv_cache`` = FakeKVCache
+                             semantics (test_tail_page_cow.py:14-16), request
+                             rows.  The bridge's host logic run over them is
+                             pinned by the reference's bridge-test literals
+                             (test_tail_page_cow.py:61-383,
+                             test_req_row_incremental.py:151-473) and by the
+                             content invariant "slot path of every route holds
+                             the value ids of its prefix and nodes".
 """

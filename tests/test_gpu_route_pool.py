@@ -1,0 +1,171 @@
+"""Route-pool bridge on the native HIP pools vs the same trace on host pools:
+slot paths, leases, request rows, owned pages, the allocator's free list and
+every live slot's K/V bytes (all layers) must be identical at every phase."""
+
+import pytest
+import torch
+
+from helpers import pkg
+from oracle.route_pool import OracleAllocator, OracleReqPool
+
+pytestmark = pytest.mark.gpu
+
+
+def _device_run(plans, *, page_size, num_pages, layers, heads, head_dim, dev, host_phases):
+    """Runs the trace on the native pools; after each phase compares the
+    bookkeeping and the live slots' K/V bytes with the host run's phase."""
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    req, kv, alloc = npool.create_native_pools(num_pages=num_pages, page_size=page_size, dtype=torch.bfloat16,
+                                               head_num=heads, head_dim=head_dim, layer_num=layers,
+                                               max_running_requests=128, max_context_len=4096, device=dev)
+
+    def writer(slots, vids):
+        v = vids.to(dev)
+        k_rows = [dw.kv_pattern(v, l, 0, heads, head_dim).view(torch.bfloat16) for l in range(layers)]
+        v_rows = [dw.kv_pattern(v, l, 1, heads, head_dim).view(torch.bfloat16) for l in range(layers)]
+        kv.set_kv_buffer_all_layers(slots, k_rows, v_rows)
+
+    wl = dw.DrafterForkWorkload(plans=plans, req_pool=req, allocator=alloc, page_size=page_size, device=dev,
+                                writer=writer)
+    seen = []
+
+    def compare(phase):
+        torch.cuda.synchronize()
+        i = len(seen)
+        seen.append(phase)
+        hphase, hs, values = host_phases[i]
+        assert hphase == phase
+        ds = _state(wl, alloc.free_pages.tolist(), req.req_to_token)
+        assert ds == hs, f"bookkeeping differs after {phase}"
+        _check_kv(kv, values, _live_slots(hs), layers, heads, head_dim, dev, phase)
+
+    wl.run(compare)
+    assert seen == [p for p, _, _ in host_phases]
+
+
+def _host_run(plans, *, page_size, num_pages, phases):
+    dw = pkg("drafter_workload")
+    alloc = OracleAllocator(num_pages=num_pages, page_size=page_size)
+    rows = OracleReqPool(size=128, max_context_len=4096)
+    wl = dw.DrafterForkWorkload(plans=plans, req_pool=rows, allocator=alloc, page_size=page_size, device="cpu",
+                                writer=lambda s, v: alloc.kv.write(s.numpy(), v.numpy()),
+                                use_page_attention_metadata=False)
+    wl.run(lambda phase: phases.append((phase, _state(wl, alloc.free_pages, rows.req_to_token), alloc.kv.values.copy())))
+    return wl
+
+
+def _state(wl, free_pages, req_to_token):
+    out = {"free": list(free_pages)}
+    for i, r in enumerate(wl.requests):
+        b = r.bridge
+        b.check_pending_device_checks()
+        rows = {}
+        for rid, row in sorted(b.route_rows.items()):
+            n = int(row.written_length)
+            rows[rid] = (row.req_pool_index, n, row.pending_dirty_start,
+                         req_to_token[row.req_pool_index, :n].cpu().tolist())
+        b._materialize_pending_owned_pages()
+        out[i] = {
+            "prefix": b.prefix_slot_ids.cpu().tolist(),
+            "paths": {rid: p.cpu().tolist() for rid, p in sorted(b.route_slot_paths.items())},
+            "keys": dict(sorted(b.route_tail_page_keys.items())),
+            "prefix_keys": (b.prefix_tail_page_key, dict(b.prefix_partial_tail_keys)),
+            "rows": rows,
+            "owned": sorted(set(b.owned_page_ids)),
+            # page-index counts differ by design: the host run builds no page metadata
+            "counters": {k: v for k, v in b.hot_path_counters().items() if k != "attention_metadata_page_indices"},
+            "stats": list(r.stats),
+        }
+    return out
+
+
+def _live_slots(state):
+    slots = set()
+    for k, v in state.items():
+        if k == "free":
+            continue
+        slots.update(v["prefix"])
+        for p in v["paths"].values():
+            slots.update(p)
+    return sorted(slots)
+
+
+def _check_kv(kv, values, slots, layers, heads, head_dim, dev, phase):
+    dw = pkg("drafter_workload")
+    s = torch.tensor(slots, dtype=torch.long, device=dev)
+    ids = torch.tensor(values[slots], dtype=torch.long, device=dev)
+    for l in range(layers):
+        for which, buf in ((0, kv.k_buffer[l]), (1, kv.v_buffer[l])):
+            got = buf[s].view(torch.int16)
+            exp = dw.kv_pattern(ids, l, which, heads, head_dim)
+            bad = (got != exp).reshape(len(slots), -1).any(-1)
+            assert not bool(bad.any()), f"{phase}: layer {l} kv {which} differs at slots " \
+                                        f"{s[bad][:8].tolist()}"
+
+
+@pytest.mark.parametrize("case", ["config1", "config5_seed0", "config5_seed1"])
+def test_route_pool_trace_matches_host_pools(dev, case):
+    dw = pkg("drafter_workload")
+    if case == "config1":
+        plans, ps, pages = dw.config1_plans(0), 16, 4096
+    else:
+        plans, ps, pages = dw.config5_plans(8, 64, int(case[-1])), 64, 640
+    layers, heads, head_dim = 16, 8, 64
+    print(f"route-pool trace {case}: page_size {ps}, {pages} pages", flush=True)
+    host = []
+    _host_run(plans, page_size=ps, num_pages=pages, phases=host)
+    _device_run(plans, page_size=ps, num_pages=pages, layers=layers, heads=heads, head_dim=head_dim, dev=dev,
+                host_phases=host)
+
+
+def test_device_ownership_set_operations(dev):
+    sr = pkg("flashinfer_paged.sglang_runtime")
+    own = sr.DeviceOwnedPages(100, 16, dev)
+    own.mark_slots(torch.tensor([0, 17, 33, 1599], device=dev))
+    assert own == {0, 1, 2, 99}
+    own.update({40, 41})
+    own.difference_update([1])
+    own.remove(99)
+    assert sorted(own) == [0, 2, 40, 41] and 40 in own and 1 not in own and len(own) == 4
+    freed = own.sweep(torch.tensor([32, 41 * 16 + 3], device=dev))
+    assert freed.tolist() == [0, 40] and own == {2, 41}
+    with pytest.raises(KeyError):
+        own.remove(7)
+    own.clear()
+    assert own == set()
+
+
+def test_frontier_page_metadata_matches_oracle(dev):
+    from oracle import paged_kv as ref
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    req, kv, alloc = npool.create_native_pools(num_pages=640, page_size=64, dtype=torch.bfloat16, head_num=8,
+                                               head_dim=64, layer_num=2, max_running_requests=128,
+                                               max_context_len=4096, device=dev)
+    specs = []
+
+    def writer(slots, vids):
+        rows = [torch.zeros((int(slots.numel()), 8, 64), dtype=torch.bfloat16, device=dev)] * 2
+        kv.set_kv_buffer_all_layers(slots, rows, rows)
+
+    wl = dw.DrafterForkWorkload(plans=dw.config5_plans(2, 64, 3), req_pool=req, allocator=alloc, page_size=64,
+                                device=dev, writer=writer)
+    orig = wl.requests[0].bridge.prepare_frontier
+
+    def spy(routes, **kw):
+        ids, md = orig(routes, **kw)
+        paths = [wl.requests[0].bridge.route_slot_paths[int(r.route_id)].tolist() for r in routes]
+        specs.append((md, paths))
+        return ids, md
+
+    wl.requests[0].bridge.prepare_frontier = spy
+    wl.run()
+    assert specs
+    for md, paths in specs:
+        exp = ref.paged_metadata(paths, 64)
+        spec = md.paged_decode_spec
+        assert spec.kv_indptr.tolist() == exp.kv_indptr
+        assert spec.kv_indices.tolist() == exp.kv_page_indices
+        assert spec.kv_last_page_len.tolist() == exp.kv_last_page_len
+        assert md.seq_lens_cpu.tolist() == exp.seq_lens
