@@ -31,6 +31,9 @@ constexpr int kTileKeys = 64;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleLog2 = 8.0f;
+// Largest row block of one work item: 16 row tiles of 16 (head_dim 128 with
+// pages of >= 16 tokens); other shapes take up to 12 row tiles.
+constexpr int kMaxRowsPerItem = 256;
 
 struct AttnArgs {
   const char* q;
@@ -465,6 +468,436 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
   }
 }
 
+// ---------------------------------------------------------------------------
+// head_dim 128: KV streamed into LDS with direct global->LDS loads.
+//
+// The K and V rows of a 64-key tile land in LDS through
+// global_load_lds_dwordx4 (each lane's 16 bytes go to the wave's 1 KiB block
+// at its lane position), so no registers or VALU work stage the KV.  A ring
+// of STAGES tiles keeps STAGES-1 tiles in flight while one is computed, with
+// one barrier per tile.  Rows are row-major in LDS with their 16-byte granules
+// XOR-swizzled by key: K by (key & 15), so the 16 keys a score-MFMA operand
+// read touches hit 16 distinct granules; V by 2*(key & 7), so the transposing
+// reads below spread over the banks.
+//
+// V^T for O^T += V^T P^T comes from ds_read_b64_tr_b16: within a 16-lane block,
+// output lane i, element e is element (i % 4) of the 8 bytes that source lane
+// 4e + i/4 addressed.  A lane with block index g and in-block index s = 4e + q
+// addresses V[key][16*dt + 4q .. 4q + 3] with key = 32*kk + 4g + e (first read)
+// or that key + 16 (second read), so output lane i holds V[key(g, e)][16dt + i]:
+// the A operand of the MFMA with its eight k-elements in the key order of the
+// score tile's C layout (keys 4g..4g+3 and 16+4g..16+4g+3 of the 32-key half).
+// ---------------------------------------------------------------------------
+constexpr int kRowBytes128 = 128 * 2;
+constexpr int kHalf128 = kTileKeys * kRowBytes128;  // 16 KiB of K, then 16 KiB of V
+constexpr int kTile128 = 2 * kHalf128;
+
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ v4i16 lds_read_tr16(const char* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4i16*)(reinterpret_cast<uintptr_t>(p)));
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0, vmcnt[5:4] in bits 15:14, expcnt 7, lgkmcnt 15).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// 16 bytes from global memory into LDS at (wave-uniform base + 16 * lane).
+// Issued as inline assembly so the compiler's wait-count pass, which would
+// wait for every outstanding load before each LDS read, leaves the ring's
+// in-flight tiles alone; the kernel waits for them explicitly (wait_vmcnt).
+__device__ __forceinline__ void dma16(const char* gaddr, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base) : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
+}
+
+typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
+
+// Physical pages of the 4-key blocks a wave loads in a tile: with NW waves,
+// wave w loads blocks NW*j + w (keys 4*(NW*j + w) .. +3) for j < 16/NW.  Page
+// size is a power of two >= 16, so a block never straddles a page (the split's
+// last block clamps to its last key).  Scalar loads: wave-uniform, counted
+// apart from the KV loads.
+template <int NW>
+__device__ __forceinline__ void tile_pages(const_i32_ptr pages, int t0, int last_key, int page_shift, int wave,
+                                           int (&pid)[16 / NW]) {
+#pragma unroll
+  for (int j = 0; j < 16 / NW; ++j) pid[j] = pages[min(t0 + 4 * (NW * j + wave), last_key) >> page_shift];
+}
+
+// Issue the K and V rows of one tile into a stage: lane l of wave w loads,
+// for each of its blocks b = NW*j + w, granule (l % 16) of the swizzled row of
+// key 4b + l/16 into the 1 KiB block b of the K and V halves.
+template <int NW>
+__device__ __forceinline__ void issue_tile(const char* head_base, int64_t page_stride, int64_t token_stride,
+                                           int64_t v_offset, const int (&pid)[16 / NW], int t0, int last_key,
+                                           int page_size, int wave, int lane, uint32_t stage) {
+  const int c16p = lane & 15;
+#pragma unroll
+  for (int j = 0; j < 16 / NW; ++j) {
+    const int blk = NW * j + wave;
+    const int key = 4 * blk + (lane >> 4);
+    const int p = min(t0 + key, last_key);
+    const char* row = head_base + int64_t(pid[j]) * page_stride + int64_t(p & (page_size - 1)) * token_stride;
+    dma16(row + ((c16p ^ (key & 15)) << 4), stage + blk * 1024);
+    dma16(row + v_offset + ((c16p ^ ((key & 7) << 1)) << 4), stage + kHalf128 + blk * 1024);
+  }
+}
+
+// Per-wave state of the rows a compute wave owns.
+template <bool BF16, int RT>
+struct RowState {
+  typename Mfma<BF16>::frag qf[RT][4];
+  f32x4 o[RT][8];
+  float m_run[RT];
+  float l_run[RT];
+  uint64_t tbits[RT];
+  int climit[RT];
+};
+
+// Scores S^T = K Q^T of one 64-key tile for a wave's RT row tiles.
+template <bool BF16, int RT>
+__device__ __forceinline__ void d128_scores(const RowState<BF16, RT>& st, const char* sb, int grp, int r16,
+                                            f32x4 (&s)[RT][4]) {
+  typedef Mfma<BF16> M;
+  typedef typename M::frag frag;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int kt = 0; kt < 4; ++kt) {
+    frag af[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      af[ks] = __builtin_bit_cast(
+          frag, *reinterpret_cast<const uint4*>(sb + (kt * 16 + r16) * kRowBytes128 + (((ks * 4 + grp) ^ r16) << 4)));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) s[rt][kt] = M::run(af[ks], st.qf[rt][ks], s[rt][kt]);
+  }
+}
+
+// Online softmax of one tile's scores (lazy rescale, applied branch-free so
+// the tile's instructions form one block the scheduler can interleave with
+// the next tile's score MFMAs) and O^T += V^T P^T with V^T from transposing
+// LDS reads.  MASKED tiles apply the tree / causal / length mask.
+template <bool BF16, int RT, bool MASKED>
+__device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][4], const char* sb, int t0,
+                                                int kv_end, int col0, int mask_mode, float scale_log2, int grp,
+                                                int r16) {
+  typedef Mfma<BF16> M;
+  typedef typename M::frag frag;
+  frag pf[RT][2];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = t0 + kt * 16 + grp * 4 + i;
+          bool vis = p < kv_end;
+          if (mask_mode == ATLAS_MASK_TREE) {
+            const int b = p - col0;
+            const bool bit = ((st.tbits[rt] >> (b & 63)) & 1ull) != 0;
+            vis = vis & ((p < col0) | ((b < 64) & bit));
+          } else if (mask_mode == ATLAS_MASK_CAUSAL) {
+            vis = vis & (p <= st.climit[rt]);
+          }
+          s[rt][kt][i] = vis ? s[rt][kt][i] : -INFINITY;
+        }
+      }
+    }
+    float mx = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
+                     fmaxf(fmaxf(s[rt][1][0], s[rt][1][1]), fmaxf(s[rt][1][2], s[rt][1][3])));
+    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[rt][2][0], s[rt][2][1]), fmaxf(s[rt][2][2], s[rt][2][3])),
+                         fmaxf(fmaxf(s[rt][3][0], s[rt][3][1]), fmaxf(s[rt][3][2], s[rt][3][3]))));
+    mx = wave_max_across_groups(mx) * scale_log2;
+    // Rescale only when the row maximum grew by more than kRescaleLog2 (so P
+    // stays below 2^kRescaleLog2); alpha = 1 leaves O and l unchanged.
+    const bool grow = mx > st.m_run[rt] + kRescaleLog2;
+    const float m_new = grow ? fmaxf(st.m_run[rt], mx) : st.m_run[rt];
+    const float alpha = (grow && st.m_run[rt] != -INFINITY) ? __builtin_amdgcn_exp2f(st.m_run[rt] - m_new)
+                                                            : (grow ? 0.f : 1.f);
+    st.l_run[rt] *= alpha;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] *= alpha;
+    st.m_run[rt] = m_new;
+    const float neg_m = m_new == -INFINITY ? 0.f : -m_new;
+    uint32_t pk[4][2];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][0], scale_log2, neg_m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][1], scale_log2, neg_m));
+      const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][2], scale_log2, neg_m));
+      const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][3], scale_log2, neg_m));
+      pk[kt][0] = M::pack2(p0, p1);
+      pk[kt][1] = M::pack2(p2, p3);
+      st.l_run[rt] = M::sum2(pk[kt][1], M::sum2(pk[kt][0], st.l_run[rt]));
+    }
+    pf[rt][0] = __builtin_bit_cast(frag, uint4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]});
+    pf[rt][1] = __builtin_bit_cast(frag, uint4{pk[2][0], pk[2][1], pk[3][0], pk[3][1]});
+  }
+
+  const int e = r16 >> 2;
+  const int q = r16 & 3;
+  const char* vb = sb + kHalf128;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int key0 = 32 * kk + 4 * grp + e;
+    const char* vrow = vb + key0 * kRowBytes128 + ((q & 1) << 3);
+    const int vsw = (key0 & 7) << 1;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const char* p0 = vrow + (((2 * dt + (q >> 1)) ^ vsw) << 4);
+      const v4i16 lo = lds_read_tr16(p0);
+      const v4i16 hi = lds_read_tr16(p0 + 16 * kRowBytes128);
+      const frag av = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run(av, pf[rt][kk], st.o[rt][dt]);
+    }
+  }
+}
+
+// The KV ring holds kStages128 tiles.  Tile k is issued at loop iteration
+// k - 3; iteration t waits for tile t+1 (whose keys feed the score MFMAs
+// overlapped with tile t's softmax), then issues tile t+3 into the stage tile
+// t-1 used: tiles t and t+1 are being read, t+2 and t+3 are in flight.
+constexpr int kStages128 = 4;
+
+template <int NW>
+__device__ __forceinline__ void d128_issue(int k, int nt, const char* head_base, const AttnArgs& a,
+                                           const_i32_ptr pages, int (&pid)[16 / NW], int t_first, int last_key,
+                                           int wave, int lane, uint32_t lds0) {
+  if (k < nt) {
+    const int t0 = t_first + k * kTileKeys;
+    issue_tile<NW>(head_base, a.page_stride, a.token_stride, a.v_offset, pid, t0, last_key, a.page_size, wave, lane,
+                   lds0 + (k % kStages128) * kTile128);
+    if (k + 1 < nt) tile_pages<NW>(pages, t0 + kTileKeys, last_key, a.page_shift, wave, pid);
+  }
+}
+
+__device__ __forceinline__ void bare_barrier() {
+  // A bare s_barrier: the workgroup fence of __syncthreads would also wait
+  // for the tiles still in flight.
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Waits until tile `k` has landed given that tiles up to min(k + ahead, nt-1)
+// were issued after it (ahead <= 2).
+template <int NW>
+__device__ __forceinline__ void d128_wait(int k, int ahead, int nt) {
+  constexpr int L = 2 * (16 / NW);
+  const int after = min(ahead, nt - 1 - k);
+  if (after >= 2) wait_vmcnt<2 * L>();
+  else if (after == 1) wait_vmcnt<L>();
+  else wait_vmcnt<0>();
+}
+
+// Pre-loop ring step: tile 0 landed (tiles 1 and 2 may be in flight).
+template <int NW>
+__device__ __forceinline__ void d128_ring_first(int nt) {
+  d128_wait<NW>(0, 2, nt);
+  bare_barrier();
+}
+
+// Ring step of iteration t: tile t+1 landed (t+2 may be in flight), every
+// wave is past iteration t-1, issue tile t+3.
+template <int NW>
+__device__ __forceinline__ void d128_ring_step(int t, int nt, const char* head_base, const AttnArgs& a,
+                                               const_i32_ptr pages, int (&pid)[16 / NW], int t_first, int last_key,
+                                               int wave, int lane, uint32_t lds0) {
+  if (t + 1 < nt) d128_wait<NW>(t + 1, 1, nt);
+  bare_barrier();
+  d128_issue<NW>(t + 3, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+}
+
+// Rows of one compute wave: row tiles wave + NW * r for r < RT.  Loads the
+// queries and masks, runs the pipelined tile loop and writes the output (or
+// the split's partial state).
+template <bool BF16, int NW, int RT>
+__device__ __forceinline__ void d128_rows(const AttnArgs& a, const atlas_attn_work_t& w, const char* lds,
+                                          const char* head_base, const_i32_ptr pages, int (&pid)[16 / NW],
+                                          int t_first, int nt, int nt_plain, int last_key, int kv_end, int col0,
+                                          int qo_start, int qo_len, int kv_len, int wave, int lane, uint32_t lds0) {
+  typedef Mfma<BF16> M;
+  typedef typename M::frag frag;
+  constexpr int D = 128;
+  const int grp = lane >> 4;
+  const int r16 = lane & 15;
+  const int G = a.group;
+  const int kvh = w.kv_head;
+
+  RowState<BF16, RT> st;
+  int node_of[RT];
+  int head_of[RT];
+  bool row_ok[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int lr = (wave + NW * rt) * 16 + r16;
+    row_ok[rt] = lr < w.num_rows;
+    const int prow = w.row_start + (row_ok[rt] ? lr : 0);
+    node_of[rt] = prow / G;
+    head_of[rt] = kvh * G + (prow - node_of[rt] * G);
+    st.m_run[rt] = -INFINITY;
+    st.l_run[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const char* qrow = a.q + ((int64_t(qo_start + node_of[rt]) * a.q_stride_token +
+                               int64_t(head_of[rt]) * a.q_stride_head) * 2);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      uint4 v = *reinterpret_cast<const uint4*>(qrow + (ks * 32 + grp * 8) * 2);
+      if (!row_ok[rt]) v = uint4{0, 0, 0, 0};
+      st.qf[rt][ks] = __builtin_bit_cast(frag, v);
+    }
+    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && row_ok[rt]) ? a.tree_mask[qo_start + node_of[rt]] : 0ull;
+    st.climit[rt] = kv_len - qo_len + node_of[rt];
+  }
+  wait_vmcnt<0>();  // queries and masks (tiles 0..2 are issued later)
+
+  if (nt > 0) {
+    f32x4 s_cur[RT][4];
+    f32x4 s_nxt[RT][4];
+    d128_ring_first<NW>(nt);
+    d128_scores<BF16, RT>(st, lds, grp, r16, s_cur);
+    const int n_pipe = nt - 1;
+    const int plain_end = min(nt_plain, n_pipe);
+    int t = 0;
+    for (; t < plain_end; ++t) {
+      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+      d128_scores<BF16, RT>(st, lds + ((t + 1) % kStages128) * kTile128, grp, r16, s_nxt);
+      d128_softmax_pv<BF16, RT, false>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
+                                       col0, a.mask_mode, a.scale_log2, grp, r16);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s_cur[rt][kt] = s_nxt[rt][kt];
+    }
+    for (; t < n_pipe; ++t) {
+      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+      d128_scores<BF16, RT>(st, lds + ((t + 1) % kStages128) * kTile128, grp, r16, s_nxt);
+      d128_softmax_pv<BF16, RT, true>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
+                                      col0, a.mask_mode, a.scale_log2, grp, r16);
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int kt = 0; kt < 4; ++kt) s_cur[rt][kt] = s_nxt[rt][kt];
+    }
+    d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+    if (t < nt_plain)
+      d128_softmax_pv<BF16, RT, false>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
+                                       col0, a.mask_mode, a.scale_log2, grp, r16);
+    else
+      d128_softmax_pv<BF16, RT, true>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
+                                      col0, a.mask_mode, a.scale_log2, grp, r16);
+  }
+
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float l_tot = wave_sum_across_groups(st.l_run[rt]);
+    if (!row_ok[rt]) continue;
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float lse2 = l_tot > 0.f ? st.m_run[rt] + __builtin_log2f(l_tot) : -INFINITY;
+    const int lr = (wave + NW * rt) * 16 + r16;
+    if (w.partial_row < 0) {
+      char* orow = a.out + ((int64_t(qo_start + node_of[rt]) * a.out_stride_token +
+                             int64_t(head_of[rt]) * a.out_stride_head) * 2);
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const uint32_t lo = uint32_t(M::from_float(st.o[rt][dt][0] * inv)) |
+                            (uint32_t(M::from_float(st.o[rt][dt][1] * inv)) << 16);
+        const uint32_t hi = uint32_t(M::from_float(st.o[rt][dt][2] * inv)) |
+                            (uint32_t(M::from_float(st.o[rt][dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(orow + (dt * 16 + grp * 4) * 2) = uint2{lo, hi};
+      }
+      if (a.lse != nullptr && grp == 0)
+        a.lse[int64_t(qo_start + node_of[rt]) * a.num_qo_heads + head_of[rt]] = lse2 * kLn2;
+    } else {
+      const int64_t prow = int64_t(w.partial_row) + lr;
+      float* po = a.part_o + prow * D;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + grp * 4) = st.o[rt][dt] * inv;
+      if (grp == 0) a.part_lse[prow] = lse2;
+    }
+  }
+}
+
+// NW waves (4 or 8) per workgroup; wave w owns row tiles w and, with
+// RT_MAX = 2, w + NW.  Each wave keeps its rows' queries, output accumulators
+// and softmax state in architectural VGPRs.  Waves without rows only load.
+template <bool BF16, int NW, int RT_MAX>
+__global__ __launch_bounds__(NW * 64, 1) void tree_attn_d128_kernel(AttnArgs a) {
+  static_assert(NW == 4 || NW == 8, "four or eight waves");
+  static_assert(RT_MAX == 1 || RT_MAX == 2, "one or two row tiles per wave");
+  constexpr int D = 128;
+
+  __shared__ __attribute__((aligned(1024))) char lds[kStages128 * kTile128];
+
+  const atlas_attn_work_t w = a.work[blockIdx.x];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int req = w.req;
+  const int qo_start = a.qo_indptr[req];
+  const int qo_len = a.qo_indptr[req + 1] - qo_start;
+  const int kv_len = a.kv_len[req];
+  const int kv_end = min(w.kv_end, kv_len);
+
+  int vis_all = kv_end;
+  int col0 = 0;
+  if (a.mask_mode == ATLAS_MASK_TREE) {
+    col0 = a.mask_col_start[req];
+    vis_all = min(vis_all, col0);
+  } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
+    vis_all = min(vis_all, kv_len - qo_len + 1);
+  }
+
+  const int t_first = __builtin_amdgcn_readfirstlane(w.kv_start < kv_end ? w.kv_start : kv_end);
+  const int nt = __builtin_amdgcn_readfirstlane((kv_end - t_first + kTileKeys - 1) / kTileKeys);
+  // Leading tiles wholly below vis_all need no mask.
+  const int nt_plain = __builtin_amdgcn_readfirstlane(
+      min(nt, vis_all >= t_first + kTileKeys ? (vis_all - t_first) / kTileKeys : 0));
+  const int last_key = __builtin_amdgcn_readfirstlane(kv_end - 1);
+  const char* head_base = a.kv + int64_t(w.kv_head) * D * 2;
+  const const_i32_ptr pages = (const_i32_ptr)(a.kv_indices + a.kv_indptr[req]);
+  const uint32_t lds0 = lds_offset(lds);
+  wait_vmcnt<0>();
+
+  // Prologue: tiles 0, 1, 2 in flight, page ids of tile 3 loaded.
+  int pid[16 / NW];
+#pragma unroll
+  for (int j = 0; j < 16 / NW; ++j) pid[j] = 0;
+  if (nt > 0) tile_pages<NW>(pages, t_first, last_key, a.page_shift, wave, pid);
+#pragma unroll
+  for (int k = 0; k < 3; ++k) d128_issue<NW>(k, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+
+  const int row_tiles = (w.num_rows + 15) / 16;
+  const int mine = (wave < row_tiles ? 1 : 0) + (RT_MAX == 2 && wave + NW < row_tiles ? 1 : 0);
+  if (RT_MAX == 2 && mine == 2) {
+    d128_rows<BF16, NW, RT_MAX>(a, w, lds, head_base, pages, pid, t_first, nt, nt_plain, last_key, kv_end, col0,
+                                qo_start, qo_len, kv_len, wave, lane, lds0);
+  } else if (mine >= 1) {
+    d128_rows<BF16, NW, 1>(a, w, lds, head_base, pages, pid, t_first, nt, nt_plain, last_key, kv_end, col0, qo_start,
+                           qo_len, kv_len, wave, lane, lds0);
+  } else if (nt > 0) {
+    d128_ring_first<NW>(nt);
+    for (int t = 0; t < nt; ++t)
+      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+  }
+}
+
 struct MergeArgs {
   const atlas_attn_merge_t* merge;
   const int32_t* qo_indptr;
@@ -583,12 +1016,41 @@ void launch_shape(const AttnArgs& args, int num_work, hipStream_t stream) {
   hipLaunchKernelGGL((tree_attn_kernel<D, BF16, RT, NWC>), dim3(num_work), dim3(kThreads), 0, stream, args);
 }
 
+// head_dim 128 with power-of-two pages of >= 16 tokens: KV streamed by
+// direct-to-LDS loads through a 4-tile ring (one workgroup of 8 waves per
+// CU, two waves per SIMD).  Up to 8 row tiles: one tile per wave; up to 16:
+// two tiles per wave.
+template <bool BF16>
+bool launch_d128(const AttnArgs& args, int num_work, int row_tiles, hipStream_t stream) {
+  if (row_tiles <= 8)
+    hipLaunchKernelGGL((tree_attn_d128_kernel<BF16, 8, 1>), dim3(num_work), dim3(512), 0, stream, args);
+  else if (row_tiles <= 16)
+    hipLaunchKernelGGL((tree_attn_d128_kernel<BF16, 8, 2>), dim3(num_work), dim3(512), 0, stream, args);
+  else
+    return false;
+  return true;
+}
+
 template <int D, bool BF16>
 int launch_attn(const AttnArgs& args, int num_work, int row_tiles, const MergeArgs& margs, int num_merge,
                 int max_rows, hipStream_t stream) {
   int rc;
   int nwc, rt;
+  if constexpr (D == 128) {
+    if (args.page_shift >= 4) {
+      if (!launch_d128<BF16>(args, num_work, row_tiles, stream)) {
+        set_error("no kernel shape for %d row tiles", row_tiles);
+        return ATLAS_EUNSUPPORTED;
+      }
+      if ((rc = launch_status("tree_attn_d128_kernel"))) return rc;
+      goto merge;
+    }
+  }
   choose_shape(row_tiles, nwc, rt);
+  if (row_tiles > 3 * kWaves) {
+    set_error("no kernel shape for %d row tiles", row_tiles);
+    return ATLAS_EUNSUPPORTED;
+  }
   switch (rt * 10 + nwc) {
     case 11: launch_shape<D, BF16, 1, 1>(args, num_work, stream); break;
     case 12: launch_shape<D, BF16, 1, 2>(args, num_work, stream); break;
@@ -604,6 +1066,7 @@ int launch_attn(const AttnArgs& args, int num_work, int row_tiles, const MergeAr
       return ATLAS_EUNSUPPORTED;
   }
   if ((rc = launch_status("tree_attn_kernel"))) return rc;
+merge:
   if (num_merge > 0) {
     const dim3 grid(num_merge, max_rows);
     hipLaunchKernelGGL((tree_attn_merge_kernel<D, BF16>), grid, dim3(kMergeThreads), 0, stream, margs);
@@ -640,8 +1103,8 @@ extern "C" int atlas_tree_verify_attn(
   ATLAS_REQUIRE(mask_mode != ATLAS_MASK_TREE || (tree_mask_dev && mask_col_start_dev),
                 "tree mask mode needs tree_mask and mask_col_start");
   ATLAS_REQUIRE(num_work >= 0 && num_merge >= 0, "negative work counts");
-  ATLAS_REQUIRE(max_rows_per_item > 0 && max_rows_per_item <= 3 * kWaves * 16,
-                "max_rows_per_item %d out of range (1..%d)", max_rows_per_item, 3 * kWaves * 16);
+  ATLAS_REQUIRE(max_rows_per_item > 0 && max_rows_per_item <= kMaxRowsPerItem,
+                "max_rows_per_item %d out of range (1..%d)", max_rows_per_item, kMaxRowsPerItem);
   ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(q) & 15) == 0 && (reinterpret_cast<uintptr_t>(kv_cache) & 15) == 0 &&
                     (reinterpret_cast<uintptr_t>(out) & 7) == 0,
                 "q / kv_cache must be 16-byte aligned and out 8-byte aligned");

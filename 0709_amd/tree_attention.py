@@ -22,8 +22,9 @@ import torch
 from . import _lib
 
 TILE_KEYS = 64
-MAX_ROWS_PER_ITEM = 192  # 4 waves x 3 row tiles of 16
-DEFAULT_ROWS_PER_ITEM = 64  # 4 waves x 1 row tile: 3 workgroups per CU
+MAX_ROWS_PER_ITEM = 256  # 8 waves x 2 row tiles of 16 (head_dim 128, pages of >= 16 tokens)
+MAX_ROWS_PER_ITEM_OTHER = 192  # 4 waves x 3 row tiles of 16 (other shapes)
+DEFAULT_ROWS_PER_ITEM = 64  # 4 waves x 1 row tile
 MAX_TREE_WIDTH = 64
 MAX_SPLITS = 1024
 DEFAULT_CU_COUNT = 256
@@ -127,9 +128,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._kv_layout = kv_layout
         self._backend = backend
         self._plan: AttentionPlan | None = None
-        self.split_target_items = 2 * DEFAULT_CU_COUNT
+        # None: chosen per plan (see plan())
+        self.split_target_items: int | None = None
         self.min_tiles_per_split = 1
-        self.max_rows_per_item = DEFAULT_ROWS_PER_ITEM
+        self.max_rows_per_item: int | None = None
         self._meta_buf: torch.Tensor | None = None
         self._indices_buf: torch.Tensor | None = None
         self._bits_buf: torch.Tensor | None = None
@@ -237,7 +239,21 @@ class BatchPrefillWithPagedKVCacheWrapper:
 
         # ---- work decomposition ----
         group = hq // hkv
-        row_block = max(16, min(MAX_ROWS_PER_ITEM, int(self.max_rows_per_item)))
+        direct = d == 128 and ps >= 16 and (ps & (ps - 1)) == 0
+        if self.max_rows_per_item is None:
+            # head_dim-128 kernel: at most 128 rows (8 waves x 1 row tile) per
+            # item, the rows of a KV head split into equal blocks.
+            rows_max = max((qo_lens[b] * (hq // hkv) for b in range(batch)), default=1)
+            cap = 128 if direct else DEFAULT_ROWS_PER_ITEM
+            nblk = max(1, math.ceil(rows_max / cap))
+            row_block = 16 * math.ceil(math.ceil(rows_max / nblk) / 16)
+        else:
+            row_block = int(self.max_rows_per_item)
+        row_block = max(16, min(MAX_ROWS_PER_ITEM if direct else MAX_ROWS_PER_ITEM_OTHER, row_block))
+        split_target = self.split_target_items
+        if split_target is None:
+            # one 8-wave workgroup per CU for the head_dim-128 kernel
+            split_target = DEFAULT_CU_COUNT if direct else 2 * DEFAULT_CU_COUNT
         blocks = []  # (req, row_start, num_rows)
         for b in range(batch):
             rows = qo_lens[b] * group
@@ -249,7 +265,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             if rows == 0:
                 blocks.append((b, 0, 0))
         unit_tiles = sum(hkv * math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks)
-        tiles_per_split = max(self.min_tiles_per_split, math.ceil(unit_tiles / max(1, self.split_target_items)))
+        tiles_per_split = max(self.min_tiles_per_split, math.ceil(unit_tiles / max(1, split_target)))
         # the merge kernel combines at most MAX_SPLITS states per row
         max_tiles = max((math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks), default=0)
         tiles_per_split = max(tiles_per_split, math.ceil(max_tiles / MAX_SPLITS))

@@ -51,7 +51,7 @@ def _ev():
 
 
 class HeadlineStep:
-    def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None):
+    def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None, max_rows=None):
         wl = _pkg("workloads")
         ffv = _pkg("flashinfer_full_verify")
         self.ffv = ffv
@@ -82,6 +82,8 @@ class HeadlineStep:
         self.wrapper = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
         if split_target is not None:
             self.wrapper.split_target_items = split_target
+        if max_rows is not None:
+            self.wrapper.max_rows_per_item = max_rows
         self.kv_indices_host = self.kv.kv_indices.cpu().tolist()
         # physical slots of the tree node positions (page table lookup on host, once)
         pos = torch.arange(prefix_len, self.kv_len)
@@ -341,6 +343,7 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-legs", action="store_true")
     ap.add_argument("--split-target", type=int, default=None)
+    ap.add_argument("--max-rows", type=int, default=None)
     ap.add_argument("--commit-pool-gb", type=float, default=200.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -348,7 +351,7 @@ def main():
                                    "and has no multi-GPU leg", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
-    step = HeadlineStep(dev, split_target=args.split_target)
+    step = HeadlineStep(dev, split_target=args.split_target, max_rows=args.max_rows)
     step.capture()
     for _ in range(args.warmup):
         step.step()
@@ -390,7 +393,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "tree_attn_kernel + tree_attn_merge_kernel (one verify attention launch pair)",
+            "kernel": "tree_attn_d128_kernel + tree_attn_merge_kernel (one verify attention launch pair)",
             "algorithmic_bytes_per_launch": bytes_layer,
         },
         "components": {
