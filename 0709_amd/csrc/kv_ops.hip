@@ -1,9 +1,10 @@
 // All-layer KV movement kernels: slot-to-slot move (tail-page copy-on-write),
 // dense append (write_suffix_kv / set_kv_buffer) and page-table commit
 // compaction (target_kv_commit).  Each is an HBM-bound copy of 16-byte
-// vectors; one launch covers every layer (grid.y = layer * 2 + {K, V}) and
-// consecutive lanes move consecutive vectors of one token row, so a wave moves
-// 1 KiB contiguous per row segment.
+// vectors and one launch covers every layer.  Move and append: grid.y =
+// layer * 2 + {K, V}, consecutive lanes move consecutive vectors of one token
+// row.  Commit: one wave per (item, layer), its slots resolved once per wave
+// through the page table.
 #include "common.hpp"
 
 namespace atlas {
@@ -101,66 +102,64 @@ __device__ __forceinline__ int64_t position_slot(int64_t pos, int req, const int
   return int64_t(kv_indices[base + lp]) * g.page_size + off;
 }
 
+// Commit compaction modes.  kCopy: in place (no destination aliases another
+// item's source).  kGather: rows -> workspace [layer][kv][item][row].
+// kScatter: workspace -> destination rows.
 enum CommitMode { kCopy = 0, kGather = 1, kScatter = 2 };
 
-// Commit compaction.  kCopy: in place (no destination aliases another item's
-// source).  kGather: rows -> workspace [layer][kv][item][row].  kScatter:
-// workspace -> destination rows.
+// Commit compaction, one wave per (item, layer): the item's positions, page
+// table entries and slots are wave-uniform (scalar loads), and the wave moves
+// the K row and the V row with every lane holding row_vecs/64 vectors of each
+// in flight.  Block = 4 waves = 4 consecutive layers of one item.
+constexpr int kRowWaves = 4;
+
 template <int MODE, bool INLINE>
-__global__ __launch_bounds__(kThreads) void kv_commit_kernel(
-    LayerTable lt, SlotGeom g, const int32_t* __restrict__ kv_indptr,
+__global__ __launch_bounds__(kThreads) void kv_commit_rows_kernel(
+    LayerTable lt, SlotGeom g, int nl, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ item_req,
-    const int64_t* __restrict__ src_pos, const int64_t* __restrict__ dst_pos, InlineItems items,
-    int64_t n, char* __restrict__ ws, int layer0) {
-  const int layer = blockIdx.y >> 1;
-  const bool is_v = blockIdx.y & 1;
-  char* base = const_cast<char*>(is_v ? lt.v[layer] : lt.k[layer]);
-  const int64_t total = n * g.row_vecs;
-  const int64_t row_bytes = int64_t(g.row_vecs) * 16;
-  char* wsl = ws ? ws + ((int64_t(layer0 + layer) * 2 + (is_v ? 1 : 0)) * n) * row_bytes : nullptr;
-  const int64_t first = int64_t(blockIdx.x) * kThreads * kUnroll + threadIdx.x;
-  uint4 buf[kUnroll];
-  int64_t dofs[kUnroll];
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    const int64_t idx = first + int64_t(u) * kThreads;
-    dofs[u] = -1;
-    if (idx < total) {
-      int64_t item;
-      int vec;
-      split_row(idx, g, item, vec);
-      int req;
-      int64_t sp, dp;
-      if (INLINE) {
-        req = items.req[item];
-        sp = items.src[item];
-        dp = items.dst[item];
-      } else {
-        req = item_req ? item_req[item] : 0;
-        sp = src_pos[item];
-        dp = dst_pos[item];
-      }
-      const int64_t voff = int64_t(vec) * 16;
-      if (MODE == kCopy || MODE == kGather) {
-        const int64_t so = slot_offset(position_slot(sp, req, kv_indptr, kv_indices, g), g) + voff;
-        buf[u] = *reinterpret_cast<const uint4*>(base + so);
-        dofs[u] = (MODE == kCopy)
-                      ? slot_offset(position_slot(dp, req, kv_indptr, kv_indices, g), g) + voff
-                      : item * row_bytes + voff;
-      } else {
-        buf[u] = *reinterpret_cast<const uint4*>(wsl + item * row_bytes + voff);
-        dofs[u] = slot_offset(position_slot(dp, req, kv_indptr, kv_indices, g), g) + voff;
-      }
-    }
+    const int64_t* __restrict__ src_pos, const int64_t* __restrict__ dst_pos, InlineItems items, int64_t n,
+    char* __restrict__ ws, int layer0) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int layer = blockIdx.y * kRowWaves + wave;
+  if (layer >= nl) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t item = blockIdx.x;
+  int req;
+  int64_t sp, dp;
+  if (INLINE) {
+    req = items.req[item];
+    sp = items.src[item];
+    dp = items.dst[item];
+  } else {
+    req = item_req ? item_req[item] : 0;
+    sp = src_pos[item];
+    dp = dst_pos[item];
   }
-#pragma unroll
-  for (int u = 0; u < kUnroll; ++u) {
-    if (dofs[u] < 0) continue;
-    if (MODE == kGather) {
-      *reinterpret_cast<uint4*>(wsl + dofs[u]) = buf[u];
-    } else {
-      *reinterpret_cast<uint4*>(base + dofs[u]) = buf[u];
-    }
+  req = __builtin_amdgcn_readfirstlane(req);
+  const int64_t row_bytes = int64_t(g.row_vecs) * 16;
+  int64_t src_off = 0, dst_off = 0;
+  if (MODE != kScatter) src_off = slot_offset(position_slot(sp, req, kv_indptr, kv_indices, g), g);
+  if (MODE != kGather) dst_off = slot_offset(position_slot(dp, req, kv_indptr, kv_indices, g), g);
+  const char* src_k;
+  const char* src_v;
+  char* dst_k;
+  char* dst_v;
+  {
+    char* kb = const_cast<char*>(lt.k[layer]);
+    char* vb = const_cast<char*>(lt.v[layer]);
+    char* wk = ws ? ws + ((int64_t(layer0 + layer) * 2 + 0) * n + item) * row_bytes : nullptr;
+    char* wv = ws ? ws + ((int64_t(layer0 + layer) * 2 + 1) * n + item) * row_bytes : nullptr;
+    src_k = (MODE == kScatter) ? wk : kb + src_off;
+    src_v = (MODE == kScatter) ? wv : vb + src_off;
+    dst_k = (MODE == kGather) ? wk : kb + dst_off;
+    dst_v = (MODE == kGather) ? wv : vb + dst_off;
+  }
+#pragma unroll 2
+  for (int v = lane; v < g.row_vecs; v += 64) {
+    const uint4 a = *reinterpret_cast<const uint4*>(src_k + int64_t(v) * 16);
+    const uint4 b = *reinterpret_cast<const uint4*>(src_v + int64_t(v) * 16);
+    *reinterpret_cast<uint4*>(dst_k + int64_t(v) * 16) = a;
+    *reinterpret_cast<uint4*>(dst_v + int64_t(v) * 16) = b;
   }
 }
 
@@ -285,16 +284,16 @@ int commit_impl(const void* const* k_layers, const void* const* v_layers, int nu
       const int nl = std::min(ATLAS_MAX_LAYERS_PER_LAUNCH, num_layers - l0);
       LayerTable lt;
       fill_table(lt, k_layers, v_layers, l0, nl);
-      const dim3 grid = copy_grid(n, g, nl);
+      const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>((nl + kRowWaves - 1) / kRowWaves));
       if (!staging) {
-        hipLaunchKernelGGL((kv_commit_kernel<kCopy, INLINE>), grid, dim3(kThreads), 0, stream, lt, g,
+        hipLaunchKernelGGL((kv_commit_rows_kernel<kCopy, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
                            kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
       } else if (pass == 0) {
-        hipLaunchKernelGGL((kv_commit_kernel<kGather, INLINE>), grid, dim3(kThreads), 0, stream, lt,
-                           g, kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
+        hipLaunchKernelGGL((kv_commit_rows_kernel<kGather, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
+                           kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
       } else {
-        hipLaunchKernelGGL((kv_commit_kernel<kScatter, INLINE>), grid, dim3(kThreads), 0, stream, lt,
-                           g, kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
+        hipLaunchKernelGGL((kv_commit_rows_kernel<kScatter, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
+                           kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
       }
       if ((rc = launch_status("kv_commit_kernel"))) return rc;
     }
@@ -312,7 +311,7 @@ extern "C" int atlas_kv_commit_paged(const void* const* k_layers, const void* co
                                      const int32_t* item_req_dev, const int64_t* src_pos_dev,
                                      const int64_t* dst_pos_dev, int64_t n, int needs_staging,
                                      void* workspace_dev, size_t workspace_bytes, void* stream) {
-  ATLAS_REQUIRE(n >= 0, "n must be non-negative");
+  ATLAS_REQUIRE(n >= 0 && n < (int64_t(1) << 31), "n must be in [0, 2^31)");
   if (n == 0) return ATLAS_OK;
   ATLAS_REQUIRE(src_pos_dev && dst_pos_dev, "position arrays must not be NULL");
   int rc = check_layers(k_layers, v_layers, num_layers);

@@ -14,6 +14,9 @@ __global__ void fill_u32_kernel(uint32_t* p, int64_t n, uint32_t value) {
     p[i] = value;
 }
 
+// Slot paths list the slots of a page consecutively, so only the first slot
+// of each run of same-page slots sets the bit (one atomic per page run, not
+// per slot).
 __global__ void mark_pages_kernel(uint32_t* bitmap, int64_t num_pages, const int64_t* slots, int64_t n,
                                   int64_t page_size) {
   for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
@@ -22,6 +25,10 @@ __global__ void mark_pages_kernel(uint32_t* bitmap, int64_t num_pages, const int
     if (s < 0) continue;
     const int64_t page = s / page_size;
     if (page >= num_pages) continue;
+    if (i > 0) {
+      const int64_t prev = slots[i - 1];
+      if (prev >= 0 && prev / page_size == page) continue;
+    }
     atomicOr(&bitmap[page >> 5], 1u << (page & 31));
   }
 }

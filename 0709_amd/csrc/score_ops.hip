@@ -19,61 +19,98 @@ __device__ __forceinline__ float load_logit(const char* row, int64_t i) {
   }
 }
 
-// Block r: lse of logits row r (natural log, fp32 accumulation), then every
-// gather that reads row r.
+__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
+  for (int off = 32; off > 0; off >>= 1) {
+    const float o = __shfl_xor(v, off);
+    v = is_max ? fmaxf(v, o) : v + o;
+  }
+  const int wave = threadIdx.x >> 6;
+  __syncthreads();  // red[] reuse across calls
+  if ((threadIdx.x & 63) == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < kThreads / 64; ++w) t = is_max ? fmaxf(t, red[w]) : t + red[w];
+  return t;
+}
+
+// 16 bytes of logits -> up to 8 floats.
 template <int DT>
+struct Vec {
+  static constexpr int kElems = DT == ATLAS_DTYPE_F32 ? 4 : 8;
+  float x[kElems];
+  __device__ __forceinline__ void load(const char* p) {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    if constexpr (DT == ATLAS_DTYPE_F32) {
+      x[0] = __uint_as_float(u.x);
+      x[1] = __uint_as_float(u.y);
+      x[2] = __uint_as_float(u.z);
+      x[3] = __uint_as_float(u.w);
+    } else {
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        if constexpr (DT == ATLAS_DTYPE_F16) {
+          x[2 * k] = static_cast<float>(__builtin_bit_cast(_Float16, uint16_t(w[k] & 0xffff)));
+          x[2 * k + 1] = static_cast<float>(__builtin_bit_cast(_Float16, uint16_t(w[k] >> 16)));
+        } else {
+          x[2 * k] = __uint_as_float(w[k] << 16);
+          x[2 * k + 1] = __uint_as_float(w[k] & 0xffff0000u);
+        }
+      }
+    }
+  }
+};
+
+// Block r: log-sum-exp of logits row r (natural log, fp32) in two passes over
+// the row -- the maximum, then the sum of exp2((x - max) * log2 e) (the second
+// pass reads the row back from L2) -- with 16-byte loads when the row is
+// 16-byte aligned; then every gather that reads row r.
+template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(const char* logits, int64_t row_stride_bytes,
                                                                    int64_t vocab, const int32_t* rows,
                                                                    const int64_t* tokens, int64_t n,
                                                                    float* row_lse, float* out) {
-  __shared__ float red_m[kThreads / 64];
-  __shared__ float red_s[kThreads / 64];
+  __shared__ float red[kThreads / 64];
+  __shared__ float lse_sh;
+  constexpr float kLog2e = 1.4426950408889634f;
+  constexpr int EPV = Vec<DT>::kElems;
   const int r = blockIdx.x;
   const char* row = logits + int64_t(r) * row_stride_bytes;
-  float m = -INFINITY, s = 0.f;
-  for (int64_t i = threadIdx.x; i < vocab; i += kThreads) {
-    const float x = load_logit<DT>(row, i);
-    if (x > m) {
-      s = s * expf(m - x) + 1.f;
-      m = x;
-    } else {
-      s += expf(x - m);
-    }
+  const int64_t nvec = VEC ? vocab / EPV : 0;
+
+  float m = -INFINITY;
+  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
+    Vec<DT> x;
+    x.load(row + v * 16);
+#pragma unroll
+    for (int k = 0; k < EPV; ++k) m = fmaxf(m, x.x[k]);
   }
-  // Wave reduction of (m, s) pairs.
-  for (int off = 32; off > 0; off >>= 1) {
-    const float om = __shfl_xor(m, off);
-    const float os = __shfl_xor(s, off);
-    const float nm = fmaxf(m, om);
-    const float a = (m == -INFINITY) ? 0.f : s * expf(m - nm);
-    const float b = (om == -INFINITY) ? 0.f : os * expf(om - nm);
-    m = nm;
-    s = a + b;
+  for (int64_t i = nvec * EPV + threadIdx.x; i < vocab; i += kThreads) m = fmaxf(m, load_logit<DT>(row, i));
+  m = block_reduce(m, true, red);
+
+  const float mb = m == -INFINITY ? 0.f : m * kLog2e;
+  float s = 0.f;
+  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
+    Vec<DT> x;
+    x.load(row + v * 16);
+#pragma unroll
+    for (int k = 0; k < EPV; ++k) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x.x[k], kLog2e, -mb));
   }
-  const int wave = threadIdx.x >> 6;
-  if ((threadIdx.x & 63) == 0) {
-    red_m[wave] = m;
-    red_s[wave] = s;
-  }
-  __syncthreads();
-  __shared__ float lse_sh;
+  for (int64_t i = nvec * EPV + threadIdx.x; i < vocab; i += kThreads)
+    s += __builtin_amdgcn_exp2f(__builtin_fmaf(load_logit<DT>(row, i), kLog2e, -mb));
+  s = block_reduce(s, false, red);
+
   if (threadIdx.x == 0) {
-    float mm = -INFINITY, ss = 0.f;
-    for (int w = 0; w < kThreads / 64; ++w) {
-      const float nm = fmaxf(mm, red_m[w]);
-      const float a = (mm == -INFINITY) ? 0.f : ss * expf(mm - nm);
-      const float b = (red_m[w] == -INFINITY) ? 0.f : red_s[w] * expf(red_m[w] - nm);
-      mm = nm;
-      ss = a + b;
-    }
-    lse_sh = mm + logf(ss);
+    lse_sh = m + logf(s);
     if (row_lse) row_lse[r] = lse_sh;
   }
   __syncthreads();
+  const float lse = lse_sh;
   for (int64_t i = threadIdx.x; i < n; i += kThreads) {
     if (rows[i] != r) continue;
     const int64_t t = tokens[i];
-    out[i] = (t >= 0 && t < vocab) ? load_logit<DT>(row, t) - lse_sh : NAN;
+    out[i] = (t >= 0 && t < vocab) ? load_logit<DT>(row, t) - lse : NAN;
   }
 }
 
@@ -95,14 +132,22 @@ extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride,
   hipStream_t s = static_cast<hipStream_t>(stream);
   const char* lg = static_cast<const char*>(logits_dev);
   const dim3 grid(static_cast<unsigned>(num_rows));
+  const bool vec = (reinterpret_cast<uintptr_t>(logits_dev) % 16) == 0 && stride_bytes % 16 == 0;
+#define ATLAS_GATHER_LAUNCH(DT)                                                                              \
+  do {                                                                                                       \
+    if (vec)                                                                                                 \
+      hipLaunchKernelGGL((gather_logprobs_kernel<DT, true>), grid, dim3(kThreads), 0, s, lg, stride_bytes,   \
+                         vocab, row_dev, token_dev, n, row_lse_dev, out_dev);                                \
+    else                                                                                                     \
+      hipLaunchKernelGGL((gather_logprobs_kernel<DT, false>), grid, dim3(kThreads), 0, s, lg, stride_bytes,  \
+                         vocab, row_dev, token_dev, n, row_lse_dev, out_dev);                                \
+  } while (0)
   if (dtype == ATLAS_DTYPE_F32)
-    hipLaunchKernelGGL(gather_logprobs_kernel<ATLAS_DTYPE_F32>, grid, dim3(kThreads), 0, s, lg, stride_bytes, vocab,
-                       row_dev, token_dev, n, row_lse_dev, out_dev);
+    ATLAS_GATHER_LAUNCH(ATLAS_DTYPE_F32);
   else if (dtype == ATLAS_DTYPE_F16)
-    hipLaunchKernelGGL(gather_logprobs_kernel<ATLAS_DTYPE_F16>, grid, dim3(kThreads), 0, s, lg, stride_bytes, vocab,
-                       row_dev, token_dev, n, row_lse_dev, out_dev);
+    ATLAS_GATHER_LAUNCH(ATLAS_DTYPE_F16);
   else
-    hipLaunchKernelGGL(gather_logprobs_kernel<ATLAS_DTYPE_BF16>, grid, dim3(kThreads), 0, s, lg, stride_bytes, vocab,
-                       row_dev, token_dev, n, row_lse_dev, out_dev);
+    ATLAS_GATHER_LAUNCH(ATLAS_DTYPE_BF16);
+#undef ATLAS_GATHER_LAUNCH
   return launch_status("gather_logprobs_kernel");
 }

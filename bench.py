@@ -42,6 +42,18 @@ HBM_PEAK_GBPS = 8000.0
 METRIC = "tree-verify attn µs/layer + KV commit/COW GB/s, 8B geom, 16k prefix, 1 GPU"
 
 
+def _measured_traffic(path: Path) -> int | None:
+    """HBM bytes per attention launch pair from the committed counter summary
+    (``hbm_bytes_per_launch: N`` in its text block), or None."""
+    try:
+        for line in path.read_text().splitlines():
+            if line.startswith("hbm_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        return None
+    return None
+
+
 def _pkg(name):
     return importlib.import_module(f"0709_amd.{name}")
 
@@ -205,17 +217,30 @@ def _mean_ms(pairs):
     return statistics.fmean(a.elapsed_time(b) for a, b in pairs) if pairs else float("nan")
 
 
-def commit_leg(dev, *, pool_gb=200.0, requests=32, iters=50):
-    """Batched 32-request commit, 8B geometry, bf16, pages scattered over a
-    pool of about ``pool_gb`` GB (32 layers x pages x 64 KiB)."""
+def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
+    """Batched Target verify: 32 requests, Llama-3.1-8B KV geometry, bf16,
+    page 16, prefixes uniform in [1024, 16384], pages scattered over a pool of
+    about ``pool_gb`` GB (32 layers x pages x 64 KiB).  Each request has a
+    k=3 d=4 tree (12 queries, ancestor mask).  Times the 32-layer masked
+    attention, then the per-request 4-token commit (dedup node ids: a one-pass
+    in-place copy) and the prune of the tree pages."""
     kv_ops = _pkg("kv_ops")
     wl = _pkg("workloads")
+    ffv = _pkg("flashinfer_full_verify")
+    lib = _pkg("_lib")
+
     geom = wl.LLAMA_8B
     ps = 16
     page_bytes = 2 * ps * geom.kv_heads * geom.head_dim * 2
     gen = torch.Generator().manual_seed(4)
     prefixes = [int(x) for x in torch.randint(1024, 16385, (requests,), generator=gen)]
-    need_pages = sum(math.ceil((p + 12) / ps) for p in prefixes)
+    routes = [wl.tree_routes(100 + b) for b in range(requests)]
+    specs = [ffv.build_deduplicated_tree_spec_from_paths(paths=r, prefix_len=p, page_size=ps, device=dev)
+             for r, p in zip(routes, prefixes)]
+    nodes = [sp.node_count for sp, _ in specs]
+    kv_lens = [p + n for p, n in zip(prefixes, nodes)]
+    req_pages = [math.ceil(k / ps) for k in kv_lens]
+    need_pages = sum(req_pages)
     pool = None
     while pool is None:
         pool_pages = max(need_pages + 64, int(pool_gb * 1e9 / (geom.layers * page_bytes)))
@@ -226,36 +251,145 @@ def commit_leg(dev, *, pool_gb=200.0, requests=32, iters=50):
             pool_gb /= 2
             if pool_gb < 1:
                 raise
-    perm = torch.randperm(pool_pages, generator=gen)[:need_pages].to(torch.int32)
-    indptr, req, src, dst = [0], [], [], []
-    for b, p in enumerate(prefixes):
-        indptr.append(indptr[-1] + math.ceil((p + 12) / ps))
-        nodes = sorted(int(x) for x in torch.randperm(12, generator=gen)[:4])
-        nodes = [0, 1, 2, 3] if b % 3 == 0 else nodes
-        for i, nd in enumerate(nodes):
-            req.append(b)
-            src.append(p + nd)
-            dst.append(p + i)
+    perm = torch.randperm(pool_pages, generator=gen)[:need_pages]
+    used = perm.to(dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    for l in range(geom.layers):
+        pool[l, used] = (torch.randn((need_pages, 2, ps, geom.kv_heads, geom.head_dim), generator=g, device=dev)
+                         * 0.1).to(torch.bfloat16)
     layers = list(pool.unbind(0))
-    args = dict(kv_indptr=torch.tensor(indptr, dtype=torch.int32, device=dev), kv_indices=perm.to(dev),
-                item_req=torch.tensor(req, dtype=torch.int32, device=dev))
-    src_t = torch.tensor(src, device=dev)
-    dst_t = torch.tensor(dst, device=dev)
-    staging = kv_ops.commit_positions_need_staging(src, dst, req)
-    for _ in range(5):
-        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+    kv_indptr_h = [0]
+    for n in req_pages:
+        kv_indptr_h.append(kv_indptr_h[-1] + n)
+    qo_h = [0]
+    for n in nodes:
+        qo_h.append(qo_h[-1] + n)
+    flat_mask = torch.cat([sp.bool_mask for sp, _ in specs])
+    kv_indptr = torch.tensor(kv_indptr_h, dtype=torch.int32, device=dev)
+    kv_indices = perm.to(torch.int32).to(dev)
+    last = torch.tensor([k - (n - 1) * ps for k, n in zip(kv_lens, req_pages)], dtype=torch.int32, device=dev)
+    qo = torch.tensor(qo_h, dtype=torch.int32, device=dev)
+    nnz = qo_h[-1]
+    q = [(torch.randn((nnz, geom.q_heads, geom.head_dim), generator=g, device=dev) * 0.1).to(torch.bfloat16)
+         for _ in range(layers_timed)]
+    outs = [torch.empty_like(x) for x in q]
+    ws = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(qo, kv_indptr, kv_indices, last, geom.q_heads, geom.kv_heads, geom.head_dim, ps, custom_mask=flat_mask,
+           causal=False, q_data_type=torch.bfloat16)
+
+    def fwd():
+        for l in range(layers_timed):
+            w.run(q[l], layers[l], out=outs[l])
+
+    fwd()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fwd()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    graph.replay()
     torch.cuda.synchronize()
     a, b = _ev(), _ev()
     a.record()
     for _ in range(iters):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    attn_us = a.elapsed_time(b) * 1000.0 / (iters * layers_timed)
+    attn_bytes = sum(wl.verify_attention_bytes(geom, kv_len=k, nodes=n, page_size=ps) for k, n in zip(kv_lens, nodes))
+
+    # commit: the selected route of every request (dedup node ids)
+    sel = [int(torch.randint(0, len(r), (1,), generator=gen)) for r in routes]
+    item_req, src, dst = [], [], []
+    for bi, ((_, rnodes), p) in enumerate(zip(specs, prefixes)):
+        for i, nd in enumerate(rnodes[sel[bi]]):
+            item_req.append(bi)
+            src.append(p + nd)
+            dst.append(p + i)
+    staging = kv_ops.commit_positions_need_staging(src, dst, item_req)
+    args = dict(kv_indptr=kv_indptr, kv_indices=kv_indices,
+                item_req=torch.tensor(item_req, dtype=torch.int32, device=dev))
+    src_t = torch.tensor(src, device=dev)
+    dst_t = torch.tensor(dst, device=dev)
+    for _ in range(5):
+        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(50):
         kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
     b.record()
     torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000.0 / iters
+    commit_call_us = a.elapsed_time(b) * 1000.0 / 50
+    # device time of the commit launch: 20 commits replayed from a HIP graph
+    # (no per-call host work between them)
+    with torch.cuda.stream(side):
+        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+    torch.cuda.current_stream().wait_stream(side)
+    cgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(cgraph):
+        for _ in range(20):
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+    cgraph.replay()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(5):
+        cgraph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    commit_us = a.elapsed_time(b) * 1000.0 / 100
     moved = len(src) * geom.layers * geom.token_bytes()
-    out = {"us": us, "moved_bytes": moved, "GBps": 2 * moved / (us * 1e-6) / 1e9,
-           "pool_GB": round(pool.numel() * 2 / 1e9, 1), "requests": requests, "tokens": len(src)}
-    del pool, layers
+
+    # prune: pages of every request owned; live = prefix + committed tokens
+    words = (pool_pages + 31) // 32
+    owned = torch.zeros(words, dtype=torch.int32, device=dev)
+    live_bm = torch.zeros_like(owned)
+    free_pages = torch.zeros(pool_pages, dtype=torch.int64, device=dev)
+    free_count = torch.zeros(1, dtype=torch.int64, device=dev)
+    idx_all = perm.to(torch.int64)
+    live_sampled, all_page_slots = [], []
+    for bi, (p, npg) in enumerate(zip(prefixes, req_pages)):
+        pg = idx_all[kv_indptr_h[bi]: kv_indptr_h[bi + 1]]
+        all_page_slots.append(pg * ps)
+        keep = p + len(routes[bi][sel[bi]])
+        pos = torch.arange(0, keep, ps).tolist() + [keep - 1]
+        live_sampled.append(pg[torch.tensor(pos) // ps] * ps + torch.tensor(pos) % ps)
+    all_slots = torch.cat(all_page_slots).to(dev)
+    live_slots = torch.cat(live_sampled).to(dev)
+    stream = lib.stream_of(dev)
+    L = lib.load()
+
+    def prune():
+        rc = L.atlas_mark_pages(lib.ptr(owned), pool_pages, lib.ptr(all_slots), int(all_slots.numel()), ps, stream)
+        lib.check(rc, "atlas_mark_pages")
+        rc = L.atlas_prune_pages(lib.ptr(owned), lib.ptr(live_bm), pool_pages, lib.ptr(live_slots),
+                                 int(live_slots.numel()), ps, lib.ptr(free_pages), lib.ptr(free_count), stream)
+        lib.check(rc, "atlas_prune_pages")
+
+    prune()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(20):
+        prune()
+    b.record()
+    torch.cuda.synchronize()
+    prune_us = a.elapsed_time(b) * 1000.0 / 20
+    freed = int(free_count.item())
+    out = {
+        "requests": requests, "nodes_per_request": nodes[0], "mean_prefix": round(sum(prefixes) / requests, 1),
+        "pool_GB": round(pool.numel() * 2 / 1e9, 1), "work_items": w.current_plan.num_work,
+        "attention_us_per_layer": round(attn_us, 3),
+        "attention_GBps": round(attn_bytes / (attn_us * 1e-6) / 1e9, 1),
+        "attention_frac": round(attn_bytes / (attn_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+        "attention_bytes_per_layer": attn_bytes,
+        "commit_us": round(commit_us, 3), "commit_call_us": round(commit_call_us, 3), "commit_moved_bytes": moved,
+        "commit_GBps": round(2 * moved / (commit_us * 1e-6) / 1e9, 1), "commit_staging": bool(staging),
+        "mark_and_prune_us": round(prune_us, 3), "pruned_pages": freed,
+    }
+    del pool, layers, q, outs, ws, graph, cgraph
     torch.cuda.empty_cache()
     return out
 
@@ -301,6 +435,61 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50):
     return {"us": us, "moved_bytes": moved, "GBps": 2 * moved / (us * 1e-6) / 1e9, "slots": len(src)}
 
 
+def drafter_leg(dev, *, requests=8, repeats=3):
+    """Drafter route-pool fork stress (Llama-3.2-1B KV geometry, bf16, page
+    64): 8 requests, each forking to 9 routes at random fill levels of its
+    partial tail page, 8 decode steps, commit + promote of 3 routes, prune,
+    one 4-token fallback EXTEND and a decode step after it -- the route-pool
+    bridge driving the native pools (device page ownership, batched
+    copy-on-write, device slot allocation and page metadata).  The model is
+    replaced by one all-layer K/V append per step.  Wall time per phase, GPU
+    synchronised at each phase end."""
+    dw = _pkg("drafter_workload")
+    npool = _pkg("flashinfer_paged.native_pool")
+    geom = _pkg("workloads").LLAMA_1B
+    ps = 64
+    runs = []
+    for rep in range(repeats):
+        req_pool, kv, alloc = npool.create_native_pools(
+            num_pages=640, page_size=ps, dtype=torch.bfloat16, head_num=geom.kv_heads, head_dim=geom.head_dim,
+            layer_num=geom.layers, max_running_requests=128, max_context_len=4096, device=dev)
+        rows = (torch.randn((2048, geom.kv_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
+
+        def writer(slots, vids, kv=kv, rows=rows):
+            n = int(slots.numel())
+            kv.set_kv_buffer_all_layers(slots, [rows[:n]] * geom.layers, [rows[:n]] * geom.layers)
+
+        work = dw.DrafterForkWorkload(plans=dw.config5_plans(requests, ps, rep), req_pool=req_pool, allocator=alloc,
+                                      page_size=ps, device=dev, writer=writer)
+        marks = []
+
+        def on_phase(name, marks=marks):
+            torch.cuda.synchronize()
+            marks.append((name, time.perf_counter()))
+
+        torch.cuda.synchronize()
+        marks.append(("start", time.perf_counter()))
+        work.run(on_phase)
+        spans = {}
+        for (_, t0), (name, t1) in zip(marks, marks[1:]):
+            spans[name] = (t1 - t0) * 1e6
+        cow_pages = sum(r.bridge.cow_pages_copied for r in work.requests)
+        cow_tokens = sum(r.bridge.cow_tokens_copied for r in work.requests)
+        runs.append((spans, cow_pages, cow_tokens))
+        del work, req_pool, kv, alloc
+        torch.cuda.empty_cache()
+    decode = [statistics.fmean(sp[f"decode{t}"] for t in range(8)) for sp, _, _ in runs]
+    return {
+        "requests": requests, "routes_per_request": 9, "page_size": ps,
+        "decode_step_us": round(statistics.median(decode), 1),
+        "commit_promote_prune_us": round(statistics.median(sp["commit"] for sp, _, _ in runs), 1),
+        "fallback_extend_us": round(statistics.median(sp["extend"] for sp, _, _ in runs), 1),
+        "prefill_us": round(statistics.median(sp["prefill"] for sp, _, _ in runs), 1),
+        "cow_pages_copied": runs[-1][1], "cow_tokens_copied": runs[-1][2],
+        "note": "wall time of the host-driven bridge per phase (all 8 requests), model replaced by a K/V append",
+    }
+
+
 def cpu_baseline(step: HeadlineStep, budget_s: float):
     """Oracle float32 attention over a bounded number of the headline's layers."""
     import numpy as np
@@ -344,6 +533,8 @@ def main():
     ap.add_argument("--no-legs", action="store_true")
     ap.add_argument("--split-target", type=int, default=None)
     ap.add_argument("--max-rows", type=int, default=None)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="also run device-to-device copies of MIB MiB (calibrates HBM byte counters)")
     ap.add_argument("--commit-pool-gb", type=float, default=200.0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -352,6 +543,13 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     step = HeadlineStep(dev, split_target=args.split_target, max_rows=args.max_rows)
+    if args.copy_calibration:
+        src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     step.capture()
     for _ in range(args.warmup):
         step.step()
@@ -392,7 +590,10 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": _measured_traffic(ROOT / "profiles" / "tree_attn_forest16k_traffic.md"),
+            "traffic_source": "profiles/tree_attn_forest16k_traffic.md (FETCH_SIZE x 2.0 + WRITE_SIZE x 1.0, "
+                              "copy-calibrated)",
             "kernel": "tree_attn_d128_kernel + tree_attn_merge_kernel (one verify attention launch pair)",
             "algorithmic_bytes_per_launch": bytes_layer,
         },
@@ -405,9 +606,10 @@ def main():
         },
     }
     if not args.no_legs:
-        result["components"]["commit_batched_32req"] = commit_leg(dev, pool_gb=args.commit_pool_gb)
+        result["components"]["batched_32req"] = batched_leg(dev, pool_gb=args.commit_pool_gb)
         result["components"]["cow_8req_9routes"] = cow_leg(dev)
-        result["kv_commit_GBps"] = round(result["components"]["commit_batched_32req"]["GBps"], 1)
+        result["components"]["drafter_fork_8req"] = drafter_leg(dev)
+        result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
         result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_baseline_seconds)

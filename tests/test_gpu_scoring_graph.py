@@ -28,6 +28,23 @@ def test_gather_logprobs_matches_oracle(dev, dtype):
     assert np.abs(out - exp).max() <= 2e-4  # fp32 accumulation over 128256 logits
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("shape,offset", [((7, 1003), 0), ((5, 1001), 1), ((3, 9), 1)])
+def test_gather_logprobs_unaligned_and_ragged_rows(dev, dtype, shape, offset):
+    """Row starts that are not 16-byte aligned (scalar path) and vocabularies
+    that are not a multiple of the vector width (vector path tail)."""
+    tr = pkg("target_runtime")
+    gen = torch.Generator().manual_seed(shape[1] + offset)
+    full = (torch.randn((shape[0], shape[1] + offset), generator=gen) * 4).to(dtype)
+    logits = full[:, offset:]
+    rows = [r % shape[0] for r in range(11)]
+    toks = [int(x) for x in torch.randint(0, shape[1], (11,), generator=gen)]
+    out = tr.gather_token_logprobs(logits.to(dev) if offset == 0 else full.to(dev)[:, offset:], rows, toks)
+    lp = osc.log_softmax(logits.double().numpy())
+    exp = np.array([lp[r, t] for r, t in zip(rows, toks)])
+    assert np.abs(out.cpu().numpy() - exp).max() <= 2e-5
+
+
 def _backend(tr, **attrs):
     b = object.__new__(tr.DirectFlashInferMaskedTreeVerifyBackend)
     b.score_weights = None
