@@ -252,8 +252,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         row_block = max(16, min(MAX_ROWS_PER_ITEM if direct else MAX_ROWS_PER_ITEM_OTHER, row_block))
         split_target = self.split_target_items
         if split_target is None:
-            # one 8-wave workgroup per CU for the head_dim-128 kernel
-            split_target = DEFAULT_CU_COUNT if direct else 2 * DEFAULT_CU_COUNT
+            # One 8-wave workgroup per CU for the head_dim-128 kernel; a batch of
+            # unequal requests gets two items per CU, dispatched longest first.
+            per_cu = 1 if (direct and batch == 1) else 2
+            split_target = per_cu * DEFAULT_CU_COUNT
         blocks = []  # (req, row_start, num_rows)
         for b in range(batch):
             rows = qo_lens[b] * group
@@ -276,14 +278,16 @@ class BatchPrefillWithPagedKVCacheWrapper:
             for (b, r0, nr) in blocks:
                 tiles = math.ceil(kv_lens[b] / TILE_KEYS)
                 splits = max(1, math.ceil(tiles / tiles_per_split))
+                # balanced splits of the request's tiles
+                per = math.ceil(tiles / splits) if tiles else 0
                 for h in range(hkv):
                     if splits == 1:
                         work.append((b, h, r0, nr, 0, kv_lens[b], -1, 0))
                         continue
                     base = partial_rows
                     for s in range(splits):
-                        k0 = s * tiles_per_split * TILE_KEYS
-                        k1 = min(kv_lens[b], (s + 1) * tiles_per_split * TILE_KEYS)
+                        k0 = s * per * TILE_KEYS
+                        k1 = min(kv_lens[b], (s + 1) * per * TILE_KEYS)
                         work.append((b, h, r0, nr, k0, k1, base + s * nr, 0))
                     merge.append((b, h, r0, nr, base, splits, 0, 0))
                     partial_rows += splits * nr
@@ -291,6 +295,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 break
             tiles_per_split *= 2
         max_rows = max((nr for (_, _, nr) in blocks), default=1)
+        # Largest items first: workgroups are dispatched in order, so the
+        # long ones start early and the short ones fill in behind them.
+        work.sort(key=lambda it: -(it[5] - it[4]))
 
         meta_vals: list[int] = []
         for item in work:
