@@ -1,11 +1,17 @@
 // Ancestor-masked paged tree / forest verify attention for gfx950.
 //
-// One workgroup (4 waves) handles one work item: a block of packed query rows
-// (row = node * group + head_in_group, so the `group` query heads sharing a KV
-// head are stacked as rows) of one KV head against one split of the request's
-// keys.  Keys stream through LDS in tiles of 64 gathered through the page
-// table; the next tile is prefetched into registers while the current one is
-// multiplied.
+// A work item is a block of packed query rows (row = node * group +
+// head_in_group, so the `group` query heads sharing a KV head are stacked as
+// rows) of one KV head against one split of the request's keys; keys are
+// processed in tiles of 64 gathered through the page table.  Two kernels:
+//
+//   tree_attn_d128_kernel  head_dim 128, pages of >= 16 tokens: 8 waves, KV
+//                          streamed into a 4-tile LDS ring by direct
+//                          global->LDS loads, V^T read with transposing LDS
+//                          loads, scores of the next tile pipelined against
+//                          the current tile's softmax (see its section below);
+//   tree_attn_kernel       other shapes: 4 waves, KV staged through registers
+//                          into LDS one tile ahead.
 //
 // MFMA formulation (v_mfma_f32_16x16x32 f16/bf16), per 16-row tile:
 //   S^T[key, row] = K[key, :] . Q[row, :]     A = K from LDS, B = Q in registers
@@ -14,8 +20,8 @@
 // 4*(l/16)..+3, so every lane holds scores and outputs of a single query row:
 // the online softmax needs only two cross-lane reductions (max) per tile and
 // none for the rescale.  P^T feeds the second MFMA straight from registers
-// because V^T is written to LDS with its keys in the order in which the score
-// tile's C layout hands them out (see vt_position).
+// because V^T is presented to it with its keys in the order in which the
+// score tile's C layout hands them out (see vt_position).
 //
 // Masks are applied in registers: keys below mask_col_start are visible to
 // every row, keys at and after it use the row's 64-bit ancestor bitmask; tiles
