@@ -60,8 +60,8 @@ struct AttnArgs {
   int64_t out_stride_token;  // elements
   int64_t out_stride_head;   // elements
   float* lse;
-  float* part_o;
-  float* part_lse;
+  uint16_t* part_o;  // normalised partial O rows in the output dtype
+  float* part_lse;    // base-2 LSE of each partial row
   float scale_log2;  // sm_scale * log2(e)
   int mask_mode;
   int group;
@@ -73,6 +73,8 @@ struct AttnArgs {
 typedef __fp16 fp16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 half2v __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x2v __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef short v4i16 __attribute__((ext_vector_type(4)));
 
 template <bool BF16>
 struct Mfma;
@@ -85,6 +87,11 @@ struct Mfma<false> {
   typedef f16x8 frag;
   static __device__ __forceinline__ f32x4 run(frag a, frag b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  // K = 16 form: a and b hold four 16-bit elements each.
+  static __device__ __forceinline__ f32x4 run16(v4i16 a, v4i16 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b), c, 0, 0,
+                                                 0);
   }
   static __device__ __forceinline__ uint16_t from_float(float x) {
     _Float16 h = static_cast<_Float16>(x);
@@ -104,6 +111,9 @@ struct Mfma<true> {
   typedef bf16x8 frag;
   static __device__ __forceinline__ f32x4 run(frag a, frag b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 run16(v4i16 a, v4i16 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint16_t from_float(float x) {
     __bf16 h = static_cast<__bf16>(x);
@@ -201,12 +211,11 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
   const int grp = lane >> 4;
   const int r16 = lane & 15;
 
-  const int req = w.req;
   const int kvh = w.kv_head;
-  const int qo_start = a.qo_indptr[req];
-  const int qo_len = a.qo_indptr[req + 1] - qo_start;
-  const int kv_len = a.kv_len[req];
-  const int pt_base = a.kv_indptr[req];
+  const int qo_start = w.qo_start;
+  const int qo_len = w.qo_len;
+  const int kv_len = w.kv_len;
+  const int pt_base = w.page_offset;
   const int kv_end = min(w.kv_end, kv_len);
   const int G = a.group;
   const int64_t head_off = int64_t(kvh) * D * 2;
@@ -215,7 +224,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
   int vis_all = kv_end;
   int col0 = 0;
   if (a.mask_mode == ATLAS_MASK_TREE) {
-    col0 = a.mask_col_start[req];
+    col0 = w.mask_col_start;
     vis_all = min(vis_all, col0);
   } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
     vis_all = min(vis_all, kv_len - qo_len + 1);
@@ -463,11 +472,14 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
         a.lse[int64_t(qo_start + node_of[rt]) * a.num_qo_heads + head_of[rt]] = lse2 * kLn2;
     } else {
       const int64_t prow = int64_t(w.partial_row) + lr;
-      float* po = a.part_o + prow * D;
+      char* po = reinterpret_cast<char*>(a.part_o + prow * D);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
-        const f32x4 v = o[rt][dt] * inv;
-        *reinterpret_cast<f32x4*>(po + dt * 16 + grp * 4) = v;
+        const uint32_t lo = uint32_t(M::from_float(o[rt][dt][0] * inv)) |
+                            (uint32_t(M::from_float(o[rt][dt][1] * inv)) << 16);
+        const uint32_t hi = uint32_t(M::from_float(o[rt][dt][2] * inv)) |
+                            (uint32_t(M::from_float(o[rt][dt][3] * inv)) << 16);
+        *reinterpret_cast<uint2*>(po + (dt * 16 + grp * 4) * 2) = uint2{lo, hi};
       }
       if (grp == 0) a.part_lse[prow] = lse2;
     }
@@ -498,8 +510,6 @@ constexpr int kRowBytes128 = 128 * 2;
 constexpr int kHalf128 = kTileKeys * kRowBytes128;  // 16 KiB of K, then 16 KiB of V
 constexpr int kTile128 = 2 * kHalf128;
 
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-
 __device__ __forceinline__ v4i16 lds_read_tr16(const char* p) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
       (__attribute__((address_space(3))) v4i16*)(reinterpret_cast<uintptr_t>(p)));
@@ -525,31 +535,17 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const __attribute__((address_space(3))) char*)(p)));
 }
 
-typedef const __attribute__((address_space(4))) int32_t* const_i32_ptr;
-
-// Physical pages of the 4-key blocks a wave loads in a tile: with NW waves,
-// wave w loads blocks NW*j + w (keys 4*(NW*j + w) .. +3) for j < 16/NW.  Page
-// size is a power of two >= 16, so a block never straddles a page (the split's
-// last block clamps to its last key).  Scalar loads: wave-uniform, counted
-// apart from the KV loads.
-template <int NW>
-__device__ __forceinline__ void tile_pages(const_i32_ptr pages, int t0, int last_key, int page_shift, int wave,
-                                           int (&pid)[16 / NW]) {
-#pragma unroll
-  for (int j = 0; j < 16 / NW; ++j) pid[j] = pages[min(t0 + 4 * (NW * j + wave), last_key) >> page_shift];
-}
-
-// Issue the K and V rows of one tile into a stage: lane l of wave w loads,
-// for each of its blocks b = NW*j + w, granule (l % 16) of the swizzled row of
+// Issue the K and V rows of one tile into a stage: lane l of loader li loads,
+// for each of its blocks b = NL*j + li, granule (l % 16) of the swizzled row of
 // key 4b + l/16 into the 1 KiB block b of the K and V halves.
-template <int NW>
+template <int NL>
 __device__ __forceinline__ void issue_tile(const char* head_base, int64_t page_stride, int64_t token_stride,
-                                           int64_t v_offset, const int (&pid)[16 / NW], int t0, int last_key,
-                                           int page_size, int wave, int lane, uint32_t stage) {
+                                           int64_t v_offset, const int (&pid)[16 / NL], int t0, int last_key,
+                                           int page_size, int li, int lane, uint32_t stage) {
   const int c16p = lane & 15;
 #pragma unroll
-  for (int j = 0; j < 16 / NW; ++j) {
-    const int blk = NW * j + wave;
+  for (int j = 0; j < 16 / NL; ++j) {
+    const int blk = NL * j + li;
     const int key = 4 * blk + (lane >> 4);
     const int p = min(t0 + key, last_key);
     const char* row = head_base + int64_t(pid[j]) * page_stride + int64_t(p & (page_size - 1)) * token_stride;
@@ -558,138 +554,72 @@ __device__ __forceinline__ void issue_tile(const char* head_base, int64_t page_s
   }
 }
 
-// Per-wave state of the rows a compute wave owns.
-template <bool BF16, int RT>
-struct RowState {
-  typename Mfma<BF16>::frag qf[RT][4];
-  f32x4 o[RT][8];
-  float m_run[RT];
-  float l_run[RT];
-  uint64_t tbits[RT];
-  int climit[RT];
+// What one workgroup streams: the split's tiles, their page ids and the LDS
+// ring, plus this wave's loader index (li < 0: the wave issues no loads).
+//
+// Page ids reach a loader wave 64 at a time: lane l of `win_cur` holds the id
+// of the split's page 64*win + l (clamped to its last page), `win_nxt` the
+// next 64.  A tile's pages never straddle a window (a tile is 64 aligned keys,
+// pages are a power of two >= 16 tokens), and the ids of a block are read with
+// v_readlane, so the loop issues no scalar memory loads whose completion would
+// be tied to the LDS reads' counter.
+template <int NL>
+struct Ring {
+  const char* head_base;
+  const int32_t* pages;  // the request's page ids
+  int64_t page_stride, token_stride, v_offset;
+  int page_size, page_shift;
+  int t_first, nt, last_key;
+  int page0, last_page;  // first and last page of the split
+  int win;
+  int win_cur, win_nxt;
+  int li, lane;
+  uint32_t lds0;
 };
 
-// Scores S^T = K Q^T of one 64-key tile for a wave's RT row tiles.
-template <bool BF16, int RT>
-__device__ __forceinline__ void d128_scores(const RowState<BF16, RT>& st, const char* sb, int grp, int r16,
-                                            f32x4 (&s)[RT][4]) {
-  typedef Mfma<BF16> M;
-  typedef typename M::frag frag;
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt)
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) s[rt][kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int kt = 0; kt < 4; ++kt) {
-    frag af[4];
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      af[ks] = __builtin_bit_cast(
-          frag, *reinterpret_cast<const uint4*>(sb + (kt * 16 + r16) * kRowBytes128 + (((ks * 4 + grp) ^ r16) << 4)));
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) s[rt][kt] = M::run(af[ks], st.qf[rt][ks], s[rt][kt]);
+template <int NL>
+__device__ __forceinline__ int window_ids(const Ring<NL>& r, int w) {
+  return r.pages[min(r.page0 + 64 * w + r.lane, r.last_page)];
+}
+
+// Vector loads of the first two page windows (loader waves); the caller waits
+// for them together with the queries before the first tile is issued.
+template <int NL>
+__device__ __forceinline__ void ring_load_windows(Ring<NL>& r) {
+  r.win = 0;
+  if (r.li >= 0 && r.nt > 0) {
+    r.win_cur = window_ids<NL>(r, 0);
+    r.win_nxt = window_ids<NL>(r, 1);
   }
 }
 
-// Online softmax of one tile's scores (lazy rescale, applied branch-free so
-// the tile's instructions form one block the scheduler can interleave with
-// the next tile's score MFMAs) and O^T += V^T P^T with V^T from transposing
-// LDS reads.  MASKED tiles apply the tree / causal / length mask.
-template <bool BF16, int RT, bool MASKED>
-__device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][4], const char* sb, int t0,
-                                                int kv_end, int col0, int mask_mode, float scale_log2, int grp,
-                                                int r16) {
-  typedef Mfma<BF16> M;
-  typedef typename M::frag frag;
-  frag pf[RT][2];
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    if constexpr (MASKED) {
-#pragma unroll
-      for (int kt = 0; kt < 4; ++kt) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = t0 + kt * 16 + grp * 4 + i;
-          bool vis = p < kv_end;
-          if (mask_mode == ATLAS_MASK_TREE) {
-            const int b = p - col0;
-            const bool bit = ((st.tbits[rt] >> (b & 63)) & 1ull) != 0;
-            vis = vis & ((p < col0) | ((b < 64) & bit));
-          } else if (mask_mode == ATLAS_MASK_CAUSAL) {
-            vis = vis & (p <= st.climit[rt]);
-          }
-          s[rt][kt][i] = vis ? s[rt][kt][i] : -INFINITY;
-        }
-      }
-    }
-    float mx = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
-                     fmaxf(fmaxf(s[rt][1][0], s[rt][1][1]), fmaxf(s[rt][1][2], s[rt][1][3])));
-    mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[rt][2][0], s[rt][2][1]), fmaxf(s[rt][2][2], s[rt][2][3])),
-                         fmaxf(fmaxf(s[rt][3][0], s[rt][3][1]), fmaxf(s[rt][3][2], s[rt][3][3]))));
-    mx = wave_max_across_groups(mx) * scale_log2;
-    // Rescale only when the row maximum grew by more than kRescaleLog2 (so P
-    // stays below 2^kRescaleLog2); alpha = 1 leaves O and l unchanged.
-    const bool grow = mx > st.m_run[rt] + kRescaleLog2;
-    const float m_new = grow ? fmaxf(st.m_run[rt], mx) : st.m_run[rt];
-    const float alpha = (grow && st.m_run[rt] != -INFINITY) ? __builtin_amdgcn_exp2f(st.m_run[rt] - m_new)
-                                                            : (grow ? 0.f : 1.f);
-    st.l_run[rt] *= alpha;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] *= alpha;
-    st.m_run[rt] = m_new;
-    const float neg_m = m_new == -INFINITY ? 0.f : -m_new;
-    uint32_t pk[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][0], scale_log2, neg_m));
-      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][1], scale_log2, neg_m));
-      const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][2], scale_log2, neg_m));
-      const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][kt][3], scale_log2, neg_m));
-      pk[kt][0] = M::pack2(p0, p1);
-      pk[kt][1] = M::pack2(p2, p3);
-      st.l_run[rt] = M::sum2(pk[kt][1], M::sum2(pk[kt][0], st.l_run[rt]));
-    }
-    pf[rt][0] = __builtin_bit_cast(frag, uint4{pk[0][0], pk[0][1], pk[1][0], pk[1][1]});
-    pf[rt][1] = __builtin_bit_cast(frag, uint4{pk[2][0], pk[2][1], pk[3][0], pk[3][1]});
-  }
-
-  const int e = r16 >> 2;
-  const int q = r16 & 3;
-  const char* vb = sb + kHalf128;
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    const int key0 = 32 * kk + 4 * grp + e;
-    const char* vrow = vb + key0 * kRowBytes128 + ((q & 1) << 3);
-    const int vsw = (key0 & 7) << 1;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const char* p0 = vrow + (((2 * dt + (q >> 1)) ^ vsw) << 4);
-      const v4i16 lo = lds_read_tr16(p0);
-      const v4i16 hi = lds_read_tr16(p0 + 16 * kRowBytes128);
-      const frag av = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-#pragma unroll
-      for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run(av, pf[rt][kk], st.o[rt][dt]);
-    }
-  }
-}
-
-// The KV ring holds kStages128 tiles.  Tile k is issued at loop iteration
-// k - 3; iteration t waits for tile t+1 (whose keys feed the score MFMAs
-// overlapped with tile t's softmax), then issues tile t+3 into the stage tile
-// t-1 used: tiles t and t+1 are being read, t+2 and t+3 are in flight.
+// The KV ring holds kStages128 tiles.  Tile k is issued at ring step k - 3;
+// ring step t waits for tile t+1, joins the workgroup barrier and issues tile
+// t+3 into the stage tile t-1 used.  Waves that pipeline the next tile's
+// scores compute tile t after step t (reading tiles t and t+1); the others
+// compute tile t before step t.  Either way every wave is past its last read
+// of tile t-1 at step t's barrier.
 constexpr int kStages128 = 4;
 
-template <int NW>
-__device__ __forceinline__ void d128_issue(int k, int nt, const char* head_base, const AttnArgs& a,
-                                           const_i32_ptr pages, int (&pid)[16 / NW], int t_first, int last_key,
-                                           int wave, int lane, uint32_t lds0) {
-  if (k < nt) {
-    const int t0 = t_first + k * kTileKeys;
-    issue_tile<NW>(head_base, a.page_stride, a.token_stride, a.v_offset, pid, t0, last_key, a.page_size, wave, lane,
-                   lds0 + (k % kStages128) * kTile128);
-    if (k + 1 < nt) tile_pages<NW>(pages, t0 + kTileKeys, last_key, a.page_shift, wave, pid);
+template <int NL>
+__device__ __forceinline__ void ring_issue(Ring<NL>& r, int k) {
+  if (r.li >= 0 && k < r.nt) {
+    const int t0 = r.t_first + k * kTileKeys;
+    const int wk = ((t0 >> r.page_shift) - r.page0) >> 6;
+    if (wk != r.win) {
+      // Advance one window; the next one is needed no sooner than 16 tiles on.
+      r.win = wk;
+      r.win_cur = r.win_nxt;
+      r.win_nxt = window_ids<NL>(r, wk + 1);
+    }
+    int pid[16 / NL];
+#pragma unroll
+    for (int j = 0; j < 16 / NL; ++j) {
+      const int rel = (min(t0 + 4 * (NL * j + r.li), r.last_key) >> r.page_shift) - r.page0;
+      pid[j] = __builtin_amdgcn_readlane(r.win_cur, rel & 63);
+    }
+    issue_tile<NL>(r.head_base, r.page_stride, r.token_stride, r.v_offset, pid, t0, r.last_key, r.page_size, r.li,
+                   r.lane, r.lds0 + (k % kStages128) * kTile128);
   }
 }
 
@@ -702,212 +632,558 @@ __device__ __forceinline__ void bare_barrier() {
 }
 
 // Waits until tile `k` has landed given that tiles up to min(k + ahead, nt-1)
-// were issued after it (ahead <= 2).
-template <int NW>
-__device__ __forceinline__ void d128_wait(int k, int ahead, int nt) {
-  constexpr int L = 2 * (16 / NW);
+// were issued after it (ahead <= 2).  Waves that issue nothing have nothing
+// outstanding, so the wait returns at once.
+template <int NL>
+__device__ __forceinline__ void ring_wait(int k, int ahead, int nt) {
+  constexpr int L = 2 * (16 / NL);
   const int after = min(ahead, nt - 1 - k);
   if (after >= 2) wait_vmcnt<2 * L>();
   else if (after == 1) wait_vmcnt<L>();
   else wait_vmcnt<0>();
 }
 
-// Pre-loop ring step: tile 0 landed (tiles 1 and 2 may be in flight).
-template <int NW>
-__device__ __forceinline__ void d128_ring_first(int nt) {
-  d128_wait<NW>(0, 2, nt);
+// Prologue: tiles 0, 1, 2 in flight (page windows already loaded).
+template <int NL>
+__device__ __forceinline__ void ring_start(Ring<NL>& r) {
+#pragma unroll
+  for (int k = 0; k < 3; ++k) ring_issue<NL>(r, k);
+}
+
+// Page windows and the caller's queries (issued just before) land together,
+// then tiles 0..2 are issued.
+template <int NL>
+__device__ __forceinline__ void ring_begin(Ring<NL>& r) {
+  ring_load_windows<NL>(r);
+  wait_vmcnt<0>();
+  ring_start<NL>(r);
+}
+
+// Tile 0 landed (tiles 1 and 2 may be in flight).
+template <int NL>
+__device__ __forceinline__ void ring_first(const Ring<NL>& r) {
+  ring_wait<NL>(0, 2, r.nt);
   bare_barrier();
 }
 
-// Ring step of iteration t: tile t+1 landed (t+2 may be in flight), every
-// wave is past iteration t-1, issue tile t+3.
-template <int NW>
-__device__ __forceinline__ void d128_ring_step(int t, int nt, const char* head_base, const AttnArgs& a,
-                                               const_i32_ptr pages, int (&pid)[16 / NW], int t_first, int last_key,
-                                               int wave, int lane, uint32_t lds0) {
-  if (t + 1 < nt) d128_wait<NW>(t + 1, 1, nt);
+template <int NL>
+__device__ __forceinline__ void ring_step(Ring<NL>& r, int t) {
+  if (t + 1 < r.nt) ring_wait<NL>(t + 1, 1, r.nt);
   bare_barrier();
-  d128_issue<NW>(t + 3, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+  ring_issue<NL>(r, t + 3);
 }
 
-// Rows of one compute wave: row tiles wave + NW * r for r < RT.  Loads the
-// queries and masks, runs the pipelined tile loop and writes the output (or
-// the split's partial state).
-template <bool BF16, int NW, int RT>
-__device__ __forceinline__ void d128_rows(const AttnArgs& a, const atlas_attn_work_t& w, const char* lds,
-                                          const char* head_base, const_i32_ptr pages, int (&pid)[16 / NW],
-                                          int t_first, int nt, int nt_plain, int last_key, int kv_end, int col0,
-                                          int qo_start, int qo_len, int kv_len, int wave, int lane, uint32_t lds0) {
+// A wave with no rows: loads its share of the tiles (if it is a loader) and
+// keeps the workgroup's barrier count.
+template <int NL>
+__device__ __forceinline__ void ring_only(Ring<NL>& r) {
+  ring_begin<NL>(r);
+  if (r.nt > 0) {
+    ring_first<NL>(r);
+    for (int t = 0; t < r.nt; ++t) ring_step<NL>(r, t);
+  }
+}
+
+// Per-wave state of the row tiles a wave owns.
+template <bool BF16, int RT>
+struct RowState {
+  typename Mfma<BF16>::frag qf[RT][4];
+  f32x4 o[RT][8];
+  float m_run[RT];
+  float l_run[RT];
+  uint64_t tbits[RT];
+  int climit[RT];
+  int node_of[RT];
+  int head_of[RT];
+  int lrow[RT];  // row index inside the item
+  bool row_ok[RT];
+};
+
+// Scores S^T = K Q^T of the NKT 16-key blocks kb0 .. kb0+NKT-1 of one tile for
+// a wave's RT row tiles (NKT = 4: the whole 64-key tile).
+template <bool BF16, int RT, int NKT>
+__device__ __forceinline__ void d128_scores(const RowState<BF16, RT>& st, const char* sb, int kb0, int grp, int r16,
+                                            f32x4 (&s)[RT][NKT]) {
   typedef Mfma<BF16> M;
   typedef typename M::frag frag;
-  constexpr int D = 128;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int j = 0; j < NKT; ++j) s[rt][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int j = 0; j < NKT; ++j) {
+    const int kt = kb0 + j;
+    frag af[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      af[ks] = __builtin_bit_cast(
+          frag, *reinterpret_cast<const uint4*>(sb + (kt * 16 + r16) * kRowBytes128 + (((ks * 4 + grp) ^ r16) << 4)));
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) s[rt][j] = M::run(af[ks], st.qf[rt][ks], s[rt][j]);
+  }
+}
+
+// Online softmax of the scores of blocks kb0 .. kb0+NKT-1 and O^T += V^T P^T
+// with V^T from transposing LDS reads.  The running maximum moves only when a
+// row's maximum grew by more than kRescaleLog2 (P stays below 2^kRescaleLog2),
+// so the rescale of O and l is skipped for the whole wave on most tiles.
+// MASKED tiles apply the tree / causal / length mask.
+template <bool BF16, int RT, int NKT, bool MASKED>
+__device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][NKT], const char* sb, int kb0,
+                                                int t0, int kv_end, int col0, int mask_mode, float scale_log2,
+                                                int grp, int r16) {
+  typedef Mfma<BF16> M;
+  typedef typename M::frag frag;
+  uint32_t pk[RT][NKT][2];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    if constexpr (MASKED) {
+#pragma unroll
+      for (int j = 0; j < NKT; ++j) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int p = t0 + (kb0 + j) * 16 + grp * 4 + i;
+          bool vis = p < kv_end;
+          if (mask_mode == ATLAS_MASK_TREE) {
+            const int b = p - col0;
+            const bool bit = ((st.tbits[rt] >> (b & 63)) & 1ull) != 0;
+            vis = vis & ((p < col0) | ((b < 64) & bit));
+          } else if (mask_mode == ATLAS_MASK_CAUSAL) {
+            vis = vis & (p <= st.climit[rt]);
+          }
+          s[rt][j][i] = vis ? s[rt][j][i] : -INFINITY;
+        }
+      }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NKT; ++j)
+      mx = fmaxf(mx, fmaxf(fmaxf(s[rt][j][0], s[rt][j][1]), fmaxf(s[rt][j][2], s[rt][j][3])));
+    mx = wave_max_across_groups(mx) * scale_log2;
+    const bool grow = mx > st.m_run[rt] + kRescaleLog2;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float m_new = grow ? mx : st.m_run[rt];
+      const float alpha = (grow && st.m_run[rt] != -INFINITY) ? __builtin_amdgcn_exp2f(st.m_run[rt] - m_new)
+                                                              : (grow ? 0.f : 1.f);
+      st.l_run[rt] *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] *= alpha;
+      st.m_run[rt] = m_new;
+    }
+    const float neg_m = st.m_run[rt] == -INFINITY ? 0.f : -st.m_run[rt];
+#pragma unroll
+    for (int j = 0; j < NKT; ++j) {
+      const float p0 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][j][0], scale_log2, neg_m));
+      const float p1 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][j][1], scale_log2, neg_m));
+      const float p2 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][j][2], scale_log2, neg_m));
+      const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][j][3], scale_log2, neg_m));
+      pk[rt][j][0] = M::pack2(p0, p1);
+      pk[rt][j][1] = M::pack2(p2, p3);
+      st.l_run[rt] = M::sum2(pk[rt][j][1], M::sum2(pk[rt][j][0], st.l_run[rt]));
+    }
+  }
+
+  const int e = r16 >> 2;
+  const int q = r16 & 3;
+  const char* vb = sb + kHalf128;
+  if constexpr (NKT == 1) {
+    // 16 keys: one half of a 32-key block, through the K=16 MFMA whose A and B
+    // operands are exactly one transposing read and one packed score block.
+    const int kk = kb0 >> 1;
+    const int key0 = 32 * kk + 4 * grp + e;
+    const char* vrow = vb + (key0 + 16 * (kb0 & 1)) * kRowBytes128 + ((q & 1) << 3);
+    const int vsw = (key0 & 7) << 1;
+    v4i16 pb[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) pb[rt] = __builtin_bit_cast(v4i16, uint2{pk[rt][0][0], pk[rt][0][1]});
+#pragma unroll
+    for (int dt = 0; dt < 8; ++dt) {
+      const v4i16 av = lds_read_tr16(vrow + (((2 * dt + (q >> 1)) ^ vsw) << 4));
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run16(av, pb[rt], st.o[rt][dt]);
+    }
+  } else {
+    frag pf[RT][NKT / 2];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int h = 0; h < NKT / 2; ++h)
+        pf[rt][h] = __builtin_bit_cast(frag, uint4{pk[rt][2 * h][0], pk[rt][2 * h][1], pk[rt][2 * h + 1][0],
+                                                   pk[rt][2 * h + 1][1]});
+#pragma unroll
+    for (int h = 0; h < NKT / 2; ++h) {
+      const int kk = (kb0 >> 1) + h;
+      const int key0 = 32 * kk + 4 * grp + e;
+      const char* vrow = vb + key0 * kRowBytes128 + ((q & 1) << 3);
+      const int vsw = (key0 & 7) << 1;
+#pragma unroll
+      for (int dt = 0; dt < 8; ++dt) {
+        const char* p0 = vrow + (((2 * dt + (q >> 1)) ^ vsw) << 4);
+        const v4i16 lo = lds_read_tr16(p0);
+        const v4i16 hi = lds_read_tr16(p0 + 16 * kRowBytes128);
+        const frag av = __builtin_bit_cast(frag, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run(av, pf[rt][h], st.o[rt][dt]);
+      }
+    }
+  }
+}
+
+// Per-item values every wave needs.
+struct ItemCtx {
+  int t_first, nt, nt_plain, kv_end, col0, qo_start, qo_len, kv_len;
+};
+
+// Loads the queries, masks and softmax state of row tiles tile0 + tstride*rt.
+template <bool BF16, int RT>
+__device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const AttnArgs& a, const atlas_attn_work_t& w,
+                                               const ItemCtx& c, int tile0, int tstride, int lane) {
+  typedef typename Mfma<BF16>::frag frag;
   const int grp = lane >> 4;
   const int r16 = lane & 15;
   const int G = a.group;
-  const int kvh = w.kv_head;
-
-  RowState<BF16, RT> st;
-  int node_of[RT];
-  int head_of[RT];
-  bool row_ok[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const int lr = (wave + NW * rt) * 16 + r16;
-    row_ok[rt] = lr < w.num_rows;
-    const int prow = w.row_start + (row_ok[rt] ? lr : 0);
-    node_of[rt] = prow / G;
-    head_of[rt] = kvh * G + (prow - node_of[rt] * G);
+    const int lr = (tile0 + tstride * rt) * 16 + r16;
+    st.lrow[rt] = lr;
+    st.row_ok[rt] = lr < w.num_rows;
+    const int prow = w.row_start + (st.row_ok[rt] ? lr : 0);
+    st.node_of[rt] = prow / G;
+    st.head_of[rt] = w.kv_head * G + (prow - st.node_of[rt] * G);
     st.m_run[rt] = -INFINITY;
     st.l_run[rt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const char* qrow = a.q + ((int64_t(qo_start + node_of[rt]) * a.q_stride_token +
-                               int64_t(head_of[rt]) * a.q_stride_head) * 2);
+    const char* qrow = a.q + ((int64_t(c.qo_start + st.node_of[rt]) * a.q_stride_token +
+                               int64_t(st.head_of[rt]) * a.q_stride_head) * 2);
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       uint4 v = *reinterpret_cast<const uint4*>(qrow + (ks * 32 + grp * 8) * 2);
-      if (!row_ok[rt]) v = uint4{0, 0, 0, 0};
+      if (!st.row_ok[rt]) v = uint4{0, 0, 0, 0};
       st.qf[rt][ks] = __builtin_bit_cast(frag, v);
     }
-    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && row_ok[rt]) ? a.tree_mask[qo_start + node_of[rt]] : 0ull;
-    st.climit[rt] = kv_len - qo_len + node_of[rt];
+    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && st.row_ok[rt]) ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
+    st.climit[rt] = c.kv_len - c.qo_len + st.node_of[rt];
   }
-  wait_vmcnt<0>();  // queries and masks (tiles 0..2 are issued later)
+}
 
-  if (nt > 0) {
-    f32x4 s_cur[RT][4];
-    f32x4 s_nxt[RT][4];
-    d128_ring_first<NW>(nt);
-    d128_scores<BF16, RT>(st, lds, grp, r16, s_cur);
+// The tile loop of one wave: RT row tiles over key blocks kb0 .. kb0+NKT-1 of
+// every tile.  PIPE computes tile t+1's scores while tile t's softmax and P.V
+// run (RT = 1, whole tiles); otherwise each tile is computed before its ring
+// step.
+template <bool BF16, int NL, int RT, int NKT, bool PIPE>
+__device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, const AttnArgs& a, const ItemCtx& c,
+                                          const char* lds, int kb0, int lane) {
+  const int grp = lane >> 4;
+  const int r16 = lane & 15;
+  const int nt = r.nt;
+  if (nt <= 0) return;
+  ring_first<NL>(r);
+  if constexpr (PIPE) {
+    f32x4 s_cur[RT][NKT];
+    f32x4 s_nxt[RT][NKT];
+    d128_scores<BF16, RT, NKT>(st, lds, kb0, grp, r16, s_cur);
     const int n_pipe = nt - 1;
-    const int plain_end = min(nt_plain, n_pipe);
+    const int plain_end = min(c.nt_plain, n_pipe);
     int t = 0;
     for (; t < plain_end; ++t) {
-      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
-      d128_scores<BF16, RT>(st, lds + ((t + 1) % kStages128) * kTile128, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, false>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
-                                       col0, a.mask_mode, a.scale_log2, grp, r16);
+      ring_step<NL>(r, t);
+      d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
+      d128_softmax_pv<BF16, RT, NKT, false>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+                                            c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
+                                            grp, r16);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s_cur[rt][kt] = s_nxt[rt][kt];
+        for (int j = 0; j < NKT; ++j) s_cur[rt][j] = s_nxt[rt][j];
     }
     for (; t < n_pipe; ++t) {
-      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
-      d128_scores<BF16, RT>(st, lds + ((t + 1) % kStages128) * kTile128, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, true>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
-                                      col0, a.mask_mode, a.scale_log2, grp, r16);
+      ring_step<NL>(r, t);
+      d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
+      d128_softmax_pv<BF16, RT, NKT, true>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+                                           c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
+                                           grp, r16);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
-        for (int kt = 0; kt < 4; ++kt) s_cur[rt][kt] = s_nxt[rt][kt];
+        for (int j = 0; j < NKT; ++j) s_cur[rt][j] = s_nxt[rt][j];
     }
-    d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
-    if (t < nt_plain)
-      d128_softmax_pv<BF16, RT, false>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
-                                       col0, a.mask_mode, a.scale_log2, grp, r16);
+    ring_step<NL>(r, t);
+    if (t < c.nt_plain)
+      d128_softmax_pv<BF16, RT, NKT, false>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+                                            c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
+                                            grp, r16);
     else
-      d128_softmax_pv<BF16, RT, true>(st, s_cur, lds + (t % kStages128) * kTile128, t_first + t * kTileKeys, kv_end,
-                                      col0, a.mask_mode, a.scale_log2, grp, r16);
-  }
-
-#pragma unroll
-  for (int rt = 0; rt < RT; ++rt) {
-    const float l_tot = wave_sum_across_groups(st.l_run[rt]);
-    if (!row_ok[rt]) continue;
-    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
-    const float lse2 = l_tot > 0.f ? st.m_run[rt] + __builtin_log2f(l_tot) : -INFINITY;
-    const int lr = (wave + NW * rt) * 16 + r16;
-    if (w.partial_row < 0) {
-      char* orow = a.out + ((int64_t(qo_start + node_of[rt]) * a.out_stride_token +
-                             int64_t(head_of[rt]) * a.out_stride_head) * 2);
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint32_t lo = uint32_t(M::from_float(st.o[rt][dt][0] * inv)) |
-                            (uint32_t(M::from_float(st.o[rt][dt][1] * inv)) << 16);
-        const uint32_t hi = uint32_t(M::from_float(st.o[rt][dt][2] * inv)) |
-                            (uint32_t(M::from_float(st.o[rt][dt][3] * inv)) << 16);
-        *reinterpret_cast<uint2*>(orow + (dt * 16 + grp * 4) * 2) = uint2{lo, hi};
-      }
-      if (a.lse != nullptr && grp == 0)
-        a.lse[int64_t(qo_start + node_of[rt]) * a.num_qo_heads + head_of[rt]] = lse2 * kLn2;
-    } else {
-      const int64_t prow = int64_t(w.partial_row) + lr;
-      float* po = a.part_o + prow * D;
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + grp * 4) = st.o[rt][dt] * inv;
-      if (grp == 0) a.part_lse[prow] = lse2;
+      d128_softmax_pv<BF16, RT, NKT, true>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+                                           c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
+                                           grp, r16);
+  } else {
+    f32x4 s[RT][NKT];
+    int t = 0;
+    for (; t < c.nt_plain; ++t) {
+      const char* sb = lds + (t % kStages128) * kTile128;
+      d128_scores<BF16, RT, NKT>(st, sb, kb0, grp, r16, s);
+      d128_softmax_pv<BF16, RT, NKT, false>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
+                                            a.mask_mode, a.scale_log2, grp, r16);
+      ring_step<NL>(r, t);
+    }
+    for (; t < nt; ++t) {
+      const char* sb = lds + (t % kStages128) * kTile128;
+      d128_scores<BF16, RT, NKT>(st, sb, kb0, grp, r16, s);
+      d128_softmax_pv<BF16, RT, NKT, true>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
+                                           a.mask_mode, a.scale_log2, grp, r16);
+      ring_step<NL>(r, t);
     }
   }
 }
 
-// NW waves (4 or 8) per workgroup; wave w owns row tiles w and, with
-// RT_MAX = 2, w + NW.  Each wave keeps its rows' queries, output accumulators
-// and softmax state in architectural VGPRs.  Waves without rows only load.
-template <bool BF16, int NW, int RT_MAX>
-__global__ __launch_bounds__(NW * 64, 1) void tree_attn_d128_kernel(AttnArgs a) {
-  static_assert(NW == 4 || NW == 8, "four or eight waves");
-  static_assert(RT_MAX == 1 || RT_MAX == 2, "one or two row tiles per wave");
+// Writes one finished row (the final output, or the split's partial state,
+// both in the output dtype) for the lanes' D columns 16*dt + 4*grp .. +3, dt
+// in [dt0, dt0 + NDT).
+template <bool BF16, int NDT>
+__device__ __forceinline__ void d128_store(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c, int node,
+                                           int head, int lrow, bool row_ok, const f32x4 (&o)[NDT], int dt0,
+                                           float inv, float lse2, bool write_lse, int grp) {
+  typedef Mfma<BF16> M;
   constexpr int D = 128;
+  if (!row_ok) return;
+  const bool final_row = w.partial_row < 0;
+  const int64_t prow = int64_t(w.partial_row) + lrow;
+  char* orow = final_row ? a.out + ((int64_t(c.qo_start + node) * a.out_stride_token +
+                                     int64_t(head) * a.out_stride_head) * 2)
+                         : reinterpret_cast<char*>(a.part_o + prow * D);
+#pragma unroll
+  for (int i = 0; i < NDT; ++i) {
+    const int dt = dt0 + i;
+    const uint32_t lo = uint32_t(M::from_float(o[i][0] * inv)) | (uint32_t(M::from_float(o[i][1] * inv)) << 16);
+    const uint32_t hi = uint32_t(M::from_float(o[i][2] * inv)) | (uint32_t(M::from_float(o[i][3] * inv)) << 16);
+    *reinterpret_cast<uint2*>(orow + (dt * 16 + grp * 4) * 2) = uint2{lo, hi};
+  }
+  if (write_lse && grp == 0) {
+    if (!final_row) a.part_lse[prow] = lse2;
+    else if (a.lse != nullptr) a.lse[int64_t(c.qo_start + node) * a.num_qo_heads + head] = lse2 * kLn2;
+  }
+}
 
+// Whole row tiles: normalise and store.
+template <bool BF16, int RT>
+__device__ __forceinline__ void d128_store_rows(RowState<BF16, RT>& st, const AttnArgs& a,
+                                                const atlas_attn_work_t& w, const ItemCtx& c, int lane) {
+  const int grp = lane >> 4;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const float l_tot = wave_sum_across_groups(st.l_run[rt]);
+    const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+    const float lse2 = l_tot > 0.f ? st.m_run[rt] + __builtin_log2f(l_tot) : -INFINITY;
+    d128_store<BF16, 8>(a, w, c, st.node_of[rt], st.head_of[rt], st.lrow[rt], st.row_ok[rt], st.o[rt], 0, inv, lse2,
+                        true, grp);
+  }
+}
+
+// Key parts of one row tile held by S waves (part index p, LDS slot base j0 of
+// the tile's first part): each part's unnormalised O, running max and row sum
+// go to LDS; after a workgroup barrier, part p combines the S states for D
+// columns [128 p / S, 128 (p + 1) / S) and stores them.  The caller's barriers
+// bracket the LDS exchange (every wave of the workgroup takes part in them).
+constexpr int kPartBytes = 8 * 64 * 16 + 2 * 64 * 4;  // O^T accumulators, then m and l per lane
+
+template <bool BF16>
+__device__ __forceinline__ void d128_part_put(const RowState<BF16, 1>& st, char* lds, int slot, int lane) {
+  char* base = lds + slot * kPartBytes;
+#pragma unroll
+  for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(base + (dt * 64 + lane) * 16) = st.o[0][dt];
+  reinterpret_cast<float*>(base + 8 * 64 * 16)[lane] = st.m_run[0];
+  reinterpret_cast<float*>(base + 8 * 64 * 16)[64 + lane] = wave_sum_across_groups(st.l_run[0]);
+}
+
+template <bool BF16, int S>
+__device__ __forceinline__ void d128_part_merge(const RowState<BF16, 1>& st, const char* lds, int slot0, int p,
+                                                const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c,
+                                                int lane) {
+  constexpr int NDT = 8 / S;
+  float m[S], l[S];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    const float* ml = reinterpret_cast<const float*>(lds + (slot0 + i) * kPartBytes + 8 * 64 * 16);
+    m[i] = ml[lane];
+    l[i] = ml[64 + lane];
+    mx = fmaxf(mx, m[i]);
+  }
+  float wsum = 0.f;
+  float wt[S];
+#pragma unroll
+  for (int i = 0; i < S; ++i) {
+    wt[i] = m[i] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m[i] - mx);
+    wsum += wt[i] * l[i];
+  }
+  f32x4 o[NDT];
+#pragma unroll
+  for (int k = 0; k < NDT; ++k) {
+    const int dt = p * NDT + k;
+    o[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < S; ++i)
+      o[k] += wt[i] * *reinterpret_cast<const f32x4*>(lds + (slot0 + i) * kPartBytes + (dt * 64 + lane) * 16);
+  }
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const float lse2 = wsum > 0.f ? mx + __builtin_log2f(wsum) : -INFINITY;
+  d128_store<BF16, NDT>(a, w, c, st.node_of[0], st.head_of[0], st.lrow[0], st.row_ok[0], o, p * NDT, inv, lse2,
+                        p == 0, lane >> 4);
+}
+
+// Row tiles of an item whose count T = 4k + R with k <= 2 and R in {1, 2}:
+// waves 0..3 (one per SIMD) own whole tiles w and w + 4 (k per wave); the R
+// leftover tiles are split by keys over waves 4..7 (R = 1: four 16-key
+// quarters of every tile; R = 2: two 32-key halves per tile), which also
+// issue all the KV loads.  Every SIMD then carries k + R/4 tile-units instead
+// of the k + 1 (or more) of one tile per wave.
+template <bool BF16>
+__device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c,
+                                                char* lds, Ring<4>& r, int T, int wave, int lane) {
+  const int R = T & 3;
+  const int k = T >> 2;
+  if (wave < 4) {
+    if (k == 2) {
+      RowState<BF16, 2> st;
+      d128_load_rows<BF16, 2>(st, a, w, c, wave, 4, lane);
+      ring_begin<4>(r);
+      d128_loop<BF16, 4, 2, 4, false>(st, r, a, c, lds, 0, lane);
+      d128_store_rows<BF16, 2>(st, a, w, c, lane);
+    } else if (k == 1) {
+      RowState<BF16, 1> st;
+      d128_load_rows<BF16, 1>(st, a, w, c, wave, 4, lane);
+      ring_begin<4>(r);
+      d128_loop<BF16, 4, 1, 4, true>(st, r, a, c, lds, 0, lane);
+      d128_store_rows<BF16, 1>(st, a, w, c, lane);
+    } else {
+      ring_only<4>(r);
+    }
+    bare_barrier();
+    bare_barrier();
+    return;
+  }
+  const int j = wave - 4;
+  RowState<BF16, 1> st;
+  if (R == 1) {
+    d128_load_rows<BF16, 1>(st, a, w, c, 4 * k, 0, lane);
+    ring_begin<4>(r);
+    d128_loop<BF16, 4, 1, 1, false>(st, r, a, c, lds, j, lane);
+    bare_barrier();
+    d128_part_put<BF16>(st, lds, j, lane);
+    bare_barrier();
+    d128_part_merge<BF16, 4>(st, lds, 0, j, a, w, c, lane);
+  } else {
+    d128_load_rows<BF16, 1>(st, a, w, c, 4 * k + (j >> 1), 0, lane);
+    ring_begin<4>(r);
+    d128_loop<BF16, 4, 1, 2, false>(st, r, a, c, lds, 2 * (j & 1), lane);
+    bare_barrier();
+    d128_part_put<BF16>(st, lds, j, lane);
+    bare_barrier();
+    d128_part_merge<BF16, 2>(st, lds, j & ~1, j & 1, a, w, c, lane);
+  }
+}
+
+// Other row counts: tile i on wave i % 8 (two per wave past 8 tiles); every
+// wave loads its share of the KV.
+template <bool BF16>
+__device__ __forceinline__ void d128_item_rr(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c,
+                                             char* lds, Ring<8>& r, int T, int wave, int lane) {
+  const int mine = (wave < T ? 1 : 0) + (wave + 8 < T ? 1 : 0);
+  if (mine == 2) {
+    RowState<BF16, 2> st;
+    d128_load_rows<BF16, 2>(st, a, w, c, wave, 8, lane);
+    ring_begin<8>(r);
+    d128_loop<BF16, 8, 2, 4, false>(st, r, a, c, lds, 0, lane);
+    d128_store_rows<BF16, 2>(st, a, w, c, lane);
+  } else if (mine == 1) {
+    RowState<BF16, 1> st;
+    d128_load_rows<BF16, 1>(st, a, w, c, wave, 8, lane);
+    ring_begin<8>(r);
+    d128_loop<BF16, 8, 1, 4, true>(st, r, a, c, lds, 0, lane);
+    d128_store_rows<BF16, 1>(st, a, w, c, lane);
+  } else {
+    ring_only<8>(r);
+  }
+}
+
+template <int NL>
+__device__ __forceinline__ void ring_init(Ring<NL>& r, const AttnArgs& a, const char* head_base, const int32_t* pages,
+                                          const ItemCtx& c, int last_key, int li, int lane, uint32_t lds0) {
+  r.head_base = head_base;
+  r.pages = pages;
+  r.page_stride = a.page_stride;
+  r.token_stride = a.token_stride;
+  r.v_offset = a.v_offset;
+  r.page_size = a.page_size;
+  r.page_shift = a.page_shift;
+  r.t_first = c.t_first;
+  r.nt = c.nt;
+  r.last_key = last_key;
+  r.page0 = c.t_first >> a.page_shift;
+  r.last_page = max(last_key, 0) >> a.page_shift;
+  r.win = 0;
+  r.win_cur = 0;
+  r.win_nxt = 0;
+  r.li = li;
+  r.lane = lane;
+  r.lds0 = lds0;
+}
+
+// 8 waves (two per SIMD), one workgroup per CU.  The item's row-tile count
+// picks the wave layout (d128_item_split / d128_item_rr).
+template <bool BF16>
+__global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
+  constexpr int D = 128;
   __shared__ __attribute__((aligned(1024))) char lds[kStages128 * kTile128];
 
   const atlas_attn_work_t w = a.work[blockIdx.x];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int req = w.req;
-  const int qo_start = a.qo_indptr[req];
-  const int qo_len = a.qo_indptr[req + 1] - qo_start;
-  const int kv_len = a.kv_len[req];
-  const int kv_end = min(w.kv_end, kv_len);
+  ItemCtx c;
+  c.qo_start = w.qo_start;
+  c.qo_len = w.qo_len;
+  c.kv_len = w.kv_len;
+  c.kv_end = min(w.kv_end, c.kv_len);
 
-  int vis_all = kv_end;
-  int col0 = 0;
+  int vis_all = c.kv_end;
+  c.col0 = 0;
   if (a.mask_mode == ATLAS_MASK_TREE) {
-    col0 = a.mask_col_start[req];
-    vis_all = min(vis_all, col0);
+    c.col0 = w.mask_col_start;
+    vis_all = min(vis_all, c.col0);
   } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
-    vis_all = min(vis_all, kv_len - qo_len + 1);
+    vis_all = min(vis_all, c.kv_len - c.qo_len + 1);
   }
 
-  const int t_first = __builtin_amdgcn_readfirstlane(w.kv_start < kv_end ? w.kv_start : kv_end);
-  const int nt = __builtin_amdgcn_readfirstlane((kv_end - t_first + kTileKeys - 1) / kTileKeys);
+  c.t_first = __builtin_amdgcn_readfirstlane(w.kv_start < c.kv_end ? w.kv_start : c.kv_end);
+  c.nt = __builtin_amdgcn_readfirstlane((c.kv_end - c.t_first + kTileKeys - 1) / kTileKeys);
   // Leading tiles wholly below vis_all need no mask.
-  const int nt_plain = __builtin_amdgcn_readfirstlane(
-      min(nt, vis_all >= t_first + kTileKeys ? (vis_all - t_first) / kTileKeys : 0));
-  const int last_key = __builtin_amdgcn_readfirstlane(kv_end - 1);
+  c.nt_plain = __builtin_amdgcn_readfirstlane(
+      min(c.nt, vis_all >= c.t_first + kTileKeys ? (vis_all - c.t_first) / kTileKeys : 0));
+  const int last_key = __builtin_amdgcn_readfirstlane(c.kv_end - 1);
   const char* head_base = a.kv + int64_t(w.kv_head) * D * 2;
-  const const_i32_ptr pages = (const_i32_ptr)(a.kv_indices + a.kv_indptr[req]);
+  const int32_t* pages = a.kv_indices + w.page_offset;
   const uint32_t lds0 = lds_offset(lds);
-  wait_vmcnt<0>();
 
-  // Prologue: tiles 0, 1, 2 in flight, page ids of tile 3 loaded.
-  int pid[16 / NW];
-#pragma unroll
-  for (int j = 0; j < 16 / NW; ++j) pid[j] = 0;
-  if (nt > 0) tile_pages<NW>(pages, t_first, last_key, a.page_shift, wave, pid);
-#pragma unroll
-  for (int k = 0; k < 3; ++k) d128_issue<NW>(k, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
-
-  const int row_tiles = (w.num_rows + 15) / 16;
-  const int mine = (wave < row_tiles ? 1 : 0) + (RT_MAX == 2 && wave + NW < row_tiles ? 1 : 0);
-  if (RT_MAX == 2 && mine == 2) {
-    d128_rows<BF16, NW, RT_MAX>(a, w, lds, head_base, pages, pid, t_first, nt, nt_plain, last_key, kv_end, col0,
-                                qo_start, qo_len, kv_len, wave, lane, lds0);
-  } else if (mine >= 1) {
-    d128_rows<BF16, NW, 1>(a, w, lds, head_base, pages, pid, t_first, nt, nt_plain, last_key, kv_end, col0, qo_start,
-                           qo_len, kv_len, wave, lane, lds0);
-  } else if (nt > 0) {
-    d128_ring_first<NW>(nt);
-    for (int t = 0; t < nt; ++t)
-      d128_ring_step<NW>(t, nt, head_base, a, pages, pid, t_first, last_key, wave, lane, lds0);
+  const int T = __builtin_amdgcn_readfirstlane((w.num_rows + 15) / 16);
+  const int R = T & 3;
+  if (T <= 10 && (R == 1 || R == 2)) {
+    Ring<4> r;
+    ring_init<4>(r, a, head_base, pages, c, last_key, wave >= 4 ? wave - 4 : -1, lane, lds0);
+    d128_item_split<BF16>(a, w, c, lds, r, T, wave, lane);
+  } else {
+    Ring<8> r;
+    ring_init<8>(r, a, head_base, pages, c, last_key, wave, lane, lds0);
+    d128_item_rr<BF16>(a, w, c, lds, r, T, wave, lane);
   }
 }
 
 struct MergeArgs {
   const atlas_attn_merge_t* merge;
   const int32_t* qo_indptr;
-  const float* part_o;
+  const uint16_t* part_o;
   const float* part_lse;
   char* out;
   int64_t out_stride_token;
@@ -917,34 +1193,72 @@ struct MergeArgs {
   int num_qo_heads;
 };
 
-// One workgroup per packed row: the split LSEs give weights
-// w_s = exp2(lse_s - max) (kept in LDS), then threads sweep (split, 16-byte
-// dim chunk) pairs with independent loads and reduce the per-thread sums
-// through LDS.
+// One workgroup per packed row.  Thread (split lane sl, chunk c) merges the
+// 16-byte chunk c of the splits sl, sl + 16, ... online: each group of two
+// splits is loaded (partial O and LSE together) and folded into a running
+// maximum, weight sum and accumulator, so a row costs one round of loads.  The
+// per-thread states are then rescaled to the block maximum and summed over
+// the split lanes through LDS.
 constexpr int kMergeThreads = 256;
+
+template <bool BF16>
+__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (BF16) {
+      f[2 * i] = __uint_as_float(u[i] << 16);
+      f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    } else {
+      const half2v h = __builtin_bit_cast(half2v, u[i]);
+      f[2 * i] = static_cast<float>(h[0]);
+      f[2 * i + 1] = static_cast<float>(h[1]);
+    }
+  }
+}
 
 template <int D, bool BF16>
 __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArgs a) {
   typedef Mfma<BF16> M;
-  constexpr int CHUNKS = D / 4;                       // float4 chunks per row
+  constexpr int CHUNKS = D / 8;                       // 16-byte chunks per row
   constexpr int SPLIT_LANES = kMergeThreads / CHUNKS;  // splits read in parallel
-  __shared__ float w_sh[1024];
   __shared__ float red[kMergeThreads / 64];
-  __shared__ f32x4 acc_sh[SPLIT_LANES][CHUNKS];
+  __shared__ float acc_sh[SPLIT_LANES][CHUNKS][9];  // padded against bank conflicts
+  __shared__ float wsum_sh[SPLIT_LANES];
   const atlas_attn_merge_t mi = a.merge[blockIdx.x];
   const int row = blockIdx.y;
   if (row >= mi.num_rows) return;
   const int tid = threadIdx.x;
-  const int ns = min(mi.num_splits, 1024);
+  const int ns = mi.num_splits;
   const int64_t base = int64_t(mi.partial_row) + row;
+  const int chunk = tid % CHUNKS;
+  const int sl = tid / CHUNKS;
 
-  float mx = -INFINITY;
-  for (int sp = tid; sp < ns; sp += kMergeThreads) {
-    const float l = a.part_lse[base + int64_t(sp) * mi.num_rows];
-    w_sh[sp] = l;
-    mx = fmaxf(mx, l);
+  float m_t = -INFINITY, wsum_t = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = sl; s0 < ns; s0 += 2 * SPLIT_LANES) {
+    const int s1 = s0 + SPLIT_LANES;
+    const int64_t r0 = base + int64_t(s0) * mi.num_rows;
+    const int64_t r1 = base + int64_t(s1 < ns ? s1 : s0) * mi.num_rows;
+    const float l0 = a.part_lse[r0];
+    const float l1 = s1 < ns ? a.part_lse[r1] : -INFINITY;
+    const uint4 raw0 = *reinterpret_cast<const uint4*>(a.part_o + r0 * D + chunk * 8);
+    const uint4 raw1 = *reinterpret_cast<const uint4*>(a.part_o + r1 * D + chunk * 8);
+    const float m_new = fmaxf(m_t, fmaxf(l0, l1));
+    if (m_new == -INFINITY) continue;
+    const float sc = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_t - m_new);
+    const float w0 = l0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l0 - m_new);
+    const float w1 = l1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l1 - m_new);
+    float v0[8], v1[8];
+    unpack8<BF16>(raw0, v0);
+    unpack8<BF16>(raw1, v1);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * sc + w0 * v0[i] + w1 * v1[i];
+    wsum_t = wsum_t * sc + w0 + w1;
+    m_t = m_new;
   }
-  mx = wave_max_across_groups(mx);
+  // block maximum of the per-thread maxima
+  float mx = wave_max_across_groups(m_t);
   mx = fmaxf(mx, __shfl_xor(mx, 8));
   mx = fmaxf(mx, __shfl_xor(mx, 4));
   mx = fmaxf(mx, __shfl_xor(mx, 2));
@@ -952,46 +1266,35 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArg
   if ((tid & 63) == 0) red[tid >> 6] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  float wpart = 0.f;
-  for (int sp = tid; sp < ns; sp += kMergeThreads) {
-    const float wv = mx == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(w_sh[sp] - mx);
-    w_sh[sp] = wv;
-    wpart += wv;
-  }
-  __syncthreads();
-  const int chunk = tid % CHUNKS;
-  const int lane_split = tid / CHUNKS;
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int sp = lane_split; sp < ns; sp += SPLIT_LANES) {
-    const float wv = w_sh[sp];
-    const f32x4 v =
-        *reinterpret_cast<const f32x4*>(a.part_o + (base + int64_t(sp) * mi.num_rows) * D + chunk * 4);
-    acc += wv * v;
-  }
-  acc_sh[lane_split][chunk] = acc;
-  // total weight
-  wpart = wave_sum_across_groups(wpart);
-  wpart += __shfl_xor(wpart, 8);
-  wpart += __shfl_xor(wpart, 4);
-  wpart += __shfl_xor(wpart, 2);
-  wpart += __shfl_xor(wpart, 1);
-  __syncthreads();
-  if ((tid & 63) == 0) red[tid >> 6] = wpart;
-  __syncthreads();
-  const float wsum = red[0] + red[1] + red[2] + red[3];
-  if (tid < CHUNKS) {
-    f32x4 tot = acc_sh[0][tid];
+  const float f = (m_t == -INFINITY || mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_t - mx);
 #pragma unroll
-    for (int k = 1; k < SPLIT_LANES; ++k) tot += acc_sh[k][tid];
+  for (int i = 0; i < 8; ++i) acc_sh[sl][chunk][i] = acc[i] * f;
+  if (chunk == 0) wsum_sh[sl] = wsum_t * f;
+  __syncthreads();
+  if (tid < CHUNKS) {
+    float tot[8];
+    float wsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) tot[i] = 0.f;
+#pragma unroll
+    for (int k = 0; k < SPLIT_LANES; ++k) {
+      wsum += wsum_sh[k];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) tot[i] += acc_sh[k][tid][i];
+    }
     const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
     const int prow_q = mi.row_start + row;
     const int node = prow_q / a.group;
     const int head = mi.kv_head * a.group + (prow_q - node * a.group);
     const int qo_start = a.qo_indptr[mi.req];
     char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
-    const uint32_t lo = uint32_t(M::from_float(tot[0] * inv)) | (uint32_t(M::from_float(tot[1] * inv)) << 16);
-    const uint32_t hi = uint32_t(M::from_float(tot[2] * inv)) | (uint32_t(M::from_float(tot[3] * inv)) << 16);
-    *reinterpret_cast<uint2*>(orow + tid * 8) = uint2{lo, hi};
+    uint32_t pk[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      pk[i] = uint32_t(M::from_float(tot[2 * i] * inv)) | (uint32_t(M::from_float(tot[2 * i + 1] * inv)) << 16);
+    // 8-byte stores: output rows are only required to be 8-byte aligned.
+    *reinterpret_cast<uint2*>(orow + tid * 16) = uint2{pk[0], pk[1]};
+    *reinterpret_cast<uint2*>(orow + tid * 16 + 8) = uint2{pk[2], pk[3]};
     if (tid == 0 && a.lse != nullptr)
       a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] =
           wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
@@ -1024,16 +1327,11 @@ void launch_shape(const AttnArgs& args, int num_work, hipStream_t stream) {
 
 // head_dim 128 with power-of-two pages of >= 16 tokens: KV streamed by
 // direct-to-LDS loads through a 4-tile ring (one workgroup of 8 waves per
-// CU, two waves per SIMD).  Up to 8 row tiles: one tile per wave; up to 16:
-// two tiles per wave.
+// CU, two waves per SIMD), up to 16 row tiles per item.
 template <bool BF16>
 bool launch_d128(const AttnArgs& args, int num_work, int row_tiles, hipStream_t stream) {
-  if (row_tiles <= 8)
-    hipLaunchKernelGGL((tree_attn_d128_kernel<BF16, 8, 1>), dim3(num_work), dim3(512), 0, stream, args);
-  else if (row_tiles <= 16)
-    hipLaunchKernelGGL((tree_attn_d128_kernel<BF16, 8, 2>), dim3(num_work), dim3(512), 0, stream, args);
-  else
-    return false;
+  if (row_tiles > 16) return false;
+  hipLaunchKernelGGL((tree_attn_d128_kernel<BF16>), dim3(num_work), dim3(512), 0, stream, args);
   return true;
 }
 
@@ -1153,12 +1451,12 @@ extern "C" int atlas_tree_verify_attn(
   if (num_merge > 0) {
     ATLAS_REQUIRE(merge_dev != nullptr && workspace_dev != nullptr, "split work needs merge list and workspace");
     // The planner places the partial O rows first and the partial LSE after
-    // them: workspace = [partial_rows * D floats][partial_rows floats].
-    ATLAS_REQUIRE(workspace_bytes % (size_t(head_dim + 1) * 4) == 0,
-                  "workspace_bytes must be partial_rows * (head_dim + 1) * 4");
-    const size_t partial_rows = workspace_bytes / (size_t(head_dim + 1) * 4);
-    args.part_o = static_cast<float*>(workspace_dev);
-    args.part_lse = args.part_o + partial_rows * head_dim;
+    // them: workspace = [partial_rows * D 16-bit values][partial_rows floats].
+    const size_t row_bytes = size_t(head_dim) * 2 + 4;
+    ATLAS_REQUIRE(workspace_bytes % row_bytes == 0, "workspace_bytes must be partial_rows * (2 * head_dim + 4)");
+    const size_t partial_rows = workspace_bytes / row_bytes;
+    args.part_o = static_cast<uint16_t*>(workspace_dev);
+    args.part_lse = reinterpret_cast<float*>(args.part_o + partial_rows * head_dim);
     margs.merge = merge_dev;
     margs.qo_indptr = qo_indptr_dev;
     margs.part_o = args.part_o;

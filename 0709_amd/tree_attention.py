@@ -30,6 +30,12 @@ MAX_SPLITS = 1024
 DEFAULT_CU_COUNT = 256
 
 
+def _partial_row_bytes(head_dim: int) -> int:
+    """Workspace bytes of one split partial row: the normalised O in the output
+    dtype (16-bit) and its fp32 base-2 LSE."""
+    return 2 * head_dim + 4
+
+
 @dataclass
 class AttentionPlan:
     batch: int
@@ -111,8 +117,9 @@ def unpack_bits_little(packed: torch.Tensor, count: int) -> torch.Tensor:
 class BatchPrefillWithPagedKVCacheWrapper:
     """Paged prefill attention with a custom (tree) mask on the gfx950 kernel.
 
-    ``float_workspace_buffer`` holds the fp32 split-KV partial states (like
-    FlashInfer's workspace); its size bounds how finely keys are split.
+    ``float_workspace_buffer`` holds the split-KV partial states (like
+    FlashInfer's workspace: the partial O in the output dtype and an fp32 LSE
+    per row); its size bounds how finely keys are split.
     """
 
     def __init__(
@@ -241,10 +248,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
         group = hq // hkv
         direct = d == 128 and ps >= 16 and (ps & (ps - 1)) == 0
         if self.max_rows_per_item is None:
-            # head_dim-128 kernel: at most 128 rows (8 waves x 1 row tile) per
-            # item, the rows of a KV head split into equal blocks.
+            # head_dim-128 kernel: up to 160 rows (10 row tiles: two per wave on
+            # waves 0..3, leftovers split by keys over waves 4..7) in one block,
+            # so the keys are streamed once; more rows split into equal blocks.
             rows_max = max((qo_lens[b] * (hq // hkv) for b in range(batch)), default=1)
-            cap = 128 if direct else DEFAULT_ROWS_PER_ITEM
+            cap = 160 if direct else DEFAULT_ROWS_PER_ITEM
             nblk = max(1, math.ceil(rows_max / cap))
             row_block = 16 * math.ceil(math.ceil(rows_max / nblk) / 16)
         else:
@@ -271,7 +279,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # the merge kernel combines at most MAX_SPLITS states per row
         max_tiles = max((math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks), default=0)
         tiles_per_split = max(tiles_per_split, math.ceil(max_tiles / MAX_SPLITS))
-        ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // (4 * (d + 1))
+        ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
         while True:
             work, merge = [], []
             partial_rows = 0
@@ -280,15 +288,18 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 splits = max(1, math.ceil(tiles / tiles_per_split))
                 # balanced splits of the request's tiles
                 per = math.ceil(tiles / splits) if tiles else 0
+                # request values every item repeats (qo_start, qo_len, kv_len,
+                # mask column start, page offset) and padding to 16 ints
+                req_vals = (qo[b], qo_lens[b], kv_lens[b], cols[b], kvp[b], 0, 0, 0, 0)
                 for h in range(hkv):
                     if splits == 1:
-                        work.append((b, h, r0, nr, 0, kv_lens[b], -1, 0))
+                        work.append((b, h, r0, nr, 0, kv_lens[b], -1) + req_vals)
                         continue
                     base = partial_rows
                     for s in range(splits):
                         k0 = s * per * TILE_KEYS
                         k1 = min(kv_lens[b], (s + 1) * per * TILE_KEYS)
-                        work.append((b, h, r0, nr, k0, k1, base + s * nr, 0))
+                        work.append((b, h, r0, nr, k0, k1, base + s * nr) + req_vals)
                     merge.append((b, h, r0, nr, base, splits, 0, 0))
                     partial_rows += splits * nr
             if partial_rows <= ws_rows_cap:
@@ -419,7 +430,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             lse = torch.empty((int(q.shape[0]), plan.num_qo_heads), dtype=torch.float32, device=device)
         if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous()):
             raise ValueError("lse must be a contiguous float32 tensor")
-        ws_bytes = plan.partial_rows * (plan.head_dim + 1) * 4
+        ws_bytes = plan.partial_rows * _partial_row_bytes(plan.head_dim)
         lib = _lib.load()
         rc = lib.atlas_tree_verify_attn(
             _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride,

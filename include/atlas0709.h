@@ -114,17 +114,25 @@ int atlas_kv_commit_paged_host(const void* const* k_layers, const void* const* v
  * Ancestor-masked paged tree / forest verify attention.
  * ---------------------------------------------------------------------- */
 
-/* Work item of one attention workgroup (filled by the host planner). */
+/* Work item of one attention workgroup (filled by the host planner).  The
+ * per-request values after partial_row repeat what qo_indptr, kv_len,
+ * mask_col_start and kv_indptr hold for `req`, so a workgroup reads everything
+ * it needs to start streaming in one 64-byte load. */
 typedef struct {
   int32_t req;          /* request index */
   int32_t kv_head;      /* KV head */
   int32_t row_start;    /* first packed query row (node * group + head_in_group) */
-  int32_t num_rows;     /* packed rows handled (<= 16 * 4 * row tiles per wave) */
+  int32_t num_rows;     /* packed rows handled (<= 256) */
   int32_t kv_start;     /* first key position (multiple of 64) */
   int32_t kv_end;       /* one past the last key position of this split */
   int32_t partial_row;  /* first row in the partial buffers, or -1 when the item
                            is the only split and writes the final output */
-  int32_t pad;
+  int32_t qo_start;     /* qo_indptr[req] */
+  int32_t qo_len;       /* qo_indptr[req + 1] - qo_indptr[req] */
+  int32_t kv_len;       /* kv_len[req] */
+  int32_t mask_col_start; /* mask_col_start[req] (tree mask), else 0 */
+  int32_t page_offset;  /* kv_indptr[req] */
+  int32_t pad[4];
 } atlas_attn_work_t;
 
 /* Merge item: combines `num_splits` partial states of one row block. */
@@ -152,7 +160,10 @@ typedef struct {
  * FlashInfer NHD pages [pages, 2, page_size, Hkv, D] addressed with the
  * strides above; out: [nnz, Hq, D] in the input dtype; lse (optional, may be
  * NULL): [nnz, Hq] fp32, natural-log log-sum-exp of the scaled scores.
- * workspace_dev holds fp32 partial states: partial_rows * (D + 1) * 4 bytes.
+ * workspace_dev holds the split partial states: partial_rows rows of D
+ * 16-bit values in the output dtype (the normalised partial O, as FlashInfer
+ * keeps its split-KV temporaries in the output type), then partial_rows fp32
+ * base-2 LSEs: partial_rows * (2 * D + 4) bytes.
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with
  * causal=False and custom_mask as used by run_flashinfer_full_verify
  * (src/atlas_0709/flashinfer_full_verify.py:953-985, :1223). */

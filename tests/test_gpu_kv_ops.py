@@ -156,6 +156,62 @@ def test_batched_commit_device_positions(dev):
         np.testing.assert_array_equal(bits16(a), e)
 
 
+@pytest.mark.parametrize("as_tensors", [False, True])
+def test_commit_long_route_many_layers(dev, as_tensors):
+    """A 200-node route over 6 layers: more items than fit the kernel argument
+    block, layers not a multiple of the per-launch layer group, aliasing
+    source/destination positions (staged)."""
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(6)
+    layers, pages, ps, h, d = 6, 40, 16, 8, 128
+    cpu = [_rand(gen, (pages, 2, ps, h, d), torch.bfloat16) for _ in range(layers)]
+    perm = torch.randperm(pages, generator=gen).to(torch.int32)
+    prefix_len = 130
+    node_ids = sorted(torch.randperm(400, generator=gen)[:200].tolist())
+    src = [prefix_len + n for n in node_ids]
+    dst = list(range(prefix_len, prefix_len + len(node_ids)))
+    assert kv.commit_positions_need_staging(src, dst)
+    devs = [t.to(dev) for t in cpu]
+    s_arg, d_arg = (torch.tensor(src, device=dev), torch.tensor(dst, device=dev)) if as_tensors else (src, dst)
+    kv.commit_paged(devs, s_arg, d_arg, kv_indptr=torch.tensor([0, pages], dtype=torch.int32, device=dev),
+                    kv_indices=perm.to(dev))
+    torch.cuda.synchronize()
+    expect = [bits16(t).copy() for t in cpu]
+    ref.commit(expect, prefix_len, node_ids, perm.tolist())
+    for a, b in zip(devs, expect):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
+def test_commit_disjoint_device_positions_without_staging(dev):
+    """Disjoint source and destination sets with staging switched off, over
+    several requests, more items than fit the kernel argument block."""
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(7)
+    layers, pages, ps, h, d = 5, 48, 16, 4, 64
+    cpu = [_rand(gen, (pages, 2, ps, h, d), torch.float16) for _ in range(layers)]
+    perm = torch.randperm(pages, generator=gen).to(torch.int32)
+    indptr = [0, 16, 32, 48]
+    req, src, dst = [], [], []
+    for b in range(3):
+        for i in range(40):
+            req.append(b)
+            src.append(128 + 3 * i)      # positions 128..245 of request b
+            dst.append(2 * i)            # positions 0..78
+    assert not kv.commit_positions_need_staging(src, dst, req)
+    devs = [t.to(dev) for t in cpu]
+    kv.commit_paged(devs, torch.tensor(src, device=dev), torch.tensor(dst, device=dev),
+                    kv_indptr=torch.tensor(indptr, dtype=torch.int32, device=dev), kv_indices=perm.to(dev),
+                    item_req=torch.tensor(req, dtype=torch.int32, device=dev), needs_staging=False)
+    torch.cuda.synchronize()
+    expect = [bits16(t).copy() for t in cpu]
+    for layer in expect:
+        for r, s, t in zip(req, src, dst):
+            pt = perm[indptr[r]: indptr[r + 1]].tolist()
+            layer[pt[t // ps], :, t % ps] = layer[pt[s // ps], :, s % ps]
+    for a, b in zip(devs, expect):
+        np.testing.assert_array_equal(bits16(a), b)
+
+
 def test_append_token_pool_set_kv_buffer(dev):
     kv = pkg("kv_ops")
     gen = torch.Generator().manual_seed(6)

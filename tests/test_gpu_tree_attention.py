@@ -160,6 +160,22 @@ def test_row_blocking_variants(dev, max_rows):
     assert w.current_plan.max_rows <= max(16, max_rows)
 
 
+@pytest.mark.parametrize("n_routes,max_rows", [(2, 32), (6, 96), (9, 144), (10, 160), (11, 176), (16, 256)])
+@pytest.mark.parametrize("split_target", [None, 1])
+def test_row_tile_counts_cover_every_wave_layout(dev, n_routes, max_rows, split_target):
+    """One row block of T = 2, 6, 9, 10, 11, 16 tiles (n_routes disjoint routes
+    of depth 4, four query heads per KV head): leftover tiles split by keys into
+    halves (2, 6, 10) or quarters (9), two tiles per wave (11, 16); with the
+    keys split over work items (partial states merged) and without."""
+    gen = torch.Generator().manual_seed(40 + n_routes)
+    routes = [tuple(int(x) for x in torch.randint(0, 128256, (4,), generator=gen)) for _ in range(n_routes)]
+    c = _build(dev, seed=40 + n_routes, prefix_len=2000, routes=routes, dominant_tree=split_target is None)
+    assert c["n"] * 4 == max_rows
+    w, _, _ = _run_and_check(dev, c, max_rows=max_rows, split_target=split_target)
+    assert w.current_plan.max_rows == max_rows
+    assert (w.current_plan.num_merge > 0) == (split_target is None)
+
+
 def test_forest_16k_unit_scale(dev):
     gen = torch.Generator().manual_seed(4)
     routes = _routes(gen, 9, 4, share=True)
