@@ -554,6 +554,11 @@ __device__ __forceinline__ void issue_tile(const char* head_base, int64_t page_s
   }
 }
 
+// Per-item values every wave needs.
+struct ItemCtx {
+  int t_first, nt, nt_plain, kv_end, col0, qo_start, qo_len, kv_len;
+};
+
 // What one workgroup streams: the split's tiles, their page ids and the LDS
 // ring, plus this wave's loader index (li < 0: the wave issues no loads).
 //
@@ -643,20 +648,39 @@ __device__ __forceinline__ void ring_wait(int k, int ahead, int nt) {
   else wait_vmcnt<0>();
 }
 
-// Prologue: tiles 0, 1, 2 in flight (page windows already loaded).
+// Queries of the item's rows, staged through LDS at kQOffset (stage 3 and the
+// 32 KiB past the ring): row r (local) is 256 bytes at kQOffset + 256 r with
+// its 16-byte granules XOR-swizzled by (r & 15), rows past num_rows repeat the
+// last row.  Loader li issues the 1 KiB blocks (four rows) li, li + NL, ...
+constexpr int kQOffset = 3 * kTile128;
+constexpr int kLdsBytes128 = kStages128 * kTile128 + 32 * 1024;
+
 template <int NL>
-__device__ __forceinline__ void ring_start(Ring<NL>& r) {
-#pragma unroll
-  for (int k = 0; k < 3; ++k) ring_issue<NL>(r, k);
+__device__ __forceinline__ void issue_q(const Ring<NL>& r, const AttnArgs& a, const atlas_attn_work_t& w,
+                                       const ItemCtx& c, int T) {
+  const int gp = r.lane & 15;
+  for (int i = r.li; i < 4 * T; i += NL) {
+    const int row = 4 * i + (r.lane >> 4);
+    const int pr = w.row_start + min(row, w.num_rows - 1);
+    const int node = pr / a.group;
+    const int head = w.kv_head * a.group + (pr - node * a.group);
+    const char* src = a.q + ((int64_t(c.qo_start + node) * a.q_stride_token + int64_t(head) * a.q_stride_head) * 2);
+    dma16(src + ((gp ^ (row & 15)) << 4), r.lds0 + kQOffset + i * 1024);
+  }
 }
 
-// Page windows and the caller's queries (issued just before) land together,
-// then tiles 0..2 are issued.
+// Loader waves: page windows first (waited alone), then tile 0, the queries
+// and tiles 1, 2, so the KV stream starts one round trip after the work item
+// and the queries land with tile 0.
 template <int NL>
-__device__ __forceinline__ void ring_begin(Ring<NL>& r) {
+__device__ __forceinline__ void ring_begin(Ring<NL>& r, const AttnArgs& a, const atlas_attn_work_t& w,
+                                           const ItemCtx& c, int T) {
   ring_load_windows<NL>(r);
   wait_vmcnt<0>();
-  ring_start<NL>(r);
+  ring_issue<NL>(r, 0);
+  if (r.li >= 0 && r.nt > 0) issue_q<NL>(r, a, w, c, T);
+  ring_issue<NL>(r, 1);
+  ring_issue<NL>(r, 2);
 }
 
 // Tile 0 landed (tiles 1 and 2 may be in flight).
@@ -676,8 +700,9 @@ __device__ __forceinline__ void ring_step(Ring<NL>& r, int t) {
 // A wave with no rows: loads its share of the tiles (if it is a loader) and
 // keeps the workgroup's barrier count.
 template <int NL>
-__device__ __forceinline__ void ring_only(Ring<NL>& r) {
-  ring_begin<NL>(r);
+__device__ __forceinline__ void ring_only(Ring<NL>& r, const AttnArgs& a, const atlas_attn_work_t& w,
+                                          const ItemCtx& c, int T) {
+  ring_begin<NL>(r, a, w, c, T);
   if (r.nt > 0) {
     ring_first<NL>(r);
     for (int t = 0; t < r.nt; ++t) ring_step<NL>(r, t);
@@ -831,12 +856,8 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
   }
 }
 
-// Per-item values every wave needs.
-struct ItemCtx {
-  int t_first, nt, nt_plain, kv_end, col0, qo_start, qo_len, kv_len;
-};
-
-// Loads the queries, masks and softmax state of row tiles tile0 + tstride*rt.
+// Row bookkeeping, tree masks and softmax state of row tiles tile0 +
+// tstride*rt (the queries arrive through LDS, see d128_read_q).
 template <bool BF16, int RT>
 __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const AttnArgs& a, const atlas_attn_work_t& w,
                                                const ItemCtx& c, int tile0, int tstride, int lane) {
@@ -856,16 +877,28 @@ __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const Att
     st.l_run[rt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const char* qrow = a.q + ((int64_t(c.qo_start + st.node_of[rt]) * a.q_stride_token +
-                               int64_t(st.head_of[rt]) * a.q_stride_head) * 2);
+    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && st.row_ok[rt]) ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
+    st.climit[rt] = c.kv_len - c.qo_len + st.node_of[rt];
+  }
+}
+
+// Queries of the wave's rows from the LDS staging area into registers (rows
+// past num_rows are zeroed).  Runs right after the first ring step: stage 3
+// is overwritten only after the next barrier.
+template <bool BF16, int RT>
+__device__ __forceinline__ void d128_read_q(RowState<BF16, RT>& st, const char* lds, int lane) {
+  typedef typename Mfma<BF16>::frag frag;
+  const int grp = lane >> 4;
+  const int r16 = lane & 15;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const char* qrow = lds + kQOffset + st.lrow[rt] * 256;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      uint4 v = *reinterpret_cast<const uint4*>(qrow + (ks * 32 + grp * 8) * 2);
+      uint4 v = *reinterpret_cast<const uint4*>(qrow + (((ks * 4 + grp) ^ r16) << 4));
       if (!st.row_ok[rt]) v = uint4{0, 0, 0, 0};
       st.qf[rt][ks] = __builtin_bit_cast(frag, v);
     }
-    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && st.row_ok[rt]) ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
-    st.climit[rt] = c.kv_len - c.qo_len + st.node_of[rt];
   }
 }
 
@@ -881,6 +914,7 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
   const int nt = r.nt;
   if (nt <= 0) return;
   ring_first<NL>(r);
+  d128_read_q<BF16, RT>(st, lds, lane);
   if constexpr (PIPE) {
     f32x4 s_cur[RT][NKT];
     f32x4 s_nxt[RT][NKT];
@@ -1049,17 +1083,17 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
     if (k == 2) {
       RowState<BF16, 2> st;
       d128_load_rows<BF16, 2>(st, a, w, c, wave, 4, lane);
-      ring_begin<4>(r);
+      ring_begin<4>(r, a, w, c, T);
       d128_loop<BF16, 4, 2, 4, false>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 2>(st, a, w, c, lane);
     } else if (k == 1) {
       RowState<BF16, 1> st;
       d128_load_rows<BF16, 1>(st, a, w, c, wave, 4, lane);
-      ring_begin<4>(r);
+      ring_begin<4>(r, a, w, c, T);
       d128_loop<BF16, 4, 1, 4, true>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 1>(st, a, w, c, lane);
     } else {
-      ring_only<4>(r);
+      ring_only<4>(r, a, w, c, T);
     }
     bare_barrier();
     bare_barrier();
@@ -1069,7 +1103,7 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
   RowState<BF16, 1> st;
   if (R == 1) {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k, 0, lane);
-    ring_begin<4>(r);
+    ring_begin<4>(r, a, w, c, T);
     d128_loop<BF16, 4, 1, 1, false>(st, r, a, c, lds, j, lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
@@ -1077,7 +1111,7 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
     d128_part_merge<BF16, 4>(st, lds, 0, j, a, w, c, lane);
   } else {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k + (j >> 1), 0, lane);
-    ring_begin<4>(r);
+    ring_begin<4>(r, a, w, c, T);
     d128_loop<BF16, 4, 1, 2, false>(st, r, a, c, lds, 2 * (j & 1), lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
@@ -1095,17 +1129,17 @@ __device__ __forceinline__ void d128_item_rr(const AttnArgs& a, const atlas_attn
   if (mine == 2) {
     RowState<BF16, 2> st;
     d128_load_rows<BF16, 2>(st, a, w, c, wave, 8, lane);
-    ring_begin<8>(r);
+    ring_begin<8>(r, a, w, c, T);
     d128_loop<BF16, 8, 2, 4, false>(st, r, a, c, lds, 0, lane);
     d128_store_rows<BF16, 2>(st, a, w, c, lane);
   } else if (mine == 1) {
     RowState<BF16, 1> st;
     d128_load_rows<BF16, 1>(st, a, w, c, wave, 8, lane);
-    ring_begin<8>(r);
+    ring_begin<8>(r, a, w, c, T);
     d128_loop<BF16, 8, 1, 4, true>(st, r, a, c, lds, 0, lane);
     d128_store_rows<BF16, 1>(st, a, w, c, lane);
   } else {
-    ring_only<8>(r);
+    ring_only<8>(r, a, w, c, T);
   }
 }
 
@@ -1137,7 +1171,7 @@ __device__ __forceinline__ void ring_init(Ring<NL>& r, const AttnArgs& a, const 
 template <bool BF16>
 __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   constexpr int D = 128;
-  __shared__ __attribute__((aligned(1024))) char lds[kStages128 * kTile128];
+  __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes128];
 
   const atlas_attn_work_t w = a.work[blockIdx.x];
   const int lane = threadIdx.x & 63;
