@@ -1227,14 +1227,16 @@ struct MergeArgs {
   int num_qo_heads;
 };
 
-// One workgroup per packed row.  Thread (split lane sl, chunk c) merges the
-// 16-byte chunk c of the splits sl, sl + 16, ... online: each group of two
-// splits is loaded (partial O and LSE together) and folded into a running
-// maximum, weight sum and accumulator, so a row costs one round of loads.  The
-// per-thread states are then rescaled to the block maximum and summed over
-// the split lanes through LDS.
+// One wave per packed row, four rows per workgroup.  Lane (g, c) folds the
+// 16-byte chunk c of splits g, g + G, g + 2G, ... (G = 64 / (D / 8) split
+// groups) online, four splits per round of independent loads; the groups
+// then combine through cross-lane reductions.  No LDS and no workgroup
+// barriers, so a row costs the merge item load and about one round of
+// partial-state loads.
 constexpr int kMergeThreads = 256;
+constexpr int kMergeRowsPerBlock = kMergeThreads / 64;
 
+// Eight 16-bit values (fp16 or bf16) to floats.
 template <bool BF16>
 __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
   const uint32_t u[4] = {v.x, v.y, v.z, v.w};
@@ -1251,88 +1253,82 @@ __device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
   }
 }
 
+template <int CH>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
+  return wave_max_across_groups(v);
+}
+template <int CH>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (CH <= 8) v += __shfl_xor(v, 8);
+  return wave_sum_across_groups(v);
+}
+
 template <int D, bool BF16>
 __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArgs a) {
   typedef Mfma<BF16> M;
-  constexpr int CHUNKS = D / 8;                       // 16-byte chunks per row
-  constexpr int SPLIT_LANES = kMergeThreads / CHUNKS;  // splits read in parallel
-  __shared__ float red[kMergeThreads / 64];
-  __shared__ float acc_sh[SPLIT_LANES][CHUNKS][9];  // padded against bank conflicts
-  __shared__ float wsum_sh[SPLIT_LANES];
+  constexpr int CH = D / 8;   // 16-byte chunks per row
+  constexpr int G = 64 / CH;  // split groups per wave
+  static_assert(CH == 8 || CH == 16, "head_dim 64 or 128");
   const atlas_attn_merge_t mi = a.merge[blockIdx.x];
-  const int row = blockIdx.y;
+  const int row = blockIdx.y * kMergeRowsPerBlock + (threadIdx.x >> 6);
   if (row >= mi.num_rows) return;
-  const int tid = threadIdx.x;
+  const int lane = threadIdx.x & 63;
+  const int g = lane / CH;
+  const int c = lane % CH;
   const int ns = mi.num_splits;
   const int64_t base = int64_t(mi.partial_row) + row;
-  const int chunk = tid % CHUNKS;
-  const int sl = tid / CHUNKS;
 
-  float m_t = -INFINITY, wsum_t = 0.f;
+  float m_t = -INFINITY, wsum = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = sl; s0 < ns; s0 += 2 * SPLIT_LANES) {
-    const int s1 = s0 + SPLIT_LANES;
-    const int64_t r0 = base + int64_t(s0) * mi.num_rows;
-    const int64_t r1 = base + int64_t(s1 < ns ? s1 : s0) * mi.num_rows;
-    const float l0 = a.part_lse[r0];
-    const float l1 = s1 < ns ? a.part_lse[r1] : -INFINITY;
-    const uint4 raw0 = *reinterpret_cast<const uint4*>(a.part_o + r0 * D + chunk * 8);
-    const uint4 raw1 = *reinterpret_cast<const uint4*>(a.part_o + r1 * D + chunk * 8);
-    const float m_new = fmaxf(m_t, fmaxf(l0, l1));
+  for (int s0 = g; s0 < ns; s0 += 4 * G) {
+    float l[4];
+    uint4 raw[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int sp = s0 + k * G;
+      const int64_t r = base + int64_t(sp < ns ? sp : s0) * mi.num_rows;
+      l[k] = sp < ns ? a.part_lse[r] : -INFINITY;
+      raw[k] = *reinterpret_cast<const uint4*>(a.part_o + r * D + c * 8);
+    }
+    const float m_new = fmaxf(fmaxf(m_t, fmaxf(l[0], l[1])), fmaxf(l[2], l[3]));
     if (m_new == -INFINITY) continue;
     const float sc = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_t - m_new);
-    const float w0 = l0 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l0 - m_new);
-    const float w1 = l1 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l1 - m_new);
-    float v0[8], v1[8];
-    unpack8<BF16>(raw0, v0);
-    unpack8<BF16>(raw1, v1);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] = acc[i] * sc + w0 * v0[i] + w1 * v1[i];
-    wsum_t = wsum_t * sc + w0 + w1;
+    for (int i = 0; i < 8; ++i) acc[i] *= sc;
+    wsum *= sc;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const float wk = l[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l[k] - m_new);
+      float v[8];
+      unpack8<BF16>(raw[k], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
+      wsum += wk;
+    }
     m_t = m_new;
   }
-  // block maximum of the per-thread maxima
-  float mx = wave_max_across_groups(m_t);
-  mx = fmaxf(mx, __shfl_xor(mx, 8));
-  mx = fmaxf(mx, __shfl_xor(mx, 4));
-  mx = fmaxf(mx, __shfl_xor(mx, 2));
-  mx = fmaxf(mx, __shfl_xor(mx, 1));
-  if ((tid & 63) == 0) red[tid >> 6] = mx;
-  __syncthreads();
-  mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float mx = group_max<CH>(m_t);
   const float f = (m_t == -INFINITY || mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_t - mx);
+  wsum = group_sum<CH>(wsum * f);
 #pragma unroll
-  for (int i = 0; i < 8; ++i) acc_sh[sl][chunk][i] = acc[i] * f;
-  if (chunk == 0) wsum_sh[sl] = wsum_t * f;
-  __syncthreads();
-  if (tid < CHUNKS) {
-    float tot[8];
-    float wsum = 0.f;
+  for (int i = 0; i < 8; ++i) acc[i] = group_sum<CH>(acc[i] * f);
+  if (g != 0) return;
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const int prow_q = mi.row_start + row;
+  const int node = prow_q / a.group;
+  const int head = mi.kv_head * a.group + (prow_q - node * a.group);
+  const int qo_start = a.qo_indptr[mi.req];
+  char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
+  uint32_t pk[4];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) tot[i] = 0.f;
-#pragma unroll
-    for (int k = 0; k < SPLIT_LANES; ++k) {
-      wsum += wsum_sh[k];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) tot[i] += acc_sh[k][tid][i];
-    }
-    const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-    const int prow_q = mi.row_start + row;
-    const int node = prow_q / a.group;
-    const int head = mi.kv_head * a.group + (prow_q - node * a.group);
-    const int qo_start = a.qo_indptr[mi.req];
-    char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
-    uint32_t pk[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      pk[i] = uint32_t(M::from_float(tot[2 * i] * inv)) | (uint32_t(M::from_float(tot[2 * i + 1] * inv)) << 16);
-    // 8-byte stores: output rows are only required to be 8-byte aligned.
-    *reinterpret_cast<uint2*>(orow + tid * 16) = uint2{pk[0], pk[1]};
-    *reinterpret_cast<uint2*>(orow + tid * 16 + 8) = uint2{pk[2], pk[3]};
-    if (tid == 0 && a.lse != nullptr)
-      a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] =
-          wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
-  }
+  for (int i = 0; i < 4; ++i)
+    pk[i] = uint32_t(M::from_float(acc[2 * i] * inv)) | (uint32_t(M::from_float(acc[2 * i + 1] * inv)) << 16);
+  // 8-byte stores: output rows are only required to be 8-byte aligned.
+  *reinterpret_cast<uint2*>(orow + c * 16) = uint2{pk[0], pk[1]};
+  *reinterpret_cast<uint2*>(orow + c * 16 + 8) = uint2{pk[2], pk[3]};
+  if (c == 0 && a.lse != nullptr)
+    a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] = wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
 }
 
 // Work-shape choice: the fewest (compute waves x row tiles) slots that cover
@@ -1406,7 +1402,7 @@ int launch_attn(const AttnArgs& args, int num_work, int row_tiles, const MergeAr
   if ((rc = launch_status("tree_attn_kernel"))) return rc;
 merge:
   if (num_merge > 0) {
-    const dim3 grid(num_merge, max_rows);
+    const dim3 grid(num_merge, (max_rows + kMergeRowsPerBlock - 1) / kMergeRowsPerBlock);
     hipLaunchKernelGGL((tree_attn_merge_kernel<D, BF16>), grid, dim3(kMergeThreads), 0, stream, margs);
     if ((rc = launch_status("tree_attn_merge_kernel"))) return rc;
   }
