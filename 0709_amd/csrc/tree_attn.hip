@@ -128,6 +128,34 @@ struct Mfma<true> {
   }
 };
 
+// Visibility of the four keys p0 .. p0+3 a lane holds in one 16-key block
+// (bit i for key p0 + i), branch-free: keys at or past kv_end are hidden; in
+// tree mode keys below col0 (the prefix) are visible and key p >= col0 follows
+// bit p - col0 of the row's ancestor word; in causal mode keys up to climit.
+template <int MODE>
+__device__ __forceinline__ uint32_t key_bits4(uint64_t tbits, int climit, int p0, int col0, int kv_end) {
+  const int nlen = min(max(kv_end - p0, 0), 4);
+  uint32_t vis = (1u << nlen) - 1u;
+  if constexpr (MODE == ATLAS_MASK_TREE) {
+    const int off = p0 - col0;
+    const uint32_t up = off < 64 ? uint32_t(tbits >> (off & 63)) : 0u;  // off >= 0: bits off .. off+3
+    const int k = min(max(-off, 0), 4);                                   // off < 0: k keys of the prefix
+    const uint32_t down = uint32_t(tbits << (k & 63)) | ((1u << k) - 1u);
+    vis &= (off >= 0 ? up : down) & 15u;
+  } else if constexpr (MODE == ATLAS_MASK_CAUSAL) {
+    const int nc = min(max(climit - p0 + 1, 0), 4);
+    vis &= (1u << nc) - 1u;
+  }
+  return vis;
+}
+// Runtime mode without branches: every variant is computed and selected.
+__device__ __forceinline__ uint32_t key_bits4(int mode, uint64_t tbits, int climit, int p0, int col0, int kv_end) {
+  const uint32_t tree = key_bits4<ATLAS_MASK_TREE>(tbits, climit, p0, col0, kv_end);
+  const uint32_t causal = key_bits4<ATLAS_MASK_CAUSAL>(tbits, climit, p0, col0, kv_end);
+  const uint32_t none = key_bits4<ATLAS_MASK_NONE>(tbits, climit, p0, col0, kv_end);
+  return mode == ATLAS_MASK_TREE ? tree : (mode == ATLAS_MASK_CAUSAL ? causal : none);
+}
+
 // Position inside a 32-key block of V^T at which key k (0..31) is stored.  The
 // B operand of the P.V MFMA is built from two score tiles: lane group g holds
 // keys 4g..4g+3 of the first tile and 16+4g..16+4g+3 of the second as its
@@ -385,18 +413,9 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
       if (need_mask) {
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
+          const uint32_t vis = key_bits4(a.mask_mode, tbits[rt], climit[rt], t0 + kt * 16 + grp * 4, col0, kv_end);
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int p = t0 + kt * 16 + grp * 4 + i;
-            bool vis = p < kv_end;
-            if (a.mask_mode == ATLAS_MASK_TREE) {
-              const int b = p - col0;
-              vis = vis && (p < col0 || (b < 64 && ((tbits[rt] >> (b & 63)) & 1ull)));
-            } else if (a.mask_mode == ATLAS_MASK_CAUSAL) {
-              vis = vis && p <= climit[rt];
-            }
-            s[rt][kt][i] = vis ? s[rt][kt][i] : -INFINITY;
-          }
+          for (int i = 0; i < 4; ++i) s[rt][kt][i] = ((vis >> i) & 1u) ? s[rt][kt][i] : -INFINITY;
         }
       }
       float mx = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
@@ -754,8 +773,10 @@ __device__ __forceinline__ void d128_scores(const RowState<BF16, RT>& st, const 
 // with V^T from transposing LDS reads.  The running maximum moves only when a
 // row's maximum grew by more than kRescaleLog2 (P stays below 2^kRescaleLog2),
 // so the rescale of O and l is skipped for the whole wave on most tiles.
-// MASKED tiles apply the tree / causal / length mask.
-template <bool BF16, int RT, int NKT, bool MASKED>
+// kMasked tiles apply the tree / causal / length mask; kPlain tiles none.
+constexpr int kPlain = 0;
+constexpr int kMasked = 1;
+template <bool BF16, int RT, int NKT, int MODE>
 __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][NKT], const char* sb, int kb0,
                                                 int t0, int kv_end, int col0, int mask_mode, float scale_log2,
                                                 int grp, int r16) {
@@ -764,22 +785,13 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
   uint32_t pk[RT][NKT][2];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    if constexpr (MASKED) {
+    if constexpr (MODE != kPlain) {
 #pragma unroll
       for (int j = 0; j < NKT; ++j) {
+        const uint32_t vis = key_bits4(mask_mode, st.tbits[rt], st.climit[rt], t0 + (kb0 + j) * 16 + grp * 4, col0,
+                                       kv_end);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int p = t0 + (kb0 + j) * 16 + grp * 4 + i;
-          bool vis = p < kv_end;
-          if (mask_mode == ATLAS_MASK_TREE) {
-            const int b = p - col0;
-            const bool bit = ((st.tbits[rt] >> (b & 63)) & 1ull) != 0;
-            vis = vis & ((p < col0) | ((b < 64) & bit));
-          } else if (mask_mode == ATLAS_MASK_CAUSAL) {
-            vis = vis & (p <= st.climit[rt]);
-          }
-          s[rt][j][i] = vis ? s[rt][j][i] : -INFINITY;
-        }
+        for (int i = 0; i < 4; ++i) s[rt][j][i] = ((vis >> i) & 1u) ? s[rt][j][i] : -INFINITY;
       }
     }
     float mx = -INFINITY;
@@ -925,7 +937,7 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     for (; t < plain_end; ++t) {
       ring_step<NL>(r, t);
       d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, NKT, false>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+      d128_softmax_pv<BF16, RT, NKT, kPlain>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
                                             c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
                                             grp, r16);
 #pragma unroll
@@ -936,7 +948,7 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     for (; t < n_pipe; ++t) {
       ring_step<NL>(r, t);
       d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, NKT, true>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
                                            c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
                                            grp, r16);
 #pragma unroll
@@ -946,11 +958,11 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     }
     ring_step<NL>(r, t);
     if (t < c.nt_plain)
-      d128_softmax_pv<BF16, RT, NKT, false>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+      d128_softmax_pv<BF16, RT, NKT, kPlain>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
                                             c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
                                             grp, r16);
     else
-      d128_softmax_pv<BF16, RT, NKT, true>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
+      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
                                            c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
                                            grp, r16);
   } else {
@@ -959,14 +971,14 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     for (; t < c.nt_plain; ++t) {
       const char* sb = lds + (t % kStages128) * kTile128;
       d128_scores<BF16, RT, NKT>(st, sb, kb0, grp, r16, s);
-      d128_softmax_pv<BF16, RT, NKT, false>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
+      d128_softmax_pv<BF16, RT, NKT, kPlain>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
                                             a.mask_mode, a.scale_log2, grp, r16);
       ring_step<NL>(r, t);
     }
     for (; t < nt; ++t) {
       const char* sb = lds + (t % kStages128) * kTile128;
       d128_scores<BF16, RT, NKT>(st, sb, kb0, grp, r16, s);
-      d128_softmax_pv<BF16, RT, NKT, true>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
+      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
                                            a.mask_mode, a.scale_log2, grp, r16);
       ring_step<NL>(r, t);
     }

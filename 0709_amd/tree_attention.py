@@ -63,7 +63,7 @@ class AttentionPlan:
     partial_rows: int
     kv_lens: list[int]
     qo_lens: list[int]
-    tiles_per_split: int
+    tiles_per_split: int  # most key tiles any work item streams
 
     def device_view(self, offset: int) -> int:
         return int(self.meta.data_ptr()) + 4 * offset
@@ -260,10 +260,12 @@ class BatchPrefillWithPagedKVCacheWrapper:
         row_block = max(16, min(MAX_ROWS_PER_ITEM if direct else MAX_ROWS_PER_ITEM_OTHER, row_block))
         split_target = self.split_target_items
         if split_target is None:
-            # One 8-wave workgroup per CU for the head_dim-128 kernel; a batch of
-            # unequal requests gets two items per CU, dispatched longest first.
-            per_cu = 1 if (direct and batch == 1) else 2
-            split_target = per_cu * DEFAULT_CU_COUNT
+            # One 8-wave workgroup per CU for the head_dim-128 kernel, leaving a
+            # sixteenth of the CUs free (the previous launch's tail still holds
+            # some; measured 27.2-27.4 us/layer at 232-240 items against 28.3 at
+            # 256 on the forest headline); a batch of unequal requests gets two
+            # items per CU, dispatched longest first.
+            split_target = DEFAULT_CU_COUNT * 15 // 16 if (direct and batch == 1) else 2 * DEFAULT_CU_COUNT
         blocks = []  # (req, row_start, num_rows)
         for b in range(batch):
             rows = qo_lens[b] * group
@@ -275,19 +277,25 @@ class BatchPrefillWithPagedKVCacheWrapper:
             if rows == 0:
                 blocks.append((b, 0, 0))
         unit_tiles = sum(hkv * math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks)
-        tiles_per_split = max(self.min_tiles_per_split, math.ceil(unit_tiles / max(1, split_target)))
+        # Tiles per split as a fraction, so the split count per request rounds
+        # down and the items do not exceed the target (one per CU when a single
+        # request fills the device).
+        tiles_per_split = max(float(self.min_tiles_per_split), unit_tiles / max(1, split_target))
         # the merge kernel combines at most MAX_SPLITS states per row
         max_tiles = max((math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks), default=0)
-        tiles_per_split = max(tiles_per_split, math.ceil(max_tiles / MAX_SPLITS))
+        tiles_per_split = max(tiles_per_split, max_tiles / MAX_SPLITS)
         ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
         while True:
             work, merge = [], []
             partial_rows = 0
             for (b, r0, nr) in blocks:
                 tiles = math.ceil(kv_lens[b] / TILE_KEYS)
-                splits = max(1, math.ceil(tiles / tiles_per_split))
-                # balanced splits of the request's tiles
-                per = math.ceil(tiles / splits) if tiles else 0
+                splits = max(1, min(tiles, int(tiles / tiles_per_split + 1e-9)))
+                # balanced splits of the request's tiles: `per` tiles each, one
+                # more for the last `extra` splits (the last one holds the
+                # request's partial tail tile)
+                per = tiles // splits if tiles else 0
+                extra = tiles - per * splits
                 # request values every item repeats (qo_start, qo_len, kv_len,
                 # mask column start, page offset) and padding to 16 ints
                 req_vals = (qo[b], qo_lens[b], kv_lens[b], cols[b], kvp[b], 0, 0, 0, 0)
@@ -297,8 +305,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
                         continue
                     base = partial_rows
                     for s in range(splits):
-                        k0 = s * per * TILE_KEYS
-                        k1 = min(kv_lens[b], (s + 1) * per * TILE_KEYS)
+                        t0 = s * per + max(0, s - (splits - extra))
+                        t1 = t0 + per + (1 if s >= splits - extra else 0)
+                        k0 = t0 * TILE_KEYS
+                        k1 = min(kv_lens[b], t1 * TILE_KEYS)
                         work.append((b, h, r0, nr, k0, k1, base + s * nr) + req_vals)
                     merge.append((b, h, r0, nr, base, splits, 0, 0))
                     partial_rows += splits * nr
@@ -307,8 +317,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
             tiles_per_split *= 2
         max_rows = max((nr for (_, _, nr) in blocks), default=1)
         # Largest items first: workgroups are dispatched in order, so the
-        # long ones start early and the short ones fill in behind them.
-        work.sort(key=lambda it: -(it[5] - it[4]))
+        # long ones start early and the short ones fill in behind them.  Equal
+        # items cycle through the KV heads, so with workgroups spread over the
+        # 8 XCDs round-robin each KV head's splits share one XCD's L2 (and
+        # their queries) when there are 8 KV heads.
+        work.sort(key=lambda it: (-(it[5] - it[4]), it[0], it[2], it[4], it[1]))
 
         meta_vals: list[int] = []
         for item in work:
@@ -348,7 +361,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             qo_indptr=meta[qo_off:], kv_indptr=meta[kvp_off:], kv_indices=indices,
             tree_mask=bits_buf, meta=meta, num_work=len(work), num_merge=len(merge), work_offset=0,
             merge_offset=merge_off, kv_len_offset=kvlen_off, col_offset=col_off, max_rows=max_rows,
-            partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=tiles_per_split,
+            partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens,
+            tiles_per_split=max((math.ceil((it[5] - it[4]) / TILE_KEYS) for it in work), default=0),
         )
 
     def _persistent(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:
