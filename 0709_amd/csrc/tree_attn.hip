@@ -164,16 +164,35 @@ __device__ __forceinline__ int vt_position(int k) {
   return ((k & 15) >> 2) * 8 + ((k >> 4) << 2) + (k & 3);
 }
 
+// Maxima of scores.  The IEEE maximum builtins map to v_maximum(3)_f32, which
+// need no canonicalised operands (fmaxf makes the compiler quieten every MFMA
+// result with an extra v_max_f32 first).  Scores are never NaN: masked keys
+// are -inf, which every finite score exceeds.
+__device__ __forceinline__ float max2f(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+__device__ __forceinline__ float max3f(float a, float b, float c) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(a, b), c);
+}
+// Maximum over the N scores of a lane: one three-input maximum per two values.
+template <int N>
+__device__ __forceinline__ float lane_max(const float (&v)[N]) {
+  static_assert(N >= 2, "at least two values");
+  float m = max2f(v[0], v[1]);
+#pragma unroll
+  for (int i = 2; i + 1 < N; i += 2) m = max3f(m, v[i], v[i + 1]);
+  if constexpr (N % 2 == 1) m = max2f(m, v[N - 1]);
+  return m;
+}
+
 // Reductions across the four 16-lane rows of a wave (lanes l, l^16, l^32,
 // l^48) with the gfx950 row-swap permutes: swapping a register with itself
 // yields each lane's value and its partner's, so no selection is needed.
 __device__ __forceinline__ float xor32_max(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor16_max(float v) {
   const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  return max2f(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 __device__ __forceinline__ float xor32_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
@@ -418,11 +437,12 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
           for (int i = 0; i < 4; ++i) s[rt][kt][i] = ((vis >> i) & 1u) ? s[rt][kt][i] : -INFINITY;
         }
       }
-      float mx = fmaxf(fmaxf(fmaxf(s[rt][0][0], s[rt][0][1]), fmaxf(s[rt][0][2], s[rt][0][3])),
-                       fmaxf(fmaxf(s[rt][1][0], s[rt][1][1]), fmaxf(s[rt][1][2], s[rt][1][3])));
-      mx = fmaxf(mx, fmaxf(fmaxf(fmaxf(s[rt][2][0], s[rt][2][1]), fmaxf(s[rt][2][2], s[rt][2][3])),
-                           fmaxf(fmaxf(s[rt][3][0], s[rt][3][1]), fmaxf(s[rt][3][2], s[rt][3][3]))));
-      mx = wave_max_across_groups(mx) * a.scale_log2;
+      float sv[16];
+#pragma unroll
+      for (int kt = 0; kt < 4; ++kt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[4 * kt + i] = s[rt][kt][i];
+      const float mx = wave_max_across_groups(lane_max<16>(sv)) * a.scale_log2;
       // Lazy rescale: keep the running reference max until a row's max grows
       // by more than kRescaleLog2 (P stays below 2^kRescaleLog2), so most
       // tiles skip the O rescale.
@@ -622,7 +642,9 @@ __device__ __forceinline__ void ring_load_windows(Ring<NL>& r) {
 // t+3 into the stage tile t-1 used.  Waves that pipeline the next tile's
 // scores compute tile t after step t (reading tiles t and t+1); the others
 // compute tile t before step t.  Either way every wave is past its last read
-// of tile t-1 at step t's barrier.
+// of tile t-1 at step t's barrier.  (Issuing a third tile ahead, where no wave
+// pipelines, measured slower: the extra loads in flight congest the paged
+// stream.)
 constexpr int kStages128 = 4;
 
 template <int NL>
@@ -794,11 +816,12 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
         for (int i = 0; i < 4; ++i) s[rt][j][i] = ((vis >> i) & 1u) ? s[rt][j][i] : -INFINITY;
       }
     }
-    float mx = -INFINITY;
+    float sv[4 * NKT];
 #pragma unroll
     for (int j = 0; j < NKT; ++j)
-      mx = fmaxf(mx, fmaxf(fmaxf(s[rt][j][0], s[rt][j][1]), fmaxf(s[rt][j][2], s[rt][j][3])));
-    mx = wave_max_across_groups(mx) * scale_log2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sv[4 * j + i] = s[rt][j][i];
+    float mx = wave_max_across_groups(lane_max<4 * NKT>(sv)) * scale_log2;
     const bool grow = mx > st.m_run[rt] + kRescaleLog2;
     if (__builtin_amdgcn_ballot_w64(grow) != 0) {
       const float m_new = grow ? mx : st.m_run[rt];
@@ -1083,29 +1106,30 @@ __device__ __forceinline__ void d128_part_merge(const RowState<BF16, 1>& st, con
 // Row tiles of an item whose count T = 4k + R with k <= 2 and R in {1, 2}:
 // waves 0..3 (one per SIMD) own whole tiles w and w + 4 (k per wave); the R
 // leftover tiles are split by keys over waves 4..7 (R = 1: four 16-key
-// quarters of every tile; R = 2: two 32-key halves per tile), which also
-// issue all the KV loads.  Every SIMD then carries k + R/4 tile-units instead
-// of the k + 1 (or more) of one tile per wave.
-template <bool BF16>
+// quarters of every tile; R = 2: two 32-key halves per tile).  Every SIMD
+// then carries k + R/4 tile-units instead of the k + 1 (or more) of one tile
+// per wave.  All eight waves issue KV loads: with four loaders the paged
+// stream alone runs at two thirds of the eight-loader rate.
+template <bool BF16, int NL>
 __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c,
-                                                char* lds, Ring<4>& r, int T, int wave, int lane) {
+                                                char* lds, Ring<NL>& r, int T, int wave, int lane) {
   const int R = T & 3;
   const int k = T >> 2;
   if (wave < 4) {
     if (k == 2) {
       RowState<BF16, 2> st;
       d128_load_rows<BF16, 2>(st, a, w, c, wave, 4, lane);
-      ring_begin<4>(r, a, w, c, T);
-      d128_loop<BF16, 4, 2, 4, false>(st, r, a, c, lds, 0, lane);
+      ring_begin<NL>(r, a, w, c, T);
+      d128_loop<BF16, NL, 2, 4, false>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 2>(st, a, w, c, lane);
     } else if (k == 1) {
       RowState<BF16, 1> st;
       d128_load_rows<BF16, 1>(st, a, w, c, wave, 4, lane);
-      ring_begin<4>(r, a, w, c, T);
-      d128_loop<BF16, 4, 1, 4, true>(st, r, a, c, lds, 0, lane);
+      ring_begin<NL>(r, a, w, c, T);
+      d128_loop<BF16, NL, 1, 4, true>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 1>(st, a, w, c, lane);
     } else {
-      ring_only<4>(r, a, w, c, T);
+      ring_only<NL>(r, a, w, c, T);
     }
     bare_barrier();
     bare_barrier();
@@ -1115,16 +1139,16 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
   RowState<BF16, 1> st;
   if (R == 1) {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k, 0, lane);
-    ring_begin<4>(r, a, w, c, T);
-    d128_loop<BF16, 4, 1, 1, false>(st, r, a, c, lds, j, lane);
+    ring_begin<NL>(r, a, w, c, T);
+    d128_loop<BF16, NL, 1, 1, false>(st, r, a, c, lds, j, lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
     bare_barrier();
     d128_part_merge<BF16, 4>(st, lds, 0, j, a, w, c, lane);
   } else {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k + (j >> 1), 0, lane);
-    ring_begin<4>(r, a, w, c, T);
-    d128_loop<BF16, 4, 1, 2, false>(st, r, a, c, lds, 2 * (j & 1), lane);
+    ring_begin<NL>(r, a, w, c, T);
+    d128_loop<BF16, NL, 1, 2, false>(st, r, a, c, lds, 2 * (j & 1), lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
     bare_barrier();
@@ -1216,9 +1240,9 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   const int T = __builtin_amdgcn_readfirstlane((w.num_rows + 15) / 16);
   const int R = T & 3;
   if (T <= 10 && (R == 1 || R == 2)) {
-    Ring<4> r;
-    ring_init<4>(r, a, head_base, pages, c, last_key, wave >= 4 ? wave - 4 : -1, lane, lds0);
-    d128_item_split<BF16>(a, w, c, lds, r, T, wave, lane);
+    Ring<8> r;
+    ring_init<8>(r, a, head_base, pages, c, last_key, wave, lane, lds0);
+    d128_item_split<BF16, 8>(a, w, c, lds, r, T, wave, lane);
   } else {
     Ring<8> r;
     ring_init<8>(r, a, head_base, pages, c, last_key, wave, lane, lds0);

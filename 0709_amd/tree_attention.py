@@ -292,8 +292,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 tiles = math.ceil(kv_lens[b] / TILE_KEYS)
                 splits = max(1, min(tiles, int(tiles / tiles_per_split + 1e-9)))
                 # balanced splits of the request's tiles: `per` tiles each, one
-                # more for the last `extra` splits (the last one holds the
-                # request's partial tail tile)
+                # more for the first `extra` splits, so the last split, which
+                # holds the request's masked tail tile (the costliest to
+                # compute), has one tile less
                 per = tiles // splits if tiles else 0
                 extra = tiles - per * splits
                 # request values every item repeats (qo_start, qo_len, kv_len,
@@ -305,8 +306,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                         continue
                     base = partial_rows
                     for s in range(splits):
-                        t0 = s * per + max(0, s - (splits - extra))
-                        t1 = t0 + per + (1 if s >= splits - extra else 0)
+                        t0 = s * per + min(s, extra)
+                        t1 = t0 + per + (1 if s < extra else 0)
                         k0 = t0 * TILE_KEYS
                         k1 = min(kv_lens[b], t1 * TILE_KEYS)
                         work.append((b, h, r0, nr, k0, k1, base + s * nr) + req_vals)
