@@ -56,6 +56,7 @@ struct AttnArgs {
   const uint64_t* tree_mask;
   const int32_t* mask_col_start;
   const atlas_attn_work_t* work;
+  const int32_t* page_window;  // per-item first page-id windows (64 ids), or null
   char* out;
   int64_t out_stride_token;  // elements
   int64_t out_stride_head;   // elements
@@ -596,6 +597,7 @@ __device__ __forceinline__ void issue_tile(const char* head_base, int64_t page_s
 // Per-item values every wave needs.
 struct ItemCtx {
   int t_first, nt, nt_plain, kv_end, col0, qo_start, qo_len, kv_len;
+  int win0;  // this lane's id of the item's first page-id window (plan-provided)
 };
 
 // What one workgroup streams: the split's tiles, their page ids and the LDS
@@ -628,12 +630,15 @@ __device__ __forceinline__ int window_ids(const Ring<NL>& r, int w) {
 
 // Vector loads of the first two page windows (loader waves); the caller waits
 // for them together with the queries before the first tile is issued.
+// win0: the item's first window when the plan provides it (loaded at
+// workgroup start, before the work item arrived), else -1 (lane 0 decides).
+// The second window is needed only by splits of more than 64 pages.
 template <int NL>
-__device__ __forceinline__ void ring_load_windows(Ring<NL>& r) {
+__device__ __forceinline__ void ring_load_windows(Ring<NL>& r, bool have_win0, int win0) {
   r.win = 0;
   if (r.li >= 0 && r.nt > 0) {
-    r.win_cur = window_ids<NL>(r, 0);
-    r.win_nxt = window_ids<NL>(r, 1);
+    r.win_cur = have_win0 ? win0 : window_ids<NL>(r, 0);
+    if (r.last_page - r.page0 >= 64) r.win_nxt = window_ids<NL>(r, 1);
   }
 }
 
@@ -712,11 +717,12 @@ __device__ __forceinline__ void issue_q(const Ring<NL>& r, const AttnArgs& a, co
 
 // Loader waves: page windows first (waited alone), then tile 0, the queries
 // and tiles 1, 2, so the KV stream starts one round trip after the work item
-// and the queries land with tile 0.
+// and the queries land with tile 0.  (Issuing the queries ahead of the page
+// window wait measured slower: they delay tile 0.)
 template <int NL>
 __device__ __forceinline__ void ring_begin(Ring<NL>& r, const AttnArgs& a, const atlas_attn_work_t& w,
                                            const ItemCtx& c, int T) {
-  ring_load_windows<NL>(r);
+  ring_load_windows<NL>(r, a.page_window != nullptr, c.win0);
   wait_vmcnt<0>();
   ring_issue<NL>(r, 0);
   if (r.li >= 0 && r.nt > 0) issue_q<NL>(r, a, w, c, T);
@@ -792,19 +798,21 @@ __device__ __forceinline__ void d128_scores(const RowState<BF16, RT>& st, const 
 }
 
 // Online softmax of the scores of blocks kb0 .. kb0+NKT-1 and O^T += V^T P^T
-// with V^T from transposing LDS reads.  The running maximum moves only when a
-// row's maximum grew by more than kRescaleLog2 (P stays below 2^kRescaleLog2),
-// so the rescale of O and l is skipped for the whole wave on most tiles.
-// kMasked tiles apply the tree / causal / length mask; kPlain tiles none.
+// with V^T from transposing LDS reads, in three phases so that a pipelining
+// wave can place the next tile's score MFMAs between them:
+//   d128_rowmax  mask (kMasked tiles), row maxima and the lazy rescale: the
+//                running maximum moves only when a row's maximum grew by more
+//                than kRescaleLog2 (P stays below 2^kRescaleLog2), so the
+//                rescale of O and l, a branch, is skipped on most tiles;
+//   d128_exp     P = exp2(s * scale - m), packed to 16 bits, row sums;
+//   d128_pv      O^T += V^T P^T.
+// d128_exp and d128_pv contain no branches: placed after d128_rowmax they
+// form one basic block with whatever MFMAs the caller puts beside them.
 constexpr int kPlain = 0;
 constexpr int kMasked = 1;
 template <bool BF16, int RT, int NKT, int MODE>
-__device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][NKT], const char* sb, int kb0,
-                                                int t0, int kv_end, int col0, int mask_mode, float scale_log2,
-                                                int grp, int r16) {
-  typedef Mfma<BF16> M;
-  typedef typename M::frag frag;
-  uint32_t pk[RT][NKT][2];
+__device__ __forceinline__ void d128_rowmax(RowState<BF16, RT>& st, f32x4 (&s)[RT][NKT], int kb0, int t0,
+                                            int kv_end, int col0, int mask_mode, float scale_log2, int grp) {
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
     if constexpr (MODE != kPlain) {
@@ -832,6 +840,15 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
       for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] *= alpha;
       st.m_run[rt] = m_new;
     }
+  }
+}
+
+template <bool BF16, int RT, int NKT>
+__device__ __forceinline__ void d128_exp(RowState<BF16, RT>& st, const f32x4 (&s)[RT][NKT], float scale_log2,
+                                         uint32_t (&pk)[RT][NKT][2]) {
+  typedef Mfma<BF16> M;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
     const float neg_m = st.m_run[rt] == -INFINITY ? 0.f : -st.m_run[rt];
 #pragma unroll
     for (int j = 0; j < NKT; ++j) {
@@ -844,7 +861,13 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
       st.l_run[rt] = M::sum2(pk[rt][j][1], M::sum2(pk[rt][j][0], st.l_run[rt]));
     }
   }
+}
 
+template <bool BF16, int RT, int NKT>
+__device__ __forceinline__ void d128_pv(RowState<BF16, RT>& st, const uint32_t (&pk)[RT][NKT][2], const char* sb,
+                                        int kb0, int grp, int r16) {
+  typedef Mfma<BF16> M;
+  typedef typename M::frag frag;
   const int e = r16 >> 2;
   const int q = r16 & 3;
   const char* vb = sb + kHalf128;
@@ -891,6 +914,31 @@ __device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&
   }
 }
 
+template <bool BF16, int RT, int NKT, int MODE>
+__device__ __forceinline__ void d128_softmax_pv(RowState<BF16, RT>& st, f32x4 (&s)[RT][NKT], const char* sb, int kb0,
+                                                int t0, int kv_end, int col0, int mask_mode, float scale_log2,
+                                                int grp, int r16) {
+  uint32_t pk[RT][NKT][2];
+  d128_rowmax<BF16, RT, NKT, MODE>(st, s, kb0, t0, kv_end, col0, mask_mode, scale_log2, grp);
+  d128_exp<BF16, RT, NKT>(st, s, scale_log2, pk);
+  d128_pv<BF16, RT, NKT>(st, pk, sb, kb0, grp, r16);
+}
+
+// One pipelined step: the softmax of tile t (scores s_cur, stage sb) with the
+// score MFMAs of tile t+1 (stage sb_next) between its exp and its P.V, all in
+// one basic block after the row maxima.
+template <bool BF16, int RT, int NKT, int MODE>
+__device__ __forceinline__ void d128_pipe_step(RowState<BF16, RT>& st, f32x4 (&s_cur)[RT][NKT],
+                                               f32x4 (&s_nxt)[RT][NKT], const char* sb, const char* sb_next, int kb0,
+                                               int t0, int kv_end, int col0, int mask_mode, float scale_log2,
+                                               int grp, int r16) {
+  uint32_t pk[RT][NKT][2];
+  d128_rowmax<BF16, RT, NKT, MODE>(st, s_cur, kb0, t0, kv_end, col0, mask_mode, scale_log2, grp);
+  d128_exp<BF16, RT, NKT>(st, s_cur, scale_log2, pk);
+  d128_scores<BF16, RT, NKT>(st, sb_next, kb0, grp, r16, s_nxt);
+  d128_pv<BF16, RT, NKT>(st, pk, sb, kb0, grp, r16);
+}
+
 // Row bookkeeping, tree masks and softmax state of row tiles tile0 +
 // tstride*rt (the queries arrive through LDS, see d128_read_q).
 template <bool BF16, int RT>
@@ -912,9 +960,20 @@ __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const Att
     st.l_run[rt] = 0.f;
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    st.tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && st.row_ok[rt]) ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
+    st.tbits[rt] = 0ull;
     st.climit[rt] = c.kv_len - c.qo_len + st.node_of[rt];
   }
+}
+
+// The rows' tree ancestor words.  Loaded after the ring's first tiles are
+// issued: they are needed only by the masked tiles at the end of a split, and
+// loading them before would put a round trip ahead of the first KV tile.
+template <bool BF16, int RT>
+__device__ __forceinline__ void d128_load_masks(RowState<BF16, RT>& st, const AttnArgs& a, const ItemCtx& c) {
+  if (a.mask_mode != ATLAS_MASK_TREE) return;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    st.tbits[rt] = st.row_ok[rt] ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
 }
 
 // Queries of the wave's rows from the LDS staging area into registers (rows
@@ -959,10 +1018,9 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     int t = 0;
     for (; t < plain_end; ++t) {
       ring_step<NL>(r, t);
-      d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, NKT, kPlain>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
-                                            c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
-                                            grp, r16);
+      d128_pipe_step<BF16, RT, NKT, kPlain>(st, s_cur, s_nxt, lds + (t % kStages128) * kTile128,
+                                            lds + ((t + 1) % kStages128) * kTile128, kb0, c.t_first + t * kTileKeys,
+                                            c.kv_end, c.col0, a.mask_mode, a.scale_log2, grp, r16);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -970,10 +1028,9 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     }
     for (; t < n_pipe; ++t) {
       ring_step<NL>(r, t);
-      d128_scores<BF16, RT, NKT>(st, lds + ((t + 1) % kStages128) * kTile128, kb0, grp, r16, s_nxt);
-      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
-                                           c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
-                                           grp, r16);
+      d128_pipe_step<BF16, RT, NKT, kMasked>(st, s_cur, s_nxt, lds + (t % kStages128) * kTile128,
+                                             lds + ((t + 1) % kStages128) * kTile128, kb0, c.t_first + t * kTileKeys,
+                                             c.kv_end, c.col0, a.mask_mode, a.scale_log2, grp, r16);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -1120,12 +1177,14 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
       RowState<BF16, 2> st;
       d128_load_rows<BF16, 2>(st, a, w, c, wave, 4, lane);
       ring_begin<NL>(r, a, w, c, T);
-      d128_loop<BF16, NL, 2, 4, false>(st, r, a, c, lds, 0, lane);
+      d128_load_masks<BF16, 2>(st, a, c);
+      d128_loop<BF16, NL, 2, 4, true>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 2>(st, a, w, c, lane);
     } else if (k == 1) {
       RowState<BF16, 1> st;
       d128_load_rows<BF16, 1>(st, a, w, c, wave, 4, lane);
       ring_begin<NL>(r, a, w, c, T);
+      d128_load_masks<BF16, 1>(st, a, c);
       d128_loop<BF16, NL, 1, 4, true>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 1>(st, a, w, c, lane);
     } else {
@@ -1140,6 +1199,7 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
   if (R == 1) {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k, 0, lane);
     ring_begin<NL>(r, a, w, c, T);
+    d128_load_masks<BF16, 1>(st, a, c);
     d128_loop<BF16, NL, 1, 1, false>(st, r, a, c, lds, j, lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
@@ -1148,6 +1208,7 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
   } else {
     d128_load_rows<BF16, 1>(st, a, w, c, 4 * k + (j >> 1), 0, lane);
     ring_begin<NL>(r, a, w, c, T);
+    d128_load_masks<BF16, 1>(st, a, c);
     d128_loop<BF16, NL, 1, 2, false>(st, r, a, c, lds, 2 * (j & 1), lane);
     bare_barrier();
     d128_part_put<BF16>(st, lds, j, lane);
@@ -1166,12 +1227,14 @@ __device__ __forceinline__ void d128_item_rr(const AttnArgs& a, const atlas_attn
     RowState<BF16, 2> st;
     d128_load_rows<BF16, 2>(st, a, w, c, wave, 8, lane);
     ring_begin<8>(r, a, w, c, T);
+    d128_load_masks<BF16, 2>(st, a, c);
     d128_loop<BF16, 8, 2, 4, false>(st, r, a, c, lds, 0, lane);
     d128_store_rows<BF16, 2>(st, a, w, c, lane);
   } else if (mine == 1) {
     RowState<BF16, 1> st;
     d128_load_rows<BF16, 1>(st, a, w, c, wave, 8, lane);
     ring_begin<8>(r, a, w, c, T);
+    d128_load_masks<BF16, 1>(st, a, c);
     d128_loop<BF16, 8, 1, 4, true>(st, r, a, c, lds, 0, lane);
     d128_store_rows<BF16, 1>(st, a, w, c, lane);
   } else {
@@ -1209,10 +1272,14 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   constexpr int D = 128;
   __shared__ __attribute__((aligned(1024))) char lds[kLdsBytes128];
 
-  const atlas_attn_work_t w = a.work[blockIdx.x];
   const int lane = threadIdx.x & 63;
+  // The item's first page-id window depends only on the workgroup index, so
+  // it is requested before (and travels with) the work item.
+  const int win0 = a.page_window != nullptr ? a.page_window[int64_t(blockIdx.x) * 64 + lane] : 0;
+  const atlas_attn_work_t w = a.work[blockIdx.x];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   ItemCtx c;
+  c.win0 = win0;
   c.qo_start = w.qo_start;
   c.qo_len = w.qo_len;
   c.kv_len = w.kv_len;
@@ -1265,12 +1332,13 @@ struct MergeArgs {
 
 // One wave per packed row, four rows per workgroup.  Lane (g, c) folds the
 // 16-byte chunk c of splits g, g + G, g + 2G, ... (G = 64 / (D / 8) split
-// groups) online, four splits per round of independent loads; the groups
-// then combine through cross-lane reductions.  No LDS and no workgroup
-// barriers, so a row costs the merge item load and about one round of
-// partial-state loads.
+// groups) online, kMergeUnroll splits per round of independent loads (one
+// round covers 32 splits at head_dim 128); the groups then combine through
+// cross-lane reductions.  No LDS and no workgroup barriers, so a row costs
+// the merge item load and one round of partial-state loads.
 constexpr int kMergeThreads = 256;
 constexpr int kMergeRowsPerBlock = kMergeThreads / 64;
+constexpr int kMergeUnroll = 8;
 
 // Eight 16-bit values (fp16 or bf16) to floats.
 template <bool BF16>
@@ -1317,24 +1385,31 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArg
 
   float m_t = -INFINITY, wsum = 0.f;
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = g; s0 < ns; s0 += 4 * G) {
-    float l[4];
-    uint4 raw[4];
+  for (int s0 = g; s0 < ns; s0 += kMergeUnroll * G) {
+    float l[kMergeUnroll];
+    uint4 raw[kMergeUnroll];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kMergeUnroll; ++k) {
+      // Splits past the last re-read split s0 (always present) and are
+      // given weight zero: unconditional loads stay in one batch, where a
+      // guarded load would be followed by a wait of its own.
       const int sp = s0 + k * G;
       const int64_t r = base + int64_t(sp < ns ? sp : s0) * mi.num_rows;
-      l[k] = sp < ns ? a.part_lse[r] : -INFINITY;
+      const float lv = a.part_lse[r];
       raw[k] = *reinterpret_cast<const uint4*>(a.part_o + r * D + c * 8);
+      l[k] = sp < ns ? lv : -INFINITY;
     }
-    const float m_new = fmaxf(fmaxf(m_t, fmaxf(l[0], l[1])), fmaxf(l[2], l[3]));
-    if (m_new == -INFINITY) continue;
+    float m_new = m_t;
+#pragma unroll
+    for (int k = 0; k < kMergeUnroll; ++k) m_new = max2f(m_new, l[k]);
+    // No early exit on an all-masked round: a branch here would hold the O
+    // loads back behind the LSE loads.  With m_new = -inf every weight is 0.
     const float sc = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_t - m_new);
 #pragma unroll
     for (int i = 0; i < 8; ++i) acc[i] *= sc;
     wsum *= sc;
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < kMergeUnroll; ++k) {
       const float wk = l[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l[k] - m_new);
       float v[8];
       unpack8<BF16>(raw[k], v);
@@ -1448,14 +1523,54 @@ merge:
 }  // namespace
 }  // namespace atlas
 
+namespace atlas {
+namespace {
+
+// Plan-time page-id windows: lane l of item i receives the id of the item's
+// page (first page + l), clamped to the item's last page, exactly the window
+// the head_dim-128 kernel would otherwise read after loading the work item.
+__global__ __launch_bounds__(64) void attn_page_windows_kernel(const atlas_attn_work_t* work,
+                                                               const int32_t* kv_indices, int page_shift,
+                                                               int32_t* window) {
+  const atlas_attn_work_t w = work[blockIdx.x];
+  const int l = threadIdx.x;
+  const int kv_end = min(w.kv_end, w.kv_len);
+  const int t_first = w.kv_start < kv_end ? w.kv_start : kv_end;
+  int id = 0;
+  if (t_first < kv_end) {
+    const int page0 = t_first >> page_shift;
+    const int last_page = (kv_end - 1) >> page_shift;
+    id = kv_indices[int64_t(w.page_offset) + min(page0 + l, last_page)];
+  }
+  window[int64_t(blockIdx.x) * 64 + l] = id;
+}
+
+}  // namespace
+}  // namespace atlas
+
 using namespace atlas;
+
+extern "C" int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
+                                       const int32_t* kv_indices_dev, int page_size, int32_t* window_dev,
+                                       void* stream) {
+  ATLAS_REQUIRE(num_work >= 0, "negative work count");
+  if (num_work == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(work_dev && kv_indices_dev && window_dev, "work, kv_indices and window must not be NULL");
+  ATLAS_REQUIRE(page_size > 0 && (page_size & (page_size - 1)) == 0, "page_size must be a power of two, got %d",
+                page_size);
+  const int shift = __builtin_ctz(static_cast<unsigned>(page_size));
+  hipLaunchKernelGGL(attn_page_windows_kernel, dim3(num_work), dim3(64), 0, static_cast<hipStream_t>(stream),
+                     work_dev, kv_indices_dev, shift, window_dev);
+  return launch_status("attn_page_windows_kernel");
+}
 
 extern "C" int atlas_tree_verify_attn(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
-    const atlas_attn_work_t* work_dev, int num_work, const atlas_attn_merge_t* merge_dev,
+    const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
+    const atlas_attn_merge_t* merge_dev,
     int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
@@ -1502,6 +1617,7 @@ extern "C" int atlas_tree_verify_attn(
   args.tree_mask = tree_mask_dev;
   args.mask_col_start = mask_col_start_dev;
   args.work = work_dev;
+  args.page_window = page_window_dev;
   args.out = static_cast<char*>(out);
   args.out_stride_token = out_stride_token;
   args.out_stride_head = out_stride_head;

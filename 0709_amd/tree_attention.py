@@ -64,6 +64,7 @@ class AttentionPlan:
     kv_lens: list[int]
     qo_lens: list[int]
     tiles_per_split: int  # most key tiles any work item streams
+    page_windows: torch.Tensor | None = None  # int32 [num_work * 64]: first page ids of each item
 
     def device_view(self, offset: int) -> int:
         return int(self.meta.data_ptr()) + 4 * offset
@@ -137,6 +138,9 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._plan: AttentionPlan | None = None
         # None: chosen per plan (see plan())
         self.split_target_items: int | None = None
+        # Plan-time page-id windows for the head_dim-128 kernel (off: the
+        # kernel reads them from the page table after its work item).
+        self.use_page_windows: bool = True
         self.min_tiles_per_split = 1
         self.max_rows_per_item: int | None = None
         self._meta_buf: torch.Tensor | None = None
@@ -355,6 +359,16 @@ class BatchPrefillWithPagedKVCacheWrapper:
             if nb:
                 bits_buf[:nb].copy_(tree_bits, non_blocking=non_blocking)
 
+        # First page-id window of every work item, gathered on the device once
+        # per plan (the page table is fixed until the next plan), so the
+        # head_dim-128 kernel requests its first page ids with its work item.
+        windows = None
+        if direct and work and self.use_page_windows:
+            windows = self._persistent("_windows_buf", 64 * len(work), torch.int32)
+            rc = _lib.load().atlas_attn_page_windows(int(meta.data_ptr()), len(work), _lib.ptr(indices), ps,
+                                                     _lib.ptr(windows), _lib.stream_of(device))
+            _lib.check(rc, "atlas_attn_page_windows")
+
         self._plan = AttentionPlan(
             batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,
             sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
@@ -364,6 +378,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             merge_offset=merge_off, kv_len_offset=kvlen_off, col_offset=col_off, max_rows=max_rows,
             partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens,
             tiles_per_split=max((math.ceil((it[5] - it[4]) / TILE_KEYS) for it in work), default=0),
+            page_windows=windows,
         )
 
     def _persistent(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:
@@ -452,6 +467,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             _lib.ptr(plan.qo_indptr), _lib.ptr(plan.kv_indptr), _lib.ptr(plan.kv_indices),
             plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
             plan.device_view(plan.col_offset), plan.device_view(plan.work_offset), plan.num_work,
+            _lib.ptr(plan.page_windows) if plan.page_windows is not None else None,
             plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge, plan.max_rows,
             plan.num_qo_heads, plan.num_kv_heads, plan.head_dim, plan.page_size, plan.sm_scale,
             _lib.dtype_code(q.dtype), _lib.ptr(out), out.stride(0), out.stride(1),

@@ -148,6 +148,21 @@ typedef struct {
   int32_t pad1;
 } atlas_attn_merge_t;
 
+/* First page-id window of every work item: window_dev[64 * i + l] = the page
+ * id (from kv_indices_dev, at work[i].page_offset) of item i's page
+ * work[i].kv_start / page_size + l, clamped to the item's last page, for
+ * l < 64.  Run once per plan, after the work list and page table are in
+ * place; atlas_tree_verify_attn then takes window_dev as page_window_dev
+ * (NULL: the kernel reads the window from kv_indices after the work item).
+ * With it a head_dim-128 workgroup requests its first page ids together with
+ * its work item instead of one round trip later.  page_size must be a power
+ * of two.  No counterpart in the reference: it is part of this library's
+ * plan, as FlashInfer's plan keeps scheduling metadata of its own
+ * (src/atlas_0709/flashinfer_full_verify.py:953-985 calls that plan). */
+int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
+                            const int32_t* kv_indices_dev, int page_size, int32_t* window_dev,
+                            void* stream);
+
 /* Mask modes. */
 #define ATLAS_MASK_NONE 0   /* every key < kv_len visible */
 #define ATLAS_MASK_TREE 1   /* keys < mask_col_start[req] visible; key p >= that
@@ -174,6 +189,7 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
                            const int32_t* kv_len_dev, int mask_mode,
                            const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
                            const atlas_attn_work_t* work_dev, int num_work,
+                           const int32_t* page_window_dev,
                            const atlas_attn_merge_t* merge_dev, int num_merge,
                            int max_rows_per_item, int num_qo_heads, int num_kv_heads,
                            int head_dim, int page_size, float sm_scale, int dtype, void* out,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 1
+    assert lib.atlas_abi_version() == 2
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -48,7 +48,8 @@ def test_argument_errors_are_reported_without_device_work():
         None, 0, 0, 0,         # kv cache, page stride, V offset, token stride
         None, None, None, None,  # qo_indptr, kv_indptr, kv_indices, kv_len
         0, None, None,         # mask mode, tree mask, mask column start
-        None, 0, None, 0,      # work, merge lists
+        None, 0, None,         # work list, page windows
+        None, 0,               # merge list
         1, 32, 8, 96, 16,      # rows per item, Hq, Hkv, head_dim (unsupported), page size
         ctypes.c_float(0.1), 0,
         None, 0, 0, None,      # out, out strides, lse

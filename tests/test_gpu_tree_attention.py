@@ -302,3 +302,51 @@ def test_reference_plan_helper_and_kv_tuple(dev):
                                   masks=[c["mask"]])
     assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
     assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("split_target", [None, 1, 64])
+def test_page_windows_match_page_table_path(dev, split_target):
+    """Plan-time page-id windows: each item's window holds the ids of its first
+    64 pages (clamped to its last page), and attention with them is bit-equal
+    to attention reading the page table after the work item.  Split target 1
+    gives one split of ~330 pages per KV head, so the kernel still loads later
+    windows from the page table."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(31)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=31, prefix_len=5000, routes=routes, spare_pages=20)
+    last = ffv.last_page_len(c["kv_len"], c["ps"])
+    q, kv = c["q"].to(dev), c["kv"].to(dev)
+    results = []
+    for use in (True, False):
+        ws = torch.empty(64 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        w.use_page_windows = use
+        if split_target is not None:
+            w.split_target_items = split_target
+        w.plan(
+            torch.tensor([0, c["n"]], dtype=torch.int32, device=dev),
+            torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev),
+            c["order"].to(dev), torch.tensor([last], dtype=torch.int32, device=dev),
+            c["hq"], c["hkv"], c["d"], c["ps"], causal=False, custom_mask=c["spec"].bool_mask,
+            q_data_type=c["dtype"],
+        )
+        out, lse = w.run(q, kv, return_lse=True)
+        torch.cuda.synchronize()
+        results.append((w.current_plan, out.cpu(), lse.cpu()))
+    (plan, out_a, lse_a), (plan_b, out_b, lse_b) = results
+    assert plan.page_windows is not None and plan_b.page_windows is None
+    assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
+    win = plan.page_windows.cpu().view(-1, 64)
+    meta = plan.meta.cpu()
+    order = c["order"].tolist()
+    ps = c["ps"]
+    for i in range(plan.num_work):
+        item = meta[16 * i : 16 * i + 16].tolist()
+        kv_start, kv_end, kv_len, page_offset = item[4], item[5], item[9], item[11]
+        end = min(kv_end, kv_len)
+        t0 = min(kv_start, end)
+        if t0 < end:
+            p0, lp = t0 // ps, (end - 1) // ps
+            assert win[i].tolist() == [order[page_offset + min(p0 + l, lp)] for l in range(64)], f"item {i}"
