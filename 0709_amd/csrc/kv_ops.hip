@@ -13,6 +13,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnroll = 4;
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
 struct InlineItems {
   int64_t src[ATLAS_MAX_INLINE_ITEMS];
   int64_t dst[ATLAS_MAX_INLINE_ITEMS];
@@ -46,6 +48,50 @@ __global__ __launch_bounds__(kThreads) void kv_move_kernel(LayerTable lt, SlotGe
 #pragma unroll
   for (int u = 0; u < kUnroll; ++u) {
     if (dofs[u] >= 0) *reinterpret_cast<uint4*>(base + dofs[u]) = buf[u];
+  }
+}
+
+// One wave per moved slot, for rows of CPR 1 KiB chunks (1 KiB and 2 KiB
+// token rows).  The slot pair is wave-uniform and resolved to byte offsets
+// once; the wave then copies the slot's K and V rows in every layer of the
+// table, LB layers (2 * LB * CPR chunks per lane) in flight.  No branch splits
+// a batch (a branch makes the compiler wait for every outstanding access,
+// stores included, before each store): layers past the last one copy the last
+// layer again, the same bytes to the same place.  dst and src slots are
+// disjoint, so the copies of different waves never overlap.
+template <int CPR, int LB>
+__global__ __launch_bounds__(kThreads) void kv_move_rows_kernel(LayerTable lt, SlotGeom g, int num_layers,
+                                                                const int64_t* __restrict__ dst,
+                                                                const int64_t* __restrict__ src, int64_t n) {
+  const int64_t item = int64_t(blockIdx.x) * (kThreads / 64) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (item >= n) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t so = slot_offset(src[item], g) + int64_t(lane) * 16;
+  const int64_t dof = slot_offset(dst[item], g) + int64_t(lane) * 16;
+  for (int l0 = 0; l0 < num_layers; l0 += LB) {
+    u32x4v buf[LB][2][CPR];
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int l = min(l0 + i, num_layers - 1);
+      const char* kb = lt.k[l];
+      const char* vb = lt.v[l];
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) {
+        buf[i][0][c] = *reinterpret_cast<const u32x4v*>(kb + so + c * 1024);
+        buf[i][1][c] = *reinterpret_cast<const u32x4v*>(vb + so + c * 1024);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int l = min(l0 + i, num_layers - 1);
+      char* kb = const_cast<char*>(lt.k[l]);
+      char* vb = const_cast<char*>(lt.v[l]);
+#pragma unroll
+      for (int c = 0; c < CPR; ++c) {
+        *reinterpret_cast<u32x4v*>(kb + dof + c * 1024) = buf[i][0][c];
+        *reinterpret_cast<u32x4v*>(vb + dof + c * 1024) = buf[i][1][c];
+      }
+    }
   }
 }
 
@@ -113,7 +159,10 @@ enum CommitMode { kCopy = 0, kGather = 1, kScatter = 2 };
 // in flight.  Block = 4 waves = 4 consecutive layers of one item.
 constexpr int kRowWaves = 4;
 
-template <int MODE, bool INLINE>
+// CPR: 1 KiB chunks per token row (1 or 2: every load of the row is issued
+// before its stores, so a wave keeps its whole K and V rows in flight), or 0
+// for other row sizes (a loop of 16-byte vectors).
+template <int MODE, bool INLINE, int CPR>
 __global__ __launch_bounds__(kThreads) void kv_commit_rows_kernel(
     LayerTable lt, SlotGeom g, int nl, const int32_t* __restrict__ kv_indptr,
     const int32_t* __restrict__ kv_indices, const int32_t* __restrict__ item_req,
@@ -154,12 +203,26 @@ __global__ __launch_bounds__(kThreads) void kv_commit_rows_kernel(
     dst_k = (MODE == kGather) ? wk : kb + dst_off;
     dst_v = (MODE == kGather) ? wv : vb + dst_off;
   }
+  if constexpr (CPR > 0) {
+    u32x4v a[CPR], b[CPR];
+#pragma unroll
+    for (int c = 0; c < CPR; ++c) {
+      a[c] = *reinterpret_cast<const u32x4v*>(src_k + int64_t(c * 64 + lane) * 16);
+      b[c] = *reinterpret_cast<const u32x4v*>(src_v + int64_t(c * 64 + lane) * 16);
+    }
+#pragma unroll
+    for (int c = 0; c < CPR; ++c) {
+      *reinterpret_cast<u32x4v*>(dst_k + int64_t(c * 64 + lane) * 16) = a[c];
+      *reinterpret_cast<u32x4v*>(dst_v + int64_t(c * 64 + lane) * 16) = b[c];
+    }
+  } else {
 #pragma unroll 2
-  for (int v = lane; v < g.row_vecs; v += 64) {
-    const uint4 a = *reinterpret_cast<const uint4*>(src_k + int64_t(v) * 16);
-    const uint4 b = *reinterpret_cast<const uint4*>(src_v + int64_t(v) * 16);
-    *reinterpret_cast<uint4*>(dst_k + int64_t(v) * 16) = a;
-    *reinterpret_cast<uint4*>(dst_v + int64_t(v) * 16) = b;
+    for (int v = lane; v < g.row_vecs; v += 64) {
+      const uint4 a = *reinterpret_cast<const uint4*>(src_k + int64_t(v) * 16);
+      const uint4 b = *reinterpret_cast<const uint4*>(src_v + int64_t(v) * 16);
+      *reinterpret_cast<uint4*>(dst_k + int64_t(v) * 16) = a;
+      *reinterpret_cast<uint4*>(dst_v + int64_t(v) * 16) = b;
+    }
   }
 }
 
@@ -227,6 +290,18 @@ extern "C" int atlas_kv_move_slots(const void* const* k_layers, const void* cons
     const int nl = std::min(ATLAS_MAX_LAYERS_PER_LAUNCH, num_layers - l0);
     LayerTable lt;
     fill_table(lt, k_layers, v_layers, l0, nl);
+    if (g.row_vecs == 64 || g.row_vecs == 128) {
+      // 1 KiB or 2 KiB token rows: one wave per slot, all layers
+      const dim3 grid(static_cast<unsigned>((n + kThreads / 64 - 1) / (kThreads / 64)));
+      if (g.row_vecs == 64)
+        hipLaunchKernelGGL((kv_move_rows_kernel<1, 8>), grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                           lt, g, nl, dst_slots_dev, src_slots_dev, n);
+      else
+        hipLaunchKernelGGL((kv_move_rows_kernel<2, 4>), grid, dim3(kThreads), 0, static_cast<hipStream_t>(stream),
+                           lt, g, nl, dst_slots_dev, src_slots_dev, n);
+      if ((rc = launch_status("kv_move_rows_kernel"))) return rc;
+      continue;
+    }
     hipLaunchKernelGGL(kv_move_kernel, copy_grid(n, g, nl), dim3(kThreads), 0,
                        static_cast<hipStream_t>(stream), lt, g, dst_slots_dev, src_slots_dev, n);
     if ((rc = launch_status("kv_move_kernel"))) return rc;
@@ -270,6 +345,38 @@ extern "C" int atlas_kv_append(const void* const* k_layers, const void* const* v
 namespace atlas {
 namespace {
 
+template <bool INLINE, int MODE>
+void launch_commit_mode(int cpr, dim3 grid, hipStream_t stream, const LayerTable& lt, const SlotGeom& g, int nl,
+                        const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* item_req,
+                        const int64_t* src_pos, const int64_t* dst_pos, const InlineItems& items, int64_t n,
+                        char* ws, int l0) {
+  if (cpr == 1)
+    hipLaunchKernelGGL((kv_commit_rows_kernel<MODE, INLINE, 1>), grid, dim3(kThreads), 0, stream, lt, g, nl,
+                       kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
+  else if (cpr == 2)
+    hipLaunchKernelGGL((kv_commit_rows_kernel<MODE, INLINE, 2>), grid, dim3(kThreads), 0, stream, lt, g, nl,
+                       kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
+  else
+    hipLaunchKernelGGL((kv_commit_rows_kernel<MODE, INLINE, 0>), grid, dim3(kThreads), 0, stream, lt, g, nl,
+                       kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
+}
+
+template <bool INLINE>
+void launch_commit_rows(int mode, int cpr, dim3 grid, hipStream_t stream, const LayerTable& lt, const SlotGeom& g,
+                        int nl, const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* item_req,
+                        const int64_t* src_pos, const int64_t* dst_pos, const InlineItems& items, int64_t n,
+                        char* ws, int l0) {
+  if (mode == kCopy)
+    launch_commit_mode<INLINE, kCopy>(cpr, grid, stream, lt, g, nl, kv_indptr, kv_indices, item_req, src_pos,
+                                      dst_pos, items, n, ws, l0);
+  else if (mode == kGather)
+    launch_commit_mode<INLINE, kGather>(cpr, grid, stream, lt, g, nl, kv_indptr, kv_indices, item_req, src_pos,
+                                        dst_pos, items, n, ws, l0);
+  else
+    launch_commit_mode<INLINE, kScatter>(cpr, grid, stream, lt, g, nl, kv_indptr, kv_indices, item_req, src_pos,
+                                         dst_pos, items, n, ws, l0);
+}
+
 template <bool INLINE>
 int commit_impl(const void* const* k_layers, const void* const* v_layers, int num_layers,
                 const SlotGeom& g, const int32_t* kv_indptr, const int32_t* kv_indices,
@@ -285,16 +392,10 @@ int commit_impl(const void* const* k_layers, const void* const* v_layers, int nu
       LayerTable lt;
       fill_table(lt, k_layers, v_layers, l0, nl);
       const dim3 grid(static_cast<unsigned>(n), static_cast<unsigned>((nl + kRowWaves - 1) / kRowWaves));
-      if (!staging) {
-        hipLaunchKernelGGL((kv_commit_rows_kernel<kCopy, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
-                           kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
-      } else if (pass == 0) {
-        hipLaunchKernelGGL((kv_commit_rows_kernel<kGather, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
-                           kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
-      } else {
-        hipLaunchKernelGGL((kv_commit_rows_kernel<kScatter, INLINE>), grid, dim3(kThreads), 0, stream, lt, g, nl,
-                           kv_indptr, kv_indices, item_req, src_pos, dst_pos, items, n, ws, l0);
-      }
+      const int mode = !staging ? kCopy : (pass == 0 ? kGather : kScatter);
+      const int cpr = g.row_vecs == 64 ? 1 : (g.row_vecs == 128 ? 2 : 0);
+      launch_commit_rows<INLINE>(mode, cpr, grid, stream, lt, g, nl, kv_indptr, kv_indices, item_req, src_pos,
+                                 dst_pos, items, n, ws, l0);
       if ((rc = launch_status("kv_commit_kernel"))) return rc;
     }
   }

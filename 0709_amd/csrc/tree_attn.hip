@@ -1178,7 +1178,7 @@ __device__ __forceinline__ void d128_item_split(const AttnArgs& a, const atlas_a
       d128_load_rows<BF16, 2>(st, a, w, c, wave, 4, lane);
       ring_begin<NL>(r, a, w, c, T);
       d128_load_masks<BF16, 2>(st, a, c);
-      d128_loop<BF16, NL, 2, 4, true>(st, r, a, c, lds, 0, lane);
+      d128_loop<BF16, NL, 2, 4, false>(st, r, a, c, lds, 0, lane);
       d128_store_rows<BF16, 2>(st, a, w, c, lane);
     } else if (k == 1) {
       RowState<BF16, 1> st;

@@ -324,23 +324,41 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
     b.record()
     torch.cuda.synchronize()
     commit_call_us = a.elapsed_time(b) * 1000.0 / 50
-    # device time of the commit launch: 20 commits replayed from a HIP graph
-    # (no per-call host work between them)
+    # Device time of the commit launch, from HIP graphs (no per-call host
+    # work between launches).  Cold: 40 commit instances in rotation, each
+    # with its own page table (the same positions on other physical pages),
+    # 1.3 GB of rows in all, more than L2 plus the 256 MB Infinity Cache, so
+    # every copy streams from and to HBM.  Hot: one instance repeated (its
+    # 16 MiB of rows stay in the caches).
+    n_inst = 40
+    inst_args = [args] + [dict(args, kv_indices=torch.randperm(pool_pages, generator=gen)[:need_pages]
+                               .to(torch.int32).to(dev)) for _ in range(n_inst - 1)]
     with torch.cuda.stream(side):
         kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
     torch.cuda.current_stream().wait_stream(side)
     cgraph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(cgraph):
+        for k in range(n_inst):
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **inst_args[k])
+    hgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(hgraph):
         for _ in range(20):
             kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
     cgraph.replay()
+    hgraph.replay()
     torch.cuda.synchronize()
     a.record()
     for _ in range(5):
         cgraph.replay()
     b.record()
     torch.cuda.synchronize()
-    commit_us = a.elapsed_time(b) * 1000.0 / 100
+    commit_us = a.elapsed_time(b) * 1000.0 / (5 * n_inst)
+    a.record()
+    for _ in range(5):
+        hgraph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    hot_commit_us = a.elapsed_time(b) * 1000.0 / 100
     moved = len(src) * geom.layers * geom.token_bytes()
 
     # prune: pages of every request owned; live = prefix + committed tokens
@@ -387,17 +405,25 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
         "attention_bytes_per_layer": attn_bytes,
         "commit_us": round(commit_us, 3), "commit_call_us": round(commit_call_us, 3), "commit_moved_bytes": moved,
         "commit_GBps": round(2 * moved / (commit_us * 1e-6) / 1e9, 1), "commit_staging": bool(staging),
+        "commit_instances": n_inst, "hot_commit_us": round(hot_commit_us, 3),
+        "hot_commit_GBps": round(2 * moved / (hot_commit_us * 1e-6) / 1e9, 1),
         "mark_and_prune_us": round(prune_us, 3), "pruned_pages": freed,
     }
-    del pool, layers, q, outs, ws, graph, cgraph
+    del pool, layers, q, outs, ws, graph, cgraph, hgraph, inst_args
     torch.cuda.empty_cache()
     return out
 
 
-def cow_leg(dev, *, requests=8, routes=9, iters=50):
+def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
     """Drafter tail-page copy-on-write: per request, 9 forked routes share a
     partially filled 64-token tail page; 8 of them get private copies, all in
-    one move launch (Llama-3.2-1B KV geometry, bf16, flat token pool)."""
+    one move launch (Llama-3.2-1B KV geometry, bf16, flat token pool).
+
+    ``instances`` independent copy-on-write steps (disjoint source and
+    destination pages, 189 MB of source plus destination rows each) are
+    timed in rotation, so the working set (1.5 GB) exceeds L2 and the 256 MB
+    Infinity Cache and every copy streams from and to HBM.  The same step
+    repeated on one instance (``hot_*``) runs from those caches."""
     kv_ops = _pkg("kv_ops")
     wl = _pkg("workloads")
     geom = wl.LLAMA_1B
@@ -408,31 +434,42 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50):
                 for _ in range(geom.layers)]
     v_layers = [torch.empty_like(k_layers[0]) for _ in range(geom.layers)]
     perm = torch.randperm(pool_pages, generator=gen)
-    src, dst = [], []
+    tail_lens = [int(torch.randint(1, ps, (1,), generator=gen)) for _ in range(requests)]
+    sets = []
     j = 0
-    for b in range(requests):
-        tail_page = int(perm[j])
-        j += 1
-        tail_len = int(torch.randint(1, ps, (1,), generator=gen))
-        for _ in range(routes - 1):
-            new_page = int(perm[j])
+    for _ in range(instances):
+        src, dst = [], []
+        for b in range(requests):
+            tail_page = int(perm[j])
             j += 1
-            src.extend(tail_page * ps + o for o in range(tail_len))
-            dst.extend(new_page * ps + o for o in range(tail_len))
-    src_t = torch.tensor(src, device=dev)
-    dst_t = torch.tensor(dst, device=dev)
-    for _ in range(5):
-        kv_ops.move_slots(k_layers, v_layers, dst_t, src_t)
+            for _ in range(routes - 1):
+                new_page = int(perm[j])
+                j += 1
+                src.extend(tail_page * ps + o for o in range(tail_lens[b]))
+                dst.extend(new_page * ps + o for o in range(tail_lens[b]))
+        sets.append((torch.tensor(dst, device=dev), torch.tensor(src, device=dev)))
+    slots = int(sets[0][1].numel())
+    for d_t, s_t in sets:
+        kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
     torch.cuda.synchronize()
     a, b = _ev(), _ev()
     a.record()
-    for _ in range(iters):
-        kv_ops.move_slots(k_layers, v_layers, dst_t, src_t)
+    for i in range(iters):
+        d_t, s_t = sets[i % instances]
+        kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
     b.record()
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1000.0 / iters
-    moved = len(src) * geom.layers * geom.token_bytes()
-    return {"us": us, "moved_bytes": moved, "GBps": 2 * moved / (us * 1e-6) / 1e9, "slots": len(src)}
+    a.record()
+    for _ in range(iters):
+        kv_ops.move_slots(k_layers, v_layers, sets[0][0], sets[0][1])
+    b.record()
+    torch.cuda.synchronize()
+    hot_us = a.elapsed_time(b) * 1000.0 / iters
+    moved = slots * geom.layers * geom.token_bytes()
+    return {"us": us, "moved_bytes": moved, "GBps": 2 * moved / (us * 1e-6) / 1e9, "slots": slots,
+            "instances": instances, "working_set_bytes": 2 * moved * instances,
+            "hot_us": hot_us, "hot_GBps": 2 * moved / (hot_us * 1e-6) / 1e9}
 
 
 def drafter_leg(dev, *, requests=8, repeats=3):
