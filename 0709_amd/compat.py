@@ -12,10 +12,10 @@ this package in:
   reference's module names in ``sys.modules``.
 
 ``flashinfer=True`` also registers a ``flashinfer`` module exposing
-``BatchPrefillWithPagedKVCacheWrapper`` and ``packbits`` backed by the gfx950
-kernels, when no ``flashinfer`` is importable (the reference creates its
-verify wrapper through ``flashinfer.BatchPrefillWithPagedKVCacheWrapper``,
-``flashinfer_full_verify.py:502-507``, ``:953``).
+``BatchPrefillWithPagedKVCacheWrapper``, ``BatchDecodeWithPagedKVCacheWrapper``
+and ``packbits`` backed by the gfx950 kernels, when no ``flashinfer`` is
+importable (the reference creates its verify and decode wrappers through those
+names, ``flashinfer_full_verify.py:502-507``, ``:882-888``, ``:953``).
 """
 
 from __future__ import annotations
@@ -40,7 +40,8 @@ HOT_PATH: dict[str, tuple[str, tuple[str, ...]]] = {
         "flashinfer_full_verify", ("TreeSpec", "build_path_tree_tokens_from_paths", "build_deduplicated_path_tree_tokens",
                                    "ancestors_inclusive", "build_tree_spec_from_paths",
                                    "build_deduplicated_tree_spec_from_paths", "prefix_layer_to_paged_kv",
-                                   "write_suffix_kv", "first_tensor", "packbits")),
+                                   "write_suffix_kv", "first_tensor", "packbits", "make_decode_wrapper",
+                                   "plan_decode_wrapper")),
     "atlas_0709.target_runtime": (
         "target_runtime", ("VerifyRoutePayload", "DirectFlashInferMaskedTreeVerifyBackend")),
     "atlas_0709.types": ("types", ("TargetRouteScore", "TargetVerifyResult")),
@@ -76,8 +77,9 @@ def install_atlas_0709_alias(*, flashinfer: bool = False) -> dict[str, str]:
         except ImportError:
             shim = _types.ModuleType("flashinfer")
             shim.BatchPrefillWithPagedKVCacheWrapper = _ours("tree_attention").BatchPrefillWithPagedKVCacheWrapper
+            shim.BatchDecodeWithPagedKVCacheWrapper = _ours("decode_attention").BatchDecodeWithPagedKVCacheWrapper
             shim.packbits = _ours("flashinfer_full_verify").packbits
-            shim.__doc__ = "FlashInfer verify-attention names backed by the gfx950 tree-attention kernels."
+            shim.__doc__ = "FlashInfer verify and decode attention names backed by the gfx950 paged-attention kernels."
             sys.modules["flashinfer"] = shim
             done["flashinfer"] = "registered"
     return done

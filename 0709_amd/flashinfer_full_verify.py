@@ -323,6 +323,9 @@ def first_tensor(value) -> torch.Tensor:
     raise TypeError(f"expected tensor output, got {type(value).__name__}")
 
 
+from .decode_attention import make_decode_wrapper, plan_decode_wrapper  # noqa: E402  (decode wrapper helpers)
+
+
 def make_prefill_wrapper(*, args, flashinfer=None) -> BatchPrefillWithPagedKVCacheWrapper:
     """Workspace-backed wrapper (``flashinfer_full_verify.py:877-879``)."""
     workspace = torch.empty(int(args.workspace_mb) * 1024 * 1024, dtype=torch.uint8, device=args.device)

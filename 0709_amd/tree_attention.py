@@ -328,6 +328,19 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # their queries) when there are 8 KV heads.
         work.sort(key=lambda it: (-(it[5] - it[4]), it[0], it[2], it[4], it[1]))
 
+        self._install(
+            batch=batch, hq=hq, hkv=hkv, d=d, ps=ps, sm_scale=sm_scale, q_dtype=q_dtype, kv_dtype=kv_dtype,
+            mask_mode=mask_mode, work=work, merge=merge, kv_lens=kv_lens, cols=cols, qo=qo, kvp=kvp,
+            qo_lens=qo_lens, indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits,
+            partial_rows=partial_rows, max_rows=max_rows, direct=direct, non_blocking=non_blocking)
+
+    def _install(self, *, batch, hq, hkv, d, ps, sm_scale, q_dtype, kv_dtype, mask_mode, work, merge, kv_lens, cols,
+                 qo, kvp, qo_lens, indices_src, tree_bits, partial_rows, max_rows, direct, non_blocking) -> None:
+        """Write a planned work list into the persistent device buffers and
+        make it the current plan.  ``work`` holds 16-int work items, ``merge``
+        8-int merge items; ``qo`` / ``kvp`` are the per-request indptr lists
+        the merge kernel and callers read."""
+        device = self.device
         meta_vals: list[int] = []
         for item in work:
             meta_vals.extend(item)
@@ -347,7 +360,6 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # same (or a smaller) shape.
         meta = self._persistent("_meta_buf", len(meta_vals), torch.int32)
         meta[: len(meta_vals)].copy_(torch.tensor(meta_vals, dtype=torch.int32), non_blocking=non_blocking)
-        indices_src = paged_kv_indices.reshape(-1)
         n_idx = int(indices_src.numel())
         indices = self._persistent("_indices_buf", n_idx, torch.int32)
         if n_idx:

@@ -472,6 +472,97 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
             "hot_us": hot_us, "hot_GBps": 2 * moved / (hot_us * 1e-6) / 1e9}
 
 
+def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, cascade=True):
+    """Drafter paged decode attention (Llama-3.2-1B geometry: 16 layers, 32 q
+    heads, 8 KV heads, head_dim 64; bf16, page 64): ``requests`` x ``routes``
+    forked routes, one query each.  The routes of a request share its full
+    prefix pages and own a private tail page (the copy-on-write copy of the
+    partial prefix page plus ``steps`` decoded tokens).  Prefix lengths follow
+    the fork-stress workload (128..1024 tokens) unless ``prefix_len`` is given.
+    Times the 16 layers' decode attention replayed from a HIP graph; bytes are
+    counted over unique pages (each shared page once) and per route."""
+    da = _pkg("decode_attention")
+    dw = _pkg("drafter_workload")
+    geom = _pkg("workloads").LLAMA_1B
+    ps = 64
+    plans = dw.config5_plans(requests, ps, 0)
+    prefixes = [p.prefix_len if prefix_len is None else int(prefix_len) for p in plans]
+    gen = torch.Generator().manual_seed(9)
+    indptr, indices, last = [0], [], []
+    unique_pages = 0
+    route_tokens = 0
+    nxt = 0
+    for pre in prefixes:
+        full = pre // ps
+        shared = list(range(nxt, nxt + full))
+        nxt += full
+        unique_pages += full
+        for _ in range(routes):
+            own = pre - full * ps + steps
+            own_pages = (own + ps - 1) // ps
+            pages = shared + list(range(nxt, nxt + own_pages))
+            nxt += own_pages
+            unique_pages += own_pages
+            indices.extend(pages)
+            indptr.append(len(indices))
+            last.append(full * ps + own - (len(pages) - 1) * ps)
+            route_tokens += full * ps + own
+    pool_pages = nxt + 8
+    perm = torch.randperm(pool_pages, generator=gen)
+    phys = [int(perm[i]) for i in indices]
+    batch = requests * routes
+    layers = [(torch.randn((pool_pages, 2, ps, geom.kv_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
+              for _ in range(geom.layers)]
+    q = [(torch.randn((batch, geom.q_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
+         for _ in range(geom.layers)]
+    outs = [torch.empty_like(x) for x in q]
+    ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = da.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    w.use_cascade = cascade
+    w.plan(torch.tensor(indptr, dtype=torch.int32, device=dev), torch.tensor(phys, dtype=torch.int32, device=dev),
+           torch.tensor(last, dtype=torch.int32, device=dev), geom.q_heads, geom.kv_heads, geom.head_dim, ps,
+           data_type=torch.bfloat16, q_data_type=torch.bfloat16)
+
+    def fwd():
+        for l in range(geom.layers):
+            w.run(q[l], layers[l], out=outs[l])
+
+    fwd()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fwd()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fwd()
+    graph.replay()
+    torch.cuda.synchronize()
+    a, b = _ev(), _ev()
+    a.record()
+    for _ in range(iters):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    us = a.elapsed_time(b) * 1000.0 / (iters * geom.layers)
+    row = geom.token_bytes()  # K and V of one token, one layer
+    q_bytes = 2 * batch * geom.q_heads * geom.head_dim * 2
+    unique_bytes = unique_pages * ps * row + q_bytes
+    route_bytes = route_tokens * row + q_bytes
+    out = {
+        "requests": requests, "routes_per_request": routes, "prefix_lens": sorted(set(prefixes))[:3] + (
+            ["..."] if len(set(prefixes)) > 3 else []),
+        "cascade_groups": w.cascade_groups, "work_items": w.current_plan.num_work,
+        "merge_items": w.current_plan.num_merge,
+        "us_per_layer": round(us, 3), "unique_bytes_per_layer": unique_bytes, "route_bytes_per_layer": route_bytes,
+        "GBps_unique": round(unique_bytes / (us * 1e-6) / 1e9, 1),
+        "frac_unique": round(unique_bytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+    }
+    del layers, q, outs, ws, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def drafter_leg(dev, *, requests=8, repeats=3):
     """Drafter route-pool fork stress (Llama-3.2-1B KV geometry, bf16, page
     64): 8 requests, each forking to 9 routes at random fill levels of its
@@ -645,6 +736,8 @@ def main():
     if not args.no_legs:
         result["components"]["batched_32req"] = batched_leg(dev, pool_gb=args.commit_pool_gb)
         result["components"]["cow_8req_9routes"] = cow_leg(dev)
+        result["components"]["drafter_decode_attn"] = decode_leg(dev)
+        result["components"]["drafter_decode_attn_8k"] = decode_leg(dev, prefix_len=8192)
         result["components"]["drafter_fork_8req"] = drafter_leg(dev)
         result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
         result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)

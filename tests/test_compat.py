@@ -35,6 +35,10 @@ def test_registers_modules_when_reference_absent(clean_modules):
     assert SGLangRoutePoolBridge is pkg("flashinfer_paged.sglang_runtime").SGLangRoutePoolBridge
     assert build_deduplicated_tree_spec_from_paths is pkg("flashinfer_full_verify").build_deduplicated_tree_spec_from_paths
     assert flashinfer.BatchPrefillWithPagedKVCacheWrapper is pkg("tree_attention").BatchPrefillWithPagedKVCacheWrapper
+    assert flashinfer.BatchDecodeWithPagedKVCacheWrapper is pkg("decode_attention").BatchDecodeWithPagedKVCacheWrapper
+    from atlas_0709.flashinfer_full_verify import make_decode_wrapper, plan_decode_wrapper
+    assert make_decode_wrapper is pkg("decode_attention").make_decode_wrapper
+    assert plan_decode_wrapper is pkg("decode_attention").plan_decode_wrapper
 
 
 def test_patches_only_hot_path_names_of_loaded_reference_modules(clean_modules):
