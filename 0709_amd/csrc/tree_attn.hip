@@ -63,6 +63,12 @@ struct AttnArgs {
   float* lse;
   uint16_t* part_o;  // normalised partial O rows in the output dtype
   float* part_lse;    // base-2 LSE of each partial row
+  // Fused append (head_dim-128 kernel): K / V rows of each request's newest
+  // qo_len tokens, [token, head, D] with these strides (elements), or null.
+  const char* app_k;
+  const char* app_v;
+  int64_t app_stride_token;
+  int64_t app_stride_head;
   float scale_log2;  // sm_scale * log2(e)
   int mask_mode;
   int group;
@@ -1265,6 +1271,31 @@ __device__ __forceinline__ void ring_init(Ring<NL>& r, const AttnArgs& a, const 
   r.lds0 = lds0;
 }
 
+// Fused append: the request's newest qo_len tokens occupy its last qo_len key
+// positions.  The rows of those positions that fall in this item's key range
+// are copied, for this item's KV head, from the caller's K / V rows into the
+// paged cache before any tile is loaded (the loads of the masked tail tile
+// read them back).  32 lanes per position (16 granules of K, 16 of V), 16
+// positions per pass.  The planner gives every (request, KV head) a single row
+// block, so no other workgroup reads these rows.
+__device__ __forceinline__ void d128_append_rows(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c) {
+  const int first_new = c.kv_len - c.qo_len;
+  const int a0 = max(c.t_first, first_new);
+  const int a1 = c.kv_end;
+  const int tid = threadIdx.x;
+  const int g = tid & 15;
+  const bool is_v = (tid >> 4) & 1;
+  for (int p = a0 + (tid >> 5); p < a1; p += 16) {
+    const int node = p - first_new;
+    const char* src = (is_v ? a.app_v : a.app_k) +
+                      (int64_t(c.qo_start + node) * a.app_stride_token + int64_t(w.kv_head) * a.app_stride_head) * 2;
+    const int32_t pid = a.kv_indices[int64_t(w.page_offset) + (p >> a.page_shift)];
+    char* dst = const_cast<char*>(a.kv) + int64_t(pid) * a.page_stride + int64_t(p & (a.page_size - 1)) * a.token_stride +
+                (is_v ? a.v_offset : 0) + int64_t(w.kv_head) * 256;
+    *reinterpret_cast<uint4*>(dst + g * 16) = *reinterpret_cast<const uint4*>(src + g * 16);
+  }
+}
+
 // 8 waves (two per SIMD), one workgroup per CU.  The item's row-tile count
 // picks the wave layout (d128_item_split / d128_item_rr).
 template <bool BF16>
@@ -1303,6 +1334,12 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   const char* head_base = a.kv + int64_t(w.kv_head) * D * 2;
   const int32_t* pages = a.kv_indices + w.page_offset;
   const uint32_t lds0 = lds_offset(lds);
+  if (a.app_k != nullptr && max(c.t_first, c.kv_len - c.qo_len) < c.kv_end) {
+    // every wave's stores are acknowledged before any wave issues a load
+    d128_append_rows(a, w, c);
+    wait_vmcnt<0>();
+    bare_barrier();
+  }
 
   const int T = __builtin_amdgcn_readfirstlane((w.num_rows + 15) / 16);
   const int R = T & 3;
@@ -1564,7 +1601,7 @@ extern "C" int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int nu
   return launch_status("attn_page_windows_kernel");
 }
 
-extern "C" int atlas_tree_verify_attn(
+static int verify_attn_impl(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
@@ -1574,7 +1611,8 @@ extern "C" int atlas_tree_verify_attn(
     int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
-    void* stream) {
+    void* stream, const void* append_k, const void* append_v, int64_t append_stride_token,
+    int64_t append_stride_head) {
   ATLAS_REQUIRE(q && kv_cache && out, "q, kv_cache and out must not be NULL");
   ATLAS_REQUIRE(qo_indptr_dev && kv_indptr_dev && kv_indices_dev && kv_len_dev,
                 "indptr / indices / kv_len arrays must not be NULL");
@@ -1628,6 +1666,10 @@ extern "C" int atlas_tree_verify_attn(
   args.num_qo_heads = num_qo_heads;
   args.page_size = page_size;
   args.page_shift = ilog2_exact(page_size);
+  args.app_k = static_cast<const char*>(append_k);
+  args.app_v = static_cast<const char*>(append_v);
+  args.app_stride_token = append_stride_token;
+  args.app_stride_head = append_stride_head;
 
   MergeArgs margs{};
   if (num_merge > 0) {
@@ -1657,4 +1699,52 @@ extern "C" int atlas_tree_verify_attn(
                 : launch_attn<128, false>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s);
   return bf16 ? launch_attn<64, true>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s)
               : launch_attn<64, false>(args, num_work, row_tiles, margs, num_merge, max_rows_per_item, s);
+}
+
+extern "C" int atlas_tree_verify_attn(
+    const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
+    const atlas_attn_merge_t* merge_dev,
+    int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
+    int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
+    void* stream) {
+  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
+                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, nullptr,
+                          nullptr, 0, 0);
+}
+
+extern "C" int atlas_tree_verify_attn_append(
+    const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
+    const atlas_attn_merge_t* merge_dev,
+    int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
+    int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
+    const void* append_k, const void* append_v, int64_t append_stride_token, int64_t append_stride_head,
+    void* stream) {
+  ATLAS_REQUIRE(append_k && append_v, "append_k and append_v must not be NULL");
+  if (head_dim != 128 || page_size < 16 || (page_size & (page_size - 1)) != 0) {
+    set_error("the fused append needs head_dim 128 and a power-of-two page_size >= 16");
+    return ATLAS_EUNSUPPORTED;
+  }
+  ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(append_k) & 15) == 0 && (reinterpret_cast<uintptr_t>(append_v) & 15) == 0,
+                "append rows must be 16-byte aligned");
+  ATLAS_REQUIRE(append_stride_token % 8 == 0 && append_stride_head % 8 == 0,
+                "append strides must be multiples of 8 elements");
+  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
+                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, append_k,
+                          append_v, append_stride_token, append_stride_head);
 }

@@ -65,6 +65,9 @@ class AttentionPlan:
     qo_lens: list[int]
     tiles_per_split: int  # most key tiles any work item streams
     page_windows: torch.Tensor | None = None  # int32 [num_work * 64]: first page ids of each item
+    # run(append_key_states=...) can write the newest rows inside the launch:
+    # head_dim-128 kernel, one row block per (request, KV head)
+    fused_append: bool = False
 
     def device_view(self, offset: int) -> int:
         return int(self.meta.data_ptr()) + 4 * offset
@@ -333,6 +336,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             mask_mode=mask_mode, work=work, merge=merge, kv_lens=kv_lens, cols=cols, qo=qo, kvp=kvp,
             qo_lens=qo_lens, indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits,
             partial_rows=partial_rows, max_rows=max_rows, direct=direct, non_blocking=non_blocking)
+        # one row block per (request, KV head): blocks start at row 0 only
+        self._plan.fused_append = direct and all(r0 == 0 for (_, r0, _) in blocks)
 
     def _install(self, *, batch, hq, hkv, d, ps, sm_scale, q_dtype, kv_dtype, mask_mode, work, merge, kv_lens, cols,
                  qo, kvp, qo_lens, indices_src, tree_bits, partial_rows, max_rows, direct, non_blocking) -> None:
@@ -423,7 +428,16 @@ class BatchPrefillWithPagedKVCacheWrapper:
         out: torch.Tensor | None = None,
         lse: torch.Tensor | None = None,
         return_lse: bool = False,
+        append_key_states: torch.Tensor | None = None,
+        append_value_states: torch.Tensor | None = None,
     ):
+        """Attention of the planned batch.  With ``append_key_states`` and
+        ``append_value_states`` ([nnz, Hkv, D], one row per query token), each
+        request's rows are first written to its last qo_len key positions,
+        inside the same launch: ``write_suffix_kv`` followed by ``run`` as one
+        kernel (``flashinfer_full_verify.py:1216-1223``).  Needs a head_dim-128
+        plan with one row block per (request, KV head)
+        (``current_plan.fused_append``); otherwise NotImplementedError."""
         plan = self._plan
         if plan is None:
             raise RuntimeError("plan() must be called before run()")
@@ -474,7 +488,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             raise ValueError("lse must be a contiguous float32 tensor")
         ws_bytes = plan.partial_rows * _partial_row_bytes(plan.head_dim)
         lib = _lib.load()
-        rc = lib.atlas_tree_verify_attn(
+        common = (
             _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride,
             _lib.ptr(plan.qo_indptr), _lib.ptr(plan.kv_indptr), _lib.ptr(plan.kv_indices),
             plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
@@ -484,9 +498,31 @@ class BatchPrefillWithPagedKVCacheWrapper:
             plan.num_qo_heads, plan.num_kv_heads, plan.head_dim, plan.page_size, plan.sm_scale,
             _lib.dtype_code(q.dtype), _lib.ptr(out), out.stride(0), out.stride(1),
             _lib.ptr(lse) if lse is not None else None, _lib.ptr(self._workspace) if ws_bytes else None,
-            ws_bytes, _lib.stream_of(device),
+            ws_bytes,
         )
-        _lib.check(rc, "atlas_tree_verify_attn")
+        if append_key_states is None and append_value_states is None:
+            rc = lib.atlas_tree_verify_attn(*common, _lib.stream_of(device))
+            _lib.check(rc, "atlas_tree_verify_attn")
+        else:
+            k_new, v_new = append_key_states, append_value_states
+            if k_new is None or v_new is None:
+                raise ValueError("append_key_states and append_value_states go together")
+            if not plan.fused_append:
+                raise NotImplementedError(
+                    "the fused append needs a head_dim-128 plan with one row block per (request, KV head); "
+                    "call write_suffix_kv, then run()")
+            _lib.require_device(k_new, v_new, what="fused append")
+            want = (plan.nnz, plan.num_kv_heads, plan.head_dim)
+            for name, t in (("append_key_states", k_new), ("append_value_states", v_new)):
+                if t.ndim != 3 or tuple(t.shape[1:]) != want[1:] or int(t.shape[0]) < plan.nnz:
+                    raise ValueError(f"{name} must be [nnz, {plan.num_kv_heads}, {plan.head_dim}], got {tuple(t.shape)}")
+                if t.dtype != plan.kv_dtype or t.stride(-1) != 1:
+                    raise ValueError(f"{name} must have the cache dtype and contiguous rows")
+            if k_new.stride() != v_new.stride():
+                raise ValueError("append_key_states and append_value_states must have the same strides")
+            rc = lib.atlas_tree_verify_attn_append(*common, _lib.ptr(k_new), _lib.ptr(v_new), k_new.stride(0),
+                                                   k_new.stride(1), _lib.stream_of(device))
+            _lib.check(rc, "atlas_tree_verify_attn_append")
         if want_lse:
             return out, lse
         return out

@@ -136,11 +136,17 @@ class HeadlineStep:
                           causal=False, q_data_type=torch.float16)
         return route_nodes
 
-    def forward(self, with_append=True):
-        """The per-layer device work of the verify forward: append the tree
-        nodes' K/V, then masked attention (append before attention)."""
+    def forward(self, with_append=True, fused=True):
+        """The per-layer device work of the verify forward: write the tree
+        nodes' K/V, then masked attention.  ``fused``: both in one launch per
+        layer (the rows are written inside the attention kernel); otherwise
+        an append launch, then the attention."""
         for l in range(self.geom.layers):
             layer = self.layers[l]
+            if with_append and fused:
+                self.wrapper.run(self.q[l], layer, out=self.outs[l], append_key_states=self.k_new[l],
+                                 append_value_states=self.v_new[l])
+                continue
             if with_append:
                 self.kv_ops.append_paged([layer], [self.k_new[l]], [self.v_new[l]], dst_slots=self.tree_slots)
             self.wrapper.run(self.q[l], layer, out=self.outs[l])
@@ -157,6 +163,9 @@ class HeadlineStep:
             self.forward()
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize()
+        self.graph_fwd_separate = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph_fwd_separate):
+            self.forward(fused=False)
         self.graph_fwd = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph_fwd):
             self.forward()
@@ -202,12 +211,15 @@ class HeadlineStep:
         freed = int(self.free_count.item())
         return int(best.route_id), len(nodes), freed
 
-    def attention_only(self, replays):
+    def attention_only(self, replays, graph=None):
+        """ms per layer of back-to-back replays of the attention graph (or of
+        ``graph``, another 32-layer graph)."""
+        graph = graph if graph is not None else self.graph_attn
         torch.cuda.synchronize()
         a, b = _ev(), _ev()
         a.record()
         for _ in range(replays):
-            self.graph_attn.replay()
+            graph.replay()
         b.record()
         torch.cuda.synchronize()
         return a.elapsed_time(b) / (replays * self.geom.layers)
@@ -728,6 +740,9 @@ def main():
         "components": {
             "attention_us_per_layer": round(attn_us, 3),
             "forward_append_plus_attention_us_per_layer": round(_mean_ms(step.fwd_events) * 1000.0 / 32, 3),
+            "forward_fused_us_per_layer": round(step.attention_only(20, step.graph_fwd) * 1000.0, 3),
+            "forward_separate_append_us_per_layer": round(step.attention_only(20, step.graph_fwd_separate) * 1000.0,
+                                                          3),
             "commit_us": round(_mean_ms(step.commit_events) * 1000.0, 3),
             "prune_us": round(_mean_ms(step.prune_events) * 1000.0, 3),
             "selected_route": route, "committed_tokens": committed, "pruned_pages": freed,

@@ -196,6 +196,34 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
                            int64_t out_stride_token, int64_t out_stride_head, float* lse,
                            void* workspace_dev, size_t workspace_bytes, void* stream);
 
+/* The same attention with the request's newest rows written first: for every
+ * request, the K and V rows of its qo_len query tokens (append_k / append_v,
+ * [token, Hkv, D] with the given strides in elements, token index = the
+ * query row) go to its last qo_len key positions in the paged cache, inside
+ * the attention launch, before any key tile is read.  One launch per layer
+ * instead of write_suffix_kv followed by the attention
+ * (src/atlas_0709/flashinfer_full_verify.py:1216-1222 writes with
+ * write_suffix_kv, :1027-1042, then runs the wrapper, :1223).
+ * head_dim 128 with a power-of-two page_size >= 16 (else ATLAS_EUNSUPPORTED).
+ * The work list must give every (request, KV head) a single row block: the
+ * items covering a request's newest positions write them for their KV head. */
+int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t q_stride_head,
+                                  const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
+                                  int64_t token_stride, const int32_t* qo_indptr_dev,
+                                  const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
+                                  const int32_t* kv_len_dev, int mask_mode,
+                                  const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                                  const atlas_attn_work_t* work_dev, int num_work,
+                                  const int32_t* page_window_dev,
+                                  const atlas_attn_merge_t* merge_dev, int num_merge,
+                                  int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                                  int head_dim, int page_size, float sm_scale, int dtype, void* out,
+                                  int64_t out_stride_token, int64_t out_stride_head, float* lse,
+                                  void* workspace_dev, size_t workspace_bytes,
+                                  const void* append_k, const void* append_v,
+                                  int64_t append_stride_token, int64_t append_stride_head,
+                                  void* stream);
+
 /* ------------------------------------------------------------------------
  * Reachability prune and free-list return.
  * ---------------------------------------------------------------------- */

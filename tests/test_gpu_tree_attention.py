@@ -350,3 +350,107 @@ def test_page_windows_match_page_table_path(dev, split_target):
         if t0 < end:
             p0, lp = t0 // ps, (end - 1) // ps
             assert win[i].tolist() == [order[page_offset + min(p0 + l, lp)] for l in range(64)], f"item {i}"
+
+
+@pytest.mark.parametrize("prefix_len,split_target", [(16384, None), (16384, 1), (300, None), (4000, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_append_matches_append_then_attention(dev, prefix_len, split_target, dtype):
+    """run(append_key_states=, append_value_states=) writes the tree nodes'
+    K/V rows at positions prefix_len + i inside the attention launch: the
+    cache equals the one a separate append leaves (bit-exact), and the
+    output equals the separate append + attention (bit-exact) and the oracle
+    (2e-3).  Split target 1 leaves one split per KV head; 4096 splits the
+    tree positions over several items."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    kv_ops = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(prefix_len + 3)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=prefix_len + 5, prefix_len=prefix_len, routes=routes, dtype=dtype, spare_pages=9)
+    n, ps, hkv, d = c["n"], c["ps"], c["hkv"], c["d"]
+    k_new = (torch.randn((n, hkv, d), generator=gen) * 0.5).to(dtype)
+    v_new = (torch.randn((n, hkv, d), generator=gen) * 0.1).to(dtype)
+    order = c["order"].tolist()
+    pos = [prefix_len + i for i in range(n)]
+    slots = torch.tensor([order[p // ps] * ps + p % ps for p in pos], dtype=torch.int64, device=dev)
+    last = ffv.last_page_len(c["kv_len"], ps)
+    results = []
+    for fused in (False, True):
+        kv = c["kv"].to(dev)
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+        if split_target is not None:
+            w.split_target_items = split_target
+        w.plan(torch.tensor([0, n], dtype=torch.int32, device=dev),
+               torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev), c["order"].to(dev),
+               torch.tensor([last], dtype=torch.int32, device=dev), c["hq"], hkv, d, ps,
+               custom_mask=c["spec"].bool_mask, q_data_type=dtype)
+        assert w.current_plan.fused_append
+        if fused:
+            out, lse = w.run(c["q"].to(dev), kv, return_lse=True, append_key_states=k_new.to(dev),
+                             append_value_states=v_new.to(dev))
+        else:
+            kv_ops.append_paged([kv], [k_new.to(dev)], [v_new.to(dev)], dst_slots=slots)
+            out, lse = w.run(c["q"].to(dev), kv, return_lse=True)
+        torch.cuda.synchronize()
+        results.append((kv.cpu(), out.cpu(), lse.cpu()))
+    (kv_a, out_a, lse_a), (kv_b, out_b, lse_b) = results
+    assert torch.equal(kv_a.view(torch.int16), kv_b.view(torch.int16))
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)) and torch.equal(lse_a, lse_b)
+    ro, rl = oatt.masked_attention(c["q"].double().numpy(), kv_b.double().numpy(), [0, n], [0, c["pages"]],
+                                   order, [last], masks=[c["mask"]])
+    assert float(np.abs(out_b.float().numpy() - ro).max()) <= ATOL
+    assert float(np.abs(lse_b.numpy() - rl).max()) <= ATOL
+
+
+def test_fused_append_batched_requests_and_refusals(dev):
+    """Two ragged requests in one plan (causal mode, each appending its own
+    newest rows), then the cases the fused append refuses: several row blocks
+    per KV head (the rows could be read by another block before they are
+    written) and head_dim 64."""
+    ta = pkg("tree_attention")
+    gen = torch.Generator().manual_seed(77)
+    hq, hkv, d, ps = 32, 8, 128, 16
+    qo_lens, kv_lens = [5, 11], [700, 2100]
+    pages = [math.ceil(k / ps) for k in kv_lens]
+    pool = sum(pages) + 5
+    perm = torch.randperm(pool, generator=gen).tolist()
+    table = [perm[: pages[0]], perm[pages[0]: pages[0] + pages[1]]]
+    kv = (torch.randn((pool, 2, ps, hkv, d), generator=gen) * 0.3).half()
+    q = (torch.randn((sum(qo_lens), hq, d), generator=gen) * 0.3).half()
+    k_new = (torch.randn((sum(qo_lens), hkv, d), generator=gen) * 0.3).half()
+    v_new = (torch.randn((sum(qo_lens), hkv, d), generator=gen) * 0.1).half()
+    qo = [0, qo_lens[0], sum(qo_lens)]
+    kvp = [0, pages[0], sum(pages)]
+    last = [k - (p - 1) * ps for k, p in zip(kv_lens, pages)]
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32), torch.tensor(kvp, dtype=torch.int32),
+           torch.tensor(table[0] + table[1], dtype=torch.int32, device=dev), torch.tensor(last, dtype=torch.int32),
+           hq, hkv, d, ps, causal=True, q_data_type=torch.float16)
+    kv_dev = kv.to(dev)
+    out = w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev))
+    torch.cuda.synchronize()
+    expect = kv.clone()
+    for b in range(2):
+        for i in range(qo_lens[b]):
+            p = kv_lens[b] - qo_lens[b] + i
+            expect[table[b][p // ps], 0, p % ps] = k_new[qo[b] + i]
+            expect[table[b][p // ps], 1, p % ps] = v_new[qo[b] + i]
+    got = kv_dev.cpu()
+    assert torch.equal(got.view(torch.int16), expect.view(torch.int16))
+    ro, _ = oatt.masked_attention(q.double().numpy(), expect.double().numpy(), qo, kvp, table[0] + table[1], last,
+                                  causal=True)
+    assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+    # several row blocks per KV head: refused
+    w.max_rows_per_item = 16
+    w.plan(torch.tensor(qo, dtype=torch.int32), torch.tensor(kvp, dtype=torch.int32),
+           torch.tensor(table[0] + table[1], dtype=torch.int32, device=dev), torch.tensor(last, dtype=torch.int32),
+           hq, hkv, d, ps, causal=True, q_data_type=torch.float16)
+    assert not w.current_plan.fused_append
+    with pytest.raises(NotImplementedError):
+        w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev))
+    # head_dim 64: refused
+    w64 = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(8 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w64.plan(torch.tensor([0, 2], dtype=torch.int32), torch.tensor([0, 1], dtype=torch.int32),
+             torch.tensor([0], dtype=torch.int32, device=dev), torch.tensor([5], dtype=torch.int32),
+             8, 8, 64, 16, causal=True, q_data_type=torch.float16)
+    assert not w64.current_plan.fused_append
