@@ -15,7 +15,7 @@ def _rand(gen, shape, dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
-@pytest.mark.parametrize("layers,heads,dim", [(2, 8, 64), (3, 8, 128), (1, 2, 64)])
+@pytest.mark.parametrize("layers,heads,dim", [(2, 8, 64), (3, 8, 128), (1, 2, 64), (17, 8, 64), (9, 8, 128)])
 def test_move_slots_matches_values_dst_eq_src(dev, dtype, layers, heads, dim):
     kv = pkg("kv_ops")
     gen = torch.Generator().manual_seed(1)
