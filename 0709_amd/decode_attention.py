@@ -53,6 +53,8 @@ from .tree_attention import (
 # Routes whose page lists begin with at least this many identical full pages
 # share one cascade prefix pass.
 CASCADE_MIN_SHARED_PAGES = 2
+# Shortest key split of a cascade's long streams, in 64-key tiles.
+CASCADE_MIN_TILES_PER_SPLIT = 2
 
 
 def _unit_scale(value, name: str) -> None:
@@ -224,15 +226,16 @@ class BatchDecodeWithPagedKVCacheWrapper:
                 yield t0, t0 + per + (1 if s_ < extra else 0)
 
         # Split the long streams (shared prefixes, and whole routes outside
-        # groups) so that all items together fill the device about twice, the
-        # long streams alone at least once (the per-route tails are short).
+        # groups) so that they alone fill the device about twice, in splits of
+        # at least CASCADE_MIN_TILES_PER_SPLIT tiles: the per-route tails are
+        # short and add their own items; shorter splits cost more merge work
+        # than they gain.
         tail_items = sum(hkv * n for _, n, _ in groups if n > 1)
         long_tiles = sum(hkv * tiles(c * ps if n > 1 else kv_lens[g0]) for g0, n, c in groups)
         if pf.split_target_items is not None:
-            long_target = max(1, pf.split_target_items - tail_items)
+            tiles_per_split = max(1.0, long_tiles / max(1, pf.split_target_items - tail_items))
         else:
-            long_target = max(DEFAULT_CU_COUNT, 2 * DEFAULT_CU_COUNT - tail_items)
-        tiles_per_split = max(1.0, long_tiles / long_target)
+            tiles_per_split = max(float(CASCADE_MIN_TILES_PER_SPLIT), long_tiles / (2 * DEFAULT_CU_COUNT))
         ws_rows_cap = pf._workspace.numel() * pf._workspace.element_size() // _partial_row_bytes(d)
         while True:
             work, merge, qo, qo_lens, plan_kv_lens = [], [], [0], [], []

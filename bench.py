@@ -484,7 +484,7 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
             "hot_us": hot_us, "hot_GBps": 2 * moved / (hot_us * 1e-6) / 1e9}
 
 
-def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, cascade=True):
+def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, cascade=True, split_target=None):
     """Drafter paged decode attention (Llama-3.2-1B geometry: 16 layers, 32 q
     heads, 8 KV heads, head_dim 64; bf16, page 64): ``requests`` x ``routes``
     forked routes, one query each.  The routes of a request share its full
@@ -531,6 +531,7 @@ def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, 
     ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
     w = da.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
     w.use_cascade = cascade
+    w.split_target_items = split_target
     w.plan(torch.tensor(indptr, dtype=torch.int32, device=dev), torch.tensor(phys, dtype=torch.int32, device=dev),
            torch.tensor(last, dtype=torch.int32, device=dev), geom.q_heads, geom.kv_heads, geom.head_dim, ps,
            data_type=torch.bfloat16, q_data_type=torch.bfloat16)
