@@ -69,6 +69,12 @@ struct AttnArgs {
   const char* app_v;
   int64_t app_stride_token;
   int64_t app_stride_head;
+  // Rotary embedding of the fused step, or null: cos / sin rows [token, D]
+  // (stride in elements, token index = the query row) rotate the queries as
+  // they are read and the appended K rows before they are written.
+  const char* rope_cos;
+  const char* rope_sin;
+  int64_t rope_stride_token;
   float scale_log2;  // sm_scale * log2(e)
   int mask_mode;
   int group;
@@ -134,6 +140,50 @@ struct Mfma<true> {
                                            bf16x2v{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
   }
 };
+
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+
+template <bool BF16>
+__device__ __forceinline__ float half_to_float(uint32_t bits) {
+  if constexpr (BF16) return __builtin_bit_cast(float, bits << 16);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, uint16_t(bits)));
+}
+
+// Rounds to the 16-bit type and back.
+template <bool BF16>
+__device__ __forceinline__ float round16(float x) {
+  return half_to_float<BF16>(Mfma<BF16>::from_float(x));
+}
+
+// Rotary embedding of 8 consecutive 16-bit elements x at dims d .. d+7 with
+// their rotate-half partners xp (dims d +- D/2) and the cos / sin of the same
+// dims, rounded like the elementwise 16-bit tensor ops it replaces
+// (q * cos + rotate_half(q) * sin, src/atlas_0709/flashinfer_full_verify.py:324-333):
+// each product is rounded to the 16-bit type, then their sum.  rotate_half
+// negates the second half, so the first half subtracts.  (A 16-bit product of
+// 16-bit operands is exact in fp32 and fp32 carries more than 2p + 2 bits, so
+// computing in fp32 and rounding once per op equals the 16-bit ops.)
+template <bool BF16>
+__device__ __forceinline__ u32x4v rope8(u32x4v x, u32x4v xp, u32x4v c, u32x4v s, bool first_half) {
+  // Contracting a product into the sum (a 16-bit FMA) would skip its rounding.
+#pragma clang fp contract(off)
+  u32x4v r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t packed = 0;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const int sh = 16 * h;
+      const float a = round16<BF16>(half_to_float<BF16>((x[i] >> sh) & 0xffffu) *
+                                    half_to_float<BF16>((c[i] >> sh) & 0xffffu));
+      const float b = round16<BF16>(half_to_float<BF16>((xp[i] >> sh) & 0xffffu) *
+                                    half_to_float<BF16>((s[i] >> sh) & 0xffffu));
+      packed |= uint32_t(Mfma<BF16>::from_float(first_half ? a - b : a + b)) << sh;
+    }
+    r[i] = packed;
+  }
+  return r;
+}
 
 // Visibility of the four keys p0 .. p0+3 a lane holds in one 16-key block
 // (bit i for key p0 + i), branch-free: keys at or past kv_end are hidden; in
@@ -775,6 +825,10 @@ struct RowState {
   int head_of[RT];
   int lrow[RT];  // row index inside the item
   bool row_ok[RT];
+  // Rotary cos / sin of the lane's query granules (fused step with RoPE):
+  // granule ks * 4 + grp of each row tile's node, live until d128_read_q.
+  u32x4v rcos[RT][4];
+  u32x4v rsin[RT][4];
 };
 
 // Scores S^T = K Q^T of the NKT 16-key blocks kb0 .. kb0+NKT-1 of one tile for
@@ -969,6 +1023,18 @@ __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const Att
     st.tbits[rt] = 0ull;
     st.climit[rt] = c.kv_len - c.qo_len + st.node_of[rt];
   }
+  if (a.rope_cos != nullptr) {
+    // Issued ahead of the page windows: ring_begin's wait covers both.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const int64_t off = int64_t(c.qo_start + st.node_of[rt]) * a.rope_stride_token * 2;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        st.rcos[rt][ks] = *reinterpret_cast<const u32x4v*>(a.rope_cos + off + (ks * 4 + grp) * 16);
+        st.rsin[rt][ks] = *reinterpret_cast<const u32x4v*>(a.rope_sin + off + (ks * 4 + grp) * 16);
+      }
+    }
+  }
 }
 
 // The rows' tree ancestor words.  Loaded after the ring's first tiles are
@@ -983,10 +1049,11 @@ __device__ __forceinline__ void d128_load_masks(RowState<BF16, RT>& st, const At
 }
 
 // Queries of the wave's rows from the LDS staging area into registers (rows
-// past num_rows are zeroed).  Runs right after the first ring step: stage 3
-// is overwritten only after the next barrier.
+// past num_rows are zeroed), rotated when the step carries RoPE tables.  Runs
+// right after the first ring step: stage 3 is overwritten only after the next
+// barrier.
 template <bool BF16, int RT>
-__device__ __forceinline__ void d128_read_q(RowState<BF16, RT>& st, const char* lds, int lane) {
+__device__ __forceinline__ void d128_read_q(RowState<BF16, RT>& st, const char* lds, bool rope, int lane) {
   typedef typename Mfma<BF16>::frag frag;
   const int grp = lane >> 4;
   const int r16 = lane & 15;
@@ -999,6 +1066,19 @@ __device__ __forceinline__ void d128_read_q(RowState<BF16, RT>& st, const char* 
       if (!st.row_ok[rt]) v = uint4{0, 0, 0, 0};
       st.qf[rt][ks] = __builtin_bit_cast(frag, v);
     }
+  }
+  if (rope) {
+    // Granules ks and ks + 2 hold dims d and d + D/2: each other's partners.
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4v lo = __builtin_bit_cast(u32x4v, st.qf[rt][ks]);
+        const u32x4v hi = __builtin_bit_cast(u32x4v, st.qf[rt][ks + 2]);
+        st.qf[rt][ks] = __builtin_bit_cast(frag, rope8<BF16>(lo, hi, st.rcos[rt][ks], st.rsin[rt][ks], true));
+        st.qf[rt][ks + 2] =
+            __builtin_bit_cast(frag, rope8<BF16>(hi, lo, st.rcos[rt][ks + 2], st.rsin[rt][ks + 2], false));
+      }
   }
 }
 
@@ -1014,7 +1094,7 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
   const int nt = r.nt;
   if (nt <= 0) return;
   ring_first<NL>(r);
-  d128_read_q<BF16, RT>(st, lds, lane);
+  d128_read_q<BF16, RT>(st, lds, a.rope_cos != nullptr, lane);
   if constexpr (PIPE) {
     f32x4 s_cur[RT][NKT];
     f32x4 s_nxt[RT][NKT];
@@ -1276,8 +1356,9 @@ __device__ __forceinline__ void ring_init(Ring<NL>& r, const AttnArgs& a, const 
 // are copied, for this item's KV head, from the caller's K / V rows into the
 // paged cache before any tile is loaded (the loads of the masked tail tile
 // read them back).  32 lanes per position (16 granules of K, 16 of V), 16
-// positions per pass.  The planner gives every (request, KV head) a single row
+// positions per pass; with RoPE tables the K granules are rotated on the way.  The planner gives every (request, KV head) a single row
 // block, so no other workgroup reads these rows.
+template <bool BF16>
 __device__ __forceinline__ void d128_append_rows(const AttnArgs& a, const atlas_attn_work_t& w, const ItemCtx& c) {
   const int first_new = c.kv_len - c.qo_len;
   const int a0 = max(c.t_first, first_new);
@@ -1292,7 +1373,14 @@ __device__ __forceinline__ void d128_append_rows(const AttnArgs& a, const atlas_
     const int32_t pid = a.kv_indices[int64_t(w.page_offset) + (p >> a.page_shift)];
     char* dst = const_cast<char*>(a.kv) + int64_t(pid) * a.page_stride + int64_t(p & (a.page_size - 1)) * a.token_stride +
                 (is_v ? a.v_offset : 0) + int64_t(w.kv_head) * 256;
-    *reinterpret_cast<uint4*>(dst + g * 16) = *reinterpret_cast<const uint4*>(src + g * 16);
+    u32x4v v = *reinterpret_cast<const u32x4v*>(src + g * 16);
+    if (a.rope_cos != nullptr && !is_v) {
+      const int64_t off = int64_t(c.qo_start + node) * a.rope_stride_token * 2 + g * 16;
+      const u32x4v partner = *reinterpret_cast<const u32x4v*>(src + (g ^ 8) * 16);
+      v = rope8<BF16>(v, partner, *reinterpret_cast<const u32x4v*>(a.rope_cos + off),
+                      *reinterpret_cast<const u32x4v*>(a.rope_sin + off), g < 8);
+    }
+    *reinterpret_cast<u32x4v*>(dst + g * 16) = v;
   }
 }
 
@@ -1336,7 +1424,7 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   const uint32_t lds0 = lds_offset(lds);
   if (a.app_k != nullptr && max(c.t_first, c.kv_len - c.qo_len) < c.kv_end) {
     // every wave's stores are acknowledged before any wave issues a load
-    d128_append_rows(a, w, c);
+    d128_append_rows<BF16>(a, w, c);
     wait_vmcnt<0>();
     bare_barrier();
   }
@@ -1612,7 +1700,7 @@ static int verify_attn_impl(
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream, const void* append_k, const void* append_v, int64_t append_stride_token,
-    int64_t append_stride_head) {
+    int64_t append_stride_head, const void* rope_cos, const void* rope_sin, int64_t rope_stride_token) {
   ATLAS_REQUIRE(q && kv_cache && out, "q, kv_cache and out must not be NULL");
   ATLAS_REQUIRE(qo_indptr_dev && kv_indptr_dev && kv_indices_dev && kv_len_dev,
                 "indptr / indices / kv_len arrays must not be NULL");
@@ -1670,6 +1758,9 @@ static int verify_attn_impl(
   args.app_v = static_cast<const char*>(append_v);
   args.app_stride_token = append_stride_token;
   args.app_stride_head = append_stride_head;
+  args.rope_cos = static_cast<const char*>(rope_cos);
+  args.rope_sin = static_cast<const char*>(rope_sin);
+  args.rope_stride_token = rope_stride_token;
 
   MergeArgs margs{};
   if (num_merge > 0) {
@@ -1717,7 +1808,7 @@ extern "C" int atlas_tree_verify_attn(
                           mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, nullptr,
-                          nullptr, 0, 0);
+                          nullptr, 0, 0, nullptr, nullptr, 0);
 }
 
 extern "C" int atlas_tree_verify_attn_append(
@@ -1731,8 +1822,12 @@ extern "C" int atlas_tree_verify_attn_append(
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     const void* append_k, const void* append_v, int64_t append_stride_token, int64_t append_stride_head,
-    void* stream) {
+    const void* rope_cos, const void* rope_sin, int64_t rope_stride_token, void* stream) {
   ATLAS_REQUIRE(append_k && append_v, "append_k and append_v must not be NULL");
+  ATLAS_REQUIRE((rope_cos == nullptr) == (rope_sin == nullptr), "rope_cos and rope_sin go together");
+  ATLAS_REQUIRE(rope_cos == nullptr || ((reinterpret_cast<uintptr_t>(rope_cos) & 15) == 0 &&
+                                        (reinterpret_cast<uintptr_t>(rope_sin) & 15) == 0 && rope_stride_token % 8 == 0),
+                "rope tables must be 16-byte aligned with a token stride that is a multiple of 8 elements");
   if (head_dim != 128 || page_size < 16 || (page_size & (page_size - 1)) != 0) {
     set_error("the fused append needs head_dim 128 and a power-of-two page_size >= 16");
     return ATLAS_EUNSUPPORTED;
@@ -1746,5 +1841,5 @@ extern "C" int atlas_tree_verify_attn_append(
                           mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, append_k,
-                          append_v, append_stride_token, append_stride_head);
+                          append_v, append_stride_token, append_stride_head, rope_cos, rope_sin, rope_stride_token);
 }

@@ -118,6 +118,20 @@ def unpack_bits_little(packed: torch.Tensor, count: int) -> torch.Tensor:
     return bits.reshape(-1)[:count].to(torch.bool)
 
 
+def _rope_table(t: torch.Tensor, name: str, plan: AttentionPlan, dtype: torch.dtype) -> torch.Tensor:
+    """A rotary cos or sin table as [rows, D] with contiguous, 16-byte aligned rows."""
+    if t.shape[-1] != plan.head_dim or t.stride(-1) != 1:
+        raise ValueError(f"rope {name} rows must be contiguous [.., {plan.head_dim}], got {tuple(t.shape)}")
+    t = t.reshape(-1, plan.head_dim)
+    if int(t.shape[0]) < plan.nnz:
+        raise ValueError(f"rope {name} has {int(t.shape[0])} rows for {plan.nnz} query tokens")
+    if t.dtype != dtype:
+        raise TypeError(f"rope {name} must have q's dtype {dtype}, got {t.dtype}")
+    if t.stride(0) % 8 != 0 or int(t.data_ptr()) % 16 != 0:
+        t = t.contiguous()
+    return t
+
+
 class BatchPrefillWithPagedKVCacheWrapper:
     """Paged prefill attention with a custom (tree) mask on the gfx950 kernel.
 
@@ -430,6 +444,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         return_lse: bool = False,
         append_key_states: torch.Tensor | None = None,
         append_value_states: torch.Tensor | None = None,
+        rope_cos_sin: tuple[torch.Tensor, torch.Tensor] | None = None,
     ):
         """Attention of the planned batch.  With ``append_key_states`` and
         ``append_value_states`` ([nnz, Hkv, D], one row per query token), each
@@ -437,7 +452,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
         inside the same launch: ``write_suffix_kv`` followed by ``run`` as one
         kernel (``flashinfer_full_verify.py:1216-1223``).  Needs a head_dim-128
         plan with one row block per (request, KV head)
-        (``current_plan.fused_append``); otherwise NotImplementedError."""
+        (``current_plan.fused_append``); otherwise NotImplementedError.
+
+        ``rope_cos_sin=(cos, sin)`` ([nnz, D] in q's dtype, row = query token,
+        as ``rope_cos_sin`` returns them, ``flashinfer_full_verify.py:259-301``)
+        goes with the fused append: ``q`` and ``append_key_states`` are then
+        the projections before the rotary embedding, and the launch applies
+        ``apply_rope_with_cos_sin`` (``:324-333``, called at ``:1213``) itself,
+        with the same rounding, so the cache receives the K rows the reference
+        writes, bit for bit."""
         plan = self._plan
         if plan is None:
             raise RuntimeError("plan() must be called before run()")
@@ -501,6 +524,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             ws_bytes,
         )
         if append_key_states is None and append_value_states is None:
+            if rope_cos_sin is not None:
+                raise NotImplementedError("rope_cos_sin is applied only together with the fused append")
             rc = lib.atlas_tree_verify_attn(*common, _lib.stream_of(device))
             _lib.check(rc, "atlas_tree_verify_attn")
         else:
@@ -520,8 +545,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
                     raise ValueError(f"{name} must have the cache dtype and contiguous rows")
             if k_new.stride() != v_new.stride():
                 raise ValueError("append_key_states and append_value_states must have the same strides")
+            cos = sin = None
+            if rope_cos_sin is not None:
+                cos, sin = (_rope_table(t, name, plan, q.dtype) for t, name in zip(rope_cos_sin, ("cos", "sin")))
+                _lib.require_device(cos, sin, what="rotary tables")
+                if cos.stride(0) != sin.stride(0):
+                    raise ValueError("rope cos and sin must have the same row stride")
             rc = lib.atlas_tree_verify_attn_append(*common, _lib.ptr(k_new), _lib.ptr(v_new), k_new.stride(0),
-                                                   k_new.stride(1), _lib.stream_of(device))
+                                                   k_new.stride(1), _lib.ptr(cos), _lib.ptr(sin),
+                                                   cos.stride(0) if cos is not None else 0, _lib.stream_of(device))
             _lib.check(rc, "atlas_tree_verify_attn_append")
         if want_lse:
             return out, lse

@@ -88,6 +88,12 @@ class HeadlineStep:
         shp = (self.n, self.geom.kv_heads, self.geom.head_dim)
         self.k_new = [(torch.randn(shp, generator=g, device=dev) * 0.1).half() for _ in range(self.geom.layers)]
         self.v_new = [(torch.randn(shp, generator=g, device=dev) * 0.1).half() for _ in range(self.geom.layers)]
+        # rotary tables of the tree positions (prefix_len + depth), fp32 angles
+        # rounded to the dtype, Llama-3.1 theta
+        inv = 1.0 / (500000.0 ** (torch.arange(0, self.geom.head_dim, 2, dtype=torch.float32) / self.geom.head_dim))
+        emb = torch.outer((prefix_len + spec.depths.cpu()).float(), inv)
+        emb = torch.cat((emb, emb), dim=-1)
+        self.rope_cos, self.rope_sin = emb.cos().half().to(dev), emb.sin().half().to(dev)
         self.verify_logits = (torch.randn((self.n, 128256), generator=g, device=dev) * 2.0).half()
         self.prefix_logits = (torch.randn((128256,), generator=g, device=dev) * 2.0).half()
         ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
@@ -136,13 +142,28 @@ class HeadlineStep:
                           causal=False, q_data_type=torch.float16)
         return route_nodes
 
-    def forward(self, with_append=True, fused=True):
+    def _rotate(self, x):
+        h = x.shape[-1] // 2
+        cos, sin = self.rope_cos[:, None, :], self.rope_sin[:, None, :]
+        return (x * cos) + (torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin)
+
+    def forward(self, with_append=True, fused=True, rope=None):
         """The per-layer device work of the verify forward: write the tree
         nodes' K/V, then masked attention.  ``fused``: both in one launch per
         layer (the rows are written inside the attention kernel); otherwise
-        an append launch, then the attention."""
+        an append launch, then the attention.  ``rope``: the queries and keys
+        arrive before the rotary embedding, which runs inside the launch
+        ("fused") or as the reference's torch ops ahead of it ("torch")."""
         for l in range(self.geom.layers):
             layer = self.layers[l]
+            if rope == "fused":
+                self.wrapper.run(self.q[l], layer, out=self.outs[l], append_key_states=self.k_new[l],
+                                 append_value_states=self.v_new[l], rope_cos_sin=(self.rope_cos, self.rope_sin))
+                continue
+            if rope == "torch":
+                self.wrapper.run(self._rotate(self.q[l]), layer, out=self.outs[l],
+                                 append_key_states=self._rotate(self.k_new[l]), append_value_states=self.v_new[l])
+                continue
             if with_append and fused:
                 self.wrapper.run(self.q[l], layer, out=self.outs[l], append_key_states=self.k_new[l],
                                  append_value_states=self.v_new[l])
@@ -166,6 +187,12 @@ class HeadlineStep:
         self.graph_fwd_separate = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph_fwd_separate):
             self.forward(fused=False)
+        self.graph_fwd_rope = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph_fwd_rope):
+            self.forward(rope="fused")
+        self.graph_fwd_torch_rope = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph_fwd_torch_rope):
+            self.forward(rope="torch")
         self.graph_fwd = torch.cuda.CUDAGraph()
         with torch.cuda.graph(self.graph_fwd):
             self.forward()
@@ -744,6 +771,9 @@ def main():
             "forward_fused_us_per_layer": round(step.attention_only(20, step.graph_fwd) * 1000.0, 3),
             "forward_separate_append_us_per_layer": round(step.attention_only(20, step.graph_fwd_separate) * 1000.0,
                                                           3),
+            "forward_fused_rope_us_per_layer": round(step.attention_only(20, step.graph_fwd_rope) * 1000.0, 3),
+            "forward_torch_rope_then_fused_us_per_layer": round(
+                step.attention_only(20, step.graph_fwd_torch_rope) * 1000.0, 3),
             "commit_us": round(_mean_ms(step.commit_events) * 1000.0, 3),
             "prune_us": round(_mean_ms(step.prune_events) * 1000.0, 3),
             "selected_route": route, "committed_tokens": committed, "pruned_pages": freed,

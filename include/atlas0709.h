@@ -206,7 +206,13 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
  * write_suffix_kv, :1027-1042, then runs the wrapper, :1223).
  * head_dim 128 with a power-of-two page_size >= 16 (else ATLAS_EUNSUPPORTED).
  * The work list must give every (request, KV head) a single row block: the
- * items covering a request's newest positions write them for their KV head. */
+ * items covering a request's newest positions write them for their KV head.
+ * rope_cos / rope_sin (both or neither; [token, D] rows, stride in elements,
+ * token index = the query row): q and append_k arrive before the rotary
+ * embedding, which is applied in the launch with the rounding of the 16-bit
+ * tensor ops q * cos + rotate_half(q) * sin that it replaces
+ * (apply_rope_with_cos_sin, src/atlas_0709/flashinfer_full_verify.py:324-333,
+ * called at :1213): the cache receives the rotated K rows bit for bit. */
 int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                                   const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
                                   int64_t token_stride, const int32_t* qo_indptr_dev,
@@ -222,7 +228,8 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
                                   void* workspace_dev, size_t workspace_bytes,
                                   const void* append_k, const void* append_v,
                                   int64_t append_stride_token, int64_t append_stride_head,
-                                  void* stream);
+                                  const void* rope_cos, const void* rope_sin,
+                                  int64_t rope_stride_token, void* stream);
 
 /* ------------------------------------------------------------------------
  * Reachability prune and free-list return.

@@ -24,6 +24,11 @@ Pinning (what each function is checked against in ``tests/``):
                              SGLang's own allocator is absent: parity unpinned
                              against it (only against this restated policy).
 * ``scoring``             -- reference literals (test_target_kv_commit.py:76-367)
+* ``rope.apply_rope``     -- torch's own 16-bit elementwise ops on the CPU
+                             (q * cos + rotate_half(q) * sin, bit for bit, f16
+                             and bf16), the identity at angle 0, rotate_half at
+                             cos 0 / sin 1, and a plain fp32 rotation within
+                             one 16-bit rounding step
 * ``route_pool``          -- host pools for the route-pool trace: the
                              ``PagedAllocator`` policy above, slot contents as
                              value ids with ``move_kv_cache`` = FakeKVCache

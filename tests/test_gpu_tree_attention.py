@@ -454,3 +454,133 @@ def test_fused_append_batched_requests_and_refusals(dev):
              torch.tensor([0], dtype=torch.int32, device=dev), torch.tensor([5], dtype=torch.int32),
              8, 8, 64, 16, causal=True, q_data_type=torch.float16)
     assert not w64.current_plan.fused_append
+
+
+def _rope_tables(positions: torch.Tensor, d: int, dtype: torch.dtype, theta: float = 500000.0):
+    """cos / sin rows as the reference builds them without a rotary module
+    (flashinfer_full_verify.py:242-256): fp32 angles, rounded to the dtype."""
+    inv = 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat((torch.outer(positions.float(), inv),) * 2, dim=-1)
+    return emb.cos().to(dtype), emb.sin().to(dtype)
+
+
+def _torch_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """apply_rope_with_cos_sin (flashinfer_full_verify.py:324-333) as 16-bit tensor ops."""
+    h = x.shape[-1] // 2
+    return (x * cos[:, None, :]) + (torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin[:, None, :])
+
+
+@pytest.mark.parametrize("prefix_len,split_target", [(16384, None), (300, None), (4000, 4096)])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_fused_rope_matches_reference_rope_then_append(dev, prefix_len, split_target, dtype):
+    """run(..., rope_cos_sin=(cos, sin)) given the projections before the
+    rotary embedding (positions prefix_len + depth, as the reference's verify
+    step builds them, flashinfer_full_verify.py:1197-1213): the cache holds
+    the K rows that the reference's rotation + write_suffix_kv leave and the
+    oracle's per-op rounding gives (bit-exact), and the output equals the
+    attention of the torch-rotated queries (bit-exact) and the oracle (2e-3)."""
+    from oracle import rope as orope
+
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    kv_ops = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(prefix_len + 11)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=prefix_len + 13, prefix_len=prefix_len, routes=routes, dtype=dtype, spare_pages=9)
+    n, ps, hkv, d, hq = c["n"], c["ps"], c["hkv"], c["d"], c["hq"]
+    q_raw = (torch.randn((n, hq, d), generator=gen) * 2.0).to(dtype)
+    k_raw = (torch.randn((n, hkv, d), generator=gen) * 2.0).to(dtype)
+    v_new = (torch.randn((n, hkv, d), generator=gen) * 0.1).to(dtype)
+    cos, sin = _rope_tables(prefix_len + c["spec"].depths.cpu(), d, dtype)
+    cos_d, sin_d = cos.to(dev), sin.to(dev)
+    q_rot = _torch_rope(q_raw.to(dev), cos_d, sin_d)
+    k_rot = _torch_rope(k_raw.to(dev), cos_d, sin_d)
+    odt = "f16" if dtype == torch.float16 else "bf16"
+    k_or = orope.apply_rope(k_raw.float().numpy(), cos.float().numpy(), sin.float().numpy(), odt)
+    assert np.array_equal(k_rot.float().cpu().numpy(), k_or)
+    order = c["order"].tolist()
+    slots = torch.tensor([order[p // ps] * ps + p % ps for p in range(prefix_len, prefix_len + n)],
+                         dtype=torch.int64, device=dev)
+    last = ffv.last_page_len(c["kv_len"], ps)
+    results = []
+    for fused in (False, True):
+        kv = c["kv"].to(dev)
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+        if split_target is not None:
+            w.split_target_items = split_target
+        w.plan(torch.tensor([0, n], dtype=torch.int32, device=dev),
+               torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev), c["order"].to(dev),
+               torch.tensor([last], dtype=torch.int32, device=dev), hq, hkv, d, ps,
+               custom_mask=c["spec"].bool_mask, q_data_type=dtype)
+        if fused:
+            out, lse = w.run(q_raw.to(dev), kv, return_lse=True, append_key_states=k_raw.to(dev),
+                             append_value_states=v_new.to(dev), rope_cos_sin=(cos_d, sin_d))
+        else:
+            kv_ops.append_paged([kv], [k_rot], [v_new.to(dev)], dst_slots=slots)
+            out, lse = w.run(q_rot, kv, return_lse=True)
+        torch.cuda.synchronize()
+        results.append((kv.cpu(), out.cpu(), lse.cpu()))
+    (kv_a, out_a, lse_a), (kv_b, out_b, lse_b) = results
+    assert torch.equal(kv_a.view(torch.int16), kv_b.view(torch.int16))
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)) and torch.equal(lse_a, lse_b)
+    ro, rl = oatt.masked_attention(q_rot.double().cpu().numpy(), kv_b.double().numpy(), [0, n], [0, c["pages"]],
+                                   order, [last], masks=[c["mask"]])
+    assert float(np.abs(out_b.float().numpy() - ro).max()) <= ATOL
+    assert float(np.abs(lse_b.numpy() - rl).max()) <= ATOL
+
+
+def test_fused_rope_batched_requests_and_refusals(dev):
+    """Two ragged causal requests whose cos / sin rows follow their own
+    positions (table row = query row): the cache gets the oracle-rotated K
+    rows and V rows unchanged, and the output matches the oracle on the
+    oracle-rotated queries.  Then the refusals: RoPE without the fused
+    append, tables of another dtype, too few table rows."""
+    from oracle import rope as orope
+
+    ta = pkg("tree_attention")
+    gen = torch.Generator().manual_seed(91)
+    hq, hkv, d, ps = 32, 8, 128, 32
+    qo_lens, kv_lens = [6, 13], [900, 2500]
+    pages = [math.ceil(k / ps) for k in kv_lens]
+    pool = sum(pages) + 3
+    perm = torch.randperm(pool, generator=gen).tolist()
+    table = [perm[: pages[0]], perm[pages[0]: pages[0] + pages[1]]]
+    dt = torch.bfloat16
+    kv = (torch.randn((pool, 2, ps, hkv, d), generator=gen) * 0.3).to(dt)
+    q = (torch.randn((sum(qo_lens), hq, d), generator=gen) * 0.5).to(dt)
+    k_new = (torch.randn((sum(qo_lens), hkv, d), generator=gen) * 0.5).to(dt)
+    v_new = (torch.randn((sum(qo_lens), hkv, d), generator=gen) * 0.1).to(dt)
+    positions = torch.cat([torch.arange(k - l, k) for k, l in zip(kv_lens, qo_lens)])
+    cos, sin = _rope_tables(positions, d, dt)
+    qo = [0, qo_lens[0], sum(qo_lens)]
+    kvp = [0, pages[0], sum(pages)]
+    last = [k - (p - 1) * ps for k, p in zip(kv_lens, pages)]
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), "NHD")
+    w.plan(torch.tensor(qo, dtype=torch.int32), torch.tensor(kvp, dtype=torch.int32),
+           torch.tensor(table[0] + table[1], dtype=torch.int32, device=dev), torch.tensor(last, dtype=torch.int32),
+           hq, hkv, d, ps, causal=True, q_data_type=dt)
+    kv_dev = kv.to(dev)
+    out = w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev),
+                rope_cos_sin=(cos.to(dev), sin.to(dev)))
+    torch.cuda.synchronize()
+    k_rot = torch.from_numpy(orope.apply_rope(k_new.float().numpy(), cos.float().numpy(), sin.float().numpy(),
+                                              "bf16")).to(dt)
+    q_rot = orope.apply_rope(q.float().numpy(), cos.float().numpy(), sin.float().numpy(), "bf16")
+    expect = kv.clone()
+    for b in range(2):
+        for i in range(qo_lens[b]):
+            p = kv_lens[b] - qo_lens[b] + i
+            expect[table[b][p // ps], 0, p % ps] = k_rot[qo[b] + i]
+            expect[table[b][p // ps], 1, p % ps] = v_new[qo[b] + i]
+    assert torch.equal(kv_dev.cpu().view(torch.int16), expect.view(torch.int16))
+    ro, _ = oatt.masked_attention(q_rot.astype(np.float64), expect.double().numpy(), qo, kvp,
+                                  table[0] + table[1], last, causal=True)
+    assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+    with pytest.raises(NotImplementedError):
+        w.run(q.to(dev), kv_dev, rope_cos_sin=(cos.to(dev), sin.to(dev)))
+    with pytest.raises(TypeError):
+        w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev),
+              rope_cos_sin=(cos.half().to(dev), sin.half().to(dev)))
+    with pytest.raises(ValueError):
+        w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev),
+              rope_cos_sin=(cos[:-1].to(dev), sin[:-1].to(dev)))

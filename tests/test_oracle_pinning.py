@@ -367,3 +367,38 @@ def test_weights_normalised():
     assert osc.normalise_weights([1.0, 3.0]) == (0.25, 0.75)
     with pytest.raises(ValueError):
         osc.normalise_weights([-1.0])
+
+
+@pytest.mark.parametrize("dtype", ["f16", "bf16"])
+def test_rope_matches_torch_16bit_ops(dtype):
+    """The oracle's per-op rounding equals torch's own 16-bit tensor ops (what
+    apply_rope_with_cos_sin runs, flashinfer_full_verify.py:324-333) bit for
+    bit, and reduces to the identity at angle 0 and to rotate_half at cos 0 /
+    sin 1; a plain fp32 rotation stays within one rounding step."""
+    from oracle import rope as orope
+
+    tdt = torch.float16 if dtype == "f16" else torch.bfloat16
+    gen = torch.Generator().manual_seed(5)
+    n, h, d = 37, 4, 128
+    x = (torch.randn((n, h, d), generator=gen) * 3.0).to(tdt)
+    pos = torch.arange(1000, 1000 + n, dtype=torch.float32)
+    inv = 1.0 / (500000.0 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    emb = torch.cat((torch.outer(pos, inv),) * 2, dim=-1)
+    cos, sin = emb.cos().to(tdt), emb.sin().to(tdt)
+
+    def rot(t):
+        return torch.cat((-t[..., d // 2:], t[..., : d // 2]), dim=-1)
+
+    want = (x * cos[:, None, :]) + (rot(x) * sin[:, None, :])
+    got = orope.apply_rope(x.float().numpy(), cos.float().numpy(), sin.float().numpy(), dtype)
+    assert np.array_equal(got, want.float().numpy())
+    # a dropped rounding step would differ somewhere in these inputs
+    unrounded = x.float() * cos.float()[:, None, :] + rot(x.float()) * sin.float()[:, None, :]
+    assert not np.array_equal(orope.round_to(unrounded.numpy(), dtype), got)
+    # a wrong sign or half swap of rotate_half fails the plain-rotation bound
+    ulp = 2.0 ** -10 if dtype == "f16" else 2.0 ** -7
+    assert float(np.abs(got - unrounded.numpy()).max()) <= 4 * ulp * float(np.abs(unrounded.numpy()).max())
+    one, zero = np.ones((n, d), np.float32), np.zeros((n, d), np.float32)
+    xs = x.float().numpy()
+    assert np.array_equal(orope.apply_rope(xs, one, zero, dtype), xs)
+    assert np.array_equal(orope.apply_rope(xs, zero, one, dtype), orope.rotate_half(xs))
