@@ -65,7 +65,7 @@ class AttnMerge(ctypes.Structure):
     ]
 
 
-# name -> argtypes; restype is c_int for every entry point.
+# name -> argtypes; restype is c_int (a status) unless _RESTYPES says otherwise.
 _SIGNATURES: dict[str, list] = {
     "atlas_abi_version": [],
     "atlas_kv_move_slots": [_VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp],
@@ -98,7 +98,26 @@ _SIGNATURES: dict[str, list] = {
     "atlas_alloc_extend_slots": [_vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_paged_metadata": [_vp, _vp, _vp, ctypes.c_int, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _vp],
     "atlas_gather_logprobs": [_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp],
+    "atlas_frontier_workspace_bytes": [_c_i64, _c_i64, ctypes.c_int],
+    "atlas_frontier_topk": [
+        _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _c_i64, ctypes.c_int, _vp, ctypes.c_int, _c_i64, _vp,
+        _c_i64, _vp, _vp, _vp, _vp, _vp, _vp, ctypes.c_size_t, _vp,
+    ],
+    "atlas_candidate_select": [
+        _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp,
+    ],
 }
+# entry points whose return value is not an int status
+_RESTYPES: dict[str, type] = {"atlas_frontier_workspace_bytes": ctypes.c_int64}
+
+FRONTIER_NONE = -1
+FRONTIER_ORDER = 0
+FRONTIER_ORDER_BY_ROOT = 1
+FRONTIER_SELECT_GLOBAL = 2
+FRONTIER_SELECT_PER_ROOT = 3
+FRONTIER_PACK = 4
+MAX_FRONTIER_K = 32
+MAX_FRONTIER_CANDIDATES = 4096
 
 _lock = threading.Lock()
 _lib: ctypes.CDLL | None = None
@@ -126,7 +145,7 @@ def load() -> ctypes.CDLL:
         lib.atlas_last_error.argtypes = []
         for name, argtypes in _SIGNATURES.items():
             fn = getattr(lib, name)
-            fn.restype = ctypes.c_int
+            fn.restype = _RESTYPES.get(name, ctypes.c_int)
             fn.argtypes = argtypes
         _lib = lib
         return lib

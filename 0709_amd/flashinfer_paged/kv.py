@@ -1,5 +1,5 @@
-"""Logical route / node store driving the route pool (the parts of reference
-``flashinfer_paged/kv.py:21-258`` the commit-and-promote path uses).
+"""Logical route / node store driving the route pool and the frontier (the
+parts of reference ``flashinfer_paged/kv.py:21-258`` those paths use).
 
 Nodes and routes are ids only; the physical KV of a node lives wherever the
 route pool placed it.  Ids start at 1 and increase (``kv.py:30-31``).
@@ -10,7 +10,7 @@ from __future__ import annotations
 from dataclasses import dataclass
 from typing import Callable, Sequence
 
-from .types import DecodePhase, PrefixKVView, RouteKVView, RouteState
+from .types import DecodePhase, PendingCandidate, PrefixKVView, RouteKVView, RouteState
 
 
 @dataclass
@@ -55,6 +55,16 @@ class KVTreeStore:
         self.routes[int(route.route_id)] = route
         return route
 
+    def get_route(self, route_id: int) -> RouteState:
+        return self.routes[int(route_id)]
+
+    def get_routes(self, route_ids) -> list[RouteState]:
+        return [self.get_route(r) for r in route_ids]
+
+    def node_counter_state(self) -> tuple[int, int]:
+        """(next node id, step) without consuming an id."""
+        return self._next_node, 1
+
     def new_root_route(self, pending_token_id: int, prefix: PrefixKVView) -> RouteState:
         rid = self.allocate_route_id()
         return self.register_route(RouteState(route_id=rid, stage1_root_id=rid, parent_route_id=None,
@@ -95,12 +105,47 @@ class KVTreeStore:
             cumulative_logprob=float(cumulative_logprob), stage1_depth=route.stage1_depth,
             stage2_depth=route.stage2_depth, kv_view=route.kv_view.fork()))
 
+    def materialize_route_descriptors(self, selected: Sequence[PendingCandidate],
+                                      parent_routes: Sequence[RouteState]) -> list[RouteState]:
+        """One new route per selected candidate, forked from its parent route,
+        with the candidate's token pending (``kv.py:113-152``)."""
+        parents = {route.route_id: route for route in parent_routes}
+        out: list[RouteState] = []
+        for cand in selected:
+            parent = parents.get(cand.parent_route_id)
+            if parent is None:
+                parent = self.get_route(cand.parent_route_id)
+            rid = self.allocate_route_id()
+            if parent.token_logprobs and len(parent.token_logprobs) != parent.total_materialized_depth():
+                raise ValueError(
+                    "decoded parent token_logprobs must match its materialized path: "
+                    f"route_id={parent.route_id}, logprobs={len(parent.token_logprobs)}, "
+                    f"materialized_depth={parent.total_materialized_depth()}")
+            local = float(cand.cumulative_logprob - cand.parent_logprob)
+            route = RouteState(route_id=rid, stage1_root_id=cand.stage1_root_id, parent_route_id=parent.route_id,
+                               materialized_leaf_node_id=parent.materialized_leaf_node_id,
+                               pending_token_id=int(cand.pending_token_id),
+                               cumulative_logprob=float(cand.cumulative_logprob), stage1_depth=parent.stage1_depth,
+                               stage2_depth=parent.stage2_depth, kv_view=parent.kv_view.fork(),
+                               token_logprobs=(*parent.token_logprobs, local) if parent.token_logprobs else ())
+            out.append(self.register_route(route))
+        return out
+
     def release_routes_without_descendants(self, previous: Sequence[RouteState], nxt: Sequence[RouteState]) -> None:
         for hook in self._release_hooks:
             hook(previous, nxt)
 
     def tokens_for_node_ids(self, node_ids: Sequence[int]) -> tuple[int, ...]:
         return tuple(self.nodes[int(n)].token_id for n in node_ids)
+
+    def tokens_for_view(self, kv_view: RouteKVView) -> tuple[int, ...]:
+        return self.tokens_for_node_ids(kv_view.node_ids)
+
+    def materialized_token_path(self, route: RouteState) -> tuple[int, ...]:
+        return self.tokens_for_view(route.kv_view)
+
+    def pending_token_path(self, route: RouteState) -> tuple[int, ...]:
+        return (*self.materialized_token_path(route), int(route.pending_token_id))
 
     def node_path_for_route(self, route: RouteState) -> tuple[int, ...]:
         return tuple(route.kv_view.node_ids)

@@ -1,5 +1,5 @@
-"""Route / prefix views carried across the Drafter boundary (reference
-``flashinfer_paged/types.py:10-70``, ``:113-131``)."""
+"""Route / prefix views and frontier candidates carried across the Drafter
+boundary (reference ``flashinfer_paged/types.py:10-142``)."""
 
 from __future__ import annotations
 
@@ -60,6 +60,47 @@ class RouteState:
 
 
 @dataclass(frozen=True)
+class PendingCandidate:
+    parent_route_id: int
+    stage1_root_id: int
+    pending_token_id: int
+    cumulative_logprob: float
+    rank_in_parent: int = 0
+    parent_logprob: float = 0.0
+
+
+@dataclass(frozen=True)
+class PendingCandidateBatch:
+    """Device-resident candidate descriptors for one frontier depth (the
+    columns may be strided views of the packed candidate records)."""
+
+    parent_route_ids: torch.Tensor
+    stage1_root_ids: torch.Tensor
+    parent_row_indices: torch.Tensor
+    pending_token_ids: torch.Tensor
+    cumulative_logprobs: torch.Tensor
+    parent_logprobs: torch.Tensor
+    ranks_in_parent: torch.Tensor
+    candidates_per_parent: int
+
+    @property
+    def candidate_count(self) -> int:
+        return int(self.pending_token_ids.numel())
+
+
+@dataclass(frozen=True)
+class FrontierSelectionStats:
+    candidate_count: int = 0
+    selected_count: int = 0
+    host_materialization_batches: int = 0
+    host_materialization_elements: int = 0
+    host_transfer_batches: int = 0
+    host_transfer_elements: int = 0
+    selection_device: str = "cpu"
+    new_node_ids_source: str = "unknown"
+
+
+@dataclass(frozen=True)
 class DraftPrefixState:
     token_ids: torch.Tensor
     prefix_kv_view: PrefixKVView
@@ -77,3 +118,13 @@ class FrontierDecodeOutput:
     model_ms: float = 0.0
     kv_append_ms: float = 0.0
     metadata: Mapping[str, Any] = field(default_factory=dict)
+
+
+@dataclass(frozen=True)
+class FrontierStepOutput:
+    decoded_routes: list[RouteState]
+    next_routes: list[RouteState]
+    candidates: list[PendingCandidate]
+    selected_candidates: list[PendingCandidate]
+    decode_output: FrontierDecodeOutput
+    selection_stats: FrontierSelectionStats = field(default_factory=FrontierSelectionStats)

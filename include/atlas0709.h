@@ -307,6 +307,79 @@ int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t nu
                           const int64_t* token_dev, int64_t n, float* row_lse_dev,
                           float* out_dev, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Drafter frontier: per-parent top-k, candidate order / selection, records.
+ * ---------------------------------------------------------------------- */
+
+#define ATLAS_MAX_FRONTIER_K 32
+#define ATLAS_MAX_FRONTIER_CANDIDATES 4096
+
+/* Candidate order / selection modes. */
+#define ATLAS_FRONTIER_NONE (-1)          /* top-k only (records: order column -1) */
+#define ATLAS_FRONTIER_ORDER 0            /* full stable order -> order_out */
+#define ATLAS_FRONTIER_ORDER_BY_ROOT 1    /* the same with stage-1 root as first key */
+#define ATLAS_FRONTIER_SELECT_GLOBAL 2    /* first num_selected of the order */
+#define ATLAS_FRONTIER_SELECT_PER_ROOT 3  /* first num_selected of every root, roots ascending */
+#define ATLAS_FRONTIER_PACK 4             /* records with a given selection */
+
+/* Workspace bytes of atlas_frontier_topk for rows x vocab logits and k (any
+ * contents; calls that share a workspace must be stream-ordered).  Negative
+ * on bad arguments. */
+int64_t atlas_frontier_workspace_bytes(int64_t rows, int64_t vocab, int k);
+
+/* One frontier depth on the device, two launches, no host synchronisation.
+ * For each logits row r ([rows, vocab] with row_stride elements; fp16, bf16
+ * or fp32), the k tokens with the largest log_softmax(row) -- computed in
+ * fp32 as (x - max) - log(sum exp(x - max)) and rounded to the logits dtype
+ * -- in descending order, equal values by ascending token id:
+ * token_logprobs_out[r, j] (logits dtype), token_ids_out[r, j].  Replaces
+ * batch_parent_token_candidates' log_softmax + topk
+ * (src/atlas_0709/flashinfer_paged/sampling.py:107-153).  With `proposal`
+ * (fp32 Gumbel scores [rows, vocab], proposal_stride elements) the tokens are
+ * the top-k of the proposal and their log-probs are gathered
+ * (:139-153, the do_sample path).
+ * With records_out ([rows * k + num_node_ids, 8] int64) the candidates of
+ * build_pending_candidate_batch (frontier.py:127-185; parent_info_dev [rows, 3]:
+ * route id, stage-1 root id, parent cumulative log-prob as float64 bits) are
+ * written in the record layout of materialize_pending_candidate_batch
+ * (frontier.py:188-265): kind 0, parent route, stage-1 root, token, rank in
+ * parent, cumulative log-prob bits (parent + token log-prob in float64),
+ * parent log-prob bits, selection order; then num_node_ids rows of kind 1
+ * holding node_ids_dev.  select_mode ATLAS_FRONTIER_SELECT_GLOBAL / _PER_ROOT
+ * selects as GlobalTopKSelection / PerStage1RootTopKSelection.select_indices
+ * (frontier.py:58-124, utils.py:46-123) into selected_out and the order
+ * column; ATLAS_FRONTIER_NONE leaves the order column -1.  k <= 32 and at most
+ * 4096 candidates with records. */
+int atlas_frontier_topk(const void* logits_dev, int64_t rows, int64_t vocab, int64_t row_stride,
+                        int dtype, const float* proposal_dev, int64_t proposal_stride, int k,
+                        const int64_t* parent_info_dev, int select_mode, int64_t num_selected,
+                        const int64_t* node_ids_dev, int64_t num_node_ids,
+                        void* token_logprobs_out, int64_t* token_ids_out, int64_t* records_out,
+                        int64_t* parent_rows_out, int64_t* selected_out, void* workspace_dev,
+                        size_t workspace_bytes, void* stream);
+
+/* Order / select / pack a candidate batch given as six columns (element
+ * strides in strides[0..5]: parent route, root, token, rank, cumulative
+ * log-prob, parent log-prob).  The order is that of stable_candidate_order
+ * (src/atlas_0709/flashinfer_paged/utils.py:46-83): cumulative log-prob
+ * descending (NaN first, -0.0 == 0.0), then parent route, rank in parent and
+ * token id ascending, then the original index; ORDER_BY_ROOT and
+ * SELECT_PER_ROOT put the stage-1 root (ascending) first.
+ * ORDER / ORDER_BY_ROOT: order_out[count] (the permutation).
+ * SELECT_GLOBAL: global_topk_candidate_indices (:86-95) -> selected_out.
+ * SELECT_PER_ROOT: per_root_topk_candidate_indices (:98-123), roots taken from
+ * the candidates -> selected_out.  With records_out the candidates and the
+ * selection order (or -1) are packed as materialize_pending_candidate_batch
+ * does (frontier.py:188-265); PACK takes that selection from selected_in_dev
+ * (num_selected_in entries; out-of-range entries are ignored).  count <= 4096. */
+int atlas_candidate_select(const int64_t* parent_route_ids, const int64_t* stage1_root_ids,
+                           const int64_t* pending_token_ids, const int64_t* ranks_in_parent,
+                           const double* cumulative_logprobs, const double* parent_logprobs,
+                           const int64_t* strides, int64_t count, int mode, int64_t num_selected,
+                           const int64_t* selected_in_dev, int64_t num_selected_in,
+                           const int64_t* node_ids_dev, int64_t num_node_ids, int64_t* order_out,
+                           int64_t* selected_out, int64_t* records_out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

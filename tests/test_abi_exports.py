@@ -12,7 +12,7 @@ def _declared_symbols() -> set[str]:
     names = set()
     for header in (ROOT / "include").glob("*.h"):
         text = header.read_text()
-        names.update(re.findall(r"^\s*(?:int|const char\*)\s+(atlas_\w+)\s*\(", text, flags=re.M))
+        names.update(re.findall(r"^\s*(?:int|int64_t|const char\*)\s+(atlas_\w+)\s*\(", text, flags=re.M))
     return names
 
 

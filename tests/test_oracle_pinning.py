@@ -402,3 +402,105 @@ def test_rope_matches_torch_16bit_ops(dtype):
     xs = x.float().numpy()
     assert np.array_equal(orope.apply_rope(xs, one, zero, dtype), xs)
     assert np.array_equal(orope.apply_rope(xs, zero, one, dtype), orope.rotate_half(xs))
+
+
+def _ofr():
+    from oracle import frontier as ofr
+    return ofr
+
+
+def _cols(rows):
+    """Candidate columns from (parent, root, token, cumulative, rank, parent_lp) tuples."""
+    return {
+        "parent_route_ids": np.array([r[0] for r in rows], np.int64),
+        "stage1_root_ids": np.array([r[1] for r in rows], np.int64),
+        "pending_token_ids": np.array([r[2] for r in rows], np.int64),
+        "cumulative_logprobs": np.array([r[3] for r in rows], np.float64),
+        "ranks_in_parent": np.array([r[4] for r in rows], np.int64),
+        "parent_logprobs": np.array([r[5] if len(r) > 5 else 0.0 for r in rows], np.float64),
+    }
+
+
+def test_frontier_order_reference_literals():
+    """test_paged_frontier_selection.py:79-130: complete score ties order by
+    parent route, rank, token (global), and by root first (per root)."""
+    ofr = _ofr()
+    c = _cols([(20, 200, 7, -1.0, 0), (10, 100, 1, -1.0, 1), (10, 100, 9, -1.0, 0), (10, 100, 2, -1.0, 0),
+               (5, 500, 0, -1.0, 2), (99, 900, 4, -0.5, 3)])
+    sel = ofr.select_global(c, 6)
+    assert c["pending_token_ids"][sel].tolist() == [4, 0, 2, 9, 1, 7]
+    assert sel.tolist() == ofr.python_order(c)
+    c = _cols([(20, 200, 8, -1.0, 0), (20, 200, 3, -1.0, 1), (10, 100, 9, -1.0, 0), (10, 100, 4, -1.0, 1),
+               (21, 200, 7, -1.0, 0), (21, 200, 2, -1.0, 1), (11, 100, 6, -1.0, 0), (11, 100, 1, -1.0, 1)])
+    sel = ofr.select_per_root(c, 2, [(200, 4), (100, 4)])
+    assert c["stage1_root_ids"][sel].tolist() == [100, 100, 200, 200]
+    assert c["parent_route_ids"][sel].tolist() == [10, 10, 20, 20]
+
+
+def test_frontier_stable_order_equals_python_order_brute_force():
+    """The successive stable argsorts give the Python-object order
+    (utils.py:27-43) on batches dense with exact ties, NaN and -0.0 aside."""
+    ofr = _ofr()
+    rng = np.random.default_rng(3)
+    for _ in range(200):
+        n = int(rng.integers(1, 40))
+        rows = [(int(rng.integers(0, 4)), int(rng.integers(0, 3)), int(rng.integers(0, 5)),
+                 float(rng.integers(-3, 1)) * 0.5, int(rng.integers(0, 3))) for _ in range(n)]
+        c = _cols(rows)
+        assert ofr.stable_order(c).tolist() == ofr.python_order(c)
+        by_root = ofr.stable_order(c, include_stage1_root=True).tolist()
+        assert by_root == sorted(range(n), key=lambda i: (rows[i][1], ofr.python_order(c).index(i)))
+
+
+def test_frontier_topk_matches_torch_log_softmax_topk():
+    """parent_token_candidates = torch.topk(torch.log_softmax(rows)) on distinct
+    fp32 values (sampling.py:131-134); on 16-bit rows the chosen values are
+    torch's (the order of equal values is unspecified there); the Gumbel path
+    takes the proposal's top-k and gathers the log-probs (:135-153)."""
+    ofr = _ofr()
+    gen = torch.Generator().manual_seed(8)
+    x = torch.randn((6, 3000), generator=gen) * 4.0
+    lp, ids = ofr.parent_token_candidates(x.numpy(), 5, "f32")
+    tv, ti = torch.topk(torch.log_softmax(x, dim=-1), k=5, dim=-1)
+    assert np.array_equal(ids, ti.numpy())
+    assert np.allclose(lp, tv.numpy(), atol=2e-6, rtol=0)
+    from oracle import rope as orope
+    for tdt, odt, ulp in ((torch.float16, "f16", 2.0 ** -10), (torch.bfloat16, "bf16", 2.0 ** -7)):
+        xr = (torch.randn((4, 5000), generator=gen) * 0.5).to(tdt)
+        lp, ids = ofr.parent_token_candidates(xr.float().numpy(), 9, odt)
+        # torch's device kernel rounds (x - max) - log(sum) once from fp32 (its
+        # CPU 16-bit path rounds elsewhere): compare with the fp32 log-softmax
+        # rounded once -- equal but for rare rounding-boundary cases
+        ref = orope.round_to(torch.log_softmax(xr.float(), dim=-1).numpy(), odt)
+        got = np.take_along_axis(ref, ids, axis=-1)
+        assert float(np.abs(lp - got).max()) <= ulp * 8 and float(np.mean(lp == got)) > 0.95
+        assert np.array_equal(np.sort(ref, axis=-1)[:, ::-1][:, :9], lp)
+        # equal values come in ascending token order
+        for r in range(4):
+            for j in range(8):
+                if lp[r, j] == lp[r, j + 1]:
+                    assert ids[r, j] < ids[r, j + 1]
+    prop = torch.randn((6, 3000), generator=gen)
+    lp, ids = ofr.parent_token_candidates(x.numpy(), 4, "f32", proposal=prop.numpy())
+    assert np.array_equal(ids, torch.topk(prop, k=4, dim=-1).indices.numpy())
+    assert np.allclose(lp, torch.log_softmax(x, dim=-1).gather(-1, torch.from_numpy(ids)).numpy(), atol=2e-6)
+
+
+def test_frontier_depth_and_records_literals():
+    """test_paged_frontier_selection.py:189-275: two equal rows, k=2, four
+    candidates, the two selected are those of route 1; 4 x 8 record elements
+    (+ 2 rows of node ids); parent log-prob travels in column 6."""
+    ofr = _ofr()
+    logits = np.array([[0.0, 3.0, 3.0, 0.0, 0.0]] * 2, np.float32)
+    lp, ids = ofr.parent_token_candidates(logits, 2, "f32")
+    assert ids.tolist() == [[1, 2], [1, 2]]
+    c = ofr.build_candidates([1, 2], [1, 2], [0.0, 0.0], lp, ids)
+    sel = ofr.select_global(c, 2)
+    assert c["parent_route_ids"][sel].tolist() == [1, 1] and c["pending_token_ids"][sel].tolist() == [1, 2]
+    rec = ofr.pack_records(c, sel)
+    assert rec.size == 4 * 8 and rec[:, 7].tolist() == [0, 1, -1, -1]
+    rec = ofr.pack_records(c, sel, node_ids=[101, 102])
+    assert rec.size == (4 + 2) * 8 and rec[4:, :2].tolist() == [[1, 101], [1, 102]]
+    one = _cols([(7, 3, 11, -4.5, 2, -3.25)])
+    rec = ofr.pack_records(one, np.array([0]))
+    assert rec[0, 6] == np.float64(-3.25).view(np.int64) and rec[0, 5] == np.float64(-4.5).view(np.int64)
