@@ -32,8 +32,20 @@ HOT_PATH: dict[str, tuple[str, tuple[str, ...]]] = {
         "flashinfer_paged.paged_metadata", ("FlashInferPagedKVMetadata", "build_flashinfer_paged_kv_metadata")),
     "atlas_0709.flashinfer_paged.types": (
         "flashinfer_paged.types", ("DecodePhase", "PrefixKVView", "RouteKVView", "RouteState", "DraftPrefixState",
-                                   "FrontierDecodeOutput")),
+                                   "FrontierDecodeOutput", "PendingCandidate", "PendingCandidateBatch",
+                                   "FrontierSelectionStats", "FrontierStepOutput")),
     "atlas_0709.flashinfer_paged.kv": ("flashinfer_paged.kv", ("KVTreeNode", "KVTreeStore")),
+    "atlas_0709.flashinfer_paged.sampling": (
+        "flashinfer_paged.sampling", ("DrafterSamplingConfig", "DrafterSamplingContext", "batch_parent_token_candidates",
+                                      "single_parent_token_candidates")),
+    "atlas_0709.flashinfer_paged.utils": (
+        "flashinfer_paged.utils", ("topk_logprobs", "global_topk_candidates", "stable_candidate_order",
+                                   "global_topk_candidate_indices", "per_root_topk_candidate_indices",
+                                   "group_candidates_by_stage1_root", "topk_pairs_to_python", "logprob_of_token")),
+    "atlas_0709.flashinfer_paged.frontier": (
+        "flashinfer_paged.frontier", ("GlobalTopKSelection", "PerStage1RootTopKSelection",
+                                      "build_pending_candidate_batch", "materialize_pending_candidate_batch",
+                                      "collect_pending_candidates", "advance_frontier_one_token")),
     "atlas_0709.flashinfer_paged.sglang_runtime": (
         "flashinfer_paged.sglang_runtime", ("SGLangRoutePoolBridge", "SGLangRouteRow", "SGLangFlashInferFrontierModelBackend")),
     "atlas_0709.flashinfer_full_verify": (

@@ -11,7 +11,8 @@
 //                          writes its candidates; the last row to finish orders
 //                          and selects all candidates (last-arriver counters,
 //                          cleared by the stats launch; no workgroup waits
-//                          for another).
+//                          for another; the hand-offs are agent-scope atomic
+//                          stores and loads, see publish_i64).
 // The ordering works on any candidate batch as its own launch too
 // (candidate_select_kernel).
 #include "common.hpp"
@@ -23,7 +24,9 @@ constexpr int kFThreads = 256;
 constexpr int kMaxK = ATLAS_MAX_FRONTIER_K;
 constexpr int kMaxCand = ATLAS_MAX_FRONTIER_CANDIDATES;
 constexpr int kMaxChunks = kFThreads;  // the row merge gives each chunk list one thread
-constexpr int kTile = 512;             // candidates per LDS tile of the ordering
+constexpr int kTile = 256;             // candidates per LDS tile of the ordering
+constexpr int kFewMax = 64;            // global selections of up to this many take the bounded path
+constexpr float kLog2e = 1.4426950408889634f;
 
 // ---------------------------------------------------------------- keys
 // Order-preserving map of a float to u32 (larger float -> larger key).
@@ -63,7 +66,10 @@ struct Group {
   float x[kElems];
   __device__ __forceinline__ void load(const char* p) {
     const uint4 u = *reinterpret_cast<const uint4*>(p);
-    const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+    decode(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t, u));
+  }
+  __device__ __forceinline__ void decode(__attribute__((ext_vector_type(4))) uint32_t u) {
+    const uint32_t w[4] = {u[0], u[1], u[2], u[3]};
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       if constexpr (DT == ATLAS_DTYPE_F32) {
@@ -99,20 +105,122 @@ __device__ __forceinline__ void for_chunk(const char* row, int64_t c0, int64_t c
   for (int64_t i = i0 + t; i < c1; i += kFThreads) f(i, load_one<DT>(row, i));
 }
 
+typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
+constexpr int kRegGroups = 4;  // 16-byte groups per thread a register-held chunk has at most
+
+// A chunk of a 16-byte aligned row held in registers: thread t holds groups
+// t, t + kFThreads, ... (all loads issued together, so a caller can start
+// them before it waits for anything else); chunks of at most
+// kRegGroups * kFThreads groups.
+template <int DT>
+struct ChunkRegs {
+  static constexpr int E = Group<DT>::kElems;
+  static constexpr int ES = DT == ATLAS_DTYPE_F32 ? 4 : 2;
+  u32x4v v[kRegGroups];
+  int64_t c0, c1, ng;
+  __device__ __forceinline__ void load(const char* row, int64_t c0_, int64_t c1_) {
+    c0 = c0_;
+    c1 = c1_;
+    ng = (c1 - c0) / E;
+    if (ng == 0) return;
+#pragma unroll
+    for (int i = 0; i < kRegGroups; ++i) {
+      // clamped, unconditional: every load of the batch is issued back to back
+      const int64_t g = min<int64_t>(threadIdx.x + int64_t(i) * kFThreads, ng - 1);
+      v[i] = *reinterpret_cast<const u32x4v*>(row + (c0 + g * E) * ES);
+    }
+  }
+  // f(index, value) over the chunk; the tail past the last whole group is read
+  // element by element.
+  template <typename F>
+  __device__ __forceinline__ void visit(const char* row, F&& f) const {
+#pragma unroll
+    for (int i = 0; i < kRegGroups; ++i) {
+      const int64_t g = threadIdx.x + int64_t(i) * kFThreads;
+      if (g < ng) {
+        Group<DT> x;
+        x.decode(v[i]);
+#pragma unroll
+        for (int e = 0; e < E; ++e) f(c0 + g * E + e, x.x[e]);
+      }
+    }
+    for (int64_t i = c0 + ng * E + threadIdx.x; i < c1; i += kFThreads) f(i, load_one<DT>(row, i));
+  }
+};
+
 // ---------------------------------------------------------------- reductions
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-  const uint32_t lo = __shfl_xor(static_cast<int>(uint32_t(v)), m);
-  const uint32_t hi = __shfl_xor(static_cast<int>(uint32_t(v >> 32)), m);
+// Wave reductions through DPP lane moves (no LDS round trips): swap within
+// pairs and quads, mirror within 8 and 16 lanes, then row 0 into row 1 and
+// row 2 into row 3 (row_bcast15), rows 0-1 into rows 2-3 (row_bcast31); lane
+// 63 ends with the whole wave, which readlane hands to every lane.  Lanes a
+// broadcast step leaves out receive `identity`.
+constexpr int kDppXor1 = 0xB1;     // quad_perm [1, 0, 3, 2]
+constexpr int kDppXor2 = 0x4E;     // quad_perm [2, 3, 0, 1]
+constexpr int kDppHalfMirror = 0x141;
+constexpr int kDppMirror = 0x140;
+constexpr int kDppBcast15 = 0x142;
+constexpr int kDppBcast31 = 0x143;
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp32(uint32_t identity, uint32_t v) {
+  return static_cast<uint32_t>(
+      __builtin_amdgcn_update_dpp(static_cast<int>(identity), static_cast<int>(v), CTRL, ROWS, 0xf, false));
+}
+
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint64_t dpp64(uint64_t identity, uint64_t v) {
+  const uint32_t lo = dpp32<CTRL, ROWS>(uint32_t(identity), uint32_t(v));
+  const uint32_t hi = dpp32<CTRL, ROWS>(uint32_t(identity >> 32), uint32_t(v >> 32));
   return (uint64_t(hi) << 32) | lo;
 }
 
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-#pragma unroll
-  for (int m = 32; m > 0; m >>= 1) {
-    const uint64_t o = shfl_xor_u64(v, m);
-    v = o > v ? o : v;
-  }
-  return v;
+  v = umax64(v, dpp64<kDppXor1, 0xf>(0, v));
+  v = umax64(v, dpp64<kDppXor2, 0xf>(0, v));
+  v = umax64(v, dpp64<kDppHalfMirror, 0xf>(0, v));
+  v = umax64(v, dpp64<kDppMirror, 0xf>(0, v));
+  v = umax64(v, dpp64<kDppBcast15, 0xa>(0, v));
+  v = umax64(v, dpp64<kDppBcast31, 0xc>(0, v));
+  const uint32_t lo = __builtin_amdgcn_readlane(static_cast<int>(uint32_t(v)), 63);
+  const uint32_t hi = __builtin_amdgcn_readlane(static_cast<int>(uint32_t(v >> 32)), 63);
+  return (uint64_t(hi) << 32) | lo;
+}
+
+// Hand-off between workgroups of one launch without an L2 write-back: the
+// values another workgroup reads are stored and loaded as agent-scope atomics
+// (coherent across the XCDs' L2s), and a writer waits until its stores are
+// acknowledged before it counts itself in with a relaxed agent-scope add.  (An
+// agent-scope release fence would write back the XCD's whole L2 in every
+// workgroup.)
+__device__ __forceinline__ void publish_i64(int64_t* p, int64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int64_t fetch_i64(const int64_t* p) {
+  return __hip_atomic_load(const_cast<int64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() {
+  __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0)
+}
+// Counts the calling workgroup in (after every thread's wait_stores and a
+// barrier); true in the workgroup that arrives last of `total`.
+__device__ __forceinline__ bool arrive_last(int32_t* counter, int total, int* flag) {
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *flag = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == total - 1;
+  __syncthreads();
+  return *flag != 0;
+}
+
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  v += static_cast<int>(dpp32<kDppXor1, 0xf>(0u, static_cast<uint32_t>(v)));
+  v += static_cast<int>(dpp32<kDppXor2, 0xf>(0u, static_cast<uint32_t>(v)));
+  v += static_cast<int>(dpp32<kDppHalfMirror, 0xf>(0u, static_cast<uint32_t>(v)));
+  v += static_cast<int>(dpp32<kDppMirror, 0xf>(0u, static_cast<uint32_t>(v)));
+  v += static_cast<int>(dpp32<kDppBcast15, 0xa>(0u, static_cast<uint32_t>(v)));
+  v += static_cast<int>(dpp32<kDppBcast31, 0xc>(0u, static_cast<uint32_t>(v)));
+  return __builtin_amdgcn_readlane(v, 63);
 }
 
 // Online (max, sum of exp(x - max)) pairs.
@@ -124,22 +232,31 @@ __device__ __forceinline__ void ms_add(float& m, float& s, float m2, float s2) {
     return;
   }
   if (m2 > m) {
-    s = s * expf(m - m2) + s2;
+    s = s * __builtin_amdgcn_exp2f((m - m2) * kLog2e) + s2;
     m = m2;
   } else {
-    s = s + s2 * expf(m2 - m);
+    s = s + s2 * __builtin_amdgcn_exp2f((m2 - m) * kLog2e);
   }
 }
 
-// Block combine of per-thread (m, s) in a fixed order (waves by xor steps,
-// then wave 0..3), so every workgroup of a row derives the same result.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ void ms_dpp(float& m, float& s) {
+  const float m2 = __uint_as_float(dpp32<CTRL, ROWS>(__float_as_uint(-INFINITY), __float_as_uint(m)));
+  const float s2 = __uint_as_float(dpp32<CTRL, ROWS>(0u, __float_as_uint(s)));
+  ms_add(m, s, m2, s2);
+}
+
+// Block combine of per-thread (m, s) in a fixed order (the wave's DPP steps,
+// then waves 0..3), so every workgroup of a row derives the same result.
 __device__ __forceinline__ void block_ms(float& m, float& s, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    const float m2 = __shfl_xor(m, o);
-    const float s2 = __shfl_xor(s, o);
-    ms_add(m, s, m2, s2);
-  }
+  ms_dpp<kDppXor1, 0xf>(m, s);
+  ms_dpp<kDppXor2, 0xf>(m, s);
+  ms_dpp<kDppHalfMirror, 0xf>(m, s);
+  ms_dpp<kDppMirror, 0xf>(m, s);
+  ms_dpp<kDppBcast15, 0xa>(m, s);
+  ms_dpp<kDppBcast31, 0xc>(m, s);
+  m = __uint_as_float(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(m)), 63));
+  s = __uint_as_float(__builtin_amdgcn_readlane(static_cast<int>(__float_as_uint(s)), 63));
   const int wave = threadIdx.x >> 6;
   __syncthreads();
   if ((threadIdx.x & 63) == 0) {
@@ -228,7 +345,15 @@ struct CandCols {
   const double* cum;
   const double* plp;
   int64_t s_parent, s_root, s_token, s_rank, s_cum, s_plp;
+  bool coherent;  // written by other workgroups of this launch: agent-scope loads
 };
+
+__device__ __forceinline__ int64_t col_i64(const int64_t* p, bool coherent) {
+  return coherent ? fetch_i64(p) : *p;
+}
+__device__ __forceinline__ double col_f64(const double* p, bool coherent) {
+  return coherent ? __longlong_as_double(fetch_i64(reinterpret_cast<const int64_t*>(p))) : *p;
+}
 
 // Descending order of doubles as u64: NaN first (torch sorts NaN above every
 // number), -0.0 equal to +0.0.
@@ -249,31 +374,34 @@ struct Cand {
 
 __device__ __forceinline__ Cand load_cand(const CandCols& c, int64_t i) {
   Cand r;
-  r.root = c.root[i * c.s_root];
-  r.cum = dorder(c.cum[i * c.s_cum]);
-  r.parent = c.parent[i * c.s_parent];
-  r.rank = c.rank[i * c.s_rank];
-  r.token = c.token[i * c.s_token];
+  r.root = col_i64(c.root + i * c.s_root, c.coherent);
+  r.cum = dorder(col_f64(c.cum + i * c.s_cum, c.coherent));
+  r.parent = col_i64(c.parent + i * c.s_parent, c.coherent);
+  r.rank = col_i64(c.rank + i * c.s_rank, c.coherent);
+  r.token = col_i64(c.token + i * c.s_token, c.coherent);
   return r;
 }
 
-// Does candidate a (index ia) come before b (index ib)?  Keys: stage-1 root
-// ascending (by_root), cumulative log-prob descending, parent route, rank in
-// parent, token id ascending, then the original index (a stable sort's order).
-__device__ __forceinline__ bool cand_before(const Cand& a, int64_t ia, const Cand& b, int64_t ib, bool by_root) {
-  if (by_root && a.root != b.root) return a.root < b.root;
-  if (a.cum != b.cum) return a.cum > b.cum;
-  if (a.parent != b.parent) return a.parent < b.parent;
-  if (a.rank != b.rank) return a.rank < b.rank;
-  if (a.token != b.token) return a.token < b.token;
-  return ia < ib;
-}
-
+// LDS of the ordering: a tile of candidates by column (the score first, the
+// other keys read only on equal scores), and per candidate its position and
+// selection order (16 bits: at most 4096 candidates).
 struct SelectSmem {
-  Cand tile[kTile];
-  int pos[kMaxCand];  // position in the order (per root: inside the candidate's root)
-  int sel[kMaxCand];  // selection order, or -1
+  uint64_t cum[kTile];
+  int64_t root[kTile];
+  int64_t parent[kTile];
+  int64_t rank[kTile];
+  int64_t token[kTile];
+  int16_t pos[kMaxCand];  // position in the order (per root: inside the candidate's root)
+  int16_t sel[kMaxCand];  // selection order, or -1
+  // global top-n with small n: wave lists of the threads' best scores, the
+  // bound, and the candidates at or above it with their counts
+  uint64_t wave_best[kFThreads / 64][kFewMax];
+  uint64_t bound;
+  int num_few;
+  int few[kFewMax * 4];
+  int few_count[kFewMax * 4];
 };
+static_assert(kMaxCand <= 32767, "positions are 16-bit");
 
 enum SelectMode : int {
   kOrder = ATLAS_FRONTIER_ORDER,
@@ -298,9 +426,22 @@ struct SelectArgs {
   bool records_filled;    // columns 0..6 already hold the candidates
 };
 
-// Position of every candidate in the order: the number of candidates that come
-// before it (per root: before it inside its root), counted against LDS tiles
-// of the candidates.  One workgroup of kFThreads.
+__device__ __forceinline__ void load_tile(const SelectArgs& a, SelectSmem& sm, int64_t t0, int n) {
+  for (int j = threadIdx.x; j < n; j += kFThreads) {
+    const Cand x = load_cand(a.cols, t0 + j);
+    sm.cum[j] = x.cum;
+    sm.root[j] = x.root;
+    sm.parent[j] = x.parent;
+    sm.rank[j] = x.rank;
+    sm.token[j] = x.token;
+  }
+}
+
+// Position of every candidate in the order: the number of candidates that
+// come before it.  Keys: stage-1 root ascending (by_root), cumulative log-prob
+// descending, parent route, rank in parent, token id ascending, then the
+// original index (a stable sort's order).  within_root: count only the
+// candidates of the same root.  One workgroup of kFThreads.
 __device__ void count_before(const SelectArgs& a, SelectSmem& sm, bool by_root, bool within_root) {
   const int t = threadIdx.x;
   const int64_t C = a.count;
@@ -313,18 +454,110 @@ __device__ void count_before(const SelectArgs& a, SelectSmem& sm, bool by_root, 
     for (int64_t t0 = 0; t0 < C; t0 += kTile) {
       const int n = static_cast<int>(min<int64_t>(kTile, C - t0));
       __syncthreads();
-      for (int j = t; j < n; j += kFThreads) sm.tile[j] = load_cand(a.cols, t0 + j);
+      load_tile(a, sm, t0, n);
       __syncthreads();
-      if (mine)
-        for (int j = 0; j < n; ++j) {
-          const Cand& x = sm.tile[j];
-          const bool b = cand_before(x, t0 + j, me, c, by_root) && (!within_root || x.root == me.root);
-          before += b ? 1 : 0;
-        }
+      if (!mine) continue;
+      // Branch-free and unrolled, so the LDS reads of several candidates are
+      // in flight together (equal scores are common: 16-bit log-probs).
+#pragma unroll 8
+      for (int j = 0; j < n; ++j) {
+        const int64_t rj = sm.root[j];
+        const uint64_t cj = sm.cum[j];
+        const int64_t pj = sm.parent[j], kj = sm.rank[j], tj = sm.token[j];
+        const bool same = !by_root || rj == me.root;
+        const bool tie_first = pj < me.parent ||
+                               (pj == me.parent && (kj < me.rank || (kj == me.rank && (tj < me.token ||
+                                                                                       (tj == me.token && t0 + j < c)))));
+        const bool b = same ? (cj > me.cum || (cj == me.cum && tie_first)) : (!within_root && rj < me.root);
+        before += b ? 1 : 0;
+      }
     }
-    if (mine) sm.pos[c] = before;
+    if (mine) sm.pos[c] = static_cast<int16_t>(before);
   }
   __syncthreads();
+}
+
+// Global top-n for n <= kFewMax.  T = the n-th largest of the threads' best
+// scores is at most the n-th best score (n candidates reach it), so only
+// candidates scoring at least T can be among the first n.  Those (few; at
+// most 4 * kFewMax, else false) get their exact positions, each counted by
+// the 64 lanes of one wave over all candidates.
+__device__ bool select_global_few(const SelectArgs& a, SelectSmem& sm) {
+  const int t = threadIdx.x;
+  const int lane = t & 63;
+  const int wave = t >> 6;
+  const int64_t C = a.count;
+  const int n = static_cast<int>(a.num_selected);
+  uint64_t head = 0;
+  for (int64_t c = t; c < C; c += kFThreads)
+    head = umax64(head, dorder(col_f64(a.cols.cum + c * a.cols.s_cum, a.cols.coherent)));
+  if (t == 0) sm.num_few = 0;
+  for (int r = 0; r < n; ++r) {
+    const uint64_t m = wave_max_u64(head);
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(head == m && m != 0);
+    if (hit != 0 && lane == __builtin_ctzll(hit)) head = 0;
+    if (lane == 0) sm.wave_best[wave][r] = m;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int p = 0;
+    head = lane < kFThreads / 64 ? sm.wave_best[lane][0] : 0;
+    for (int r = 0; r < n; ++r) {
+      const uint64_t m = wave_max_u64(head);
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < kFThreads / 64 && head == m && m != 0);
+      if (hit != 0 && lane == __builtin_ctzll(hit)) {
+        ++p;
+        head = p < n ? sm.wave_best[lane][p] : 0;
+      }
+      if (lane == 0 && r == n - 1) sm.bound = m;
+    }
+  }
+  __syncthreads();
+  const uint64_t bound = sm.bound;
+  for (int64_t c = t; c < C; c += kFThreads) {
+    sm.sel[c] = -1;
+    if (dorder(col_f64(a.cols.cum + c * a.cols.s_cum, a.cols.coherent)) >= bound) {
+      const int i = atomicAdd(&sm.num_few, 1);
+      if (i < kFewMax * 4) {
+        sm.few[i] = static_cast<int>(c);
+        sm.few_count[i] = 0;
+      }
+    }
+  }
+  __syncthreads();
+  const int nf = sm.num_few;
+  if (nf > kFewMax * 4) return false;
+  for (int64_t t0 = 0; t0 < C; t0 += kTile) {
+    const int nt = static_cast<int>(min<int64_t>(kTile, C - t0));
+    __syncthreads();
+    load_tile(a, sm, t0, nt);
+    __syncthreads();
+    for (int f = wave; f < nf; f += kFThreads / 64) {
+      const int64_t c = sm.few[f];
+      const Cand me = load_cand(a.cols, c);
+      int before = 0;
+      for (int j = lane; j < nt; j += 64) {
+        const uint64_t cj = sm.cum[j];
+        const int64_t pj = sm.parent[j], kj = sm.rank[j], tj = sm.token[j];
+        const bool tie_first = pj < me.parent ||
+                               (pj == me.parent && (kj < me.rank || (kj == me.rank && (tj < me.token ||
+                                                                                       (tj == me.token && t0 + j < c)))));
+        before += (cj > me.cum || (cj == me.cum && tie_first)) ? 1 : 0;
+      }
+      before = wave_sum_i32(before);
+      if (lane == 0) sm.few_count[f] += before;
+    }
+  }
+  __syncthreads();
+  for (int f = t; f < nf; f += kFThreads) {
+    const int p = sm.few_count[f];
+    if (p < n) {
+      const int c = sm.few[f];
+      sm.sel[c] = static_cast<int16_t>(p);
+      a.selected_out[p] = c;
+    }
+  }
+  return true;
 }
 
 __device__ void select_block(const SelectArgs& a, SelectSmem& sm) {
@@ -337,11 +570,12 @@ __device__ void select_block(const SelectArgs& a, SelectSmem& sm) {
       for (int64_t c = t; c < C; c += kFThreads) a.order_out[sm.pos[c]] = c;
       return;
     case kSelectGlobal:
+      if (a.num_selected <= kFewMax && select_global_few(a, sm)) break;
       count_before(a, sm, false, false);
       for (int64_t c = t; c < C; c += kFThreads) {
         const int p = sm.pos[c];
         const bool chosen = p < a.num_selected;
-        sm.sel[c] = chosen ? p : -1;
+        sm.sel[c] = static_cast<int16_t>(chosen ? p : -1);
         if (chosen) a.selected_out[p] = c;
       }
       break;
@@ -351,20 +585,20 @@ __device__ void select_block(const SelectArgs& a, SelectSmem& sm) {
       for (int64_t base = 0; base < C; base += kFThreads) {
         const int64_t c = base + t;
         const bool mine = c < C;
-        const int64_t my_root = mine ? a.cols.root[c * a.cols.s_root] : 0;
+        const int64_t my_root = mine ? col_i64(a.cols.root + c * a.cols.s_root, a.cols.coherent) : 0;
         int off = 0;
         for (int64_t t0 = 0; t0 < C; t0 += kTile) {
           const int n = static_cast<int>(min<int64_t>(kTile, C - t0));
           __syncthreads();
-          for (int j = t; j < n; j += kFThreads) sm.tile[j].root = a.cols.root[(t0 + j) * a.cols.s_root];
+          for (int j = t; j < n; j += kFThreads) sm.root[j] = col_i64(a.cols.root + (t0 + j) * a.cols.s_root, a.cols.coherent);
           __syncthreads();
           if (mine)
-            for (int j = 0; j < n; ++j) off += (sm.tile[j].root < my_root && sm.pos[t0 + j] < a.num_selected) ? 1 : 0;
+            for (int j = 0; j < n; ++j) off += (sm.root[j] < my_root && sm.pos[t0 + j] < a.num_selected) ? 1 : 0;
         }
         if (mine) {
           const int in_root = sm.pos[c];
           const bool chosen = in_root < a.num_selected;
-          sm.sel[c] = chosen ? off + in_root : -1;
+          sm.sel[c] = static_cast<int16_t>(chosen ? off + in_root : -1);
           if (chosen) a.selected_out[off + in_root] = c;
         }
       }
@@ -375,7 +609,7 @@ __device__ void select_block(const SelectArgs& a, SelectSmem& sm) {
       if (t == 0)
         for (int64_t i = 0; i < a.num_selected_in; ++i) {
           const int64_t c = a.selected_in[i];
-          if (c >= 0 && c < C) sm.sel[c] = static_cast<int>(i);
+          if (c >= 0 && c < C) sm.sel[c] = static_cast<int16_t>(i < 32767 ? i : -1);
         }
       break;
   }
@@ -417,6 +651,7 @@ struct FrontierArgs {
   int64_t proposal_stride;
   int rows, k, num_chunks;
   int64_t chunk_len;
+  bool reg_chunks;  // chunks fit ChunkRegs (aligned rows use it)
   const int64_t* parent_info;  // [rows, 3]: route id, stage-1 root id, log-prob bits
   void* token_logprobs;        // [rows, k] in the logits dtype
   int64_t* token_ids;          // [rows, k]
@@ -441,15 +676,26 @@ __global__ __launch_bounds__(kFThreads) void frontier_stats_kernel(FrontierArgs 
   const char* rp = a.logits + int64_t(row) * a.row_stride_bytes;
   const int64_t c0 = int64_t(chunk) * a.chunk_len;
   const int64_t c1 = min(a.vocab, c0 + a.chunk_len);
+  // Per thread: the maximum over its elements, then the sum of
+  // exp2((x - max) * log2 e) over them -- from registers when the row is
+  // aligned, else re-read from cache.
   float m = -INFINITY, s = 0.f;
-  for_chunk<DT>(rp, c0, c1, [&](int64_t, float x) {
-    if (x > m) {
-      s = (m == -INFINITY ? 0.f : s * expf(m - x)) + 1.f;
-      m = x;
-    } else if (x != -INFINITY) {
-      s += expf(x - m);
+  if (a.reg_chunks && (reinterpret_cast<uintptr_t>(rp) & 15) == 0) {
+    ChunkRegs<DT> cr;
+    cr.load(rp, c0, c1);
+    cr.visit(rp, [&](int64_t, float x) { m = fmaxf(m, x); });
+    if (m != -INFINITY) {
+      const float mb = m * kLog2e;
+      cr.visit(rp, [&](int64_t, float x) { s += __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -mb)); });
     }
-  });
+  } else {
+    for_chunk<DT>(rp, c0, c1, [&](int64_t, float x) { m = fmaxf(m, x); });
+    if (m != -INFINITY) {
+      const float mb = m * kLog2e;
+      for_chunk<DT>(rp, c0, c1,
+                    [&](int64_t, float x) { s += __builtin_amdgcn_exp2f(__builtin_fmaf(x, kLog2e, -mb)); });
+    }
+  }
   block_ms(m, s, red);
   if (threadIdx.x == 0) a.stats[int64_t(row) * a.num_chunks + chunk] = float2{m, s};
 }
@@ -476,6 +722,12 @@ __global__ __launch_bounds__(kFThreads) void frontier_topk_kernel(FrontierArgs a
   const int row = blockIdx.y;
   const int k = a.k;
   const char* rp = a.logits + int64_t(row) * a.row_stride_bytes;
+  const int64_t c0 = int64_t(chunk) * a.chunk_len;
+  const int64_t c1 = min(a.vocab, c0 + a.chunk_len);
+  // The chunk's loads go out before the wait for the row statistics.
+  const bool regs = a.reg_chunks && a.proposal == nullptr && (reinterpret_cast<uintptr_t>(rp) & 15) == 0;
+  ChunkRegs<DT> cr;
+  if (regs) cr.load(rp, c0, c1);
 
   // The row's log-sum-exp from its chunk statistics (same order everywhere).
   float m = -INFINITY, s = 0.f;
@@ -488,36 +740,56 @@ __global__ __launch_bounds__(kFThreads) void frontier_topk_kernel(FrontierArgs a
   const float row_max = m;
   const float lse = logf(s);
 
-  const int64_t c0 = int64_t(chunk) * a.chunk_len;
-  const int64_t c1 = min(a.vocab, c0 + a.chunk_len);
   TopList<KM> L;
   L.clear();
-  if (a.proposal == nullptr) {
-    // log_softmax rounded to the logits dtype: ((x - max) - lse)
-    for_chunk<DT>(rp, c0, c1, [&](int64_t i, float x) {
-      L.push(token_key(round_dt<DT>((x - row_max) - lse), uint32_t(i)), k);
+  // log_softmax rounded to the logits dtype: ((x - max) - lse)
+  auto push_lp = [&](int64_t i, float x) { L.push(token_key(round_dt<DT>((x - row_max) - lse), uint32_t(i)), k); };
+  if (regs) {
+    // Each thread's largest logit (the first of equal ones) is an element of
+    // the chunk, so the k-th largest of their keys bounds the chunk's k-th
+    // key from below.  Only elements whose unrounded log-prob can round up to
+    // the bound's value compute a key (a margin over half a 16-bit ulp), so
+    // the insertion work no longer runs for almost every element.
+    float mx = -INFINITY;
+    int64_t mi = -1;
+    cr.visit(rp, [&](int64_t i, float x) {
+      const bool up = x > mx;
+      mx = up ? x : mx;
+      mi = up ? i : mi;
     });
+    TopList<KM> one;
+    one.clear();
+    if (mi >= 0) one.a[0] = token_key(round_dt<DT>((mx - row_max) - lse), uint32_t(mi));
+    block_topk<KM>(one, k, lists, wave_lists, best);
+    const uint64_t bound = best[k - 1];
+    float cut = -INFINITY;
+    if (bound != 0) {
+      const float lb = key_value(bound);
+      cut = lb - (fabsf(lb) * 0x1p-6f + 1e-7f);
+    }
+    cr.visit(rp, [&](int64_t i, float x) {
+      const float u = (x - row_max) - lse;
+      if (u >= cut) L.push(token_key(round_dt<DT>(u), uint32_t(i)), k);
+    });
+  } else if (a.proposal == nullptr) {
+    for_chunk<DT>(rp, c0, c1, push_lp);
   } else {
     const char* pp = reinterpret_cast<const char*>(a.proposal + int64_t(row) * a.proposal_stride);
     for_chunk<ATLAS_DTYPE_F32>(pp, c0, c1, [&](int64_t i, float x) { L.push(token_key(x, uint32_t(i)), k); });
   }
   block_topk<KM>(L, k, lists, wave_lists, best);
-  uint64_t* my_list = a.lists + (int64_t(row) * a.num_chunks + chunk) * k;
-  if (t < k) my_list[t] = best[t];
+  int64_t* my_list = reinterpret_cast<int64_t*>(a.lists) + (int64_t(row) * a.num_chunks + chunk) * k;
+  if (t < k) publish_i64(my_list + t, static_cast<int64_t>(best[t]));
+  wait_stores();
 
   // Last chunk of the row merges the row.
-  __threadfence();
-  __syncthreads();
-  if (t == 0) flag = atomicAdd(&a.counters[row], 1) == a.num_chunks - 1;
-  __syncthreads();
-  if (!flag) return;
-  __threadfence();
+  if (!arrive_last(&a.counters[row], a.num_chunks, &flag)) return;
   L.clear();
   if (t < a.num_chunks) {
-    const uint64_t* src = a.lists + (int64_t(row) * a.num_chunks + t) * k;
+    const int64_t* src = reinterpret_cast<const int64_t*>(a.lists) + (int64_t(row) * a.num_chunks + t) * k;
 #pragma unroll
     for (int i = 0; i < KM; ++i)
-      if (i < k) L.a[i] = src[i];
+      if (i < k) L.a[i] = static_cast<uint64_t>(fetch_i64(src + i));
   }
   block_topk<KM>(L, k, lists, wave_lists, best);
   if (t < k) {
@@ -537,29 +809,26 @@ __global__ __launch_bounds__(kFThreads) void frontier_topk_kernel(FrontierArgs a
     a.token_ids[c] = id;
     if (a.parent_rows != nullptr) a.parent_rows[c] = row;
     if (a.sel.records != nullptr) {
+      // columns the last row's workgroup reads go out as agent-scope stores
       int64_t* r = a.sel.records + c * 8;
       const int64_t* pi = a.parent_info + int64_t(row) * 3;
       const double plp = __longlong_as_double(pi[2]);
       r[0] = 0;
-      r[1] = pi[0];
-      r[2] = pi[1];
-      r[3] = id;
-      r[4] = t;
-      r[5] = __double_as_longlong(plp + static_cast<double>(lp));
-      r[6] = pi[2];
+      publish_i64(r + 1, pi[0]);
+      publish_i64(r + 2, pi[1]);
+      publish_i64(r + 3, id);
+      publish_i64(r + 4, t);
+      publish_i64(r + 5, __double_as_longlong(plp + static_cast<double>(lp)));
+      publish_i64(r + 6, pi[2]);
       r[7] = -1;
     }
   }
   if (a.sel.mode < 0) return;
+  wait_stores();
 
   // Last row orders and selects every candidate (best[] is read above before
   // the barrier that precedes the ordering's first use of the shared bytes).
-  __threadfence();
-  __syncthreads();
-  if (t == 0) flag = atomicAdd(&a.counters[a.rows], 1) == a.rows - 1;
-  __syncthreads();
-  if (!flag) return;
-  __threadfence();
+  if (!arrive_last(&a.counters[a.rows], a.rows, &flag)) return;
   select_block(a.sel, sm);
 }
 
@@ -584,27 +853,36 @@ int launch_frontier(const FrontierArgs& a, hipStream_t s) {
 struct Geometry {
   int num_chunks;
   int64_t chunk_len;
+  bool reg_chunks;
 };
 
-// Chunks of a multiple of 8 elements, enough (row, chunk) workgroups to cover
-// the device about twice, at most kMaxChunks per row.
-Geometry frontier_geometry(int64_t rows, int64_t vocab) {
-  constexpr int64_t kTargetGroups = 1024;
+// Chunks of a multiple of 8 elements: about 768 (row, chunk) workgroups (all
+// resident at once), chunks that fit in registers (kRegGroups 16-byte groups
+// per thread) where the vocabulary allows, at least ~512 elements, at most
+// kMaxChunks per row.
+Geometry frontier_geometry(int64_t rows, int64_t vocab, int esize) {
+  constexpr int64_t kTargetGroups = 768;
+  const int64_t reg_len = int64_t(kFThreads) * kRegGroups * (16 / esize);
   int64_t nc = (kTargetGroups + rows - 1) / rows;
-  nc = std::min<int64_t>(nc, (vocab + 1023) / 1024);
+  nc = std::min<int64_t>(nc, (vocab + 511) / 512);
+  nc = std::max<int64_t>(nc, (vocab + reg_len - 1) / reg_len);
   nc = std::max<int64_t>(1, std::min<int64_t>(nc, kMaxChunks));
   int64_t len = (vocab + nc - 1) / nc;
   len = (len + 7) / 8 * 8;
   nc = (vocab + len - 1) / len;
-  return Geometry{static_cast<int>(nc), len};
+  return Geometry{static_cast<int>(nc), len, len <= reg_len};
 }
 
 size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 
-size_t workspace_bytes(int64_t rows, int64_t vocab, int k) {
-  const Geometry g = frontier_geometry(rows, vocab);
+size_t workspace_bytes_for(int64_t rows, int64_t vocab, int k, int esize) {
+  const Geometry g = frontier_geometry(rows, vocab, esize);
   return align256(size_t(rows + 1) * 4) + align256(size_t(rows) * g.num_chunks * sizeof(float2)) +
          align256(size_t(rows) * g.num_chunks * k * sizeof(uint64_t));
+}
+
+size_t workspace_bytes(int64_t rows, int64_t vocab, int k) {
+  return std::max(workspace_bytes_for(rows, vocab, k, 2), workspace_bytes_for(rows, vocab, k, 4));
 }
 
 }  // namespace
@@ -657,7 +935,7 @@ extern "C" int atlas_frontier_topk(const void* logits, int64_t rows, int64_t voc
                 workspace_bytes_given, workspace_bytes(rows, vocab, k));
 
   const int esize = dtype == ATLAS_DTYPE_F32 ? 4 : 2;
-  const Geometry g = frontier_geometry(rows, vocab);
+  const Geometry g = frontier_geometry(rows, vocab, esize);
   char* ws = static_cast<char*>(workspace_dev);
   FrontierArgs a{};
   a.logits = static_cast<const char*>(logits);
@@ -669,6 +947,7 @@ extern "C" int atlas_frontier_topk(const void* logits, int64_t rows, int64_t voc
   a.k = k;
   a.num_chunks = g.num_chunks;
   a.chunk_len = g.chunk_len;
+  a.reg_chunks = g.reg_chunks;
   a.parent_info = parent_info_dev;
   a.token_logprobs = token_logprobs_out;
   a.token_ids = token_ids_out;
@@ -689,6 +968,7 @@ extern "C" int atlas_frontier_topk(const void* logits, int64_t rows, int64_t voc
     s.cols.cum = reinterpret_cast<const double*>(records_out + 5);
     s.cols.plp = reinterpret_cast<const double*>(records_out + 6);
     s.cols.s_parent = s.cols.s_root = s.cols.s_token = s.cols.s_rank = s.cols.s_cum = s.cols.s_plp = 8;
+    s.cols.coherent = true;
     s.count = count;
     s.num_selected = num_selected;
     s.node_ids = node_ids_dev;
@@ -717,7 +997,7 @@ extern "C" int atlas_candidate_select(const int64_t* parent_route_ids, const int
   ATLAS_REQUIRE(num_node_ids >= 0 && (num_node_ids == 0 || node_ids_dev != nullptr), "bad node ids");
   SelectArgs a{};
   a.cols = CandCols{parent_route_ids, stage1_root_ids, pending_token_ids, ranks_in_parent, cumulative_logprobs,
-                    parent_logprobs, strides[0], strides[1], strides[2], strides[3], strides[4], strides[5]};
+                    parent_logprobs, strides[0], strides[1], strides[2], strides[3], strides[4], strides[5], false};
   if (count > 0) {
     const int rc = check_cols(a.cols);
     if (rc != ATLAS_OK) return rc;

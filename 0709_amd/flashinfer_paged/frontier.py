@@ -9,11 +9,11 @@ torch launches and three host-to-device tensor builds).
 
 from __future__ import annotations
 
-import struct
 from collections import Counter
 from dataclasses import dataclass
 from typing import Any, Protocol, Sequence
 
+import numpy as np
 import torch
 
 from .. import _lib
@@ -112,10 +112,9 @@ def _parent_info(decoded_routes: Sequence[RouteState], device: torch.device) -> 
     host-to-device copy."""
     host = torch.empty((len(decoded_routes), 3), dtype=torch.int64, pin_memory=True)
     rows = host.numpy()
-    for i, route in enumerate(decoded_routes):
-        rows[i, 0] = int(route.route_id)
-        rows[i, 1] = int(route.stage1_root_id)
-        rows[i, 2] = struct.unpack("=q", struct.pack("=d", float(route.cumulative_logprob)))[0]
+    rows[:, 0] = [int(r.route_id) for r in decoded_routes]
+    rows[:, 1] = [int(r.stage1_root_id) for r in decoded_routes]
+    rows[:, 2] = np.asarray([float(r.cumulative_logprob) for r in decoded_routes], dtype=np.float64).view(np.int64)
     return host.to(device, non_blocking=True)
 
 
@@ -172,30 +171,37 @@ def build_pending_candidate_batch(decoded_routes: Sequence[RouteState], next_tok
     return batch
 
 
-def _float64_from_int64_bits(value: int) -> float:
-    return struct.unpack("=d", struct.pack("=q", int(value)))[0]
+def _new_candidates(parent, root, token, cum, rank, plp) -> list[PendingCandidate]:
+    """PendingCandidate objects from column lists with their field dicts set
+    directly (the frozen dataclass's __init__ costs more than the rest of a
+    frontier depth); equal to PendingCandidate(...) field for field."""
+    new, setattr_ = object.__new__, object.__setattr__
+    out = []
+    for a, b, c, d, e, f in zip(parent, root, token, cum, rank, plp):
+        o = new(PendingCandidate)
+        setattr_(o, "__dict__", {"parent_route_id": a, "stage1_root_id": b, "pending_token_id": c,
+                                 "cumulative_logprob": d, "rank_in_parent": e, "parent_logprob": f})
+        out.append(o)
+    return out
 
 
 def _materialize_records(packed: torch.Tensor, candidate_count: int, selected_count: int,
                          new_node_ids_cpu, transferred_node_count: int, new_node_ids_source: str):
-    rows = packed.detach().cpu().tolist()
-    materialized: list[PendingCandidate] = []
+    host = packed.detach().cpu().numpy()
+    cand = host[:candidate_count]
+    materialized = _new_candidates(cand[:, 1].tolist(), cand[:, 2].tolist(), cand[:, 3].tolist(),
+                                   cand[:, 5].view(np.float64).tolist(), cand[:, 4].tolist(),
+                                   cand[:, 6].view(np.float64).tolist())
     by_order: list[PendingCandidate | None] = [None] * selected_count
-    for row in rows[:candidate_count]:
-        cand = PendingCandidate(parent_route_id=int(row[1]), stage1_root_id=int(row[2]),
-                                pending_token_id=int(row[3]), cumulative_logprob=_float64_from_int64_bits(row[5]),
-                                rank_in_parent=int(row[4]), parent_logprob=_float64_from_int64_bits(row[6]))
-        materialized.append(cand)
-        so = int(row[7])
-        if 0 <= so < selected_count:
-            by_order[so] = cand
+    for i in np.flatnonzero((cand[:, 7] >= 0) & (cand[:, 7] < selected_count)).tolist():
+        by_order[int(cand[i, 7])] = materialized[i]
     if any(c is None for c in by_order):
         raise RuntimeError("selected candidate order was not fully materialized")
     selected = [c for c in by_order if c is not None]
     if new_node_ids_cpu is not None:
         node_ids = [int(n) for n in new_node_ids_cpu]
     else:
-        node_ids = [int(row[1]) for row in rows[candidate_count:]]
+        node_ids = host[candidate_count:, 1].tolist()
         if len(node_ids) != transferred_node_count:
             raise RuntimeError("new node id transfer produced the wrong number of ids")
     on_device = packed.device.type != "cpu"
@@ -302,7 +308,18 @@ def _resolve_new_node_ids(decode_output: FrontierDecodeOutput, *, expected_count
 
 
 def _node_counter_state(route_store: KVTreeStore) -> tuple[int, int] | None:
+    """(next node id, step) of the store's id counter without consuming an
+    id: this package's store reports it; a store counting with
+    itertools.count (``kv.py:30``) is read through its pickling state
+    (``frontier.py:443-456``)."""
     state = getattr(route_store, "node_counter_state", None)
     if callable(state):
         return state()
-    return None
+    reduce_method = getattr(getattr(route_store, "_node_ids", None), "__reduce__", None)
+    if not callable(reduce_method):
+        return None
+    try:
+        args = reduce_method()[1]
+        return int(args[0]), (int(args[1]) if len(args) > 1 else 1)
+    except (IndexError, TypeError, ValueError):
+        return None

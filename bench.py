@@ -603,6 +603,97 @@ def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, 
     return out
 
 
+def frontier_leg(dev, *, rows=72, vocab=128256, k=3, iters=20):
+    """One Drafter frontier depth at the 8-request x 9-route fork shape: 72
+    parent rows of Llama-3.2-1B next-token logits (vocab 128256, bf16), k=3
+    children per parent, the global top-3 of the 216 candidates.  Times the
+    launch pair replayed from a HIP graph (device time; the logits are read
+    by both launches, 18.5 MB from HBM), the whole per-depth call by wall
+    clock (parent rows to the device, launch pair, one copy of the records
+    back, host materialisation), and the same depth as the reference's
+    sequence of torch ops on the same device."""
+    fr = _pkg("flashinfer_paged.frontier")
+    nat = _pkg("flashinfer_paged._frontier_native")
+    types = _pkg("flashinfer_paged.types")
+    lib = _pkg("_lib")
+    g = torch.Generator(device=dev).manual_seed(17)
+    logits = (torch.randn((rows, vocab), generator=g, device=dev) * 3.0).to(torch.bfloat16)
+    routes = [types.RouteState(route_id=1 + i, stage1_root_id=1 + i // 9, parent_route_id=None,
+                               materialized_leaf_node_id=None, pending_token_id=0,
+                               cumulative_logprob=-0.125 * (i % 5), stage1_depth=1, stage2_depth=0,
+                               kv_view=types.PrefixKVView(committed_length=64).fork()) for i in range(rows)]
+    parent_info = fr._parent_info(routes, dev)
+
+    def launch():
+        return nat.frontier_topk(logits, k, parent_info=parent_info, select_mode=lib.FRONTIER_SELECT_GLOBAL,
+                                 num_selected=k)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(3):
+            launch()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = launch()
+    torch.cuda.synchronize()
+    a, b = _ev(), _ev()
+    a.record()
+    for _ in range(iters):
+        graph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    device_us = a.elapsed_time(b) * 1000.0 / iters
+
+    def depth():
+        _, records, _ = fr._fused(routes, logits, k=k, sampling=None, relative_parent_paths=None,
+                                  select_mode=lib.FRONTIER_SELECT_GLOBAL, num_selected=k)
+        return fr._materialize_records(records, rows * k, k, (), 0, "not_applicable")[1]
+
+    def torch_depth():
+        # the reference's depth as torch ops: log_softmax + topk, candidate
+        # columns from host lists, four stable argsorts, packed records, one copy
+        lp, ids = torch.topk(torch.log_softmax(logits, dim=-1), k=k, dim=-1)
+        rid = torch.tensor([r.route_id for r in routes], device=dev, dtype=torch.long).repeat_interleave(k)
+        root = torch.tensor([r.stage1_root_id for r in routes], device=dev, dtype=torch.long).repeat_interleave(k)
+        plp = torch.tensor([r.cumulative_logprob for r in routes], device=dev,
+                           dtype=torch.float64).repeat_interleave(k)
+        rank = torch.arange(k, device=dev, dtype=torch.long).repeat(rows)
+        cum = plp + lp.reshape(-1).to(torch.float64)
+        tok = ids.reshape(-1)
+        order = torch.arange(rows * k, device=dev, dtype=torch.long)
+        for values, desc in ((tok, False), (rank, False), (rid, False), (cum, True)):
+            order = order.index_select(0, torch.argsort(values.index_select(0, order), dim=0, descending=desc,
+                                                        stable=True))
+        sel = order[:k]
+        so = torch.full((rows * k,), -1, device=dev, dtype=torch.long)
+        so[sel] = torch.arange(k, device=dev, dtype=torch.long)
+        rec = torch.stack((torch.zeros_like(rid), rid, root, tok, rank, cum.view(torch.int64), plp.view(torch.int64),
+                           so), dim=1)
+        host = rec.cpu().tolist()
+        return [(h[1], h[3]) for h in sorted((h for h in host if h[7] >= 0), key=lambda h: h[7])]
+
+    def wall(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            r = fn()
+        return (time.perf_counter() - t0) * 1e6 / n, r
+
+    call_us, chosen = wall(depth, iters)
+    torch_us, chosen_t = wall(torch_depth, iters)
+    assert [(c.parent_route_id, c.pending_token_id) for c in chosen] == chosen_t, "frontier selection mismatch"
+    nbytes = rows * vocab * 2
+    return {"rows": rows, "vocab": vocab, "k": k, "dtype": "bf16", "selection": "global top-3",
+            "device_us": round(device_us, 3), "logits_bytes": nbytes,
+            "GBps": round(nbytes / (device_us * 1e-6) / 1e9, 1),
+            "frac": round(nbytes / (device_us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+            "depth_call_us": round(call_us, 1), "torch_sequence_us": round(torch_us, 1)}
+
+
 def drafter_leg(dev, *, requests=8, repeats=3):
     """Drafter route-pool fork stress (Llama-3.2-1B KV geometry, bf16, page
     64): 8 requests, each forking to 9 routes at random fill levels of its
@@ -785,6 +876,7 @@ def main():
         result["components"]["drafter_decode_attn"] = decode_leg(dev)
         result["components"]["drafter_decode_attn_8k"] = decode_leg(dev, prefix_len=8192)
         result["components"]["drafter_fork_8req"] = drafter_leg(dev)
+        result["components"]["drafter_frontier_depth"] = frontier_leg(dev)
         result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
         result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)
     if not args.no_cpu_baseline:
