@@ -24,6 +24,15 @@ Pinning (what each function is checked against in ``tests/``):
                              SGLang's own allocator is absent: parity unpinned
                              against it (only against this restated policy).
 * ``scoring``             -- reference literals (test_target_kv_commit.py:76-367)
+* ``frontier``            -- reference literals of the frontier selection tests
+                             (test_paged_frontier_selection.py:79-130, :189-275),
+                             the Python-object order by brute force (utils.py:27-43),
+                             torch ``topk(log_softmax)``: fp32 exactly, 16-bit rows
+                             against torch's fp32 log-softmax rounded once (torch's
+                             device kernel rounds there; its CPU 16-bit path does
+                             not). The order of equal log-probs inside a parent's
+                             top-k (ascending token) is parity unpinned: torch.topk
+                             leaves it open.
 * ``rope.apply_rope``     -- torch's own 16-bit elementwise ops on the CPU
                              (q * cos + rotate_half(q) * sin, bit for bit, f16
                              and bf16), the identity at angle 0, rotate_half at

@@ -374,3 +374,48 @@ def test_frontier_refusals(dev):
         fr.build_pending_candidate_batch(_routes(types, 200), big, k=32)
     with pytest.raises(ValueError):
         fr.build_pending_candidate_batch(_routes(types, 3), x.to(dev), k=2)
+
+
+def test_frontier_edge_shapes(dev):
+    """Edge shapes of one depth: a single parent, vocab below the chunk size
+    and equal to k, rows with a stride wider than the vocabulary (a slice of
+    a bigger tensor, 16-byte aligned and not), a row of equal logits (ties
+    everywhere), -inf logits, records without a selection (order column -1)
+    with node ids appended."""
+    sampling = pkg("flashinfer_paged.sampling")
+    fr = pkg("flashinfer_paged.frontier")
+    types = pkg("flashinfer_paged.types")
+    gen = torch.Generator().manual_seed(3)
+
+    def check(x, k, dt="f32"):
+        lp, ids = sampling.batch_parent_token_candidates(x.to(dev) if x.device.type == "cpu" else x, k=k,
+                                                         sampling=None, relative_parent_paths=[()] * x.shape[0])
+        olp, oids = ofr.parent_token_candidates(x.float().cpu().numpy(), k, dt)
+        assert np.array_equal(ids.cpu().numpy(), oids)
+        got = lp.float().cpu().numpy()
+        if dt == "f32":
+            assert np.allclose(got, olp, atol=1e-5, rtol=0, equal_nan=True)
+        else:
+            assert np.array_equal(got, olp)
+
+    check(torch.randn((1, 3), generator=gen), 3)
+    check(torch.randn((2, 7), generator=gen), 5)
+    big = (torch.randn((4, 1000), generator=gen) * 2).half().to(dev)
+    check(big[:, :640], 4, "f16")       # stride 1000 elements: rows 16-byte aligned
+    check(big[:, 3:650], 4, "f16")      # rows start 6 bytes in: element loads
+    flat = torch.zeros((3, 5000), dtype=torch.bfloat16)
+    check(flat, 6, "bf16")              # all equal: tokens 0..5
+    ninf = torch.randn((2, 300), generator=gen)
+    ninf[:, ::2] = float("-inf")
+    check(ninf, 3)
+    routes = [types.RouteState(route_id=5 + i, stage1_root_id=1, parent_route_id=None, materialized_leaf_node_id=None,
+                               pending_token_id=0, cumulative_logprob=0.5 * i, stage1_depth=0, stage2_depth=0,
+                               kv_view=types.PrefixKVView(committed_length=1).fork()) for i in range(3)]
+    x = torch.randn((3, 900), generator=gen).to(dev)
+    batch, records, _ = fr._fused(routes, x, k=2, sampling=None, relative_parent_paths=None,
+                                  node_ids=torch.tensor([41, 42, 43]))
+    torch.cuda.synchronize()
+    rec = records.cpu().numpy()
+    assert rec.shape == (6 + 3, 8) and (rec[:6, 7] == -1).all()
+    assert rec[6:, :2].tolist() == [[1, 41], [1, 42], [1, 43]] and (rec[6:, 2:] == 0).all()
+    assert rec[:6, 1].tolist() == [5, 5, 6, 6, 7, 7] and rec[:6, 4].tolist() == [0, 1] * 3
