@@ -106,7 +106,7 @@ __device__ __forceinline__ void for_chunk(const char* row, int64_t c0, int64_t c
 }
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
-constexpr int kRegGroups = 4;  // 16-byte groups per thread a register-held chunk has at most
+constexpr int kRegGroups = 8;  // 16-byte groups per thread a register-held chunk has at most
 
 // A chunk of a 16-byte aligned row held in registers: thread t holds groups
 // t, t + kFThreads, ... (all loads issued together, so a caller can start
@@ -757,11 +757,14 @@ __global__ __launch_bounds__(kFThreads) void frontier_topk_kernel(FrontierArgs a
       mx = up ? x : mx;
       mi = up ? i : mi;
     });
-    TopList<KM> one;
-    one.clear();
-    if (mi >= 0) one.a[0] = token_key(round_dt<DT>((mx - row_max) - lse), uint32_t(mi));
-    block_topk<KM>(one, k, lists, wave_lists, best);
-    const uint64_t bound = best[k - 1];
+    // (per wave: the k-th largest of its 64 keys bounds the chunk's k-th key
+    // as well, without a barrier)
+    uint64_t head = mi >= 0 ? token_key(round_dt<DT>((mx - row_max) - lse), uint32_t(mi)) : 0;
+    uint64_t bound = 0;
+    for (int r = 0; r < k; ++r) {
+      bound = wave_max_u64(head);
+      if (head == bound) head = 0;  // keys are distinct
+    }
     float cut = -INFINITY;
     if (bound != 0) {
       const float lb = key_value(bound);
@@ -856,12 +859,12 @@ struct Geometry {
   bool reg_chunks;
 };
 
-// Chunks of a multiple of 8 elements: about 768 (row, chunk) workgroups (all
-// resident at once), chunks that fit in registers (kRegGroups 16-byte groups
-// per thread) where the vocabulary allows, at least ~512 elements, at most
-// kMaxChunks per row.
+// Chunks of a multiple of 8 elements: about 512 (row, chunk) workgroups (all
+// resident at once) but no more chunks than register-held chunks need
+// (kRegGroups 16-byte groups per thread) unless the rows are few, at least
+// ~512 elements, at most kMaxChunks per row.
 Geometry frontier_geometry(int64_t rows, int64_t vocab, int esize) {
-  constexpr int64_t kTargetGroups = 768;
+  constexpr int64_t kTargetGroups = 512;
   const int64_t reg_len = int64_t(kFThreads) * kRegGroups * (16 / esize);
   int64_t nc = (kTargetGroups + rows - 1) / rows;
   nc = std::min<int64_t>(nc, (vocab + 511) / 512);
