@@ -200,6 +200,10 @@ class NativeReqToTokenPool:
         if hasattr(req, "req_pool_idx"):
             req.req_pool_idx = None
 
+    # the bridge may write all routes' row slices of a frontier in one
+    # tensor-index write
+    batched_row_writes = True
+
     def write(self, indices, values: torch.Tensor) -> None:
         self.req_to_token[indices] = values.to(device=self.device, dtype=torch.int64)
 

@@ -732,8 +732,6 @@ class SGLangRoutePoolBridge:
         if not active_routes:
             raise ValueError("active_routes cannot be empty")
         req_indices = self.ensure_route_rows(active_routes)
-        input_ids = torch.tensor([int(r.pending_token_id) for r in active_routes], dtype=torch.long,
-                                 device=self.device)
         paths = [self._slot_path_for_route(r) for r in active_routes]
         paths, dirty = self._copy_partial_tail_pages_with_dirty_starts(active_routes, paths)
         for index, start in dirty.items():
@@ -760,15 +758,25 @@ class SGLangRoutePoolBridge:
                                  "tail-page copy-on-write is not active")
         self._record_pending_owned_slots(output_slot_ids)
 
+        # Every route's new path (its path, then its new slot) in one buffer;
+        # the routes keep views of it.
+        pieces: list[torch.Tensor] = []
+        for i, path in enumerate(paths):
+            pieces.append(path)
+            pieces.append(output_slot_ids[i : i + 1])
+        flat = torch.cat(pieces)
         positions: list[int] = []
         full_paths: list[torch.Tensor] = []
-        for i, (route, path) in enumerate(zip(active_routes, paths)):
+        segments: list[tuple[int, int, torch.Tensor, str]] = []
+        off = 0
+        for route, path in zip(active_routes, paths):
             rid = int(route.route_id)
             row = self.route_rows[rid]
-            full = torch.cat([path, output_slot_ids[i : i + 1]])
             prev = int(path.numel())
+            full = flat[off : off + prev + 1]
+            off += prev + 1
             if int(row.written_length) == 0:
-                start, values, kind = 0, full, "full_init"
+                start, kind = 0, "full_init"
             else:
                 if int(row.written_length) != prev:
                     raise RuntimeError(
@@ -776,21 +784,54 @@ class SGLangRoutePoolBridge:
                         f"route_id={rid}, written_length={int(row.written_length)}, physical_path_length={prev}"
                     )
                 if row.pending_dirty_start is None:
-                    start, values, kind = prev, full[prev:], "append"
+                    start, kind = prev, "append"
                 else:
-                    start = int(row.pending_dirty_start)
-                    values, kind = full[start:], "cow_patch"
-            self._write_req_token_slice(int(row.req_pool_index), start, values, write_kind=kind)
-            row.written_length = int(full.numel())
-            row.pending_dirty_start = None
-            self.route_slot_paths[rid] = full
-            if prev % self.page_size == 0 or rid not in self.route_tail_page_keys:
-                self.route_tail_page_keys[rid] = self._new_tail_page_key()
-            positions.append(int(full.numel()) - 1)
+                    start, kind = int(row.pending_dirty_start), "cow_patch"
+            segments.append((int(row.req_pool_index), start, full[start:], kind))
+            positions.append(prev)
             full_paths.append(full)
 
+        def commit_route(i: int) -> None:
+            # a route's state moves on only once its row write went through
+            rid = int(active_routes[i].route_id)
+            row = self.route_rows[rid]
+            prev = positions[i]
+            row.written_length = prev + 1
+            row.pending_dirty_start = None
+            self.route_slot_paths[rid] = full_paths[i]
+            if prev % self.page_size == 0 or rid not in self.route_tail_page_keys:
+                self.route_tail_page_keys[rid] = self._new_tail_page_key()
+
+        # input ids, sequence lengths, positions (and, for a pool that takes
+        # them, the request-row write indices) reach the device in one copy
+        b = len(active_routes)
+        host = [int(r.pending_token_id) for r in active_routes] + seq_lens + positions
+        batched = bool(getattr(self.req_to_token_pool, "batched_row_writes", False))
+        write_rows: list[int] = []
+        write_pos: list[int] = []
+        if batched:
+            for req_row, start, values, _ in segments:
+                n = int(values.numel())
+                write_rows.extend([req_row] * n)
+                write_pos.extend(range(start, start + n))
+        on_device = torch.device(self.device).type != "cpu"
+        packed = torch.tensor(host + write_rows + write_pos, dtype=torch.long, pin_memory=on_device)
+        if on_device:
+            packed = packed.to(self.device, non_blocking=True)
+        input_ids, seq_dev, pos_dev = packed[:b], packed[b : 2 * b], packed[2 * b : 3 * b]
+        if batched:
+            nw = len(write_rows)
+            self._write_req_token_slices(segments, packed[3 * b : 3 * b + nw], packed[3 * b + nw :])
+            for i in range(b):
+                commit_route(i)
+        else:
+            # per-route slice writes, as a foreign pool (and the reference's
+            # tests of its write log) expect them
+            for i, (req_row, start, values, kind) in enumerate(segments):
+                self._write_req_token_slice(req_row, start, values, write_kind=kind)
+                commit_route(i)
+
         seq_cpu = torch.tensor(seq_lens, dtype=torch.long)
-        seq_dev = seq_cpu.to(self.device)
         tokens = int(sum(seq_lens))
         spec = None
         attn_ps = 1
@@ -808,7 +849,7 @@ class SGLangRoutePoolBridge:
         self.attention_metadata_page_indices += page_indices
         meta = SGLangRouteKVMetadata(
             req_pool_indices=req_indices, seq_lens=seq_dev, out_cache_loc=output_slot_ids,
-            positions=torch.tensor(positions, dtype=torch.long, device=self.device), orig_seq_lens=seq_dev,
+            positions=pos_dev, orig_seq_lens=seq_dev,
             seq_lens_sum=tokens, seq_lens_cpu=seq_cpu, attention_page_size=attn_ps, token_index_count=tokens,
             page_index_count=page_indices, paged_decode_spec=spec,
         )
@@ -891,18 +932,26 @@ class SGLangRoutePoolBridge:
     def _write_req_token_row(self, req_pool_index: int, slot_path: torch.Tensor) -> None:
         self._write_req_token_slice(req_pool_index, 0, slot_path, write_kind="full_init")
 
-    def _write_req_token_slice(self, req_pool_index: int, start: int, slot_ids: torch.Tensor, *,
-                               write_kind: str) -> None:
-        """Write ``slot_ids`` into a request row at ``start`` (slice API, then
-        the tensor-index form); counters count successful writes only
-        (``sglang_runtime.py:1031-1092``)."""
+    def _write_req_token_slices(self, segments, rows: torch.Tensor, positions: torch.Tensor) -> None:
+        """The request-row writes of one frontier, (row, start, slot ids,
+        kind) each, as one tensor-index write (rows / positions already on the
+        device) into a pool that declares ``batched_row_writes``; checks and
+        counters per segment as for ``_write_req_token_slice``."""
+        for req_row, start, values, kind in segments:
+            self._check_req_write(req_row, start, int(values.numel()), kind)
+        values = torch.cat([v for _, _, v, _ in segments]) if len(segments) > 1 else segments[0][2]
+        try:
+            self.req_to_token_pool.write((rows, positions), values)
+        except Exception as exc:
+            raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
+        for _, _, values, kind in segments:
+            self._count_req_write(int(values.numel()), kind)
+
+    def _check_req_write(self, req_pool_index: int, start: int, n: int, write_kind: str) -> None:
         if write_kind not in {"full_init", "append", "cow_patch"}:
             raise ValueError(f"unknown req-row write kind: {write_kind}")
-        start = int(start)
         if start < 0:
             raise ValueError("req-row write start must be non-negative")
-        values = _as_long(slot_ids, self.device)
-        n = int(values.numel())
         if n <= 0:
             raise ValueError("req-row write cannot be empty")
         end = start + n
@@ -915,15 +964,8 @@ class SGLangRoutePoolBridge:
                 f"write_end={end}, req_pool_context_capacity={int(cap)}, req_pool_index={int(req_pool_index)}. "
                 "Increase --context-length or recreate the runner with a larger ReqToTokenPool."
             )
-        try:
-            self.req_to_token_pool.write((int(req_pool_index), slice(start, end)), values)
-        except Exception:
-            pos = torch.arange(start, end, dtype=torch.long, device=values.device)
-            rows = torch.full_like(pos, int(req_pool_index))
-            try:
-                self.req_to_token_pool.write((rows, pos), values)
-            except Exception as exc:
-                raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
+
+    def _count_req_write(self, n: int, write_kind: str) -> None:
         self.req_row_write_calls += 1
         self.req_row_elements_written += n
         if write_kind == "full_init":
@@ -937,6 +979,29 @@ class SGLangRoutePoolBridge:
         else:
             self.req_row_cow_patch_calls += 1
             self.req_row_cow_patch_elements += n
+
+    def _write_req_token_slice(self, req_pool_index: int, start: int, slot_ids: torch.Tensor, *,
+                               write_kind: str) -> None:
+        """Write ``slot_ids`` into a request row at ``start`` (slice API, then
+        the tensor-index form); counters count successful writes only
+        (``sglang_runtime.py:1031-1092``)."""
+        if write_kind not in {"full_init", "append", "cow_patch"}:
+            raise ValueError(f"unknown req-row write kind: {write_kind}")
+        start = int(start)
+        values = _as_long(slot_ids, self.device)
+        n = int(values.numel())
+        self._check_req_write(req_pool_index, start, n, write_kind)
+        end = start + n
+        try:
+            self.req_to_token_pool.write((int(req_pool_index), slice(start, end)), values)
+        except Exception:
+            pos = torch.arange(start, end, dtype=torch.long, device=values.device)
+            rows = torch.full_like(pos, int(req_pool_index))
+            try:
+                self.req_to_token_pool.write((rows, pos), values)
+            except Exception as exc:
+                raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
+        self._count_req_write(n, write_kind)
 
     def hot_path_counters(self) -> dict[str, int]:
         return {name: int(getattr(self, name)) for name in _COUNTERS}
