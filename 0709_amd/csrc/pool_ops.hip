@@ -70,6 +70,74 @@ __global__ __launch_bounds__(kSweepThreads) void sweep_kernel(uint32_t* owned, c
   if (tid == kSweepThreads - 1) *free_count = scan[tid];
 }
 
+// Mark and sweep in one workgroup for pools whose live bitmap fits in LDS
+// (kFusedWords words): the live bits are set with LDS atomics (the marking
+// rule of mark_pages_kernel), then the sweep of sweep_kernel reads them from
+// LDS.  The live bitmap is also written out, as the three-launch path leaves
+// it.  Each thread takes up to kFusedBatch slots, all loaded before the first
+// atomic.  Larger slot lists go to the marking grid: one workgroup marking
+// tens of thousands of slots measured slower than the three launches.
+constexpr int64_t kFusedWords = 16384;
+constexpr int kFusedBatch = 4;
+constexpr int64_t kFusedMaxSlots = int64_t(kSweepThreads) * kFusedBatch;
+
+__global__ __launch_bounds__(kSweepThreads) void prune_fused_kernel(uint32_t* owned, uint32_t* live_out,
+                                                                    int64_t num_pages, int64_t num_words,
+                                                                    const int64_t* slots, int64_t n,
+                                                                    int64_t page_size, int page_shift,
+                                                                    int64_t* free_pages, int64_t* free_count) {
+  __shared__ uint32_t live[kFusedWords];
+  __shared__ int64_t scan[kSweepThreads];
+  const int tid = threadIdx.x;
+  for (int64_t w = tid; w < num_words; w += kSweepThreads) live[w] = 0u;
+  __syncthreads();
+  {
+    int64_t cur[kFusedBatch], prev[kFusedBatch];
+#pragma unroll
+    for (int k = 0; k < kFusedBatch; ++k) {
+      const int64_t i = int64_t(k) * kSweepThreads + tid;
+      cur[k] = i < n ? slots[i] : -1;
+      prev[k] = (i > 0 && i < n) ? slots[i - 1] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kFusedBatch; ++k) {
+      if (cur[k] < 0) continue;
+      const int64_t page = page_shift >= 0 ? cur[k] >> page_shift : cur[k] / page_size;
+      if (page >= num_pages) continue;
+      if (prev[k] >= 0 && (page_shift >= 0 ? prev[k] >> page_shift : prev[k] / page_size) == page) continue;
+      atomicOr(&live[page >> 5], 1u << (page & 31));
+    }
+  }
+  __syncthreads();
+  const int64_t per = (num_words + kSweepThreads - 1) / kSweepThreads;
+  const int64_t w0 = min(num_words, int64_t(tid) * per);
+  const int64_t w1 = min(num_words, w0 + per);
+  int64_t cnt = 0;
+  for (int64_t w = w0; w < w1; ++w) cnt += __popc(owned[w] & ~live[w]);
+  scan[tid] = cnt;
+  __syncthreads();
+  for (int off = 1; off < kSweepThreads; off <<= 1) {
+    const int64_t add = tid >= off ? scan[tid - off] : 0;
+    __syncthreads();
+    scan[tid] += add;
+    __syncthreads();
+  }
+  int64_t pos = scan[tid] - cnt;
+  for (int64_t w = w0; w < w1; ++w) {
+    const uint32_t ow = owned[w];
+    const uint32_t lv = live[w];
+    uint32_t rel = ow & ~lv;
+    while (rel) {
+      const int b = __ffs(rel) - 1;
+      free_pages[pos++] = w * 32 + b;
+      rel &= rel - 1;
+    }
+    owned[w] = ow & lv;
+    live_out[w] = lv;
+  }
+  if (tid == kSweepThreads - 1) *free_count = scan[tid];
+}
+
 // Page tables from concatenated slot paths.  Thread per page: the page id is
 // the slot of the page's first token divided by page_size; the layout check
 // requires that first slot to be page-aligned and every later slot of the page
@@ -197,6 +265,13 @@ extern "C" int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitm
   ATLAS_REQUIRE(n_live_slots == 0 || live_slots_dev, "live slots must not be NULL");
   hipStream_t s = static_cast<hipStream_t>(stream);
   const int64_t words = (num_pages + 31) / 32;
+  if (words <= kFusedWords && n_live_slots <= kFusedMaxSlots) {
+    hipLaunchKernelGGL(prune_fused_kernel, dim3(1), dim3(kSweepThreads), 0, s, owned_bitmap_dev,
+                       live_bitmap_dev, num_pages, words, live_slots_dev, n_live_slots, page_size,
+                       ilog2_exact(page_size), free_pages_dev,
+                       free_count_dev);
+    return launch_status("prune_fused_kernel");
+  }
   const int fill_blocks = static_cast<int>(std::min<int64_t>((words + 255) / 256, 1024));
   hipLaunchKernelGGL(fill_u32_kernel, dim3(fill_blocks), dim3(256), 0, s, live_bitmap_dev, words, 0u);
   int rc = launch_status("fill_u32_kernel");

@@ -70,6 +70,38 @@ def test_prune_random_matches_oracle(dev, num_pages):
     assert freed == exp_freed and left == exp_left
 
 
+@pytest.mark.parametrize("num_pages,n_slots,ps", [
+    (524288, 3000, 16),   # one workgroup: the largest bitmap kept in LDS
+    (4096, 4096, 16),     # one workgroup: the most slots it takes
+    (4096, 4000, 24),     # one workgroup, page size not a power of two
+    (524289, 3000, 16),   # clear + mark + sweep launches: bitmap too large for LDS
+    (4096, 4097, 16),     # the same launches: more slots than one workgroup takes
+])
+def test_prune_fused_and_multi_launch_paths(dev, num_pages, n_slots, ps):
+    """Both prune paths give releasable = sorted(owned - live), owned &= live
+    (sglang_runtime.py:507-539) and leave the live bitmap set; slots that are
+    negative or past the pool are ignored."""
+    lib = _lib()
+    rng = np.random.default_rng(num_pages + n_slots + ps)
+    owned = set(rng.choice(num_pages, size=min(num_pages, 20000), replace=False).tolist())
+    slots = rng.integers(-ps, (num_pages + 8) * ps, size=n_slots)
+    slots[::97] = -1
+    live = {int(x) // ps for x in slots if 0 <= x < num_pages * ps}
+    owned_bm = _bitmap(owned, num_pages, dev)
+    live_bm = torch.full_like(owned_bm, -1)
+    free = torch.full((num_pages,), -1, dtype=torch.int64, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+    slots_t = torch.tensor(slots, dtype=torch.int64, device=dev)
+    rc = lib.load().atlas_prune_pages(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, lib.ptr(slots_t),
+                                      n_slots, ps, lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev))
+    lib.check(rc, "prune")
+    torch.cuda.synchronize()
+    n = int(cnt.item())
+    assert free[:n].cpu().tolist() == sorted(owned - live)
+    assert _set_from_bitmap(owned_bm) == owned & live
+    assert _set_from_bitmap(live_bm) == live
+
+
 def test_prune_empty_live_frees_everything_ascending(dev):
     owned = {5, 3, 900, 64, 31, 32}
     freed, left = _prune(dev, owned, [], 1000, 16)
