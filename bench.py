@@ -462,7 +462,9 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
     destination pages, 189 MB of source plus destination rows each) are
     timed in rotation, so the working set (1.5 GB) exceeds L2 and the 256 MB
     Infinity Cache and every copy streams from and to HBM.  The same step
-    repeated on one instance (``hot_*``) runs from those caches."""
+    repeated on one instance (``hot_*``) runs from those caches.  ``us`` is the
+    device time per launch from a HIP graph; ``call_us`` the eager per-call
+    time with the host work between launches."""
     kv_ops = _pkg("kv_ops")
     wl = _pkg("workloads")
     geom = wl.LLAMA_1B
@@ -492,22 +494,51 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
         kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
     torch.cuda.synchronize()
     a, b = _ev(), _ev()
+    # Per eager call: host work between launches included.
     a.record()
     for i in range(iters):
         d_t, s_t = sets[i % instances]
         kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
     b.record()
     torch.cuda.synchronize()
-    us = a.elapsed_time(b) * 1000.0 / iters
-    a.record()
-    for _ in range(iters):
+    call_us = a.elapsed_time(b) * 1000.0 / iters
+    # Device time of the launch, from a HIP graph of the instances in
+    # rotation (no host work between launches), as the commit leg is timed.
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
         kv_ops.move_slots(k_layers, v_layers, sets[0][0], sets[0][1])
+    torch.cuda.current_stream().wait_stream(side)
+    rounds = max(1, iters // instances)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(rounds * instances):
+            d_t, s_t = sets[i % instances]
+            kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
+    hgraph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(hgraph):
+        for _ in range(rounds * instances):
+            kv_ops.move_slots(k_layers, v_layers, sets[0][0], sets[0][1])
+    graph.replay()
+    hgraph.replay()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(3):
+        graph.replay()
     b.record()
     torch.cuda.synchronize()
-    hot_us = a.elapsed_time(b) * 1000.0 / iters
+    us = a.elapsed_time(b) * 1000.0 / (3 * rounds * instances)
+    a.record()
+    for _ in range(3):
+        hgraph.replay()
+    b.record()
+    torch.cuda.synchronize()
+    hot_us = a.elapsed_time(b) * 1000.0 / (3 * rounds * instances)
+    del graph, hgraph
     moved = slots * geom.layers * geom.token_bytes()
     return {"us": us, "moved_bytes": moved, "GBps": 2 * moved / (us * 1e-6) / 1e9, "slots": slots,
             "instances": instances, "working_set_bytes": 2 * moved * instances,
+            "call_us": call_us, "call_GBps": 2 * moved / (call_us * 1e-6) / 1e9,
             "hot_us": hot_us, "hot_GBps": 2 * moved / (hot_us * 1e-6) / 1e9}
 
 
