@@ -823,7 +823,11 @@ __global__ __launch_bounds__(kFThreads) void frontier_topk_kernel(FrontierArgs a
       publish_i64(r + 4, t);
       publish_i64(r + 5, __double_as_longlong(plp + static_cast<double>(lp)));
       publish_i64(r + 6, pi[2]);
-      r[7] = -1;
+      // The order column belongs to the selecting workgroup whenever one
+      // runs (it writes r[7] of every candidate, -1 included); a plain store
+      // here as well would leave two XCDs' L2s holding the line dirty, and
+      // the value that reaches memory would depend on their write-back order.
+      if (a.sel.mode < 0) r[7] = -1;
     }
   }
   if (a.sel.mode < 0) return;

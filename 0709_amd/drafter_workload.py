@@ -14,8 +14,10 @@ The sequence per request (``run``):
 2. ``steps`` frontier decode steps; before step t every active route forks
    into ``forks[t]`` children (forks happen at arbitrary fill levels of the
    shared tail page, so the children's first frontier copies the tail);
-3. commit a route (an ancestor of a random final route at depth
-   ``commit_depth``), keep its descendants, promote, prune;
+3. commit a route (an ancestor at depth ``commit_depth`` of a random final
+   route, or, with ``select="best"``, of the final route with the highest
+   sum of its nodes' log-probs, each node drawn as -(u * 5), u uniform in
+   [0, 1)), keep its descendants, promote, prune;
 4. ``post_steps`` decode steps of the kept routes;
 5. fallback EXTEND: drop every route, prune, append ``extend_tokens``
    known tokens to the prefix with one EXTEND, then decode ``post_steps``
@@ -60,14 +62,16 @@ class ForkPlan:
     post_steps: int
     extend_tokens: tuple[int, ...]
     seed: int
+    select: str = "random"  # "random" or "best" (highest sum of node log-probs)
 
 
 def config1_plans(seed: int = 0) -> list[ForkPlan]:
     """1000-token prefix (tail page holds 8 at page 16), k=3 routes of depth 4
-    forking at the prefix; commit one whole route, keep it."""
+    forking at the prefix; commit the whole route with the highest sum of
+    random node log-probs, keep it."""
     rng = random.Random(seed)
     return [ForkPlan(prefix_len=1000, steps=4, forks={0: 3}, commit_depth=4, post_steps=1,
-                     extend_tokens=tuple(rng.randrange(VOCAB) for _ in range(4)), seed=seed)]
+                     extend_tokens=tuple(rng.randrange(VOCAB) for _ in range(4)), seed=seed, select="best")]
 
 
 def config5_plans(n_requests: int = 8, page_size: int = 64, seed: int = 0) -> list[ForkPlan]:
@@ -130,6 +134,11 @@ class RequestState:
     prefix_value_ids: list[int] = field(default_factory=list)
     node_value_ids: dict[int, int] = field(default_factory=dict)
     stats: list[dict[str, int]] = field(default_factory=list)
+    # select="best": each materialized node's log-prob, from its own generator
+    # (the request's main generator, which draws tokens, is left as it is)
+    node_logprobs: dict[int, float] = field(default_factory=dict)
+    logprob_rng: random.Random | None = None
+    selected_route_id: int | None = None
 
 
 class DrafterForkWorkload:
@@ -155,7 +164,8 @@ class DrafterForkWorkload:
                                            use_page_attention_metadata=use_page_attention_metadata)
             executor = PatternExecutor(self._record_writer, self.ids)
             backend = SGLangFlashInferFrontierModelBackend(route_store=store, executor=executor, route_pool=bridge)
-            self.requests.append(RequestState(plan, store, bridge, backend, random.Random(plan.seed)))
+            self.requests.append(RequestState(plan, store, bridge, backend, random.Random(plan.seed),
+                                              logprob_rng=random.Random(plan.seed + 0x5EED)))
         self._last_write: tuple[torch.Tensor, torch.Tensor] | None = None
 
     def _record_writer(self, slots: torch.Tensor, vids: torch.Tensor) -> None:
@@ -196,6 +206,8 @@ class DrafterForkWorkload:
         slots, vids = self._last_write
         for nid, v in zip(out.new_node_ids, vids.tolist()):
             req.node_value_ids[int(nid)] = int(v)
+            if req.plan.select == "best":
+                req.node_logprobs[int(nid)] = -(req.logprob_rng.random() * 5.0)
         req.store.mark_routes_materialized(req.active, out.new_node_ids, DecodePhase.STAGE1)
         for r in req.active:
             r.pending_token_id = req.rng.randrange(VOCAB)
@@ -211,7 +223,14 @@ class DrafterForkWorkload:
 
     def commit(self) -> None:
         for req in self.requests:
-            final = req.rng.choice(req.active)
+            if req.plan.select == "best":
+                # the Target's target_best order (src/atlas_0709/target_runtime.py:444-451):
+                # score, then the draft path log-prob, then the lower route id
+                final = max(req.active, key=lambda r: (self.route_score(req, r), float(r.cumulative_logprob),
+                                                       -int(r.route_id)))
+            else:
+                final = req.rng.choice(req.active)
+            req.selected_route_id = int(final.route_id)
             committed = final
             while committed.total_materialized_depth() > req.plan.commit_depth:
                 committed = req.store.routes[int(committed.parent_route_id)]
@@ -255,6 +274,14 @@ class DrafterForkWorkload:
         cb("post_decode")
         self.fallback_extend()
         cb("extend")
+
+    @staticmethod
+    def route_score(req: RequestState, route: RouteState) -> float:
+        """Sum of the log-probs of a route's materialized nodes, in node order."""
+        total = 0.0
+        for n in route.kv_view.node_ids:
+            total += req.node_logprobs[int(n)]
+        return total
 
     # ------------------------------------------------------------ expected content
     def expected_path_values(self, req: RequestState, route: RouteState) -> list[int]:

@@ -212,7 +212,8 @@ def _tree_spec(
     flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.
-        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask)
+        # The version counter lets plan() notice an in-place change of the mask.
+        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask, flat_mask._version)
     return TreeSpec(
         flat_token_ids=flat_token_ids,
         parent_indices=list(parent_indices),

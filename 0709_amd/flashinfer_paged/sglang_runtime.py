@@ -657,7 +657,16 @@ class SGLangRoutePoolBridge:
             raise RuntimeError(
                 "SGLang KV pool does not expose move_kv_cache(); tail-page copy-on-write cannot be performed"
             )
-        move(destination.to(dtype=torch.long), source.to(dtype=torch.long))
+        destination = destination.to(dtype=torch.long)
+        source = source.to(dtype=torch.long)
+        # The all-layer move copies every slot independently, so a page that
+        # is both written and read would race; copy-on-write destinations are
+        # freshly allocated pages, which no source path can hold.
+        dst_pages = torch.div(destination, self.page_size, rounding_mode="floor")
+        src_pages = torch.div(source, self.page_size, rounding_mode="floor")
+        self._check_or_defer(~torch.isin(dst_pages, src_pages).any(),
+                             "copy-on-write destination pages overlap its source pages")
+        move(destination, source)
 
     # ------------------------------------------------------------ copy-on-write
     def _copy_partial_tail_pages(self, routes: Sequence[RouteState], slot_paths: Sequence[torch.Tensor]):

@@ -111,6 +111,25 @@ def tree_mask_from_dense(mask2d: torch.Tensor) -> tuple[int, torch.Tensor] | Non
     return col0, bits
 
 
+def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
+    """The (col0, bits) window the tree builder attached to a single-request
+    dense mask, if it still describes this plan: one request, one ancestor
+    word per query row, col0 within the keys and at most 64 tree columns, and
+    the mask not modified in place since (its version counter unchanged).
+    Otherwise None, and the plan derives the window from the mask itself."""
+    cached = getattr(custom_mask, "_atlas_tree_window", None) if custom_mask is not None else None
+    if cached is None or len(qo_lens) != 1 or len(cached) != 3:
+        return None
+    col0, bits, version = cached
+    if version != custom_mask._version or int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
+        return None
+    if int(bits.numel()) != qo_lens[0] or not (0 <= int(col0) <= kv_lens[0]):
+        return None
+    if kv_lens[0] - int(col0) > MAX_TREE_WIDTH:
+        return None
+    return int(col0), bits
+
+
 def unpack_bits_little(packed: torch.Tensor, count: int) -> torch.Tensor:
     """Inverse of a little-bit-order packbits over ``count`` booleans."""
     b = packed.to(torch.uint8).reshape(-1).to(torch.int32)
@@ -237,8 +256,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             if causal:
                 raise ValueError("custom masks require causal=False")
             mask_mode = _lib.MASK_TREE
-            cached = getattr(custom_mask, "_atlas_tree_window", None) if custom_mask is not None else None
-            if cached is not None and batch == 1:
+            cached = _cached_tree_window(custom_mask, qo_lens, kv_lens)
+            if cached is not None:
                 col0, bits = cached
                 cols = [int(col0)]
                 tree_bits = bits.to(device=device, dtype=torch.int64)

@@ -120,3 +120,55 @@ def verify_attention_bytes(geom: Geometry, *, kv_len: int, nodes: int, page_size
 def verify_attention_flops(geom: Geometry, visible_keys: Sequence[int]) -> int:
     """4 * Hq * D flops per visible (query, key) pair (QK^T and PV)."""
     return 4 * geom.q_heads * geom.head_dim * int(sum(visible_keys))
+
+
+@dataclass
+class BatchedVerifyCase:
+    """Host description of the batched Target verify (32 requests, 8B
+    geometry, page 16): per request a committed prefix, a k=3 d=4 tree of
+    independent routes, its pages scattered over a pool, and the route its
+    commit selects.  ``page_ids`` lists every request's pages in request
+    order (request b's pages are ``page_ids[kv_indptr[b]:kv_indptr[b + 1]]``)."""
+
+    page_size: int
+    pool_pages: int
+    prefixes: list[int]
+    routes: list[list[tuple[int, ...]]]
+    nodes: list[int]
+    kv_lens: list[int]
+    req_pages: list[int]
+    kv_indptr: list[int]
+    qo_indptr: list[int]
+    page_ids: torch.Tensor  # int64 [sum(req_pages)], distinct pool pages
+    selected: list[int]  # route index committed per request
+
+    @property
+    def need_pages(self) -> int:
+        return self.kv_indptr[-1]
+
+
+def batched_verify_case(*, pool_pages: int, requests: int = 32, page_size: int = 16, seed: int = 4,
+                        min_prefix: int = 1024, max_prefix: int = 16384) -> BatchedVerifyCase:
+    """Seeded batched verify: prefixes uniform in [min_prefix, max_prefix],
+    routes ``tree_routes(100 + b)`` (12 nodes after dedup), pages drawn
+    without replacement from ``pool_pages`` by a random permutation, and a
+    uniformly drawn route to commit per request."""
+    gen = torch.Generator().manual_seed(seed)
+    prefixes = [int(x) for x in torch.randint(min_prefix, max_prefix + 1, (requests,), generator=gen)]
+    routes = [tree_routes(100 + b) for b in range(requests)]
+    nodes = [len({tuple(r[: i + 1]) for r in rs for i in range(len(r))}) for rs in routes]
+    kv_lens = [p + n for p, n in zip(prefixes, nodes)]
+    req_pages = [math.ceil(k / page_size) for k in kv_lens]
+    kv_indptr = [0]
+    for n in req_pages:
+        kv_indptr.append(kv_indptr[-1] + n)
+    qo_indptr = [0]
+    for n in nodes:
+        qo_indptr.append(qo_indptr[-1] + n)
+    if kv_indptr[-1] > pool_pages:
+        raise ValueError(f"pool of {pool_pages} pages is smaller than the {kv_indptr[-1]} pages requested")
+    page_ids = torch.randperm(pool_pages, generator=gen)[: kv_indptr[-1]]
+    selected = [int(torch.randint(0, len(r), (1,), generator=gen)) for r in routes]
+    return BatchedVerifyCase(page_size=page_size, pool_pages=pool_pages, prefixes=prefixes, routes=routes,
+                             nodes=nodes, kv_lens=kv_lens, req_pages=req_pages, kv_indptr=kv_indptr,
+                             qo_indptr=qo_indptr, page_ids=page_ids, selected=selected)

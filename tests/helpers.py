@@ -21,3 +21,28 @@ def bits16(t):
     if isinstance(t, torch.Tensor):
         return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
     return np.asarray(t).view(np.uint16)
+
+
+def check_allocator_invariants(num_pages, free_pages, owned_by_request, live_slots_by_request, page_size, where=""):
+    """What the paged allocator's arithmetic fixes, whatever its free-list order:
+    the free list has no duplicates; the free pages, each request's owned pages
+    and the padding page 0 are pairwise disjoint and together cover the pool
+    (pages 0..num_pages); every live slot (committed prefix and route paths)
+    lies on a page its own request owns."""
+    free = [int(p) for p in free_pages]
+    assert len(set(free)) == len(free), f"{where}: duplicate pages in the free list"
+    seen = {0: "padding"}
+    for p in free:
+        assert p not in seen, f"{where}: free page {p} is also {seen[p]}"
+        seen[p] = "free"
+    for r, owned in enumerate(owned_by_request):
+        for p in owned:
+            p = int(p)
+            assert p not in seen, f"{where}: page {p} owned by request {r} is also {seen[p]}"
+            seen[p] = f"owned by request {r}"
+    assert set(seen) == set(range(num_pages + 1)), \
+        f"{where}: {num_pages + 1 - len(seen)} pages are neither free nor owned"
+    for r, (owned, slots) in enumerate(zip(owned_by_request, live_slots_by_request)):
+        mine = {int(p) for p in owned}
+        stray = {int(s) // page_size for s in slots} - mine
+        assert not stray, f"{where}: request {r} has live slots on pages it does not own: {sorted(stray)[:8]}"

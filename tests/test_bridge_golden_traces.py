@@ -1,4 +1,4 @@
-"""Multi-step route-pool bridge traces against the reference's own bridge.
+"""Multi-step route-pool bridge traces against the reference's bridge classes.
 
 ``tests/golden/bridge_traces.json`` holds the traces of
 ``tests/golden/bridge_trace.py`` run over the reference's ``KVTreeStore``,
@@ -8,7 +8,15 @@
 package's classes on the same host pools; every pool call (allocations, KV
 moves, request-row writes, frees), every frontier's slots and counters, and
 the bridge's state after every phase (slot paths, leases, rows, owned pages,
-reference counts, counters) must be equal."""
+reference counts, counters) must be equal.
+
+What the fixture does not come from: the pools under both bridges are the
+oracle's host pools (``oracle/route_pool.py``), whose free-list policy is a
+restatement of SGLang's paged allocator (SGLang is absent), and the fallback
+EXTEND is the reference's sequence of bridge calls made by the generator,
+because its model forward needs SGLang.  So the bridge logic is pinned
+against the reference; the allocator's free-list order is pinned only by the
+invariants its arithmetic fixes, checked here on every phase of both traces."""
 
 import json
 import os
@@ -17,7 +25,7 @@ from types import SimpleNamespace
 
 import pytest
 
-from helpers import pkg
+from helpers import check_allocator_invariants, pkg
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
 sys.path.insert(0, GOLDEN)
@@ -77,6 +85,31 @@ def test_bridge_trace_equals_reference(golden, scenario):
         assert d is None, f"{scenario}: first difference at {d[0]}: ours {d[1]!r}, reference {d[2]!r}"
 
 
+def _unrle(runs):
+    return [first + i for first, n in runs for i in range(n)]
+
+
+def _check_trace_invariants(trace, label):
+    ps, num_pages = trace["page_size"], trace["num_pages"]
+    for ph in trace["phases"]:
+        owned = [_unrle(r["owned_pages"]) for r in ph["requests"]]
+        live = []
+        for r in ph["requests"]:
+            slots = _unrle(r["prefix"]) if r["prefix"] is not None else []
+            for path in r["paths"].values():
+                slots.extend(_unrle(path))
+            live.append(slots)
+        check_allocator_invariants(num_pages, _unrle(ph["free_pages"]), owned, live, ps,
+                                   where=f"{label} after {ph['phase']}")
+
+
+@pytest.mark.parametrize("scenario", bridge_trace.SCENARIOS)
+def test_trace_allocator_invariants(golden, scenario):
+    _check_trace_invariants(golden[scenario], f"{scenario} (fixture)")
+    ours = json.loads(json.dumps(bridge_trace.run(_mods(), scenario, _extend, oracle_pools=route_pool)))
+    _check_trace_invariants(ours, scenario)
+
+
 def test_golden_traces_exercise_the_rules(golden):
     """The fixture covers what it is meant to: tail copies, request-row
     full inits and appends, promotion, prune frees and the EXTEND.  (A
@@ -94,3 +127,32 @@ def test_golden_traces_exercise_the_rules(golden):
     assert any(d.get("req_row_append_calls", 0) for d in deltas)
     stats = [s for sc in golden.values() for ph in sc["phases"] for s in ph.get("stats", [])]
     assert all(s["released_kv_pages"] >= 0 for s in stats) and any(s["released_kv_pages"] for s in stats)
+
+
+def test_allocator_invariant_check_catches_planted_mistakes(golden):
+    """The invariant check fails on a free page that is also owned, on a
+    duplicate free page, on a leaked page and on a live slot off its owner's
+    pages."""
+    import copy
+
+    trace = golden["fork_mid_page_page4"]
+    _check_trace_invariants(trace, "unchanged")
+    ph = -1
+    owned0 = _unrle(trace["phases"][ph]["requests"][0]["owned_pages"])
+    plants = []
+    t = copy.deepcopy(trace)  # owned page also on the free list
+    t["phases"][ph]["free_pages"].append([owned0[0], 1])
+    plants.append(t)
+    t = copy.deepcopy(trace)  # duplicate free page
+    t["phases"][ph]["free_pages"].append(list(t["phases"][ph]["free_pages"][0][:1]) + [1])
+    plants.append(t)
+    t = copy.deepcopy(trace)  # a page leaked: neither free nor owned
+    t["phases"][ph]["requests"][0]["owned_pages"] = [[p, 1] for p in owned0[1:]]
+    plants.append(t)
+    t = copy.deepcopy(trace)  # a live slot on a page the request does not own
+    stray = next(p for p in range(1, trace["num_pages"] + 1) if p not in owned0)
+    t["phases"][ph]["requests"][0]["prefix"].append([stray * trace["page_size"], 1])
+    plants.append(t)
+    for t in plants:
+        with pytest.raises(AssertionError):
+            _check_trace_invariants(t, "planted")

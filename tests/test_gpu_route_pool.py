@@ -1,12 +1,17 @@
 """Route-pool bridge on the native HIP pools vs the same trace on host pools:
 slot paths, leases, request rows, owned pages, the allocator's free list and
-every live slot's K/V bytes (all layers) must be identical at every phase."""
+every live slot's K/V bytes (all layers) must be identical at every phase.
+Both runs must also hold, at every phase, the invariants the allocator's
+arithmetic fixes (free, owned and padding pages partition the pool, no
+duplicate free page, live slots on their own request's pages), and
+configuration 1 must commit the route the Target's target_best order picks."""
 
 import pytest
 import torch
 
-from helpers import pkg
+from helpers import check_allocator_invariants, pkg
 from oracle.route_pool import OracleAllocator, OracleReqPool
+from oracle.scoring import select_best
 
 pytestmark = pytest.mark.gpu
 
@@ -37,11 +42,13 @@ def _device_run(plans, *, page_size, num_pages, layers, heads, head_dim, dev, ho
         hphase, hs, values = host_phases[i]
         assert hphase == phase
         ds = _state(wl, alloc.free_pages.tolist(), req.req_to_token)
+        _check_invariants(ds, num_pages, page_size, f"device run after {phase}")
         assert ds == hs, f"bookkeeping differs after {phase}"
         _check_kv(kv, values, _live_slots(hs), layers, heads, head_dim, dev, phase)
 
     wl.run(compare)
     assert seen == [p for p, _, _ in host_phases]
+    return wl
 
 
 def _host_run(plans, *, page_size, num_pages, phases):
@@ -51,7 +58,19 @@ def _host_run(plans, *, page_size, num_pages, phases):
     wl = dw.DrafterForkWorkload(plans=plans, req_pool=rows, allocator=alloc, page_size=page_size, device="cpu",
                                 writer=lambda s, v: alloc.kv.write(s.numpy(), v.numpy()),
                                 use_page_attention_metadata=False)
-    wl.run(lambda phase: phases.append((phase, _state(wl, alloc.free_pages, rows.req_to_token), alloc.kv.values.copy())))
+    candidates = []
+
+    def record(phase):
+        state = _state(wl, alloc.free_pages, rows.req_to_token)
+        _check_invariants(state, num_pages, page_size, f"host run after {phase}")
+        phases.append((phase, state, alloc.kv.values.copy()))
+        if phase.startswith("decode"):
+            # the routes the commit chooses among are the last stage-1 step's
+            candidates[:] = [[(int(r.route_id), tuple(int(n) for n in r.kv_view.node_ids),
+                               float(r.cumulative_logprob)) for r in q.active] for q in wl.requests]
+
+    wl.run(record)
+    wl.commit_candidates = candidates
     return wl
 
 
@@ -78,6 +97,12 @@ def _state(wl, free_pages, req_to_token):
             "stats": list(r.stats),
         }
     return out
+
+
+def _check_invariants(state, num_pages, page_size, where):
+    reqs = [v for k, v in state.items() if k != "free"]
+    live = [list(v["prefix"]) + [x for p in v["paths"].values() for x in p] for v in reqs]
+    check_allocator_invariants(num_pages, state["free"], [v["owned"] for v in reqs], live, page_size, where)
 
 
 def _live_slots(state):
@@ -114,9 +139,18 @@ def test_route_pool_trace_matches_host_pools(dev, case):
     layers, heads, head_dim = 16, 8, 64
     print(f"route-pool trace {case}: page_size {ps}, {pages} pages", flush=True)
     host = []
-    _host_run(plans, page_size=ps, num_pages=pages, phases=host)
-    _device_run(plans, page_size=ps, num_pages=pages, layers=layers, heads=heads, head_dim=head_dim, dev=dev,
-                host_phases=host)
+    hw = _host_run(plans, page_size=ps, num_pages=pages, phases=host)
+    dw_run = _device_run(plans, page_size=ps, num_pages=pages, layers=layers, heads=heads, head_dim=head_dim,
+                         dev=dev, host_phases=host)
+    assert [r.selected_route_id for r in dw_run.requests] == [r.selected_route_id for r in hw.requests]
+    if case == "config1":
+        # the committed route is the best by (sum of node log-probs, draft
+        # log-prob, -route id), recomputed from the candidates and node log-probs
+        req = hw.requests[0]
+        scores = [{"selection_score": sum(req.node_logprobs[n] for n in nodes), "draft_path_logprob": cum,
+                   "route_id": rid} for rid, nodes, cum in hw.commit_candidates[0]]
+        assert len(scores) == 3
+        assert req.selected_route_id == select_best(scores)["route_id"]
 
 
 def test_device_ownership_set_operations(dev):

@@ -105,3 +105,23 @@ def test_plan_argument_validation_without_gpu():
         w.plan(torch.tensor([0, 1]), torch.tensor([0, 1]), torch.tensor([0]), torch.tensor([1]), 4, 2, 64, 16)
     with pytest.raises(NotImplementedError):
         ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "HND")
+
+
+def test_cached_tree_window_validated_against_plan():
+    ffv = pkg("flashinfer_full_verify")
+    ta = pkg("tree_attention")
+    spec = ffv.build_tree_spec_from_paths(paths=[(1, 2, 3), (1, 5, 6)], prefix_len=20, page_size=4, device="cpu")
+    n, kv = spec.node_count, spec.kv_len
+    mask = spec.bool_mask
+    col0, bits = ta._cached_tree_window(mask, [n], [kv])
+    assert col0 == 20 and bits.tolist() == spec.tree_mask.tolist()
+    # a plan of another shape, or of several requests, does not take the window
+    assert ta._cached_tree_window(mask, [n], [kv + 1]) is None
+    assert ta._cached_tree_window(mask, [n - 1], [kv]) is None
+    assert ta._cached_tree_window(mask, [n, 1], [kv, kv]) is None
+    # an in-place change of the mask invalidates it; the dense path then agrees
+    # (undeduplicated: node 3 is the second path's root, node 4 its child)
+    mask[4 * kv + 23] = False  # row 4 no longer sees tree node 3
+    assert ta._cached_tree_window(mask, [n], [kv]) is None
+    col0, bits2 = ta.tree_mask_from_dense(mask.view(n, kv))
+    assert col0 == 20 and int(bits[4]) == 0b11000 and int(bits2[4]) == 0b10000

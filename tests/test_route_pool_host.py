@@ -532,3 +532,22 @@ def test_allocation_errors_name_the_allocator_calls():
         b._allocate_full_pages(2)
     with pytest.raises(ValueError):
         b.allocate_token_slots(0)
+
+
+class OverlappingAllocator(MonotoneAllocator):
+    """Hands out page 0 again: a destination that is also a source page."""
+
+    def alloc(self, count):
+        n = count // self.page_size
+        pages = torch.zeros(n, dtype=torch.long)
+        return (pages[:, None] * self.page_size + torch.arange(self.page_size)[None, :]).reshape(-1)
+
+
+def test_cow_rejects_destination_pages_that_overlap_sources():
+    sr, _ = _mods()
+    b = sr.SGLangRoutePoolBridge(req_to_token_pool=RowTable(), token_to_kv_pool_allocator=OverlappingAllocator(4),
+                                 page_size=4, device="cpu", use_page_attention_metadata=True)
+    tail = L(0, 1, 2)
+    with pytest.raises(RuntimeError, match="overlap"):
+        b._copy_partial_tail_pages(ids(1, 2), [tail, tail])
+    assert b.token_to_kv_pool_allocator.kv_cache.moves == []
