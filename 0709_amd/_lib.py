@@ -31,6 +31,7 @@ MASK_TREE = 1
 MASK_CAUSAL = 2
 
 MAX_LAYERS_PER_LAUNCH = 64
+ATTN_SCRATCH_BYTES = 16777216  # device scratch of atlas_tree_verify_attn_noalloc
 MAX_INLINE_ITEMS = 64
 
 _c_i32 = ctypes.c_int32
@@ -90,6 +91,11 @@ _SIGNATURES: dict[str, list] = {
         _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_size_t,
         _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp,
+    ],
+    "atlas_tree_verify_attn_noalloc": [
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
+        _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+        ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp,
     ],
     "atlas_attn_page_windows": [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp],
     "atlas_prune_pages": [_vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp],

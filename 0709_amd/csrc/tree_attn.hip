@@ -26,6 +26,8 @@
 // Masks are applied in registers: keys below mask_col_start are visible to
 // every row, keys at and after it use the row's 64-bit ancestor bitmask; tiles
 // wholly inside the always-visible range skip the mask code.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace atlas {
@@ -1770,6 +1772,7 @@ static int verify_attn_impl(
     const size_t row_bytes = size_t(head_dim) * 2 + 4;
     ATLAS_REQUIRE(workspace_bytes % row_bytes == 0, "workspace_bytes must be partial_rows * (2 * head_dim + 4)");
     const size_t partial_rows = workspace_bytes / row_bytes;
+    ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0, "workspace must be 16-byte aligned");
     args.part_o = static_cast<uint16_t*>(workspace_dev);
     args.part_lse = reinterpret_cast<float*>(args.part_o + partial_rows * head_dim);
     margs.merge = merge_dev;
@@ -1842,4 +1845,71 @@ extern "C" int atlas_tree_verify_attn_append(
                           max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, append_k,
                           append_v, append_stride_token, append_stride_head, rope_cos, rope_sin, rope_stride_token);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free verify attention.  The split-KV partial states live in a
+// file-scope device array instead of a caller workspace: one copy per GPU,
+// loaded with the code object and held until the process ends.  Its device
+// address is looked up once per device (hipGetSymbolAddress, with that device
+// current) and only that address is ever handed to kernels: in host code the
+// array's name is a host-side stand-in, not a device address.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) char scratch[ATLAS_ATTN_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices];
+
+// Device address of the current device's scratch array.
+int current_device_scratch(void** out) {
+  int dev = -1;
+  int rc = hip_status(hipGetDevice(&dev), "hipGetDevice");
+  if (rc != ATLAS_OK) return rc;
+  ATLAS_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "device %d beyond the %d scratch slots", dev,
+                kMaxScratchDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    rc = hip_status(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    if (rc != ATLAS_OK) return rc;
+    ATLAS_REQUIRE(p != nullptr, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ATLAS_OK;
+}
+
+}  // namespace
+
+extern "C" int atlas_tree_verify_attn_noalloc(
+    const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads,
+    int num_kv_heads, int head_dim, int page_size, float sm_scale, int dtype, void* out,
+    int64_t out_stride_token, int64_t out_stride_head, float* lse, int64_t partial_rows, void* stream) {
+  ATLAS_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128, got %d", head_dim);
+  ATLAS_REQUIRE(partial_rows >= 0, "negative partial_rows");
+  const size_t row_bytes = size_t(head_dim) * 2 + 4;
+  ATLAS_REQUIRE(size_t(partial_rows) <= size_t(ATLAS_ATTN_SCRATCH_BYTES) / row_bytes,
+                "%lld partial rows of %zu bytes exceed the %d-byte device scratch (at most %zu rows at head_dim %d)",
+                (long long)partial_rows, row_bytes, ATLAS_ATTN_SCRATCH_BYTES,
+                size_t(ATLAS_ATTN_SCRATCH_BYTES) / row_bytes, head_dim);
+  ATLAS_REQUIRE(num_merge == 0 || partial_rows > 0, "a split plan needs partial_rows > 0");
+  void* ws = nullptr;
+  if (num_merge > 0 && num_work > 0) {
+    const int rc = current_device_scratch(&ws);
+    if (rc != ATLAS_OK) return rc;
+  }
+  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
+                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          out_stride_token, out_stride_head, lse, ws, ws ? size_t(partial_rows) * row_bytes : 0,
+                          stream, nullptr, nullptr, 0, 0, nullptr, nullptr, 0);
 }

@@ -231,6 +231,38 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
                                   const void* rope_cos, const void* rope_sin,
                                   int64_t rope_stride_token, void* stream);
 
+/* Size of the device scratch array behind atlas_tree_verify_attn_noalloc:
+ * 16 MiB per GPU, i.e. up to 64,527 partial rows at head_dim 128
+ * (2 * 128 + 4 bytes each) or 127,100 at head_dim 64. */
+#define ATLAS_ATTN_SCRATCH_BYTES 16777216
+
+/* atlas_tree_verify_attn without a workspace: the split-KV partial states
+ * (partial_rows rows, the count the plan produced; 0 when the plan has no
+ * merge items) go to a device array of ATLAS_ATTN_SCRATCH_BYTES that the
+ * library holds on every GPU it runs on until the process ends, so the call
+ * allocates nothing and needs no workspace from the caller.  A plan whose
+ * partial_rows * (2 * head_dim + 4) exceeds that size is rejected with
+ * ATLAS_EINVAL.  Every call on one GPU shares that GPU's array (nothing in it
+ * needs to start at zero): calls that overlap on one GPU, on different
+ * streams, race and must not be issued.  Results equal atlas_tree_verify_attn
+ * with a workspace bit for bit (same kernels).
+ * No counterpart in the reference: it exists for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops that
+ * forbid allocation). */
+int atlas_tree_verify_attn_noalloc(const void* q, int64_t q_stride_token, int64_t q_stride_head,
+                                   const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
+                                   int64_t token_stride, const int32_t* qo_indptr_dev,
+                                   const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
+                                   const int32_t* kv_len_dev, int mask_mode,
+                                   const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                                   const atlas_attn_work_t* work_dev, int num_work,
+                                   const int32_t* page_window_dev,
+                                   const atlas_attn_merge_t* merge_dev, int num_merge,
+                                   int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                                   int head_dim, int page_size, float sm_scale, int dtype, void* out,
+                                   int64_t out_stride_token, int64_t out_stride_head, float* lse,
+                                   int64_t partial_rows, void* stream);
+
 /* ------------------------------------------------------------------------
  * Reachability prune and free-list return.
  * ---------------------------------------------------------------------- */
