@@ -813,6 +813,21 @@ def cpu_baseline(step: HeadlineStep, budget_s: float):
                       f"(kv_len {step.kv_len}, {step.n} nodes)"}
 
 
+def profile_attention(step: HeadlineStep, launches: int) -> None:
+    """The headline's verify attention alone, eagerly, one layer per launch
+    (the launch pair a counter run attributes to its kernels)."""
+    step.outs = [torch.empty_like(q) for q in step.q]
+    step.plan()
+    torch.cuda.synchronize()
+    plan = step.wrapper.current_plan
+    print(f"profile: {plan.num_work} work items, {plan.num_merge} merge items, {launches} launches", flush=True)
+    for i in range(launches):
+        l = i % step.geom.layers
+        step.wrapper.run(step.q[l], step.layers[l], out=step.outs[l])
+        torch.cuda.synchronize()
+        print(f"profile: launch {i} (layer {l}) done", flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -826,6 +841,9 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run device-to-device copies of MIB MiB (calibrates HBM byte counters)")
     ap.add_argument("--commit-pool-gb", type=float, default=200.0)
+    ap.add_argument("--profile-attention", type=int, default=0, metavar="N",
+                    help="only plan the headline step and run N eager attention launches (one per layer, "
+                         "printing after each), for counter collection")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU; the path is data-parallel across requests "
@@ -833,6 +851,9 @@ def main():
         sys.exit(2)
     dev = torch.device("cuda:0")
     step = HeadlineStep(dev, split_target=args.split_target, max_rows=args.max_rows)
+    if args.profile_attention:
+        profile_attention(step, args.profile_attention)
+        return
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
