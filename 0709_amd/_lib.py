@@ -41,6 +41,7 @@ _VPP = ctypes.POINTER(ctypes.c_void_p)
 
 
 class AttnWork(ctypes.Structure):
+    """atlas_attn_work_t (64 bytes)."""
     _fields_ = [
         ("req", _c_i32),
         ("kv_head", _c_i32),
@@ -49,11 +50,17 @@ class AttnWork(ctypes.Structure):
         ("kv_start", _c_i32),
         ("kv_end", _c_i32),
         ("partial_row", _c_i32),
-        ("pad", _c_i32),
+        ("qo_start", _c_i32),
+        ("qo_len", _c_i32),
+        ("kv_len", _c_i32),
+        ("mask_col_start", _c_i32),
+        ("page_offset", _c_i32),
+        ("pad", _c_i32 * 4),
     ]
 
 
 class AttnMerge(ctypes.Structure):
+    """atlas_attn_merge_t (32 bytes)."""
     _fields_ = [
         ("req", _c_i32),
         ("kv_head", _c_i32),
@@ -103,7 +110,10 @@ _SIGNATURES: dict[str, list] = {
     "atlas_alloc_decode_slots": [_vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_alloc_extend_slots": [_vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_paged_metadata": [_vp, _vp, _vp, ctypes.c_int, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _vp],
-    "atlas_gather_logprobs": [_vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp],
+    "atlas_gather_logprobs_workspace_bytes": [_c_i64, _c_i64],
+    "atlas_gather_logprobs": [
+        _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp, ctypes.c_size_t, _vp,
+    ],
     "atlas_frontier_workspace_bytes": [_c_i64, _c_i64, ctypes.c_int],
     "atlas_frontier_topk": [
         _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _c_i64, ctypes.c_int, _vp, ctypes.c_int, _c_i64, _vp,
@@ -114,7 +124,10 @@ _SIGNATURES: dict[str, list] = {
     ],
 }
 # entry points whose return value is not an int status
-_RESTYPES: dict[str, type] = {"atlas_frontier_workspace_bytes": ctypes.c_int64}
+_RESTYPES: dict[str, type] = {
+    "atlas_frontier_workspace_bytes": ctypes.c_int64,
+    "atlas_gather_logprobs_workspace_bytes": ctypes.c_int64,
+}
 
 FRONTIER_NONE = -1
 FRONTIER_ORDER = 0

@@ -1,12 +1,14 @@
 // Route scoring: per-row log-sum-exp over the vocabulary and the gather of the
 // log-probabilities of the verified tokens, so a verify needs one small
 // device-to-host copy instead of one scalar read per token.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace atlas {
 namespace {
 
-constexpr int kThreads = 1024;
+constexpr int kThreads = 256;
 
 template <int DT>
 __device__ __forceinline__ float load_logit(const char* row, int64_t i) {
@@ -17,21 +19,6 @@ __device__ __forceinline__ float load_logit(const char* row, int64_t i) {
   } else {
     return static_cast<float>(reinterpret_cast<const __bf16*>(row)[i]);
   }
-}
-
-__device__ __forceinline__ float block_reduce(float v, bool is_max, float* red) {
-  for (int off = 32; off > 0; off >>= 1) {
-    const float o = __shfl_xor(v, off);
-    v = is_max ? fmaxf(v, o) : v + o;
-  }
-  const int wave = threadIdx.x >> 6;
-  __syncthreads();  // red[] reuse across calls
-  if ((threadIdx.x & 63) == 0) red[wave] = v;
-  __syncthreads();
-  float t = red[0];
-#pragma unroll
-  for (int w = 1; w < kThreads / 64; ++w) t = is_max ? fmaxf(t, red[w]) : t + red[w];
-  return t;
 }
 
 // 16 bytes of logits -> up to 8 floats.
@@ -62,55 +49,148 @@ struct Vec {
   }
 };
 
-// Block r: log-sum-exp of logits row r (natural log, fp32) in two passes over
-// the row -- the maximum, then the sum of exp2((x - max) * log2 e) (the second
-// pass reads the row back from L2) -- with 16-byte loads when the row is
-// 16-byte aligned; then every gather that reads row r.
+// Workgroup (c, r) reads chunk c of logits row r once: the chunk's maximum m
+// and the sum of exp(x - m), kept online per thread (16-byte loads when the
+// rows are 16-byte aligned), then reduced over the workgroup.  It writes the
+// pair through to memory (agent scope: read by whichever XCD finishes the
+// row) and counts itself into the row's counter; the row's last chunk
+// combines the pairs in chunk order -- a fixed order, whichever chunk arrives
+// last, so the LSE is the same on every run -- writes the row LSE and every
+// gather that reads row r, and clears the counter for the next call.
+struct GatherArgs {
+  const char* logits;
+  int64_t row_stride_bytes;
+  int64_t vocab;
+  const int32_t* rows;
+  const int64_t* tokens;
+  int64_t n;
+  float* row_lse;
+  float* out;
+  float2* stats;    // [num_rows, num_chunks]
+  int32_t* counters;  // [num_rows], zero between calls
+  int num_chunks;
+  int64_t chunk_len;  // elements, a multiple of 8 (the last chunk may be shorter)
+};
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kPre = 2;  // gathers per thread whose logits are loaded up front
+
+// (m, s) pairs: s is a sum of exp(x - m).
+__device__ __forceinline__ void pair_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * __builtin_amdgcn_exp2f((m - mn) * kLog2e) + s2 * __builtin_amdgcn_exp2f((m2 - mn) * kLog2e);
+  m = mn;
+}
+
 template <int DT, bool VEC>
-__global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(const char* logits, int64_t row_stride_bytes,
-                                                                   int64_t vocab, const int32_t* rows,
-                                                                   const int64_t* tokens, int64_t n,
-                                                                   float* row_lse, float* out) {
-  __shared__ float red[kThreads / 64];
+__global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a) {
+  __shared__ float red_m[kThreads / 64];
+  __shared__ float red_s[kThreads / 64];
+  __shared__ int last_sh;
   __shared__ float lse_sh;
-  constexpr float kLog2e = 1.4426950408889634f;
   constexpr int EPV = Vec<DT>::kElems;
-  const int r = blockIdx.x;
-  const char* row = logits + int64_t(r) * row_stride_bytes;
-  const int64_t nvec = VEC ? vocab / EPV : 0;
+  const int c = blockIdx.x;
+  const int r = blockIdx.y;
+  const int t = threadIdx.x;
+  const char* row = a.logits + int64_t(r) * a.row_stride_bytes;
+  const int64_t c0 = int64_t(c) * a.chunk_len;
+  const int64_t c1 = min(a.vocab, c0 + a.chunk_len);
 
-  float m = -INFINITY;
-  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
-    Vec<DT> x;
-    x.load(row + v * 16);
+  // The gathers that read row r (the first kPre * kThreads of them): their
+  // logits are loaded now, with the chunk, so the row's last chunk only
+  // subtracts the LSE (every chunk loads them; it is not known yet which
+  // chunk finishes last).
+  float gx[kPre];
+  int64_t gi[kPre];
 #pragma unroll
-    for (int k = 0; k < EPV; ++k) m = fmaxf(m, x.x[k]);
+  for (int k = 0; k < kPre; ++k) {
+    const int64_t i = t + int64_t(k) * kThreads;
+    gi[k] = -1;
+    gx[k] = NAN;
+    if (i < a.n && a.rows[i] == r) {
+      const int64_t tok = a.tokens[i];
+      gi[k] = i;
+      if (tok >= 0 && tok < a.vocab) gx[k] = load_logit<DT>(row, tok);
+    }
   }
-  for (int64_t i = nvec * EPV + threadIdx.x; i < vocab; i += kThreads) m = fmaxf(m, load_logit<DT>(row, i));
-  m = block_reduce(m, true, red);
 
-  const float mb = m == -INFINITY ? 0.f : m * kLog2e;
-  float s = 0.f;
-  for (int64_t v = threadIdx.x; v < nvec; v += kThreads) {
-    Vec<DT> x;
-    x.load(row + v * 16);
+  float m = -INFINITY, s = 0.f;
+  int64_t scalar0 = c0;
+  if constexpr (VEC) {
+    // whole vectors of the chunk (chunk starts are multiples of 8 elements)
+    const int64_t v0 = c0 / EPV;
+    const int64_t v1 = c1 / EPV;
+    scalar0 = v1 * EPV;
+#pragma unroll 4
+    for (int64_t v = v0 + t; v < v1; v += kThreads) {
+      Vec<DT> x;
+      x.load(row + v * 16);
+      float vm = x.x[0];
 #pragma unroll
-    for (int k = 0; k < EPV; ++k) s += __builtin_amdgcn_exp2f(__builtin_fmaf(x.x[k], kLog2e, -mb));
+      for (int k = 1; k < EPV; ++k) vm = fmaxf(vm, x.x[k]);
+      const float mn = fmaxf(m, vm);
+      float acc = m == -INFINITY ? 0.f : s * __builtin_amdgcn_exp2f((m - mn) * kLog2e);
+      const float mb = mn == -INFINITY ? 0.f : mn * kLog2e;  // (an all -inf vector adds zeros)
+#pragma unroll
+      for (int k = 0; k < EPV; ++k) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(x.x[k], kLog2e, -mb));
+      m = mn;
+      s = acc;
+    }
   }
-  for (int64_t i = nvec * EPV + threadIdx.x; i < vocab; i += kThreads)
-    s += __builtin_amdgcn_exp2f(__builtin_fmaf(load_logit<DT>(row, i), kLog2e, -mb));
-  s = block_reduce(s, false, red);
+  for (int64_t i = scalar0 + t; i < c1; i += kThreads) {
+    const float x = load_logit<DT>(row, i);
+    pair_merge(m, s, x, 1.f);
+  }
+  // workgroup reduction of (m, s)
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) pair_merge(m, s, __shfl_xor(m, off), __shfl_xor(s, off));
+  if ((t & 63) == 0) {
+    red_m[t >> 6] = m;
+    red_s[t >> 6] = s;
+  }
+  __syncthreads();
+  if (t == 0) {
+    float bm = red_m[0], bs = red_s[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / 64; ++w) pair_merge(bm, bs, red_m[w], red_s[w]);
+    float2* slot = a.stats + int64_t(r) * a.num_chunks + c;
+    const uint64_t bits = uint64_t(__float_as_uint(bm)) | (uint64_t(__float_as_uint(bs)) << 32);
+    __hip_atomic_store(reinterpret_cast<uint64_t*>(slot), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the pair is in memory
+    const int old = __hip_atomic_fetch_add(a.counters + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_sh = old == a.num_chunks - 1;
+  }
+  __syncthreads();
+  if (!last_sh) return;
 
-  if (threadIdx.x == 0) {
-    lse_sh = m + logf(s);
-    if (row_lse) row_lse[r] = lse_sh;
+  // Last chunk of row r: combine the chunk pairs in chunk order (one per lane
+  // of wave 0, then a fixed pairwise tree).
+  if (t < 64) {
+    float cm = -INFINITY, cs = 0.f;
+    for (int k = t; k < a.num_chunks; k += 64) {
+      const uint64_t bits = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.stats + int64_t(r) * a.num_chunks + k),
+                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      pair_merge(cm, cs, __uint_as_float(uint32_t(bits)), __uint_as_float(uint32_t(bits >> 32)));
+    }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) pair_merge(cm, cs, __shfl_xor(cm, off), __shfl_xor(cs, off));
+    if (t == 0) {
+      lse_sh = cm + __builtin_log2f(cs) * kLn2;
+      if (a.row_lse) a.row_lse[r] = lse_sh;
+      __hip_atomic_store(a.counters + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   __syncthreads();
   const float lse = lse_sh;
-  for (int64_t i = threadIdx.x; i < n; i += kThreads) {
-    if (rows[i] != r) continue;
-    const int64_t t = tokens[i];
-    out[i] = (t >= 0 && t < vocab) ? load_logit<DT>(row, t) - lse : NAN;
+#pragma unroll
+  for (int k = 0; k < kPre; ++k)
+    if (gi[k] >= 0) a.out[gi[k]] = gx[k] - lse;
+  for (int64_t i = t + int64_t(kPre) * kThreads; i < a.n; i += kThreads) {
+    if (a.rows[i] != r) continue;
+    const int64_t tok = a.tokens[i];
+    a.out[i] = (tok >= 0 && tok < a.vocab) ? load_logit<DT>(row, tok) - lse : NAN;
   }
 }
 
@@ -119,28 +199,71 @@ __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(const char* l
 
 using namespace atlas;
 
+namespace atlas {
+namespace {
+// Chunks per row: enough (row, chunk) workgroups to cover the device about
+// twice, chunks of at least 1024 logits, at most 256 chunks per row.
+struct GatherGeom {
+  int num_chunks;
+  int64_t chunk_len;
+};
+GatherGeom gather_geom(int64_t num_rows, int64_t vocab) {
+  const int64_t want = (512 + num_rows - 1) / num_rows;
+  const int64_t by_len = (vocab + 1023) / 1024;
+  int64_t chunks = std::max<int64_t>(1, std::min<int64_t>({want, by_len, 256}));
+  int64_t len = (vocab + chunks - 1) / chunks;
+  len = (len + 7) / 8 * 8;
+  chunks = (vocab + len - 1) / len;
+  return GatherGeom{int(chunks), len};
+}
+size_t align256(size_t x) { return (x + 255) / 256 * 256; }
+}  // namespace
+}  // namespace atlas
+
+extern "C" int64_t atlas_gather_logprobs_workspace_bytes(int64_t num_rows, int64_t vocab) {
+  if (num_rows <= 0 || vocab <= 0 || num_rows >= (int64_t(1) << 31)) return -1;
+  const GatherGeom g = gather_geom(num_rows, vocab);
+  return int64_t(align256(size_t(num_rows) * 4) + size_t(num_rows) * g.num_chunks * sizeof(float2));
+}
+
 extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows, int64_t vocab,
                                      int dtype, const int32_t* row_dev, const int64_t* token_dev, int64_t n,
-                                     float* row_lse_dev, float* out_dev, void* stream) {
+                                     float* row_lse_dev, float* out_dev, void* workspace_dev, size_t workspace_bytes,
+                                     void* stream) {
   ATLAS_REQUIRE(logits_dev && num_rows > 0 && vocab > 0, "bad logits arguments");
   ATLAS_REQUIRE(n == 0 || (row_dev && token_dev && out_dev), "gather buffers must not be NULL");
   ATLAS_REQUIRE(num_rows < (int64_t(1) << 31), "too many rows");
   const int es = dtype == ATLAS_DTYPE_F32 ? 4 : 2;
   ATLAS_REQUIRE(dtype == ATLAS_DTYPE_F32 || dtype == ATLAS_DTYPE_F16 || dtype == ATLAS_DTYPE_BF16, "bad dtype");
   ATLAS_REQUIRE(row_stride >= vocab, "row_stride (elements) must cover the vocabulary");
-  const int64_t stride_bytes = row_stride * es;
+  const int64_t need = atlas_gather_logprobs_workspace_bytes(num_rows, vocab);
+  ATLAS_REQUIRE(workspace_dev != nullptr && workspace_bytes >= size_t(need),
+                "workspace of %lld bytes needed (atlas_gather_logprobs_workspace_bytes), got %zu", (long long)need,
+                workspace_bytes);
+  ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0, "workspace must be 16-byte aligned");
+  const GatherGeom g = gather_geom(num_rows, vocab);
+  GatherArgs a{};
+  a.logits = static_cast<const char*>(logits_dev);
+  a.row_stride_bytes = row_stride * es;
+  a.vocab = vocab;
+  a.rows = row_dev;
+  a.tokens = token_dev;
+  a.n = n;
+  a.row_lse = row_lse_dev;
+  a.out = out_dev;
+  a.counters = static_cast<int32_t*>(workspace_dev);
+  a.stats = reinterpret_cast<float2*>(static_cast<char*>(workspace_dev) + align256(size_t(num_rows) * 4));
+  a.num_chunks = g.num_chunks;
+  a.chunk_len = g.chunk_len;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const char* lg = static_cast<const char*>(logits_dev);
-  const dim3 grid(static_cast<unsigned>(num_rows));
-  const bool vec = (reinterpret_cast<uintptr_t>(logits_dev) % 16) == 0 && stride_bytes % 16 == 0;
-#define ATLAS_GATHER_LAUNCH(DT)                                                                              \
-  do {                                                                                                       \
-    if (vec)                                                                                                 \
-      hipLaunchKernelGGL((gather_logprobs_kernel<DT, true>), grid, dim3(kThreads), 0, s, lg, stride_bytes,   \
-                         vocab, row_dev, token_dev, n, row_lse_dev, out_dev);                                \
-    else                                                                                                     \
-      hipLaunchKernelGGL((gather_logprobs_kernel<DT, false>), grid, dim3(kThreads), 0, s, lg, stride_bytes,  \
-                         vocab, row_dev, token_dev, n, row_lse_dev, out_dev);                                \
+  const dim3 grid(static_cast<unsigned>(g.num_chunks), static_cast<unsigned>(num_rows));
+  const bool vec = (reinterpret_cast<uintptr_t>(logits_dev) % 16) == 0 && a.row_stride_bytes % 16 == 0;
+#define ATLAS_GATHER_LAUNCH(DT)                                                                          \
+  do {                                                                                                   \
+    if (vec)                                                                                             \
+      hipLaunchKernelGGL((gather_logprobs_kernel<DT, true>), grid, dim3(kThreads), 0, s, a);             \
+    else                                                                                                 \
+      hipLaunchKernelGGL((gather_logprobs_kernel<DT, false>), grid, dim3(kThreads), 0, s, a);            \
   } while (0)
   if (dtype == ATLAS_DTYPE_F32)
     ATLAS_GATHER_LAUNCH(ATLAS_DTYPE_F32);

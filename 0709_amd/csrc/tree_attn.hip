@@ -119,6 +119,10 @@ struct Mfma<false> {
     return __builtin_amdgcn_fdot2(__builtin_bit_cast(half2v, packed), half2v{(_Float16)1.0f, (_Float16)1.0f}, acc,
                                   false);
   }
+  // Fragments of a matrix of ones (the A operand that turns a P^T MFMA into
+  // row sums).
+  static __device__ __forceinline__ frag ones8() { return __builtin_bit_cast(frag, u16x8(0x3C00)); }
+  static __device__ __forceinline__ v4i16 ones4() { return v4i16(short(0x3C00)); }
 };
 
 template <>
@@ -141,6 +145,8 @@ struct Mfma<true> {
     return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2v, packed),
                                            bf16x2v{(__bf16)1.0f, (__bf16)1.0f}, acc, false);
   }
+  static __device__ __forceinline__ frag ones8() { return __builtin_bit_cast(frag, u16x8(0x3F80)); }
+  static __device__ __forceinline__ v4i16 ones4() { return v4i16(short(0x3F80)); }
 };
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
@@ -584,6 +590,137 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
   }
 }
 
+struct MergeArgs {
+  const atlas_attn_merge_t* merge;
+  const int32_t* qo_indptr;
+  const uint16_t* part_o;
+  const float* part_lse;
+  char* out;
+  int64_t out_stride_token;
+  int64_t out_stride_head;
+  float* lse;
+  int group;
+  int num_qo_heads;
+};
+
+// One wave per packed row, four rows per workgroup.  Lane (g, c) folds the
+// 16-byte chunk c of splits g, g + G, g + 2G, ... (G = 64 / (D / 8) split
+// groups) online, kMergeUnroll splits per round of independent loads (one
+// round covers 32 splits at head_dim 128); the groups then combine through
+// cross-lane reductions.  No LDS and no workgroup barriers, so a row costs
+// the merge item load and one round of partial-state loads.
+constexpr int kMergeThreads = 256;
+constexpr int kMergeRowsPerBlock = kMergeThreads / 64;
+constexpr int kMergeUnroll = 8;
+
+// Eight 16-bit values (fp16 or bf16) to floats.
+template <bool BF16>
+__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
+  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    if constexpr (BF16) {
+      f[2 * i] = __uint_as_float(u[i] << 16);
+      f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
+    } else {
+      const half2v h = __builtin_bit_cast(half2v, u[i]);
+      f[2 * i] = static_cast<float>(h[0]);
+      f[2 * i + 1] = static_cast<float>(h[1]);
+    }
+  }
+}
+
+template <int CH>
+__device__ __forceinline__ float group_max(float v) {
+  if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
+  return wave_max_across_groups(v);
+}
+template <int CH>
+__device__ __forceinline__ float group_sum(float v) {
+  if constexpr (CH <= 8) v += __shfl_xor(v, 8);
+  return wave_sum_across_groups(v);
+}
+
+// Merges the split states of packed row `row` of merge item `mi` and writes
+// the final output row (and LSE), one wave per row.
+template <int D, bool BF16>
+__device__ __forceinline__ void merge_row(const MergeArgs& a, const atlas_attn_merge_t& mi, int row, int lane) {
+  typedef Mfma<BF16> M;
+  constexpr int CH = D / 8;   // 16-byte chunks per row
+  constexpr int G = 64 / CH;  // split groups per wave
+  static_assert(CH == 8 || CH == 16, "head_dim 64 or 128");
+  const int g = lane / CH;
+  const int c = lane % CH;
+  const int ns = mi.num_splits;
+  const int64_t base = int64_t(mi.partial_row) + row;
+
+  float m_t = -INFINITY, wsum = 0.f;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int s0 = g; s0 < ns; s0 += kMergeUnroll * G) {
+    float l[kMergeUnroll];
+    uint4 raw[kMergeUnroll];
+#pragma unroll
+    for (int k = 0; k < kMergeUnroll; ++k) {
+      // Splits past the last re-read split s0 (always present) and are
+      // given weight zero: unconditional loads stay in one batch, where a
+      // guarded load would be followed by a wait of its own.
+      const int sp = s0 + k * G;
+      const int64_t r = base + int64_t(sp < ns ? sp : s0) * mi.num_rows;
+      const float lv = a.part_lse[r];
+      raw[k] = *reinterpret_cast<const uint4*>(a.part_o + r * D + c * 8);
+      l[k] = sp < ns ? lv : -INFINITY;
+    }
+    float m_new = m_t;
+#pragma unroll
+    for (int k = 0; k < kMergeUnroll; ++k) m_new = max2f(m_new, l[k]);
+    // No early exit on an all-masked round: a branch here would hold the O
+    // loads back behind the LSE loads.  With m_new = -inf every weight is 0.
+    const float sc = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_t - m_new);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) acc[i] *= sc;
+    wsum *= sc;
+#pragma unroll
+    for (int k = 0; k < kMergeUnroll; ++k) {
+      const float wk = l[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l[k] - m_new);
+      float v[8];
+      unpack8<BF16>(raw[k], v);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
+      wsum += wk;
+    }
+    m_t = m_new;
+  }
+  const float mx = group_max<CH>(m_t);
+  const float f = (m_t == -INFINITY || mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_t - mx);
+  wsum = group_sum<CH>(wsum * f);
+#pragma unroll
+  for (int i = 0; i < 8; ++i) acc[i] = group_sum<CH>(acc[i] * f);
+  if (g != 0) return;
+  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
+  const int prow_q = mi.row_start + row;
+  const int node = prow_q / a.group;
+  const int head = mi.kv_head * a.group + (prow_q - node * a.group);
+  const int qo_start = a.qo_indptr[mi.req];
+  char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
+  uint32_t pk[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    pk[i] = uint32_t(M::from_float(acc[2 * i] * inv)) | (uint32_t(M::from_float(acc[2 * i + 1] * inv)) << 16);
+  // 8-byte stores: output rows are only required to be 8-byte aligned.
+  *reinterpret_cast<uint2*>(orow + c * 16) = uint2{pk[0], pk[1]};
+  *reinterpret_cast<uint2*>(orow + c * 16 + 8) = uint2{pk[2], pk[3]};
+  if (c == 0 && a.lse != nullptr)
+    a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] = wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
+}
+
+template <int D, bool BF16>
+__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArgs a) {
+  const atlas_attn_merge_t mi = a.merge[blockIdx.x];
+  const int row = blockIdx.y * kMergeRowsPerBlock + (threadIdx.x >> 6);
+  if (row >= mi.num_rows) return;
+  merge_row<D, BF16>(a, mi, row, threadIdx.x & 63);
+}
+
 // ---------------------------------------------------------------------------
 // head_dim 128: KV streamed into LDS with direct global->LDS loads.
 //
@@ -627,6 +764,14 @@ __device__ __forceinline__ void wait_vmcnt() {
 // in-flight tiles alone; the kernel waits for them explicitly (wait_vmcnt).
 __device__ __forceinline__ void dma16(const char* gaddr, uint32_t lds_base) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gaddr), "s"(lds_base) : "memory", "m0");
+}
+
+// The same load with a wave-uniform 64-bit base in SGPRs and a 32-bit per-lane
+// offset: the base's arithmetic runs on the scalar unit, the offsets stay in
+// registers for the whole loop.
+__device__ __forceinline__ void dma16_s(const char* sbase, uint32_t voff, uint32_t lds_base) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(sbase), "s"(lds_base)
+               : "memory", "m0");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
@@ -674,11 +819,16 @@ struct Ring {
   int64_t page_stride, token_stride, v_offset;
   int page_size, page_shift;
   int t_first, nt, last_key;
+  int nt_full;           // leading tiles whose 64 keys all lie before last_key + 1
   int page0, last_page;  // first and last page of the split
   int win;
   int win_cur, win_nxt;
   int li, lane;
   uint32_t lds0;
+  // Lane offsets of the loader's blocks j inside their page (row within the
+  // page plus the swizzled granule), K and V halves: the same on every tile
+  // of a full tile (tiles start at multiples of 64 keys).
+  uint32_t off_k[16 / NL], off_v[16 / NL];
 };
 
 template <int NL>
@@ -727,8 +877,24 @@ __device__ __forceinline__ void ring_issue(Ring<NL>& r, int k) {
       const int rel = (min(t0 + 4 * (NL * j + r.li), r.last_key) >> r.page_shift) - r.page0;
       pid[j] = __builtin_amdgcn_readlane(r.win_cur, rel & 63);
     }
-    issue_tile<NL>(r.head_base, r.page_stride, r.token_stride, r.v_offset, pid, t0, r.last_key, r.page_size, r.li,
-                   r.lane, r.lds0 + (k % kStages128) * kTile128);
+    const uint32_t stage = r.lds0 + (k % kStages128) * kTile128;
+    if (k < r.nt_full) {
+      // A block's four keys share one page (pages hold >= 16 aligned keys),
+      // so its row base is wave-uniform: page base + the tile's start inside
+      // a page of more than 64 keys, on the scalar unit.
+      const int64_t tile_in_page = int64_t(t0 & (r.page_size - 1) & ~(kTileKeys - 1)) * r.token_stride;
+#pragma unroll
+      for (int j = 0; j < 16 / NL; ++j) {
+        const int blk = NL * j + r.li;
+        const char* kbase = r.head_base + int64_t(pid[j]) * r.page_stride + tile_in_page;
+        dma16_s(kbase, r.off_k[j], stage + blk * 1024);
+        dma16_s(kbase + r.v_offset, r.off_v[j], stage + kHalf128 + blk * 1024);
+      }
+    } else {
+      // The split's last, partial tile: keys past the last one re-read it.
+      issue_tile<NL>(r.head_base, r.page_stride, r.token_stride, r.v_offset, pid, t0, r.last_key, r.page_size,
+                     r.li, r.lane, stage);
+    }
   }
 }
 
@@ -820,7 +986,9 @@ struct RowState {
   typename Mfma<BF16>::frag qf[RT][4];
   f32x4 o[RT][8];
   float m_run[RT];
-  float l_run[RT];
+  // Row sums of P, accumulated by an MFMA of a ones matrix with P^T beside
+  // the P.V MFMAs: every element holds the lane's row sum over all keys.
+  f32x4 l_acc[RT];
   uint64_t tbits[RT];
   int climit[RT];
   int node_of[RT];
@@ -891,13 +1059,17 @@ __device__ __forceinline__ void d128_rowmax(RowState<BF16, RT>& st, f32x4 (&s)[R
     for (int j = 0; j < NKT; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) sv[4 * j + i] = s[rt][j][i];
-    float mx = wave_max_across_groups(lane_max<4 * NKT>(sv)) * scale_log2;
-    const bool grow = mx > st.m_run[rt] + kRescaleLog2;
-    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+    // The lane's own maximum decides whether any row can have grown; only
+    // then are the four lanes of each row reduced (a row's maximum grows
+    // past the threshold only if one of its lanes' maxima does).
+    const float lane_mx = lane_max<4 * NKT>(sv) * scale_log2;
+    if (__builtin_amdgcn_ballot_w64(lane_mx > st.m_run[rt] + kRescaleLog2) != 0) {
+      const float mx = wave_max_across_groups(lane_mx);
+      const bool grow = mx > st.m_run[rt] + kRescaleLog2;
       const float m_new = grow ? mx : st.m_run[rt];
       const float alpha = (grow && st.m_run[rt] != -INFINITY) ? __builtin_amdgcn_exp2f(st.m_run[rt] - m_new)
                                                               : (grow ? 0.f : 1.f);
-      st.l_run[rt] *= alpha;
+      st.l_acc[rt] *= alpha;
 #pragma unroll
       for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] *= alpha;
       st.m_run[rt] = m_new;
@@ -920,7 +1092,6 @@ __device__ __forceinline__ void d128_exp(RowState<BF16, RT>& st, const f32x4 (&s
       const float p3 = __builtin_amdgcn_exp2f(__builtin_fmaf(s[rt][j][3], scale_log2, neg_m));
       pk[rt][j][0] = M::pack2(p0, p1);
       pk[rt][j][1] = M::pack2(p2, p3);
-      st.l_run[rt] = M::sum2(pk[rt][j][1], M::sum2(pk[rt][j][0], st.l_run[rt]));
     }
   }
 }
@@ -949,6 +1120,9 @@ __device__ __forceinline__ void d128_pv(RowState<BF16, RT>& st, const uint32_t (
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run16(av, pb[rt], st.o[rt][dt]);
     }
+    const v4i16 ones = M::ones4();
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) st.l_acc[rt] = M::run16(ones, pb[rt], st.l_acc[rt]);
   } else {
     frag pf[RT][NKT / 2];
 #pragma unroll
@@ -972,6 +1146,9 @@ __device__ __forceinline__ void d128_pv(RowState<BF16, RT>& st, const uint32_t (
 #pragma unroll
         for (int rt = 0; rt < RT; ++rt) st.o[rt][dt] = M::run(av, pf[rt][h], st.o[rt][dt]);
       }
+      const frag ones = M::ones8();
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st.l_acc[rt] = M::run(ones, pf[rt][h], st.l_acc[rt]);
     }
   }
 }
@@ -1019,7 +1196,7 @@ __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const Att
     st.node_of[rt] = prow / G;
     st.head_of[rt] = w.kv_head * G + (prow - st.node_of[rt] * G);
     st.m_run[rt] = -INFINITY;
-    st.l_run[rt] = 0.f;
+    st.l_acc[rt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int dt = 0; dt < 8; ++dt) st.o[rt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
     st.tbits[rt] = 0ull;
@@ -1188,7 +1365,7 @@ __device__ __forceinline__ void d128_store_rows(RowState<BF16, RT>& st, const At
   const int grp = lane >> 4;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) {
-    const float l_tot = wave_sum_across_groups(st.l_run[rt]);
+    const float l_tot = st.l_acc[rt][0];
     const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
     const float lse2 = l_tot > 0.f ? st.m_run[rt] + __builtin_log2f(l_tot) : -INFINITY;
     d128_store<BF16, 8>(a, w, c, st.node_of[rt], st.head_of[rt], st.lrow[rt], st.row_ok[rt], st.o[rt], 0, inv, lse2,
@@ -1209,7 +1386,7 @@ __device__ __forceinline__ void d128_part_put(const RowState<BF16, 1>& st, char*
 #pragma unroll
   for (int dt = 0; dt < 8; ++dt) *reinterpret_cast<f32x4*>(base + (dt * 64 + lane) * 16) = st.o[0][dt];
   reinterpret_cast<float*>(base + 8 * 64 * 16)[lane] = st.m_run[0];
-  reinterpret_cast<float*>(base + 8 * 64 * 16)[64 + lane] = wave_sum_across_groups(st.l_run[0]);
+  reinterpret_cast<float*>(base + 8 * 64 * 16)[64 + lane] = st.l_acc[0][0];
 }
 
 template <bool BF16, int S>
@@ -1351,6 +1528,17 @@ __device__ __forceinline__ void ring_init(Ring<NL>& r, const AttnArgs& a, const 
   r.li = li;
   r.lane = lane;
   r.lds0 = lds0;
+  r.nt_full = c.nt - ((c.t_first + c.nt * kTileKeys - 1 > last_key) ? 1 : 0);
+  static_assert(NL % 4 == 0, "block keys & 15 must not depend on the block's round j");
+  const int c16p = lane & 15;
+  const int kmask = min(a.page_size, kTileKeys) - 1;
+#pragma unroll
+  for (int j = 0; j < 16 / NL; ++j) {
+    const int key = 4 * (NL * j + li) + (lane >> 4);
+    const uint32_t row = uint32_t(key & kmask) * uint32_t(a.token_stride);
+    r.off_k[j] = row + uint32_t((c16p ^ (key & 15)) << 4);
+    r.off_v[j] = row + uint32_t((c16p ^ ((key & 7) << 1)) << 4);
+  }
 }
 
 // Fused append: the request's newest qo_len tokens occupy its last qo_len key
@@ -1444,130 +1632,6 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   }
 }
 
-struct MergeArgs {
-  const atlas_attn_merge_t* merge;
-  const int32_t* qo_indptr;
-  const uint16_t* part_o;
-  const float* part_lse;
-  char* out;
-  int64_t out_stride_token;
-  int64_t out_stride_head;
-  float* lse;
-  int group;
-  int num_qo_heads;
-};
-
-// One wave per packed row, four rows per workgroup.  Lane (g, c) folds the
-// 16-byte chunk c of splits g, g + G, g + 2G, ... (G = 64 / (D / 8) split
-// groups) online, kMergeUnroll splits per round of independent loads (one
-// round covers 32 splits at head_dim 128); the groups then combine through
-// cross-lane reductions.  No LDS and no workgroup barriers, so a row costs
-// the merge item load and one round of partial-state loads.
-constexpr int kMergeThreads = 256;
-constexpr int kMergeRowsPerBlock = kMergeThreads / 64;
-constexpr int kMergeUnroll = 8;
-
-// Eight 16-bit values (fp16 or bf16) to floats.
-template <bool BF16>
-__device__ __forceinline__ void unpack8(uint4 v, float (&f)[8]) {
-  const uint32_t u[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    if constexpr (BF16) {
-      f[2 * i] = __uint_as_float(u[i] << 16);
-      f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-    } else {
-      const half2v h = __builtin_bit_cast(half2v, u[i]);
-      f[2 * i] = static_cast<float>(h[0]);
-      f[2 * i + 1] = static_cast<float>(h[1]);
-    }
-  }
-}
-
-template <int CH>
-__device__ __forceinline__ float group_max(float v) {
-  if constexpr (CH <= 8) v = fmaxf(v, __shfl_xor(v, 8));
-  return wave_max_across_groups(v);
-}
-template <int CH>
-__device__ __forceinline__ float group_sum(float v) {
-  if constexpr (CH <= 8) v += __shfl_xor(v, 8);
-  return wave_sum_across_groups(v);
-}
-
-template <int D, bool BF16>
-__global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArgs a) {
-  typedef Mfma<BF16> M;
-  constexpr int CH = D / 8;   // 16-byte chunks per row
-  constexpr int G = 64 / CH;  // split groups per wave
-  static_assert(CH == 8 || CH == 16, "head_dim 64 or 128");
-  const atlas_attn_merge_t mi = a.merge[blockIdx.x];
-  const int row = blockIdx.y * kMergeRowsPerBlock + (threadIdx.x >> 6);
-  if (row >= mi.num_rows) return;
-  const int lane = threadIdx.x & 63;
-  const int g = lane / CH;
-  const int c = lane % CH;
-  const int ns = mi.num_splits;
-  const int64_t base = int64_t(mi.partial_row) + row;
-
-  float m_t = -INFINITY, wsum = 0.f;
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  for (int s0 = g; s0 < ns; s0 += kMergeUnroll * G) {
-    float l[kMergeUnroll];
-    uint4 raw[kMergeUnroll];
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) {
-      // Splits past the last re-read split s0 (always present) and are
-      // given weight zero: unconditional loads stay in one batch, where a
-      // guarded load would be followed by a wait of its own.
-      const int sp = s0 + k * G;
-      const int64_t r = base + int64_t(sp < ns ? sp : s0) * mi.num_rows;
-      const float lv = a.part_lse[r];
-      raw[k] = *reinterpret_cast<const uint4*>(a.part_o + r * D + c * 8);
-      l[k] = sp < ns ? lv : -INFINITY;
-    }
-    float m_new = m_t;
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) m_new = max2f(m_new, l[k]);
-    // No early exit on an all-masked round: a branch here would hold the O
-    // loads back behind the LSE loads.  With m_new = -inf every weight is 0.
-    const float sc = m_t == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_t - m_new);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[i] *= sc;
-    wsum *= sc;
-#pragma unroll
-    for (int k = 0; k < kMergeUnroll; ++k) {
-      const float wk = l[k] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(l[k] - m_new);
-      float v[8];
-      unpack8<BF16>(raw[k], v);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) acc[i] += wk * v[i];
-      wsum += wk;
-    }
-    m_t = m_new;
-  }
-  const float mx = group_max<CH>(m_t);
-  const float f = (m_t == -INFINITY || mx == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_t - mx);
-  wsum = group_sum<CH>(wsum * f);
-#pragma unroll
-  for (int i = 0; i < 8; ++i) acc[i] = group_sum<CH>(acc[i] * f);
-  if (g != 0) return;
-  const float inv = wsum > 0.f ? 1.f / wsum : 0.f;
-  const int prow_q = mi.row_start + row;
-  const int node = prow_q / a.group;
-  const int head = mi.kv_head * a.group + (prow_q - node * a.group);
-  const int qo_start = a.qo_indptr[mi.req];
-  char* orow = a.out + ((int64_t(qo_start + node) * a.out_stride_token + int64_t(head) * a.out_stride_head) * 2);
-  uint32_t pk[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-    pk[i] = uint32_t(M::from_float(acc[2 * i] * inv)) | (uint32_t(M::from_float(acc[2 * i + 1] * inv)) << 16);
-  // 8-byte stores: output rows are only required to be 8-byte aligned.
-  *reinterpret_cast<uint2*>(orow + c * 16) = uint2{pk[0], pk[1]};
-  *reinterpret_cast<uint2*>(orow + c * 16 + 8) = uint2{pk[2], pk[3]};
-  if (c == 0 && a.lse != nullptr)
-    a.lse[int64_t(qo_start + node) * a.num_qo_heads + head] = wsum > 0.f ? (mx + __builtin_log2f(wsum)) * kLn2 : -INFINITY;
-}
 
 // Work-shape choice: the fewest (compute waves x row tiles) slots that cover
 // the row tiles, preferring more waves (fewer tiles per wave).
@@ -1697,8 +1761,7 @@ static int verify_attn_impl(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev,
-    int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream, const void* append_k, const void* append_v, int64_t append_stride_token,
@@ -1726,6 +1789,10 @@ static int verify_attn_impl(
                 "q strides must be multiples of 8 elements and out strides multiples of 4");
   ATLAS_REQUIRE(page_stride % 16 == 0 && token_stride % 16 == 0 && kv_v_offset % 16 == 0,
                 "kv strides must be multiples of 16 bytes");
+  // (the head_dim-128 kernel keeps a row's offset inside its page, up to 63
+  // token rows plus 256 bytes, in 32 bits)
+  ATLAS_REQUIRE(token_stride > 0 && token_stride <= (int64_t(1) << 25), "token_stride %lld out of range",
+                (long long)token_stride);
   if (num_work == 0) return ATLAS_OK;
   ATLAS_REQUIRE(work_dev != nullptr, "work list must not be NULL");
   const int row_tiles = (max_rows_per_item + 15) / 16;
@@ -1801,8 +1868,7 @@ extern "C" int atlas_tree_verify_attn(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev,
-    int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream) {
@@ -1820,8 +1886,7 @@ extern "C" int atlas_tree_verify_attn_append(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev,
-    int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     const void* append_k, const void* append_v, int64_t append_stride_token, int64_t append_stride_head,

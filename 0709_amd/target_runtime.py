@@ -89,12 +89,30 @@ def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Seq
     tok = idx[:n]
     row = idx[n:].to(torch.int32)
     lib = _lib.load()
+    need = int(lib.atlas_gather_logprobs_workspace_bytes(int(lg.shape[0]), int(lg.shape[1])))
+    if need < 0:
+        raise ValueError(f"bad logits shape {tuple(lg.shape)}")
+    ws = _scoring_workspace(device, need)
     rc = lib.atlas_gather_logprobs(
         _lib.ptr(lg), lg.stride(0), int(lg.shape[0]), int(lg.shape[1]), _lib.dtype_code(lg.dtype),
-        _lib.ptr(row), _lib.ptr(tok), n, None, _lib.ptr(out), _lib.stream_of(device),
+        _lib.ptr(row), _lib.ptr(tok), n, None, _lib.ptr(out), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(device),
     )
     _lib.check(rc, "atlas_gather_logprobs")
     return out
+
+
+_SCORING_WS: dict = {}
+
+
+def _scoring_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The scoring launch's chunk statistics and row counters: zero-filled once
+    per device (and when it grows); every launch leaves its counters zero."""
+    key = (device.type, device.index)
+    ws = _SCORING_WS.get(key)
+    if ws is None or int(ws.numel()) < nbytes:
+        ws = torch.zeros(max(nbytes, 1 << 16), dtype=torch.uint8, device=device)
+        _SCORING_WS[key] = ws
+    return ws
 
 
 def rotate_half(hidden_states: torch.Tensor) -> torch.Tensor:

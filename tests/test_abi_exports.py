@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 3
+    assert lib.atlas_abi_version() == 4
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -62,3 +62,16 @@ def test_argument_errors_are_reported_without_device_work():
         assert "probe" in str(exc)
     else:
         raise AssertionError("check() did not raise")
+
+
+def test_gather_logprobs_workspace_contract_without_device_work():
+    """The scoring call sizes its workspace from (rows, vocab) and refuses a
+    smaller one before any launch."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    need = lib.atlas_gather_logprobs_workspace_bytes(34, 128256)
+    assert need > 34 * 8 and lib.atlas_gather_logprobs_workspace_bytes(0, 10) < 0
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the call refuses first
+    rc = lib.atlas_gather_logprobs(fake, 128256, 34, 128256, lib_mod.DTYPE_F16, fake, fake, 4, None, fake,
+                                   fake, need - 1, None)
+    assert rc == lib_mod.ATLAS_EINVAL and b"workspace" in lib.atlas_last_error()

@@ -584,3 +584,4 @@ def test_fused_rope_batched_requests_and_refusals(dev):
     with pytest.raises(ValueError):
         w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev),
               rope_cos_sin=(cos[:-1].to(dev), sin[:-1].to(dev)))
+
