@@ -112,7 +112,8 @@ _SIGNATURES: dict[str, list] = {
     "atlas_paged_metadata": [_vp, _vp, _vp, ctypes.c_int, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _vp],
     "atlas_gather_logprobs_workspace_bytes": [_c_i64, _c_i64],
     "atlas_gather_logprobs": [
-        _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp, ctypes.c_size_t, _vp,
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp,
+        ctypes.c_size_t, _vp,
     ],
     "atlas_frontier_workspace_bytes": [_c_i64, _c_i64, ctypes.c_int],
     "atlas_frontier_topk": [

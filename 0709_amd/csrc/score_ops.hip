@@ -53,28 +53,34 @@ struct Vec {
 // and the sum of exp(x - m), kept online per thread (16-byte loads when the
 // rows are 16-byte aligned), then reduced over the workgroup.  It writes the
 // pair through to memory (agent scope: read by whichever XCD finishes the
-// row) and counts itself into the row's counter; the row's last chunk
-// combines the pairs in chunk order -- a fixed order, whichever chunk arrives
-// last, so the LSE is the same on every run -- writes the row LSE and every
-// gather that reads row r, and clears the counter for the next call.
+// row) into its slot of the row, then reads the row's slots: the workgroup
+// that finds all of them filled -- at least the last one to store, possibly
+// several, which then write the same values -- combines the pairs in chunk
+// order (a fixed order, so the LSE is the same on every run), writes the row
+// LSE and every gather of row r, and empties the slots for the next call.  A
+// slot is (max bits, ~sum bits): a non-negative sum has its sign bit clear,
+// so a filled slot has bit 63 set and an empty (zero) slot has not.
 struct GatherArgs {
   const char* logits;
   int64_t row_stride_bytes;
+  const char* logits2;          // rows num_rows1 .. come from here (or null)
+  int64_t row_stride2_bytes;
+  int64_t num_rows1;
   int64_t vocab;
   const int32_t* rows;
   const int64_t* tokens;
   int64_t n;
   float* row_lse;
   float* out;
-  float2* stats;    // [num_rows, num_chunks]
-  int32_t* counters;  // [num_rows], zero between calls
+  uint64_t* slots;  // [num_rows, num_chunks], zero between calls
   int num_chunks;
   int64_t chunk_len;  // elements, a multiple of 8 (the last chunk may be shorter)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
-constexpr int kPre = 2;  // gathers per thread whose logits are loaded up front
+constexpr int kPre = 2;  // gathers per thread whose logits are loaded ahead of the combine
+constexpr uint64_t kFilled = 1ull << 63;
 
 // (m, s) pairs: s is a sum of exp(x - m).
 __device__ __forceinline__ void pair_merge(float& m, float& s, float m2, float s2) {
@@ -88,32 +94,26 @@ template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a) {
   __shared__ float red_m[kThreads / 64];
   __shared__ float red_s[kThreads / 64];
-  __shared__ int last_sh;
+  __shared__ int full_sh;
   __shared__ float lse_sh;
   constexpr int EPV = Vec<DT>::kElems;
   const int c = blockIdx.x;
   const int r = blockIdx.y;
   const int t = threadIdx.x;
-  const char* row = a.logits + int64_t(r) * a.row_stride_bytes;
+  const char* row = r < a.num_rows1 ? a.logits + int64_t(r) * a.row_stride_bytes
+                                    : a.logits2 + (int64_t(r) - a.num_rows1) * a.row_stride2_bytes;
   const int64_t c0 = int64_t(c) * a.chunk_len;
   const int64_t c1 = min(a.vocab, c0 + a.chunk_len);
 
-  // The gathers that read row r (the first kPre * kThreads of them): their
-  // logits are loaded now, with the chunk, so the row's last chunk only
-  // subtracts the LSE (every chunk loads them; it is not known yet which
-  // chunk finishes last).
-  float gx[kPre];
-  int64_t gi[kPre];
+  // Row and token of the first kPre * kThreads gathers, requested before the
+  // chunk (no branch on them: a branch would wait for them first).
+  int32_t grow[kPre];
+  int64_t gtok[kPre];
 #pragma unroll
   for (int k = 0; k < kPre; ++k) {
-    const int64_t i = t + int64_t(k) * kThreads;
-    gi[k] = -1;
-    gx[k] = NAN;
-    if (i < a.n && a.rows[i] == r) {
-      const int64_t tok = a.tokens[i];
-      gi[k] = i;
-      if (tok >= 0 && tok < a.vocab) gx[k] = load_logit<DT>(row, tok);
-    }
+    const int64_t i = min(t + int64_t(k) * kThreads, max(a.n - 1, int64_t(0)));
+    grow[k] = a.n > 0 ? a.rows[i] : -1;
+    gtok[k] = a.n > 0 ? a.tokens[i] : 0;
   }
 
   float m = -INFINITY, s = 0.f;
@@ -143,6 +143,16 @@ __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a)
     const float x = load_logit<DT>(row, i);
     pair_merge(m, s, x, 1.f);
   }
+  // The gathered logits go out now and land while the pair is published.
+  float gx[kPre];
+  bool gmine[kPre];
+#pragma unroll
+  for (int k = 0; k < kPre; ++k) {
+    gmine[k] = t + int64_t(k) * kThreads < a.n && grow[k] == r;
+    const bool ok = gtok[k] >= 0 && gtok[k] < a.vocab;
+    gx[k] = load_logit<DT>(row, ok ? gtok[k] : 0);
+    if (!ok) gx[k] = NAN;
+  }
   // workgroup reduction of (m, s)
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) pair_merge(m, s, __shfl_xor(m, off), __shfl_xor(s, off));
@@ -151,42 +161,44 @@ __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a)
     red_s[t >> 6] = s;
   }
   __syncthreads();
+  uint64_t* rs = a.slots + int64_t(r) * a.num_chunks;
   if (t == 0) {
     float bm = red_m[0], bs = red_s[0];
 #pragma unroll
     for (int w = 1; w < kThreads / 64; ++w) pair_merge(bm, bs, red_m[w], red_s[w]);
-    float2* slot = a.stats + int64_t(r) * a.num_chunks + c;
-    const uint64_t bits = uint64_t(__float_as_uint(bm)) | (uint64_t(__float_as_uint(bs)) << 32);
-    __hip_atomic_store(reinterpret_cast<uint64_t*>(slot), bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the pair is in memory
-    const int old = __hip_atomic_fetch_add(a.counters + r, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last_sh = old == a.num_chunks - 1;
+    const uint64_t slot = uint64_t(__float_as_uint(bm)) | (uint64_t(~__float_as_uint(bs)) << 32);
+    __hip_atomic_store(rs + c, slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the slot is in memory
   }
   __syncthreads();
-  if (!last_sh) return;
 
-  // Last chunk of row r: combine the chunk pairs in chunk order (one per lane
-  // of wave 0, then a fixed pairwise tree).
+  // Read the row's slots; combine in chunk order (one per lane of wave 0,
+  // then a fixed pairwise tree) when all are filled.
   if (t < 64) {
     float cm = -INFINITY, cs = 0.f;
+    bool all = true;
     for (int k = t; k < a.num_chunks; k += 64) {
-      const uint64_t bits = __hip_atomic_load(reinterpret_cast<uint64_t*>(a.stats + int64_t(r) * a.num_chunks + k),
-                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      pair_merge(cm, cs, __uint_as_float(uint32_t(bits)), __uint_as_float(uint32_t(bits >> 32)));
+      const uint64_t v = __hip_atomic_load(rs + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      all = all && (v & kFilled) != 0;
+      pair_merge(cm, cs, __uint_as_float(uint32_t(v)), __uint_as_float(~uint32_t(v >> 32)));
     }
+    const bool full = __builtin_amdgcn_ballot_w64(!all) == 0;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) pair_merge(cm, cs, __shfl_xor(cm, off), __shfl_xor(cs, off));
     if (t == 0) {
+      full_sh = full;
       lse_sh = cm + __builtin_log2f(cs) * kLn2;
-      if (a.row_lse) a.row_lse[r] = lse_sh;
-      __hip_atomic_store(a.counters + r, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
   __syncthreads();
+  if (!full_sh) return;
   const float lse = lse_sh;
+  if (t == 0 && a.row_lse) a.row_lse[r] = lse;
+  for (int k = t; k < a.num_chunks; k += kThreads)
+    __hip_atomic_store(rs + k, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
   for (int k = 0; k < kPre; ++k)
-    if (gi[k] >= 0) a.out[gi[k]] = gx[k] - lse;
+    if (gmine[k]) a.out[t + int64_t(k) * kThreads] = gx[k] - lse;
   for (int64_t i = t + int64_t(kPre) * kThreads; i < a.n; i += kThreads) {
     if (a.rows[i] != r) continue;
     const int64_t tok = a.tokens[i];
@@ -216,48 +228,55 @@ GatherGeom gather_geom(int64_t num_rows, int64_t vocab) {
   chunks = (vocab + len - 1) / len;
   return GatherGeom{int(chunks), len};
 }
-size_t align256(size_t x) { return (x + 255) / 256 * 256; }
 }  // namespace
 }  // namespace atlas
 
 extern "C" int64_t atlas_gather_logprobs_workspace_bytes(int64_t num_rows, int64_t vocab) {
   if (num_rows <= 0 || vocab <= 0 || num_rows >= (int64_t(1) << 31)) return -1;
   const GatherGeom g = gather_geom(num_rows, vocab);
-  return int64_t(align256(size_t(num_rows) * 4) + size_t(num_rows) * g.num_chunks * sizeof(float2));
+  return int64_t(size_t(num_rows) * g.num_chunks * sizeof(uint64_t));
 }
 
-extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows, int64_t vocab,
+extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows,
+                                     const void* logits2_dev, int64_t row_stride2, int64_t num_rows2, int64_t vocab,
                                      int dtype, const int32_t* row_dev, const int64_t* token_dev, int64_t n,
                                      float* row_lse_dev, float* out_dev, void* workspace_dev, size_t workspace_bytes,
                                      void* stream) {
   ATLAS_REQUIRE(logits_dev && num_rows > 0 && vocab > 0, "bad logits arguments");
+  ATLAS_REQUIRE(num_rows2 >= 0 && (num_rows2 == 0 || logits2_dev != nullptr), "bad second logits arguments");
   ATLAS_REQUIRE(n == 0 || (row_dev && token_dev && out_dev), "gather buffers must not be NULL");
-  ATLAS_REQUIRE(num_rows < (int64_t(1) << 31), "too many rows");
+  const int64_t total_rows = num_rows + num_rows2;
+  ATLAS_REQUIRE(total_rows < (int64_t(1) << 31), "too many rows");
   const int es = dtype == ATLAS_DTYPE_F32 ? 4 : 2;
   ATLAS_REQUIRE(dtype == ATLAS_DTYPE_F32 || dtype == ATLAS_DTYPE_F16 || dtype == ATLAS_DTYPE_BF16, "bad dtype");
-  ATLAS_REQUIRE(row_stride >= vocab, "row_stride (elements) must cover the vocabulary");
-  const int64_t need = atlas_gather_logprobs_workspace_bytes(num_rows, vocab);
+  ATLAS_REQUIRE(row_stride >= vocab && (num_rows2 == 0 || row_stride2 >= vocab),
+                "row strides (elements) must cover the vocabulary");
+  const int64_t need = atlas_gather_logprobs_workspace_bytes(total_rows, vocab);
   ATLAS_REQUIRE(workspace_dev != nullptr && workspace_bytes >= size_t(need),
                 "workspace of %lld bytes needed (atlas_gather_logprobs_workspace_bytes), got %zu", (long long)need,
                 workspace_bytes);
   ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0, "workspace must be 16-byte aligned");
-  const GatherGeom g = gather_geom(num_rows, vocab);
+  const GatherGeom g = gather_geom(total_rows, vocab);
   GatherArgs a{};
   a.logits = static_cast<const char*>(logits_dev);
   a.row_stride_bytes = row_stride * es;
+  a.logits2 = static_cast<const char*>(logits2_dev);
+  a.row_stride2_bytes = row_stride2 * es;
+  a.num_rows1 = num_rows;
   a.vocab = vocab;
   a.rows = row_dev;
   a.tokens = token_dev;
   a.n = n;
   a.row_lse = row_lse_dev;
   a.out = out_dev;
-  a.counters = static_cast<int32_t*>(workspace_dev);
-  a.stats = reinterpret_cast<float2*>(static_cast<char*>(workspace_dev) + align256(size_t(num_rows) * 4));
+  a.slots = static_cast<uint64_t*>(workspace_dev);
   a.num_chunks = g.num_chunks;
   a.chunk_len = g.chunk_len;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const dim3 grid(static_cast<unsigned>(g.num_chunks), static_cast<unsigned>(num_rows));
-  const bool vec = (reinterpret_cast<uintptr_t>(logits_dev) % 16) == 0 && a.row_stride_bytes % 16 == 0;
+  const dim3 grid(static_cast<unsigned>(g.num_chunks), static_cast<unsigned>(total_rows));
+  const bool vec = (reinterpret_cast<uintptr_t>(logits_dev) % 16) == 0 && a.row_stride_bytes % 16 == 0 &&
+                   (num_rows2 == 0 ||
+                    ((reinterpret_cast<uintptr_t>(logits2_dev) % 16) == 0 && a.row_stride2_bytes % 16 == 0));
 #define ATLAS_GATHER_LAUNCH(DT)                                                                          \
   do {                                                                                                   \
     if (vec)                                                                                             \

@@ -53,6 +53,15 @@ class FullVerifyState:
     paged_prefix_kv: list[torch.Tensor]
 
 
+def tensor_version(t: torch.Tensor) -> int | None:
+    """The tensor's in-place version counter, or None for an inference tensor
+    (created under torch.inference_mode, which keeps no counter)."""
+    try:
+        return int(t._version)
+    except RuntimeError:
+        return None
+
+
 def ceil_div(value: int, divisor: int) -> int:
     return (int(value) + int(divisor) - 1) // int(divisor)
 
@@ -212,8 +221,9 @@ def _tree_spec(
     flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.
-        # The version counter lets plan() notice an in-place change of the mask.
-        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask, flat_mask._version)
+        # The version counter lets plan() notice an in-place change of the mask
+        # (inference tensors have none: None).
+        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask, tensor_version(flat_mask))
     return TreeSpec(
         flat_token_ids=flat_token_ids,
         parent_indices=list(parent_indices),

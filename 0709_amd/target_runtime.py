@@ -32,6 +32,7 @@ import numpy as np
 import torch
 
 from . import _lib, kv_ops
+from .decode_attention import make_decode_wrapper, plan_decode_wrapper
 from .flashinfer_full_verify import (
     FullVerifyState,
     build_deduplicated_tree_spec_from_paths,
@@ -72,13 +73,22 @@ def verify_payload_from_mapping(item: dict) -> VerifyRoutePayload:
     )
 
 
-def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Sequence[int]) -> torch.Tensor:
+def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Sequence[int],
+                          extra_logits: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 ``log_softmax(logits[row])[token]`` for each (row, token) pair,
-    computed on the device in one launch.  ``logits``: [rows, vocab] or [vocab]."""
+    computed on the device in one launch.  ``logits``: [rows, vocab] or [vocab].
+    With ``extra_logits`` ([rows2, vocab] or [vocab], same dtype and vocab),
+    row indices ``rows .. rows + rows2 - 1`` name its rows, in the same launch."""
     device = _lib.require_device(logits, what="route scoring")
     lg = logits.reshape(1, -1) if logits.ndim == 1 else logits
     if lg.ndim != 2 or lg.stride(-1) != 1:
         raise ValueError("logits must be [rows, vocab] with contiguous rows")
+    lg2 = None
+    if extra_logits is not None:
+        _lib.require_device(logits, extra_logits, what="route scoring")
+        lg2 = extra_logits.reshape(1, -1) if extra_logits.ndim == 1 else extra_logits
+        if lg2.ndim != 2 or lg2.stride(-1) != 1 or int(lg2.shape[1]) != int(lg.shape[1]) or lg2.dtype != lg.dtype:
+            raise ValueError("extra_logits must be [rows, vocab] rows of the same vocabulary and dtype")
     n = len(rows)
     out = torch.empty(n, dtype=torch.float32, device=device)
     if n == 0:
@@ -89,13 +99,15 @@ def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Seq
     tok = idx[:n]
     row = idx[n:].to(torch.int32)
     lib = _lib.load()
-    need = int(lib.atlas_gather_logprobs_workspace_bytes(int(lg.shape[0]), int(lg.shape[1])))
+    rows2 = 0 if lg2 is None else int(lg2.shape[0])
+    need = int(lib.atlas_gather_logprobs_workspace_bytes(int(lg.shape[0]) + rows2, int(lg.shape[1])))
     if need < 0:
         raise ValueError(f"bad logits shape {tuple(lg.shape)}")
     ws = _scoring_workspace(device, need)
     rc = lib.atlas_gather_logprobs(
-        _lib.ptr(lg), lg.stride(0), int(lg.shape[0]), int(lg.shape[1]), _lib.dtype_code(lg.dtype),
-        _lib.ptr(row), _lib.ptr(tok), n, None, _lib.ptr(out), _lib.ptr(ws), int(ws.numel()), _lib.stream_of(device),
+        _lib.ptr(lg), lg.stride(0), int(lg.shape[0]), _lib.ptr(lg2), lg2.stride(0) if lg2 is not None else 0, rows2,
+        int(lg.shape[1]), _lib.dtype_code(lg.dtype), _lib.ptr(row), _lib.ptr(tok), n, None, _lib.ptr(out),
+        _lib.ptr(ws), int(ws.numel()), _lib.stream_of(device),
     )
     _lib.check(rc, "atlas_gather_logprobs")
     return out
@@ -105,8 +117,8 @@ _SCORING_WS: dict = {}
 
 
 def _scoring_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
-    """The scoring launch's chunk statistics and row counters: zero-filled once
-    per device (and when it grows); every launch leaves its counters zero."""
+    """The scoring launch's chunk statistics: zero-filled once per device (and
+    when it grows); every launch leaves them zero."""
     key = (device.type, device.index)
     ws = _SCORING_WS.get(key)
     if ws is None or int(ws.numel()) < nbytes:
@@ -138,10 +150,20 @@ def rope_cos_sin(model, positions: torch.Tensor, head_dim: int, dtype: torch.dty
 
 
 @torch.inference_mode()
-def run_full_verify(*, model, wrapper, state: FullVerifyState, prefix_len: int, page_size: int) -> torch.Tensor:
+def run_full_verify(*, model, wrapper, state: FullVerifyState, prefix_len: int, page_size: int,
+                    fused: bool | None = None) -> torch.Tensor:
     """Masked tree forward of a Llama-layout model: per layer RMSNorm, QKV,
     RoPE at prefix_len + depth, ``write_suffix_kv`` then tree attention
-    (append before attention, as ``flashinfer_full_verify.py:1207-1223``)."""
+    (append before attention, as ``flashinfer_full_verify.py:1207-1223``).
+
+    When the plan allows it (head_dim 128, power-of-two pages of >= 16
+    tokens, one row block per (request, KV head): ``current_plan.fused_append``)
+    the rotary embedding, the append and the attention are one launch per
+    layer (``wrapper.run(q, kv, append_key_states=k, append_value_states=v,
+    rope_cos_sin=(cos, sin))`` on the projections before RoPE), which writes
+    the cache and returns the output of the separate ops bit for bit.
+    ``fused=False`` runs the separate ops; ``fused=True`` requires the fused
+    launch."""
     cfg = model.config
     base = model.model
     head_dim = getattr(cfg, "head_dim", None) or int(cfg.hidden_size) // int(cfg.num_attention_heads)
@@ -150,22 +172,84 @@ def run_full_verify(*, model, wrapper, state: FullVerifyState, prefix_len: int, 
     hidden = base.embed_tokens(state.tree.flat_token_ids)
     positions = int(prefix_len) + state.tree.depths.to(device=hidden.device, dtype=torch.long)
     cos, sin = rope_cos_sin(model, positions, head_dim, hidden.dtype, hidden.device)
-    cos, sin = cos[:, None, :], sin[:, None, :]
+    plan = getattr(wrapper, "current_plan", None)
+    can_fuse = plan is not None and bool(getattr(plan, "fused_append", False))
+    if fused and not can_fuse:
+        raise NotImplementedError("the plan does not allow the fused verify step (see current_plan.fused_append)")
+    use_fused = can_fuse if fused is None else bool(fused)
+    cos3, sin3 = cos[:, None, :], sin[:, None, :]
     for layer_idx, layer in enumerate(base.layers):
         residual = hidden
         normed = layer.input_layernorm(hidden)
         q = layer.self_attn.q_proj(normed).reshape(n, hq, head_dim)
         k = layer.self_attn.k_proj(normed).reshape(n, hkv, head_dim)
         v = layer.self_attn.v_proj(normed).reshape(n, hkv, head_dim).contiguous()
-        q = (q * cos + rotate_half(q) * sin).contiguous()
-        k = (k * cos + rotate_half(k) * sin).contiguous()
         kv_cache = state.paged_prefix_kv[layer_idx]
-        write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size)
-        attn = first_tensor(wrapper.run(q, kv_cache)).reshape(n, hq * head_dim)
+        if use_fused:
+            out = wrapper.run(q.contiguous(), kv_cache, append_key_states=k.contiguous(), append_value_states=v,
+                              rope_cos_sin=(cos, sin))
+        else:
+            q = (q * cos3 + rotate_half(q) * sin3).contiguous()
+            k = (k * cos3 + rotate_half(k) * sin3).contiguous()
+            write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size)
+            out = wrapper.run(q, kv_cache)
+        attn = first_tensor(out).reshape(n, hq * head_dim)
         hidden = residual + layer.self_attn.o_proj(attn)
         residual = hidden
         hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
     return model.lm_head(base.norm(hidden))
+
+
+def next_argmax_inputs(logits: torch.Tensor) -> torch.Tensor:
+    """Greedy next token (``flashinfer_full_verify.py:444-445``)."""
+    return torch.argmax(logits, dim=-1).to(dtype=torch.long)
+
+
+@dataclass
+class FullDecodeState:
+    input_ids: torch.Tensor
+    paged_prefix_kv: list
+
+
+@torch.inference_mode()
+def run_full_ar_decode(*, model, wrappers, state: FullDecodeState, prefix_len: int, page_size: int) -> torch.Tensor:
+    """Greedy autoregressive decode steps of a Llama-layout model on the paged
+    prefix KV, one planned decode wrapper per step
+    (``flashinfer_full_verify.py:1066-1122``): per layer RMSNorm, QKV, RoPE at
+    the step's position, ``write_suffix_kv`` of the new token, then paged
+    decode attention over the prefix and the new token."""
+    cfg = model.config
+    base = model.model
+    head_dim = getattr(cfg, "head_dim", None) or int(cfg.hidden_size) // int(cfg.num_attention_heads)
+    hq, hkv = int(cfg.num_attention_heads), int(cfg.num_key_value_heads)
+    input_ids = state.input_ids
+    logits = None
+    for step_idx, wrapper in enumerate(wrappers):
+        hidden = base.embed_tokens(input_ids.reshape(-1))
+        pos = int(prefix_len) + int(step_idx)
+        cos, sin = rope_cos_sin(model, torch.tensor([pos], device=hidden.device), head_dim, hidden.dtype,
+                                hidden.device)
+        cos, sin = cos[:, None, :], sin[:, None, :]
+        for layer_idx, layer in enumerate(base.layers):
+            residual = hidden
+            normed = layer.input_layernorm(hidden)
+            q = layer.self_attn.q_proj(normed).reshape(1, hq, head_dim)
+            k = layer.self_attn.k_proj(normed).reshape(1, hkv, head_dim)
+            v = layer.self_attn.v_proj(normed).reshape(1, hkv, head_dim).contiguous()
+            q = (q * cos + rotate_half(q) * sin).contiguous()
+            k = (k * cos + rotate_half(k) * sin).contiguous()
+            kv_cache = state.paged_prefix_kv[layer_idx]
+            write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size,
+                            start_pos=pos)
+            attn = first_tensor(wrapper.run(q, kv_cache)).reshape(1, hq * head_dim)
+            hidden = residual + layer.self_attn.o_proj(attn)
+            residual = hidden
+            hidden = residual + layer.mlp(layer.post_attention_layernorm(hidden))
+        logits = model.lm_head(base.norm(hidden))
+        input_ids = next_argmax_inputs(logits)
+    if logits is None:
+        raise RuntimeError("decode steps must be positive")
+    return logits
 
 
 class DirectFlashInferMaskedTreeVerifyBackend:
@@ -221,8 +305,12 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         self._paged_prefix_kv: list[torch.Tensor] | None = None
         self._prefix_logits: torch.Tensor | None = None
         self._committed_verify_rounds = 0
+        self._fallback_decode_wrapper = None
         self._last_fallback_ar_profile = None
         self.match_logits_dtype_rounding = True
+        # run the verify forward's RoPE + append + attention as one launch per
+        # layer when the plan allows it (None: whenever it does)
+        self.fused_verify_step: bool | None = None
 
     # ------------------------------------------------------------ prefill
     @torch.inference_mode()
@@ -296,7 +384,7 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         state = FullVerifyState(tree=tree, paged_prefix_kv=self._paged_prefix_kv)
         plan_prefill_wrapper(self._wrapper, tree, args=self.config, config=self.model.config, dtype=self.dtype)
         logits = run_full_verify(model=self.model, wrapper=self._wrapper, state=state, prefix_len=len(prefix),
-                                 page_size=self.config.page_size)
+                                 page_size=self.config.page_size, fused=self.fused_verify_step)
         scores = self._score_routes(routes=routes, paths=paths, prefix_logits=self._prefix_logits[0],
                                     verify_logits=logits, route_to_node_paths=route_nodes)
         selected, sampling_meta = self._select_route_with_metadata(
@@ -316,8 +404,27 @@ class DirectFlashInferMaskedTreeVerifyBackend:
             **sampling_meta,
         }
         if reason is not None:
-            raise NotImplementedError(
-                f"fallback AR ({reason}) needs paged decode attention, which this package does not provide"
+            generated = self._generate_fallback_ar(
+                max_tokens=(self.fallback_ar_tokens if fallback_max_tokens is None
+                            else min(int(fallback_max_tokens), self.fallback_ar_tokens)),
+                eos_token_id=eos_token_id,
+            )
+            return TargetVerifyResult(
+                selected_route_id=None,
+                scores=scores,
+                decision="fallback_ar",
+                fallback_token_ids=tuple(generated),
+                fallback_reason=reason,
+                metadata={
+                    **common,
+                    "prefix_len_after": len(self.prefix_token_ids),
+                    "target_kv_commit": "fallback_ar_in_place",
+                    "target_reprefill_after_verify": False,
+                    "fallback_triggered": True,
+                    "fallback_reason": reason,
+                    "fallback_token_count": len(generated),
+                    "fallback_ar_profile": self._last_fallback_ar_profile,
+                },
             )
         idx = next(i for i, r in enumerate(routes) if int(r.route_id) == int(selected.route_id))
         path, nodes = self._truncate_selected_path(token_ids=paths[idx], node_ids=route_nodes[idx],
@@ -504,16 +611,19 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         logits, token t > 0 the verify row of the route's node t - 1
         (``target_runtime.py:722-765``).  One device launch per logits tensor
         and one device-to-host copy for all routes."""
-        first_rows, first_toks, rows, toks = [], [], [], []
+        # One launch for both logits tensors: the verify rows, then the
+        # prefix logits as row n_verify.
+        vl = verify_logits.reshape(1, -1) if verify_logits.ndim == 1 else verify_logits
+        n_verify = int(vl.shape[0])
+        rows, toks = [], []
+        for path in paths:
+            rows.append(n_verify)
+            toks.append(int(path[0]))
         for path, nodes in zip(paths, route_to_node_paths):
-            first_rows.append(0)
-            first_toks.append(int(path[0]))
             for off in range(1, len(path)):
                 rows.append(int(nodes[off - 1]))
                 toks.append(int(path[off]))
-        a = gather_token_logprobs(prefix_logits, first_rows, first_toks)
-        b = gather_token_logprobs(verify_logits, rows, toks)
-        values = torch.cat((a, b)).cpu().numpy()
+        values = gather_token_logprobs(vl, rows, toks, extra_logits=prefix_logits).cpu().numpy()
         if self.match_logits_dtype_rounding and verify_logits.dtype in (torch.float16, torch.bfloat16):
             # The reference reads log_softmax outputs in the logits dtype.
             values = torch.from_numpy(values).to(verify_logits.dtype).float().numpy()
@@ -535,6 +645,66 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                 draft_token_logprobs=tuple(float(v) for v in route.draft_token_logprobs),
             ))
         return scores
+
+    # ------------------------------------------------------------ fallback AR
+    def _generate_fallback_ar(self, *, max_tokens: int, eos_token_id: int | None) -> list[int]:
+        """Greedy decode of up to ``max_tokens`` tokens on the committed prefix
+        in place (``target_runtime.py:767-851``): the first token is the
+        argmax of the prefix logits; each step plans the paged decode wrapper
+        for the grown sequence, runs one decode forward (its K/V appended to
+        the prefix pages) and keeps its logits as the next prefix logits.
+        Stops after an EOS token."""
+        if self._paged_prefix_kv is None or self._prefix_logits is None:
+            raise RuntimeError("target fallback AR requires initialized prefix KV")
+        max_tokens = int(max_tokens)
+        if max_tokens <= 0:
+            return []
+        prefix_len = len(self.prefix_token_ids)
+        self._ensure_page_capacity(math.ceil((prefix_len + max_tokens) / int(self.config.page_size)))
+        generated: list[int] = []
+        input_ids = next_argmax_inputs(self._prefix_logits)
+        was_cached = self._fallback_decode_wrapper is not None
+        profile = self.profile_fallback_ar
+        setup_s = plan_s = model_s = 0.0
+        t0 = self._profile_clock() if profile else 0.0
+        if self._fallback_decode_wrapper is None:
+            self._fallback_decode_wrapper = make_decode_wrapper(args=self.config)
+        if profile:
+            setup_s = self._profile_clock() - t0
+        wrapper = self._fallback_decode_wrapper
+        for step_idx in range(max_tokens):
+            token_id = int(input_ids.reshape(-1)[0].detach().cpu())
+            generated.append(token_id)
+            t0 = self._profile_clock() if profile else 0.0
+            plan_decode_wrapper(wrapper, seq_len=prefix_len + step_idx + 1, args=self.config,
+                                config=self.model.config, dtype=self.dtype)
+            if profile:
+                t1 = self._profile_clock()
+                plan_s += t1 - t0
+            logits = run_full_ar_decode(model=self.model, wrappers=[wrapper],
+                                        state=FullDecodeState(input_ids=input_ids,
+                                                              paged_prefix_kv=self._paged_prefix_kv),
+                                        prefix_len=prefix_len + step_idx, page_size=self.config.page_size)
+            if profile:
+                model_s += self._profile_clock() - t1
+            self._prefix_logits = logits.detach()
+            if eos_token_id is not None and token_id == int(eos_token_id):
+                break
+            input_ids = next_argmax_inputs(logits)
+        self.prefix_token_ids = (*self.prefix_token_ids, *generated)
+        self._committed_verify_rounds += 1
+        self._last_fallback_ar_profile = (
+            {"enabled": True, "wrapper_was_cached": was_cached, "wrapper_setup_seconds": setup_s,
+             "decode_plan_seconds": plan_s, "model_forward_seconds": model_s, "token_count": len(generated)}
+            if profile else None
+        )
+        return generated
+
+    def _profile_clock(self) -> float:
+        device = torch.device(self.config.device)
+        if device.type == "cuda" and torch.cuda.is_available():
+            torch.cuda.synchronize(device)
+        return time.perf_counter()
 
     # ------------------------------------------------------------ KV state
     def _ensure_page_capacity(self, required_pages: int) -> None:

@@ -115,13 +115,16 @@ def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     """The (col0, bits) window the tree builder attached to a single-request
     dense mask, if it still describes this plan: one request, one ancestor
     word per query row, col0 within the keys and at most 64 tree columns, and
-    the mask not modified in place since (its version counter unchanged).
+    the mask not modified in place since (its version counter unchanged; an
+    inference tensor keeps no counter, and its window is taken as built).
     Otherwise None, and the plan derives the window from the mask itself."""
     cached = getattr(custom_mask, "_atlas_tree_window", None) if custom_mask is not None else None
     if cached is None or len(qo_lens) != 1 or len(cached) != 3:
         return None
     col0, bits, version = cached
-    if version != custom_mask._version or int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
+    from .flashinfer_full_verify import tensor_version
+
+    if version != tensor_version(custom_mask) or int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
         return None
     if int(bits.numel()) != qo_lens[0] or not (0 <= int(col0) <= kv_lens[0]):
         return None

@@ -147,6 +147,15 @@ class BatchedVerifyCase:
         return self.kv_indptr[-1]
 
 
+def batched_verify_need_pages(*, requests: int = 32, page_size: int = 16, seed: int = 4, min_prefix: int = 1024,
+                              max_prefix: int = 16384) -> int:
+    """Pages the batched verify's requests occupy (to size its pool)."""
+    gen = torch.Generator().manual_seed(seed)
+    prefixes = [int(x) for x in torch.randint(min_prefix, max_prefix + 1, (requests,), generator=gen)]
+    nodes = [len({tuple(r[: i + 1]) for r in tree_routes(100 + b) for i in range(len(r))}) for b in range(requests)]
+    return sum(math.ceil((p + n) / page_size) for p, n in zip(prefixes, nodes))
+
+
 def batched_verify_case(*, pool_pages: int, requests: int = 32, page_size: int = 16, seed: int = 4,
                         min_prefix: int = 1024, max_prefix: int = 16384) -> BatchedVerifyCase:
     """Seeded batched verify: prefixes uniform in [min_prefix, max_prefix],

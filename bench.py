@@ -63,7 +63,8 @@ def _ev():
 
 
 class HeadlineStep:
-    def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None, max_rows=None):
+    def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None, max_rows=None,
+                 routes=None):
         wl = _pkg("workloads")
         ffv = _pkg("flashinfer_full_verify")
         self.ffv = ffv
@@ -74,7 +75,7 @@ class HeadlineStep:
         self.geom = wl.LLAMA_8B
         self.prefix_len = prefix_len
         self.ps = page_size
-        self.routes = wl.forest_routes(seed)
+        self.routes = wl.forest_routes(seed) if routes is None else list(routes)
         spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=self.routes, prefix_len=prefix_len,
                                                               page_size=page_size, device=dev)
         self.n = spec.node_count
@@ -147,7 +148,7 @@ class HeadlineStep:
         cos, sin = self.rope_cos[:, None, :], self.rope_sin[:, None, :]
         return (x * cos) + (torch.cat((-x[..., h:], x[..., :h]), dim=-1) * sin)
 
-    def forward(self, with_append=True, fused=True, rope=None):
+    def forward(self, with_append=True, fused=True, rope=None, with_lse=False):
         """The per-layer device work of the verify forward: write the tree
         nodes' K/V, then masked attention.  ``fused``: both in one launch per
         layer (the rows are written inside the attention kernel); otherwise
@@ -170,13 +171,14 @@ class HeadlineStep:
                 continue
             if with_append:
                 self.kv_ops.append_paged([layer], [self.k_new[l]], [self.v_new[l]], dst_slots=self.tree_slots)
-            self.wrapper.run(self.q[l], layer, out=self.outs[l])
+            self.wrapper.run(self.q[l], layer, out=self.outs[l], lse=self.lses[l] if with_lse else None)
 
     def capture(self):
         """HIP graphs of the 32-layer forward (append + attention) and of the
         attention launches alone.  plan() writes into the wrapper's persistent
         buffers, so replays use the plan of the current step."""
         self.outs = [torch.empty_like(q) for q in self.q]
+        self.lses = [torch.empty(q.shape[:2], dtype=torch.float32, device=q.device) for q in self.q]
         self.plan()
         side = torch.cuda.Stream()
         side.wait_stream(torch.cuda.current_stream())
@@ -252,6 +254,39 @@ class HeadlineStep:
         return a.elapsed_time(b) / (replays * self.geom.layers)
 
 
+def attention_leg(dev, *, prefix_len, routes, with_lse, replays=10):
+    """Verify attention alone, 32 layers of Llama-3.1-8B KV geometry, fp16,
+    page 16, from a HIP graph of the 32 layers' launches (each layer its own
+    KV pages, so the working set exceeds the caches): µs per layer and the
+    fraction of the HBM roofline."""
+    wl = _pkg("workloads")
+    step = HeadlineStep(dev, prefix_len=prefix_len, routes=routes)
+    step.outs = [torch.empty_like(q) for q in step.q]
+    step.lses = [torch.empty(q.shape[:2], dtype=torch.float32, device=q.device) for q in step.q]
+    step.plan()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step.forward(with_append=False, with_lse=with_lse)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step.forward(with_append=False, with_lse=with_lse)
+    graph.replay()
+    us = step.attention_only(replays, graph) * 1000.0
+    nbytes = wl.verify_attention_bytes(step.geom, kv_len=step.kv_len, nodes=step.n, page_size=step.ps)
+    plan = step.wrapper.current_plan
+    out = {"prefix_len": prefix_len, "nodes": step.n, "kv_len": step.kv_len, "lse": with_lse,
+           "work_items": plan.num_work, "merge_items": plan.num_merge, "us_per_layer": round(us, 3),
+           "bytes_per_layer": nbytes, "roofline_us": round(nbytes / (HBM_PEAK_GBPS * 1e3), 3),
+           "GBps": round(nbytes / (us * 1e-6) / 1e9, 1), "frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4),
+           "tree_tokens_per_s": round(step.n / (us * 1e-6 * step.geom.layers), 1)}
+    del step, graph
+    torch.cuda.empty_cache()
+    return out
+
+
 def _mean_ms(pairs):
     return statistics.fmean(a.elapsed_time(b) for a, b in pairs) if pairs else float("nan")
 
@@ -271,15 +306,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
     geom = wl.LLAMA_8B
     ps = 16
     page_bytes = 2 * ps * geom.kv_heads * geom.head_dim * 2
-    gen = torch.Generator().manual_seed(4)
-    prefixes = [int(x) for x in torch.randint(1024, 16385, (requests,), generator=gen)]
-    routes = [wl.tree_routes(100 + b) for b in range(requests)]
-    specs = [ffv.build_deduplicated_tree_spec_from_paths(paths=r, prefix_len=p, page_size=ps, device=dev)
-             for r, p in zip(routes, prefixes)]
-    nodes = [sp.node_count for sp, _ in specs]
-    kv_lens = [p + n for p, n in zip(prefixes, nodes)]
-    req_pages = [math.ceil(k / ps) for k in kv_lens]
-    need_pages = sum(req_pages)
+    need_pages = wl.batched_verify_need_pages(requests=requests, page_size=ps)
     pool = None
     while pool is None:
         pool_pages = max(need_pages + 64, int(pool_gb * 1e9 / (geom.layers * page_bytes)))
@@ -290,19 +317,21 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
             pool_gb /= 2
             if pool_gb < 1:
                 raise
-    perm = torch.randperm(pool_pages, generator=gen)[:need_pages]
+    case = wl.batched_verify_case(pool_pages=pool_pages, requests=requests, page_size=ps)
+    prefixes, routes, nodes, kv_lens, req_pages = case.prefixes, case.routes, case.nodes, case.kv_lens, case.req_pages
+    specs = [ffv.build_deduplicated_tree_spec_from_paths(paths=r, prefix_len=p, page_size=ps, device=dev)
+             for r, p in zip(routes, prefixes)]
+    assert [sp.node_count for sp, _ in specs] == nodes
+    perm = case.page_ids
+    gen = torch.Generator().manual_seed(41)  # instances of the cold commit leg
     used = perm.to(dev)
     g = torch.Generator(device=dev).manual_seed(5)
     for l in range(geom.layers):
         pool[l, used] = (torch.randn((need_pages, 2, ps, geom.kv_heads, geom.head_dim), generator=g, device=dev)
                          * 0.1).to(torch.bfloat16)
     layers = list(pool.unbind(0))
-    kv_indptr_h = [0]
-    for n in req_pages:
-        kv_indptr_h.append(kv_indptr_h[-1] + n)
-    qo_h = [0]
-    for n in nodes:
-        qo_h.append(qo_h[-1] + n)
+    kv_indptr_h = case.kv_indptr
+    qo_h = case.qo_indptr
     flat_mask = torch.cat([sp.bool_mask for sp, _ in specs])
     kv_indptr = torch.tensor(kv_indptr_h, dtype=torch.int32, device=dev)
     kv_indices = perm.to(torch.int32).to(dev)
@@ -342,7 +371,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
     attn_bytes = sum(wl.verify_attention_bytes(geom, kv_len=k, nodes=n, page_size=ps) for k, n in zip(kv_lens, nodes))
 
     # commit: the selected route of every request (dedup node ids)
-    sel = [int(torch.randint(0, len(r), (1,), generator=gen)) for r in routes]
+    sel = case.selected
     item_req, src, dst = [], [], []
     for bi, ((_, rnodes), p) in enumerate(zip(specs, prefixes)):
         for i, nd in enumerate(rnodes[sel[bi]]):
@@ -399,6 +428,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
     torch.cuda.synchronize()
     hot_commit_us = a.elapsed_time(b) * 1000.0 / 100
     moved = len(src) * geom.layers * geom.token_bytes()
+    floors = commit_floors(dev, layers, inst_args, item_req, src, dst, moved, ps, side, lib)
 
     # prune: pages of every request owned; live = prefix + committed tokens
     words = (pool_pages + 31) // 32
@@ -447,9 +477,63 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
         "commit_instances": n_inst, "hot_commit_us": round(hot_commit_us, 3),
         "hot_commit_GBps": round(2 * moved / (hot_commit_us * 1e-6) / 1e9, 1),
         "mark_and_prune_us": round(prune_us, 3), "pruned_pages": freed,
+        **floors,
     }
     del pool, layers, q, outs, ws, graph, cgraph, hgraph, inst_args
     torch.cuda.empty_cache()
+    return out
+
+
+def commit_floors(dev, layers, inst_args, item_req, src, dst, moved, ps, side, lib):
+    """Cold floors for the batched commit, each from a HIP graph over the same
+    40 instances as ``commit_us``: the same K/V rows (every layer) moved by the
+    commit kernel with their slots resolved through the page tables on the
+    host (identity page table on the device, so no lookups before the rows),
+    and a plain contiguous device copy of as many bytes (torch copy_, 40
+    source / destination pairs, 1.3 GB)."""
+    kv_ops = _pkg("kv_ops")
+    n_inst = len(inst_args)
+    slot_sets = []
+    for args in inst_args:
+        idx = args["kv_indices"].cpu().to(torch.int64)
+        indptr = args["kv_indptr"].cpu().tolist()
+
+        def slot(req, pos):
+            return int(idx[indptr[req] + pos // ps]) * ps + pos % ps
+
+        slot_sets.append((torch.tensor([slot(r, p) for r, p in zip(item_req, src)], device=dev),
+                          torch.tensor([slot(r, p) for r, p in zip(item_req, dst)], device=dev)))
+
+    def rows(k):
+        s_t, d_t = slot_sets[k]
+        kv_ops.commit_paged(layers, s_t, d_t, needs_staging=False)
+
+    bufs = torch.empty((2 * n_inst, moved), dtype=torch.uint8, device=dev)
+    bufs.fill_(1)
+    with torch.cuda.stream(side):
+        rows(0)
+        bufs[1].copy_(bufs[0])
+    torch.cuda.current_stream().wait_stream(side)
+    g_rows = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_rows):
+        for k in range(n_inst):
+            rows(k)
+    g_copy = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_copy):
+        for k in range(n_inst):
+            bufs[2 * k + 1].copy_(bufs[2 * k])
+    out = {}
+    for name, g in (("floor_same_rows_no_lookup_us", g_rows), ("floor_contiguous_copy_us", g_copy)):
+        g.replay()
+        torch.cuda.synchronize()
+        a, b = _ev(), _ev()
+        a.record()
+        for _ in range(5):
+            g.replay()
+        b.record()
+        torch.cuda.synchronize()
+        out[name] = round(a.elapsed_time(b) * 1000.0 / (5 * n_inst), 3)
+    del bufs, g_rows, g_copy
     return out
 
 
@@ -810,7 +894,80 @@ def cpu_baseline(step: HeadlineStep, budget_s: float):
     us = statistics.fmean(times) * 1e6
     return {"value": us, "unit": "µs/layer", "cores": cores, "kind": "port",
             "sample": f"oracle float32 masked attention, {len(times)} of 32 layers of the headline step "
-                      f"(kv_len {step.kv_len}, {step.n} nodes)"}
+                      f"(kv_len {step.kv_len}, {step.n} nodes)",
+            "legs": cpu_kv_legs(step)}
+
+
+def _median_us(fn, reps=20, warm=3):
+    for _ in range(warm):
+        fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts) * 1e6
+
+
+def cpu_kv_legs(step: HeadlineStep):
+    """The reference's own torch ops for the KV legs, on the host cores
+    (torch threads): the commit of the headline's selected route over 32
+    layers (target_runtime.py:886-912), write_suffix_kv of its tree nodes in
+    every layer (flashinfer_full_verify.py:1027-1042), the prune's live-page
+    set algebra (sglang_runtime.py:507-539), and the copy-on-write of the
+    8-request x 9-route fork (one move per copied page, every layer,
+    sglang_runtime.py:760-785) at Llama-3.2-1B geometry, bf16, page 64.
+    Median of 20 calls after 3 warm-ups, on CPU copies of the inputs."""
+    from oracle import torch_path as tp
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    cores = torch.get_num_threads()
+    ps = step.ps
+    # identity page order, as the reference's Target keeps its prefix KV
+    layers = [torch.empty((step.pages, 2, ps, step.geom.kv_heads, step.geom.head_dim), dtype=torch.float16)
+              for _ in range(step.geom.layers)]
+    for l, layer in enumerate(layers):
+        layer.copy_(step.layers[l][torch.tensor(step.kv_indices_host, device=step.dev).long()].cpu())
+    k_new = [k.cpu() for k in step.k_new]
+    v_new = [v.cpu() for v in step.v_new]
+    _, parents, _, route_nodes = _oracle_dedup(step.routes)
+    nodes = route_nodes[5 % len(route_nodes)]
+    commit_us = _median_us(lambda: tp.commit_torch(layers, step.prefix_len, nodes, ps))
+    append_us = _median_us(lambda: [tp.write_suffix_kv_torch(layer, k, v, step.prefix_len, ps)
+                                    for layer, k, v in zip(layers, k_new, v_new)])
+    owned = set(range(step.pages))
+    live_path = torch.arange(step.prefix_len + len(nodes))
+    prefix_slots = torch.arange(step.prefix_len)
+    prune_us = _median_us(lambda: tp.prune_torch(owned, prefix_slots, [live_path], ps))
+    # copy-on-write: the fork leg's shape on a compact pool (9 pages per request)
+    geom = _pkg("workloads").LLAMA_1B
+    cps, requests, routes = 64, 8, 9
+    gen = torch.Generator().manual_seed(5)
+    tail_lens = [int(torch.randint(1, cps, (1,), generator=gen)) for _ in range(requests)]
+    slots = requests * routes * cps
+    k_pool = [torch.randn((slots, geom.kv_heads, geom.head_dim)).to(torch.bfloat16) for _ in range(geom.layers)]
+    v_pool = [torch.randn((slots, geom.kv_heads, geom.head_dim)).to(torch.bfloat16) for _ in range(geom.layers)]
+    copies = []
+    for b in range(requests):
+        src = torch.arange(tail_lens[b]) + b * routes * cps
+        for r in range(1, routes):
+            copies.append((src + r * cps, src))
+    cow_us = _median_us(lambda: tp.cow_copy_torch(k_pool, v_pool, copies))
+    cow_bytes = 2 * sum(int(d.numel()) for d, _ in copies) * geom.layers * geom.token_bytes()
+    commit_bytes = 2 * len(nodes) * step.geom.layers * step.geom.token_bytes()
+    return {"cores": cores, "kind": "reference torch ops (oracle/torch_path.py)",
+            "commit_us": round(commit_us, 1), "commit_GBps": round(commit_bytes / (commit_us * 1e-6) / 1e9, 2),
+            "append_us": round(append_us, 1), "prune_us": round(prune_us, 1),
+            "cow_8req_9routes_us": round(cow_us, 1), "cow_GBps": round(cow_bytes / (cow_us * 1e-6) / 1e9, 2),
+            "sample": f"commit of {len(nodes)} tokens and append of {step.n} nodes over 32 layers of the headline "
+                      f"step; prune of its {step.pages} pages; copy-on-write of {len(copies)} tail pages "
+                      f"x 16 layers (1B geometry)"}
+
+
+def _oracle_dedup(routes):
+    from oracle import paged_kv as ref
+
+    return ref.dedup_tree(routes)
 
 
 def profile_attention(step: HeadlineStep, launches: int) -> None:
@@ -922,7 +1079,16 @@ def main():
             "selected_route": route, "committed_tokens": committed, "pruned_pages": freed,
         },
     }
+    result["components"]["committed_tokens_per_s"] = round(committed / (ms_per_step * 1e-3), 1)
+    result["components"]["tree_tokens_per_s_attention"] = round(step.n / (attn_us * 1e-6 * step.geom.layers), 1)
     if not args.no_legs:
+        wl = _pkg("workloads")
+        # configuration 2 (one layer's shape: 4096 prefix, k=3 d=4 of independent
+        # routes, 12 nodes, with the LSE) and the 16k-prefix k=3 d=4 tree
+        result["components"]["config2_4k_tree_lse"] = attention_leg(dev, prefix_len=4096, routes=wl.tree_routes(0),
+                                                                    with_lse=True)
+        result["components"]["tree_16k_k3_d4"] = attention_leg(dev, prefix_len=16384, routes=wl.tree_routes(0),
+                                                               with_lse=False)
         result["components"]["batched_32req"] = batched_leg(dev, pool_gb=args.commit_pool_gb)
         result["components"]["cow_8req_9routes"] = cow_leg(dev)
         result["components"]["drafter_decode_attn"] = decode_leg(dev)

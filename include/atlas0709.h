@@ -328,19 +328,23 @@ int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_d
  * ---------------------------------------------------------------------- */
 
 /* out[i] = log_softmax(logits[row[i]])[token[i]] in fp32 for n gathers over
- * rows of `vocab` logits (dtype fp16, bf16, or ATLAS_DTYPE_F32 = 2), one
- * launch: every row is read once, in chunks spread over the device, and its
+ * rows of `vocab` logits (dtype fp16, bf16, or ATLAS_DTYPE_F32 = 2): rows
+ * 0 .. num_rows-1 of logits_dev, then rows num_rows .. num_rows+num_rows2-1
+ * from logits2_dev (optional: num_rows2 = 0, NULL), so the verify logits and
+ * the prefix logits of a Target verify are scored together.  One launch:
+ * every row is read once, in chunks spread over the device, and its
  * log-sum-exp combined from the chunks in a fixed order (row_lse_dev, if not
- * NULL, receives it).  workspace_dev holds the chunk statistics and one
- * counter per row: at least atlas_gather_logprobs_workspace_bytes(num_rows,
- * vocab) bytes, 16-byte aligned, zero-filled before its first use; every call
- * leaves it reusable (calls sharing it must be stream-ordered).  Replaces the
+ * NULL, receives it).  workspace_dev holds the chunk statistics: at least
+ * atlas_gather_logprobs_workspace_bytes(num_rows, vocab) bytes, 16-byte
+ * aligned, zero-filled before its first use; every call leaves it zero again
+ * (calls sharing it must be stream-ordered).  Replaces the
  * two full-vocab log_softmax calls and the per-token gathers of
  * DirectFlashInferMaskedTreeVerifyBackend._score_routes
  * (src/atlas_0709/target_runtime.py:732-742). */
 #define ATLAS_DTYPE_F32 2
 int64_t atlas_gather_logprobs_workspace_bytes(int64_t num_rows, int64_t vocab);
 int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows,
+                          const void* logits2_dev, int64_t row_stride2, int64_t num_rows2,
                           int64_t vocab, int dtype, const int32_t* row_dev,
                           const int64_t* token_dev, int64_t n, float* row_lse_dev,
                           float* out_dev, void* workspace_dev, size_t workspace_bytes,

@@ -72,6 +72,6 @@ def test_gather_logprobs_workspace_contract_without_device_work():
     need = lib.atlas_gather_logprobs_workspace_bytes(34, 128256)
     assert need > 34 * 8 and lib.atlas_gather_logprobs_workspace_bytes(0, 10) < 0
     fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the call refuses first
-    rc = lib.atlas_gather_logprobs(fake, 128256, 34, 128256, lib_mod.DTYPE_F16, fake, fake, 4, None, fake,
-                                   fake, need - 1, None)
+    rc = lib.atlas_gather_logprobs(fake, 128256, 34, None, 0, 0, 128256, lib_mod.DTYPE_F16, fake, fake, 4, None,
+                                   fake, fake, need - 1, None)
     assert rc == lib_mod.ATLAS_EINVAL and b"workspace" in lib.atlas_last_error()

@@ -45,6 +45,27 @@ def test_gather_logprobs_unaligned_and_ragged_rows(dev, dtype, shape, offset):
     assert np.abs(out.cpu().numpy() - exp).max() <= 2e-5
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_gather_logprobs_two_logits_tensors_in_one_launch(dev, dtype):
+    """Rows of a second logits tensor (the prefix logits) follow the first
+    tensor's rows in one launch; repeated calls reuse the workspace (left
+    zero by each call) and give the same values bit for bit; out-of-range
+    tokens give NaN."""
+    tr = pkg("target_runtime")
+    gen = torch.Generator().manual_seed(3)
+    verify = (torch.randn((34, 128256), generator=gen) * 3).to(dtype)
+    prefix = (torch.randn((128256,), generator=gen) * 3).to(dtype)
+    rows = [34] * 9 + [int(x) for x in torch.randint(0, 34, (27,), generator=gen)] + [5]
+    toks = [int(x) for x in torch.randint(0, 128256, (36,), generator=gen)] + [128256]
+    first = tr.gather_token_logprobs(verify.to(dev), rows, toks, extra_logits=prefix.to(dev)).cpu()
+    again = tr.gather_token_logprobs(verify.to(dev), rows, toks, extra_logits=prefix.to(dev)).cpu()
+    assert torch.equal(first.view(torch.int32), again.view(torch.int32))
+    lp = osc.log_softmax(torch.cat((verify, prefix[None])).double().numpy())
+    exp = np.array([lp[r, t] for r, t in zip(rows[:-1], toks[:-1])])
+    assert np.abs(first[:-1].numpy() - exp).max() <= 2e-4
+    assert math.isnan(float(first[-1]))
+
+
 def _backend(tr, **attrs):
     b = object.__new__(tr.DirectFlashInferMaskedTreeVerifyBackend)
     b.score_weights = None

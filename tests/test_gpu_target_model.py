@@ -1,0 +1,177 @@
+"""The Target drop-in on a small Llama-layout model built here from torch.nn
+(random weights, nothing downloaded): 2 layers, hidden 1024, 8 query heads,
+2 KV heads, head_dim 128, fp16, page 16.
+
+* The verify forward with RoPE, append and attention fused into one launch per
+  layer returns the logits, scores, selected route and committed KV cache of
+  the separate ops (torch RoPE, write_suffix_kv, attention) bit for bit
+  (src/atlas_0709/flashinfer_full_verify.py:1207-1223).
+* The fallback AR (src/atlas_0709/target_runtime.py:767-851) starts from the
+  argmax of the prefix logits, appends every generated token's K/V to the
+  prefix pages, and each step's logits match a dense float32 recomputation of
+  that step from the same weights and cache within 2e-2 (fp16 activations
+  through two layers), with the same greedy tokens wherever the dense top-2
+  margin exceeds that tolerance.
+"""
+
+import math
+from types import SimpleNamespace
+
+import pytest
+import torch
+from torch import nn
+
+from helpers import pkg
+
+pytestmark = pytest.mark.gpu
+
+HIDDEN, HQ, HKV, D, LAYERS, VOCAB, PS = 1024, 8, 2, 128, 2, 1000, 16
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, n, eps=1e-5):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(n))
+        self.eps = eps
+
+    def forward(self, x):
+        y = x.float()
+        y = y * torch.rsqrt(y.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (y * self.weight.float()).to(x.dtype)
+
+
+class MLP(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.gate_proj = nn.Linear(HIDDEN, 2 * HIDDEN, bias=False)
+        self.up_proj = nn.Linear(HIDDEN, 2 * HIDDEN, bias=False)
+        self.down_proj = nn.Linear(2 * HIDDEN, HIDDEN, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(nn.functional.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Layer(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.input_layernorm = RMSNorm(HIDDEN)
+        self.post_attention_layernorm = RMSNorm(HIDDEN)
+        self.self_attn = nn.Module()
+        self.self_attn.q_proj = nn.Linear(HIDDEN, HQ * D, bias=False)
+        self.self_attn.k_proj = nn.Linear(HIDDEN, HKV * D, bias=False)
+        self.self_attn.v_proj = nn.Linear(HIDDEN, HKV * D, bias=False)
+        self.self_attn.o_proj = nn.Linear(HQ * D, HIDDEN, bias=False)
+        self.mlp = MLP()
+
+
+class TinyLlama(nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.model = nn.Module()
+        self.model.embed_tokens = nn.Embedding(VOCAB, HIDDEN)
+        self.model.layers = nn.ModuleList([Layer() for _ in range(LAYERS)])
+        self.model.norm = RMSNorm(HIDDEN)
+        self.lm_head = nn.Linear(HIDDEN, VOCAB, bias=False)
+        self.config = SimpleNamespace(hidden_size=HIDDEN, num_attention_heads=HQ, num_key_value_heads=HKV,
+                                      head_dim=D, rope_theta=500000.0, vocab_size=VOCAB)
+
+
+def _model(dev, seed):
+    torch.manual_seed(seed)
+    m = TinyLlama()
+    with torch.no_grad():
+        m.model.embed_tokens.weight.normal_(0.0, 1.0)
+    return m.half().to(dev).eval()
+
+
+def _backend(dev, model, *, prefix_len, seed, **kw):
+    tr = pkg("target_runtime")
+    cfg = SimpleNamespace(k=3, d=4, page_size=PS, device=str(dev), workspace_mb=64, flashinfer_backend="auto",
+                          use_packed_custom_mask=False)
+    b = tr.DirectFlashInferMaskedTreeVerifyBackend(config=cfg, model=model, **kw)
+    g = torch.Generator(device=dev).manual_seed(seed)
+    pages = math.ceil(prefix_len / PS)
+    b._paged_prefix_kv = [(torch.randn((pages, 2, PS, HKV, D), generator=g, device=dev) * 0.5).half()
+                          for _ in range(LAYERS)]
+    b.prefix_token_ids = tuple(int(x) for x in torch.randint(0, VOCAB, (prefix_len,), generator=g, device=dev))
+    b._prefix_logits = (torch.randn((1, VOCAB), generator=g, device=dev) * 3).half()
+    return b
+
+
+def _routes(seed):
+    tr = pkg("target_runtime")
+    g = torch.Generator().manual_seed(seed)
+    return [tr.VerifyRoutePayload(route_id=10 + i, token_ids=tuple(int(x) for x in torch.randint(0, VOCAB, (4,), generator=g)),
+                                  draft_logprob=-0.5 * i) for i in range(3)]
+
+
+def test_fused_verify_forward_equals_separate_ops(dev):
+    model = _model(dev, 1)
+    results = []
+    for fused in (True, False):
+        b = _backend(dev, model, prefix_len=300, seed=2)
+        b.fused_verify_step = fused
+        routes = _routes(3)
+        res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=routes)
+        torch.cuda.synchronize()
+        assert b._wrapper.current_plan.fused_append
+        results.append((res, [x.clone() for x in b._paged_prefix_kv], b.prefix_token_ids, b._prefix_logits.clone()))
+    (ra, kva, pa, la), (rb, kvb, pb, lb) = results
+    assert ra.selected_route_id == rb.selected_route_id and pa == pb
+    assert [s.token_logprobs for s in ra.scores] == [s.token_logprobs for s in rb.scores]
+    assert torch.equal(la.view(torch.int16), lb.view(torch.int16))
+    for x, y in zip(kva, kvb):
+        assert torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
+def _dense_step_logits(model, cache, seq_len, token, pos):
+    """One decode step of the tiny model in float32 over the first seq_len
+    rows of the paged cache (whose row pos already holds this token's K/V,
+    written by the step under test; it is recomputed here and checked)."""
+    tr = pkg("target_runtime")
+    base = model.model
+    h = base.embed_tokens(torch.tensor([token], device=cache[0].device))
+    cos, sin = tr.rope_cos_sin(model, torch.tensor([pos], device=h.device), D, h.dtype, h.device)
+    cos, sin = cos[:, None, :], sin[:, None, :]
+    for li, layer in enumerate(base.layers):
+        x = layer.input_layernorm(h)
+        q = layer.self_attn.q_proj(x).reshape(1, HQ, D)
+        k = layer.self_attn.k_proj(x).reshape(1, HKV, D)
+        q = q * cos + tr.rotate_half(q) * sin
+        k = k * cos + tr.rotate_half(k) * sin
+        kv = cache[li].reshape(-1, 2, PS, HKV, D)
+        keys = kv[:, 0].reshape(-1, HKV, D)[:seq_len].float()
+        vals = kv[:, 1].reshape(-1, HKV, D)[:seq_len].float()
+        if li == 0:  # the first layer's K row depends on the token alone: written bit for bit
+            assert torch.equal(kv[pos // PS, 0, pos % PS].view(torch.int16), k[0].view(torch.int16))
+        out = []
+        for hh in range(HQ):
+            kh = keys[:, hh // (HQ // HKV)]
+            s = (kh @ q[0, hh].float()) / math.sqrt(D)
+            p = torch.softmax(s, dim=0)
+            out.append(p @ vals[:, hh // (HQ // HKV)])
+        attn = torch.stack(out).reshape(1, HQ * D).half()
+        h = h + layer.self_attn.o_proj(attn)
+        h = h + layer.mlp(layer.post_attention_layernorm(h))
+    return model.lm_head(base.norm(h)).float()
+
+
+def test_fallback_ar_decodes_on_the_prefix_pages(dev):
+    model = _model(dev, 4)
+    b = _backend(dev, model, prefix_len=203, seed=5, fallback_threshold=1e9, fallback_ar_tokens=4)
+    prefix_len = len(b.prefix_token_ids)
+    first = int(torch.argmax(b._prefix_logits, dim=-1))
+    res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=_routes(6))
+    torch.cuda.synchronize()
+    assert res.decision == "fallback_ar" and res.selected_route_id is None
+    toks = list(res.fallback_token_ids)
+    assert len(toks) == 4 and toks[0] == first
+    assert b.prefix_token_ids[prefix_len:] == tuple(toks) and res.metadata["prefix_len_after"] == prefix_len + 4
+    # replay the steps densely: step i consumed token i at position prefix_len + i
+    for i, tok in enumerate(toks):
+        dense = _dense_step_logits(model, b._paged_prefix_kv, prefix_len + i + 1, tok, prefix_len + i)
+        if i + 1 < len(toks):
+            top2 = torch.topk(dense[0], 2).values
+            if float((top2[0] - top2[1]).detach()) > 2e-2:
+                assert int(torch.argmax(dense)) == toks[i + 1], f"step {i}: greedy token differs"
+    assert float((b._prefix_logits.float() - dense).abs().max()) <= 2e-2

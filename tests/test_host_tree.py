@@ -125,3 +125,16 @@ def test_cached_tree_window_validated_against_plan():
     assert ta._cached_tree_window(mask, [n], [kv]) is None
     col0, bits2 = ta.tree_mask_from_dense(mask.view(n, kv))
     assert col0 == 20 and int(bits[4]) == 0b11000 and int(bits2[4]) == 0b10000
+
+
+def test_cached_tree_window_of_inference_tensors():
+    """A mask built under torch.inference_mode keeps no version counter; its
+    window is still taken when the plan's shape matches."""
+    ffv = pkg("flashinfer_full_verify")
+    ta = pkg("tree_attention")
+    with torch.inference_mode():
+        spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=[(1, 2, 3), (1, 5, 6)], prefix_len=20,
+                                                              page_size=4, device="cpu")
+        got = ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len])
+    assert got is not None and got[0] == 20 and got[1].tolist() == spec.tree_mask.tolist()
+    assert ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len + 3]) is None

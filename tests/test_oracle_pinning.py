@@ -504,3 +504,64 @@ def test_frontier_depth_and_records_literals():
     one = _cols([(7, 3, 11, -4.5, 2, -3.25)])
     rec = ofr.pack_records(one, np.array([0]))
     assert rec[0, 6] == np.float64(-3.25).view(np.int64) and rec[0, 5] == np.float64(-4.5).view(np.int64)
+
+
+# ---------------------------------------------------------------- torch CPU path (baseline legs)
+def test_torch_path_commit_and_append_equal_numpy_restatement():
+    """The torch restatement of the reference's commit (target_runtime.py:886-912)
+    and write_suffix_kv (flashinfer_full_verify.py:1027-1042) equal the numpy
+    oracle, pinned by the reference literals above, bit for bit; and the
+    commit literal holds for it directly."""
+    from oracle import torch_path as tp
+
+    cache = torch.from_numpy(_commit_cache().copy())
+    tp.commit_torch([cache], 3, (0, 2), 4)
+    assert cache[0, 0, 3, 0, 0] == 103 and cache[1, 0, 0, 0, 0] == 105
+    rng = np.random.default_rng(9)
+    for _ in range(10):
+        layers = [rng.standard_normal((8, 2, 4, 2, 3)).astype(np.float32) for _ in range(3)]
+        nodes = sorted(rng.choice(9, size=4, replace=False).tolist())
+        mine = [torch.from_numpy(x.copy()) for x in layers]
+        tp.commit_torch(mine, 11, nodes, 4)
+        ref.commit(layers, 11, nodes)
+        for a, b in zip(mine, layers):
+            assert np.array_equal(a.numpy(), b)
+        key = rng.standard_normal((5, 2, 3)).astype(np.float32)
+        val = rng.standard_normal((5, 2, 3)).astype(np.float32)
+        cache = rng.standard_normal((8, 2, 4, 2, 3)).astype(np.float32)
+        mine = torch.from_numpy(cache.copy())
+        tp.write_suffix_kv_torch(mine, torch.from_numpy(key), torch.from_numpy(val), 13, 4)
+        ref.write_suffix(cache, key, val, 13)
+        assert np.array_equal(mine.numpy(), cache)
+
+
+def test_torch_path_cow_and_prune_equal_numpy_restatement():
+    """Per-page move_kv_cache copies equal the oracle's move (FakeKVCache
+    semantics, tests/test_tail_page_cow.py:14-16); the torch prune equals
+    sorted(owned - live) with the reference's sampled live pages and the
+    reference literals (tests/test_tail_page_cow.py:241-293)."""
+    from oracle import torch_path as tp
+
+    rng = np.random.default_rng(10)
+    k = [rng.standard_normal((64, 2, 3)).astype(np.float32) for _ in range(2)]
+    v = [rng.standard_normal((64, 2, 3)).astype(np.float32) for _ in range(2)]
+    tk, tv = [torch.from_numpy(x.copy()) for x in k], [torch.from_numpy(x.copy()) for x in v]
+    copies = [(torch.tensor([40, 41, 42]), torch.tensor([8, 9, 10])), (torch.tensor([44, 45]), torch.tensor([8, 9]))]
+    tp.cow_copy_torch(tk, tv, copies)
+    ref.move_kv(k, v, [40, 41, 42, 44, 45], [8, 9, 10, 8, 9])
+    for a, b in zip(tk + tv, k + v):
+        assert np.array_equal(a.numpy(), b)
+    assert tp.prune_torch({0, 10, 11}, torch.tensor([0, 1, 40]), [torch.tensor([0, 1, 40, 41])], 4) == [11]
+    assert tp.prune_torch({0, 10, 11}, torch.tensor([0, 1]), [torch.tensor([0, 1, 40])], 4) == [11]
+    for _ in range(20):
+        ps = int(rng.choice([1, 4, 16]))
+        owned = set(rng.choice(200, size=60, replace=False).tolist())
+        paths = []
+        for _ in range(3):
+            pages = rng.choice(200, size=4, replace=False)
+            length = int(rng.integers(1, 4 * ps + 1))
+            paths.append([int(pages[i // ps]) * ps + i % ps for i in range(length)])
+        prefix = paths[0][: ps * 2]
+        expect, _ = ref.prune(owned, prefix, paths, ps)
+        got = tp.prune_torch(owned, torch.tensor(prefix), [torch.tensor(p) for p in paths], ps)
+        assert got == expect
