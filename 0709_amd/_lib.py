@@ -110,6 +110,10 @@ _SIGNATURES: dict[str, list] = {
     "atlas_alloc_decode_slots": [_vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_alloc_extend_slots": [_vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_paged_metadata": [_vp, _vp, _vp, ctypes.c_int, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _vp],
+    "atlas_pool_prepare_frontier": [
+        _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _c_i64,
+        _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp,
+    ],
     "atlas_gather_logprobs_workspace_bytes": [_c_i64, _c_i64],
     "atlas_gather_logprobs": [
         _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _c_i64, _vp, _vp, _vp,

@@ -240,6 +240,139 @@ __global__ __launch_bounds__(1024) void alloc_extend_kernel(const int64_t* prefi
   }
 }
 
+// ---------------------------------------------------------------------------
+// Frontier step of many requests: one workgroup per active route.
+// ---------------------------------------------------------------------------
+constexpr int kFrontierThreads = 256;
+
+struct FrontierLimits {
+  int64_t num_free;
+  int64_t page_size;
+  int64_t num_pages;
+  int64_t req_rows;
+  int64_t row_stride;
+  int64_t flat_total;
+  int64_t cow_total;
+  int64_t page_total;
+  int64_t num_flag_groups;
+  int64_t num_routes;
+};
+
+__device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
+
+// Every index a descriptor carries stays inside the buffers the launch was
+// given; a route that fails is skipped (and reported through flags[0]).
+__device__ bool frontier_route_ok(const atlas_pool_frontier_route_t& d, const FrontierLimits& L) {
+  const int64_t ps = L.page_size;
+  if (d.prev_len < 0 || d.prev_len + 1 > L.row_stride) return false;
+  if (d.prev_len > 0 && d.path == nullptr) return false;
+  if (d.flat_offset < 0 || d.flat_offset + d.prev_len + 1 > L.flat_total) return false;
+  const int64_t npages = (d.prev_len + ps) / ps;
+  if (d.page_offset < 0 || d.page_offset + npages > L.page_total) return false;
+  if (d.cow_tail != 0 && d.cow_tail != d.prev_len % ps) return false;
+  if (d.cow_tail > 0 && (d.cow_free_index < 0 || d.cow_free_index >= L.num_free || d.cow_offset < 0 ||
+                         d.cow_offset + d.cow_tail > L.cow_total))
+    return false;
+  if ((d.prev_len % ps == 0) != (d.new_free_index >= 0) || d.new_free_index >= L.num_free) return false;
+  if (d.req_row < 0 || d.req_row >= L.req_rows || d.write_start < 0 || d.write_start > d.prev_len) return false;
+  if (d.group_first < 0 || d.group_count < 1 || d.group_first + d.group_count > L.num_routes) return false;
+  return d.flag_index >= 0 && d.flag_index < L.num_flag_groups;
+}
+
+// Decode slot of a route (the allocator's decode rule applied to its new
+// path) and the page its copy-on-write tail moves to (-1: none).
+__device__ __forceinline__ int64_t frontier_decode_slot(const atlas_pool_frontier_route_t& d, const int64_t* free_pages,
+                                                        int64_t ps, int64_t& cow_page) {
+  cow_page = d.cow_tail > 0 ? free_pages[d.cow_free_index] : -1;
+  if (d.new_free_index >= 0) return free_pages[d.new_free_index] * ps;
+  const int64_t last = d.cow_tail > 0 ? cow_page * ps + (d.cow_tail - 1) : d.path[d.prev_len - 1];
+  return last + 1;
+}
+
+// Slot p of the new path: the old path, its copied tail on the fresh page,
+// then the decode slot.
+__device__ __forceinline__ int64_t frontier_slot(const atlas_pool_frontier_route_t& d, int64_t p, int64_t cow_page,
+                                                 int64_t out, int64_t ps) {
+  if (p == d.prev_len) return out;
+  const int64_t cut = d.prev_len - d.cow_tail;
+  if (d.cow_tail > 0 && p >= cut) return cow_page * ps + (p - cut);
+  return d.path[p];
+}
+
+__global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
+    const atlas_pool_frontier_route_t* __restrict__ routes, FrontierLimits L, const int64_t* __restrict__ free_pages,
+    int64_t* __restrict__ req_to_token, int64_t* __restrict__ flat, int64_t* __restrict__ out_slots,
+    int64_t* __restrict__ cow_dst, int64_t* __restrict__ cow_src, int32_t* __restrict__ kv_indptr,
+    int32_t* __restrict__ kv_last, int32_t* __restrict__ seq_lens, int32_t* __restrict__ page_ids,
+    int64_t* __restrict__ flags) {
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const atlas_pool_frontier_route_t d = routes[r];
+  const int64_t ps = L.page_size;
+  if (!frontier_route_ok(d, L)) {
+    if (tid == 0) flags[0] = 0;
+    return;
+  }
+  int64_t cow_page;
+  const int64_t out = frontier_decode_slot(d, free_pages, ps, cow_page);
+  const int64_t n = d.prev_len + 1;
+  const int64_t npages = (n + ps - 1) / ps;
+  int64_t* fl = flags + 1 + 3 * d.flag_index;
+  if (tid == 0) {
+    out_slots[r] = out;
+    seq_lens[r] = static_cast<int32_t>(n);
+    kv_last[r] = static_cast<int32_t>(n - (npages - 1) * ps);
+    kv_indptr[r + 1] = static_cast<int32_t>(d.page_offset + npages);
+    if (r == 0) kv_indptr[0] = 0;
+    if (d.owned_bitmap != nullptr) {
+      const int64_t pg = floor_div(out, ps);
+      if (pg >= 0 && pg < L.num_pages) atomicOr(&d.owned_bitmap[pg >> 5], 1u << (pg & 31));
+      if (cow_page >= 0 && cow_page < L.num_pages) atomicOr(&d.owned_bitmap[cow_page >> 5], 1u << (cow_page & 31));
+    }
+  }
+  // New path, request-row slice, page table and layout check.
+  bool layout_ok = true;
+  for (int64_t p = tid; p < n; p += kFrontierThreads) {
+    const int64_t v = frontier_slot(d, p, cow_page, out, ps);
+    flat[d.flat_offset + p] = v;
+    if (p >= d.write_start) req_to_token[d.req_row * L.row_stride + p] = v;
+    const int64_t in_page = p % ps;
+    if (in_page == 0) {
+      page_ids[d.page_offset + p / ps] = static_cast<int32_t>(floor_div(v, ps));
+      if (((v % ps) + ps) % ps != 0) layout_ok = false;
+    } else if (v != frontier_slot(d, p - in_page, cow_page, out, ps) + in_page) {
+      layout_ok = false;
+    }
+  }
+  if (!layout_ok) fl[0] = 0;
+  // Copy-on-write slot pairs; the fresh page must not be a copy source of
+  // the same request.
+  if (d.cow_tail > 0) {
+    const int64_t cut = d.prev_len - d.cow_tail;
+    for (int64_t t = tid; t < d.cow_tail; t += kFrontierThreads) {
+      cow_dst[d.cow_offset + t] = cow_page * ps + t;
+      cow_src[d.cow_offset + t] = d.path[cut + t];
+    }
+    bool disjoint = true;
+    for (int64_t s = d.group_first; s < d.group_first + d.group_count; ++s) {
+      const atlas_pool_frontier_route_t e = routes[s];
+      if (e.cow_tail == 0 || !frontier_route_ok(e, L)) continue;
+      const int64_t ecut = e.prev_len - e.cow_tail;
+      for (int64_t t = tid; t < e.cow_tail; t += kFrontierThreads)
+        if (floor_div(e.path[ecut + t], ps) == cow_page) disjoint = false;
+    }
+    if (!disjoint) fl[2] = 0;
+  }
+  // Distinct decode slots among the request's routes.
+  for (int64_t s = d.group_first + tid; s < d.group_first + d.group_count; s += kFrontierThreads) {
+    if (s == r) continue;
+    const atlas_pool_frontier_route_t e = routes[s];
+    if (!frontier_route_ok(e, L)) continue;
+    int64_t ecow;
+    if (frontier_decode_slot(e, free_pages, ps, ecow) == out) fl[1] = 0;
+  }
+}
+
 }  // namespace
 }  // namespace atlas
 
@@ -323,4 +456,31 @@ extern "C" int atlas_alloc_extend_slots(const int64_t* prefix_lens_dev, const in
   hipLaunchKernelGGL(alloc_extend_kernel, dim3(1), dim3(1024), 0, static_cast<hipStream_t>(stream),
                      prefix_lens_dev, seq_lens_dev, last_loc_dev, free_pages_dev, page_size, bs, out_dev);
   return launch_status("alloc_extend_kernel");
+}
+
+extern "C" int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, int num_routes,
+                                      const int64_t* free_pages_dev, int64_t num_free, int64_t page_size,
+                                      int64_t num_pages, int64_t* req_to_token_dev, int64_t req_rows,
+                                      int64_t req_row_stride, int64_t* flat_dev, int64_t flat_total,
+                                      int64_t* out_slots_dev, int64_t* cow_dst_dev, int64_t* cow_src_dev,
+                                      int64_t cow_total, int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev,
+                                      int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
+                                      int64_t* flags_dev, int64_t num_flag_groups, void* stream) {
+  ATLAS_REQUIRE(num_routes >= 0 && page_size > 0 && num_pages > 0, "bad route count / page arguments");
+  if (num_routes == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(routes_dev && req_to_token_dev && flat_dev && out_slots_dev && kv_indptr_dev && kv_last_page_len_dev &&
+                    seq_lens_dev && kv_page_indices_dev && flags_dev,
+                "frontier buffers must not be NULL");
+  ATLAS_REQUIRE(num_free >= 0 && (num_free == 0 || free_pages_dev), "free list must not be NULL");
+  ATLAS_REQUIRE(cow_total >= 0 && (cow_total == 0 || (cow_dst_dev && cow_src_dev)), "copy-on-write lists missing");
+  ATLAS_REQUIRE(req_rows > 0 && req_row_stride > 0, "request-row pool must not be empty");
+  ATLAS_REQUIRE(flat_total >= num_routes && page_total >= num_routes && num_flag_groups > 0,
+                "output sizes too small for %d routes", num_routes);
+  FrontierLimits L{num_free, page_size, num_pages, req_rows, req_row_stride, flat_total, cow_total, page_total,
+                   num_flag_groups, num_routes};
+  hipLaunchKernelGGL(frontier_prepare_kernel, dim3(num_routes), dim3(kFrontierThreads), 0,
+                     static_cast<hipStream_t>(stream), routes_dev, L, free_pages_dev, req_to_token_dev, flat_dev,
+                     out_slots_dev, cow_dst_dev, cow_src_dev, kv_indptr_dev, kv_last_page_len_dev, seq_lens_dev,
+                     kv_page_indices_dev, flags_dev);
+  return launch_status("frontier_prepare_kernel");
 }

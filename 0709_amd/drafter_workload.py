@@ -33,7 +33,8 @@ from typing import Any, Callable, Sequence
 import torch
 
 from .flashinfer_paged.kv import KVTreeStore
-from .flashinfer_paged.sglang_runtime import SGLangFlashInferFrontierModelBackend, SGLangRoutePoolBridge
+from .flashinfer_paged.sglang_runtime import (SGLangFlashInferFrontierModelBackend, SGLangRoutePoolBridge,
+                                              fused_frontier_supported)
 from .flashinfer_paged.types import DecodePhase, RouteState
 
 VOCAB = 128256
@@ -149,8 +150,13 @@ class DrafterForkWorkload:
 
     def __init__(self, *, plans: Sequence[ForkPlan], req_pool: Any, allocator: Any, page_size: int,
                  device, writer: Callable[[torch.Tensor, torch.Tensor], None],
-                 use_page_attention_metadata: bool = True) -> None:
+                 use_page_attention_metadata: bool = True, batched: bool = False) -> None:
         self.page_size = int(page_size)
+        # batched: each decode step runs every request's frontier as one
+        # step (SGLangFlashInferFrontierModelBackend.decode_frontiers), whose
+        # writer call covers all requests' new slots in request order -- the
+        # value ids the per-request calls take one after another
+        self.batched = bool(batched)
         self.device = torch.device(device)
         self.allocator = allocator
         self.req_pool = req_pool
@@ -203,8 +209,31 @@ class DrafterForkWorkload:
         if step is not None and step in req.plan.forks:
             self._fork(req, req.plan.forks[step])
         out = req.backend.decode_frontier_one_token(req.active)
-        slots, vids = self._last_write
-        for nid, v in zip(out.new_node_ids, vids.tolist()):
+        _, vids = self._last_write
+        self._after_decode(req, out, vids.tolist())
+
+    def decode_steps(self, reqs: Sequence[RequestState], step: int | None = None) -> None:
+        """One decode step of several requests: one batched frontier step in
+        batched mode, else one call per request in order."""
+        if not self.batched or not fused_frontier_supported([r.bridge for r in reqs]):
+            for req in reqs:
+                self.decode_step(req, step)
+            return
+        for req in reqs:
+            if step is not None and step in req.plan.forks:
+                self._fork(req, req.plan.forks[step])
+        outs = SGLangFlashInferFrontierModelBackend.decode_frontiers([r.backend for r in reqs],
+                                                                     [r.active for r in reqs])
+        _, vids = self._last_write
+        values = vids.tolist()
+        off = 0
+        for req, out in zip(reqs, outs):
+            n = len(out.new_node_ids)
+            self._after_decode(req, out, values[off : off + n])
+            off += n
+
+    def _after_decode(self, req: RequestState, out, values: list[int]) -> None:
+        for nid, v in zip(out.new_node_ids, values):
             req.node_value_ids[int(nid)] = int(v)
             if req.plan.select == "best":
                 req.node_logprobs[int(nid)] = -(req.logprob_rng.random() * 5.0)
@@ -212,12 +241,19 @@ class DrafterForkWorkload:
         for r in req.active:
             r.pending_token_id = req.rng.randrange(VOCAB)
 
+    def _post_steps(self) -> None:
+        if not self.batched:
+            for req in self.requests:
+                for _ in range(req.plan.post_steps):
+                    self.decode_step(req)
+            return
+        for k in range(max(r.plan.post_steps for r in self.requests)):
+            self.decode_steps([r for r in self.requests if k < r.plan.post_steps])
+
     def stage1(self, on_step: Callable[[str], None] | None = None) -> None:
         steps = max(r.plan.steps for r in self.requests)
         for t in range(steps):
-            for req in self.requests:
-                if t < req.plan.steps:
-                    self.decode_step(req, t)
+            self.decode_steps([r for r in self.requests if t < r.plan.steps], t)
             if on_step is not None:
                 on_step(f"decode{t}")
 
@@ -242,9 +278,7 @@ class DrafterForkWorkload:
             req.stats.append(stats)
 
     def post_decode(self) -> None:
-        for req in self.requests:
-            for _ in range(req.plan.post_steps):
-                self.decode_step(req)
+        self._post_steps()
 
     def fallback_extend(self) -> None:
         for req in self.requests:
@@ -257,11 +291,9 @@ class DrafterForkWorkload:
             req.prefix_value_ids = req.prefix_value_ids + list(range(before, before + n))
             req.active = [req.store.new_root_route(req.rng.randrange(VOCAB),
                                                    req.store.prefix_view(len(req.backend.prefix_token_ids)))]
-        for req in self.requests:
-            # The logical store's committed tokens lag the EXTEND suffix; the
-            # root's prefix view carries the true committed length.
-            for _ in range(req.plan.post_steps):
-                self.decode_step(req)
+        # The logical store's committed tokens lag the EXTEND suffix; the
+        # root's prefix view carries the true committed length.
+        self._post_steps()
 
     def run(self, on_phase: Callable[[str], None] | None = None) -> None:
         cb = on_phase or (lambda _name: None)

@@ -41,6 +41,10 @@ class NativeTokenToKVPool:
                                     device=self.device)
         self.k_buffer = list(self._storage[0].unbind(0))
         self.v_buffer = list(self._storage[1].unbind(0))
+        # the layer tables every all-layer call passes (fixed for the pool's life)
+        self._geom = kv_ops.token_pool_geometry(self.k_buffer[0])
+        self._k_ptrs = _lib.ptr_array([int(t.data_ptr()) for t in self.k_buffer])
+        self._v_ptrs = _lib.ptr_array([int(t.data_ptr()) for t in self.v_buffer])
 
     def get_key_buffer(self, layer_id: int) -> torch.Tensor:
         return self.k_buffer[int(layer_id)]
@@ -53,7 +57,8 @@ class NativeTokenToKVPool:
 
     def move_kv_cache(self, tgt_loc: torch.Tensor, src_loc: torch.Tensor) -> None:
         """``K[tgt] = K[src]; V[tgt] = V[src]`` in every layer, one launch."""
-        kv_ops.move_slots(self.k_buffer, self.v_buffer, tgt_loc, src_loc)
+        kv_ops.move_slots(self.k_buffer, self.v_buffer, tgt_loc, src_loc,
+                          layer_tables=(self._k_ptrs, self._v_ptrs, self._geom))
 
     def set_kv_buffer(self, layer: Any, loc: torch.Tensor, cache_k: torch.Tensor, cache_v: torch.Tensor, *args,
                       **kwargs) -> None:
@@ -64,7 +69,12 @@ class NativeTokenToKVPool:
 
     def set_kv_buffer_all_layers(self, loc: torch.Tensor, k_rows: Sequence[torch.Tensor],
                                  v_rows: Sequence[torch.Tensor]) -> None:
-        kv_ops.append_token_pool(self.k_buffer, self.v_buffer, k_rows, v_rows, loc)
+        """``set_kv_buffer`` of every layer in one launch (rows ``[n, Hkv, D]``
+        per layer, in the pool dtype)."""
+        if len(k_rows) != self.layer_num or len(v_rows) != self.layer_num:
+            raise ValueError(f"one K and one V source per layer ({self.layer_num}) are required")
+        kv_ops.append_token_pool(self.k_buffer, self.v_buffer, k_rows, v_rows, loc,
+                                 layer_tables=(self._k_ptrs, self._v_ptrs, self._geom))
 
 
 class NativePagedAllocator:
@@ -148,6 +158,14 @@ class NativePagedAllocator:
         _lib.check(rc, "atlas_alloc_extend_slots")
         self._head += new_pages
         return out
+
+    def consume_pages(self, n: int) -> None:
+        """Advance the free-list head past ``n`` pages that a kernel has
+        taken from ``free_pages`` (in order)."""
+        n = int(n)
+        if n < 0 or n > self.num_pages - self._head:
+            raise RuntimeError(f"cannot take {n} pages: {self.num_pages - self._head} are free")
+        self._head += n
 
     def free(self, free_index: torch.Tensor) -> None:
         if int(free_index.numel()) == 0:

@@ -19,6 +19,7 @@ freed-page order identical):
 
 from __future__ import annotations
 
+import ctypes
 import time
 from dataclasses import dataclass, field
 from typing import Any, Sequence
@@ -347,6 +348,10 @@ class SGLangRoutePoolBridge:
                                                         written_length=int(written_length))
 
     def ensure_route_rows(self, routes: Sequence[RouteState]) -> torch.Tensor:
+        return torch.tensor(self._route_row_indices(routes), dtype=torch.long, device=self.device)
+
+    def _route_row_indices(self, routes: Sequence[RouteState]) -> list[int]:
+        """Request rows of the routes (allocating rows for new routes)."""
         missing = [r for r in routes if int(r.route_id) not in self.route_rows]
         if missing:
             handles = [_PoolReqHandle(rid=f"atlas-{int(r.route_id)}") for r in missing]
@@ -359,8 +364,7 @@ class SGLangRoutePoolBridge:
             for route, handle, row in zip(missing, handles, rows):
                 handle.req_pool_idx = int(row)
                 self.bind_existing_route_row(route.route_id, int(row), handle=handle)
-        return torch.tensor([self.route_rows[int(r.route_id)].req_pool_index for r in routes], dtype=torch.long,
-                            device=self.device)
+        return [self.route_rows[int(r.route_id)].req_pool_index for r in routes]
 
     def release_route_rows(self, route_ids: Sequence[int]) -> None:
         for route_id in route_ids:
@@ -381,8 +385,7 @@ class SGLangRoutePoolBridge:
     def register_node_slots(self, node_ids, slot_ids) -> None:
         nodes = _int_list(node_ids)
         if isinstance(slot_ids, torch.Tensor):
-            flat = slot_ids.reshape(-1)
-            values: list[Any] = [flat[i] for i in range(int(flat.numel()))]
+            values: list[Any] = list(slot_ids.reshape(-1).unbind(0))
         else:
             values = [int(s) for s in slot_ids]
         if len(nodes) != len(values):
@@ -664,7 +667,7 @@ class SGLangRoutePoolBridge:
         # freshly allocated pages, which no source path can hold.
         dst_pages = torch.div(destination, self.page_size, rounding_mode="floor")
         src_pages = torch.div(source, self.page_size, rounding_mode="floor")
-        self._check_or_defer(~torch.isin(dst_pages, src_pages).any(),
+        self._check_or_defer(dst_pages[:, None].ne(src_pages[None, :]).all(),
                              "copy-on-write destination pages overlap its source pages")
         move(destination, source)
 
@@ -682,11 +685,37 @@ class SGLangRoutePoolBridge:
         dirty start at the copied tail.  All copies go in one move call.
         Returns the new paths and {route position: dirty start}.
         """
+        result = list(slot_paths)
+        plan = self._tail_copy_plan(routes, slot_paths)
+        if not plan:
+            return result, {}
+        dest_pages = self._allocate_full_pages(len(plan))
+        dirty: dict[int, int] = {}
+        dst_parts, src_parts = [], []
+        for page, (index, path, tail) in zip(dest_pages, plan):
+            src = path[-tail:]
+            dst = page[:tail]
+            dst_parts.append(dst)
+            src_parts.append(src)
+            new_path = torch.cat((path[:-tail], dst))
+            rid = int(routes[index].route_id)
+            self.route_slot_paths[rid] = new_path
+            self.route_tail_page_keys[rid] = self._new_tail_page_key()
+            result[index] = new_path
+            dirty[index] = int(path.numel()) - tail
+            self.cow_pages_copied += 1
+            self.cow_tokens_copied += tail
+        self._copy_kv_slots(torch.cat(dst_parts), torch.cat(src_parts))
+        return result, dirty
+
+    def _tail_copy_plan(self, routes: Sequence[RouteState], slot_paths: Sequence[torch.Tensor]):
+        """Routes whose partial tail page must be copied, as (position, path,
+        tail length) in copy order: every writer of a shared tail page (same
+        lease key) but the first."""
         if len(routes) != len(slot_paths):
             raise ValueError("routes and slot_paths must have the same length")
-        result = list(slot_paths)
         if len(routes) <= 1:
-            return result, {}
+            return []
         groups: dict[int, list[tuple[int, torch.Tensor, int]]] = {}
         unkeyed: list[tuple[int, torch.Tensor, int, int, torch.Tensor]] = []
         for index, path in enumerate(slot_paths):
@@ -711,27 +740,7 @@ class SGLangRoutePoolBridge:
             for (index, path, tail, rid, _), key in zip(unkeyed, keys):
                 self.route_tail_page_keys[rid] = int(key)
                 groups.setdefault(int(key), []).append((index, path, tail))
-        plan = [entry for group in groups.values() for entry in group[1:]]
-        if not plan:
-            return result, {}
-        dest_pages = self._allocate_full_pages(len(plan))
-        dirty: dict[int, int] = {}
-        dst_parts, src_parts = [], []
-        for page, (index, path, tail) in zip(dest_pages, plan):
-            src = path[-tail:]
-            dst = page[:tail]
-            dst_parts.append(dst)
-            src_parts.append(src)
-            new_path = torch.cat((path[:-tail], dst))
-            rid = int(routes[index].route_id)
-            self.route_slot_paths[rid] = new_path
-            self.route_tail_page_keys[rid] = self._new_tail_page_key()
-            result[index] = new_path
-            dirty[index] = int(path.numel()) - tail
-            self.cow_pages_copied += 1
-            self.cow_tokens_copied += tail
-        self._copy_kv_slots(torch.cat(dst_parts), torch.cat(src_parts))
-        return result, dirty
+        return [entry for group in groups.values() for entry in group[1:]]
 
     # ------------------------------------------------------------ frontier
     def prepare_frontier(self, active_routes: Sequence[RouteState], *,
@@ -740,7 +749,7 @@ class SGLangRoutePoolBridge:
         and page metadata for one decode step (``sglang_runtime.py:800-959``)."""
         if not active_routes:
             raise ValueError("active_routes cannot be empty")
-        req_indices = self.ensure_route_rows(active_routes)
+        req_rows = self._route_row_indices(active_routes)
         paths = [self._slot_path_for_route(r) for r in active_routes]
         paths, dirty = self._copy_partial_tail_pages_with_dirty_starts(active_routes, paths)
         for index, start in dirty.items():
@@ -811,10 +820,11 @@ class SGLangRoutePoolBridge:
             if prev % self.page_size == 0 or rid not in self.route_tail_page_keys:
                 self.route_tail_page_keys[rid] = self._new_tail_page_key()
 
-        # input ids, sequence lengths, positions (and, for a pool that takes
-        # them, the request-row write indices) reach the device in one copy
+        # input ids, sequence lengths, positions, request rows (and, for a
+        # pool that takes them, the request-row write indices) reach the
+        # device in one copy
         b = len(active_routes)
-        host = [int(r.pending_token_id) for r in active_routes] + seq_lens + positions
+        host = [int(r.pending_token_id) for r in active_routes] + seq_lens + positions + req_rows
         batched = bool(getattr(self.req_to_token_pool, "batched_row_writes", False))
         write_rows: list[int] = []
         write_pos: list[int] = []
@@ -828,9 +838,10 @@ class SGLangRoutePoolBridge:
         if on_device:
             packed = packed.to(self.device, non_blocking=True)
         input_ids, seq_dev, pos_dev = packed[:b], packed[b : 2 * b], packed[2 * b : 3 * b]
+        req_indices = packed[3 * b : 4 * b]
         if batched:
             nw = len(write_rows)
-            self._write_req_token_slices(segments, packed[3 * b : 3 * b + nw], packed[3 * b + nw :])
+            self._write_req_token_slices(segments, packed[4 * b : 4 * b + nw], packed[4 * b + nw :])
             for i in range(b):
                 commit_route(i)
         else:
@@ -863,6 +874,79 @@ class SGLangRoutePoolBridge:
             page_index_count=page_indices, paged_decode_spec=spec,
         )
         return input_ids, meta
+
+    def _plan_fused_frontier(self, active_routes: Sequence[RouteState]) -> "_FusedFrontierPlan":
+        """Host half of ``prepare_frontier`` for ``prepare_frontiers``: request
+        rows, slot paths, the copy-on-write plan with its leases, dirty starts
+        and counters, and the request-row segments, in the order
+        ``prepare_frontier`` takes them; no device work."""
+        if not active_routes:
+            raise ValueError("active_routes cannot be empty")
+        rows = self._route_row_indices(active_routes)
+        paths = [self._slot_path_for_route(r) for r in active_routes]
+        n = len(paths)
+        prevs = [int(p.numel()) for p in paths]
+        cow_tail = [0] * n
+        cow_rank = [-1] * n
+        for rank, (index, _path, tail) in enumerate(self._tail_copy_plan(active_routes, paths)):
+            rid = int(active_routes[index].route_id)
+            self.route_tail_page_keys[rid] = self._new_tail_page_key()
+            cow_tail[index] = tail
+            cow_rank[index] = rank
+            self.cow_pages_copied += 1
+            self.cow_tokens_copied += tail
+            row = self.route_rows[rid]
+            if int(row.written_length) > 0:
+                start = prevs[index] - tail
+                row.pending_dirty_start = start if row.pending_dirty_start is None else min(
+                    int(row.pending_dirty_start), start)
+        starts: list[int] = []
+        kinds: list[str] = []
+        for route, prev, req_row in zip(active_routes, prevs, rows):
+            row = self.route_rows[int(route.route_id)]
+            if int(row.written_length) == 0:
+                start, kind = 0, "full_init"
+            else:
+                if int(row.written_length) != prev:
+                    raise RuntimeError(
+                        "SGLang route-row state does not match its physical KV path: "
+                        f"route_id={int(route.route_id)}, written_length={int(row.written_length)}, "
+                        f"physical_path_length={prev}"
+                    )
+                if row.pending_dirty_start is None:
+                    start, kind = prev, "append"
+                else:
+                    start, kind = int(row.pending_dirty_start), "cow_patch"
+            self._check_req_write(req_row, start, prev + 1 - start, kind)
+            starts.append(start)
+            kinds.append(kind)
+        for i, p in enumerate(paths):
+            if prevs[i] and (p.dtype != torch.int64 or not p.is_contiguous()):
+                paths[i] = p.to(torch.int64).contiguous()
+        return _FusedFrontierPlan(list(active_routes), rows, paths, prevs, cow_tail, cow_rank,
+                                  sum(1 for t in cow_tail if t), starts, kinds)
+
+    def _finish_fused_frontier(self, plan: "_FusedFrontierPlan", full_paths: Sequence[torch.Tensor],
+                               flags: "_StepFlags", group: int) -> None:
+        """Bookkeeping of ``prepare_frontier`` once the step's launch went
+        through: request-row state, new slot paths, leases, counters and the
+        step's device checks."""
+        ps = self.page_size
+        for i, route in enumerate(plan.routes):
+            rid = int(route.route_id)
+            row = self.route_rows[rid]
+            prev = plan.prevs[i]
+            self._count_req_write(prev + 1 - plan.starts[i], plan.kinds[i])
+            row.written_length = prev + 1
+            row.pending_dirty_start = None
+            self.route_slot_paths[rid] = full_paths[i]
+            if prev % ps == 0 or rid not in self.route_tail_page_keys:
+                self.route_tail_page_keys[rid] = self._new_tail_page_key()
+        self.attention_metadata_builds += 1
+        self.attention_metadata_token_indices += sum(plan.prevs) + len(plan.prevs)
+        self.attention_metadata_page_indices += sum((p + ps) // ps for p in plan.prevs)
+        validate = bool(self.validate_page_layout)
+        self.pending_device_checks.append(lambda: flags.check(group, validate))
 
     def _check_or_defer(self, ok: torch.Tensor, message: str) -> None:
         """A device-computed condition is checked at the next report boundary
@@ -1016,6 +1100,190 @@ class SGLangRoutePoolBridge:
         return {name: int(getattr(self, name)) for name in _COUNTERS}
 
 
+@dataclass
+class _FusedFrontierPlan:
+    routes: list[RouteState]
+    rows: list[int]
+    paths: list[torch.Tensor]
+    prevs: list[int]
+    cow_tail: list[int]
+    cow_rank: list[int]
+    num_cow: int
+    starts: list[int]
+    kinds: list[str]
+
+
+class _StepFlags:
+    """Check flags of one fused frontier step (device int64s the kernel
+    clears on a failed check), read back once, at the first check."""
+
+    def __init__(self, flags: torch.Tensor) -> None:
+        self.flags = flags
+        self._host: list[int] | None = None
+
+    def check(self, group: int, validate_layout: bool) -> None:
+        if self._host is None:
+            self._host = [int(x) for x in self.flags.cpu().tolist()]
+        h = self._host
+        if not h[0]:
+            raise RuntimeError("frontier step: a route descriptor was out of range and the route was skipped")
+        base = 1 + 3 * int(group)
+        # the order prepare_frontier records these checks in
+        if not h[base + 2]:
+            raise RuntimeError("copy-on-write destination pages overlap its source pages")
+        if not h[base + 1]:
+            raise RuntimeError("SGLang allocated duplicate output KV slots across forked routes; "
+                               "tail-page copy-on-write is not active")
+        if validate_layout and not h[base]:
+            from .paged_metadata import LAYOUT_MESSAGE
+            raise RuntimeError(LAYOUT_MESSAGE)
+
+
+@dataclass(frozen=True)
+class FusedFrontierStep:
+    """One frontier step of several requests: the union batch the model runs
+    (inputs and decode metadata of every route, request by request) and each
+    request's route range ``spans[i] = (first, end)`` in it."""
+
+    input_ids: torch.Tensor
+    metadata: SGLangRouteKVMetadata
+    route_ids: torch.Tensor
+    spans: tuple[tuple[int, int], ...]
+
+
+_ROUTE_FIELDS = 14  # int64 fields of one frontier route descriptor
+
+
+def fused_frontier_supported(bridges: Sequence[SGLangRoutePoolBridge]) -> bool:
+    """True when ``prepare_frontiers`` can run these bridges in one launch:
+    distinct bridges over one native paged allocator (device free list and
+    page ownership), one request-row pool with a dense int64 device table,
+    one KV pool with ``move_kv_cache``, one page size, page metadata on."""
+    if not bridges or len({id(b) for b in bridges}) != len(bridges):
+        return False
+    b0 = bridges[0]
+    alloc, req = b0.token_to_kv_pool_allocator, b0.req_to_token_pool
+    if not callable(getattr(alloc, "consume_pages", None)) or not callable(getattr(alloc, "get_kvcache", None)):
+        return False
+    if not callable(getattr(alloc.get_kvcache(), "move_kv_cache", None)):
+        return False
+    table = getattr(req, "req_to_token", None)
+    if not (isinstance(table, torch.Tensor) and table.ndim == 2 and table.dtype == torch.int64
+            and table.is_contiguous() and table.device == alloc.device):
+        return False
+    for b in bridges:
+        if b.token_to_kv_pool_allocator is not alloc or b.req_to_token_pool is not req:
+            return False
+        if int(b.page_size) != int(b0.page_size) or not b._device_ownership or not b.use_page_attention_metadata:
+            return False
+    return True
+
+
+def prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
+                      route_lists: Sequence[Sequence[RouteState]]) -> FusedFrontierStep:
+    """``prepare_frontier`` of several requests' bridges as one step: one
+    upload, one launch (copy-on-write page choice, decode slots, new slot
+    paths, request-row writes, page tables, owned pages, checks), and one KV
+    move for every copied tail.  Each bridge ends in the state, with the
+    counters and the deferred checks, that ``prepare_frontier`` on its own
+    routes leaves, taking pages from the shared free list in request order
+    (its copy-on-write pages, then its decode pages), as the per-request
+    calls in that order do.  The reference prepares one request per call
+    (``flashinfer_paged/sglang_runtime.py:800-959``)."""
+    if len(bridges) != len(route_lists) or not bridges:
+        raise ValueError("one route list per bridge is required")
+    if not fused_frontier_supported(bridges):
+        raise ValueError("prepare_frontiers needs distinct bridges over one set of native pools "
+                         "(see fused_frontier_supported)")
+    b0 = bridges[0]
+    alloc = b0.token_to_kv_pool_allocator
+    table = b0.req_to_token_pool.req_to_token
+    ps = int(b0.page_size)
+    device = alloc.device
+    plans = [b._plan_fused_frontier(rs) for b, rs in zip(bridges, route_lists)]
+
+    desc: list[int] = []
+    tokens: list[int] = []
+    route_ids: list[int] = []
+    seq_lens: list[int] = []
+    spans: list[tuple[int, int]] = []
+    flat_off = page_off = cow_off = free_idx = 0
+    for g, (b, plan) in enumerate(zip(bridges, plans)):
+        first = len(seq_lens)
+        n = len(plan.prevs)
+        bitmap = int(b.owned_page_ids.bitmap.data_ptr())
+        cow_base = free_idx
+        free_idx += plan.num_cow
+        for i in range(n):
+            prev = plan.prevs[i]
+            tail = plan.cow_tail[i]
+            if tail:
+                cow_free, cow_at = cow_base + plan.cow_rank[i], cow_off
+                cow_off += tail
+            else:
+                cow_free, cow_at = -1, 0
+            if prev % ps == 0:
+                new_free = free_idx
+                free_idx += 1
+            else:
+                new_free = -1
+            desc += (int(plan.paths[i].data_ptr()) if prev else 0, prev, tail, cow_free, cow_at, new_free,
+                     flat_off, page_off, plan.rows[i], plan.starts[i], bitmap, first, n, g)
+            flat_off += prev + 1
+            page_off += (prev + ps) // ps
+            seq_lens.append(prev + 1)
+        tokens += [int(r.pending_token_id) for r in plan.routes]
+        route_ids += [int(r.route_id) for r in plan.routes]
+        spans.append((first, first + n))
+    num_free = int(alloc.available_size()) // ps
+    if free_idx > num_free:
+        raise RuntimeError(f"SGLang KV pool cannot allocate {free_idx} pages for the frontier step "
+                           f"({num_free} free)")
+    R = len(seq_lens)
+    nb = len(bridges)
+    positions = [n - 1 for n in seq_lens]
+    rows = [r for plan in plans for r in plan.rows]
+    host = desc + [1] * (1 + 3 * nb) + tokens + seq_lens + positions + rows + route_ids
+    packed = torch.tensor(host, dtype=torch.int64, pin_memory=True).to(device, non_blocking=True)
+    o = _ROUTE_FIELDS * R
+    flags = packed[o : o + 1 + 3 * nb]
+    o += 1 + 3 * nb
+    input_ids, seq_dev, pos_dev, req_dev, rid_dev = (packed[o + k * R : o + (k + 1) * R] for k in range(5))
+
+    F, C, P = flat_off, cow_off, page_off
+    out64 = torch.empty(F + R + 2 * C, dtype=torch.int64, device=device)
+    out32 = torch.empty(3 * R + 1 + P, dtype=torch.int32, device=device)
+    flat, out_slots = out64[:F], out64[F : F + R]
+    cow_dst, cow_src = out64[F + R : F + R + C], out64[F + R + C :]
+    kv_indptr, kv_last = out32[: R + 1], out32[R + 1 : 2 * R + 1]
+    seq32, page_ids = out32[2 * R + 1 : 3 * R + 1], out32[3 * R + 1 :]
+    lib = _lib.load()
+    rc = lib.atlas_pool_prepare_frontier(
+        _lib.ptr(packed), R, ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps,
+        int(b0.owned_page_ids.num_pages), _lib.ptr(table), int(table.shape[0]), int(table.stride(0)),
+        _lib.ptr(flat), F, _lib.ptr(out_slots), _lib.ptr(cow_dst), _lib.ptr(cow_src), C,
+        _lib.ptr(kv_indptr), _lib.ptr(kv_last), _lib.ptr(seq32), _lib.ptr(page_ids), P,
+        _lib.ptr(flags), nb, _lib.stream_of(device),
+    )
+    _lib.check(rc, "atlas_pool_prepare_frontier")
+    if C:
+        alloc.get_kvcache().move_kv_cache(cow_dst, cow_src)
+    alloc.consume_pages(free_idx)
+
+    full = flat.split(seq_lens)
+    step_flags = _StepFlags(flags)
+    for g, (b, plan) in enumerate(zip(bridges, plans)):
+        lo, hi = spans[g]
+        b._finish_fused_frontier(plan, full[lo:hi], step_flags, g)
+    meta = SGLangRouteKVMetadata(
+        req_pool_indices=req_dev, seq_lens=seq_dev, out_cache_loc=out_slots, positions=pos_dev,
+        orig_seq_lens=seq_dev, seq_lens_sum=F, seq_lens_cpu=torch.tensor(seq_lens, dtype=torch.long),
+        attention_page_size=ps, token_index_count=F, page_index_count=P,
+        paged_decode_spec=AtlasPagedDecodeSpec(kv_indptr, page_ids, kv_last, ps),
+    )
+    return FusedFrontierStep(input_ids, meta, rid_dev, tuple(spans))
+
+
 class SGLangFlashInferFrontierModelBackend:
     """Drafter frontier backend over the route pool
     (``sglang_runtime.py:1120-1346``).
@@ -1127,10 +1395,18 @@ class SGLangFlashInferFrontierModelBackend:
         input_ids, metadata = self.route_pool.prepare_frontier(active_routes)
         logits = self.executor.forward_frontier(input_ids=input_ids, route_kv_metadata=metadata)
         self.route_pool.register_node_slots(new_nodes, metadata.out_cache_loc)
+        ids = [int(r.route_id) for r in active_routes]
+        on_device = input_ids.device.type != "cpu"
+        route_ids = torch.tensor(ids, dtype=torch.long, pin_memory=on_device).to(input_ids.device,
+                                                                                 non_blocking=True)
+        return self._frontier_output(route_ids, logits, new_nodes, start, before, metadata.attention_page_size,
+                                     metadata.token_index_count, metadata.page_index_count, attention_backend)
+
+    def _frontier_output(self, route_ids, logits, new_nodes, start, before, page_size, token_indices,
+                         page_indices, attention_backend) -> FrontierDecodeOutput:
         after = self.route_pool.hot_path_counters()
         return FrontierDecodeOutput(
-            route_ids=torch.tensor([int(r.route_id) for r in active_routes], dtype=torch.long,
-                                   device=input_ids.device),
+            route_ids=route_ids,
             next_token_logits=logits, new_node_ids=tuple(new_nodes), new_node_ids_cpu=tuple(new_nodes),
             model_ms=(time.perf_counter() - start) * 1000.0,
             metadata={
@@ -1139,14 +1415,48 @@ class SGLangFlashInferFrontierModelBackend:
                 "route_tail_page_cow": True,
                 "cow_pages_copied_total": int(self.route_pool.cow_pages_copied),
                 "cow_tokens_copied_total": int(self.route_pool.cow_tokens_copied),
-                "attention_metadata_page_size": int(metadata.attention_page_size),
-                "attention_metadata_token_indices_step": int(metadata.token_index_count),
-                "attention_metadata_page_indices_step": int(metadata.page_index_count),
+                "attention_metadata_page_size": int(page_size),
+                "attention_metadata_token_indices_step": int(token_indices),
+                "attention_metadata_page_indices_step": int(page_indices),
                 "hot_path_counter_delta": {k: int(after[k] - before.get(k, 0)) for k in after},
                 "hot_path_counters_total": after,
                 "attention_backend": str(attention_backend),
             },
         )
+
+    @staticmethod
+    @torch.inference_mode()
+    def decode_frontiers(backends: Sequence["SGLangFlashInferFrontierModelBackend"],
+                         route_lists: Sequence[Sequence[RouteState]], *, executor: Any = None,
+                         attention_backend: object = None) -> list[FrontierDecodeOutput]:
+        """``decode_frontier_one_token`` of several requests as one step:
+        when their bridges share native pools, one ``prepare_frontiers`` and
+        ONE ``forward_frontier`` of the union batch (``executor``, default the
+        first backend's), whose logits rows and decode slots are handed back
+        request by request; otherwise one call per request.  Each request's
+        output and bridge state equal its own call's."""
+        if len(backends) != len(route_lists):
+            raise ValueError("one route list per backend is required")
+        bridges = [b.route_pool for b in backends]
+        if not fused_frontier_supported(bridges):
+            return [b.decode_frontier_one_token(rs, attention_backend) for b, rs in zip(backends, route_lists)]
+        start = time.perf_counter()
+        before = [b.hot_path_counters() for b in bridges]
+        new_nodes = [b.route_store.reserve_node_ids(len(rs)) for b, rs in zip(backends, route_lists)]
+        step = prepare_frontiers(bridges, route_lists)
+        ex = executor if executor is not None else backends[0].executor
+        logits = ex.forward_frontier(input_ids=step.input_ids, route_kv_metadata=step.metadata)
+        out_slots = step.metadata.out_cache_loc
+        outputs = []
+        for i, b in enumerate(backends):
+            lo, hi = step.spans[i]
+            b.route_pool.register_node_slots(new_nodes[i], out_slots[lo:hi])
+            ps = int(b.route_pool.page_size)
+            prevs = [int(x) - 1 for x in step.metadata.seq_lens_cpu[lo:hi].tolist()]
+            outputs.append(b._frontier_output(
+                step.route_ids[lo:hi], logits[lo:hi], new_nodes[i], start, before[i], ps,
+                sum(prevs) + len(prevs), sum((p + ps) // ps for p in prevs), attention_backend))
+        return outputs
 
 
 _COUNTERS = (

@@ -75,6 +75,15 @@ def _layer_ptrs(layers: Sequence[torch.Tensor], v_offset: int | None = None):
     return k, v
 
 
+def _layer_tables(k_layers: Sequence[torch.Tensor], v_layers: Sequence[torch.Tensor]):
+    """(K pointer table, V pointer table, slot geometry) of a flat token pool."""
+    if len(k_layers) != len(v_layers) or not k_layers:
+        raise ValueError("k_layers and v_layers must be non-empty and of equal length")
+    return (_lib.ptr_array([int(t.data_ptr()) for t in k_layers]),
+            _lib.ptr_array([int(t.data_ptr()) for t in v_layers]),
+            token_pool_geometry(k_layers[0]))
+
+
 def _as_long(t: torch.Tensor, device: torch.device) -> torch.Tensor:
     if t.device != device or t.dtype != torch.int64 or not t.is_contiguous():
         t = t.to(device=device, dtype=torch.int64).contiguous()
@@ -86,13 +95,16 @@ def move_slots(
     v_layers: Sequence[torch.Tensor],
     dst_slots: torch.Tensor,
     src_slots: torch.Tensor,
+    *,
+    layer_tables: tuple | None = None,
 ) -> None:
     """``K[dst] = K[src]; V[dst] = V[src]`` for every layer of a flat token pool.
 
     The SGLang ``move_kv_cache(tgt_loc, src_loc)`` contract used by the
     reference's tail-page copy-on-write
     (``flashinfer_paged/sglang_runtime.py:686-695``); ``dst`` and ``src`` must
-    be disjoint.
+    be disjoint. ``layer_tables`` = ``(k_ptrs, v_ptrs, geometry)`` built once
+    by a pool whose layer buffers never move (skips rebuilding them per call).
     """
     if len(k_layers) != len(v_layers) or not k_layers:
         raise ValueError("k_layers and v_layers must be non-empty and of equal length")
@@ -102,14 +114,14 @@ def move_slots(
         raise ValueError("move_kv_cache needs as many source as destination slots")
     if n == 0:
         return
-    geom = token_pool_geometry(k_layers[0])
     dst = _as_long(dst_slots.reshape(-1), device)
     src = _as_long(src_slots.reshape(-1), device)
-    k_ptrs = [int(t.data_ptr()) for t in k_layers]
-    v_ptrs = [int(t.data_ptr()) for t in v_layers]
+    if layer_tables is None:
+        layer_tables = _layer_tables(k_layers, v_layers)
+    k_tab, v_tab, geom = layer_tables
     lib = _lib.load()
     rc = lib.atlas_kv_move_slots(
-        _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs), len(k_ptrs), *geom.as_args(),
+        k_tab, v_tab, len(k_layers), *geom.as_args(),
         _lib.ptr(dst), _lib.ptr(src), n, _lib.stream_of(device),
     )
     _lib.check(rc, "atlas_kv_move_slots")
@@ -121,26 +133,33 @@ def append_token_pool(
     k_src: Sequence[torch.Tensor],
     v_src: Sequence[torch.Tensor],
     dst_slots: torch.Tensor,
+    *,
+    layer_tables: tuple | None = None,
 ) -> None:
     """Scatter dense rows ``[n, Hkv, D]`` into slots of every layer of a flat pool
-    (SGLang ``set_kv_buffer``, ``sglang_page_attention.py:187-194``)."""
+    (SGLang ``set_kv_buffer``, ``sglang_page_attention.py:187-194``).
+    ``layer_tables`` as for :func:`move_slots`."""
     device = _lib.require_device(k_layers[0], dst_slots, k_src[0], what="set_kv_buffer")
     n = int(dst_slots.numel())
     if n == 0:
         return
-    geom = token_pool_geometry(k_layers[0])
+    if len(k_src) != len(k_layers) or len(v_src) != len(v_layers):
+        raise ValueError("one K and one V source per layer are required")
+    if layer_tables is None:
+        layer_tables = _layer_tables(k_layers, v_layers)
+    k_tab, v_tab, geom = layer_tables
+    src_stride = k_src[0].stride(0) * k_src[0].element_size()
     for t in (*k_src, *v_src):
         if t.dtype != k_layers[0].dtype:
             raise TypeError(f"source dtype {t.dtype} does not match the pool dtype {k_layers[0].dtype}")
         if int(t.shape[0]) < n or not rows_contiguous(t):
             raise ValueError("source rows must be [n, Hkv, D] with contiguous (Hkv, D)")
-    src_stride = k_src[0].stride(0) * k_src[0].element_size()
+        if t.stride(0) * t.element_size() != src_stride:
+            raise ValueError("every K/V source must share one row stride")
     dst = _as_long(dst_slots.reshape(-1), device)
     lib = _lib.load()
     rc = lib.atlas_kv_append(
-        _lib.ptr_array([int(t.data_ptr()) for t in k_layers]),
-        _lib.ptr_array([int(t.data_ptr()) for t in v_layers]),
-        len(k_layers), *geom.as_args(),
+        k_tab, v_tab, len(k_layers), *geom.as_args(),
         _lib.ptr_array([int(t.data_ptr()) for t in k_src]),
         _lib.ptr_array([int(t.data_ptr()) for t in v_src]),
         src_stride, _lib.ptr(dst), 0, n, _lib.stream_of(device),

@@ -809,15 +809,17 @@ def frontier_leg(dev, *, rows=72, vocab=128256, k=3, iters=20):
             "depth_call_us": round(call_us, 1), "torch_sequence_us": round(torch_us, 1)}
 
 
-def drafter_leg(dev, *, requests=8, repeats=3):
+def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
     """Drafter route-pool fork stress (Llama-3.2-1B KV geometry, bf16, page
     64): 8 requests, each forking to 9 routes at random fill levels of its
     partial tail page, 8 decode steps, commit + promote of 3 routes, prune,
     one 4-token fallback EXTEND and a decode step after it -- the route-pool
     bridge driving the native pools (device page ownership, batched
     copy-on-write, device slot allocation and page metadata).  The model is
-    replaced by one all-layer K/V append per step.  Wall time per phase, GPU
-    synchronised at each phase end."""
+    replaced by one all-layer K/V append per forward.  ``batched``: each
+    decode step of the 8 requests is one fused frontier step (one launch for
+    all 72 routes, one forward); else one bridge call per request.  Wall time
+    per phase, GPU synchronised at each phase end."""
     dw = _pkg("drafter_workload")
     npool = _pkg("flashinfer_paged.native_pool")
     geom = _pkg("workloads").LLAMA_1B
@@ -834,7 +836,7 @@ def drafter_leg(dev, *, requests=8, repeats=3):
             kv.set_kv_buffer_all_layers(slots, [rows[:n]] * geom.layers, [rows[:n]] * geom.layers)
 
         work = dw.DrafterForkWorkload(plans=dw.config5_plans(requests, ps, rep), req_pool=req_pool, allocator=alloc,
-                                      page_size=ps, device=dev, writer=writer)
+                                      page_size=ps, device=dev, writer=writer, batched=batched)
         marks = []
 
         def on_phase(name, marks=marks):
@@ -860,6 +862,7 @@ def drafter_leg(dev, *, requests=8, repeats=3):
         "fallback_extend_us": round(statistics.median(sp["extend"] for sp, _, _ in runs), 1),
         "prefill_us": round(statistics.median(sp["prefill"] for sp, _, _ in runs), 1),
         "cow_pages_copied": runs[-1][1], "cow_tokens_copied": runs[-1][2],
+        "batched_frontier_step": bool(batched),
         "note": "wall time of the host-driven bridge per phase (all 8 requests), model replaced by a K/V append",
     }
 
@@ -1094,6 +1097,7 @@ def main():
         result["components"]["drafter_decode_attn"] = decode_leg(dev)
         result["components"]["drafter_decode_attn_8k"] = decode_leg(dev, prefix_len=8192)
         result["components"]["drafter_fork_8req"] = drafter_leg(dev)
+        result["components"]["drafter_fork_8req_per_request_calls"] = drafter_leg(dev, batched=False)
         result["components"]["drafter_frontier_depth"] = frontier_leg(dev)
         result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
         result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)

@@ -324,6 +324,64 @@ int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_d
                          int32_t* layout_ok_dev, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Frontier step of many requests in one launch.
+ * ---------------------------------------------------------------------- */
+
+/* One active route of a frontier step (every field is 8 bytes).  The route's
+ * new slot path is its current path with, when cow_tail > 0, the last
+ * cow_tail slots replaced by the first slots of a fresh page (copy-on-write),
+ * followed by its decode slot. */
+typedef struct {
+  const int64_t* path;    /* current slot path, prev_len int64 slots */
+  int64_t prev_len;
+  int64_t cow_tail;       /* 0, or 1 .. page_size-1 slots moved to a fresh page */
+  int64_t cow_free_index; /* that page is free_pages[cow_free_index] */
+  int64_t cow_offset;     /* its (dst, src) slot pairs go to cow_dst/cow_src[cow_offset ..] */
+  int64_t new_free_index; /* >= 0: the decode slot opens page free_pages[new_free_index]
+                             (required exactly when prev_len % page_size == 0);
+                             < 0: it is the new path's last slot + 1 */
+  int64_t flat_offset;    /* new path (prev_len + 1 slots) -> flat[flat_offset ..] */
+  int64_t page_offset;    /* its page ids -> kv_page_indices[page_offset ..] (the
+                             running sum of the earlier routes' page counts) */
+  int64_t req_row;        /* request row that receives ... */
+  int64_t write_start;    /* ... new path positions write_start .. prev_len */
+  uint32_t* owned_bitmap; /* owned-page bitmap of the route's request (NULL: none) */
+  int64_t group_first;    /* routes of the same request: group_first .. +group_count-1 */
+  int64_t group_count;
+  int64_t flag_index;     /* that request's check flags: flags[1 + 3*flag_index + k] */
+} atlas_pool_frontier_route_t;
+
+/* The device half of SGLangRoutePoolBridge.prepare_frontier for the routes of
+ * many requests that share one paged allocator, request-row pool and KV pool
+ * (src/atlas_0709/flashinfer_paged/sglang_runtime.py:800-959 per request,
+ * with allocate_decode_slots :636-659, the copy-on-write page choice of
+ * _copy_partial_tail_pages_with_dirty_starts :708-798, the request-row
+ * writes of _write_req_token_slice :1031-1092 and the page tables of
+ * paged_metadata.py:64-102).  routes_dev holds num_routes descriptors, in
+ * device memory.  Per route r it writes
+ *   flat[flat_offset ..]      the new slot path,
+ *   out_slots[r]              its decode slot,
+ *   req_to_token[req_row * req_row_stride + p], p = write_start .. prev_len,
+ *   kv_indptr[r + 1], kv_last_page_len[r], seq_lens[r] (kv_indptr[0] = 0),
+ *   kv_page_indices[page_offset ..]  page id of each page of the new path,
+ *   cow_dst/cow_src[cow_offset ..]   the slot pairs of its copy-on-write,
+ * and sets the owned bits of its decode page and copy-on-write page.
+ * Checks clear flags (which the caller sets to 1 before the call):
+ * flags[0] when a descriptor is out of range (the route is then skipped);
+ * per request, flags[1 + 3f] when a page of a new path is not page-aligned
+ * and contiguous, flags[2 + 3f] when two of its routes get one decode slot,
+ * flags[3 + 3f] when a copy-on-write page is one of its copy sources.  The
+ * KV bytes of the copied slots are not moved here (atlas_kv_move_slots). */
+int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, int num_routes,
+                           const int64_t* free_pages_dev, int64_t num_free, int64_t page_size,
+                           int64_t num_pages, int64_t* req_to_token_dev, int64_t req_rows,
+                           int64_t req_row_stride, int64_t* flat_dev, int64_t flat_total,
+                           int64_t* out_slots_dev, int64_t* cow_dst_dev, int64_t* cow_src_dev,
+                           int64_t cow_total, int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev,
+                           int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
+                           int64_t* flags_dev, int64_t num_flag_groups, void* stream);
+
+/* ------------------------------------------------------------------------
  * Route scoring.
  * ---------------------------------------------------------------------- */
 

@@ -16,9 +16,11 @@ from oracle.scoring import select_best
 pytestmark = pytest.mark.gpu
 
 
-def _device_run(plans, *, page_size, num_pages, layers, heads, head_dim, dev, host_phases):
+def _device_run(plans, *, page_size, num_pages, layers, heads, head_dim, dev, host_phases, batched=False):
     """Runs the trace on the native pools; after each phase compares the
-    bookkeeping and the live slots' K/V bytes with the host run's phase."""
+    bookkeeping and the live slots' K/V bytes with the host run's phase.
+    ``batched``: every decode step of all requests is one fused frontier step
+    (one launch for the requests' slot paths, rows and page tables)."""
     dw = pkg("drafter_workload")
     npool = pkg("flashinfer_paged.native_pool")
     req, kv, alloc = npool.create_native_pools(num_pages=num_pages, page_size=page_size, dtype=torch.bfloat16,
@@ -32,7 +34,7 @@ def _device_run(plans, *, page_size, num_pages, layers, heads, head_dim, dev, ho
         kv.set_kv_buffer_all_layers(slots, k_rows, v_rows)
 
     wl = dw.DrafterForkWorkload(plans=plans, req_pool=req, allocator=alloc, page_size=page_size, device=dev,
-                                writer=writer)
+                                writer=writer, batched=batched)
     seen = []
 
     def compare(phase):
@@ -129,19 +131,26 @@ def _check_kv(kv, values, slots, layers, heads, head_dim, dev, phase):
                                         f"{s[bad][:8].tolist()}"
 
 
-@pytest.mark.parametrize("case", ["config1", "config5_seed0", "config5_seed1"])
+@pytest.mark.parametrize("case", ["config1", "config5_seed0", "config5_seed1", "config1_batched",
+                                  "config5_seed0_batched", "config5_seed1_batched", "config5_seed2_batched"])
 def test_route_pool_trace_matches_host_pools(dev, case):
+    """The ``_batched`` cases run each decode step of all requests as one
+    fused frontier step against the same per-request host trace."""
     dw = pkg("drafter_workload")
-    if case == "config1":
+    batched = case.endswith("_batched")
+    name = case.removesuffix("_batched")
+    if name == "config1":
         plans, ps, pages = dw.config1_plans(0), 16, 4096
     else:
-        plans, ps, pages = dw.config5_plans(8, 64, int(case[-1])), 64, 640
+        plans, ps, pages = dw.config5_plans(8, 64, int(name[-1])), 64, 640
     layers, heads, head_dim = 16, 8, 64
     print(f"route-pool trace {case}: page_size {ps}, {pages} pages", flush=True)
     host = []
     hw = _host_run(plans, page_size=ps, num_pages=pages, phases=host)
     dw_run = _device_run(plans, page_size=ps, num_pages=pages, layers=layers, heads=heads, head_dim=head_dim,
-                         dev=dev, host_phases=host)
+                         dev=dev, host_phases=host, batched=batched)
+    if batched:
+        assert all(r.bridge.attention_metadata_builds > 0 for r in dw_run.requests)
     assert [r.selected_route_id for r in dw_run.requests] == [r.selected_route_id for r in hw.requests]
     if case == "config1":
         # the committed route is the best by (sum of node log-probs, draft
@@ -203,3 +212,87 @@ def test_frontier_page_metadata_matches_oracle(dev):
         assert spec.kv_indices.tolist() == exp.kv_page_indices
         assert spec.kv_last_page_len.tolist() == exp.kv_last_page_len
         assert md.seq_lens_cpu.tolist() == exp.seq_lens
+
+
+def test_fused_frontier_metadata_matches_oracle(dev):
+    """The union batch of a fused frontier step (4 requests): page tables
+    equal the oracle's paged metadata of all routes' new slot paths in request
+    order; input ids, sequence lengths, positions, request rows and decode
+    slots match each route's state."""
+    from oracle import paged_kv as ref
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    req, kv, alloc = npool.create_native_pools(num_pages=640, page_size=64, dtype=torch.bfloat16, head_num=8,
+                                               head_dim=64, layer_num=2, max_running_requests=128,
+                                               max_context_len=4096, device=dev)
+
+    def writer(slots, vids):
+        rows = [torch.zeros((int(slots.numel()), 8, 64), dtype=torch.bfloat16, device=dev)] * 2
+        kv.set_kv_buffer_all_layers(slots, rows, rows)
+
+    wl = dw.DrafterForkWorkload(plans=dw.config5_plans(4, 64, 5), req_pool=req, allocator=alloc, page_size=64,
+                                device=dev, writer=writer, batched=True)
+    ex = wl.requests[0].backend.executor
+    orig = ex.forward_frontier
+    steps = []
+
+    def spy(*, input_ids, route_kv_metadata):
+        md = route_kv_metadata
+        routes = [(q, r) for q in wl.requests for r in q.active]
+        assert int(md.out_cache_loc.numel()) == len(routes), "every request takes part in each step"
+        paths = [q.bridge.route_slot_paths[int(r.route_id)].tolist() for q, r in routes]
+        rows = [q.bridge.route_rows[int(r.route_id)].req_pool_index for q, r in routes]
+        tokens = [int(r.pending_token_id) for _, r in routes]
+        steps.append((md, input_ids.tolist(), paths, rows, tokens))
+        return orig(input_ids=input_ids, route_kv_metadata=route_kv_metadata)
+
+    ex.forward_frontier = spy
+    wl.run()
+    assert len(steps) == 10  # 8 stage-1 steps, one after the commit, one after the EXTEND
+    for md, ids, paths, rows, tokens in steps:
+        exp = ref.paged_metadata(paths, 64)
+        spec = md.paged_decode_spec
+        assert spec.kv_indptr.tolist() == exp.kv_indptr
+        assert spec.kv_indices.tolist() == exp.kv_page_indices
+        assert spec.kv_last_page_len.tolist() == exp.kv_last_page_len
+        assert md.seq_lens_cpu.tolist() == exp.seq_lens == md.seq_lens.tolist()
+        assert md.positions.tolist() == [n - 1 for n in exp.seq_lens]
+        assert md.out_cache_loc.tolist() == [p[-1] for p in paths]
+        assert md.req_pool_indices.tolist() == rows and ids == tokens
+        assert md.seq_lens_sum == sum(exp.seq_lens) and md.page_index_count == len(exp.kv_page_indices)
+
+
+def test_fused_frontier_rejects_out_of_range_descriptors(dev):
+    """A route descriptor whose request row lies outside the row table is
+    skipped by the kernel's own range checks and reported in flag 0; the
+    in-range route of the same launch is written."""
+    import ctypes
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    ps = 16
+    path = torch.arange(32, 37, dtype=torch.int64, device=dev)  # 5 slots on page 2
+    table = torch.zeros((4, 64), dtype=torch.int64, device=dev)
+    free = torch.tensor([7, 8], dtype=torch.int64, device=dev)
+    bitmap = torch.zeros(1, dtype=torch.int32, device=dev)
+    desc = []
+    for row in (1, 9):  # 9 is outside the 4-row table
+        desc += [path.data_ptr(), 5, 0, -1, 0, -1, 0 if row == 1 else 6, 0 if row == 1 else 1, row, 0,
+                 bitmap.data_ptr(), 0, 2, 0]
+    d = torch.tensor(desc, dtype=torch.int64, device=dev)
+    flags = torch.ones(4, dtype=torch.int64, device=dev)
+    flat = torch.full((12,), -5, dtype=torch.int64, device=dev)
+    out = torch.full((2,), -5, dtype=torch.int64, device=dev)
+    i32 = torch.full((3 * 2 + 1 + 2,), -5, dtype=torch.int32, device=dev)
+    print("fused frontier: out-of-range descriptor", flush=True)
+    rc = lib.atlas_pool_prepare_frontier(
+        lib_mod.ptr(d), 2, lib_mod.ptr(free), 2, ps, 32, lib_mod.ptr(table), 4, 64, lib_mod.ptr(flat), 12,
+        lib_mod.ptr(out), None, None, 0, lib_mod.ptr(i32[:3]), lib_mod.ptr(i32[3:5]), lib_mod.ptr(i32[5:7]),
+        lib_mod.ptr(i32[7:]), 2, lib_mod.ptr(flags), 1, lib_mod.stream_of(dev))
+    lib_mod.check(rc, "atlas_pool_prepare_frontier")
+    torch.cuda.synchronize()
+    assert flags.tolist() == [0, 1, 1, 1]
+    assert flat[:6].tolist() == [32, 33, 34, 35, 36, 37] and flat[6:].tolist() == [-5] * 6
+    assert out.tolist() == [37, -5]
+    assert table[1, :6].tolist() == [32, 33, 34, 35, 36, 37] and int(table[2:].abs().sum()) == 0
+    assert i32[:2].tolist() == [0, 1] and i32[3].item() == 6 and i32[5].item() == 6 and i32[7].item() == 2
+    assert bitmap.item() == 1 << 2
