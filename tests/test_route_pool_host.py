@@ -551,3 +551,57 @@ def test_cow_rejects_destination_pages_that_overlap_sources():
     with pytest.raises(RuntimeError, match="overlap"):
         b._copy_partial_tail_pages(ids(1, 2), [tail, tail])
     assert b.token_to_kv_pool_allocator.kv_cache.moves == []
+
+
+def test_fused_frontier_step_needs_native_pools():
+    """The one-launch frontier step of many requests applies only to
+    distinct bridges over one set of native pools; host pools (and a bridge
+    given twice) keep the per-request calls."""
+    sr, _ = _mods()
+    b = sr.SGLangRoutePoolBridge(req_to_token_pool=RowTable(), token_to_kv_pool_allocator=MonotoneAllocator(4),
+                                 page_size=4, device="cpu")
+    assert not sr.fused_frontier_supported([b])
+    assert not sr.fused_frontier_supported([])
+    with pytest.raises(ValueError, match="native pools"):
+        sr.prepare_frontiers([b], [ids(1)])
+
+
+def test_fused_step_flags_raise_in_prepare_frontier_order():
+    """Check flags of a fused step: a skipped descriptor first, then per
+    request the copy-on-write overlap, duplicate decode slots and page layout
+    checks, in the order prepare_frontier records them."""
+    sr, _ = _mods()
+    pm = pkg("flashinfer_paged.paged_metadata")
+    cases = [
+        ([0, 1, 1, 1], "out of range"),
+        ([1, 0, 0, 0], "overlap"),
+        ([1, 0, 0, 1], "duplicate output KV slots"),
+        ([1, 0, 1, 1], pm.LAYOUT_MESSAGE[:40]),
+    ]
+    for host, message in cases:
+        flags = sr._StepFlags(torch.tensor(host + [1, 1, 1], dtype=torch.int64))
+        with pytest.raises(RuntimeError, match=message):
+            flags.check(0, True)
+        if host[0]:
+            flags.check(1, True)  # the other request's flags are clear
+    sr._StepFlags(torch.tensor([1, 0, 1, 1], dtype=torch.int64)).check(0, False)  # layout not validated
+
+
+def test_batched_workload_on_host_pools_equals_per_request_calls():
+    """On host pools the batched drafter workload falls back to one bridge
+    call per request and leaves the same state."""
+    dw = pkg("drafter_workload")
+    from oracle.route_pool import OracleAllocator, OracleReqPool
+
+    def run(batched):
+        alloc = OracleAllocator(num_pages=640, page_size=64)
+        rows = OracleReqPool(size=128, max_context_len=4096)
+        wl = dw.DrafterForkWorkload(plans=dw.config5_plans(3, 64, 4), req_pool=rows, allocator=alloc, page_size=64,
+                                    device="cpu", writer=lambda s, v: alloc.kv.write(s.numpy(), v.numpy()),
+                                    use_page_attention_metadata=False, batched=batched)
+        wl.run()
+        return (list(alloc.free_pages), alloc.kv.values.tolist(),
+                [{r: p.tolist() for r, p in q.bridge.route_slot_paths.items()} for q in wl.requests],
+                [q.bridge.hot_path_counters() for q in wl.requests])
+
+    assert run(True) == run(False)
