@@ -353,13 +353,16 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
       cow_dst[d.cow_offset + t] = cow_page * ps + t;
       cow_src[d.cow_offset + t] = d.path[cut + t];
     }
+    // One thread per (route of the request, tail slot), so every descriptor
+    // and tail load is in flight at once.
     bool disjoint = true;
-    for (int64_t s = d.group_first; s < d.group_first + d.group_count; ++s) {
+    const int64_t slots_per_route = ps;  // a tail holds fewer than page_size slots
+    for (int64_t i = tid; i < d.group_count * slots_per_route; i += kFrontierThreads) {
+      const int64_t s = d.group_first + i / slots_per_route;
+      const int64_t t = i % slots_per_route;
       const atlas_pool_frontier_route_t e = routes[s];
-      if (e.cow_tail == 0 || !frontier_route_ok(e, L)) continue;
-      const int64_t ecut = e.prev_len - e.cow_tail;
-      for (int64_t t = tid; t < e.cow_tail; t += kFrontierThreads)
-        if (floor_div(e.path[ecut + t], ps) == cow_page) disjoint = false;
+      if (t >= e.cow_tail || !frontier_route_ok(e, L)) continue;
+      if (floor_div(e.path[e.prev_len - e.cow_tail + t], ps) == cow_page) disjoint = false;
     }
     if (!disjoint) fl[2] = 0;
   }

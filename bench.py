@@ -291,7 +291,7 @@ def _mean_ms(pairs):
     return statistics.fmean(a.elapsed_time(b) for a, b in pairs) if pairs else float("nan")
 
 
-def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
+def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, profile_launches=0):
     """Batched Target verify: 32 requests, Llama-3.1-8B KV geometry, bf16,
     page 16, prefixes uniform in [1024, 16384], pages scattered over a pool of
     about ``pool_gb`` GB (32 layers x pages x 64 KiB).  Each request has a
@@ -350,24 +350,26 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
         for l in range(layers_timed):
             w.run(q[l], layers[l], out=outs[l])
 
-    fwd()
     side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        fwd()
-    torch.cuda.current_stream().wait_stream(side)
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        fwd()
-    graph.replay()
-    torch.cuda.synchronize()
     a, b = _ev(), _ev()
-    a.record()
-    for _ in range(iters):
+    if not profile_launches:
+        fwd()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            fwd()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fwd()
         graph.replay()
-    b.record()
-    torch.cuda.synchronize()
-    attn_us = a.elapsed_time(b) * 1000.0 / (iters * layers_timed)
+        torch.cuda.synchronize()
+        print("batched leg: pool and plans ready", file=sys.stderr, flush=True)
+        a.record()
+        for _ in range(iters):
+            graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        attn_us = a.elapsed_time(b) * 1000.0 / (iters * layers_timed)
     attn_bytes = sum(wl.verify_attention_bytes(geom, kv_len=k, nodes=n, page_size=ps) for k, n in zip(kv_lens, nodes))
 
     # commit: the selected route of every request (dedup node ids)
@@ -383,9 +385,20 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
                 item_req=torch.tensor(item_req, dtype=torch.int32, device=dev))
     src_t = torch.tensor(src, device=dev)
     dst_t = torch.tensor(dst, device=dev)
+    if profile_launches:
+        # eager commit launches for counter runs, each on its own page table
+        # (the same positions on other physical pages), so every copy is cold
+        for k in range(profile_launches):
+            kv_idx = torch.randperm(pool_pages, generator=gen)[:need_pages].to(torch.int32).to(dev)
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **dict(args, kv_indices=kv_idx))
+            torch.cuda.synchronize()
+            print(f"batched leg: commit launch {k} done", file=sys.stderr, flush=True)
+        return {"profile_launches": profile_launches, "items": len(src), "moved_bytes":
+                len(src) * geom.layers * geom.token_bytes()}
     for _ in range(5):
         kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
     torch.cuda.synchronize()
+    print("batched leg: attention timed", file=sys.stderr, flush=True)
     a.record()
     for _ in range(50):
         kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
@@ -415,6 +428,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
     cgraph.replay()
     hgraph.replay()
     torch.cuda.synchronize()
+    print("batched leg: commit instances ready", file=sys.stderr, flush=True)
     a.record()
     for _ in range(5):
         cgraph.replay()
@@ -426,6 +440,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5):
         hgraph.replay()
     b.record()
     torch.cuda.synchronize()
+    print("batched leg: commit timed", file=sys.stderr, flush=True)
     hot_commit_us = a.elapsed_time(b) * 1000.0 / 100
     moved = len(src) * geom.layers * geom.token_bytes()
     floors = commit_floors(dev, layers, inst_args, item_req, src, dst, moved, ps, side, lib)
@@ -537,7 +552,7 @@ def commit_floors(dev, layers, inst_args, item_req, src, dst, moved, ps, side, l
     return out
 
 
-def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
+def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8, profile_launches=0):
     """Drafter tail-page copy-on-write: per request, 9 forked routes share a
     partially filled 64-token tail page; 8 of them get private copies, all in
     one move launch (Llama-3.2-1B KV geometry, bf16, flat token pool).
@@ -577,6 +592,16 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
     for d_t, s_t in sets:
         kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
     torch.cuda.synchronize()
+    print("cow leg: instances ready", file=sys.stderr, flush=True)
+    if profile_launches:
+        # eager launches in rotation over the instances, for counter runs
+        for i in range(profile_launches):
+            d_t, s_t = sets[i % instances]
+            kv_ops.move_slots(k_layers, v_layers, d_t, s_t)
+            torch.cuda.synchronize()
+            print(f"cow leg: move launch {i} done", file=sys.stderr, flush=True)
+        return {"profile_launches": profile_launches, "slots": slots,
+                "moved_bytes": slots * geom.layers * geom.token_bytes()}
     a, b = _ev(), _ev()
     # Per eager call: host work between launches included.
     a.record()
@@ -611,6 +636,7 @@ def cow_leg(dev, *, requests=8, routes=9, iters=50, instances=8):
         graph.replay()
     b.record()
     torch.cuda.synchronize()
+    print("cow leg: graph timed", file=sys.stderr, flush=True)
     us = a.elapsed_time(b) * 1000.0 / (3 * rounds * instances)
     a.record()
     for _ in range(3):
@@ -996,11 +1022,16 @@ def main():
     ap.add_argument("--cpu-baseline-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-legs", action="store_true")
+    ap.add_argument("--legs", default="all", metavar="NAMES",
+                    help="comma-separated component legs to run (config2, tree16k, batched, cow, decode, decode8k, "
+                         "drafter, drafter_calls, frontier), default all")
     ap.add_argument("--split-target", type=int, default=None)
     ap.add_argument("--max-rows", type=int, default=None)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run device-to-device copies of MIB MiB (calibrates HBM byte counters)")
     ap.add_argument("--commit-pool-gb", type=float, default=200.0)
+    ap.add_argument("--profile-kv", type=int, default=0, metavar="N",
+                    help="run N eager launches of the batched commit and of the copy-on-write move, then exit")
     ap.add_argument("--profile-attention", type=int, default=0, metavar="N",
                     help="only plan the headline step and run N eager attention launches (one per layer, "
                          "printing after each), for counter collection")
@@ -1010,10 +1041,20 @@ def main():
                                    "and has no multi-GPU leg", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
-    step = HeadlineStep(dev, split_target=args.split_target, max_rows=args.max_rows)
-    if args.profile_attention:
-        profile_attention(step, args.profile_attention)
+    if args.profile_kv:
+        # the commit and copy-on-write launches alone, eagerly, for counter
+        # runs (after a copy of known size that calibrates the counters)
+        if args.copy_calibration:
+            src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(3):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            del src, dst
+        print(json.dumps({"commit": batched_leg(dev, pool_gb=args.commit_pool_gb, profile_launches=args.profile_kv),
+                          "cow": cow_leg(dev, profile_launches=args.profile_kv)}))
         return
+    step = HeadlineStep(dev, split_target=args.split_target, max_rows=args.max_rows)
     if args.copy_calibration:
         src = torch.ones(args.copy_calibration << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)
@@ -1021,10 +1062,15 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.profile_attention:
+        profile_attention(step, args.profile_attention)
+        return
     step.capture()
+    print("headline: graphs captured", file=sys.stderr, flush=True)
     for _ in range(args.warmup):
         step.step()
     torch.cuda.synchronize()
+    print("headline: warmup done", file=sys.stderr, flush=True)
     step.record = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -1033,6 +1079,7 @@ def main():
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     ms_per_step = wall * 1000.0 / args.steps
+    print("headline: timed steps done", file=sys.stderr, flush=True)
     attn_ms = step.attention_only(max(10, args.steps))
     attn_us = attn_ms * 1000.0
     wl = _pkg("workloads")
@@ -1086,21 +1133,33 @@ def main():
     result["components"]["tree_tokens_per_s_attention"] = round(step.n / (attn_us * 1e-6 * step.geom.layers), 1)
     if not args.no_legs:
         wl = _pkg("workloads")
-        # configuration 2 (one layer's shape: 4096 prefix, k=3 d=4 of independent
-        # routes, 12 nodes, with the LSE) and the 16k-prefix k=3 d=4 tree
-        result["components"]["config2_4k_tree_lse"] = attention_leg(dev, prefix_len=4096, routes=wl.tree_routes(0),
-                                                                    with_lse=True)
-        result["components"]["tree_16k_k3_d4"] = attention_leg(dev, prefix_len=16384, routes=wl.tree_routes(0),
-                                                               with_lse=False)
-        result["components"]["batched_32req"] = batched_leg(dev, pool_gb=args.commit_pool_gb)
-        result["components"]["cow_8req_9routes"] = cow_leg(dev)
-        result["components"]["drafter_decode_attn"] = decode_leg(dev)
-        result["components"]["drafter_decode_attn_8k"] = decode_leg(dev, prefix_len=8192)
-        result["components"]["drafter_fork_8req"] = drafter_leg(dev)
-        result["components"]["drafter_fork_8req_per_request_calls"] = drafter_leg(dev, batched=False)
-        result["components"]["drafter_frontier_depth"] = frontier_leg(dev)
-        result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
-        result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)
+        legs = {
+            # configuration 2 (one layer's shape: 4096 prefix, k=3 d=4 of
+            # independent routes, 12 nodes, with the LSE) and the 16k-prefix
+            # k=3 d=4 tree
+            "config2": ("config2_4k_tree_lse", lambda: attention_leg(dev, prefix_len=4096,
+                                                                     routes=wl.tree_routes(0), with_lse=True)),
+            "tree16k": ("tree_16k_k3_d4", lambda: attention_leg(dev, prefix_len=16384, routes=wl.tree_routes(0),
+                                                                with_lse=False)),
+            "batched": ("batched_32req", lambda: batched_leg(dev, pool_gb=args.commit_pool_gb)),
+            "cow": ("cow_8req_9routes", lambda: cow_leg(dev)),
+            "decode": ("drafter_decode_attn", lambda: decode_leg(dev)),
+            "decode8k": ("drafter_decode_attn_8k", lambda: decode_leg(dev, prefix_len=8192)),
+            "drafter": ("drafter_fork_8req", lambda: drafter_leg(dev)),
+            "drafter_calls": ("drafter_fork_8req_per_request_calls", lambda: drafter_leg(dev, batched=False)),
+            "frontier": ("drafter_frontier_depth", lambda: frontier_leg(dev)),
+        }
+        chosen = list(legs) if args.legs == "all" else [x for x in args.legs.split(",") if x]
+        for name in chosen:
+            if name not in legs:
+                raise SystemExit(f"unknown leg {name!r}; legs: {', '.join(legs)}")
+            key, run = legs[name]
+            result["components"][key] = run()
+            print(f"leg {name} done", file=sys.stderr, flush=True)
+        if "batched_32req" in result["components"]:
+            result["kv_commit_GBps"] = round(result["components"]["batched_32req"]["commit_GBps"], 1)
+        if "cow_8req_9routes" in result["components"]:
+            result["kv_cow_GBps"] = round(result["components"]["cow_8req_9routes"]["GBps"], 1)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(step, args.cpu_baseline_seconds)
     print(json.dumps(result))
