@@ -169,9 +169,10 @@ def test_fallback_ar_decodes_on_the_prefix_pages(dev):
     assert b.prefix_token_ids[prefix_len:] == tuple(toks) and res.metadata["prefix_len_after"] == prefix_len + 4
     # replay the steps densely: step i consumed token i at position prefix_len + i
     for i, tok in enumerate(toks):
-        dense = _dense_step_logits(model, b._paged_prefix_kv, prefix_len + i + 1, tok, prefix_len + i)
+        with torch.no_grad():
+            dense = _dense_step_logits(model, b._paged_prefix_kv, prefix_len + i + 1, tok, prefix_len + i)
         if i + 1 < len(toks):
             top2 = torch.topk(dense[0], 2).values
-            if float((top2[0] - top2[1]).detach()) > 2e-2:
+            if float(top2[0] - top2[1]) > 2e-2:
                 assert int(torch.argmax(dense)) == toks[i + 1], f"step {i}: greedy token differs"
     assert float((b._prefix_logits.float() - dense).abs().max()) <= 2e-2
