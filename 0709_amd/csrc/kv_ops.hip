@@ -58,7 +58,10 @@ __global__ __launch_bounds__(kThreads) void kv_move_kernel(LayerTable lt, SlotGe
 // a batch (a branch makes the compiler wait for every outstanding access,
 // stores included, before each store): layers past the last one copy the last
 // layer again, the same bytes to the same place.  dst and src slots are
-// disjoint, so the copies of different waves never overlap.
+// disjoint, so the copies of different waves never overlap.  The stores
+// carry the non-temporal hint (the copies are not read again in this launch;
+// 30.7 -> 24.1 us for a cold 94.6 MB copy-on-write); the loads do not, since
+// a tail page's rows are the source of several copies and hit in L2.
 template <int CPR, int LB>
 __global__ __launch_bounds__(kThreads) void kv_move_rows_kernel(LayerTable lt, SlotGeom g, int num_layers,
                                                                 const int64_t* __restrict__ dst,
@@ -88,8 +91,8 @@ __global__ __launch_bounds__(kThreads) void kv_move_rows_kernel(LayerTable lt, S
       char* vb = const_cast<char*>(lt.v[l]);
 #pragma unroll
       for (int c = 0; c < CPR; ++c) {
-        *reinterpret_cast<u32x4v*>(kb + dof + c * 1024) = buf[i][0][c];
-        *reinterpret_cast<u32x4v*>(vb + dof + c * 1024) = buf[i][1][c];
+        __builtin_nontemporal_store(buf[i][0][c], reinterpret_cast<u32x4v*>(kb + dof + c * 1024));
+        __builtin_nontemporal_store(buf[i][1][c], reinterpret_cast<u32x4v*>(vb + dof + c * 1024));
       }
     }
   }
@@ -159,6 +162,8 @@ enum CommitMode { kCopy = 0, kGather = 1, kScatter = 2 };
 // in flight.  Block = 4 waves = 4 consecutive layers of one item.
 constexpr int kRowWaves = 4;
 
+// Loads and stores carry the non-temporal hint: each row is read once and
+// written once (a cold 16 MiB commit of 32 requests: 10.1 -> 7.8 us).
 // CPR: 1 KiB chunks per token row (1 or 2: every load of the row is issued
 // before its stores, so a wave keeps its whole K and V rows in flight), or 0
 // for other row sizes (a loop of 16-byte vectors).
@@ -207,13 +212,13 @@ __global__ __launch_bounds__(kThreads) void kv_commit_rows_kernel(
     u32x4v a[CPR], b[CPR];
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
-      a[c] = *reinterpret_cast<const u32x4v*>(src_k + int64_t(c * 64 + lane) * 16);
-      b[c] = *reinterpret_cast<const u32x4v*>(src_v + int64_t(c * 64 + lane) * 16);
+      a[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_k + int64_t(c * 64 + lane) * 16));
+      b[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_v + int64_t(c * 64 + lane) * 16));
     }
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
-      *reinterpret_cast<u32x4v*>(dst_k + int64_t(c * 64 + lane) * 16) = a[c];
-      *reinterpret_cast<u32x4v*>(dst_v + int64_t(c * 64 + lane) * 16) = b[c];
+      __builtin_nontemporal_store(a[c], reinterpret_cast<u32x4v*>(dst_k + int64_t(c * 64 + lane) * 16));
+      __builtin_nontemporal_store(b[c], reinterpret_cast<u32x4v*>(dst_v + int64_t(c * 64 + lane) * 16));
     }
   } else {
 #pragma unroll 2
