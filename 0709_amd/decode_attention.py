@@ -47,7 +47,7 @@ from .tree_attention import (
     BatchPrefillWithPagedKVCacheWrapper,
     _dtype_from,
     _partial_row_bytes,
-    _to_host_list,
+    _host_lists,
 )
 
 # Routes whose page lists begin with at least this many identical full pages
@@ -173,9 +173,7 @@ class BatchDecodeWithPagedKVCacheWrapper:
             raise ValueError("page_size must be positive")
         if q_dtype != kv_dtype:
             raise NotImplementedError("q and kv data types must match")
-        kvp = _to_host_list(indptr)
-        last = _to_host_list(last_page_len)
-        idx = _to_host_list(indices)
+        kvp, last, idx = _host_lists(indptr, last_page_len, indices)
         batch = len(kvp) - 1
         if len(last) != batch or any(b < a for a, b in zip(kvp, kvp[1:])) or kvp[-1] > len(idx):
             raise ValueError("indptr / indices / last_page_len sizes are inconsistent")

@@ -15,9 +15,10 @@ reference's tree / paged-KV functions.  Differences are in where the work runs:
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, field
 from typing import Sequence
 
+import numpy as np
 import torch
 
 from . import kv_ops
@@ -29,12 +30,14 @@ class TreeSpec:
     """Reference ``TreeSpec`` (``flashinfer_full_verify.py:136-149``) plus the
     compact ancestor bitmask: ``tree_mask[i]`` has bit ``j`` set iff tree node
     ``j`` is an ancestor-or-self of node ``i``; tree node ``j`` sits at key
-    position ``mask_col_start + j``."""
+    position ``mask_col_start + j``.  ``packed_mask`` (the reference's
+    ``packbits`` of ``bool_mask``) is built on first use: the verify passes
+    ``bool_mask`` unless ``use_packed_custom_mask`` is set
+    (``flashinfer_full_verify.py:963-967``)."""
 
     flat_token_ids: torch.Tensor
     parent_indices: list[int]
     depths: torch.Tensor
-    packed_mask: torch.Tensor
     bool_mask: torch.Tensor
     qo_indptr: torch.Tensor
     kv_indptr: torch.Tensor
@@ -45,6 +48,13 @@ class TreeSpec:
     kv_len: int
     tree_mask: torch.Tensor | None = None
     mask_col_start: int = 0
+    _packed: dict = field(default_factory=dict, repr=False, compare=False)
+
+    @property
+    def packed_mask(self) -> torch.Tensor:
+        if "mask" not in self._packed:
+            self._packed["mask"] = packbits(self.bool_mask)
+        return self._packed["mask"]
 
 
 @dataclass
@@ -98,13 +108,7 @@ def _validate_paths(paths: Sequence[Sequence[int]]) -> int:
     return depth
 
 
-def build_path_tree_tokens_from_paths(
-    paths: Sequence[Sequence[int]],
-    *,
-    device: torch.device | str,
-) -> tuple[torch.Tensor, list[int], torch.Tensor]:
-    """One node per path position, no sharing
-    (``flashinfer_full_verify.py:541-567``)."""
+def _path_tree_lists(paths: Sequence[Sequence[int]]) -> tuple[list[int], list[int], list[int]]:
     _validate_paths(paths)
     token_ids: list[int] = []
     parent_indices: list[int] = []
@@ -116,6 +120,17 @@ def build_path_tree_tokens_from_paths(
             parent_indices.append(parent)
             depths.append(depth_idx)
             parent = len(token_ids) - 1
+    return token_ids, parent_indices, depths
+
+
+def build_path_tree_tokens_from_paths(
+    paths: Sequence[Sequence[int]],
+    *,
+    device: torch.device | str,
+) -> tuple[torch.Tensor, list[int], torch.Tensor]:
+    """One node per path position, no sharing
+    (``flashinfer_full_verify.py:541-567``)."""
+    token_ids, parent_indices, depths = _path_tree_lists(paths)
     return (
         torch.tensor(token_ids, dtype=torch.long, device=device),
         parent_indices,
@@ -123,14 +138,7 @@ def build_path_tree_tokens_from_paths(
     )
 
 
-def build_deduplicated_path_tree_tokens(
-    paths: Sequence[Sequence[int]],
-    *,
-    device: torch.device | str,
-) -> tuple[torch.Tensor, list[int], torch.Tensor, list[list[int]]]:
-    """Prefix trie over the routes: one node per unique token prefix, numbered
-    in insertion order (route by route, depth by depth), and the route -> node
-    paths (``flashinfer_full_verify.py:570-616``)."""
+def _dedup_tree_lists(paths: Sequence[Sequence[int]]) -> tuple[list[int], list[int], list[int], list[list[int]]]:
     _validate_paths(paths)
     token_ids: list[int] = []
     parent_indices: list[int] = []
@@ -153,6 +161,18 @@ def build_deduplicated_path_tree_tokens(
             nodes.append(node)
             parent = node
         route_nodes.append(nodes)
+    return token_ids, parent_indices, depths, route_nodes
+
+
+def build_deduplicated_path_tree_tokens(
+    paths: Sequence[Sequence[int]],
+    *,
+    device: torch.device | str,
+) -> tuple[torch.Tensor, list[int], torch.Tensor, list[list[int]]]:
+    """Prefix trie over the routes: one node per unique token prefix, numbered
+    in insertion order (route by route, depth by depth), and the route -> node
+    paths (``flashinfer_full_verify.py:570-616``)."""
+    token_ids, parent_indices, depths, route_nodes = _dedup_tree_lists(paths)
     return (
         torch.tensor(token_ids, dtype=torch.long, device=device),
         parent_indices,
@@ -192,53 +212,84 @@ def _signed64(value: int) -> int:
     return value - (1 << 64) if value >= 1 << 63 else value
 
 
+def with_host_values(t: torch.Tensor, values: Sequence[int]) -> torch.Tensor:
+    """Attach the host copy of a small index tensor's values (and its version
+    counter), so a plan that reads them back skips the device-to-host copy
+    while the tensor is unchanged."""
+    t._atlas_host_values = (list(values), tensor_version(t))
+    return t
+
+
 def _tree_spec(
     *,
-    flat_token_ids: torch.Tensor,
+    token_ids: list[int],
     parent_indices: list[int],
-    depths: torch.Tensor,
+    depths: list[int],
     prefix_len: int,
     page_size: int,
     device: torch.device | str,
 ) -> TreeSpec:
-    node_count = int(flat_token_ids.numel())
-    kv_len = int(prefix_len) + node_count
+    node_count = len(token_ids)
+    prefix_len = int(prefix_len)
+    kv_len = prefix_len + node_count
     total_pages = ceil_div(kv_len, page_size)
     bits = ancestor_bitmasks(parent_indices)
     device = torch.device(device)
+    last = last_page_len(kv_len, page_size)
+    # Everything small goes to the device in one copy of one host buffer:
+    # token ids and depths (int64), the ancestor bitmasks (int64, up to 64
+    # nodes), qo/kv indptr, last page length and the identity page table
+    # (int32), then the tree block of the mask (bool).
+    compact = node_count <= 64
+    i64 = np.concatenate((
+        np.asarray(token_ids, dtype=np.int64), np.asarray(depths, dtype=np.int64),
+        np.asarray([_signed64(b) for b in bits] if compact else [], dtype=np.int64)))
+    i32 = np.concatenate((np.asarray([0, node_count, 0, total_pages, last], dtype=np.int32),
+                          np.arange(total_pages, dtype=np.int32)))
+    i32 = np.concatenate((i32, np.zeros(len(i32) % 2, dtype=np.int32)))  # keep the bool block 8-byte aligned
+    if compact:
+        words = np.asarray([b & ((1 << 64) - 1) for b in bits], dtype=np.uint64)
+        block = ((words[:, None] >> np.arange(node_count, dtype=np.uint64)[None, :]) & 1).astype(np.bool_)
+    else:
+        block = np.asarray([[(b >> j) & 1 for j in range(node_count)] for b in bits], dtype=np.bool_)
+    host = np.concatenate((i64.view(np.uint8), i32.view(np.uint8), block.reshape(-1).view(np.uint8)))
+    buf = torch.from_numpy(host).to(device)
+    o64 = 0
+    n64 = len(i64)
+    flat_token_ids = buf[o64 * 8:(o64 + node_count) * 8].view(torch.int64)
+    depths_t = buf[(o64 + node_count) * 8:(o64 + 2 * node_count) * 8].view(torch.int64)
+    tree_mask = buf[2 * node_count * 8:n64 * 8].view(torch.int64) if compact else None
+    b32 = n64 * 8
+    qo_indptr = with_host_values(buf[b32:b32 + 8].view(torch.int32), [0, node_count])
+    kv_indptr = with_host_values(buf[b32 + 8:b32 + 16].view(torch.int32), [0, total_pages])
+    kv_last = with_host_values(buf[b32 + 16:b32 + 20].view(torch.int32), [last])
+    kv_indices = buf[b32 + 20:b32 + 20 + 4 * total_pages].view(torch.int32)
+    b_block = b32 + 4 * len(i32)
     # Dense mask [node, prefix + node]: prefix columns all visible, tree column
     # j visible iff bit j of the row's ancestor bitmask.
-    mask = torch.zeros((node_count, kv_len), dtype=torch.bool, device=device)
-    mask[:, : int(prefix_len)] = True
-    tree_mask = None
-    if node_count <= 64:
-        tree_mask = torch.tensor([_signed64(b) for b in bits], dtype=torch.int64, device=device)
-        shifts = torch.arange(node_count, dtype=torch.int64, device=device)
-        mask[:, int(prefix_len) :] = ((tree_mask[:, None] >> shifts[None, :]) & 1).to(torch.bool)
-    else:
-        rows = [[(b >> j) & 1 for j in range(node_count)] for b in bits]
-        mask[:, int(prefix_len) :] = torch.tensor(rows, dtype=torch.bool, device=device)
+    mask = torch.ones((node_count, kv_len), dtype=torch.bool, device=device)
+    if node_count:
+        mask[:, prefix_len:] = buf[b_block:].view(torch.bool).view(node_count, node_count)
     flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.
         # The version counter lets plan() notice an in-place change of the mask
         # (inference tensors have none: None).
-        flat_mask._atlas_tree_window = (int(prefix_len), tree_mask, tensor_version(flat_mask))
+        flat_mask._atlas_tree_window = (prefix_len, tree_mask, tensor_version(flat_mask))
     return TreeSpec(
         flat_token_ids=flat_token_ids,
         parent_indices=list(parent_indices),
-        depths=depths,
-        packed_mask=packbits(flat_mask),
+        depths=depths_t,
         bool_mask=flat_mask,
-        qo_indptr=torch.tensor([0, node_count], dtype=torch.int32, device=device),
-        kv_indptr=torch.tensor([0, total_pages], dtype=torch.int32, device=device),
-        kv_indices=torch.arange(total_pages, dtype=torch.int32, device=device),
-        kv_last_page_len=torch.tensor([last_page_len(kv_len, page_size)], dtype=torch.int32, device=device),
+        qo_indptr=qo_indptr,
+        kv_indptr=kv_indptr,
+        kv_indices=kv_indices,
+        kv_last_page_len=kv_last,
         total_pages=total_pages,
         node_count=node_count,
         kv_len=kv_len,
         tree_mask=tree_mask,
-        mask_col_start=int(prefix_len),
+        mask_col_start=prefix_len,
     )
 
 
@@ -250,8 +301,8 @@ def build_tree_spec_from_paths(
     device: torch.device | str,
 ) -> TreeSpec:
     """Undeduplicated tree (``flashinfer_full_verify.py:655-701``)."""
-    flat, parents, depths = build_path_tree_tokens_from_paths(paths, device=device)
-    return _tree_spec(flat_token_ids=flat, parent_indices=parents, depths=depths, prefix_len=prefix_len,
+    tokens, parents, depths = _path_tree_lists(paths)
+    return _tree_spec(token_ids=tokens, parent_indices=parents, depths=depths, prefix_len=prefix_len,
                       page_size=page_size, device=device)
 
 
@@ -264,8 +315,8 @@ def build_deduplicated_tree_spec_from_paths(
 ) -> tuple[TreeSpec, list[list[int]]]:
     """Deduplicated tree and its route -> node paths
     (``flashinfer_full_verify.py:704-739``)."""
-    flat, parents, depths, route_nodes = build_deduplicated_path_tree_tokens(paths, device=device)
-    spec = _tree_spec(flat_token_ids=flat, parent_indices=parents, depths=depths, prefix_len=prefix_len,
+    tokens, parents, depths, route_nodes = _dedup_tree_lists(paths)
+    spec = _tree_spec(token_ids=tokens, parent_indices=parents, depths=depths, prefix_len=prefix_len,
                       page_size=page_size, device=device)
     return spec, route_nodes
 

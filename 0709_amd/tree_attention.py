@@ -17,6 +17,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -73,10 +74,42 @@ class AttentionPlan:
         return int(self.meta.data_ptr()) + 4 * offset
 
 
-def _to_host_list(t: torch.Tensor | list | tuple) -> list[int]:
-    if isinstance(t, torch.Tensor):
-        return [int(x) for x in t.detach().cpu().reshape(-1).tolist()]
-    return [int(x) for x in t]
+def _cached_host_values(t: torch.Tensor) -> list[int] | None:
+    """The host copy a tree builder attached to a small index tensor, if the
+    tensor has not been modified in place since (version counter unchanged)."""
+    cached = getattr(t, "_atlas_host_values", None)
+    if cached is None:
+        return None
+    from .flashinfer_full_verify import tensor_version
+
+    values, version = cached
+    return values if version == tensor_version(t) and len(values) == int(t.numel()) else None
+
+
+def _host_lists(*items: torch.Tensor | list | tuple) -> list[list[int]]:
+    """Host int lists of index arrays: lists and CPU tensors directly, device
+    tensors from their attached host copy when valid, the rest with one
+    device-to-host copy for all of them."""
+    out: list[list[int] | None] = []
+    pending: list[tuple[int, torch.Tensor]] = []
+    for i, t in enumerate(items):
+        if not isinstance(t, torch.Tensor):
+            out.append([int(x) for x in t])
+        elif t.device.type == "cpu":
+            out.append([int(x) for x in t.reshape(-1).tolist()])
+        else:
+            cached = _cached_host_values(t)
+            out.append(cached)
+            if cached is None:
+                pending.append((i, t.detach().reshape(-1)))
+    if pending:
+        flat = torch.cat([t.to(torch.int64) for _, t in pending]).cpu().tolist()
+        off = 0
+        for i, t in pending:
+            n = int(t.numel())
+            out[i] = [int(x) for x in flat[off:off + n]]
+            off += n
+    return out  # type: ignore[return-value]
 
 
 def _dtype_from(value, default: torch.dtype) -> torch.dtype:
@@ -236,9 +269,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         if q_dtype != kv_dtype:
             raise NotImplementedError("q and kv data types must match")
 
-        qo = _to_host_list(qo_indptr)
-        kvp = _to_host_list(paged_kv_indptr)
-        last = _to_host_list(paged_kv_last_page_len)
+        qo, kvp, last = _host_lists(qo_indptr, paged_kv_indptr, paged_kv_last_page_len)
         batch = len(qo) - 1
         if batch <= 0 or len(kvp) != batch + 1 or len(last) != batch:
             raise ValueError("qo_indptr / kv_indptr / kv_last_page_len sizes are inconsistent")
@@ -400,7 +431,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # HIP graph captured over run() stays valid after a re-plan of the
         # same (or a smaller) shape.
         meta = self._persistent("_meta_buf", len(meta_vals), torch.int32)
-        meta[: len(meta_vals)].copy_(torch.tensor(meta_vals, dtype=torch.int32), non_blocking=non_blocking)
+        meta[: len(meta_vals)].copy_(torch.from_numpy(np.asarray(meta_vals, dtype=np.int32)),
+                                     non_blocking=non_blocking)
         n_idx = int(indices_src.numel())
         indices = self._persistent("_indices_buf", n_idx, torch.int32)
         if n_idx:
