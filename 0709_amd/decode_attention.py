@@ -48,6 +48,7 @@ from .tree_attention import (
     _dtype_from,
     _partial_row_bytes,
     _host_lists,
+    pack_plan,
 )
 
 # Routes whose page lists begin with at least this many identical full pages
@@ -276,11 +277,13 @@ class BatchDecodeWithPagedKVCacheWrapper:
         # Longest streams first: workgroups are dispatched in order.
         work.sort(key=lambda it: -(it[5] - it[4]))
         src = indices.reshape(-1) if isinstance(indices, torch.Tensor) else torch.tensor(idx, dtype=torch.int32)
+        dec = pack_plan(work=work, merge=merge, partial_rows=partial_rows, max_rows=max(it[3] for it in work),
+                        direct=direct, fused_append=False, kv_lens=plan_kv_lens, cols=[0] * len(groups), qo=qo,
+                        kvp=kvp)
         pf._install(
             batch=len(groups), hq=hq, hkv=hkv, d=d, ps=ps, sm_scale=sm_scale, q_dtype=q_dtype, kv_dtype=kv_dtype,
-            mask_mode=_lib.MASK_NONE, work=work, merge=merge, kv_lens=plan_kv_lens, cols=[0] * len(groups),
-            qo=qo, kvp=kvp, qo_lens=qo_lens, indices_src=src, tree_bits=None, partial_rows=partial_rows,
-            max_rows=max(it[3] for it in work), direct=direct, non_blocking=non_blocking)
+            mask_mode=_lib.MASK_NONE, dec=dec, kv_lens=plan_kv_lens, qo_lens=qo_lens, indices_src=src,
+            tree_bits=None, non_blocking=non_blocking)
         self.cascade_groups = sum(1 for _, n, _ in groups if n > 1)
         return True
 

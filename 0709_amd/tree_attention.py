@@ -187,6 +187,33 @@ def _rope_table(t: torch.Tensor, name: str, plan: AttentionPlan, dtype: torch.dt
     return t
 
 
+def pack_plan(*, work, merge, partial_rows, max_rows, direct, fused_append, kv_lens, cols, qo, kvp) -> dict:
+    """A planned work list as the kernels read it: one int32 array of [work
+    items (16 ints) | merge items (8 ints) | kv_len | mask_col_start |
+    qo_indptr | kv_indptr] and the offsets of its parts.  ``fused_append``:
+    every (request, KV head) is a single row block (the launch may write the
+    newest rows itself)."""
+    meta_vals: list[int] = []
+    for item in work:
+        meta_vals.extend(item)
+    merge_off = len(meta_vals)
+    for item in merge:
+        meta_vals.extend(item)
+    kvlen_off = len(meta_vals)
+    meta_vals.extend(kv_lens)
+    col_off = len(meta_vals)
+    meta_vals.extend(cols)
+    qo_off = len(meta_vals)
+    meta_vals.extend(qo)
+    kvp_off = len(meta_vals)
+    meta_vals.extend(kvp)
+    return dict(
+        work=work, num_merge=len(merge), partial_rows=partial_rows, max_rows=max_rows, direct=direct,
+        fused_append=fused_append, meta=np.asarray(meta_vals, dtype=np.int32), merge_off=merge_off,
+        kvlen_off=kvlen_off, col_off=col_off, qo_off=qo_off, kvp_off=kvp_off, qo=qo, kvp=kvp,
+        tiles_per_split=max((math.ceil((it[5] - it[4]) / TILE_KEYS) for it in work), default=0))
+
+
 class BatchPrefillWithPagedKVCacheWrapper:
     """Paged prefill attention with a custom (tree) mask on the gfx950 kernel.
 
@@ -215,6 +242,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self.use_page_windows: bool = True
         self.min_tiles_per_split = 1
         self.max_rows_per_item: int | None = None
+        self._decomp_cache: tuple | None = None
+        self._meta_uploaded: tuple | None = None
         self._meta_buf: torch.Tensor | None = None
         self._indices_buf: torch.Tensor | None = None
         self._bits_buf: torch.Tensor | None = None
@@ -318,7 +347,24 @@ class BatchPrefillWithPagedKVCacheWrapper:
                     parts.append(res[1])
                 tree_bits = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.int64, device=device)
 
-        # ---- work decomposition ----
+        # ---- work decomposition (the same inputs give the same work list) ----
+        ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
+        key = (tuple(qo), tuple(kvp), tuple(kv_lens), tuple(cols), hq, hkv, d, ps, self.max_rows_per_item,
+               self.split_target_items, self.min_tiles_per_split, ws_rows_cap)
+        if self._decomp_cache is None or self._decomp_cache[0] != key:
+            self._decomp_cache = (key, self._decompose(batch=batch, qo=qo, kvp=kvp, qo_lens=qo_lens,
+                                                       kv_lens=kv_lens, cols=cols, hq=hq, hkv=hkv, d=d, ps=ps,
+                                                       ws_rows_cap=ws_rows_cap))
+        dec = self._decomp_cache[1]
+        self._install(
+            batch=batch, hq=hq, hkv=hkv, d=d, ps=ps, sm_scale=sm_scale, q_dtype=q_dtype, kv_dtype=kv_dtype,
+            mask_mode=mask_mode, dec=dec, kv_lens=kv_lens, qo_lens=qo_lens,
+            indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits, non_blocking=non_blocking)
+
+    def _decompose(self, *, batch, qo, kvp, qo_lens, kv_lens, cols, hq, hkv, d, ps, ws_rows_cap) -> dict:
+        """Work and merge items of a plan, and the int32 metadata the kernels
+        read: [work items | merge items | kv_len | mask_col_start | qo_indptr |
+        kv_indptr]."""
         group = hq // hkv
         direct = d == 128 and ps >= 16 and (ps & (ps - 1)) == 0
         if self.max_rows_per_item is None:
@@ -358,7 +404,6 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # the merge kernel combines at most MAX_SPLITS states per row
         max_tiles = max((math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks), default=0)
         tiles_per_split = max(tiles_per_split, max_tiles / MAX_SPLITS)
-        ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
         while True:
             work, merge = [], []
             partial_rows = 0
@@ -398,41 +443,26 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # their queries) when there are 8 KV heads.
         work.sort(key=lambda it: (-(it[5] - it[4]), it[0], it[2], it[4], it[1]))
 
-        self._install(
-            batch=batch, hq=hq, hkv=hkv, d=d, ps=ps, sm_scale=sm_scale, q_dtype=q_dtype, kv_dtype=kv_dtype,
-            mask_mode=mask_mode, work=work, merge=merge, kv_lens=kv_lens, cols=cols, qo=qo, kvp=kvp,
-            qo_lens=qo_lens, indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits,
-            partial_rows=partial_rows, max_rows=max_rows, direct=direct, non_blocking=non_blocking)
-        # one row block per (request, KV head): blocks start at row 0 only
-        self._plan.fused_append = direct and all(r0 == 0 for (_, r0, _) in blocks)
+        return pack_plan(work=work, merge=merge, partial_rows=partial_rows, max_rows=max_rows, direct=direct,
+                         fused_append=direct and all(r0 == 0 for (_, r0, _) in blocks), kv_lens=kv_lens,
+                         cols=cols, qo=qo, kvp=kvp)
 
-    def _install(self, *, batch, hq, hkv, d, ps, sm_scale, q_dtype, kv_dtype, mask_mode, work, merge, kv_lens, cols,
-                 qo, kvp, qo_lens, indices_src, tree_bits, partial_rows, max_rows, direct, non_blocking) -> None:
-        """Write a planned work list into the persistent device buffers and
-        make it the current plan.  ``work`` holds 16-int work items, ``merge``
-        8-int merge items; ``qo`` / ``kvp`` are the per-request indptr lists
-        the merge kernel and callers read."""
+    def _install(self, *, batch, hq, hkv, d, ps, sm_scale, q_dtype, kv_dtype, mask_mode, dec, kv_lens, qo_lens,
+                 indices_src, tree_bits, non_blocking) -> None:
+        """Write a planned work list (``dec``, from ``_decompose``) into the
+        persistent device buffers and make it the current plan."""
         device = self.device
-        meta_vals: list[int] = []
-        for item in work:
-            meta_vals.extend(item)
-        merge_off = len(meta_vals)
-        for item in merge:
-            meta_vals.extend(item)
-        kvlen_off = len(meta_vals)
-        meta_vals.extend(kv_lens)
-        col_off = len(meta_vals)
-        meta_vals.extend(cols)
-        qo_off = len(meta_vals)
-        meta_vals.extend(qo)
-        kvp_off = len(meta_vals)
-        meta_vals.extend(kvp)
+        meta_np = dec["meta"]
         # Persistent device buffers keep their addresses across plans, so a
         # HIP graph captured over run() stays valid after a re-plan of the
-        # same (or a smaller) shape.
-        meta = self._persistent("_meta_buf", len(meta_vals), torch.int32)
-        meta[: len(meta_vals)].copy_(torch.from_numpy(np.asarray(meta_vals, dtype=np.int32)),
-                                     non_blocking=non_blocking)
+        # same (or a smaller) shape.  Metadata equal to what the buffer already
+        # holds is not uploaded again.
+        meta = self._persistent("_meta_buf", len(meta_np), torch.int32)
+        if self._meta_uploaded is None or self._meta_uploaded[0] is not meta or \
+                not np.array_equal(self._meta_uploaded[1], meta_np):
+            meta[: len(meta_np)].copy_(torch.from_numpy(meta_np), non_blocking=non_blocking)
+            self._meta_uploaded = (meta, meta_np)
+        work = dec["work"]
         n_idx = int(indices_src.numel())
         indices = self._persistent("_indices_buf", n_idx, torch.int32)
         if n_idx:
@@ -448,7 +478,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # per plan (the page table is fixed until the next plan), so the
         # head_dim-128 kernel requests its first page ids with its work item.
         windows = None
-        if direct and work and self.use_page_windows:
+        if dec["direct"] and work and self.use_page_windows:
             windows = self._persistent("_windows_buf", 64 * len(work), torch.int32)
             rc = _lib.load().atlas_attn_page_windows(int(meta.data_ptr()), len(work), _lib.ptr(indices), ps,
                                                      _lib.ptr(windows), _lib.stream_of(device))
@@ -457,13 +487,13 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self._plan = AttentionPlan(
             batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,
             sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
-            q_dtype=q_dtype, kv_dtype=kv_dtype, nnz=qo[-1] - qo[0] if batch else 0, mask_mode=mask_mode,
-            qo_indptr=meta[qo_off:], kv_indptr=meta[kvp_off:], kv_indices=indices,
-            tree_mask=bits_buf, meta=meta, num_work=len(work), num_merge=len(merge), work_offset=0,
-            merge_offset=merge_off, kv_len_offset=kvlen_off, col_offset=col_off, max_rows=max_rows,
-            partial_rows=partial_rows, kv_lens=kv_lens, qo_lens=qo_lens,
-            tiles_per_split=max((math.ceil((it[5] - it[4]) / TILE_KEYS) for it in work), default=0),
-            page_windows=windows,
+            q_dtype=q_dtype, kv_dtype=kv_dtype, nnz=dec["qo"][-1] - dec["qo"][0] if batch else 0,
+            mask_mode=mask_mode, qo_indptr=meta[dec["qo_off"]:], kv_indptr=meta[dec["kvp_off"]:],
+            kv_indices=indices, tree_mask=bits_buf, meta=meta, num_work=len(work), num_merge=dec["num_merge"],
+            work_offset=0, merge_offset=dec["merge_off"], kv_len_offset=dec["kvlen_off"],
+            col_offset=dec["col_off"], max_rows=dec["max_rows"], partial_rows=dec["partial_rows"],
+            kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=dec["tiles_per_split"], page_windows=windows,
+            fused_append=dec["fused_append"],
         )
 
     def _persistent(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:

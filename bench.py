@@ -108,8 +108,12 @@ class HeadlineStep:
         pos = torch.arange(prefix_len, self.kv_len)
         idx = torch.tensor(self.kv_indices_host, dtype=torch.int64)
         self.tree_slots = (idx[pos // page_size] * page_size + pos % page_size).to(dev)
-        self.kv_indptr = torch.tensor([0, self.pages], dtype=torch.int32, device=dev)
-        self.last = torch.tensor([self.kv_len - (self.pages - 1) * page_size], dtype=torch.int32, device=dev)
+        # the plan reads these back on the host: their values travel with them
+        # (as with the tree builder's own index tensors), so no device read
+        last = self.kv_len - (self.pages - 1) * page_size
+        self.kv_indptr = ffv.with_host_values(torch.tensor([0, self.pages], dtype=torch.int32, device=dev),
+                                              [0, self.pages])
+        self.last = ffv.with_host_values(torch.tensor([last], dtype=torch.int32, device=dev), [last])
         # page ownership of the pool for the prune
         pool_pages = int(self.kv.pool.shape[1])
         self.pool_pages = pool_pages
