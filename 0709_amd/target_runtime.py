@@ -95,9 +95,12 @@ def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Seq
         return out
     if len(tokens) != n:
         raise ValueError("rows and tokens must have equal length")
-    idx = torch.tensor([*map(int, tokens), *map(int, rows)], dtype=torch.int64).to(device, non_blocking=True)
-    tok = idx[:n]
-    row = idx[n:].to(torch.int32)
+    # tokens (int64) and rows (int32) in one upload
+    host = np.concatenate((np.asarray(tokens, dtype=np.int64).view(np.uint8),
+                           np.asarray(rows, dtype=np.int32).view(np.uint8)))
+    idx = torch.from_numpy(host).to(device)
+    tok = idx[: 8 * n].view(torch.int64)
+    row = idx[8 * n:].view(torch.int32)
     lib = _lib.load()
     rows2 = 0 if lg2 is None else int(lg2.shape[0])
     need = int(lib.atlas_gather_logprobs_workspace_bytes(int(lg.shape[0]) + rows2, int(lg.shape[1])))
@@ -624,9 +627,11 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                 rows.append(int(nodes[off - 1]))
                 toks.append(int(path[off]))
         values = gather_token_logprobs(vl, rows, toks, extra_logits=prefix_logits).cpu().numpy()
-        if self.match_logits_dtype_rounding and verify_logits.dtype in (torch.float16, torch.bfloat16):
+        if self.match_logits_dtype_rounding and verify_logits.dtype == torch.float16:
             # The reference reads log_softmax outputs in the logits dtype.
-            values = torch.from_numpy(values).to(verify_logits.dtype).float().numpy()
+            values = values.astype(np.float16).astype(np.float32)
+        elif self.match_logits_dtype_rounding and verify_logits.dtype == torch.bfloat16:
+            values = torch.from_numpy(values).to(torch.bfloat16).float().numpy()
         first_vals = values[: len(paths)]
         rest = values[len(paths):]
         scores, k = [], 0

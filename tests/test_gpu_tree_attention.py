@@ -585,3 +585,77 @@ def test_fused_rope_batched_requests_and_refusals(dev):
         w.run(q.to(dev), kv_dev, append_key_states=k_new.to(dev), append_value_states=v_new.to(dev),
               rope_cos_sin=(cos[:-1].to(dev), sin[:-1].to(dev)))
 
+
+
+def test_plan_sees_index_tensors_changed_in_place(dev):
+    """The tree builder's index tensors carry their host values; a plan reads
+    those only while the tensor is unchanged.  After an in-place write the
+    plan reads the device values again (here: a longer last page, so one more
+    key per row, checked against the oracle)."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(31)
+    routes = _routes(gen, 3, 4, share=True)
+    c = _build(dev, seed=31, prefix_len=300, routes=routes, permute=False, spare_pages=1)
+    spec = c["spec"]
+    assert spec.kv_last_page_len._atlas_host_values[0] == [ffv.last_page_len(c["kv_len"], 16)]
+    ws = torch.empty(16 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w.plan(spec.qo_indptr, spec.kv_indptr, spec.kv_indices, spec.kv_last_page_len, c["hq"], c["hkv"], c["d"], 16,
+           causal=True, q_data_type=torch.float16)
+    assert w.current_plan.kv_lens == [c["kv_len"]]
+    # a last page one key longer reads one more row of the same page (the
+    # cache buffer holds whole pages)
+    old_last = ffv.last_page_len(c["kv_len"], 16)
+    assert old_last < 16
+    spec.kv_last_page_len.add_(1)
+    w.plan(spec.qo_indptr, spec.kv_indptr, spec.kv_indices, spec.kv_last_page_len, c["hq"], c["hkv"], c["d"], 16,
+           causal=True, q_data_type=torch.float16)
+    kv_len = c["kv_len"] + 1
+    assert w.current_plan.kv_lens == [kv_len]
+    out = w.run(c["q"].to(dev), c["kv"].to(dev))
+    torch.cuda.synchronize()
+    n = c["n"]
+    causal = np.zeros((n, kv_len), dtype=bool)
+    for i in range(n):
+        causal[i, : kv_len - n + i + 1] = True
+    ro, _ = oatt.masked_attention(c["q"].float().numpy().astype(np.float64), c["kv"].float().numpy().astype(np.float64),
+                                  [0, n], [0, c["pages"]], list(range(c["pages"])), [old_last + 1], masks=[causal])
+    assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+
+
+def test_replans_reuse_and_refresh_the_work_list(dev):
+    """Planning the same shape again reuses the work decomposition and skips
+    the metadata upload; a different shape in between re-uploads it.  Every
+    run matches the oracle."""
+    gen = torch.Generator().manual_seed(37)
+    routes = _routes(gen, 3, 4, share=True)
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    ws = torch.empty(64 * 1024 * 1024, dtype=torch.uint8, device=dev)
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    cases = [_build(dev, seed=40 + i, prefix_len=p, routes=routes) for i, p in enumerate((5000, 700, 5000))]
+    decomps = []
+    for c in cases:
+        last = ffv.last_page_len(c["kv_len"], c["ps"])
+        w.plan(torch.tensor([0, c["n"]], dtype=torch.int32, device=dev),
+               torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev), c["order"].to(dev),
+               torch.tensor([last], dtype=torch.int32, device=dev), c["hq"], c["hkv"], c["d"], c["ps"],
+               custom_mask=c["spec"].bool_mask, causal=False, q_data_type=c["dtype"])
+        decomps.append(w._decomp_cache[1])
+        out, lse = w.run(c["q"].to(dev), c["kv"].to(dev), return_lse=True)
+        torch.cuda.synchronize()
+        ro, rl = oatt.masked_attention(
+            c["q"].float().numpy().astype(np.float64), c["kv"].float().numpy().astype(np.float64),
+            [0, c["n"]], [0, c["pages"]], c["order"].tolist(), [last], masks=[c["mask"]])
+        assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL
+        assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL
+    assert decomps[0] is not decomps[1] and decomps[1] is not decomps[2]
+    assert np.array_equal(decomps[0]["meta"], decomps[2]["meta"])
+    # the same inputs twice in a row reuse the decomposition object
+    c = cases[2]
+    last = ffv.last_page_len(c["kv_len"], c["ps"])
+    w.plan(torch.tensor([0, c["n"]], dtype=torch.int32), torch.tensor([0, c["pages"]], dtype=torch.int32),
+           c["order"].to(dev), torch.tensor([last], dtype=torch.int32), c["hq"], c["hkv"], c["d"], c["ps"],
+           custom_mask=c["spec"].bool_mask, causal=False, q_data_type=c["dtype"])
+    assert w._decomp_cache[1] is decomps[2]
