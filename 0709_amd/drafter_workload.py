@@ -281,14 +281,25 @@ class DrafterForkWorkload:
         self._post_steps()
 
     def fallback_extend(self) -> None:
+        """Every request drops its routes and prunes, then the EXTENDs run in
+        request order: one batched call over the shared pools (``batched``),
+        else one call per request.  Both take the same pages in the same
+        order."""
         for req in self.requests:
             b = req.bridge
             b.retain_route_rows([])
             req.stats.append({"released_kv_pages": b.release_unreferenced_node_slots([])})
-            before = self.ids.next
-            req.backend.append_known_tokens_as_prefix(req.plan.extend_tokens)
+        before = self.ids.next
+        if self.batched:
+            SGLangFlashInferFrontierModelBackend.append_known_tokens_as_prefix_many(
+                [r.backend for r in self.requests], [r.plan.extend_tokens for r in self.requests])
+        else:
+            for req in self.requests:
+                req.backend.append_known_tokens_as_prefix(req.plan.extend_tokens)
+        for req in self.requests:
             n = len(req.plan.extend_tokens)
             req.prefix_value_ids = req.prefix_value_ids + list(range(before, before + n))
+            before += n
             req.active = [req.store.new_root_route(req.rng.randrange(VOCAB),
                                                    req.store.prefix_view(len(req.backend.prefix_token_ids)))]
         # The logical store's committed tokens lag the EXTEND suffix; the

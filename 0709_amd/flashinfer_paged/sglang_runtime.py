@@ -282,10 +282,16 @@ class SGLangRoutePoolBridge:
         )
 
     # ------------------------------------------------------------ prefix
-    def set_prefix_slots(self, slot_ids: Sequence[int] | torch.Tensor) -> None:
-        """``sglang_runtime.py:173-187``."""
+    def set_prefix_slots(self, slot_ids: Sequence[int] | torch.Tensor, *, page_ids=None) -> None:
+        """``sglang_runtime.py:173-187``.  ``page_ids``: the pages of the slot
+        path when the caller already holds them on the host (saves reading
+        the path back)."""
         self.prefix_slot_ids = _as_long(slot_ids, self.device)
-        self._refresh_prefix_cpu_metadata()
+        if page_ids is not None and int(self.prefix_slot_ids.numel()):
+            self.prefix_slot_count = int(self.prefix_slot_ids.numel())
+            self.prefix_page_ids = set(int(p) for p in page_ids)
+        else:
+            self._refresh_prefix_cpu_metadata()
         if self._device_ownership:
             self.owned_page_ids.clear()
             if self.prefix_slot_count:
@@ -1456,6 +1462,97 @@ class SGLangFlashInferFrontierModelBackend:
             outputs.append(b._frontier_output(
                 step.route_ids[lo:hi], logits[lo:hi], new_nodes[i], start, before[i], ps,
                 sum(prevs) + len(prevs), sum((p + ps) // ps for p in prevs), attention_backend))
+        return outputs
+
+    @staticmethod
+    @torch.inference_mode()
+    def append_known_tokens_as_prefix_many(backends: Sequence["SGLangFlashInferFrontierModelBackend"],
+                                           token_lists: Sequence[Sequence[int]], *,
+                                           executor: Any = None) -> list[torch.Tensor]:
+        """``append_known_tokens_as_prefix`` of several requests as one EXTEND:
+        when their bridges share native pools, one request-row allocation, one
+        ``alloc_extend`` for all requests (their new pages come off the free
+        list in request order, as one call per request takes them), one
+        request-row write and ONE ``forward_extend`` of the union batch
+        (``executor``, default the first backend's; ``out_cache_loc``,
+        ``positions`` and ``input_ids`` hold the requests' suffixes in order,
+        ``req_pool_indices`` and ``seq_lens_cpu`` one entry per request);
+        otherwise one call per request.  Each request's returned logits and
+        bridge state equal its own call's (the temporary request rows aside,
+        which are free again afterwards)."""
+        if len(backends) != len(token_lists):
+            raise ValueError("one token list per backend is required")
+        suffixes = [tuple(int(t) for t in ts) for ts in token_lists]
+        bridges = [b.route_pool for b in backends]
+        if len(backends) < 2 or not fused_frontier_supported(bridges):
+            return [b.append_known_tokens_as_prefix(sfx) for b, sfx in zip(backends, suffixes)]
+        for b, sfx in zip(backends, suffixes):
+            if not sfx:
+                raise ValueError("known prefix extension cannot be empty")
+            slots = b.route_pool.prefix_slot_ids
+            if slots is None or int(slots.numel()) != len(b.prefix_token_ids):
+                raise RuntimeError("persistent Drafter prefix slots are not initialized")
+        pool = bridges[0]
+        device = pool.device
+        prefix_lens = [len(b.prefix_token_ids) for b in backends]
+        lens = [len(sfx) for sfx in suffixes]
+        seq_lens = [p + n for p, n in zip(prefix_lens, lens)]
+        handles = [_PoolReqHandle(rid="atlas-known-prefix-extend") for _ in backends]
+        indices = pool.req_to_token_pool.alloc(handles)
+        if indices is None:
+            raise RuntimeError("SGLang ReqToTokenPool.alloc returned None for known-token extend")
+        rows = _int_list(indices)
+        for h, row in zip(handles, rows):
+            h.req_pool_idx = row
+        try:
+            lasts = torch.cat([b.route_pool.prefix_slot_ids[-1:].to(torch.long) if p
+                               else torch.full((1,), -1, dtype=torch.long, device=device)
+                               for b, p in zip(backends, prefix_lens)])
+            suffix_slots = pool.allocate_extend_slots(prefix_lens=prefix_lens, seq_lens=seq_lens, last_locs=lasts)
+            offs = np.concatenate(([0], np.cumsum(lens)))
+            fulls = [torch.cat([b.route_pool.prefix_slot_ids, suffix_slots[int(offs[i]):int(offs[i + 1])]])
+                     for i, b in enumerate(backends)]
+            # every request's whole row in one tensor-index write; each bridge
+            # checks and counts its own row as its own call would
+            host = np.concatenate((np.repeat(np.asarray(rows, dtype=np.int64), seq_lens),
+                                   np.concatenate([np.arange(n, dtype=np.int64) for n in seq_lens]),
+                                   np.asarray([t for sfx in suffixes for t in sfx], dtype=np.int64),
+                                   np.concatenate([np.arange(p, q, dtype=np.int64)
+                                                   for p, q in zip(prefix_lens, seq_lens)]),
+                                   np.asarray(rows, dtype=np.int64)))
+            dev_vals = torch.from_numpy(host).to(device)
+            total, ext = sum(seq_lens), int(offs[-1])
+            row_idx, pos_idx = dev_vals[:total], dev_vals[total:2 * total]
+            input_ids = dev_vals[2 * total:2 * total + ext]
+            positions = dev_vals[2 * total + ext:2 * total + 2 * ext]
+            req_idx = dev_vals[2 * total + 2 * ext:]
+            for b, row, full in zip(backends, rows, fulls):
+                b.route_pool._check_req_write(row, 0, int(full.numel()), "full_init")
+            try:
+                pool.req_to_token_pool.write((row_idx, pos_idx), torch.cat(fulls))
+            except Exception as exc:
+                raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
+            for b, full in zip(backends, fulls):
+                b.route_pool._count_req_write(int(full.numel()), "full_init")
+            ex = executor if executor is not None else backends[0].executor
+            logits = ex.forward_extend(input_ids=input_ids, out_cache_loc=suffix_slots, positions=positions,
+                                       req_pool_indices=req_idx,
+                                       seq_lens_cpu=torch.tensor(seq_lens, dtype=torch.long))
+        finally:
+            for h in handles:
+                if hasattr(pool.req_to_token_pool, "free"):
+                    pool.req_to_token_pool.free(h)
+        # the new prefixes' pages: each old prefix's pages and those of its
+        # suffix slots (one copy to the host for all suffixes)
+        ps = int(pool.page_size)
+        suffix_host = _int_list(suffix_slots)
+        outputs = []
+        for i, (b, sfx) in enumerate(zip(backends, suffixes)):
+            pages = set(b.route_pool.prefix_page_ids)
+            pages.update(s // ps for s in suffix_host[int(offs[i]):int(offs[i + 1])])
+            b.route_pool.set_prefix_slots(fulls[i], page_ids=pages)
+            b.prefix_token_ids = (*b.prefix_token_ids, *sfx)
+            outputs.append(logits if logits.ndim == 1 else logits[int(offs[i + 1]) - 1])
         return outputs
 
 
