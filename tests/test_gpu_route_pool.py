@@ -296,3 +296,62 @@ def test_fused_frontier_rejects_out_of_range_descriptors(dev):
     assert table[1, :6].tolist() == [32, 33, 34, 35, 36, 37] and int(table[2:].abs().sum()) == 0
     assert i32[:2].tolist() == [0, 1] and i32[3].item() == 6 and i32[5].item() == 6 and i32[7].item() == 2
     assert bitmap.item() == 1 << 2
+
+
+def test_batched_extend_equals_per_request_calls_and_refusals(dev):
+    """append_known_tokens_as_prefix_many over shared native pools against
+    one append_known_tokens_as_prefix per request, from the same state (after
+    stage 1, the commit and every request's prune): the same logits rows,
+    prefix slots, prefix pages, owned pages, free list and counters.  Empty
+    suffixes and mismatched list lengths are refused before any state
+    changes."""
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    sr = pkg("flashinfer_paged.sglang_runtime")
+
+    def setup():
+        req, kv, alloc = npool.create_native_pools(num_pages=640, page_size=64, dtype=torch.bfloat16, head_num=8,
+                                                   head_dim=64, layer_num=2, max_running_requests=128,
+                                                   max_context_len=4096, device=dev)
+
+        def writer(slots, vids):
+            rows = [torch.zeros((int(slots.numel()), 8, 64), dtype=torch.bfloat16, device=dev)] * 2
+            kv.set_kv_buffer_all_layers(slots, rows, rows)
+
+        wl = dw.DrafterForkWorkload(plans=dw.config5_plans(4, 64, 7), req_pool=req, allocator=alloc, page_size=64,
+                                    device=dev, writer=writer, batched=True)
+        wl.prefill()
+        wl.stage1()
+        wl.commit()
+        for r in wl.requests:
+            r.bridge.retain_route_rows([])
+            r.bridge.release_unreferenced_node_slots([])
+        return wl, alloc
+
+    def state(wl, alloc):
+        torch.cuda.synchronize()
+        return ([r.bridge.prefix_slot_ids.tolist() for r in wl.requests],
+                [sorted(r.bridge.prefix_page_ids) for r in wl.requests],
+                [sorted(r.bridge.owned_page_ids) for r in wl.requests],
+                alloc.free_pages.tolist(), [r.bridge.hot_path_counters() for r in wl.requests],
+                [r.backend.prefix_token_ids for r in wl.requests])
+
+    suffixes = [(5, 6, 7, 8), (9,), (10, 11), (12, 13, 14, 15, 16)]
+    wl, alloc = setup()
+    backends = [r.backend for r in wl.requests]
+    before = state(wl, alloc)
+    with pytest.raises(ValueError):
+        sr.SGLangFlashInferFrontierModelBackend.append_known_tokens_as_prefix_many(backends, suffixes[:3])
+    with pytest.raises(ValueError):
+        sr.SGLangFlashInferFrontierModelBackend.append_known_tokens_as_prefix_many(backends, [(1,), (), (2,), (3,)])
+    assert state(wl, alloc) == before
+    got = sr.SGLangFlashInferFrontierModelBackend.append_known_tokens_as_prefix_many(backends, suffixes)
+    batched = state(wl, alloc)
+
+    wl2, alloc2 = setup()
+    ref = [r.backend.append_known_tokens_as_prefix(sfx) for r, sfx in zip(wl2.requests, suffixes)]
+    assert state(wl2, alloc2) == batched
+    assert len(got) == len(ref) and all(torch.equal(a, b) for a, b in zip(got, ref))
+    for r, sfx in zip(wl.requests, suffixes):
+        assert int(r.bridge.prefix_slot_ids.numel()) == len(r.backend.prefix_token_ids)
+        assert r.backend.prefix_token_ids[-len(sfx):] == sfx
