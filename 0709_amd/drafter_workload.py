@@ -34,7 +34,7 @@ import torch
 
 from .flashinfer_paged.kv import KVTreeStore
 from .flashinfer_paged.sglang_runtime import (SGLangFlashInferFrontierModelBackend, SGLangRoutePoolBridge,
-                                              fused_frontier_supported)
+                                              fused_frontier_supported, release_unreferenced_node_slots_many)
 from .flashinfer_paged.types import DecodePhase, RouteState
 
 VOCAB = 128256
@@ -258,6 +258,26 @@ class DrafterForkWorkload:
                 on_step(f"decode{t}")
 
     def commit(self) -> None:
+        """Every request commits its selected route's path up to its commit
+        depth, keeps the routes that extend it, promotes and prunes: one
+        batched call over the shared pools (``batched``), else one call per
+        request.  Both leave the same state."""
+        picks = self.select_commits()
+        if self.batched:
+            results = SGLangFlashInferFrontierModelBackend.commit_stage1_and_promote_many(
+                [r.backend for r in self.requests], [c for c, _ in picks], [k for _, k in picks])
+        else:
+            results = [req.backend.commit_stage1_and_promote(committed_route=c, retained_routes=k)
+                       for req, (c, k) in zip(self.requests, picks)]
+        for req, (promoted, stats) in zip(self.requests, results):
+            req.active = promoted
+            req.stats.append(stats)
+
+    def select_commits(self) -> list[tuple[RouteState, list[RouteState]]]:
+        """Each request's committed route (the selected final route's ancestor
+        at the commit depth) and the active routes that extend it; records the
+        selection and the committed value ids."""
+        picks = []
         for req in self.requests:
             if req.plan.select == "best":
                 # the Target's target_best order (src/atlas_0709/target_runtime.py:444-451):
@@ -273,9 +293,8 @@ class DrafterForkWorkload:
             nodes = committed.kv_view.node_ids
             keep = [r for r in req.active if r.kv_view.node_ids[: len(nodes)] == nodes]
             req.prefix_value_ids = req.prefix_value_ids + [req.node_value_ids[int(n)] for n in nodes]
-            promoted, stats = req.backend.commit_stage1_and_promote(committed_route=committed, retained_routes=keep)
-            req.active = promoted
-            req.stats.append(stats)
+            picks.append((committed, keep))
+        return picks
 
     def post_decode(self) -> None:
         self._post_steps()
@@ -286,9 +305,14 @@ class DrafterForkWorkload:
         else one call per request.  Both take the same pages in the same
         order."""
         for req in self.requests:
-            b = req.bridge
-            b.retain_route_rows([])
-            req.stats.append({"released_kv_pages": b.release_unreferenced_node_slots([])})
+            req.bridge.retain_route_rows([])
+        bridges = [r.bridge for r in self.requests]
+        if self.batched:
+            released = release_unreferenced_node_slots_many(bridges, [[] for _ in bridges])
+        else:
+            released = [b.release_unreferenced_node_slots([]) for b in bridges]
+        for req, n in zip(self.requests, released):
+            req.stats.append({"released_kv_pages": n})
         before = self.ids.next
         if self.batched:
             SGLangFlashInferFrontierModelBackend.append_known_tokens_as_prefix_many(

@@ -104,14 +104,19 @@ class DeviceOwnedPages:
     def sweep(self, live_slots: torch.Tensor) -> torch.Tensor:
         """owned -= pages not reachable from live_slots; returns the released
         pages (ascending, on the device)."""
+        self.sweep_launch(live_slots)
+        n = int(self.free_count.item())
+        return self.free_pages[:n]
+
+    def sweep_launch(self, live_slots: torch.Tensor) -> None:
+        """The sweep without reading its count back: the released pages land
+        in ``free_pages[:free_count]`` on the device."""
         s = live_slots.reshape(-1).to(device=self.device, dtype=torch.int64).contiguous()
         lib = _lib.load()
         rc = lib.atlas_prune_pages(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, _lib.ptr(s),
                                    int(s.numel()), self.page_size, _lib.ptr(self.free_pages),
                                    _lib.ptr(self.free_count), _lib.stream_of(self.device))
         _lib.check(rc, "atlas_prune_pages")
-        n = int(self.free_count.item())
-        return self.free_pages[:n]
 
     # -- set protocol -----------------------------------------------------
     def to_set(self) -> set[int]:
@@ -430,9 +435,12 @@ class SGLangRoutePoolBridge:
                 self.req_to_token_pool.free(row.handle)
 
     # ------------------------------------------------------------ promote / prune
-    def commit_route_as_prefix(self, route: RouteState) -> torch.Tensor:
+    def commit_route_as_prefix(self, route: RouteState, *, defer_page_ids: bool = False) -> torch.Tensor:
         """Zero-copy promotion: the route's slot path becomes the prefix and
-        its tail lease carries over (``sglang_runtime.py:357-378``)."""
+        its tail lease carries over (``sglang_runtime.py:357-378``).  With
+        ``defer_page_ids`` the prefix's host page-id set is left for the
+        caller to refresh (``refresh_prefix_page_ids`` reads several bridges'
+        sets back in one copy)."""
         old_len = 0 if self.prefix_slot_ids is None else int(self.prefix_slot_ids.numel())
         path = self._slot_path_for_route(route)
         expected = old_len + len(route.kv_view.node_ids)
@@ -441,7 +449,8 @@ class SGLangRoutePoolBridge:
                 f"cannot promote route KV to prefix: slot_path_len={int(path.numel())}, expected={expected}"
             )
         self.prefix_slot_ids = path
-        self._refresh_prefix_cpu_metadata()
+        if not defer_page_ids:
+            self._refresh_prefix_cpu_metadata()
         self.prefix_partial_tail_keys.clear()
         n = int(path.numel())
         self.prefix_tail_page_key = self.route_tail_page_keys.get(int(route.route_id)) if n % self.page_size else None
@@ -528,17 +537,8 @@ class SGLangRoutePoolBridge:
         retained route reaches, in ascending page order; forget dead node
         mappings (``sglang_runtime.py:507-539``).  Returns the page count."""
         self.check_pending_device_checks()
-        live_nodes = {int(n) for n in live_node_ids}
         if self._device_ownership:
-            parts = []
-            if self.prefix_slot_ids is not None and int(self.prefix_slot_ids.numel()):
-                parts.append(self.prefix_slot_ids[:: self.page_size])
-            for path in self.route_slot_paths.values():
-                if int(path.numel()):
-                    parts.append(path[:: self.page_size])
-                    parts.append(path[-1:])
-            live = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.long, device=self.device)
-            released = self.owned_page_ids.sweep(live)
+            released = self.owned_page_ids.sweep(self._live_slot_samples())
             count = int(released.numel())
         else:
             self._materialize_pending_owned_pages()
@@ -547,19 +547,37 @@ class SGLangRoutePoolBridge:
                 live_pages.update(pages)
             releasable = sorted(self.owned_page_ids - live_pages)
             count = len(releasable)
-        for node in list(self.node_slot_ids):
-            if int(node) not in live_nodes:
-                self.node_slot_ids.pop(int(node), None)
+        self._forget_dead_nodes(live_node_ids)
         if count:
-            free = getattr(self.token_to_kv_pool_allocator, "free", None)
-            if not callable(free):
-                raise RuntimeError("SGLang token-to-KV allocator does not expose free()")
+            self._require_allocator_free()
             if self._device_ownership:
                 self.token_to_kv_pool_allocator.free_pages_prepend(released.clone())
             else:
-                free(torch.tensor([p * self.page_size for p in releasable], dtype=torch.long, device=self.device))
+                self.token_to_kv_pool_allocator.free(
+                    torch.tensor([p * self.page_size for p in releasable], dtype=torch.long, device=self.device))
                 self.owned_page_ids.difference_update(releasable)
         return count
+
+    def _live_slot_samples(self) -> torch.Tensor:
+        """One slot of every page the prefix and the retained routes reach:
+        each path's page-start slots plus its last slot."""
+        parts = []
+        if self.prefix_slot_ids is not None and int(self.prefix_slot_ids.numel()):
+            parts.append(self.prefix_slot_ids[:: self.page_size])
+        for path in self.route_slot_paths.values():
+            if int(path.numel()):
+                parts.append(path[:: self.page_size])
+                parts.append(path[-1:])
+        return torch.cat(parts) if parts else torch.zeros(0, dtype=torch.long, device=self.device)
+
+    def _forget_dead_nodes(self, live_node_ids: Sequence[int]) -> None:
+        live_nodes = {int(n) for n in live_node_ids}
+        for node in [n for n in self.node_slot_ids if n not in live_nodes]:
+            del self.node_slot_ids[node]
+
+    def _require_allocator_free(self) -> None:
+        if not callable(getattr(self.token_to_kv_pool_allocator, "free", None)):
+            raise RuntimeError("SGLang token-to-KV allocator does not expose free()")
 
     def clear_physical_state(self) -> None:
         """``sglang_runtime.py:541-576``."""
@@ -951,8 +969,7 @@ class SGLangRoutePoolBridge:
         self.attention_metadata_builds += 1
         self.attention_metadata_token_indices += sum(plan.prevs) + len(plan.prevs)
         self.attention_metadata_page_indices += sum((p + ps) // ps for p in plan.prevs)
-        validate = bool(self.validate_page_layout)
-        self.pending_device_checks.append(lambda: flags.check(group, validate))
+        self.pending_device_checks.append(_StepCheck(flags, group, bool(self.validate_page_layout)))
 
     def _check_or_defer(self, ok: torch.Tensor, message: str) -> None:
         """A device-computed condition is checked at the next report boundary
@@ -965,7 +982,9 @@ class SGLangRoutePoolBridge:
 
     def check_pending_device_checks(self) -> None:
         """Raise the first failed deferred condition (layout of frontier page
-        metadata, distinct output slots) recorded since the last check."""
+        metadata, distinct output slots) recorded since the last check.  The
+        flags of all pending fused frontier steps come back in one copy."""
+        _prefetch_step_flags([self])
         pending, self.pending_device_checks = self.pending_device_checks, []
         for check in pending:
             check()
@@ -1119,6 +1138,38 @@ class _FusedFrontierPlan:
     kinds: list[str]
 
 
+class _StepCheck:
+    """A deferred check of one request's group in a fused frontier step."""
+
+    def __init__(self, step_flags: "_StepFlags", group: int, validate_layout: bool) -> None:
+        self.step_flags = step_flags
+        self.group = int(group)
+        self.validate_layout = validate_layout
+
+    def __call__(self) -> None:
+        self.step_flags.check(self.group, self.validate_layout)
+
+
+def _prefetch_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> None:
+    """Reads the flags of every fused frontier step with a check pending on
+    these bridges, in one device-to-host copy."""
+    steps, seen = [], set()
+    for b in bridges:
+        for c in b.pending_device_checks:
+            f = getattr(c, "step_flags", None)
+            if f is not None and f._host is None and id(f) not in seen:
+                seen.add(id(f))
+                steps.append(f)
+    if len(steps) < 2:
+        return
+    flat = _int_list(torch.cat([f.flags.reshape(-1) for f in steps]))
+    off = 0
+    for f in steps:
+        n = int(f.flags.numel())
+        f._host = flat[off:off + n]
+        off += n
+
+
 class _StepFlags:
     """Check flags of one fused frontier step (device int64s the kernel
     clears on a failed check), read back once, at the first check."""
@@ -1183,6 +1234,52 @@ def fused_frontier_supported(bridges: Sequence[SGLangRoutePoolBridge]) -> bool:
         if int(b.page_size) != int(b0.page_size) or not b._device_ownership or not b.use_page_attention_metadata:
             return False
     return True
+
+
+def refresh_prefix_page_ids(bridges: Sequence[SGLangRoutePoolBridge]) -> None:
+    """Each bridge's host copy of its prefix page ids (what
+    ``_refresh_prefix_cpu_metadata`` sets), read back in one copy for all."""
+    parts, counts = [], []
+    for b in bridges:
+        slots = b.prefix_slot_ids
+        if slots is None or int(slots.numel()) == 0:
+            counts.append(0)
+            continue
+        parts.append(torch.div(slots[:: b.page_size], b.page_size, rounding_mode="floor"))
+        counts.append(int(parts[-1].numel()))
+    flat = _int_list(torch.cat(parts)) if parts else []
+    off = 0
+    for b, c in zip(bridges, counts):
+        b.prefix_slot_count = 0 if b.prefix_slot_ids is None else int(b.prefix_slot_ids.numel())
+        b.prefix_page_ids = set(flat[off:off + c])
+        off += c
+
+
+def release_unreferenced_node_slots_many(bridges: Sequence[SGLangRoutePoolBridge],
+                                         live_node_id_lists: Sequence[Sequence[int]]) -> list[int]:
+    """``release_unreferenced_node_slots`` of several bridges.  Over one native
+    allocator (``fused_frontier_supported``) every bridge's sweep is launched,
+    the released-page counts come back in one copy and the released pages are
+    prepended bridge by bridge, so the free list ends as one call per bridge in
+    this order leaves it; the deferred device checks of all bridges run first.
+    Otherwise one call per bridge.  Returns the page counts."""
+    if len(bridges) != len(live_node_id_lists):
+        raise ValueError("one live node list per bridge is required")
+    if len(bridges) < 2 or not fused_frontier_supported(bridges):
+        return [b.release_unreferenced_node_slots(live) for b, live in zip(bridges, live_node_id_lists)]
+    _prefetch_step_flags(bridges)
+    for b in bridges:
+        b.check_pending_device_checks()
+    for b in bridges:
+        b.owned_page_ids.sweep_launch(b._live_slot_samples())
+    counts = _int_list(torch.cat([b.owned_page_ids.free_count for b in bridges]))
+    alloc = bridges[0].token_to_kv_pool_allocator
+    for b, live, n in zip(bridges, live_node_id_lists, counts):
+        b._forget_dead_nodes(live)
+        if n:
+            b._require_allocator_free()
+            alloc.free_pages_prepend(b.owned_page_ids.free_pages[:n])
+    return counts
 
 
 def prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
@@ -1391,6 +1488,52 @@ class SGLangFlashInferFrontierModelBackend:
             "released_route_rows": released_rows,
             "released_kv_pages": released_pages,
         }
+
+    @staticmethod
+    def commit_stage1_and_promote_many(backends: Sequence["SGLangFlashInferFrontierModelBackend"],
+                                       committed_routes: Sequence[RouteState],
+                                       retained_route_lists: Sequence[Sequence[RouteState]]) -> list[tuple]:
+        """``commit_stage1_and_promote`` of several requests.  When their
+        bridges share native pools: the promotions and row releases run request
+        by request on the host, then every request's prefix page ids come back
+        in one copy and the prunes share one count read-back
+        (``release_unreferenced_node_slots_many``), so the free list, the
+        request rows and each request's state end as one call per request in
+        this order leaves them.  Requests with no committed node and the
+        deferred device checks are refused before any state changes.
+        Otherwise one call per request.  Returns each request's
+        ``(promoted routes, stats)``."""
+        if not (len(backends) == len(committed_routes) == len(retained_route_lists)):
+            raise ValueError("one committed route and one retained list per backend are required")
+        bridges = [b.route_pool for b in backends]
+        if len(backends) < 2 or not fused_frontier_supported(bridges):
+            return [b.commit_stage1_and_promote(committed_route=c, retained_routes=k)
+                    for b, c, k in zip(backends, committed_routes, retained_route_lists)]
+        node_paths = [b.route_store.node_path_for_route(c) for b, c in zip(backends, committed_routes)]
+        if not all(node_paths):
+            raise ValueError("cannot commit a stage-1 route with no materialized nodes")
+        _prefetch_step_flags(bridges)
+        for br in bridges:
+            br.check_pending_device_checks()
+        results, lives = [], []
+        for b, committed, keep, nodes in zip(backends, committed_routes, retained_route_lists, node_paths):
+            tokens = b.route_store.tokens_for_node_ids(nodes)
+            b.route_pool.commit_route_as_prefix(committed, defer_page_ids=True)
+            stored = b.route_store.commit_route(committed)
+            if stored != tokens:
+                raise RuntimeError("logical committed tokens changed during route promotion")
+            b.prefix_token_ids = (*b.prefix_token_ids, *tokens)
+            promoted = b.route_store.promote_routes_after_commit(
+                committed, keep, PrefixKVView(committed_length=len(b.prefix_token_ids)))
+            released_rows = b.route_pool.retain_route_rows([r.route_id for r in promoted])
+            lives.append(sorted({int(n) for r in promoted for n in r.kv_view.node_ids}))
+            results.append((promoted, {"committed_kv_tokens": len(nodes), "retained_routes": len(promoted),
+                                       "released_route_rows": released_rows}))
+        refresh_prefix_page_ids(bridges)
+        counts = release_unreferenced_node_slots_many(bridges, lives)
+        for (_, stats), n in zip(results, counts):
+            stats["released_kv_pages"] = n
+        return results
 
     @torch.inference_mode()
     def decode_frontier_one_token(self, active_routes: Sequence[RouteState],

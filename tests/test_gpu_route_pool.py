@@ -6,6 +6,8 @@ arithmetic fixes (free, owned and padding pages partition the pool, no
 duplicate free page, live slots on their own request's pages), and
 configuration 1 must commit the route the Target's target_best order picks."""
 
+import dataclasses
+
 import pytest
 import torch
 
@@ -355,3 +357,75 @@ def test_batched_extend_equals_per_request_calls_and_refusals(dev):
     for r, sfx in zip(wl.requests, suffixes):
         assert int(r.bridge.prefix_slot_ids.numel()) == len(r.backend.prefix_token_ids)
         assert r.backend.prefix_token_ids[-len(sfx):] == sfx
+
+
+def test_batched_commit_equals_per_request_calls_and_refusals(dev):
+    """commit_stage1_and_promote_many over shared native pools against one
+    commit_stage1_and_promote per request, from the same state (after stage
+    1): the same promoted routes and stats, prefix slots and pages, owned
+    pages, node slots, request rows, free list and counters, and the same
+    state again after the EXTEND phase's batched prunes.  Mismatched list
+    lengths and a committed route with no materialized node are refused
+    before any state changes."""
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    sr = pkg("flashinfer_paged.sglang_runtime")
+
+    def setup(batched_commit):
+        req, kv, alloc = npool.create_native_pools(num_pages=640, page_size=64, dtype=torch.bfloat16, head_num=8,
+                                                   head_dim=64, layer_num=2, max_running_requests=128,
+                                                   max_context_len=4096, device=dev)
+
+        def writer(slots, vids):
+            rows = [torch.zeros((int(slots.numel()), 8, 64), dtype=torch.bfloat16, device=dev)] * 2
+            kv.set_kv_buffer_all_layers(slots, rows, rows)
+
+        wl = dw.DrafterForkWorkload(plans=dw.config5_plans(5, 64, 11), req_pool=req, allocator=alloc, page_size=64,
+                                    device=dev, writer=writer, batched=True)
+        wl.prefill()
+        wl.stage1()
+        wl.batched = batched_commit
+        return wl, alloc, req
+
+    def state(wl, alloc, req):
+        torch.cuda.synchronize()
+        b = [r.bridge for r in wl.requests]
+        return ([x.prefix_slot_ids.tolist() for x in b], [sorted(x.prefix_page_ids) for x in b],
+                [x.prefix_slot_count for x in b], [sorted(x.owned_page_ids) for x in b],
+                [sorted(x.node_slot_ids) for x in b], [sorted(x.route_rows) for x in b],
+                [sorted(x.route_slot_paths) for x in b], [x.prefix_tail_page_key for x in b],
+                alloc.free_pages.tolist(), list(req._free_rows), [x.hot_path_counters() for x in b],
+                [r.backend.prefix_token_ids for r in wl.requests])
+
+    wl, alloc, req = setup(True)
+    backends = [r.backend for r in wl.requests]
+    before = state(wl, alloc, req)
+    picks = wl.select_commits()
+    many = sr.SGLangFlashInferFrontierModelBackend.commit_stage1_and_promote_many
+    with pytest.raises(ValueError):
+        many(backends, [c for c, _ in picks][:4], [k for _, k in picks])
+    c2 = picks[2][0]
+    root = dataclasses.replace(c2, kv_view=dataclasses.replace(c2.kv_view, node_ids=()))  # no materialized node
+    with pytest.raises(ValueError):
+        many(backends, [c for c, _ in picks[:2]] + [root] + [c for c, _ in picks[3:]], [k for _, k in picks])
+    assert state(wl, alloc, req) == before
+    got = many(backends, [c for c, _ in picks], [k for _, k in picks])
+    batched = state(wl, alloc, req)
+
+    wl2, alloc2, req2 = setup(False)
+    picks2 = wl2.select_commits()
+    ref = [r.backend.commit_stage1_and_promote(committed_route=c, retained_routes=k)
+           for r, (c, k) in zip(wl2.requests, picks2)]
+    assert state(wl2, alloc2, req2) == batched
+    assert [[int(x.route_id) for x in p] for p, _ in got] == [[int(x.route_id) for x in p] for p, _ in ref]
+    assert [s for _, s in got] == [s for _, s in ref]
+    assert sum(s["released_kv_pages"] for _, s in got) > 0
+
+    # the EXTEND phase's prunes: one count read-back for all against one call each
+    for w, results, batched_prune in ((wl, got, True), (wl2, ref, False)):
+        for r, (promoted, _) in zip(w.requests, results):
+            r.active = promoted
+        w.batched = batched_prune
+        w.fallback_extend()
+    assert state(wl, alloc, req) == state(wl2, alloc2, req2)
+    assert [r.stats for r in wl.requests] == [r.stats for r in wl2.requests]

@@ -587,6 +587,31 @@ def test_fused_step_flags_raise_in_prepare_frontier_order():
     sr._StepFlags(torch.tensor([1, 0, 1, 1], dtype=torch.int64)).check(0, False)  # layout not validated
 
 
+def test_pending_step_checks_read_in_one_copy_and_raise_in_order():
+    """The flags of every fused step with a check pending on a set of bridges
+    are read once, together; the checks then raise in the order recorded,
+    and a bridge's pending list is empty after its checks ran."""
+    sr, _ = _mods()
+
+    class Bridge:
+        check_pending_device_checks = sr.SGLangRoutePoolBridge.check_pending_device_checks
+
+        def __init__(self, checks):
+            self.pending_device_checks = checks
+
+    good = sr._StepFlags(torch.tensor([1, 1, 1, 1, 1, 1, 1], dtype=torch.int64))
+    bad = sr._StepFlags(torch.tensor([1, 1, 1, 1, 1, 0, 1], dtype=torch.int64))  # group 1: duplicate slots
+    a = Bridge([sr._StepCheck(good, 0, True), sr._StepCheck(bad, 0, True)])
+    b = Bridge([sr._StepCheck(good, 1, True), sr._StepCheck(bad, 1, True)])
+    sr._prefetch_step_flags([a, b])
+    assert good._host == [1] * 7 and bad._host == [1, 1, 1, 1, 1, 0, 1]
+    a.check_pending_device_checks()
+    assert a.pending_device_checks == []
+    with pytest.raises(RuntimeError, match="duplicate output KV slots"):
+        b.check_pending_device_checks()
+    assert b.pending_device_checks == []
+
+
 def test_batched_workload_on_host_pools_equals_per_request_calls():
     """On host pools the batched drafter workload falls back to one bridge
     call per request and leaves the same state."""
