@@ -223,3 +223,58 @@ def test_paged_metadata_argument_errors(dev):
         pm.build_flashinfer_paged_kv_metadata([torch.tensor([0.0], device=dev)], page_size=16)
     with pytest.raises(ValueError):
         pm.build_flashinfer_paged_kv_metadata([torch.zeros(0, dtype=torch.long, device=dev)], page_size=16)
+
+
+@pytest.mark.parametrize("num_pages,n_slots", [(4096, 900), (524289, 3000)])
+def test_mark_and_prune_graph_replays(dev, num_pages, n_slots):
+    """Ownership marks and a prune (one workgroup, or the clear + mark + sweep
+    launches of a pool too large for LDS) captured in one HIP graph and
+    replayed from the same starting bitmaps, with eager work in between:
+    every replay gives the eager run's owned bitmap, free list and count,
+    which equal the oracle's."""
+    lib = _lib()
+    rng = np.random.default_rng(num_pages + 1)
+    ps = 16
+    owned0 = set(rng.choice(num_pages, size=min(num_pages // 2, 5000), replace=False).tolist())
+    new_pages = rng.choice(num_pages, size=64, replace=False).tolist()
+    owned_bm = _bitmap(owned0, num_pages, dev)
+    start = owned_bm.clone()
+    live_bm = torch.zeros_like(owned_bm)
+    free = torch.full((num_pages,), -1, dtype=torch.int64, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+    marks = torch.tensor([p * ps + 3 for p in new_pages], dtype=torch.int64, device=dev)
+    live = torch.tensor(rng.integers(0, num_pages * ps, size=n_slots).tolist(), dtype=torch.int64, device=dev)
+    L = lib.load()
+
+    def work():
+        lib.check(L.atlas_mark_pages(lib.ptr(owned_bm), num_pages, lib.ptr(marks), int(marks.numel()), ps,
+                                     lib.stream_of(dev)), "mark")
+        lib.check(L.atlas_prune_pages(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, lib.ptr(live), n_slots, ps,
+                                      lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev)), "prune")
+
+    work()
+    torch.cuda.synchronize()
+    n = int(cnt.item())
+    eager = (owned_bm.clone(), free[:n].clone(), n)
+    exp_freed, exp_left = ref.prune(owned0 | set(new_pages), None,
+                                    [[int(s)] for s in live.cpu().tolist()], ps)
+    assert free[:n].cpu().tolist() == exp_freed and _set_from_bitmap(owned_bm) == exp_left
+    owned_bm.copy_(start)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        work()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    for rep in range(4):
+        owned_bm.copy_(start)
+        free.fill_(-1)
+        cnt.zero_()
+        scratch = torch.randn(1 << 20, device=dev).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert float(scratch) == float(scratch)
+        assert int(cnt.item()) == eager[2], f"replay {rep}: count differs"
+        assert torch.equal(owned_bm, eager[0]) and torch.equal(free[: eager[2]], eager[1]), f"replay {rep} differs"
