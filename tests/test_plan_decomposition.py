@@ -148,7 +148,7 @@ def request_mix(draw):
     return qo_lens, kv_lens, hq, hkv, d, ps, ws_rows_cap, split_target, max_rows
 
 
-@settings(max_examples=300, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+@settings(max_examples=300, deadline=None, derandomize=True, suppress_health_check=[HealthCheck.too_slow])
 @given(request_mix())
 def test_random_request_mixes_are_covered_exactly_once(mix):
     qo_lens, kv_lens, hq, hkv, d, ps, ws_rows_cap, split_target, max_rows = mix
