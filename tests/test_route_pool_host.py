@@ -630,3 +630,48 @@ def test_batched_workload_on_host_pools_equals_per_request_calls():
                 [q.bridge.hot_path_counters() for q in wl.requests])
 
     assert run(True) == run(False)
+
+
+def test_multi_request_commit_and_prune_refusals_on_host_pools():
+    """The multi-request commit and prune refuse mismatched list lengths
+    before any state changes; on host pools they make one call per request,
+    so the stats equal the per-request calls'."""
+    dw = pkg("drafter_workload")
+    sr, _ = _mods()
+    from oracle.route_pool import OracleAllocator, OracleReqPool
+
+    def setup():
+        alloc = OracleAllocator(num_pages=640, page_size=64)
+        rows = OracleReqPool(size=128, max_context_len=4096)
+        wl = dw.DrafterForkWorkload(plans=dw.config5_plans(3, 64, 9), req_pool=rows, allocator=alloc, page_size=64,
+                                    device="cpu", writer=lambda s, v: alloc.kv.write(s.numpy(), v.numpy()),
+                                    use_page_attention_metadata=False, batched=True)
+        wl.prefill()
+        wl.stage1()
+        return wl, alloc
+
+    wl, alloc = setup()
+    backends = [r.backend for r in wl.requests]
+    picks = wl.select_commits()
+    free_before = list(alloc.free_pages)
+    with pytest.raises(ValueError):
+        sr.SGLangFlashInferFrontierModelBackend.commit_stage1_and_promote_many(
+            backends, [c for c, _ in picks][:2], [k for _, k in picks])
+    with pytest.raises(ValueError):
+        sr.release_unreferenced_node_slots_many([r.bridge for r in wl.requests], [[]])
+    assert list(alloc.free_pages) == free_before
+    got = sr.SGLangFlashInferFrontierModelBackend.commit_stage1_and_promote_many(
+        backends, [c for c, _ in picks], [k for _, k in picks])
+    wl2, alloc2 = setup()
+    ref = [r.backend.commit_stage1_and_promote(committed_route=c, retained_routes=k)
+           for r, (c, k) in zip(wl2.requests, wl2.select_commits())]
+    assert [s for _, s in got] == [s for _, s in ref]
+    assert list(alloc.free_pages) == list(alloc2.free_pages)
+    bridges = [r.bridge for r in wl.requests]
+    for b in bridges:
+        b.retain_route_rows([])
+    counts = sr.release_unreferenced_node_slots_many(bridges, [[] for _ in bridges])
+    for b in [r.bridge for r in wl2.requests]:
+        b.retain_route_rows([])
+    assert counts == [b.release_unreferenced_node_slots([]) for b in [r.bridge for r in wl2.requests]]
+    assert list(alloc.free_pages) == list(alloc2.free_pages)
