@@ -134,17 +134,22 @@ def _check_kv(kv, values, slots, layers, heads, head_dim, dev, phase):
 
 
 @pytest.mark.parametrize("case", ["config1", "config5_seed0", "config5_seed1", "config1_batched",
-                                  "config5_seed0_batched", "config5_seed1_batched", "config5_seed2_batched"])
+                                  "config5_seed0_batched", "config5_seed1_batched", "config5_seed2_batched",
+                                  "config5_seed3_batched", "config5_ps16_seed4", "config5_ps16_seed5_batched"])
 def test_route_pool_trace_matches_host_pools(dev, case):
     """The ``_batched`` cases run each decode step of all requests as one
-    fused frontier step against the same per-request host trace."""
+    fused frontier step (and the commit, prune and EXTEND as one call each)
+    against the same per-request host trace; the ``_ps16`` cases use pages of
+    16 tokens."""
     dw = pkg("drafter_workload")
     batched = case.endswith("_batched")
     name = case.removesuffix("_batched")
     if name == "config1":
         plans, ps, pages = dw.config1_plans(0), 16, 4096
     else:
-        plans, ps, pages = dw.config5_plans(8, 64, int(name[-1])), 64, 640
+        # config5[_ps16]_seed<k>: the fork stress with pages of 64 (or 16) tokens
+        ps = 16 if "_ps16_" in name else 64
+        plans, pages = dw.config5_plans(8, ps, int(name.rsplit("seed", 1)[1])), 640 if ps == 64 else 2560
     layers, heads, head_dim = 16, 8, 64
     print(f"route-pool trace {case}: page_size {ps}, {pages} pages", flush=True)
     host = []
