@@ -124,6 +124,33 @@ def test_fused_verify_forward_equals_separate_ops(dev):
         assert torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+def test_three_verify_rounds_fused_equals_separate(dev):
+    """Three verify rounds in a row, each committing its selected route into
+    the prefix (300 tokens grow past the page boundary at 304, so the paged
+    prefix grows): the fused and the separate forward agree at every round
+    on the selection, committed tokens, per-token log-probs and prefix
+    logits, and end with bit-equal KV pages."""
+    model = _model(dev, 7)
+    runs = []
+    for fused in (True, False):
+        b = _backend(dev, model, prefix_len=300, seed=8)
+        b.fused_verify_step = fused
+        rounds = []
+        for r in range(3):
+            res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=_routes(20 + r))
+            torch.cuda.synchronize()
+            rounds.append((res.selected_route_id, b.prefix_token_ids, [sc.token_logprobs for sc in res.scores],
+                           b._prefix_logits.clone().view(torch.int16)))
+        runs.append((rounds, [x.clone() for x in b._paged_prefix_kv]))
+    (ra, kva), (rb, kvb) = runs
+    assert len(ra[-1][1]) > 304  # the committed prefix crossed a page boundary
+    for (sa, pa, la, xa), (sb, pb, lb, xb) in zip(ra, rb):
+        assert sa == sb and pa == pb and la == lb and torch.equal(xa, xb)
+    assert len(kva) == len(kvb)
+    for x, y in zip(kva, kvb):
+        assert x.shape == y.shape and torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
 def _dense_step_logits(model, cache, seq_len, token, pos):
     """One decode step of the tiny model in float32 over the first seq_len
     rows of the paged cache (whose row pos already holds this token's K/V,
