@@ -98,3 +98,49 @@ def test_target_sample_refusals():
                                selection_score=math.nan)]
     with pytest.raises(ValueError):
         b._select_route(nan, route_sampling_seed=1, route_sampling_round=0)
+
+
+def test_truncation_matches_oracle_and_reference_literal():
+    """``_truncate_selected_path`` (target_runtime.py:675-700): the reference
+    literal (tests/test_target_kv_commit.py:345-367), then seeded random paths,
+    limits and EOS ids against the oracle, refusals included."""
+    tr = pkg("target_runtime")
+    cut = tr.DirectFlashInferMaskedTreeVerifyBackend._truncate_selected_path
+    assert cut(token_ids=(10, 11, 12, 13), node_ids=(20, 21, 22, 23), max_tokens=3, eos_token_id=11) == \
+        ((10, 11), (20, 21))
+    rng = random.Random(5)
+    for _ in range(500):
+        n = rng.randint(1, 6)
+        toks = tuple(rng.randint(0, 5) for _ in range(n))
+        nodes = tuple(range(100, 100 + n))
+        limit = rng.choice([None, 1, 2, 3, 8])
+        eos = rng.choice([None, 0, 3, 9])
+        assert cut(token_ids=toks, node_ids=nodes, max_tokens=limit, eos_token_id=eos) == \
+            osc.truncate_path(toks, nodes, limit, eos)
+    for bad in (dict(token_ids=(), node_ids=(), max_tokens=None, eos_token_id=None),
+                dict(token_ids=(1, 2), node_ids=(3,), max_tokens=None, eos_token_id=None),
+                dict(token_ids=(1,), node_ids=(3,), max_tokens=0, eos_token_id=None)):
+        with pytest.raises(ValueError):
+            cut(**bad)
+
+
+def test_weights_and_fallback_reasons():
+    """Score weights must match the route depth; a selected route below the
+    first-token or the path threshold gives the reference's fallback reason
+    (target_runtime.py:708-720 order: first token first)."""
+    ty = pkg("types")
+    b = _backend("target_best")
+    b.score_weights = (0.5, 0.25)
+    assert b._weights_for_depth(2) == (0.5, 0.25)
+    with pytest.raises(ValueError):
+        b._weights_for_depth(3)
+    s = ty.TargetRouteScore(route_id=1, token_ids=(1, 2), target_logprob=-3.0, draft_logprob=0.0,
+                            first_token_logprob=-2.0, selection_score=-3.0)
+    b.first_token_threshold, b.fallback_threshold = None, None
+    assert b._fallback_reason(s) is None
+    b.fallback_threshold = -2.5
+    assert b._fallback_reason(s) == "path_score_below_threshold"
+    b.first_token_threshold = -1.0
+    assert b._fallback_reason(s) == "first_token_below_threshold"
+    b.first_token_threshold, b.fallback_threshold = -2.0, -3.0
+    assert b._fallback_reason(s) is None  # equal to a threshold is not below it
