@@ -75,3 +75,26 @@ def test_gather_logprobs_workspace_contract_without_device_work():
     rc = lib.atlas_gather_logprobs(fake, 128256, 34, None, 0, 0, 128256, lib_mod.DTYPE_F16, fake, fake, 4, None,
                                    fake, fake, need - 1, None)
     assert rc == lib_mod.ATLAS_EINVAL and b"workspace" in lib.atlas_last_error()
+
+
+def test_every_entry_point_refuses_null_buffers_before_device_work():
+    """Every compute entry point, called with NULL for every pointer and 1
+    for every count (``float`` arguments 1.0), returns ATLAS_EINVAL with a
+    message, without touching a device (this runs without a GPU)."""
+    import ctypes
+
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    queries = {"atlas_last_error", "atlas_abi_version", "atlas_gather_logprobs_workspace_bytes",
+               "atlas_frontier_workspace_bytes"}
+    ints = (ctypes.c_int, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64)
+    checked = []
+    for name, argtypes in lib_mod._SIGNATURES.items():
+        if name in queries:
+            continue
+        args = [1 if t in ints else 1.0 if t in (ctypes.c_float, ctypes.c_double) else None for t in argtypes]
+        rc = getattr(lib, name)(*args)
+        assert rc == lib_mod.ATLAS_EINVAL, f"{name} returned {rc}"
+        assert lib.atlas_last_error(), f"{name} left no error message"
+        checked.append(name)
+    assert len(checked) == len(_declared_symbols()) - len(queries)
