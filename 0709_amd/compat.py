@@ -11,11 +11,21 @@ this package in:
 * it is not: the same call registers this package's modules under the
   reference's module names in ``sys.modules``.
 
+The reference's wrapper factories (``make_prefill_wrapper``,
+``plan_prefill_wrapper``, ``make_decode_wrapper``, ``plan_decode_wrapper``,
+``flashinfer_full_verify.py:877-927``) are always replaced, so the verify and
+fallback-decode attention run on the gfx950 kernels whether or not some
+``flashinfer`` is importable: this package's factories ignore the
+``flashinfer`` module they are handed.
+
 ``flashinfer=True`` also registers a ``flashinfer`` module exposing
 ``BatchPrefillWithPagedKVCacheWrapper``, ``BatchDecodeWithPagedKVCacheWrapper``
 and ``packbits`` backed by the gfx950 kernels, when no ``flashinfer`` is
-importable (the reference creates its verify and decode wrappers through those
-names, ``flashinfer_full_verify.py:502-507``, ``:882-888``, ``:953``).
+importable, for code that constructs the wrappers by name (the reference's
+``import flashinfer`` in ``target_runtime.py:99`` and
+``flashinfer_full_verify.py:502-507``).  An importable ``flashinfer`` is left
+in place; what constructs its wrappers directly (SGLang's own attention
+backend inside the Drafter's model forward) then still runs it.
 """
 
 from __future__ import annotations
@@ -52,11 +62,12 @@ HOT_PATH: dict[str, tuple[str, tuple[str, ...]]] = {
         "flashinfer_full_verify", ("TreeSpec", "build_path_tree_tokens_from_paths", "build_deduplicated_path_tree_tokens",
                                    "ancestors_inclusive", "build_tree_spec_from_paths",
                                    "build_deduplicated_tree_spec_from_paths", "prefix_layer_to_paged_kv",
-                                   "write_suffix_kv", "first_tensor", "packbits", "make_decode_wrapper",
-                                   "plan_decode_wrapper")),
+                                   "write_suffix_kv", "first_tensor", "packbits", "make_prefill_wrapper",
+                                   "plan_prefill_wrapper", "make_decode_wrapper", "plan_decode_wrapper")),
     "atlas_0709.target_runtime": (
-        "target_runtime", ("VerifyRoutePayload", "DirectFlashInferMaskedTreeVerifyBackend")),
-    "atlas_0709.types": ("types", ("TargetRouteScore", "TargetVerifyResult")),
+        "target_runtime", ("VerifyRoutePayload", "verify_payload_from_mapping",
+                           "DirectFlashInferMaskedTreeVerifyBackend")),
+    "atlas_0709.types": ("types", ("PrefixState", "TargetRouteScore", "TargetVerifyResult")),
 }
 
 
@@ -65,7 +76,11 @@ def _ours(rel: str):
 
 
 def install_atlas_0709_alias(*, flashinfer: bool = False) -> dict[str, str]:
-    """Returns {reference module name: "patched" | "registered"}."""
+    """Returns {reference module name: "patched" | "registered"}, plus
+    ``"flashinfer"``: ``"registered"`` or ``"present"`` when
+    ``flashinfer=True``.  Call it before the reference's entry modules
+    (``target_server``, ``rpc``, ``distributed_system``) are imported: they
+    bind the hot-path names at import time."""
     done: dict[str, str] = {}
     for ref_name, (rel, names) in HOT_PATH.items():
         ours = _ours(rel)
@@ -94,6 +109,8 @@ def install_atlas_0709_alias(*, flashinfer: bool = False) -> dict[str, str]:
             shim.__doc__ = "FlashInfer verify and decode attention names backed by the gfx950 paged-attention kernels."
             sys.modules["flashinfer"] = shim
             done["flashinfer"] = "registered"
+        else:
+            done["flashinfer"] = "present"
     return done
 
 

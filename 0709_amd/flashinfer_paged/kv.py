@@ -33,6 +33,13 @@ class KVTreeStore:
         self.committed_token_ids: list[int] = []
         self._release_hooks: list[Callable[[Sequence[RouteState], Sequence[RouteState]], None]] = []
 
+    def reset_speculative(self) -> None:
+        """Forget every node and route; the committed tokens and the id
+        counters stay (``kv.py:37-39``: the fallback EXTEND handoff drops the
+        speculative forest this way before rebuilding stage 1)."""
+        self.nodes.clear()
+        self.routes.clear()
+
     def add_route_release_hook(self, hook) -> None:
         self._release_hooks.append(hook)
 

@@ -20,6 +20,7 @@ freed-page order identical):
 from __future__ import annotations
 
 import ctypes
+import sys
 import time
 from dataclasses import dataclass, field
 from typing import Any, Sequence
@@ -1399,6 +1400,12 @@ class SGLangFlashInferFrontierModelBackend:
     * ``forward_extend(input_ids=, out_cache_loc=, positions=,
       req_pool_indices=, seq_lens_cpu=) -> logits [n, V] or [V]``
       (one EXTEND of a known causal suffix).
+
+    The reference's SGLang executor (``forward_frontier`` and a
+    ``model_runner``, no ``forward_extend``; what ``from_runner`` builds when
+    the reference is loaded) works too: the EXTEND then runs as an SGLang
+    ``ForwardBatch`` on its runner, and each forward is preceded by the
+    reference's runner set-up, as in its own backend.
     """
 
     def __init__(self, *, route_store: KVTreeStore, executor: Any, route_pool: SGLangRoutePoolBridge) -> None:
@@ -1410,6 +1417,29 @@ class SGLangFlashInferFrontierModelBackend:
         hook = getattr(route_store, "add_route_release_hook", None)
         if callable(hook):
             hook(route_pool.reconcile_route_rows)
+
+    @classmethod
+    def from_runner(cls, *, route_store: KVTreeStore, model_runner: Any, page_size: int,
+                    device: str | torch.device = "cuda", executor: Any = None) -> "SGLangFlashInferFrontierModelBackend":
+        """``sglang_runtime.py:1139-1151``: a route pool over the runner's
+        request and KV pools (``SGLangRoutePoolBridge.from_runner``, which
+        checks the page size) and an executor that runs the Drafter model on
+        the runner.  The model forward is the caller's: ``executor`` when
+        given, else the reference's ``SGLangFlashInferPagedDecodeBackend``
+        (after the reference's runner defaults and FlashInfer check) when the
+        reference package is loaded beside this one.  Without either it
+        raises ``RuntimeError`` before touching the runner."""
+        if executor is None:
+            ref = _reference_runtime()
+            if ref is None:
+                raise RuntimeError(
+                    "from_runner needs the Drafter model executor: pass executor=, or load atlas_0709 (its "
+                    "SGLangFlashInferPagedDecodeBackend runs the SGLang ModelRunner)")
+            ref.ensure_sglang_runner_runtime_defaults(model_runner)
+            ref.assert_sglang_flashinfer_active(model_runner)
+            executor = ref.SGLangFlashInferPagedDecodeBackend(model_runner=model_runner, page_size=page_size)
+        route_pool = SGLangRoutePoolBridge.from_runner(model_runner, page_size=page_size, device=device)
+        return cls(route_store=route_store, executor=executor, route_pool=route_pool)
 
     def attach_prefilled_prefix(self, *, prompt_token_ids: Sequence[int], prefix_slot_ids,
                                 next_token_logits: torch.Tensor) -> DraftPrefixState:
@@ -1452,11 +1482,12 @@ class SGLangFlashInferFrontierModelBackend:
             suffix_slots = pool.allocate_extend_slots(prefix_lens=[prefix_len], seq_lens=[seq_len], last_locs=last)
             full = torch.cat([prefix_slots, suffix_slots])
             pool._write_req_token_row(row, full)
-            logits = self.executor.forward_extend(
-                input_ids=torch.tensor(suffix, dtype=torch.long, device=device), out_cache_loc=suffix_slots,
+            logits = _forward_extend(
+                self.executor, input_ids=torch.tensor(suffix, dtype=torch.long, device=device),
+                out_cache_loc=suffix_slots,
                 positions=torch.arange(prefix_len, seq_len, dtype=torch.long, device=device),
                 req_pool_indices=torch.tensor([row], dtype=torch.long, device=device),
-                seq_lens_cpu=torch.tensor([seq_len], dtype=torch.long))
+                seq_lens_cpu=torch.tensor([seq_len], dtype=torch.long), prefix_lens=[prefix_len])
         finally:
             if hasattr(pool.req_to_token_pool, "free"):
                 pool.req_to_token_pool.free(handle)
@@ -1542,6 +1573,7 @@ class SGLangFlashInferFrontierModelBackend:
         before = self.route_pool.hot_path_counters()
         new_nodes = self.route_store.reserve_node_ids(len(active_routes))
         input_ids, metadata = self.route_pool.prepare_frontier(active_routes)
+        _ready_runner(self.executor)
         logits = self.executor.forward_frontier(input_ids=input_ids, route_kv_metadata=metadata)
         self.route_pool.register_node_slots(new_nodes, metadata.out_cache_loc)
         ids = [int(r.route_id) for r in active_routes]
@@ -1560,8 +1592,11 @@ class SGLangFlashInferFrontierModelBackend:
             model_ms=(time.perf_counter() - start) * 1000.0,
             metadata={
                 "backend": "atlas_hip_paged_decode",
+                "reference_only": False,
                 "paged_kv": True,
+                "cascade": False,
                 "route_tail_page_cow": True,
+                "branch_safe_page_size": True,
                 "cow_pages_copied_total": int(self.route_pool.cow_pages_copied),
                 "cow_tokens_copied_total": int(self.route_pool.cow_tokens_copied),
                 "attention_metadata_page_size": int(page_size),
@@ -1570,6 +1605,7 @@ class SGLangFlashInferFrontierModelBackend:
                 "hot_path_counter_delta": {k: int(after[k] - before.get(k, 0)) for k in after},
                 "hot_path_counters_total": after,
                 "attention_backend": str(attention_backend),
+                **_executor_metadata(self.executor),
             },
         )
 
@@ -1594,6 +1630,7 @@ class SGLangFlashInferFrontierModelBackend:
         new_nodes = [b.route_store.reserve_node_ids(len(rs)) for b, rs in zip(backends, route_lists)]
         step = prepare_frontiers(bridges, route_lists)
         ex = executor if executor is not None else backends[0].executor
+        _ready_runner(ex)
         logits = ex.forward_frontier(input_ids=step.input_ids, route_kv_metadata=step.metadata)
         out_slots = step.metadata.out_cache_loc
         outputs = []
@@ -1627,7 +1664,10 @@ class SGLangFlashInferFrontierModelBackend:
             raise ValueError("one token list per backend is required")
         suffixes = [tuple(int(t) for t in ts) for ts in token_lists]
         bridges = [b.route_pool for b in backends]
-        if len(backends) < 2 or not fused_frontier_supported(bridges):
+        union_ex = executor if executor is not None else (backends[0].executor if backends else None)
+        if len(backends) < 2 or not fused_frontier_supported(bridges) or not hasattr(union_ex, "forward_extend"):
+            # a runner-backed executor (no forward_extend) returns one logits
+            # row per request, so its EXTENDs stay one per request
             return [b.append_known_tokens_as_prefix(sfx) for b, sfx in zip(backends, suffixes)]
         for b, sfx in zip(backends, suffixes):
             if not sfx:
@@ -1677,8 +1717,7 @@ class SGLangFlashInferFrontierModelBackend:
                 raise RuntimeError("failed to write SGLang req_to_token_pool route row") from exc
             for b, full in zip(backends, fulls):
                 b.route_pool._count_req_write(int(full.numel()), "full_init")
-            ex = executor if executor is not None else backends[0].executor
-            logits = ex.forward_extend(input_ids=input_ids, out_cache_loc=suffix_slots, positions=positions,
+            logits = union_ex.forward_extend(input_ids=input_ids, out_cache_loc=suffix_slots, positions=positions,
                                        req_pool_indices=req_idx,
                                        seq_lens_cpu=torch.tensor(seq_lens, dtype=torch.long))
         finally:
@@ -1697,6 +1736,100 @@ class SGLangFlashInferFrontierModelBackend:
             b.prefix_token_ids = (*b.prefix_token_ids, *sfx)
             outputs.append(logits if logits.ndim == 1 else logits[int(offs[i + 1]) - 1])
         return outputs
+
+
+# ------------------------------------------------------------------ executor glue
+# The Drafter model forward is the caller's.  An executor either implements
+# forward_frontier / forward_extend itself (the contract documented on
+# SGLangFlashInferFrontierModelBackend), or is the reference's SGLang executor
+# (``flashinfer_backends.py:64-121``: forward_frontier only, plus the
+# ModelRunner it drives), in which case the reference's runner helpers run the
+# forward exactly as its own backend does.
+
+_REFERENCE_RUNTIME = "atlas_0709.flashinfer_paged.sglang_runtime"
+
+
+def _reference_runtime():
+    """The reference's route-pool module when it is loaded beside this
+    package (the alias installed over it), else None."""
+    mod = sys.modules.get(_REFERENCE_RUNTIME)
+    if mod is None or mod is sys.modules.get(__name__):
+        return None
+    return mod
+
+
+def _ready_runner(executor: Any) -> None:
+    """Before a forward on a runner-backed executor: the reference's runner
+    defaults and eager runner (``sglang_runtime.py:1309-1310``)."""
+    runner = getattr(executor, "model_runner", None)
+    ref = _reference_runtime()
+    if runner is None or ref is None:
+        return
+    ref.ensure_sglang_runner_runtime_defaults(runner)
+    ref.ensure_sglang_eager_runner(runner)
+
+
+def _executor_metadata(executor: Any) -> dict:
+    """The executor's own runtime metadata, when it reports any
+    (``sglang_runtime.py:1344``)."""
+    meta = getattr(executor, "runtime_metadata", None)
+    return dict(meta(cascade_level=0, verify_backend="none")) if callable(meta) else {}
+
+
+def _forward_extend(executor: Any, *, input_ids: torch.Tensor, out_cache_loc: torch.Tensor,
+                    positions: torch.Tensor, req_pool_indices: torch.Tensor, seq_lens_cpu: torch.Tensor,
+                    prefix_lens: Sequence[int]) -> torch.Tensor:
+    """One EXTEND forward of known tokens: the executor's ``forward_extend``
+    when it has one; otherwise an SGLang EXTEND ``ForwardBatch`` run on the
+    executor's ModelRunner, with the fields the reference fills
+    (``sglang_runtime.py:1211-1242``), one request per entry of
+    ``seq_lens_cpu``."""
+    fwd = getattr(executor, "forward_extend", None)
+    if callable(fwd):
+        return fwd(input_ids=input_ids, out_cache_loc=out_cache_loc, positions=positions,
+                   req_pool_indices=req_pool_indices, seq_lens_cpu=seq_lens_cpu)
+    runner = getattr(executor, "model_runner", None)
+    ref = _reference_runtime()
+    if runner is None or ref is None:
+        raise RuntimeError("the Drafter executor has no forward_extend and no SGLang ModelRunner to run an EXTEND on")
+    forward_batch_cls, forward_mode_cls = ref._sglang_forward_batch_classes()
+    device = input_ids.device
+    seq_cpu = [int(x) for x in seq_lens_cpu.tolist()]
+    pre = [int(x) for x in prefix_lens]
+    ext = [a - b for a, b in zip(seq_cpu, pre)]
+    starts = [0]
+    for n in ext[:-1]:
+        starts.append(starts[-1] + n)
+    seq_lens = seq_lens_cpu.to(device=device)
+    batch = forward_batch_cls(
+        forward_mode=ref._forward_mode(forward_mode_cls, ("EXTEND", "PREFILL")),
+        batch_size=len(seq_cpu),
+        input_ids=input_ids,
+        req_pool_indices=req_pool_indices,
+        seq_lens=seq_lens,
+        out_cache_loc=out_cache_loc,
+        seq_lens_sum=sum(seq_cpu),
+        orig_seq_lens=seq_lens,
+        positions=positions,
+        seq_lens_cpu=seq_lens_cpu,
+        capture_hidden_mode=ref._capture_hidden_mode_null(),
+        is_extend_in_batch=True,
+        all_extend_in_batch=True,
+        extend_num_tokens=sum(ext),
+        extend_seq_lens=torch.tensor(ext, device=device, dtype=torch.long),
+        extend_prefix_lens=torch.tensor(pre, device=device, dtype=torch.long),
+        extend_start_loc=torch.tensor(starts, device=device, dtype=torch.long),
+        extend_seq_lens_cpu=ext,
+        extend_prefix_lens_cpu=pre,
+        extend_logprob_start_lens_cpu=[n - 1 for n in ext],
+    )
+    ref.ensure_sglang_runner_runtime_defaults(runner)
+    ref.ensure_sglang_eager_runner(runner)
+    logits = ref._extract_next_token_logits(runner.forward(batch))
+    if device.type == "cuda":
+        # the reference synchronises after the EXTEND forward (:1242)
+        torch.cuda.synchronize(device)
+    return logits
 
 
 _COUNTERS = (

@@ -43,9 +43,12 @@ from .flashinfer_full_verify import (
     prefix_layer_to_paged_kv,
     write_suffix_kv,
 )
-from .types import TargetRouteScore, TargetVerifyResult
+from .types import PrefixState, TargetRouteScore, TargetVerifyResult
 
 ROUTE_POLICIES = ("target_best", "target_sample", "first_route")
+# what runs the verify attention, reported where the reference reports its
+# FlashInfer version
+ATTENTION_LIBRARY = "atlas0709-hip-gfx950"
 
 
 @dataclass(frozen=True)
@@ -317,7 +320,9 @@ class DirectFlashInferMaskedTreeVerifyBackend:
 
     # ------------------------------------------------------------ prefill
     @torch.inference_mode()
-    def prefill(self, prompt_token_ids: Sequence[int]):
+    def prefill(self, prompt_token_ids: Sequence[int]) -> PrefixState:
+        """Prompt forward of the caller's model, its K/V laid out as the
+        committed paged prefix (``target_runtime.py:114-142``)."""
         token_ids = tuple(int(t) for t in prompt_token_ids)
         if not token_ids:
             raise ValueError("target prefill requires a non-empty prompt")
@@ -335,7 +340,56 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         self._paged_prefix_kv = layers
         self._prefix_logits = out.logits[:, -1, :].detach()
         self._committed_verify_rounds = 0
-        return self._prefix_logits[0]
+        self._last_fallback_ar_profile = None
+        return PrefixState(token_ids=token_ids, next_token_logits=self._prefix_logits[0],
+                           committed_length=len(token_ids), metadata=self.runtime_metadata())
+
+    def runtime_metadata(self) -> dict[str, object]:
+        """The keys of the reference's ``runtime_metadata``
+        (``target_runtime.py:322-359``), read by the health call and the edge
+        controller's policy checks.  ``backend`` keeps the reference's name so
+        callers that key on it still match; ``flashinfer_version`` names the
+        kernel library that runs the attention instead (no FlashInfer is
+        involved)."""
+        cfg = self.config
+        tok = self.tokenizer
+        model_cfg = getattr(self.model, "config", None)
+        vocab = getattr(model_cfg, "vocab_size", None)
+        return {
+            "backend": "direct_flashinfer_full_llama_masked_verify",
+            "model": self.model_path,
+            "model_vocab_size": None if vocab is None else int(vocab),
+            "tokenizer_vocab_size": None if tok is None else int(len(tok)),
+            "tokenizer_bos_token_id": getattr(tok, "bos_token_id", None),
+            "tokenizer_eos_token_id": getattr(tok, "eos_token_id", None),
+            "tokenizer_pad_token_id": getattr(tok, "pad_token_id", None),
+            "paged_kv": True,
+            "custom_mask": True,
+            "packed_custom_mask": bool(getattr(cfg, "use_packed_custom_mask", False)),
+            "rope_applied": True,
+            "logits_aligned": None,
+            "runtime_alignment_checked": False,
+            "semantic_correctness_required": True,
+            "page_size": cfg.page_size,
+            "dtype": getattr(cfg, "dtype", None),
+            "device": getattr(cfg, "device", None),
+            "flashinfer_version": ATTENTION_LIBRARY,
+            "persistent_target_paged_kv": True,
+            "deduplicated_tree_nodes": True,
+            "selection_policy": self._selection_policy_name(),
+            "route_selection_policy": self.route_selection_policy,
+            "route_sampling_scope": "verified_route_level_only",
+            "route_sampling_temperature": float(self.route_sampling_temperature),
+            "fallback_ar_sampling": "greedy_argmax",
+            "score_weights": None if self.score_weights is None else [float(w) for w in self.score_weights],
+            "fallback_threshold": self.fallback_threshold,
+            "first_token_threshold": self.first_token_threshold,
+            "fallback_ar_tokens": int(self.fallback_ar_tokens),
+            "fallback_decode_wrapper_reused": True,
+            "profile_fallback_ar": self.profile_fallback_ar,
+            "committed_verify_rounds": self._committed_verify_rounds,
+            "committed_prefix_length": len(self.prefix_token_ids),
+        }
 
     # ------------------------------------------------------------ verify
     @torch.inference_mode()
@@ -390,12 +444,15 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                                  page_size=self.config.page_size, fused=self.fused_verify_step)
         scores = self._score_routes(routes=routes, paths=paths, prefix_logits=self._prefix_logits[0],
                                     verify_logits=logits, route_to_node_paths=route_nodes)
+        best = max(scores, key=lambda s: (self._selection_score(s), s.draft_path_logprob, -s.route_id))
         selected, sampling_meta = self._select_route_with_metadata(
             scores, route_sampling_seed=route_sampling_seed, route_sampling_round=route_sampling_round
         )
-        best = max(scores, key=lambda s: (self._selection_score(s), s.draft_path_logprob, -s.route_id))
         reason = self._fallback_reason(selected)
+        # the key order of target_runtime.py:235-252 (later keys override the
+        # runtime metadata's)
         common = {
+            **self.runtime_metadata(),
             "route_count": len(routes),
             "path_depth": int(depth),
             "node_count": int(tree.node_count),
@@ -403,8 +460,17 @@ class DirectFlashInferMaskedTreeVerifyBackend:
             "kv_len": int(tree.kv_len),
             "prefix_len_before": len(self.prefix_token_ids),
             "selection_policy": self._selection_policy_name(),
-            "best_route_id": int(best.route_id),
+            "selection_score_name": "weighted_target_logprob" if self.score_weights is not None else "target_logprob",
+            "fallback_threshold": self.fallback_threshold,
+            "first_token_threshold": self.first_token_threshold,
+            "fallback_ar_tokens": int(self.fallback_ar_tokens),
             **sampling_meta,
+            **self._route_intervention_metadata(scores, selected),
+        }
+        best_meta = {
+            "best_route_id": int(best.route_id),
+            "best_selection_score": float(self._selection_score(best)),
+            "best_first_token_logprob": None if best.first_token_logprob is None else float(best.first_token_logprob),
         }
         if reason is not None:
             generated = self._generate_fallback_ar(
@@ -426,6 +492,7 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                     "fallback_triggered": True,
                     "fallback_reason": reason,
                     "fallback_token_count": len(generated),
+                    **best_meta,
                     "fallback_ar_profile": self._last_fallback_ar_profile,
                 },
             )
@@ -442,7 +509,9 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                 "target_kv_commit": "selected_tree_path_in_place",
                 "target_reprefill_after_verify": False,
                 "fallback_triggered": False,
+                **best_meta,
                 "selected_route_id": int(selected.route_id),
+                "selected_selection_score": float(self._selection_score(selected)),
                 "selected_path_committed_tokens": len(path),
                 "selected_path_was_truncated": len(path) != len(paths[idx]),
             },
@@ -526,6 +595,72 @@ class DirectFlashInferMaskedTreeVerifyBackend:
     @staticmethod
     def _token_path_hash(token_ids: Sequence[int]) -> str:
         return hashlib.sha256(json.dumps([int(t) for t in token_ids], separators=(",", ":")).encode("utf-8")).hexdigest()
+
+    def _route_intervention_metadata(self, scores: Sequence[TargetRouteScore],
+                                     selected: TargetRouteScore) -> dict[str, object]:
+        """Audit of the Target's choice against the first payload route
+        ("route0") and the Drafter's own top route (highest current-path draft
+        log-prob, earliest on ties), with the aggregated fields repeated at
+        the top level (``target_runtime.py:567-660``)."""
+        if not scores:
+            raise ValueError("route intervention metadata requires non-empty scores")
+        route0 = scores[0]
+        by_draft = sorted(range(len(scores)), key=lambda i: (-float(scores[i].draft_path_logprob), i))
+        rank = {int(scores[i].route_id): r for r, i in enumerate(by_draft, start=1)}
+        draft_top = scores[by_draft[0]]
+        sel_score = self._selection_score
+
+        def summary(s: TargetRouteScore) -> dict[str, object]:
+            return {
+                "route_id": int(s.route_id),
+                "token_path_hash": self._token_path_hash(s.token_ids),
+                "first_token_id": int(s.token_ids[0]),
+                "draft_rank": int(rank[int(s.route_id)]),
+                "draft_first_token_logprob": s.draft_first_token_logprob,
+                "draft_path_logprob": float(s.draft_path_logprob),
+                "legacy_cumulative_draft_logprob": float(s.draft_logprob),
+                "target_first_token_logprob": None if s.first_token_logprob is None else float(s.first_token_logprob),
+                "target_logprob": float(s.target_logprob),
+                "target_selection_score": float(sel_score(s)),
+            }
+
+        def delta(a, b):
+            return None if a is None or b is None else float(a) - float(b)
+
+        def versus(base: TargetRouteScore) -> dict[str, object]:
+            return {
+                "route_changed": tuple(selected.token_ids) != tuple(base.token_ids),
+                "first_token_changed": int(selected.token_ids[0]) != int(base.token_ids[0]),
+                "draft_first_token_logprob_delta": delta(selected.draft_first_token_logprob,
+                                                         base.draft_first_token_logprob),
+                "draft_path_logprob_delta": float(selected.draft_path_logprob) - float(base.draft_path_logprob),
+                "legacy_cumulative_draft_logprob_delta": float(selected.draft_logprob) - float(base.draft_logprob),
+                "target_first_token_logprob_delta": delta(selected.first_token_logprob, base.first_token_logprob),
+                "target_path_logprob_delta": float(selected.target_logprob) - float(base.target_logprob),
+                "target_selection_score_delta": sel_score(selected) - sel_score(base),
+            }
+
+        vs0, vs_top = versus(route0), versus(draft_top)
+        return {
+            "route_intervention": {
+                "baseline": "route0",
+                "draft_token_logprobs_available": bool(all(s.draft_token_logprobs for s in scores)),
+                "route0_is_draft_top": int(route0.route_id) == int(draft_top.route_id),
+                "route0": summary(route0),
+                "draft_top": summary(draft_top),
+                "selected": summary(selected),
+                "selected_vs_route0": vs0,
+                "selected_vs_draft_top": vs_top,
+            },
+            "selected_draft_rank": int(rank[int(selected.route_id)]),
+            "route0_route_id": int(route0.route_id),
+            "draft_top_route_id": int(draft_top.route_id),
+            "selected_route_changed_from_route0": bool(vs0["route_changed"]),
+            "selected_first_token_changed_from_route0": bool(vs0["first_token_changed"]),
+            "selected_minus_route0_draft_first_token_logprob": vs0["draft_first_token_logprob_delta"],
+            "selected_minus_route0_draft_logprob": float(vs0["draft_path_logprob_delta"]),
+            "selected_minus_route0_target_selection_score": float(vs0["target_selection_score_delta"]),
+        }
 
     def _sample_target_route(self, scores, *, route_sampling_seed, route_sampling_round):
         """Seeded route draw (``target_runtime.py:454-546``): canonical

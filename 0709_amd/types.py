@@ -1,10 +1,23 @@
-"""Result types carried across the Target verify boundary (reference
-``atlas_0709/types.py:105-148``)."""
+"""Types carried across the Target verify boundary (reference
+``atlas_0709/types.py:15-20``, ``:105-148``)."""
 
 from __future__ import annotations
 
 from dataclasses import dataclass, field
 from typing import Any, Mapping
+
+import torch
+
+
+@dataclass(frozen=True)
+class PrefixState:
+    """What ``prefill`` returns: the committed prompt, the logits of the token
+    after it, its length and the backend's runtime metadata."""
+
+    token_ids: tuple[int, ...]
+    next_token_logits: torch.Tensor
+    committed_length: int
+    metadata: Mapping[str, Any] = field(default_factory=dict)
 
 
 @dataclass(frozen=True)

@@ -203,3 +203,68 @@ def test_fallback_ar_decodes_on_the_prefix_pages(dev):
             if float(top2[0] - top2[1]) > 2e-2:
                 assert int(torch.argmax(dense)) == toks[i + 1], f"step {i}: greedy token differs"
     assert float((b._prefix_logits.float() - dense).abs().max()) <= 2e-2
+
+
+def _hf_llama(dev, seed):
+    """A transformers Llama of the tiny geometry above (random weights)."""
+    from transformers import LlamaConfig, LlamaForCausalLM
+
+    torch.manual_seed(seed)
+    cfg = LlamaConfig(vocab_size=VOCAB, hidden_size=HIDDEN, intermediate_size=2 * HIDDEN, num_hidden_layers=LAYERS,
+                      num_attention_heads=HQ, num_key_value_heads=HKV, head_dim=D, max_position_embeddings=1024,
+                      rope_theta=500000.0, attn_implementation="sdpa")
+    m = LlamaForCausalLM(cfg)
+    with torch.no_grad():
+        m.model.embed_tokens.weight.normal_(0.0, 1.0)
+    return m.half().to(dev).eval()
+
+
+def test_rpc_sequence_from_prefill_on_a_transformers_llama(dev):
+    """The reference server's sequence (rpc.py:66-128) from a real prefill:
+    health, prefill of a 300-token prompt through the model's own forward and
+    KV cache, then two verifies with commits.  Each selected route's per-token
+    log-probs match the model's own dense forward over the committed prefix
+    and the route (fp16 activations through two layers: 3e-2), the metadata
+    carries the reference's keys, and the prefix grows by the committed
+    routes."""
+    from standin_callers import (RUNTIME_METADATA_KEYS, VERIFY_COMMON_KEYS, VERIFY_SELECT_KEYS,
+                                 TargetRpcStandIn)
+
+    tr = pkg("target_runtime")
+    model = _hf_llama(dev, 11)
+    cfg = SimpleNamespace(k=3, d=4, page_size=PS, device=str(dev), dtype="float16", workspace_mb=64,
+                          flashinfer_backend="auto", use_packed_custom_mask=False)
+    backend = tr.DirectFlashInferMaskedTreeVerifyBackend(model_path="tiny-llama", config=cfg, model=model)
+    app = TargetRpcStandIn(backend, tr.verify_payload_from_mapping)
+    health = app.health()
+    assert tuple(health["metadata"]) == RUNTIME_METADATA_KEYS and health["metadata"]["committed_prefix_length"] == 0
+    g = torch.Generator().manual_seed(12)
+    prompt = [int(x) for x in torch.randint(0, VOCAB, (300,), generator=g)]
+    pre = app.prefill({"prompt_token_ids": prompt})
+    assert pre["prompt_len"] == 300 and pre["metadata"]["committed_prefix_length"] == 300
+    assert len(backend._paged_prefix_kv) == LAYERS and backend._paged_prefix_kv[0].shape[1:] == (2, PS, HKV, D)
+    prefix = list(prompt)
+    for rnd in range(2):
+        routes = [{"route_id": 10 * rnd + i, "token_ids": [int(x) for x in torch.randint(0, VOCAB, (4,), generator=g)],
+                   "draft_logprob": -0.5 * i} for i in range(3)]
+        routes[1]["token_ids"][:2] = routes[0]["token_ids"][:2]  # a shared prefix: 10 unique nodes
+        out = app.verify({"prefix_token_ids": prefix, "routes": routes})
+        torch.cuda.synchronize()
+        meta = out["metadata"]
+        for key in RUNTIME_METADATA_KEYS + VERIFY_COMMON_KEYS + VERIFY_SELECT_KEYS:
+            assert key in meta, key
+        assert meta["node_count"] == 10 and meta["prefix_len_before"] == len(prefix)
+        with torch.no_grad():
+            for s in out["scores"]:
+                ids = torch.tensor([prefix + s["token_ids"]], device=dev)
+                lps = torch.log_softmax(model(input_ids=ids).logits[0].float(), dim=-1)
+                want = [float(lps[len(prefix) - 1 + t, s["token_ids"][t]]) for t in range(4)]
+                assert s["token_logprobs"] == pytest.approx(want, abs=3e-2), (rnd, s["route_id"])
+        sel = out["selected_score"]
+        prefix = prefix + sel["token_ids"]
+        assert list(backend.prefix_token_ids) == prefix and meta["prefix_len_after"] == len(prefix)
+    assert app.health()["metadata"]["committed_verify_rounds"] == 2
+    # the next prefix logits are the model's own after the committed prefix
+    with torch.no_grad():
+        dense = model(input_ids=torch.tensor([prefix], device=dev)).logits[0, -1].float()
+    assert float((backend._prefix_logits[0].float() - dense).abs().max()) <= 5e-2
