@@ -51,15 +51,14 @@ struct Vec {
 
 // Workgroup (c, r) reads chunk c of logits row r once: the chunk's maximum m
 // and the sum of exp(x - m), kept online per thread (16-byte loads when the
-// rows are 16-byte aligned), then reduced over the workgroup.  It writes the
-// pair through to memory (agent scope: read by whichever XCD finishes the
-// row) into its slot of the row, then reads the row's slots: the workgroup
-// that finds all of them filled -- at least the last one to store, possibly
-// several, which then write the same values -- combines the pairs in chunk
-// order (a fixed order, so the LSE is the same on every run), writes the row
-// LSE and every gather of row r, and empties the slots for the next call.  A
-// slot is (max bits, ~sum bits): a non-negative sum has its sign bit clear,
-// so a filled slot has bit 63 set and an empty (zero) slot has not.
+// rows are 16-byte aligned), then reduced over the workgroup.  It stores the
+// pair into its slot of the row and counts itself in on the row's arrival
+// counter with one agent-scope read-modify-write that releases the slot; the
+// workgroup that arrives last (the counter held num_chunks - 1) acquires
+// every slot, combines the pairs in chunk order (a fixed order, so the LSE is
+// the same on every run), writes the row LSE and every gather of row r, and
+// empties the slots and the counter for the next call.  A slot is
+// (max bits, ~sum bits); every slot is written before its workgroup arrives.
 struct GatherArgs {
   const char* logits;
   int64_t row_stride_bytes;
@@ -72,7 +71,8 @@ struct GatherArgs {
   int64_t n;
   float* row_lse;
   float* out;
-  uint64_t* slots;  // [num_rows, num_chunks], zero between calls
+  uint64_t* slots;     // [num_rows, num_chunks], zero between calls
+  uint32_t* arrivals;  // [num_rows], zero between calls
   int num_chunks;
   int64_t chunk_len;  // elements, a multiple of 8 (the last chunk may be shorter)
 };
@@ -80,7 +80,6 @@ struct GatherArgs {
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 constexpr int kPre = 2;  // gathers per thread whose logits are loaded ahead of the combine
-constexpr uint64_t kFilled = 1ull << 63;
 
 // (m, s) pairs: s is a sum of exp(x - m).
 __device__ __forceinline__ void pair_merge(float& m, float& s, float m2, float s2) {
@@ -94,7 +93,7 @@ template <int DT, bool VEC>
 __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a) {
   __shared__ float red_m[kThreads / 64];
   __shared__ float red_s[kThreads / 64];
-  __shared__ int full_sh;
+  __shared__ int last_sh;
   __shared__ float lse_sh;
   constexpr int EPV = Vec<DT>::kElems;
   const int c = blockIdx.x;
@@ -168,32 +167,34 @@ __global__ __launch_bounds__(kThreads) void gather_logprobs_kernel(GatherArgs a)
     for (int w = 1; w < kThreads / 64; ++w) pair_merge(bm, bs, red_m[w], red_s[w]);
     const uint64_t slot = uint64_t(__float_as_uint(bm)) | (uint64_t(~__float_as_uint(bs)) << 32);
     __hip_atomic_store(rs + c, slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    __builtin_amdgcn_s_waitcnt(0 | (7 << 4) | (15 << 8));  // vmcnt(0): the slot is in memory
+    // The release orders the slot before the arrival; the last arriver's
+    // acquire then sees every slot (all earlier arrivals released theirs).
+    const uint32_t prev = __hip_atomic_fetch_add(a.arrivals + r, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    const bool last = prev == uint32_t(a.num_chunks - 1);
+    if (last) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    last_sh = last;
   }
   __syncthreads();
+  if (!last_sh) return;
 
-  // Read the row's slots; combine in chunk order (one per lane of wave 0,
-  // then a fixed pairwise tree) when all are filled.
+  // The last arriver: combine the row's slots in chunk order (one per lane of
+  // wave 0, then a fixed pairwise tree).
   if (t < 64) {
     float cm = -INFINITY, cs = 0.f;
-    bool all = true;
     for (int k = t; k < a.num_chunks; k += 64) {
       const uint64_t v = __hip_atomic_load(rs + k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      all = all && (v & kFilled) != 0;
       pair_merge(cm, cs, __uint_as_float(uint32_t(v)), __uint_as_float(~uint32_t(v >> 32)));
     }
-    const bool full = __builtin_amdgcn_ballot_w64(!all) == 0;
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) pair_merge(cm, cs, __shfl_xor(cm, off), __shfl_xor(cs, off));
-    if (t == 0) {
-      full_sh = full;
-      lse_sh = cm + __builtin_log2f(cs) * kLn2;
-    }
+    if (t == 0) lse_sh = cm + __builtin_log2f(cs) * kLn2;
   }
   __syncthreads();
-  if (!full_sh) return;
   const float lse = lse_sh;
-  if (t == 0 && a.row_lse) a.row_lse[r] = lse;
+  if (t == 0) {
+    if (a.row_lse) a.row_lse[r] = lse;
+    __hip_atomic_store(a.arrivals + r, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   for (int k = t; k < a.num_chunks; k += kThreads)
     __hip_atomic_store(rs + k, uint64_t(0), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
@@ -234,7 +235,8 @@ GatherGeom gather_geom(int64_t num_rows, int64_t vocab) {
 extern "C" int64_t atlas_gather_logprobs_workspace_bytes(int64_t num_rows, int64_t vocab) {
   if (num_rows <= 0 || vocab <= 0 || num_rows >= (int64_t(1) << 31)) return -1;
   const GatherGeom g = gather_geom(num_rows, vocab);
-  return int64_t(size_t(num_rows) * g.num_chunks * sizeof(uint64_t));
+  // the slots, then one arrival counter per row
+  return int64_t(size_t(num_rows) * g.num_chunks * sizeof(uint64_t) + size_t(num_rows) * sizeof(uint32_t));
 }
 
 extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t num_rows,
@@ -270,6 +272,7 @@ extern "C" int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride,
   a.row_lse = row_lse_dev;
   a.out = out_dev;
   a.slots = static_cast<uint64_t*>(workspace_dev);
+  a.arrivals = reinterpret_cast<uint32_t*>(a.slots + total_rows * g.num_chunks);
   a.num_chunks = g.num_chunks;
   a.chunk_len = g.chunk_len;
   hipStream_t s = static_cast<hipStream_t>(stream);

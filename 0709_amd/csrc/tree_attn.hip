@@ -65,6 +65,7 @@ struct AttnArgs {
   float* lse;
   uint16_t* part_o;  // normalised partial O rows in the output dtype
   float* part_lse;    // base-2 LSE of each partial row
+  int64_t part_rows;  // rows the partial area holds; split rows at or past it are not written
   // Fused append (head_dim-128 kernel): K / V rows of each request's newest
   // qo_len tokens, [token, head, D] with these strides (elements), or null.
   const char* app_k;
@@ -583,6 +584,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
         a.lse[int64_t(qo_start + node_of[rt]) * a.num_qo_heads + head_of[rt]] = lse2 * kLn2;
     } else {
       const int64_t prow = int64_t(w.partial_row) + lr;
+      if (prow >= a.part_rows) continue;
       char* po = reinterpret_cast<char*>(a.part_o + prow * D);
 #pragma unroll
       for (int dt = 0; dt < DT; ++dt) {
@@ -602,6 +604,7 @@ struct MergeArgs {
   const int32_t* qo_indptr;
   const uint16_t* part_o;
   const float* part_lse;
+  int64_t part_rows;  // rows the partial area holds; items reaching past it are skipped
   char* out;
   int64_t out_stride_token;
   int64_t out_stride_head;
@@ -725,6 +728,7 @@ __global__ __launch_bounds__(kMergeThreads) void tree_attn_merge_kernel(MergeArg
   const atlas_attn_merge_t mi = a.merge[blockIdx.x];
   const int row = blockIdx.y * kMergeRowsPerBlock + (threadIdx.x >> 6);
   if (row >= mi.num_rows) return;
+  if (mi.partial_row < 0 || int64_t(mi.partial_row) + int64_t(mi.num_splits) * mi.num_rows > a.part_rows) return;
   merge_row<D, BF16>(a, mi, row, threadIdx.x & 63);
 }
 
@@ -1356,6 +1360,7 @@ __device__ __forceinline__ void d128_store(const AttnArgs& a, const atlas_attn_w
   if (!row_ok) return;
   const bool final_row = w.partial_row < 0;
   const int64_t prow = int64_t(w.partial_row) + lrow;
+  if (!final_row && prow >= a.part_rows) return;
   char* orow = final_row ? a.out + ((int64_t(c.qo_start + node) * a.out_stride_token +
                                      int64_t(head) * a.out_stride_head) * 2)
                          : reinterpret_cast<char*>(a.part_o + prow * D);
@@ -1778,13 +1783,21 @@ extern "C" int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int nu
   return launch_status("attn_page_windows_kernel");
 }
 
-static int verify_attn_impl(
+namespace {
+int current_device_scratch(void** out);
+}
+
+// use_scratch: the split partial states go to the library's device scratch
+// array (workspace_dev is ignored, workspace_bytes gives the rows in use);
+// its address is looked up only after every argument has been checked.
+static int verify_attn_impl(bool use_scratch,
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
+    int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream, const void* append_k, const void* append_v, int64_t append_stride_token,
@@ -1856,15 +1869,25 @@ static int verify_attn_impl(
 
   MergeArgs margs{};
   if (num_merge > 0) {
-    ATLAS_REQUIRE(merge_dev != nullptr && workspace_dev != nullptr, "split work needs merge list and workspace");
+    ATLAS_REQUIRE(merge_dev != nullptr, "merge list must not be NULL when num_merge > 0");
+    ATLAS_REQUIRE(use_scratch || workspace_dev != nullptr, "workspace must not be NULL when num_merge > 0");
     // The planner places the partial O rows first and the partial LSE after
     // them: workspace = [partial_rows * D 16-bit values][partial_rows floats].
     const size_t row_bytes = size_t(head_dim) * 2 + 4;
     ATLAS_REQUIRE(workspace_bytes % row_bytes == 0, "workspace_bytes must be partial_rows * (2 * head_dim + 4)");
     const size_t partial_rows = workspace_bytes / row_bytes;
+    ATLAS_REQUIRE(merge_partial_rows > 0 && size_t(merge_partial_rows) <= partial_rows,
+                  "the merge items reference %lld partial rows but the workspace holds %zu",
+                  (long long)merge_partial_rows, partial_rows);
+    if (use_scratch) {
+      const int rc = current_device_scratch(&workspace_dev);
+      if (rc != ATLAS_OK) return rc;
+    }
     ATLAS_REQUIRE((reinterpret_cast<uintptr_t>(workspace_dev) & 15) == 0, "workspace must be 16-byte aligned");
     args.part_o = static_cast<uint16_t*>(workspace_dev);
     args.part_lse = reinterpret_cast<float*>(args.part_o + partial_rows * head_dim);
+    args.part_rows = int64_t(partial_rows);
+    margs.part_rows = int64_t(partial_rows);
     margs.merge = merge_dev;
     margs.qo_indptr = qo_indptr_dev;
     margs.part_o = args.part_o;
@@ -1891,14 +1914,15 @@ extern "C" int atlas_tree_verify_attn(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
+    int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream) {
-  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+  return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
-                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, nullptr,
                           nullptr, 0, 0, nullptr, nullptr, 0);
 }
@@ -1909,7 +1933,8 @@ extern "C" int atlas_tree_verify_attn_append(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads, int num_kv_heads, int head_dim,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
+    int num_qo_heads, int num_kv_heads, int head_dim,
     int page_size, float sm_scale, int dtype, void* out, int64_t out_stride_token,
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     const void* append_k, const void* append_v, int64_t append_stride_token, int64_t append_stride_head,
@@ -1927,10 +1952,10 @@ extern "C" int atlas_tree_verify_attn_append(
                 "append rows must be 16-byte aligned");
   ATLAS_REQUIRE(append_stride_token % 8 == 0 && append_stride_head % 8 == 0,
                 "append strides must be multiples of 8 elements");
-  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+  return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
-                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, append_k,
                           append_v, append_stride_token, append_stride_head, rope_cos, rope_sin, rope_stride_token);
 }
@@ -1978,9 +2003,15 @@ extern "C" int atlas_tree_verify_attn_noalloc(
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
-    const atlas_attn_merge_t* merge_dev, int num_merge, int max_rows_per_item, int num_qo_heads,
-    int num_kv_heads, int head_dim, int page_size, float sm_scale, int dtype, void* out,
+    const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
+    int num_qo_heads, int num_kv_heads, int head_dim, int page_size, float sm_scale, int dtype, void* out,
     int64_t out_stride_token, int64_t out_stride_head, float* lse, int64_t partial_rows, void* stream) {
+  // every buffer and shape is checked before the device is touched
+  ATLAS_REQUIRE(q && kv_cache && out, "q, kv_cache and out must not be NULL");
+  ATLAS_REQUIRE(qo_indptr_dev && kv_indptr_dev && kv_indices_dev && kv_len_dev,
+                "indptr / indices / kv_len arrays must not be NULL");
+  ATLAS_REQUIRE(num_work == 0 || work_dev != nullptr, "work list must not be NULL");
+  ATLAS_REQUIRE(num_merge == 0 || merge_dev != nullptr, "merge list must not be NULL when num_merge > 0");
   ATLAS_REQUIRE(head_dim == 64 || head_dim == 128, "head_dim must be 64 or 128, got %d", head_dim);
   ATLAS_REQUIRE(partial_rows >= 0, "negative partial_rows");
   const size_t row_bytes = size_t(head_dim) * 2 + 4;
@@ -1989,15 +2020,13 @@ extern "C" int atlas_tree_verify_attn_noalloc(
                 (long long)partial_rows, row_bytes, ATLAS_ATTN_SCRATCH_BYTES,
                 size_t(ATLAS_ATTN_SCRATCH_BYTES) / row_bytes, head_dim);
   ATLAS_REQUIRE(num_merge == 0 || partial_rows > 0, "a split plan needs partial_rows > 0");
-  void* ws = nullptr;
-  if (num_merge > 0 && num_work > 0) {
-    const int rc = current_device_scratch(&ws);
-    if (rc != ATLAS_OK) return rc;
-  }
-  return verify_attn_impl(q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+  ATLAS_REQUIRE(num_merge == 0 || (merge_partial_rows > 0 && merge_partial_rows <= partial_rows),
+                "the merge items reference %lld partial rows but partial_rows is %lld",
+                (long long)merge_partial_rows, (long long)partial_rows);
+  return verify_attn_impl(true, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
-                          max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
-                          out_stride_token, out_stride_head, lse, ws, ws ? size_t(partial_rows) * row_bytes : 0,
+                          merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
+                          out_stride_token, out_stride_head, lse, nullptr, size_t(partial_rows) * row_bytes,
                           stream, nullptr, nullptr, 0, 0, nullptr, nullptr, 0);
 }

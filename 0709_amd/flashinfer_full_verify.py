@@ -215,7 +215,8 @@ def _signed64(value: int) -> int:
 def with_host_values(t: torch.Tensor, values: Sequence[int]) -> torch.Tensor:
     """Attach the host copy of a small index tensor's values (and its version
     counter), so a plan that reads them back skips the device-to-host copy
-    while the tensor is unchanged."""
+    while the tensor is unchanged.  An inference tensor has no counter, and a
+    plan ignores the copy attached to it."""
     t._atlas_host_values = (list(values), tensor_version(t))
     return t
 
@@ -253,6 +254,17 @@ def _tree_spec(
     else:
         block = np.asarray([[(b >> j) & 1 for j in range(node_count)] for b in bits], dtype=np.bool_)
     host = np.concatenate((i64.view(np.uint8), i32.view(np.uint8), block.reshape(-1).view(np.uint8)))
+    # Normal tensors even under torch.inference_mode (the Target verify runs
+    # in it): their version counters let a plan trust the attached host
+    # values only while the tensors are unchanged.
+    with torch.inference_mode(False):
+        return _tree_spec_tensors(host, i64, i32, node_count=node_count, kv_len=kv_len, total_pages=total_pages,
+                                  last=last, prefix_len=prefix_len, compact=compact, device=device,
+                                  parent_indices=parent_indices)
+
+
+def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
+                       parent_indices) -> TreeSpec:
     buf = torch.from_numpy(host).to(device)
     o64 = 0
     n64 = len(i64)
@@ -273,8 +285,7 @@ def _tree_spec(
     flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.
-        # The version counter lets plan() notice an in-place change of the mask
-        # (inference tensors have none: None).
+        # The version counter lets plan() notice an in-place change of the mask.
         flat_mask._atlas_tree_window = (prefix_len, tree_mask, tensor_version(flat_mask))
     return TreeSpec(
         flat_token_ids=flat_token_ids,

@@ -902,9 +902,15 @@ class SGLangRoutePoolBridge:
 
     def _plan_fused_frontier(self, active_routes: Sequence[RouteState]) -> "_FusedFrontierPlan":
         """Host half of ``prepare_frontier`` for ``prepare_frontiers``: request
-        rows, slot paths, the copy-on-write plan with its leases, dirty starts
-        and counters, and the request-row segments, in the order
-        ``prepare_frontier`` takes them; no device work."""
+        rows, slot paths, the copy-on-write plan and the request-row segments,
+        in the order ``prepare_frontier`` takes them; no device work.
+
+        Planning changes nothing that a failed step would leave behind: the
+        copy-on-write routes' new leases, the copy counters and the dirty
+        starts are applied by ``_finish_fused_frontier`` once the step's pages
+        are known to exist and its launch went through.  (Path inheritance
+        and the keying of lease-less tails happen here, as in
+        ``prepare_frontier`` before its own allocation can fail.)"""
         if not active_routes:
             raise ValueError("active_routes cannot be empty")
         rows = self._route_row_indices(active_routes)
@@ -913,21 +919,16 @@ class SGLangRoutePoolBridge:
         prevs = [int(p.numel()) for p in paths]
         cow_tail = [0] * n
         cow_rank = [-1] * n
+        cow_order: list[int] = []
+        dirty: dict[int, int] = {}
         for rank, (index, _path, tail) in enumerate(self._tail_copy_plan(active_routes, paths)):
-            rid = int(active_routes[index].route_id)
-            self.route_tail_page_keys[rid] = self._new_tail_page_key()
             cow_tail[index] = tail
             cow_rank[index] = rank
-            self.cow_pages_copied += 1
-            self.cow_tokens_copied += tail
-            row = self.route_rows[rid]
-            if int(row.written_length) > 0:
-                start = prevs[index] - tail
-                row.pending_dirty_start = start if row.pending_dirty_start is None else min(
-                    int(row.pending_dirty_start), start)
+            cow_order.append(index)
+            dirty[index] = prevs[index] - tail
         starts: list[int] = []
         kinds: list[str] = []
-        for route, prev, req_row in zip(active_routes, prevs, rows):
+        for i, (route, prev, req_row) in enumerate(zip(active_routes, prevs, rows)):
             row = self.route_rows[int(route.route_id)]
             if int(row.written_length) == 0:
                 start, kind = 0, "full_init"
@@ -938,10 +939,13 @@ class SGLangRoutePoolBridge:
                         f"route_id={int(route.route_id)}, written_length={int(row.written_length)}, "
                         f"physical_path_length={prev}"
                     )
-                if row.pending_dirty_start is None:
+                pending = row.pending_dirty_start
+                if i in dirty:
+                    pending = dirty[i] if pending is None else min(int(pending), dirty[i])
+                if pending is None:
                     start, kind = prev, "append"
                 else:
-                    start, kind = int(row.pending_dirty_start), "cow_patch"
+                    start, kind = int(pending), "cow_patch"
             self._check_req_write(req_row, start, prev + 1 - start, kind)
             starts.append(start)
             kinds.append(kind)
@@ -949,14 +953,20 @@ class SGLangRoutePoolBridge:
             if prevs[i] and (p.dtype != torch.int64 or not p.is_contiguous()):
                 paths[i] = p.to(torch.int64).contiguous()
         return _FusedFrontierPlan(list(active_routes), rows, paths, prevs, cow_tail, cow_rank,
-                                  sum(1 for t in cow_tail if t), starts, kinds)
+                                  len(cow_order), starts, kinds, cow_order)
 
     def _finish_fused_frontier(self, plan: "_FusedFrontierPlan", full_paths: Sequence[torch.Tensor],
                                flags: "_StepFlags", group: int) -> None:
         """Bookkeeping of ``prepare_frontier`` once the step's launch went
-        through: request-row state, new slot paths, leases, counters and the
+        through: the copy-on-write routes' leases and counters (in copy
+        order, as ``prepare_frontier`` assigns them), request-row state, new
+        slot paths, leases of routes that opened a page, counters and the
         step's device checks."""
         ps = self.page_size
+        for index in plan.cow_order:
+            self.route_tail_page_keys[int(plan.routes[index].route_id)] = self._new_tail_page_key()
+            self.cow_pages_copied += 1
+            self.cow_tokens_copied += plan.cow_tail[index]
         for i, route in enumerate(plan.routes):
             rid = int(route.route_id)
             row = self.route_rows[rid]
@@ -1137,6 +1147,7 @@ class _FusedFrontierPlan:
     num_cow: int
     starts: list[int]
     kinds: list[str]
+    cow_order: list[int]  # route positions of the copies, in copy order
 
 
 class _StepCheck:

@@ -76,14 +76,18 @@ class AttentionPlan:
 
 def _cached_host_values(t: torch.Tensor) -> list[int] | None:
     """The host copy a tree builder attached to a small index tensor, if the
-    tensor has not been modified in place since (version counter unchanged)."""
+    tensor has not been modified in place since (version counter unchanged).
+    An inference tensor keeps no counter, so its copy cannot be trusted and
+    its values are read back."""
     cached = getattr(t, "_atlas_host_values", None)
     if cached is None:
         return None
     from .flashinfer_full_verify import tensor_version
 
     values, version = cached
-    return values if version == tensor_version(t) and len(values) == int(t.numel()) else None
+    if version is None or version != tensor_version(t) or len(values) != int(t.numel()):
+        return None
+    return values
 
 
 def _host_lists(*items: torch.Tensor | list | tuple) -> list[list[int]]:
@@ -149,7 +153,7 @@ def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     dense mask, if it still describes this plan: one request, one ancestor
     word per query row, col0 within the keys and at most 64 tree columns, and
     the mask not modified in place since (its version counter unchanged; an
-    inference tensor keeps no counter, and its window is taken as built).
+    inference tensor keeps no counter, so its window is not trusted).
     Otherwise None, and the plan derives the window from the mask itself."""
     cached = getattr(custom_mask, "_atlas_tree_window", None) if custom_mask is not None else None
     if cached is None or len(qo_lens) != 1 or len(cached) != 3:
@@ -157,7 +161,8 @@ def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     col0, bits, version = cached
     from .flashinfer_full_verify import tensor_version
 
-    if version != tensor_version(custom_mask) or int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
+    if version is None or version != tensor_version(custom_mask) or \
+            int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
         return None
     if int(bits.numel()) != qo_lens[0] or not (0 <= int(col0) <= kv_lens[0]):
         return None
@@ -242,6 +247,10 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self.use_page_windows: bool = True
         self.min_tiles_per_split = 1
         self.max_rows_per_item: int | None = None
+        # Key granule of the split boundaries (None: whole 64-key tiles).  The
+        # head_dim-128 kernel accepts splits starting at any multiple of
+        # min(page_size, 64) keys; other shapes always split at whole tiles.
+        self.split_granule_keys: int | None = None
         self._decomp_cache: tuple | None = None
         self._meta_uploaded: tuple | None = None
         self._meta_buf: torch.Tensor | None = None
@@ -350,7 +359,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # ---- work decomposition (the same inputs give the same work list) ----
         ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
         key = (tuple(qo), tuple(kvp), tuple(kv_lens), tuple(cols), hq, hkv, d, ps, self.max_rows_per_item,
-               self.split_target_items, self.min_tiles_per_split, ws_rows_cap)
+               self.split_target_items, self.min_tiles_per_split, self.split_granule_keys, ws_rows_cap)
         if self._decomp_cache is None or self._decomp_cache[0] != key:
             self._decomp_cache = (key, self._decompose(batch=batch, qo=qo, kvp=kvp, qo_lens=qo_lens,
                                                        kv_lens=kv_lens, cols=cols, hq=hq, hkv=hkv, d=d, ps=ps,
@@ -396,6 +405,12 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 blocks.append((b, r0, min(size, rows - r0)))
             if rows == 0:
                 blocks.append((b, 0, 0))
+        gran = TILE_KEYS
+        if direct and self.split_granule_keys is not None:
+            gran = int(self.split_granule_keys)
+            if gran <= 0 or gran > TILE_KEYS or gran % min(ps, TILE_KEYS) != 0 or TILE_KEYS % gran != 0:
+                raise ValueError(f"split_granule_keys must divide {TILE_KEYS} and be a multiple of "
+                                 f"min(page_size, {TILE_KEYS}) = {min(ps, TILE_KEYS)}, got {gran}")
         unit_tiles = sum(hkv * math.ceil(kv_lens[b] / TILE_KEYS) for (b, _, _) in blocks)
         # Tiles per split as a fraction, so the split count per request rounds
         # down and the items do not exceed the target (one per CU when a single
@@ -410,12 +425,13 @@ class BatchPrefillWithPagedKVCacheWrapper:
             for (b, r0, nr) in blocks:
                 tiles = math.ceil(kv_lens[b] / TILE_KEYS)
                 splits = max(1, min(tiles, int(tiles / tiles_per_split + 1e-9)))
-                # balanced splits of the request's tiles: `per` tiles each, one
-                # more for the first `extra` splits, so the last split, which
-                # holds the request's masked tail tile (the costliest to
-                # compute), has one tile less
-                per = tiles // splits if tiles else 0
-                extra = tiles - per * splits
+                # balanced splits of the request's key granules: `per` granules
+                # each, one more for the first `extra` splits, so the last
+                # split, which holds the request's masked tail tile (the
+                # costliest to compute), has one granule less
+                units = math.ceil(kv_lens[b] / gran)
+                per = units // splits if units else 0
+                extra = units - per * splits
                 # request values every item repeats (qo_start, qo_len, kv_len,
                 # mask column start, page offset) and padding to 16 ints
                 req_vals = (qo[b], qo_lens[b], kv_lens[b], cols[b], kvp[b], 0, 0, 0, 0)
@@ -427,8 +443,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
                     for s in range(splits):
                         t0 = s * per + min(s, extra)
                         t1 = t0 + per + (1 if s < extra else 0)
-                        k0 = t0 * TILE_KEYS
-                        k1 = min(kv_lens[b], t1 * TILE_KEYS)
+                        k0 = t0 * gran
+                        k1 = min(kv_lens[b], t1 * gran)
                         work.append((b, h, r0, nr, k0, k1, base + s * nr) + req_vals)
                     merge.append((b, h, r0, nr, base, splits, 0, 0))
                     partial_rows += splits * nr
@@ -601,7 +617,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
             plan.device_view(plan.col_offset), plan.device_view(plan.work_offset), plan.num_work,
             _lib.ptr(plan.page_windows) if plan.page_windows is not None else None,
-            plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge, plan.max_rows,
+            plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge,
+            plan.partial_rows if plan.num_merge else 0, plan.max_rows,
             plan.num_qo_heads, plan.num_kv_heads, plan.head_dim, plan.page_size, plan.sm_scale,
             _lib.dtype_code(q.dtype), _lib.ptr(out), out.stride(0), out.stride(1),
             _lib.ptr(lse) if lse is not None else None, _lib.ptr(self._workspace) if ws_bytes else None,

@@ -62,6 +62,11 @@ def _ev():
     return torch.cuda.Event(enable_timing=True)
 
 
+# Planner settings given on the command line, applied to every verify
+# attention wrapper the bench builds (headline and attention legs).
+PLAN_TUNING: dict = {}
+
+
 class HeadlineStep:
     def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None, max_rows=None,
                  routes=None):
@@ -99,6 +104,8 @@ class HeadlineStep:
         self.prefix_logits = (torch.randn((128256,), generator=g, device=dev) * 2.0).half()
         ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
         self.wrapper = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        for key, value in PLAN_TUNING.items():
+            setattr(self.wrapper, key, value)
         if split_target is not None:
             self.wrapper.split_target_items = split_target
         if max_rows is not None:
@@ -1029,7 +1036,10 @@ def main():
     ap.add_argument("--legs", default="all", metavar="NAMES",
                     help="comma-separated component legs to run (config2, tree16k, batched, cow, decode, decode8k, "
                          "drafter, drafter_calls, frontier), default all")
-    ap.add_argument("--split-target", type=int, default=None)
+    ap.add_argument("--split-target", type=int, default=None,
+                    help="work items a verify attention plan aims at (headline and attention legs)")
+    ap.add_argument("--split-granule", type=int, default=None, metavar="KEYS",
+                    help="key granule of the attention splits (default: the planner's)")
     ap.add_argument("--max-rows", type=int, default=None)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run device-to-device copies of MIB MiB (calibrates HBM byte counters)")
@@ -1045,6 +1055,10 @@ def main():
                                    "and has no multi-GPU leg", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
+    if args.split_target is not None:
+        PLAN_TUNING["split_target_items"] = args.split_target
+    if args.split_granule is not None:
+        PLAN_TUNING["split_granule_keys"] = args.split_granule
     if args.profile_kv:
         # the commit and copy-on-write launches alone, eagerly, for counter
         # runs (after a copy of known size that calibrates the counters)

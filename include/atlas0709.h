@@ -178,7 +178,11 @@ int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
  * workspace_dev holds the split partial states: partial_rows rows of D
  * 16-bit values in the output dtype (the normalised partial O, as FlashInfer
  * keeps its split-KV temporaries in the output type), then partial_rows fp32
- * base-2 LSEs: partial_rows * (2 * D + 4) bytes.
+ * base-2 LSEs: partial_rows * (2 * D + 4) bytes.  merge_partial_rows is the
+ * count of partial rows the merge items reference (the plan's partial_rows,
+ * passed with the merge list): a workspace holding fewer is refused with
+ * ATLAS_EINVAL before any device work, and the kernels never write or read a
+ * partial row the workspace does not hold.
  * Replaces FlashInfer BatchPrefillWithPagedKVCacheWrapper.plan/run with
  * causal=False and custom_mask as used by run_flashinfer_full_verify
  * (src/atlas_0709/flashinfer_full_verify.py:953-985, :1223). */
@@ -191,7 +195,8 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
                            const atlas_attn_work_t* work_dev, int num_work,
                            const int32_t* page_window_dev,
                            const atlas_attn_merge_t* merge_dev, int num_merge,
-                           int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                           int64_t merge_partial_rows, int max_rows_per_item,
+                           int num_qo_heads, int num_kv_heads,
                            int head_dim, int page_size, float sm_scale, int dtype, void* out,
                            int64_t out_stride_token, int64_t out_stride_head, float* lse,
                            void* workspace_dev, size_t workspace_bytes, void* stream);
@@ -222,7 +227,8 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
                                   const atlas_attn_work_t* work_dev, int num_work,
                                   const int32_t* page_window_dev,
                                   const atlas_attn_merge_t* merge_dev, int num_merge,
-                                  int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                                  int64_t merge_partial_rows, int max_rows_per_item,
+                                  int num_qo_heads, int num_kv_heads,
                                   int head_dim, int page_size, float sm_scale, int dtype, void* out,
                                   int64_t out_stride_token, int64_t out_stride_head, float* lse,
                                   void* workspace_dev, size_t workspace_bytes,
@@ -242,7 +248,9 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
  * library holds on every GPU it runs on until the process ends, so the call
  * allocates nothing and needs no workspace from the caller.  A plan whose
  * partial_rows * (2 * head_dim + 4) exceeds that size is rejected with
- * ATLAS_EINVAL.  Every call on one GPU shares that GPU's array (nothing in it
+ * ATLAS_EINVAL, and so is a partial_rows below merge_partial_rows (checked,
+ * like every buffer, before the device is touched).  Every call on one GPU
+ * shares that GPU's array (nothing in it
  * needs to start at zero): calls that overlap on one GPU, on different
  * streams, race and must not be issued.  Results equal atlas_tree_verify_attn
  * with a workspace bit for bit (same kernels).
@@ -258,7 +266,8 @@ int atlas_tree_verify_attn_noalloc(const void* q, int64_t q_stride_token, int64_
                                    const atlas_attn_work_t* work_dev, int num_work,
                                    const int32_t* page_window_dev,
                                    const atlas_attn_merge_t* merge_dev, int num_merge,
-                                   int max_rows_per_item, int num_qo_heads, int num_kv_heads,
+                                   int64_t merge_partial_rows, int max_rows_per_item,
+                                   int num_qo_heads, int num_kv_heads,
                                    int head_dim, int page_size, float sm_scale, int dtype, void* out,
                                    int64_t out_stride_token, int64_t out_stride_head, float* lse,
                                    int64_t partial_rows, void* stream);
@@ -392,7 +401,8 @@ int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, i
  * the prefix logits of a Target verify are scored together.  One launch:
  * every row is read once, in chunks spread over the device, and its
  * log-sum-exp combined from the chunks in a fixed order (row_lse_dev, if not
- * NULL, receives it).  workspace_dev holds the chunk statistics: at least
+ * NULL, receives it).  workspace_dev holds the chunk statistics and one
+ * arrival counter per row: at least
  * atlas_gather_logprobs_workspace_bytes(num_rows, vocab) bytes, 16-byte
  * aligned, zero-filled before its first use; every call leaves it zero again
  * (calls sharing it must be stream-ordered).  Replaces the

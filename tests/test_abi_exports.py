@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 5
+    assert lib.atlas_abi_version() == 6
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -49,7 +49,7 @@ def test_argument_errors_are_reported_without_device_work():
         None, None, None, None,  # qo_indptr, kv_indptr, kv_indices, kv_len
         0, None, None,         # mask mode, tree mask, mask column start
         None, 0, None,         # work list, page windows
-        None, 0,               # merge list
+        None, 0, 0,            # merge list, its partial rows
         1, 32, 8, 96, 16,      # rows per item, Hq, Hkv, head_dim (unsupported), page size
         ctypes.c_float(0.1), 0,
         None, 0, 0, None,      # out, out strides, lse
@@ -98,3 +98,68 @@ def test_every_entry_point_refuses_null_buffers_before_device_work():
         assert lib.atlas_last_error(), f"{name} left no error message"
         checked.append(name)
     assert len(checked) == len(_declared_symbols()) - len(queries)
+
+
+def _verify_args(name, **over):
+    """Arguments of a verify entry point with valid shapes (Llama-3.1-8B:
+    Hq 32, Hkv 8, head_dim 128, page 16, fp16, one work item and one merge
+    item) and never-dereferenced stand-in device pointers; ``over`` replaces
+    named ones."""
+    import ctypes
+
+    fake = ctypes.c_void_p(1 << 20)
+    row = 2 * 128 + 4
+    a = dict(q=fake, q_st=32 * 128, q_sh=128, kv=fake, page_stride=2 * 16 * 8 * 256, v_off=16 * 8 * 256,
+             token_stride=8 * 256, qo=fake, kvp=fake, kvi=fake, kvl=fake, mask_mode=1, tree=fake, col=fake,
+             work=fake, nwork=1, win=None, merge=fake, nmerge=1, merge_rows=64, rows=64, hq=32, hkv=8, d=128,
+             ps=16, scale=ctypes.c_float(0.088), dtype=0, out=fake, o_st=32 * 128, o_sh=128, lse=None)
+    a.update(over)
+    head = [a[k] for k in ("q", "q_st", "q_sh", "kv", "page_stride", "v_off", "token_stride", "qo", "kvp", "kvi",
+                           "kvl", "mask_mode", "tree", "col", "work", "nwork", "win", "merge", "nmerge",
+                           "merge_rows", "rows", "hq", "hkv", "d", "ps", "scale", "dtype", "out", "o_st", "o_sh",
+                           "lse")]
+    if name == "atlas_tree_verify_attn_noalloc":
+        return head + [a.get("partial_rows", 64), None]
+    ws = [a.get("ws", fake), a.get("ws_bytes", 64 * row)]
+    if name == "atlas_tree_verify_attn_append":
+        return head + ws + [fake, fake, 8 * 128, 128, None, None, 0, None]
+    return head + ws + [None]
+
+
+VERIFY_ENTRIES = ("atlas_tree_verify_attn", "atlas_tree_verify_attn_append", "atlas_tree_verify_attn_noalloc")
+
+
+def test_verify_entry_points_name_the_null_buffer():
+    """With valid shapes, a NULL buffer is what the refusal names, before the
+    device (or the allocation-free entry point's device scratch) is touched."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    for name in VERIFY_ENTRIES:
+        for key, what in (("q", b"q, kv_cache and out"), ("kv", b"q, kv_cache and out"),
+                          ("out", b"q, kv_cache and out"), ("kvi", b"indptr / indices"),
+                          ("work", b"work list"), ("merge", b"merge list")):
+            rc = getattr(lib, name)(*_verify_args(name, **{key: None}))
+            assert rc == lib_mod.ATLAS_EINVAL, (name, key, rc)
+            msg = lib.atlas_last_error()
+            assert what in msg and b"NULL" in msg, (name, key, msg)
+        if name != "atlas_tree_verify_attn_noalloc":
+            rc = getattr(lib, name)(*_verify_args(name, ws=None))
+            assert rc == lib_mod.ATLAS_EINVAL and b"workspace must not be NULL" in lib.atlas_last_error()
+
+
+def test_verify_entry_points_refuse_too_few_partial_rows():
+    """The merge items' partial-row count travels with the merge list; a
+    workspace or a partial_rows below it is refused before any device work."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    row = 2 * 128 + 4
+    for name in VERIFY_ENTRIES:
+        if name == "atlas_tree_verify_attn_noalloc":
+            bad = _verify_args(name, merge_rows=65, partial_rows=64)
+        else:
+            bad = _verify_args(name, merge_rows=65, ws_bytes=64 * row)
+        rc = getattr(lib, name)(*bad)
+        assert rc == lib_mod.ATLAS_EINVAL, (name, rc)
+        assert b"merge items reference 65 partial rows" in lib.atlas_last_error(), name
+        rc = getattr(lib, name)(*_verify_args(name, merge_rows=0))
+        assert rc == lib_mod.ATLAS_EINVAL and b"merge items reference 0" in lib.atlas_last_error(), name

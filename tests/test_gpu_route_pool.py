@@ -434,3 +434,80 @@ def test_batched_commit_equals_per_request_calls_and_refusals(dev):
         w.fallback_extend()
     assert state(wl, alloc, req) == state(wl2, alloc2, req2)
     assert [r.stats for r in wl.requests] == [r.stats for r in wl2.requests]
+
+
+def test_fused_frontier_refused_for_pages_leaves_no_trace(dev):
+    """A multi-request frontier step refused because the pool has too few
+    pages changes no copy-on-write lease, copy counter, dirty start, request
+    row or free page (children only inherit their parents' paths and leases,
+    as a per-request call does before its own allocation fails).  Retried
+    after the pages come back, it leaves exactly the state of the same step
+    that never failed: in particular the forked routes still get their tail
+    copies, so no two routes share a decode slot."""
+    dw = pkg("drafter_workload")
+    npool = pkg("flashinfer_paged.native_pool")
+    sr = pkg("flashinfer_paged.sglang_runtime")
+    plans = [dw.ForkPlan(prefix_len=p, steps=2, forks={0: 3}, commit_depth=1, post_steps=0, extend_tokens=(1,),
+                         seed=40 + i) for i, p in enumerate((100, 77, 130))]
+
+    def setup():
+        req, kv, alloc = npool.create_native_pools(num_pages=64, page_size=16, dtype=torch.bfloat16, head_num=2,
+                                                   head_dim=64, layer_num=2, max_running_requests=32,
+                                                   max_context_len=1024, device=dev)
+        rows = [torch.zeros((1, 2, 64), dtype=torch.bfloat16, device=dev)] * 2
+
+        def writer(slots, vids):
+            r = [x.expand(int(slots.numel()), 2, 64) for x in rows]
+            kv.set_kv_buffer_all_layers(slots, r, r)
+
+        wl = dw.DrafterForkWorkload(plans=plans, req_pool=req, allocator=alloc, page_size=16, device=dev,
+                                    writer=writer, batched=True)
+        wl.prefill()
+        for r in wl.requests:
+            wl._fork(r, 3)
+        held = alloc.alloc(int(alloc.available_size()))
+        return wl, alloc, held
+
+    def snapshot(wl):
+        torch.cuda.synchronize()
+        out = []
+        for r in wl.requests:
+            b = r.bridge
+            out.append((dict(b.route_tail_page_keys), b.next_tail_page_key, b.hot_path_counters(),
+                        {rid: (row.written_length, row.pending_dirty_start) for rid, row in b.route_rows.items()},
+                        {rid: p.tolist() for rid, p in b.route_slot_paths.items()}))
+        return out
+
+    def step(wl):
+        return sr.SGLangFlashInferFrontierModelBackend.decode_frontiers([r.backend for r in wl.requests],
+                                                                       [r.active for r in wl.requests])
+
+    wl, alloc, held = setup()
+    before = snapshot(wl)
+    free_before = alloc.free_pages[alloc._head:].tolist()
+    with pytest.raises(RuntimeError, match="cannot allocate"):
+        step(wl)
+    after = snapshot(wl)
+    assert alloc.free_pages[alloc._head:].tolist() == free_before
+    for r, (k0, n0, c0, rows0, _), (k1, n1, c1, rows1, paths1) in zip(wl.requests, before, after):
+        assert c1 == c0 and rows1 == rows0
+        # the three children still share the prefix tail's one lease: none got
+        # the fresh lease of a copy that did not happen
+        assert len({k1[int(route.route_id)] for route in r.active}) == 1
+        assert all(k1[k] == v for k, v in k0.items())
+    alloc.free(held)
+    outs = step(wl)
+    got = snapshot(wl)
+
+    wl2, alloc2, held2 = setup()
+    alloc2.free(held2)
+    step(wl2)
+    want = snapshot(wl2)
+    # node ids differ (the refused call reserved some), so compare slot state only
+    assert [(k, n, c, rows, paths) for k, n, c, rows, paths in got] == \
+           [(k, n, c, rows, paths) for k, n, c, rows, paths in want]
+    assert alloc.free_pages[alloc._head:].tolist() == alloc2.free_pages[alloc2._head:].tolist()
+    for out in outs:
+        assert out.metadata["cow_pages_copied_total"] == 2
+    slots = torch.cat([torch.tensor([int(p[-1]) for p in s[4].values() if p]) for s in got])
+    assert int(slots.unique().numel()) == int(slots.numel())

@@ -587,16 +587,27 @@ def test_fused_rope_batched_requests_and_refusals(dev):
 
 
 
-def test_plan_sees_index_tensors_changed_in_place(dev):
+@pytest.mark.parametrize("inference", [False, True])
+def test_plan_sees_index_tensors_changed_in_place(dev, inference):
     """The tree builder's index tensors carry their host values; a plan reads
     those only while the tensor is unchanged.  After an in-place write the
     plan reads the device values again (here: a longer last page, so one more
-    key per row, checked against the oracle)."""
+    key per row, checked against the oracle).  The same holds when the spec
+    is built and changed under torch.inference_mode, as the Target verify
+    does."""
+    import contextlib
+
     ta = pkg("tree_attention")
     ffv = pkg("flashinfer_full_verify")
     gen = torch.Generator().manual_seed(31)
     routes = _routes(gen, 3, 4, share=True)
-    c = _build(dev, seed=31, prefix_len=300, routes=routes, permute=False, spare_pages=1)
+    ctx = torch.inference_mode() if inference else contextlib.nullcontext()
+    with ctx:
+        c = _build(dev, seed=31, prefix_len=300, routes=routes, permute=False, spare_pages=1)
+        _plan_changed_in_place(dev, ta, ffv, c)
+
+
+def _plan_changed_in_place(dev, ta, ffv, c):
     spec = c["spec"]
     assert spec.kv_last_page_len._atlas_host_values[0] == [ffv.last_page_len(c["kv_len"], 16)]
     ws = torch.empty(16 * 1024 * 1024, dtype=torch.uint8, device=dev)

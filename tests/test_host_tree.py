@@ -127,14 +127,30 @@ def test_cached_tree_window_validated_against_plan():
     assert col0 == 20 and int(bits[4]) == 0b11000 and int(bits2[4]) == 0b10000
 
 
-def test_cached_tree_window_of_inference_tensors():
-    """A mask built under torch.inference_mode keeps no version counter; its
-    window is still taken when the plan's shape matches."""
+def test_cached_values_under_inference_mode():
+    """The Target builds its tree spec under torch.inference_mode.  The
+    builder's tensors are still normal tensors with version counters, so the
+    attached host values and window are taken while unchanged and dropped
+    after an in-place write made in inference mode; a host copy attached to
+    an inference tensor (no counter) is never trusted."""
     ffv = pkg("flashinfer_full_verify")
     ta = pkg("tree_attention")
     with torch.inference_mode():
         spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=[(1, 2, 3), (1, 5, 6)], prefix_len=20,
                                                               page_size=4, device="cpu")
+        assert not spec.bool_mask.is_inference() and not spec.kv_last_page_len.is_inference()
         got = ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len])
-    assert got is not None and got[0] == 20 and got[1].tolist() == spec.tree_mask.tolist()
-    assert ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len + 3]) is None
+        assert got is not None and got[0] == 20 and got[1].tolist() == spec.tree_mask.tolist()
+        assert ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len + 3]) is None
+        assert ta._cached_host_values(spec.kv_last_page_len) == [spec.kv_len - 4 * (spec.total_pages - 1)]
+        spec.kv_last_page_len.add_(1)
+        spec.bool_mask[spec.kv_len + 20] = False
+        assert ta._cached_host_values(spec.kv_last_page_len) is None
+        assert ta._cached_tree_window(spec.bool_mask, [spec.node_count], [spec.kv_len]) is None
+        foreign = ffv.with_host_values(torch.tensor([0, 5], dtype=torch.int32), [0, 5])
+        assert foreign.is_inference() and ta._cached_host_values(foreign) is None
+        mask = torch.ones(spec.node_count * spec.kv_len, dtype=torch.bool)
+        mask._atlas_tree_window = (20, spec.tree_mask, ffv.tensor_version(mask))
+        assert ta._cached_tree_window(mask, [spec.node_count], [spec.kv_len]) is None
+    # the host lists then come from the tensors themselves
+    assert ta._host_lists(foreign)[0] == [0, 5]

@@ -47,7 +47,8 @@ def _noalloc(w, q, kv, out, lse, partial_rows=None):
         plan.device_view(plan.kv_len_offset), plan.mask_mode, lib_mod.ptr(plan.tree_mask),
         plan.device_view(plan.col_offset), plan.device_view(plan.work_offset), plan.num_work,
         lib_mod.ptr(plan.page_windows) if plan.page_windows is not None else None,
-        plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge, plan.max_rows,
+        plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge,
+        plan.partial_rows if plan.num_merge else 0, plan.max_rows,
         plan.num_qo_heads, plan.num_kv_heads, plan.head_dim, plan.page_size, ctypes.c_float(plan.sm_scale),
         lib_mod.dtype_code(q.dtype), lib_mod.ptr(out), out.stride(0), out.stride(1), lib_mod.ptr(lse),
         plan.partial_rows if partial_rows is None else partial_rows, lib_mod.stream_of(q.device))
