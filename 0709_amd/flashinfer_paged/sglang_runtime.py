@@ -440,8 +440,8 @@ class SGLangRoutePoolBridge:
         """Zero-copy promotion: the route's slot path becomes the prefix and
         its tail lease carries over (``sglang_runtime.py:357-378``).  With
         ``defer_page_ids`` the prefix's host page-id set is left for the
-        caller to refresh (``refresh_prefix_page_ids`` reads several bridges'
-        sets back in one copy)."""
+        caller to refresh (the multi-request commit reads it back together
+        with the prune's counts)."""
         old_len = 0 if self.prefix_slot_ids is None else int(self.prefix_slot_ids.numel())
         path = self._slot_path_for_route(route)
         expected = old_len + len(route.kv_view.node_ids)
@@ -994,7 +994,7 @@ class SGLangRoutePoolBridge:
     def check_pending_device_checks(self) -> None:
         """Raise the first failed deferred condition (layout of frontier page
         metadata, distinct output slots) recorded since the last check.  The
-        flags of all pending fused frontier steps come back in one copy."""
+        flags of fused frontier steps are already on their way to the host."""
         _prefetch_step_flags([self])
         pending, self.pending_device_checks = self.pending_device_checks, []
         for check in pending:
@@ -1163,37 +1163,55 @@ class _StepCheck:
 
 
 def _prefetch_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> None:
-    """Reads the flags of every fused frontier step with a check pending on
-    these bridges, in one device-to-host copy."""
-    steps, seen = [], set()
+    """Brings the flags of every fused frontier step with a check pending on
+    these bridges to the host (each step's copy was queued behind its launch,
+    so this waits only for those copies)."""
     for b in bridges:
         for c in b.pending_device_checks:
             f = getattr(c, "step_flags", None)
-            if f is not None and f._host is None and id(f) not in seen:
-                seen.add(id(f))
-                steps.append(f)
-    if len(steps) < 2:
-        return
-    flat = _int_list(torch.cat([f.flags.reshape(-1) for f in steps]))
-    off = 0
-    for f in steps:
-        n = int(f.flags.numel())
-        f._host = flat[off:off + n]
-        off += n
+            if f is not None:
+                f.host()
 
 
 class _StepFlags:
     """Check flags of one fused frontier step (device int64s the kernel
-    clears on a failed check), read back once, at the first check."""
+    clears on a failed check).  On a device, a copy into pinned host memory is
+    queued right behind the step's launch, so the check that reads the flags
+    (at the next prune) finds them on the host instead of waiting for the
+    device work issued since."""
+
+    # (pinned buffer, event) pairs of flags already read, by flag count
+    _spare: dict[int, list] = {}
 
     def __init__(self, flags: torch.Tensor) -> None:
         self.flags = flags
         self._host: list[int] | None = None
+        self._staged = None
+        if flags.device.type == "cuda":
+            n = int(flags.numel())
+            spare = _StepFlags._spare.get(n)
+            if spare:
+                pinned, ready = spare.pop()
+            else:
+                pinned, ready = torch.empty(n, dtype=flags.dtype, pin_memory=True), torch.cuda.Event()
+            pinned.copy_(flags, non_blocking=True)
+            ready.record(torch.cuda.current_stream(flags.device))
+            self._staged = (pinned, ready)
+
+    def host(self) -> list[int]:
+        if self._host is None:
+            if self._staged is not None:
+                pinned, ready = self._staged
+                ready.synchronize()
+                self._host = [int(x) for x in pinned.tolist()]
+                self._staged = None
+                _StepFlags._spare.setdefault(len(self._host), []).append((pinned, ready))
+            else:
+                self._host = [int(x) for x in self.flags.cpu().tolist()]
+        return self._host
 
     def check(self, group: int, validate_layout: bool) -> None:
-        if self._host is None:
-            self._host = [int(x) for x in self.flags.cpu().tolist()]
-        h = self._host
+        h = self.host()
         if not h[0]:
             raise RuntimeError("frontier step: a route descriptor was out of range and the route was skipped")
         base = 1 + 3 * int(group)
@@ -1218,6 +1236,7 @@ class FusedFrontierStep:
     metadata: SGLangRouteKVMetadata
     route_ids: torch.Tensor
     spans: tuple[tuple[int, int], ...]
+    prevs: tuple[int, ...] = ()  # every route's path length before the step
 
 
 _ROUTE_FIELDS = 14  # int64 fields of one frontier route descriptor
@@ -1248,25 +1267,6 @@ def fused_frontier_supported(bridges: Sequence[SGLangRoutePoolBridge]) -> bool:
     return True
 
 
-def refresh_prefix_page_ids(bridges: Sequence[SGLangRoutePoolBridge]) -> None:
-    """Each bridge's host copy of its prefix page ids (what
-    ``_refresh_prefix_cpu_metadata`` sets), read back in one copy for all."""
-    parts, counts = [], []
-    for b in bridges:
-        slots = b.prefix_slot_ids
-        if slots is None or int(slots.numel()) == 0:
-            counts.append(0)
-            continue
-        parts.append(torch.div(slots[:: b.page_size], b.page_size, rounding_mode="floor"))
-        counts.append(int(parts[-1].numel()))
-    flat = _int_list(torch.cat(parts)) if parts else []
-    off = 0
-    for b, c in zip(bridges, counts):
-        b.prefix_slot_count = 0 if b.prefix_slot_ids is None else int(b.prefix_slot_ids.numel())
-        b.prefix_page_ids = set(flat[off:off + c])
-        off += c
-
-
 def release_unreferenced_node_slots_many(bridges: Sequence[SGLangRoutePoolBridge],
                                          live_node_id_lists: Sequence[Sequence[int]]) -> list[int]:
     """``release_unreferenced_node_slots`` of several bridges.  Over one native
@@ -1279,12 +1279,40 @@ def release_unreferenced_node_slots_many(bridges: Sequence[SGLangRoutePoolBridge
         raise ValueError("one live node list per bridge is required")
     if len(bridges) < 2 or not fused_frontier_supported(bridges):
         return [b.release_unreferenced_node_slots(live) for b, live in zip(bridges, live_node_id_lists)]
+    return _sweep_bridges(bridges, live_node_id_lists, refresh_prefix=False)
+
+
+def _sweep_bridges(bridges: Sequence[SGLangRoutePoolBridge], live_node_id_lists: Sequence[Sequence[int]], *,
+                   refresh_prefix: bool) -> list[int]:
+    """The native-pool prune of several bridges over one allocator: every
+    bridge's deferred checks first, every sweep launched, then ONE copy to
+    the host of the released-page counts (and, with ``refresh_prefix``, of
+    each bridge's prefix page ids: the page of every page-start slot);
+    the released pages are prepended bridge by bridge, so the free list ends
+    as one call per bridge in this order leaves it."""
     _prefetch_step_flags(bridges)
     for b in bridges:
         b.check_pending_device_checks()
     for b in bridges:
         b.owned_page_ids.sweep_launch(b._live_slot_samples())
-    counts = _int_list(torch.cat([b.owned_page_ids.free_count for b in bridges]))
+    parts = [b.owned_page_ids.free_count for b in bridges]
+    starts: list[int] = []
+    if refresh_prefix:
+        for b in bridges:
+            slots = b.prefix_slot_ids
+            if slots is None or int(slots.numel()) == 0:
+                starts.append(0)
+                continue
+            parts.append(torch.div(slots[:: b.page_size], b.page_size, rounding_mode="floor"))
+            starts.append(int(parts[-1].numel()))
+    flat = _int_list(torch.cat(parts) if len(parts) > 1 else parts[0])
+    counts = flat[: len(bridges)]
+    if refresh_prefix:
+        off = len(bridges)
+        for b, c in zip(bridges, starts):
+            b.prefix_slot_count = 0 if b.prefix_slot_ids is None else int(b.prefix_slot_ids.numel())
+            b.prefix_page_ids = set(flat[off:off + c])
+            off += c
     alloc = bridges[0].token_to_kv_pool_allocator
     for b, live, n in zip(bridges, live_node_id_lists, counts):
         b._forget_dead_nodes(live)
@@ -1310,6 +1338,12 @@ def prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
     if not fused_frontier_supported(bridges):
         raise ValueError("prepare_frontiers needs distinct bridges over one set of native pools "
                          "(see fused_frontier_supported)")
+    return _prepare_frontiers(bridges, route_lists)
+
+
+def _prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
+                       route_lists: Sequence[Sequence[RouteState]]) -> FusedFrontierStep:
+    """``prepare_frontiers`` once ``fused_frontier_supported`` holds."""
     b0 = bridges[0]
     alloc = b0.token_to_kv_pool_allocator
     table = b0.req_to_token_pool.req_to_token
@@ -1366,8 +1400,12 @@ def prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
     input_ids, seq_dev, pos_dev, req_dev, rid_dev = (packed[o + k * R : o + (k + 1) * R] for k in range(5))
 
     F, C, P = flat_off, cow_off, page_off
-    out64 = torch.empty(F + R + 2 * C, dtype=torch.int64, device=device)
-    out32 = torch.empty(3 * R + 1 + P, dtype=torch.int32, device=device)
+    # one allocation: the int64 outputs, then the int32 ones
+    n64 = F + R + 2 * C
+    n32 = 3 * R + 1 + P
+    out = torch.empty(n64 + (n32 + 1) // 2, dtype=torch.int64, device=device)
+    out64 = out[:n64]
+    out32 = out[n64:].view(torch.int32)[:n32]
     flat, out_slots = out64[:F], out64[F : F + R]
     cow_dst, cow_src = out64[F + R : F + R + C], out64[F + R + C :]
     kv_indptr, kv_last = out32[: R + 1], out32[R + 1 : 2 * R + 1]
@@ -1396,7 +1434,7 @@ def prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
         attention_page_size=ps, token_index_count=F, page_index_count=P,
         paged_decode_spec=AtlasPagedDecodeSpec(kv_indptr, page_ids, kv_last, ps),
     )
-    return FusedFrontierStep(input_ids, meta, rid_dev, tuple(spans))
+    return FusedFrontierStep(input_ids, meta, rid_dev, tuple(spans), tuple(n - 1 for n in seq_lens))
 
 
 class SGLangFlashInferFrontierModelBackend:
@@ -1509,7 +1547,13 @@ class SGLangFlashInferFrontierModelBackend:
     def commit_stage1_and_promote(self, *, committed_route: RouteState, retained_routes: Sequence[RouteState]):
         """Promote the committed route's path to the prefix (no KV copy),
         rebase the retained routes, free the other rows, prune
-        (``:1256-1297``)."""
+        (``:1256-1297``).  Over the native pools this is the multi-request
+        commit for one request (the new prefix's page ids and the pruned-page
+        count come back in one copy); over other pools the per-step host
+        path.  Both leave the same state."""
+        if fused_frontier_supported([self.route_pool]):
+            return SGLangFlashInferFrontierModelBackend.commit_stage1_and_promote_many(
+                [self], [committed_route], [retained_routes])[0]
         nodes = self.route_store.node_path_for_route(committed_route)
         if not nodes:
             raise ValueError("cannot commit a stage-1 route with no materialized nodes")
@@ -1548,7 +1592,9 @@ class SGLangFlashInferFrontierModelBackend:
         if not (len(backends) == len(committed_routes) == len(retained_route_lists)):
             raise ValueError("one committed route and one retained list per backend are required")
         bridges = [b.route_pool for b in backends]
-        if len(backends) < 2 or not fused_frontier_supported(bridges):
+        if not bridges:
+            return []
+        if not fused_frontier_supported(bridges):
             return [b.commit_stage1_and_promote(committed_route=c, retained_routes=k)
                     for b, c, k in zip(backends, committed_routes, retained_route_lists)]
         node_paths = [b.route_store.node_path_for_route(c) for b, c in zip(backends, committed_routes)]
@@ -1571,8 +1617,7 @@ class SGLangFlashInferFrontierModelBackend:
             lives.append(sorted({int(n) for r in promoted for n in r.kv_view.node_ids}))
             results.append((promoted, {"committed_kv_tokens": len(nodes), "retained_routes": len(promoted),
                                        "released_route_rows": released_rows}))
-        refresh_prefix_page_ids(bridges)
-        counts = release_unreferenced_node_slots_many(bridges, lives)
+        counts = _sweep_bridges(bridges, lives, refresh_prefix=True)
         for (_, stats), n in zip(results, counts):
             stats["released_kv_pages"] = n
         return results
@@ -1580,6 +1625,16 @@ class SGLangFlashInferFrontierModelBackend:
     @torch.inference_mode()
     def decode_frontier_one_token(self, active_routes: Sequence[RouteState],
                                   attention_backend: object = None) -> FrontierDecodeOutput:
+        """One Drafter decode step of this request's routes
+        (``sglang_runtime.py:1299-1346``).  Over the native pools it is the
+        multi-request step for a single request (``decode_frontiers``: one
+        upload and one launch for the routes' paths, slots, rows and page
+        table, and deferred checks read back together at the next prune);
+        over other pools the per-route host path of ``prepare_frontier``.
+        Both leave the same bridge state."""
+        if fused_frontier_supported([self.route_pool]):
+            return SGLangFlashInferFrontierModelBackend._decode_fused(
+                [self], [active_routes], None, attention_backend)[0]
         start = time.perf_counter()
         before = self.route_pool.hot_path_counters()
         new_nodes = self.route_store.reserve_node_ids(len(active_routes))
@@ -1636,10 +1691,18 @@ class SGLangFlashInferFrontierModelBackend:
         bridges = [b.route_pool for b in backends]
         if not fused_frontier_supported(bridges):
             return [b.decode_frontier_one_token(rs, attention_backend) for b, rs in zip(backends, route_lists)]
+        return SGLangFlashInferFrontierModelBackend._decode_fused(backends, route_lists, executor, attention_backend)
+
+    @staticmethod
+    def _decode_fused(backends, route_lists, executor, attention_backend) -> list[FrontierDecodeOutput]:
+        """``decode_frontiers`` once ``fused_frontier_supported`` holds."""
+        if not all(route_lists):
+            raise ValueError("active_routes cannot be empty")
+        bridges = [b.route_pool for b in backends]
         start = time.perf_counter()
         before = [b.hot_path_counters() for b in bridges]
         new_nodes = [b.route_store.reserve_node_ids(len(rs)) for b, rs in zip(backends, route_lists)]
-        step = prepare_frontiers(bridges, route_lists)
+        step = _prepare_frontiers(bridges, route_lists)
         ex = executor if executor is not None else backends[0].executor
         _ready_runner(ex)
         logits = ex.forward_frontier(input_ids=step.input_ids, route_kv_metadata=step.metadata)
@@ -1649,7 +1712,7 @@ class SGLangFlashInferFrontierModelBackend:
             lo, hi = step.spans[i]
             b.route_pool.register_node_slots(new_nodes[i], out_slots[lo:hi])
             ps = int(b.route_pool.page_size)
-            prevs = [int(x) - 1 for x in step.metadata.seq_lens_cpu[lo:hi].tolist()]
+            prevs = step.prevs[lo:hi]
             outputs.append(b._frontier_output(
                 step.route_ids[lo:hi], logits[lo:hi], new_nodes[i], start, before[i], ps,
                 sum(prevs) + len(prevs), sum((p + ps) // ps for p in prevs), attention_backend))

@@ -149,7 +149,9 @@ def append_token_pool(
         layer_tables = _layer_tables(k_layers, v_layers)
     k_tab, v_tab, geom = layer_tables
     src_stride = k_src[0].stride(0) * k_src[0].element_size()
-    for t in (*k_src, *v_src):
+    # each distinct source tensor is checked once (callers often pass one
+    # tensor for several layers)
+    for t in {id(t): t for t in (*k_src, *v_src)}.values():
         if t.dtype != k_layers[0].dtype:
             raise TypeError(f"source dtype {t.dtype} does not match the pool dtype {k_layers[0].dtype}")
         if int(t.shape[0]) < n or not rows_contiguous(t):

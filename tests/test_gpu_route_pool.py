@@ -186,8 +186,13 @@ def test_device_ownership_set_operations(dev):
     assert own == set()
 
 
-def test_frontier_page_metadata_matches_oracle(dev):
+def test_frontier_page_metadata_matches_oracle(dev, monkeypatch):
+    """The per-route host path of prepare_frontier (what a bridge over other
+    pools runs; over the native pools a request's step goes through the
+    multi-request launch, checked in test_fused_frontier_metadata_matches_oracle)."""
     from oracle import paged_kv as ref
+    sr = pkg("flashinfer_paged.sglang_runtime")
+    monkeypatch.setattr(sr, "fused_frontier_supported", lambda bridges: False)
     dw = pkg("drafter_workload")
     npool = pkg("flashinfer_paged.native_pool")
     req, kv, alloc = npool.create_native_pools(num_pages=640, page_size=64, dtype=torch.bfloat16, head_num=8,

@@ -587,10 +587,10 @@ def test_fused_step_flags_raise_in_prepare_frontier_order():
     sr._StepFlags(torch.tensor([1, 0, 1, 1], dtype=torch.int64)).check(0, False)  # layout not validated
 
 
-def test_pending_step_checks_read_in_one_copy_and_raise_in_order():
+def test_pending_step_checks_read_once_and_raise_in_order():
     """The flags of every fused step with a check pending on a set of bridges
-    are read once, together; the checks then raise in the order recorded,
-    and a bridge's pending list is empty after its checks ran."""
+    are brought to the host once; the checks then raise in the order
+    recorded, and a bridge's pending list is empty after its checks ran."""
     sr, _ = _mods()
 
     class Bridge:
