@@ -265,7 +265,12 @@ def _tree_spec(
 
 def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
                        parent_indices) -> TreeSpec:
-    buf = torch.from_numpy(host).to(device)
+    buf = torch.from_numpy(host)
+    if device.type == "cuda":
+        # pinned, so the copy is queued without waiting for the device
+        buf = buf.pin_memory().to(device, non_blocking=True)
+    else:
+        buf = buf.to(device)
     o64 = 0
     n64 = len(i64)
     flat_token_ids = buf[o64 * 8:(o64 + node_count) * 8].view(torch.int64)

@@ -226,6 +226,39 @@ def commit_positions_need_staging(
     return False
 
 
+_LAYER_TABLES: dict = {}
+
+
+def _paged_layer_tables(layers: Sequence[torch.Tensor]):
+    """(slot geometry, K pointer table, V pointer table) of a list of paged
+    layers, kept for the most recent few layer sets: a Target commits into
+    the same layer tensors every verify.  The key holds every layer's address
+    and the first layer's shape, strides and dtype, so a changed list never
+    reuses a stale table."""
+    l0 = layers[0]
+    key = (tuple(int(t.data_ptr()) for t in layers), tuple(l0.shape), l0.stride(), l0.dtype)
+    hit = _LAYER_TABLES.get(key)
+    if hit is None:
+        for t in layers[1:]:
+            if t.shape != l0.shape or t.stride() != l0.stride() or t.dtype != l0.dtype:
+                raise ValueError("every layer must have the first layer's shape, strides and dtype")
+        geom, v_off = paged_layer_geometry(l0)
+        k_ptrs, v_ptrs = _layer_ptrs(layers, v_off)
+        hit = (geom, _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs))
+        if len(_LAYER_TABLES) >= 8:
+            _LAYER_TABLES.pop(next(iter(_LAYER_TABLES)))
+        _LAYER_TABLES[key] = hit
+    return hit
+
+
+def _as_i32(t: torch.Tensor | None, device: torch.device) -> torch.Tensor | None:
+    if t is None:
+        return None
+    if t.device != device or t.dtype != torch.int32 or not t.is_contiguous():
+        t = t.to(device=device, dtype=torch.int32).contiguous()
+    return t
+
+
 def commit_paged(
     layers: Sequence[torch.Tensor],
     src_pos: Sequence[int] | torch.Tensor,
@@ -249,12 +282,11 @@ def commit_paged(
     if not layers:
         raise ValueError("no layers given")
     device = _lib.require_device(layers[0], kv_indptr, kv_indices, what="target_kv_commit")
-    geom, v_off = paged_layer_geometry(layers[0])
-    k_ptrs, v_ptrs = _layer_ptrs(layers, v_off)
+    geom, k_tab, v_tab = _paged_layer_tables(layers)
     lib = _lib.load()
     stream = _lib.stream_of(device)
-    i32_indptr = None if kv_indptr is None else kv_indptr.to(device=device, dtype=torch.int32).contiguous()
-    i32_indices = None if kv_indices is None else kv_indices.to(device=device, dtype=torch.int32).contiguous()
+    i32_indptr = _as_i32(kv_indptr, device)
+    i32_indices = _as_i32(kv_indices, device)
     host_lists = not isinstance(src_pos, torch.Tensor) and not isinstance(dst_pos, torch.Tensor) and (
         item_req is None or not isinstance(item_req, torch.Tensor)
     )
@@ -270,7 +302,7 @@ def commit_paged(
         staging = commit_positions_need_staging(src, dst, reqs) if needs_staging is None else needs_staging
         if n <= _lib.MAX_INLINE_ITEMS and not staging:
             rc = lib.atlas_kv_commit_paged_host(
-                _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs), len(layers), *geom.as_args(),
+                k_tab, v_tab, len(layers), *geom.as_args(),
                 _lib.ptr(i32_indptr), _lib.ptr(i32_indices),
                 (ctypes_i32 * n)(*reqs), (ctypes_i64 * n)(*src), (ctypes_i64 * n)(*dst), n, stream,
             )
@@ -296,7 +328,7 @@ def commit_paged(
             workspace = torch.empty(need, dtype=torch.uint8, device=device)
         ws_bytes = workspace.numel() * workspace.element_size()
     rc = lib.atlas_kv_commit_paged(
-        _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs), len(layers), *geom.as_args(),
+        k_tab, v_tab, len(layers), *geom.as_args(),
         _lib.ptr(i32_indptr), _lib.ptr(i32_indices), _lib.ptr(req_t), _lib.ptr(src_t), _lib.ptr(dst_t), n,
         1 if staging else 0, _lib.ptr(workspace if staging else None), ws_bytes, stream,
     )
