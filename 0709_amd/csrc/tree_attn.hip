@@ -80,6 +80,11 @@ struct AttnArgs {
   int64_t rope_stride_token;
   float scale_log2;  // sm_scale * log2(e)
   int mask_mode;
+  // Tree mask words per query row: 1 = one ancestor word relative to the
+  // request's mask_col_start; > 1 = one visibility word per 64-key tile from
+  // the tile holding mask_col_start to the last key (wide trees, see
+  // tile_mask_word).
+  int mask_words;
   int group;
   int num_qo_heads;
   int page_size;
@@ -227,6 +232,18 @@ __device__ __forceinline__ uint32_t key_bits4(int mode, uint64_t tbits, int clim
   const uint32_t causal = key_bits4<ATLAS_MASK_CAUSAL>(tbits, climit, p0, col0, kv_end);
   const uint32_t none = key_bits4<ATLAS_MASK_NONE>(tbits, climit, p0, col0, kv_end);
   return mode == ATLAS_MASK_TREE ? tree : (mode == ATLAS_MASK_CAUSAL ? causal : none);
+}
+
+// Wide tree masks (more than 64 tree columns): the row's visibility word for
+// the 64 keys of the tile starting at t0 (a multiple of 64): word
+// t0 / 64 - col0 / 64 of the row's words, whose bit b covers key t0 + b
+// (prefix keys set).  Tiles before the tree's first tile are wholly visible.
+// Tested with key_bits4 against the window at t0 (col0 := t0).
+__device__ __forceinline__ uint64_t tile_mask_word(const AttnArgs& a, int64_t row, int t0, int col0) {
+  const int idx = (t0 >> 6) - (col0 >> 6);
+  if (idx < 0) return ~0ull;
+  if (idx >= a.mask_words) return 0ull;
+  return a.tree_mask[row * a.mask_words + idx];
 }
 
 // Position inside a 32-key block of V^T at which key k (0..31) is stored.  The
@@ -380,7 +397,8 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
       if (!row_ok[rt]) v = uint4{0, 0, 0, 0};
       qf[rt][ks] = __builtin_bit_cast(frag, v);
     }
-    tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && row_ok[rt]) ? a.tree_mask[qo_start + node_of[rt]] : 0ull;
+    tbits[rt] = (a.mask_mode == ATLAS_MASK_TREE && a.mask_words == 1 && row_ok[rt])
+                    ? a.tree_mask[qo_start + node_of[rt]] : 0ull;
     climit[rt] = kv_len - qo_len + node_of[rt];
   }
 
@@ -503,9 +521,15 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
       if (need_mask) {
+        uint64_t wbits = tbits[rt];
+        int wcol0 = col0;
+        if (a.mask_mode == ATLAS_MASK_TREE && a.mask_words > 1) {
+          wbits = row_ok[rt] ? tile_mask_word(a, int64_t(qo_start + node_of[rt]), t0, col0) : 0ull;
+          wcol0 = t0;
+        }
 #pragma unroll
         for (int kt = 0; kt < 4; ++kt) {
-          const uint32_t vis = key_bits4(a.mask_mode, tbits[rt], climit[rt], t0 + kt * 16 + grp * 4, col0, kv_end);
+          const uint32_t vis = key_bits4(a.mask_mode, wbits, climit[rt], t0 + kt * 16 + grp * 4, wcol0, kv_end);
 #pragma unroll
           for (int i = 0; i < 4; ++i) s[rt][kt][i] = ((vis >> i) & 1u) ? s[rt][kt][i] : -INFINITY;
         }
@@ -1239,10 +1263,23 @@ __device__ __forceinline__ void d128_load_rows(RowState<BF16, RT>& st, const Att
 // loading them before would put a round trip ahead of the first KV tile.
 template <bool BF16, int RT>
 __device__ __forceinline__ void d128_load_masks(RowState<BF16, RT>& st, const AttnArgs& a, const ItemCtx& c) {
-  if (a.mask_mode != ATLAS_MASK_TREE) return;
+  if (a.mask_mode != ATLAS_MASK_TREE || a.mask_words != 1) return;
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt)
     st.tbits[rt] = st.row_ok[rt] ? a.tree_mask[c.qo_start + st.node_of[rt]] : 0ull;
+}
+
+// The mask column start a masked tile at t0 is tested against: the request's
+// for one-word masks; for wide masks the tile's own start, after the rows'
+// words of that tile are loaded.  (A wide tree is the rare case: the load
+// waits for the loads in flight, the ring's included.)
+template <bool BF16, int RT>
+__device__ __forceinline__ int d128_tile_mask(RowState<BF16, RT>& st, const AttnArgs& a, const ItemCtx& c, int t0) {
+  if (a.mask_mode != ATLAS_MASK_TREE || a.mask_words == 1) return c.col0;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+    st.tbits[rt] = st.row_ok[rt] ? tile_mask_word(a, int64_t(c.qo_start + st.node_of[rt]), t0, c.col0) : 0ull;
+  return t0;
 }
 
 // Queries of the wave's rows from the LDS staging area into registers (rows
@@ -1311,9 +1348,11 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     }
     for (; t < n_pipe; ++t) {
       ring_step<NL>(r, t);
+      const int t0 = c.t_first + t * kTileKeys;
+      const int col0_t = d128_tile_mask<BF16, RT>(st, a, c, t0);
       d128_pipe_step<BF16, RT, NKT, kMasked>(st, s_cur, s_nxt, lds + (t % kStages128) * kTile128,
-                                             lds + ((t + 1) % kStages128) * kTile128, kb0, c.t_first + t * kTileKeys,
-                                             c.kv_end, c.col0, a.mask_mode, a.scale_log2, grp, r16);
+                                             lds + ((t + 1) % kStages128) * kTile128, kb0, t0,
+                                             c.kv_end, col0_t, a.mask_mode, a.scale_log2, grp, r16);
 #pragma unroll
       for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
@@ -1326,8 +1365,9 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
                                             grp, r16);
     else
       d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s_cur, lds + (t % kStages128) * kTile128, kb0,
-                                           c.t_first + t * kTileKeys, c.kv_end, c.col0, a.mask_mode, a.scale_log2,
-                                           grp, r16);
+                                           c.t_first + t * kTileKeys, c.kv_end,
+                                           d128_tile_mask<BF16, RT>(st, a, c, c.t_first + t * kTileKeys),
+                                           a.mask_mode, a.scale_log2, grp, r16);
   } else {
     f32x4 s[RT][NKT];
     int t = 0;
@@ -1340,8 +1380,10 @@ __device__ __forceinline__ void d128_loop(RowState<BF16, RT>& st, Ring<NL>& r, c
     }
     for (; t < nt; ++t) {
       const char* sb = lds + (t % kStages128) * kTile128;
+      const int t0 = c.t_first + t * kTileKeys;
+      const int col0_t = d128_tile_mask<BF16, RT>(st, a, c, t0);
       d128_scores<BF16, RT, NKT>(st, sb, kb0, grp, r16, s);
-      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s, sb, kb0, c.t_first + t * kTileKeys, c.kv_end, c.col0,
+      d128_softmax_pv<BF16, RT, NKT, kMasked>(st, s, sb, kb0, t0, c.kv_end, col0_t,
                                            a.mask_mode, a.scale_log2, grp, r16);
       ring_step<NL>(r, t);
     }
@@ -1794,7 +1836,7 @@ static int verify_attn_impl(bool use_scratch,
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
-    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
     const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
     int num_qo_heads, int num_kv_heads, int head_dim,
@@ -1814,6 +1856,8 @@ static int verify_attn_impl(bool use_scratch,
                 mask_mode);
   ATLAS_REQUIRE(mask_mode != ATLAS_MASK_TREE || (tree_mask_dev && mask_col_start_dev),
                 "tree mask mode needs tree_mask and mask_col_start");
+  ATLAS_REQUIRE(mask_mode != ATLAS_MASK_TREE || tree_mask_words >= 1, "tree_mask_words must be >= 1, got %d",
+                tree_mask_words);
   ATLAS_REQUIRE(num_work >= 0 && num_merge >= 0, "negative work counts");
   ATLAS_REQUIRE(max_rows_per_item > 0 && max_rows_per_item <= kMaxRowsPerItem,
                 "max_rows_per_item %d out of range (1..%d)", max_rows_per_item, kMaxRowsPerItem);
@@ -1855,6 +1899,7 @@ static int verify_attn_impl(bool use_scratch,
   args.lse = lse;
   args.scale_log2 = sm_scale * kLog2e;
   args.mask_mode = mask_mode;
+  args.mask_words = mask_mode == ATLAS_MASK_TREE ? tree_mask_words : 1;
   args.group = num_qo_heads / num_kv_heads;
   args.num_qo_heads = num_qo_heads;
   args.page_size = page_size;
@@ -1912,7 +1957,7 @@ extern "C" int atlas_tree_verify_attn(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
-    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
     const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
     int num_qo_heads, int num_kv_heads, int head_dim,
@@ -1921,7 +1966,7 @@ extern "C" int atlas_tree_verify_attn(
     void* stream) {
   return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
-                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, nullptr,
                           nullptr, 0, 0, nullptr, nullptr, 0);
@@ -1931,7 +1976,7 @@ extern "C" int atlas_tree_verify_attn_append(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
-    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
     const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
     int num_qo_heads, int num_kv_heads, int head_dim,
@@ -1954,7 +1999,7 @@ extern "C" int atlas_tree_verify_attn_append(
                 "append strides must be multiples of 8 elements");
   return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
-                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, workspace_dev, workspace_bytes, stream, append_k,
                           append_v, append_stride_token, append_stride_head, rope_cos, rope_sin, rope_stride_token);
@@ -2001,7 +2046,7 @@ extern "C" int atlas_tree_verify_attn_noalloc(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
     int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
-    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+    int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
     const atlas_attn_merge_t* merge_dev, int num_merge, int64_t merge_partial_rows, int max_rows_per_item,
     int num_qo_heads, int num_kv_heads, int head_dim, int page_size, float sm_scale, int dtype, void* out,
@@ -2025,7 +2070,7 @@ extern "C" int atlas_tree_verify_attn_noalloc(
                 (long long)merge_partial_rows, (long long)partial_rows);
   return verify_attn_impl(true, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
-                          mask_col_start_dev, work_dev, num_work, page_window_dev, merge_dev, num_merge,
+                          mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
                           out_stride_token, out_stride_head, lse, nullptr, size_t(partial_rows) * row_bytes,
                           stream, nullptr, nullptr, 0, 0, nullptr, nullptr, 0);

@@ -242,9 +242,12 @@ def _tree_spec(
     # nodes), qo/kv indptr, last page length and the identity page table
     # (int32), then the tree block of the mask (bool).
     compact = node_count <= 64
+    # wide trees: one visibility word per 64-key tile of the tree region
+    tiles = _tile_words(bits, prefix_len, kv_len) if 64 < node_count <= _MAX_TILE_NODES else None
     i64 = np.concatenate((
         np.asarray(token_ids, dtype=np.int64), np.asarray(depths, dtype=np.int64),
-        np.asarray([_signed64(b) for b in bits] if compact else [], dtype=np.int64)))
+        np.asarray([_signed64(b) for b in bits] if compact else [], dtype=np.int64),
+        tiles.reshape(-1).view(np.int64) if tiles is not None else np.zeros(0, dtype=np.int64)))
     i32 = np.concatenate((np.asarray([0, node_count, 0, total_pages, last], dtype=np.int32),
                           np.arange(total_pages, dtype=np.int32)))
     i32 = np.concatenate((i32, np.zeros(len(i32) % 2, dtype=np.int32)))  # keep the bool block 8-byte aligned
@@ -260,11 +263,34 @@ def _tree_spec(
     with torch.inference_mode(False):
         return _tree_spec_tensors(host, i64, i32, node_count=node_count, kv_len=kv_len, total_pages=total_pages,
                                   last=last, prefix_len=prefix_len, compact=compact, device=device,
-                                  parent_indices=parent_indices)
+                                  parent_indices=parent_indices,
+                                  tile_shape=None if tiles is None else tiles.shape)
+
+
+# Largest tree whose per-tile mask words the builder prepares on the host
+# (larger trees: the plan derives them from the dense mask).
+_MAX_TILE_NODES = 1024
+
+
+def _tile_words(bits: Sequence[int], prefix_len: int, kv_len: int) -> np.ndarray:
+    """[nodes, tiles] uint64: for tiles prefix_len // 64 .. (kv_len - 1) // 64,
+    bit b of word j is the visibility of key 64 (prefix_len // 64 + j) + b to
+    the node: prefix keys visible, tree key prefix_len + c iff bit c of the
+    node's ancestor bitmask."""
+    t0 = prefix_len // 64
+    ntiles = (kv_len - 1) // 64 - t0 + 1
+    low = prefix_len - 64 * t0
+    out = np.zeros((len(bits), ntiles), dtype=np.uint64)
+    full = (1 << 64) - 1
+    for i, b in enumerate(bits):
+        vis = (int(b) << low) | ((1 << low) - 1)
+        for j in range(ntiles):
+            out[i, j] = (vis >> (64 * j)) & full
+    return out
 
 
 def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
-                       parent_indices) -> TreeSpec:
+                       parent_indices, tile_shape=None) -> TreeSpec:
     buf = torch.from_numpy(host)
     if device.type == "cuda":
         # pinned, so the copy is queued without waiting for the device
@@ -276,6 +302,7 @@ def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last,
     flat_token_ids = buf[o64 * 8:(o64 + node_count) * 8].view(torch.int64)
     depths_t = buf[(o64 + node_count) * 8:(o64 + 2 * node_count) * 8].view(torch.int64)
     tree_mask = buf[2 * node_count * 8:n64 * 8].view(torch.int64) if compact else None
+    tile_words = buf[2 * node_count * 8:n64 * 8].view(torch.int64).view(tile_shape) if tile_shape else None
     b32 = n64 * 8
     qo_indptr = with_host_values(buf[b32:b32 + 8].view(torch.int32), [0, node_count])
     kv_indptr = with_host_values(buf[b32 + 8:b32 + 16].view(torch.int32), [0, total_pages])
@@ -292,6 +319,8 @@ def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last,
         # Lets the attention plan skip re-deriving the bitmask from the mask.
         # The version counter lets plan() notice an in-place change of the mask.
         flat_mask._atlas_tree_window = (prefix_len, tree_mask, tensor_version(flat_mask))
+    elif tile_words is not None:
+        flat_mask._atlas_tree_tiles = (prefix_len, tile_words, tensor_version(flat_mask))
     return TreeSpec(
         flat_token_ids=flat_token_ids,
         parent_indices=list(parent_indices),

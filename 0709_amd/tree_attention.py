@@ -26,7 +26,8 @@ TILE_KEYS = 64
 MAX_ROWS_PER_ITEM = 256  # 8 waves x 2 row tiles of 16 (head_dim 128, pages of >= 16 tokens)
 MAX_ROWS_PER_ITEM_OTHER = 192  # 4 waves x 3 row tiles of 16 (other shapes)
 DEFAULT_ROWS_PER_ITEM = 64  # 4 waves x 1 row tile
-MAX_TREE_WIDTH = 64
+MAX_TREE_WIDTH = 64  # tree columns one ancestor word per row covers
+MAX_WIDE_TREE_WIDTH = 4096  # tree columns of the per-tile word layout
 MAX_SPLITS = 1024
 DEFAULT_CU_COUNT = 256
 
@@ -69,6 +70,9 @@ class AttentionPlan:
     # run(append_key_states=...) can write the newest rows inside the launch:
     # head_dim-128 kernel, one row block per (request, KV head)
     fused_append: bool = False
+    # tree mask words per query row (1: one ancestor word; more: one word per
+    # 64-key tile of the tree region, for trees wider than 64 columns)
+    mask_words: int = 1
 
     def device_view(self, offset: int) -> int:
         return int(self.meta.data_ptr()) + 4 * offset
@@ -148,6 +152,28 @@ def tree_mask_from_dense(mask2d: torch.Tensor) -> tuple[int, torch.Tensor] | Non
     return col0, bits
 
 
+def tree_tile_words_from_dense(mask2d: torch.Tensor, max_width: int = MAX_WIDE_TREE_WIDTH):
+    """(col0, words) of a wide tree mask: col0 as for ``tree_mask_from_dense``
+    and, per query row, one visibility word per 64-key tile from the tile
+    holding col0 to the last key (bit b of word j: key 64 (col0 // 64 + j) +
+    b; columns below col0 are visible); None when the non-visible region
+    spans more than ``max_width`` columns."""
+    qo, kv = (int(x) for x in mask2d.shape)
+    m = mask2d.to(torch.bool)
+    false_cols = torch.nonzero(~m.all(dim=0)) if qo else torch.zeros((0, 1), dtype=torch.long)
+    col0 = kv if false_cols.numel() == 0 else int(false_cols[0])
+    if kv - col0 > max_width:
+        return None
+    t0 = col0 // 64
+    ntiles = max(0, (kv - 1) // 64 - t0 + 1) if kv else 0
+    window = torch.zeros((qo, ntiles * 64), dtype=torch.int64, device=m.device)
+    if ntiles:
+        window[:, : kv - t0 * 64] = m[:, t0 * 64 : kv].to(torch.int64)
+    shifts = torch.arange(64, device=m.device, dtype=torch.int64)
+    words = (window.view(qo, ntiles, 64) << shifts).sum(dim=2)
+    return col0, words
+
+
 def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     """The (col0, bits) window the tree builder attached to a single-request
     dense mask, if it still describes this plan: one request, one ancestor
@@ -169,6 +195,28 @@ def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     if kv_lens[0] - int(col0) > MAX_TREE_WIDTH:
         return None
     return int(col0), bits
+
+
+def _cached_tree_tiles(custom_mask, qo_lens: list[int], kv_lens: list[int]):
+    """The per-tile words (``tree_tile_words_from_dense``) the tree builder
+    attached to a single-request dense mask of a wide tree, if they still
+    describe this plan and the mask is unchanged since (version counter);
+    otherwise None."""
+    cached = getattr(custom_mask, "_atlas_tree_tiles", None) if custom_mask is not None else None
+    if cached is None or len(qo_lens) != 1 or len(cached) != 3:
+        return None
+    col0, words, version = cached
+    from .flashinfer_full_verify import tensor_version
+
+    if version is None or version != tensor_version(custom_mask) or \
+            int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
+        return None
+    ntiles = max(0, (kv_lens[0] - 1) // 64 - int(col0) // 64 + 1) if kv_lens[0] else 0
+    if words.ndim != 2 or int(words.shape[0]) != qo_lens[0] or int(words.shape[1]) != ntiles:
+        return None
+    if not (0 <= int(col0) <= kv_lens[0]) or kv_lens[0] - int(col0) > MAX_WIDE_TREE_WIDTH:
+        return None
+    return int(col0), words
 
 
 def unpack_bits_little(packed: torch.Tensor, count: int) -> torch.Tensor:
@@ -323,16 +371,28 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # ---- mask ----
         mask_mode = _lib.MASK_CAUSAL if causal else _lib.MASK_NONE
         tree_bits = None
+        mask_words = 1
         cols = [0] * batch
         if custom_mask is not None or packed_custom_mask is not None:
             if causal:
                 raise ValueError("custom masks require causal=False")
             mask_mode = _lib.MASK_TREE
             cached = _cached_tree_window(custom_mask, qo_lens, kv_lens)
+            cached_tiles = None if cached is not None else _cached_tree_tiles(custom_mask, qo_lens, kv_lens)
             if cached is not None:
                 col0, bits = cached
                 cols = [int(col0)]
                 tree_bits = bits.to(device=device, dtype=torch.int64)
+            elif cached_tiles is not None:
+                col0, words = cached_tiles
+                cols = [int(col0)]
+                mask_words = max(1, int(words.shape[1]))
+                tree_bits = words.to(device=device, dtype=torch.int64)
+                if mask_words == 1:
+                    # a one-tile window still uses the per-tile layout (two words)
+                    mask_words = 2
+                    tree_bits = torch.cat((tree_bits, torch.zeros_like(tree_bits)), dim=1)
+                tree_bits = tree_bits.reshape(-1)
             else:
                 total = sum(qo_lens[b] * kv_lens[b] for b in range(batch))
                 if custom_mask is not None:
@@ -342,35 +402,54 @@ class BatchPrefillWithPagedKVCacheWrapper:
                 if int(flat.numel()) != total:
                     raise ValueError(f"custom mask has {int(flat.numel())} entries, expected {total}")
                 parts = []
+                segs = []
                 off = 0
                 for b in range(batch):
                     seg = flat[off : off + qo_lens[b] * kv_lens[b]].view(qo_lens[b], kv_lens[b])
                     off += qo_lens[b] * kv_lens[b]
-                    res = tree_mask_from_dense(seg)
+                    segs.append(seg)
+                    res = tree_mask_from_dense(seg) if parts is not None else None
                     if res is None:
-                        raise NotImplementedError(
-                            f"request {b}: the mask's non-visible region spans more than "
-                            f"{MAX_TREE_WIDTH} key columns; only prefix + tree masks are supported"
-                        )
+                        parts = None  # some request is wide: every request takes the per-tile layout
+                        continue
                     cols[b] = res[0]
                     parts.append(res[1])
-                tree_bits = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.int64, device=device)
+                if parts is not None:
+                    tree_bits = torch.cat(parts) if parts else torch.zeros(0, dtype=torch.int64, device=device)
+                else:
+                    # a tree wider than 64 columns: one word per 64-key tile
+                    # of every request's tree region
+                    tiles = []
+                    for b, seg in enumerate(segs):
+                        res = tree_tile_words_from_dense(seg)
+                        if res is None:
+                            raise NotImplementedError(
+                                f"request {b}: the mask's non-visible region spans more than "
+                                f"{MAX_WIDE_TREE_WIDTH} key columns; only prefix + tree masks are supported"
+                            )
+                        cols[b] = res[0]
+                        tiles.append(res[1])
+                    mask_words = max(2, max(int(t.shape[1]) for t in tiles))
+                    tree_bits = torch.cat([torch.nn.functional.pad(t, (0, mask_words - int(t.shape[1])))
+                                           for t in tiles]).reshape(-1)
 
         # ---- work decomposition (the same inputs give the same work list) ----
         ws_rows_cap = self._workspace.numel() * self._workspace.element_size() // _partial_row_bytes(d)
         key = (tuple(qo), tuple(kvp), tuple(kv_lens), tuple(cols), hq, hkv, d, ps, self.max_rows_per_item,
-               self.split_target_items, self.min_tiles_per_split, self.split_granule_keys, ws_rows_cap)
+               self.split_target_items, self.min_tiles_per_split, self.split_granule_keys, ws_rows_cap, mask_words)
         if self._decomp_cache is None or self._decomp_cache[0] != key:
             self._decomp_cache = (key, self._decompose(batch=batch, qo=qo, kvp=kvp, qo_lens=qo_lens,
                                                        kv_lens=kv_lens, cols=cols, hq=hq, hkv=hkv, d=d, ps=ps,
-                                                       ws_rows_cap=ws_rows_cap))
+                                                       ws_rows_cap=ws_rows_cap, whole_tiles=mask_words > 1))
         dec = self._decomp_cache[1]
         self._install(
             batch=batch, hq=hq, hkv=hkv, d=d, ps=ps, sm_scale=sm_scale, q_dtype=q_dtype, kv_dtype=kv_dtype,
             mask_mode=mask_mode, dec=dec, kv_lens=kv_lens, qo_lens=qo_lens,
-            indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits, non_blocking=non_blocking)
+            indices_src=paged_kv_indices.reshape(-1), tree_bits=tree_bits, mask_words=mask_words,
+            non_blocking=non_blocking)
 
-    def _decompose(self, *, batch, qo, kvp, qo_lens, kv_lens, cols, hq, hkv, d, ps, ws_rows_cap) -> dict:
+    def _decompose(self, *, batch, qo, kvp, qo_lens, kv_lens, cols, hq, hkv, d, ps, ws_rows_cap,
+                   whole_tiles=False) -> dict:
         """Work and merge items of a plan, and the int32 metadata the kernels
         read: [work items | merge items | kv_len | mask_col_start | qo_indptr |
         kv_indptr]."""
@@ -406,7 +485,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             if rows == 0:
                 blocks.append((b, 0, 0))
         gran = TILE_KEYS
-        if direct and self.split_granule_keys is not None:
+        # (wide tree masks are read per 64-key tile: their splits start on tiles)
+        if direct and self.split_granule_keys is not None and not whole_tiles:
             gran = int(self.split_granule_keys)
             if gran <= 0 or gran > TILE_KEYS or gran % min(ps, TILE_KEYS) != 0 or TILE_KEYS % gran != 0:
                 raise ValueError(f"split_granule_keys must divide {TILE_KEYS} and be a multiple of "
@@ -464,7 +544,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
                          cols=cols, qo=qo, kvp=kvp)
 
     def _install(self, *, batch, hq, hkv, d, ps, sm_scale, q_dtype, kv_dtype, mask_mode, dec, kv_lens, qo_lens,
-                 indices_src, tree_bits, non_blocking) -> None:
+                 indices_src, tree_bits, non_blocking, mask_words=1) -> None:
         """Write a planned work list (``dec``, from ``_decompose``) into the
         persistent device buffers and make it the current plan."""
         device = self.device
@@ -505,7 +585,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
             sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
             q_dtype=q_dtype, kv_dtype=kv_dtype, nnz=dec["qo"][-1] - dec["qo"][0] if batch else 0,
             mask_mode=mask_mode, qo_indptr=meta[dec["qo_off"]:], kv_indptr=meta[dec["kvp_off"]:],
-            kv_indices=indices, tree_mask=bits_buf, meta=meta, num_work=len(work), num_merge=dec["num_merge"],
+            kv_indices=indices, tree_mask=bits_buf, mask_words=int(mask_words), meta=meta, num_work=len(work),
+            num_merge=dec["num_merge"],
             work_offset=0, merge_offset=dec["merge_off"], kv_len_offset=dec["kvlen_off"],
             col_offset=dec["col_off"], max_rows=dec["max_rows"], partial_rows=dec["partial_rows"],
             kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=dec["tiles_per_split"], page_windows=windows,
@@ -615,7 +696,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride,
             _lib.ptr(plan.qo_indptr), _lib.ptr(plan.kv_indptr), _lib.ptr(plan.kv_indices),
             plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
-            plan.device_view(plan.col_offset), plan.device_view(plan.work_offset), plan.num_work,
+            plan.device_view(plan.col_offset), plan.mask_words, plan.device_view(plan.work_offset), plan.num_work,
             _lib.ptr(plan.page_windows) if plan.page_windows is not None else None,
             plan.device_view(plan.merge_offset) if plan.num_merge else None, plan.num_merge,
             plan.partial_rows if plan.num_merge else 0, plan.max_rows,

@@ -166,7 +166,14 @@ int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
 /* Mask modes. */
 #define ATLAS_MASK_NONE 0   /* every key < kv_len visible */
 #define ATLAS_MASK_TREE 1   /* keys < mask_col_start[req] visible; key p >= that
-                               visible iff bit (p - start) of tree_mask[q] */
+                               visible iff bit (p - start) of tree_mask[q]
+                               (tree_mask_words == 1); with
+                               tree_mask_words = W > 1 (wide trees), row q
+                               holds W words at tree_mask[q * W ..], word j
+                               covering the 64 keys of tile
+                               start / 64 + j (bit b: key 64 (start / 64 + j)
+                               + b, prefix keys set), and every work item
+                               must start at a multiple of 64 keys */
 #define ATLAS_MASK_CAUSAL 2 /* key p visible iff p <= kv_len - qo_len + q */
 
 /* O = softmax(Q K^T * sm_scale + M) V over paged KV, GQA (num_qo_heads a
@@ -192,6 +199,7 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
                            const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                            const int32_t* kv_len_dev, int mask_mode,
                            const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                           int tree_mask_words,
                            const atlas_attn_work_t* work_dev, int num_work,
                            const int32_t* page_window_dev,
                            const atlas_attn_merge_t* merge_dev, int num_merge,
@@ -224,6 +232,7 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
                                   const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                   const int32_t* kv_len_dev, int mask_mode,
                                   const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                                  int tree_mask_words,
                                   const atlas_attn_work_t* work_dev, int num_work,
                                   const int32_t* page_window_dev,
                                   const atlas_attn_merge_t* merge_dev, int num_merge,
@@ -263,6 +272,7 @@ int atlas_tree_verify_attn_noalloc(const void* q, int64_t q_stride_token, int64_
                                    const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                    const int32_t* kv_len_dev, int mask_mode,
                                    const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
+                                   int tree_mask_words,
                                    const atlas_attn_work_t* work_dev, int num_work,
                                    const int32_t* page_window_dev,
                                    const atlas_attn_merge_t* merge_dev, int num_merge,

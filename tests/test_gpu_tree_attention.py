@@ -727,3 +727,98 @@ def test_random_request_mixes_match_oracle(dev, seed):
     case = f"seed {seed}: hq {hq} hkv {hkv} d {d} ps {ps} {dtype} batch {batch}"
     assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL, case
     assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL, case
+
+
+@pytest.mark.parametrize("n_routes,prefix_len,split_target", [
+    (17, 300, None),    # 68 nodes: two tiles of words, unaligned tree start
+    (32, 64, 1024),     # 128 nodes from a tile boundary, many splits
+    (64, 4000, 240),    # 256 nodes after a long prefix: the tree spans five tiles of the last splits
+    (64, 16, 4096),     # 256 nodes after a tiny prefix, most items masked
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_wide_trees_beyond_64_columns(dev, n_routes, prefix_len, split_target, dtype):
+    """Trees of 65 to 256 nodes (one visibility word per 64-key tile of the
+    tree region), with and without splits, against the oracle; the dominant
+    tree case puts almost all softmax mass on each row's own ancestors, so a
+    wrong word or bit shows in full."""
+    gen = torch.Generator().manual_seed(n_routes + prefix_len)
+    routes = _routes(gen, n_routes, 4, share=False)
+    for dominant in (False, True):
+        c = _build(dev, seed=n_routes + prefix_len + dominant, prefix_len=prefix_len, routes=routes, dtype=dtype,
+                   dominant_tree=dominant)
+        assert c["n"] > 64
+        w, _, _ = _run_and_check(dev, c, split_target=split_target)
+        plan = w.current_plan
+        assert plan.mask_words >= 2
+        assert plan.mask_words == (c["kv_len"] - 1) // 64 - prefix_len // 64 + 1
+
+
+def test_wide_tree_masks_batched_with_narrow_and_dense_paths(dev):
+    """A batch mixing a 130-node tree with 12-node trees in one plan (the
+    dense mask path: every request in the per-tile layout), and a 68-node tree
+    planned from a packed mask, against the oracle request by request; also
+    the head_dim 64 kernel on a wide tree."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    gen = torch.Generator().manual_seed(21)
+    for d, hq, hkv in ((128, 32, 8), (64, 32, 8)):
+        ps = 16
+        prefixes = [700, 37, 2100]
+        route_sets = [_routes(gen, 3, 4, share=True), _routes(gen, 33, 4, share=False), _routes(gen, 3, 4, share=False)]
+        specs, qs, masks, kv_lens, pages_per, lasts = [], [], [], [], [], []
+        for p, routes in zip(prefixes, route_sets):
+            spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=routes, prefix_len=p, page_size=ps,
+                                                                  device=dev)
+            _, parents, _, _ = ref.dedup_tree(routes)
+            specs.append(spec)
+            masks.append(ref.ancestor_mask(parents, p))
+            qs.append(torch.randn((spec.node_count, hq, d), generator=gen))
+            kv_lens.append(p + spec.node_count)
+            pages_per.append(math.ceil(kv_lens[-1] / ps))
+            lasts.append(ffv.last_page_len(kv_lens[-1], ps))
+        assert specs[1].node_count > 128
+        total_pages = sum(pages_per)
+        pool = total_pages + 40
+        perm = torch.randperm(pool, generator=gen)[:total_pages].to(torch.int32)
+        kv = torch.randn((pool, 2, ps, hkv, d), generator=gen)
+        kv[:, 1] *= 0.1
+        kv = kv.to(torch.float16)
+        q = torch.cat(qs).to(torch.float16)
+        qo, kvp = [0], [0]
+        for s_, p_ in zip(specs, pages_per):
+            qo.append(qo[-1] + s_.node_count)
+            kvp.append(kvp[-1] + p_)
+        flat_mask = torch.cat([torch.from_numpy(m.reshape(-1)) for m in masks]).to(dev)
+        ws = torch.empty(64 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        w.plan(torch.tensor(qo, dtype=torch.int32, device=dev), torch.tensor(kvp, dtype=torch.int32, device=dev),
+               perm.to(dev), torch.tensor(lasts, dtype=torch.int32, device=dev), hq, hkv, d, ps,
+               custom_mask=flat_mask, q_data_type=torch.float16)
+        assert w.current_plan.mask_words >= 2
+        out, lse = w.run(q.to(dev), kv.to(dev), return_lse=True)
+        torch.cuda.synchronize()
+        ro, rl = oatt.masked_attention(q.float().numpy().astype(np.float64), kv.float().numpy().astype(np.float64),
+                                       qo, kvp, perm.tolist(), lasts, masks=masks)
+        assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL, d
+        assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL, d
+    # one request, a packed mask (no attached window: derived from the mask)
+    routes = _routes(gen, 17, 4, share=False)
+    c = _build(dev, seed=5, prefix_len=500, routes=routes)
+    _run_and_check(dev, c, use_packed=True)
+
+
+def test_wide_tree_mask_refused_beyond_its_width(dev):
+    """A mask whose non-visible region spans more columns than the per-tile
+    layout covers is refused at plan time."""
+    ta = pkg("tree_attention")
+    n, kv = 2, ta.MAX_WIDE_TREE_WIDTH + 70
+    mask = torch.ones((n, kv), dtype=torch.bool)
+    mask[0, 5] = False
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=dev)
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    pages = math.ceil(kv / 16)
+    with pytest.raises(NotImplementedError, match="spans more than"):
+        w.plan(torch.tensor([0, n], dtype=torch.int32, device=dev), torch.tensor([0, pages], dtype=torch.int32,
+               device=dev), torch.arange(pages, dtype=torch.int32, device=dev),
+               torch.tensor([kv - (pages - 1) * 16], dtype=torch.int32, device=dev), 32, 8, 128, 16,
+               custom_mask=mask.reshape(-1).to(dev), q_data_type=torch.float16)

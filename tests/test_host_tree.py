@@ -154,3 +154,49 @@ def test_cached_values_under_inference_mode():
         assert ta._cached_tree_window(mask, [spec.node_count], [spec.kv_len]) is None
     # the host lists then come from the tensors themselves
     assert ta._host_lists(foreign)[0] == [0, 5]
+
+
+def test_wide_tree_tile_words_match_brute_force():
+    """Per-tile mask words of trees wider than 64 columns: the builder's host
+    words, the plan's words derived from the dense mask and a brute-force
+    reading of the oracle's dense ancestor mask agree bit for bit (prefixes on
+    and off a tile boundary, 68 to 255 nodes)."""
+    import random
+
+    import numpy as np
+
+    from oracle import paged_kv as ref
+
+    ffv = pkg("flashinfer_full_verify")
+    ta = pkg("tree_attention")
+    rng = random.Random(3)
+    for n_routes, prefix in ((17, 100), (32, 64), (64, 1000), (40, 0)):
+        paths = [tuple(rng.randrange(500) for _ in range(4)) for _ in range(n_routes)]
+        spec, _ = ffv.build_deduplicated_tree_spec_from_paths(paths=paths, prefix_len=prefix, page_size=16,
+                                                              device="cpu")
+        n, kv = spec.node_count, spec.kv_len
+        assert n > 64
+        _, parents, _, _ = ref.dedup_tree(paths)
+        dense = ref.ancestor_mask(parents, prefix)
+        t0 = prefix // 64
+        ntiles = (kv - 1) // 64 - t0 + 1
+        brute = np.zeros((n, ntiles), dtype=np.uint64)
+        for i in range(n):
+            for j in range(ntiles):
+                word = 0
+                for b in range(64):
+                    key = 64 * (t0 + j) + b
+                    if key < kv and dense[i, key]:
+                        word |= 1 << b
+                brute[i, j] = word
+        col0, words, _ = spec.bool_mask._atlas_tree_tiles
+        assert col0 == prefix and np.array_equal(words.numpy().view(np.uint64), brute)
+        c2, w2 = ta.tree_tile_words_from_dense(torch.from_numpy(dense))
+        assert c2 == prefix and np.array_equal(w2.numpy().view(np.uint64), brute)
+        assert ta._cached_tree_tiles(spec.bool_mask, [n], [kv]) is not None
+        assert ta._cached_tree_tiles(spec.bool_mask, [n], [kv + 64]) is None
+        assert ta._cached_tree_window(spec.bool_mask, [n], [kv]) is None
+    # beyond the per-tile layout's width: refused
+    wide = torch.ones((2, ta.MAX_WIDE_TREE_WIDTH + 10), dtype=torch.bool)
+    wide[0, 3] = False
+    assert ta.tree_tile_words_from_dense(wide) is None
