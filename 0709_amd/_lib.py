@@ -59,6 +59,15 @@ class AttnWork(ctypes.Structure):
     ]
 
 
+class SlotPath(ctypes.Structure):
+    """atlas_slot_path_t (16 bytes)."""
+    _fields_ = [("slots", ctypes.c_void_p), ("len", _c_i64)]
+
+
+PRUNE_MAX_PATHS = 64
+PRUNE_PATHS_MAX_PAGES = 524288  # atlas_prune_pages_paths: one workgroup's LDS bitmap
+
+
 class AttnMerge(ctypes.Structure):
     """atlas_attn_merge_t (32 bytes)."""
     _fields_ = [
@@ -106,6 +115,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "atlas_attn_page_windows": [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp],
     "atlas_prune_pages": [_vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp],
+    "atlas_prune_pages_paths": [_vp, _vp, _c_i64, _vp, ctypes.c_int, ctypes.c_uint64, _c_i64, _vp, _vp, _vp],
     "atlas_mark_pages": [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp],
     "atlas_alloc_decode_slots": [_vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
     "atlas_alloc_extend_slots": [_vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _vp, _vp],
@@ -207,7 +217,15 @@ def require_device(*tensors: torch.Tensor | None, what: str) -> torch.device:
     return device
 
 
+# torch's current raw stream handle, without building a Stream object
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(device: torch.device) -> ctypes.c_void_p:
+    """The device's current HIP stream, as a launch argument."""
+    if _RAW_STREAM is not None:
+        idx = device.index
+        return ctypes.c_void_p(_RAW_STREAM(torch.cuda.current_device() if idx is None else idx))
     return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
 
 
@@ -230,3 +248,122 @@ def dtype_code(dtype: torch.dtype) -> int:
     if dtype == torch.float32:
         return DTYPE_F32
     raise TypeError(f"unsupported dtype {dtype}; expected float16 or bfloat16")
+
+
+class HostStaging:
+    """Pinned host memory (``hipHostMalloc``) for small host-to-device
+    uploads, handed out from a ring of four quarters.
+
+    A quarter is written again only after the copies queued from it have run:
+    when the ring leaves a quarter it records an event on the stream that
+    copied from it, and waits for that event before it enters the quarter
+    again (a quarter that more than one stream copied from waits for those
+    devices instead).  torch's pinned allocator records an event per copy;
+    this records one per quarter, so a small upload costs one numpy write and
+    one asynchronous copy."""
+
+    def __init__(self, nbytes: int = 4 << 20) -> None:
+        self.quarter = (nbytes // 4) & ~63
+        self.nbytes = 4 * self.quarter
+        p = ctypes.c_void_p()
+        rc = _hip_runtime().hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(self.nbytes), ctypes.c_uint(1))
+        if rc != 0 or not p.value:
+            raise RuntimeError(f"hipHostMalloc of {self.nbytes} staging bytes failed ({rc})")
+        buf = (ctypes.c_uint8 * self.nbytes).from_address(p.value)
+        self.host = torch.frombuffer(buf, dtype=torch.uint8)
+        self.host_np = self.host.numpy()
+        self.cur = 0  # the quarter being filled; pos never leaves it but by _leave/_enter
+        self.pos = 0
+        self.events: list = [None] * 4
+        self.users: list[set] = [set() for _ in range(4)]
+        self.lock = threading.Lock()
+
+    def _enter(self, q: int) -> None:
+        ev = self.events[q]
+        if isinstance(ev, torch.cuda.Event):
+            ev.synchronize()
+        elif ev is not None:
+            for dev in ev:
+                torch.cuda.synchronize(dev)
+        self.events[q] = None
+        self.users[q] = set()
+
+    def _leave(self, q: int) -> None:
+        users = self.users[q]
+        if not users:
+            return
+        if len(users) == 1:
+            (dev, raw), = users
+            stream = torch.cuda.current_stream(dev)
+            if stream.cuda_stream == raw:
+                ev = torch.cuda.Event()
+                ev.record(stream)
+                self.events[q] = ev
+                return
+        self.events[q] = sorted({dev for dev, _ in users})
+
+    def upload(self, host: "np.ndarray", device: torch.device) -> torch.Tensor:
+        """A device copy (uint8, ``host.nbytes`` long) of a contiguous numpy
+        array, queued on the device's current stream."""
+        import numpy as np
+
+        nbytes = int(host.nbytes)
+        src = np.ascontiguousarray(host).reshape(-1).view(np.uint8)
+        if nbytes > self.quarter or nbytes == 0:
+            return torch.from_numpy(src.copy()).to(device, non_blocking=False)
+        idx = torch.cuda.current_device() if device.index is None else device.index
+        with self.lock:
+            q = self.cur
+            start = self.pos
+            if start + nbytes > (q + 1) * self.quarter:
+                self._leave(q)
+                q = self.cur = (q + 1) % 4
+                self._enter(q)
+                start = q * self.quarter
+            self.host_np[start : start + nbytes] = src
+            out = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            out.copy_(self.host[start : start + nbytes], non_blocking=True)
+            self.users[q].add((idx, _RAW_STREAM(idx) if _RAW_STREAM is not None else
+                               torch.cuda.current_stream(idx).cuda_stream))
+            self.pos = (start + nbytes + 63) & ~63
+        return out
+
+    def upload_i64(self, values: Sequence[int], device: torch.device) -> torch.Tensor:
+        """``torch.tensor(values, dtype=torch.int64)`` on ``device``."""
+        import numpy as np
+
+        return self.upload(np.asarray(values, dtype=np.int64), device).view(torch.int64)
+
+
+_HIP = None
+_STAGING: HostStaging | None = None
+
+
+def _hip_runtime() -> ctypes.CDLL:
+    """The HIP runtime torch has loaded (resolved by its soname, so no second
+    copy is loaded)."""
+    global _HIP
+    if _HIP is None:
+        hip = ctypes.CDLL("libamdhip64.so.7")
+        hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
+        hip.hipHostMalloc.restype = ctypes.c_int
+        _HIP = hip
+    return _HIP
+
+
+def staging() -> HostStaging:
+    """The process's pinned upload ring (created on first use)."""
+    global _STAGING
+    if _STAGING is None:
+        with _lock:
+            if _STAGING is None:
+                _STAGING = HostStaging()
+    return _STAGING
+
+
+def upload_i64(values: Sequence[int], device: torch.device) -> torch.Tensor:
+    """int64 values on ``device``: through the pinned ring on a HIP device,
+    a plain tensor elsewhere."""
+    if device.type != "cuda":
+        return torch.tensor(values, dtype=torch.int64, device=device)
+    return staging().upload_i64(values, device)

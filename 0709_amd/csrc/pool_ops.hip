@@ -81,34 +81,14 @@ constexpr int64_t kFusedWords = 16384;
 constexpr int kFusedBatch = 4;
 constexpr int64_t kFusedMaxSlots = int64_t(kSweepThreads) * kFusedBatch;
 
-__global__ __launch_bounds__(kSweepThreads) void prune_fused_kernel(uint32_t* owned, uint32_t* live_out,
-                                                                    int64_t num_pages, int64_t num_words,
-                                                                    const int64_t* slots, int64_t n,
-                                                                    int64_t page_size, int page_shift,
-                                                                    int64_t* free_pages, int64_t* free_count) {
-  __shared__ uint32_t live[kFusedWords];
-  __shared__ int64_t scan[kSweepThreads];
+// Sweep phase of the one-workgroup prunes: `live` (LDS) holds the marked
+// pages; every owned page not live is released in ascending order (a scan of
+// per-thread counts over contiguous word ranges gives each thread its output
+// position), owned keeps owned & live, and the live bitmap is written out.
+__device__ __forceinline__ void fused_sweep(uint32_t* owned, uint32_t* live_out, const uint32_t* live,
+                                            int64_t num_words, int64_t* scan, int64_t* free_pages,
+                                            int64_t* free_count) {
   const int tid = threadIdx.x;
-  for (int64_t w = tid; w < num_words; w += kSweepThreads) live[w] = 0u;
-  __syncthreads();
-  {
-    int64_t cur[kFusedBatch], prev[kFusedBatch];
-#pragma unroll
-    for (int k = 0; k < kFusedBatch; ++k) {
-      const int64_t i = int64_t(k) * kSweepThreads + tid;
-      cur[k] = i < n ? slots[i] : -1;
-      prev[k] = (i > 0 && i < n) ? slots[i - 1] : -1;
-    }
-#pragma unroll
-    for (int k = 0; k < kFusedBatch; ++k) {
-      if (cur[k] < 0) continue;
-      const int64_t page = page_shift >= 0 ? cur[k] >> page_shift : cur[k] / page_size;
-      if (page >= num_pages) continue;
-      if (prev[k] >= 0 && (page_shift >= 0 ? prev[k] >> page_shift : prev[k] / page_size) == page) continue;
-      atomicOr(&live[page >> 5], 1u << (page & 31));
-    }
-  }
-  __syncthreads();
   const int64_t per = (num_words + kSweepThreads - 1) / kSweepThreads;
   const int64_t w0 = min(num_words, int64_t(tid) * per);
   const int64_t w1 = min(num_words, w0 + per);
@@ -136,6 +116,78 @@ __global__ __launch_bounds__(kSweepThreads) void prune_fused_kernel(uint32_t* ow
     live_out[w] = lv;
   }
   if (tid == kSweepThreads - 1) *free_count = scan[tid];
+}
+
+__device__ __forceinline__ int64_t page_of(int64_t slot, int64_t page_size, int page_shift) {
+  return page_shift >= 0 ? slot >> page_shift : slot / page_size;
+}
+
+__global__ __launch_bounds__(kSweepThreads) void prune_fused_kernel(uint32_t* owned, uint32_t* live_out,
+                                                                    int64_t num_pages, int64_t num_words,
+                                                                    const int64_t* slots, int64_t n,
+                                                                    int64_t page_size, int page_shift,
+                                                                    int64_t* free_pages, int64_t* free_count) {
+  __shared__ uint32_t live[kFusedWords];
+  __shared__ int64_t scan[kSweepThreads];
+  const int tid = threadIdx.x;
+  for (int64_t w = tid; w < num_words; w += kSweepThreads) live[w] = 0u;
+  __syncthreads();
+  {
+    int64_t cur[kFusedBatch], prev[kFusedBatch];
+#pragma unroll
+    for (int k = 0; k < kFusedBatch; ++k) {
+      const int64_t i = int64_t(k) * kSweepThreads + tid;
+      cur[k] = i < n ? slots[i] : -1;
+      prev[k] = (i > 0 && i < n) ? slots[i - 1] : -1;
+    }
+#pragma unroll
+    for (int k = 0; k < kFusedBatch; ++k) {
+      if (cur[k] < 0) continue;
+      const int64_t page = page_of(cur[k], page_size, page_shift);
+      if (page >= num_pages) continue;
+      if (prev[k] >= 0 && page_of(prev[k], page_size, page_shift) == page) continue;
+      atomicOr(&live[page >> 5], 1u << (page & 31));
+    }
+  }
+  __syncthreads();
+  fused_sweep(owned, live_out, live, num_words, scan, free_pages, free_count);
+}
+
+// The live paths of a prune by paths, by value in the kernel arguments.
+struct PrunePaths {
+  atlas_slot_path_t p[ATLAS_PRUNE_MAX_PATHS];
+};
+
+// Prune whose live slots are sampled from slot paths in the kernel: path p
+// contributes slots[0], slots[ps], slots[2 ps], ... and, when bit p of
+// last_mask is set, slots[len - 1] -- one slot of every page of a path laid
+// out in whole pages.  Then the sweep of prune_fused_kernel.
+__global__ __launch_bounds__(kSweepThreads) void prune_paths_kernel(uint32_t* owned, uint32_t* live_out,
+                                                                    int64_t num_pages, int64_t num_words,
+                                                                    PrunePaths paths, int num_paths,
+                                                                    uint64_t last_mask, int64_t page_size,
+                                                                    int page_shift, int64_t* free_pages,
+                                                                    int64_t* free_count) {
+  __shared__ uint32_t live[kFusedWords];
+  __shared__ int64_t scan[kSweepThreads];
+  const int tid = threadIdx.x;
+  for (int64_t w = tid; w < num_words; w += kSweepThreads) live[w] = 0u;
+  __syncthreads();
+  for (int p = 0; p < num_paths; ++p) {
+    const int64_t* slots = paths.p[p].slots;
+    const int64_t len = paths.p[p].len;
+    if (len <= 0) continue;
+    const int64_t starts = (len + page_size - 1) / page_size;
+    const int64_t samples = starts + ((last_mask >> p) & 1ull);
+    for (int64_t j = tid; j < samples; j += kSweepThreads) {
+      const int64_t slot = slots[j < starts ? j * page_size : len - 1];
+      if (slot < 0) continue;
+      const int64_t page = page_of(slot, page_size, page_shift);
+      if (page < num_pages) atomicOr(&live[page >> 5], 1u << (page & 31));
+    }
+  }
+  __syncthreads();
+  fused_sweep(owned, live_out, live, num_words, scan, free_pages, free_count);
 }
 
 // Page tables from concatenated slot paths.  Thread per page: the page id is
@@ -421,6 +473,31 @@ extern "C" int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitm
   hipLaunchKernelGGL(sweep_kernel, dim3(1), dim3(kSweepThreads), 0, s, owned_bitmap_dev, live_bitmap_dev,
                      words, free_pages_dev, free_count_dev);
   return launch_status("sweep_kernel");
+}
+
+extern "C" int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                                       const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
+                                       int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev,
+                                       void* stream) {
+  ATLAS_REQUIRE(owned_bitmap_dev && live_bitmap_dev && free_pages_dev && free_count_dev,
+                "prune buffers must not be NULL");
+  ATLAS_REQUIRE(num_pages > 0 && page_size > 0, "num_pages and page_size must be positive");
+  ATLAS_REQUIRE(num_paths >= 0 && (num_paths == 0 || paths), "paths must not be NULL");
+  if (num_paths > ATLAS_PRUNE_MAX_PATHS || (num_pages + 31) / 32 > kFusedWords) {
+    set_error("prune by paths takes at most %d paths and %lld pages (got %d, %lld)", ATLAS_PRUNE_MAX_PATHS,
+              static_cast<long long>(kFusedWords * 32), num_paths, static_cast<long long>(num_pages));
+    return ATLAS_EUNSUPPORTED;
+  }
+  PrunePaths pp{};
+  for (int p = 0; p < num_paths; ++p) {
+    ATLAS_REQUIRE(paths[p].len >= 0 && (paths[p].len == 0 || paths[p].slots), "path %d: bad slots or length", p);
+    pp.p[p] = paths[p];
+  }
+  const int64_t words = (num_pages + 31) / 32;
+  hipLaunchKernelGGL(prune_paths_kernel, dim3(1), dim3(kSweepThreads), 0, static_cast<hipStream_t>(stream),
+                     owned_bitmap_dev, live_bitmap_dev, num_pages, words, pp, num_paths, last_slot_mask, page_size,
+                     ilog2_exact(page_size), free_pages_dev, free_count_dev);
+  return launch_status("prune_paths_kernel");
 }
 
 extern "C" int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_dev,

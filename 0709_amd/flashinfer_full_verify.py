@@ -21,7 +21,7 @@ from typing import Sequence
 import numpy as np
 import torch
 
-from . import kv_ops
+from . import _lib, kv_ops
 from .tree_attention import BatchPrefillWithPagedKVCacheWrapper
 
 
@@ -291,12 +291,11 @@ def _tile_words(bits: Sequence[int], prefix_len: int, kv_len: int) -> np.ndarray
 
 def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
                        parent_indices, tile_shape=None) -> TreeSpec:
-    buf = torch.from_numpy(host)
     if device.type == "cuda":
-        # pinned, so the copy is queued without waiting for the device
-        buf = buf.pin_memory().to(device, non_blocking=True)
+        # through pinned staging, so the copy is queued without waiting for the device
+        buf = _lib.staging().upload(host, device)
     else:
-        buf = buf.to(device)
+        buf = torch.from_numpy(host).to(device)
     o64 = 0
     n64 = len(i64)
     flat_token_ids = buf[o64 * 8:(o64 + node_count) * 8].view(torch.int64)

@@ -20,6 +20,7 @@ freed-page order identical):
 from __future__ import annotations
 
 import ctypes
+import operator
 import sys
 import time
 from dataclasses import dataclass, field
@@ -118,6 +119,31 @@ class DeviceOwnedPages:
                                    int(s.numel()), self.page_size, _lib.ptr(self.free_pages),
                                    _lib.ptr(self.free_count), _lib.stream_of(self.device))
         _lib.check(rc, "atlas_prune_pages")
+
+    def sweep_paths_launch(self, paths: Sequence[torch.Tensor], with_last: Sequence[bool]) -> bool:
+        """``sweep_launch`` whose live slots are sampled from slot paths in
+        the launch (path p: its page-start slots, plus its last slot when
+        ``with_last[p]``), with no sample list built first.  Returns False,
+        launching nothing, when the paths are not contiguous int64 device
+        tensors or exceed the launch's limits (then use ``sweep_launch``)."""
+        n = len(paths)
+        if n > _lib.PRUNE_MAX_PATHS or self.num_pages > _lib.PRUNE_PATHS_MAX_PAGES:
+            return False
+        arr = (_lib.SlotPath * max(n, 1))()
+        mask = 0
+        for i, (t, last) in enumerate(zip(paths, with_last)):
+            if t.dtype != torch.int64 or not t.is_contiguous() or t.device != self.device:
+                return False
+            arr[i].slots = t.data_ptr()
+            arr[i].len = t.numel()
+            if last:
+                mask |= 1 << i
+        lib = _lib.load()
+        rc = lib.atlas_prune_pages_paths(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, arr, n, mask,
+                                         self.page_size, _lib.ptr(self.free_pages), _lib.ptr(self.free_count),
+                                         _lib.stream_of(self.device))
+        _lib.check(rc, "atlas_prune_pages_paths")
+        return True
 
     # -- set protocol -----------------------------------------------------
     def to_set(self) -> set[int]:
@@ -536,28 +562,38 @@ class SGLangRoutePoolBridge:
     def release_unreferenced_node_slots(self, live_node_ids: Sequence[int]) -> int:
         """Return every owned page that neither the committed prefix nor a
         retained route reaches, in ascending page order; forget dead node
-        mappings (``sglang_runtime.py:507-539``).  Returns the page count."""
-        self.check_pending_device_checks()
+        mappings (``sglang_runtime.py:507-539``).  Returns the page count.
+        The deferred device checks run first (over native pools: with the
+        sweep's count read-back, before any page returns to the free list)."""
         if self._device_ownership:
-            released = self.owned_page_ids.sweep(self._live_slot_samples())
-            count = int(released.numel())
-        else:
-            self._materialize_pending_owned_pages()
-            live_pages = set(self.prefix_page_ids)
-            for pages in self._page_id_sets_for_paths(list(self.route_slot_paths.values())):
-                live_pages.update(pages)
-            releasable = sorted(self.owned_page_ids - live_pages)
-            count = len(releasable)
+            return _sweep_bridges([self], [live_node_ids], refresh_prefix=False)[0]
+        self.check_pending_device_checks()
+        self._materialize_pending_owned_pages()
+        live_pages = set(self.prefix_page_ids)
+        for pages in self._page_id_sets_for_paths(list(self.route_slot_paths.values())):
+            live_pages.update(pages)
+        releasable = sorted(self.owned_page_ids - live_pages)
         self._forget_dead_nodes(live_node_ids)
-        if count:
+        if releasable:
             self._require_allocator_free()
-            if self._device_ownership:
-                self.token_to_kv_pool_allocator.free_pages_prepend(released.clone())
-            else:
-                self.token_to_kv_pool_allocator.free(
-                    torch.tensor([p * self.page_size for p in releasable], dtype=torch.long, device=self.device))
-                self.owned_page_ids.difference_update(releasable)
-        return count
+            self.token_to_kv_pool_allocator.free(
+                torch.tensor([p * self.page_size for p in releasable], dtype=torch.long, device=self.device))
+            self.owned_page_ids.difference_update(releasable)
+        return len(releasable)
+
+    def _live_paths(self) -> tuple[list[torch.Tensor], list[bool]]:
+        """The slot paths ``_live_slot_samples`` samples, and whether each
+        contributes its last slot: the prefix (page starts only), then each
+        retained route's path."""
+        paths, last = [], []
+        if self.prefix_slot_ids is not None and int(self.prefix_slot_ids.numel()):
+            paths.append(self.prefix_slot_ids)
+            last.append(False)
+        for path in self.route_slot_paths.values():
+            if int(path.numel()):
+                paths.append(path)
+                last.append(True)
+        return paths, last
 
     def _live_slot_samples(self) -> torch.Tensor:
         """One slot of every page the prefix and the retained routes reach:
@@ -928,15 +964,20 @@ class SGLangRoutePoolBridge:
             dirty[index] = prevs[index] - tail
         starts: list[int] = []
         kinds: list[str] = []
+        cap = _req_pool_capacity(self.req_to_token_pool)
+        if cap is None:
+            cap = self.max_context_len
+        route_rows = self.route_rows
         for i, (route, prev, req_row) in enumerate(zip(active_routes, prevs, rows)):
-            row = self.route_rows[int(route.route_id)]
-            if int(row.written_length) == 0:
+            row = route_rows[int(route.route_id)]
+            written = int(row.written_length)
+            if written == 0:
                 start, kind = 0, "full_init"
             else:
-                if int(row.written_length) != prev:
+                if written != prev:
                     raise RuntimeError(
                         "SGLang route-row state does not match its physical KV path: "
-                        f"route_id={int(route.route_id)}, written_length={int(row.written_length)}, "
+                        f"route_id={int(route.route_id)}, written_length={written}, "
                         f"physical_path_length={prev}"
                     )
                 pending = row.pending_dirty_start
@@ -946,7 +987,8 @@ class SGLangRoutePoolBridge:
                     start, kind = prev, "append"
                 else:
                     start, kind = int(pending), "cow_patch"
-            self._check_req_write(req_row, start, prev + 1 - start, kind)
+            if start < 0 or start > prev or (cap is not None and prev + 1 > int(cap)):
+                self._check_req_write(req_row, start, prev + 1 - start, kind)  # raises with the reason
             starts.append(start)
             kinds.append(kind)
         for i, p in enumerate(paths):
@@ -1133,7 +1175,7 @@ class SGLangRoutePoolBridge:
         self._count_req_write(n, write_kind)
 
     def hot_path_counters(self) -> dict[str, int]:
-        return {name: int(getattr(self, name)) for name in _COUNTERS}
+        return dict(zip(_COUNTERS, map(int, _get_counters(self))))
 
 
 @dataclass
@@ -1162,52 +1204,58 @@ class _StepCheck:
         self.step_flags.check(self.group, self.validate_layout)
 
 
-def _prefetch_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> None:
-    """Brings the flags of every fused frontier step with a check pending on
-    these bridges to the host (each step's copy was queued behind its launch,
-    so this waits only for those copies)."""
+def _unread_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> list["_StepFlags"]:
+    """Flags of the fused frontier steps with a check pending on these
+    bridges that are still on the device (each step once)."""
+    out: list[_StepFlags] = []
+    seen: set[int] = set()
     for b in bridges:
         for c in b.pending_device_checks:
             f = getattr(c, "step_flags", None)
-            if f is not None:
-                f.host()
+            if f is not None and f._host is None and id(f) not in seen:
+                seen.add(id(f))
+                out.append(f)
+    return out
+
+
+def _read_back(parts: Sequence[torch.Tensor], bridges: Sequence["SGLangRoutePoolBridge"]) -> list[int]:
+    """ONE copy to the host of the int64 tensors ``parts`` together with the
+    flags of every fused frontier step with a check pending on ``bridges``;
+    returns the values of ``parts``, concatenated."""
+    flags = _unread_step_flags(bridges)
+    tensors = [*parts, *(f.flags for f in flags)]
+    if not tensors:
+        return []
+    flat = _int_list(torch.cat(tensors) if len(tensors) > 1 else tensors[0])
+    off = sum(int(t.numel()) for t in parts)
+    head = flat[:off]
+    for f in flags:
+        n = int(f.flags.numel())
+        f._host = flat[off : off + n]
+        off += n
+    return head
+
+
+def _prefetch_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> None:
+    """Brings the flags of every fused frontier step with a check pending on
+    these bridges to the host, in one copy."""
+    _read_back([], bridges)
 
 
 class _StepFlags:
     """Check flags of one fused frontier step (device int64s the kernel
-    clears on a failed check).  On a device, a copy into pinned host memory is
-    queued right behind the step's launch, so the check that reads the flags
-    (at the next prune) finds them on the host instead of waiting for the
-    device work issued since."""
-
-    # (pinned buffer, event) pairs of flags already read, by flag count
-    _spare: dict[int, list] = {}
+    clears on a failed check).  They stay on the device until a check needs
+    them: the prune reads the flags of every pending step back in the copy
+    that brings its released-page counts, so a decode step queues no copy of
+    its own."""
 
     def __init__(self, flags: torch.Tensor) -> None:
         self.flags = flags
         self._host: list[int] | None = None
-        self._staged = None
-        if flags.device.type == "cuda":
-            n = int(flags.numel())
-            spare = _StepFlags._spare.get(n)
-            if spare:
-                pinned, ready = spare.pop()
-            else:
-                pinned, ready = torch.empty(n, dtype=flags.dtype, pin_memory=True), torch.cuda.Event()
-            pinned.copy_(flags, non_blocking=True)
-            ready.record(torch.cuda.current_stream(flags.device))
-            self._staged = (pinned, ready)
 
     def host(self) -> list[int]:
         if self._host is None:
-            if self._staged is not None:
-                pinned, ready = self._staged
-                ready.synchronize()
-                self._host = [int(x) for x in pinned.tolist()]
-                self._staged = None
-                _StepFlags._spare.setdefault(len(self._host), []).append((pinned, ready))
-            else:
-                self._host = [int(x) for x in self.flags.cpu().tolist()]
+            self._host = _int_list(self.flags)
         return self._host
 
     def check(self, group: int, validate_layout: bool) -> None:
@@ -1242,22 +1290,36 @@ class FusedFrontierStep:
 _ROUTE_FIELDS = 14  # int64 fields of one frontier route descriptor
 
 
+# (allocator, request pool, request table, result) of the last pools checked
+_NATIVE_POOLS: list = [None]
+
+
+def _native_pools(alloc: Any, req: Any) -> bool:
+    """A native paged allocator with a KV pool that moves rows, and a
+    request pool with a dense int64 device table on the allocator's device
+    (the answer for the last pools asked is kept)."""
+    table = getattr(req, "req_to_token", None)
+    hit = _NATIVE_POOLS[0]
+    if hit is not None and hit[0] is alloc and hit[1] is req and hit[2] is table:
+        return hit[3]
+    ok = (callable(getattr(alloc, "consume_pages", None)) and callable(getattr(alloc, "get_kvcache", None))
+          and callable(getattr(alloc.get_kvcache(), "move_kv_cache", None))
+          and isinstance(table, torch.Tensor) and table.ndim == 2 and table.dtype == torch.int64
+          and table.is_contiguous() and table.device == alloc.device)
+    _NATIVE_POOLS[0] = (alloc, req, table, bool(ok))
+    return bool(ok)
+
+
 def fused_frontier_supported(bridges: Sequence[SGLangRoutePoolBridge]) -> bool:
     """True when ``prepare_frontiers`` can run these bridges in one launch:
     distinct bridges over one native paged allocator (device free list and
     page ownership), one request-row pool with a dense int64 device table,
     one KV pool with ``move_kv_cache``, one page size, page metadata on."""
-    if not bridges or len({id(b) for b in bridges}) != len(bridges):
+    if not bridges or (len(bridges) > 1 and len({id(b) for b in bridges}) != len(bridges)):
         return False
     b0 = bridges[0]
     alloc, req = b0.token_to_kv_pool_allocator, b0.req_to_token_pool
-    if not callable(getattr(alloc, "consume_pages", None)) or not callable(getattr(alloc, "get_kvcache", None)):
-        return False
-    if not callable(getattr(alloc.get_kvcache(), "move_kv_cache", None)):
-        return False
-    table = getattr(req, "req_to_token", None)
-    if not (isinstance(table, torch.Tensor) and table.ndim == 2 and table.dtype == torch.int64
-            and table.is_contiguous() and table.device == alloc.device):
+    if not _native_pools(alloc, req):
         return False
     for b in bridges:
         if b.token_to_kv_pool_allocator is not alloc or b.req_to_token_pool is not req:
@@ -1285,16 +1347,17 @@ def release_unreferenced_node_slots_many(bridges: Sequence[SGLangRoutePoolBridge
 def _sweep_bridges(bridges: Sequence[SGLangRoutePoolBridge], live_node_id_lists: Sequence[Sequence[int]], *,
                    refresh_prefix: bool) -> list[int]:
     """The native-pool prune of several bridges over one allocator: every
-    bridge's deferred checks first, every sweep launched, then ONE copy to
-    the host of the released-page counts (and, with ``refresh_prefix``, of
-    each bridge's prefix page ids: the page of every page-start slot);
-    the released pages are prepended bridge by bridge, so the free list ends
-    as one call per bridge in this order leaves it."""
-    _prefetch_step_flags(bridges)
+    sweep launched, then ONE copy to the host of the released-page counts,
+    the flags of the bridges' pending fused frontier steps (and, with
+    ``refresh_prefix``, each bridge's prefix page ids: the page of every
+    page-start slot).  The deferred checks then run, so a failed one raises
+    before any page goes back to the free list; the released pages are
+    prepended bridge by bridge, so the free list ends as one call per bridge
+    in this order leaves it."""
     for b in bridges:
-        b.check_pending_device_checks()
-    for b in bridges:
-        b.owned_page_ids.sweep_launch(b._live_slot_samples())
+        paths, last = b._live_paths()
+        if not b.owned_page_ids.sweep_paths_launch(paths, last):
+            b.owned_page_ids.sweep_launch(b._live_slot_samples())
     parts = [b.owned_page_ids.free_count for b in bridges]
     starts: list[int] = []
     if refresh_prefix:
@@ -1303,15 +1366,18 @@ def _sweep_bridges(bridges: Sequence[SGLangRoutePoolBridge], live_node_id_lists:
             if slots is None or int(slots.numel()) == 0:
                 starts.append(0)
                 continue
-            parts.append(torch.div(slots[:: b.page_size], b.page_size, rounding_mode="floor"))
+            parts.append(slots[:: b.page_size])
             starts.append(int(parts[-1].numel()))
-    flat = _int_list(torch.cat(parts) if len(parts) > 1 else parts[0])
+    flat = _read_back(parts, bridges)
+    for b in bridges:
+        b.check_pending_device_checks()
     counts = flat[: len(bridges)]
     if refresh_prefix:
         off = len(bridges)
         for b, c in zip(bridges, starts):
             b.prefix_slot_count = 0 if b.prefix_slot_ids is None else int(b.prefix_slot_ids.numel())
-            b.prefix_page_ids = set(flat[off:off + c])
+            ps = b.page_size
+            b.prefix_page_ids = {s // ps for s in flat[off:off + c]}
             off += c
     alloc = bridges[0].token_to_kv_pool_allocator
     for b, live, n in zip(bridges, live_node_id_lists, counts):
@@ -1393,23 +1459,17 @@ def _prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
     positions = [n - 1 for n in seq_lens]
     rows = [r for plan in plans for r in plan.rows]
     host = desc + [1] * (1 + 3 * nb) + tokens + seq_lens + positions + rows + route_ids
-    packed = torch.tensor(host, dtype=torch.int64, pin_memory=True).to(device, non_blocking=True)
-    o = _ROUTE_FIELDS * R
-    flags = packed[o : o + 1 + 3 * nb]
-    o += 1 + 3 * nb
-    input_ids, seq_dev, pos_dev, req_dev, rid_dev = (packed[o + k * R : o + (k + 1) * R] for k in range(5))
+    packed = _lib.upload_i64(host, device)
+    _, flags, input_ids, seq_dev, pos_dev, req_dev, rid_dev = packed.split(
+        [_ROUTE_FIELDS * R, 1 + 3 * nb, R, R, R, R, R])
 
     F, C, P = flat_off, cow_off, page_off
     # one allocation: the int64 outputs, then the int32 ones
     n64 = F + R + 2 * C
     n32 = 3 * R + 1 + P
     out = torch.empty(n64 + (n32 + 1) // 2, dtype=torch.int64, device=device)
-    out64 = out[:n64]
-    out32 = out[n64:].view(torch.int32)[:n32]
-    flat, out_slots = out64[:F], out64[F : F + R]
-    cow_dst, cow_src = out64[F + R : F + R + C], out64[F + R + C :]
-    kv_indptr, kv_last = out32[: R + 1], out32[R + 1 : 2 * R + 1]
-    seq32, page_ids = out32[2 * R + 1 : 3 * R + 1], out32[3 * R + 1 :]
+    flat, out_slots, cow_dst, cow_src, rest = out.split([F, R, C, C, (n32 + 1) // 2])
+    kv_indptr, kv_last, seq32, page_ids, _ = rest.view(torch.int32).split([R + 1, R, R, P, n32 % 2])
     lib = _lib.load()
     rc = lib.atlas_pool_prepare_frontier(
         _lib.ptr(packed), R, ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps,
@@ -1585,8 +1645,9 @@ class SGLangFlashInferFrontierModelBackend:
         in one copy and the prunes share one count read-back
         (``release_unreferenced_node_slots_many``), so the free list, the
         request rows and each request's state end as one call per request in
-        this order leaves them.  Requests with no committed node and the
-        deferred device checks are refused before any state changes.
+        this order leaves them.  Requests with no committed node are refused
+        before any state changes; the deferred device checks run with the
+        prunes' read-back, before any page returns to the free list.
         Otherwise one call per request.  Returns each request's
         ``(promoted routes, stats)``."""
         if not (len(backends) == len(committed_routes) == len(retained_route_lists)):
@@ -1600,9 +1661,6 @@ class SGLangFlashInferFrontierModelBackend:
         node_paths = [b.route_store.node_path_for_route(c) for b, c in zip(backends, committed_routes)]
         if not all(node_paths):
             raise ValueError("cannot commit a stage-1 route with no materialized nodes")
-        _prefetch_step_flags(bridges)
-        for br in bridges:
-            br.check_pending_device_checks()
         results, lives = [], []
         for b, committed, keep, nodes in zip(backends, committed_routes, retained_route_lists, node_paths):
             tokens = b.route_store.tokens_for_node_ids(nodes)
@@ -1668,7 +1726,7 @@ class SGLangFlashInferFrontierModelBackend:
                 "attention_metadata_page_size": int(page_size),
                 "attention_metadata_token_indices_step": int(token_indices),
                 "attention_metadata_page_indices_step": int(page_indices),
-                "hot_path_counter_delta": {k: int(after[k] - before.get(k, 0)) for k in after},
+                "hot_path_counter_delta": {k: v - before.get(k, 0) for k, v in after.items()},
                 "hot_path_counters_total": after,
                 "attention_backend": str(attention_backend),
                 **_executor_metadata(self.executor),
@@ -1925,6 +1983,7 @@ _COUNTERS = (
     "hot_path_host_transfer_batches",
     "hot_path_host_transfer_elements",
 )
+_get_counters = operator.attrgetter(*_COUNTERS)
 
 
 def _allocate_kv_slots(allocator: Any, count: int, *, mode: str) -> Any:

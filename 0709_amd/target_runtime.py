@@ -102,7 +102,7 @@ def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Seq
     # without waiting for the work ahead on the stream (the logits' producer)
     host = np.concatenate((np.asarray(tokens, dtype=np.int64).view(np.uint8),
                            np.asarray(rows, dtype=np.int32).view(np.uint8)))
-    idx = torch.from_numpy(host).pin_memory().to(device, non_blocking=True)
+    idx = _lib.staging().upload(host, device)
     tok = idx[: 8 * n].view(torch.int64)
     row = idx[8 * n:].view(torch.int32)
     lib = _lib.load()

@@ -869,39 +869,54 @@ def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
             layer_num=geom.layers, max_running_requests=128, max_context_len=4096, device=dev)
         rows = (torch.randn((2048, geom.kv_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
 
-        def writer(slots, vids, kv=kv, rows=rows):
+        model = [0.0]  # wall time inside the model stand-in since the last phase end
+
+        def writer(slots, vids, kv=kv, rows=rows, model=model):
+            t0 = time.perf_counter()
             n = int(slots.numel())
             kv.set_kv_buffer_all_layers(slots, [rows[:n]] * geom.layers, [rows[:n]] * geom.layers)
+            model[0] += time.perf_counter() - t0
 
         work = dw.DrafterForkWorkload(plans=dw.config5_plans(requests, ps, rep), req_pool=req_pool, allocator=alloc,
                                       page_size=ps, device=dev, writer=writer, batched=batched)
         marks = []
 
-        def on_phase(name, marks=marks):
+        def on_phase(name, marks=marks, model=model):
             torch.cuda.synchronize()
-            marks.append((name, time.perf_counter()))
+            marks.append((name, time.perf_counter(), model[0]))
+            model[0] = 0.0
 
         torch.cuda.synchronize()
-        marks.append(("start", time.perf_counter()))
+        marks.append(("start", time.perf_counter(), 0.0))
+        model[0] = 0.0
         work.run(on_phase)
         spans = {}
-        for (_, t0), (name, t1) in zip(marks, marks[1:]):
+        for (_, t0, _), (name, t1, m) in zip(marks, marks[1:]):
             spans[name] = (t1 - t0) * 1e6
+            spans[name + "/model"] = m * 1e6
         cow_pages = sum(r.bridge.cow_pages_copied for r in work.requests)
         cow_tokens = sum(r.bridge.cow_tokens_copied for r in work.requests)
         runs.append((spans, cow_pages, cow_tokens))
         del work, req_pool, kv, alloc
         torch.cuda.empty_cache()
     decode = [statistics.fmean(sp[f"decode{t}"] for t in range(8)) for sp, _, _ in runs]
+    decode_model = [statistics.fmean(sp[f"decode{t}/model"] for t in range(8)) for sp, _, _ in runs]
     return {
         "requests": requests, "routes_per_request": 9, "page_size": ps,
         "decode_step_us": round(statistics.median(decode), 1),
+        "decode_step_model_standin_us": round(statistics.median(decode_model), 1),
+        "decode_us_per_request_step": round(statistics.median(decode) / requests, 1),
+        "decode_bridge_us_per_request_step": round(
+            statistics.median(d - m for d, m in zip(decode, decode_model)) / requests, 1),
+        "commit_promote_prune_us_per_request": round(statistics.median(sp["commit"] for sp, _, _ in runs) / requests,
+                                                     1),
         "commit_promote_prune_us": round(statistics.median(sp["commit"] for sp, _, _ in runs), 1),
         "fallback_extend_us": round(statistics.median(sp["extend"] for sp, _, _ in runs), 1),
         "prefill_us": round(statistics.median(sp["prefill"] for sp, _, _ in runs), 1),
         "cow_pages_copied": runs[-1][1], "cow_tokens_copied": runs[-1][2],
         "batched_frontier_step": bool(batched),
-        "note": "wall time of the host-driven bridge per phase (all 8 requests), model replaced by a K/V append",
+        "note": "wall time of the host-driven bridge per phase (all 8 requests), model replaced by a K/V append "
+                "(decode_step_model_standin_us: the part of decode_step_us spent in that append)",
     }
 
 

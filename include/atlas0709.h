@@ -299,6 +299,30 @@ int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int
                       const int64_t* live_slots_dev, int64_t n_live_slots, int64_t page_size,
                       int64_t* free_pages_dev, int64_t* free_count_dev, void* stream);
 
+/* One live slot path of atlas_prune_pages_paths: `len` slot ids at `slots`
+ * (device memory). */
+typedef struct {
+  const int64_t* slots;
+  int64_t len;
+} atlas_slot_path_t;
+
+#define ATLAS_PRUNE_MAX_PATHS 64
+
+/* atlas_prune_pages with the live slots sampled from slot paths inside the
+ * launch: path p (host array `paths`, copied into the launch arguments)
+ * contributes its slots at indices 0, page_size, 2 page_size, ... and, when
+ * bit p of last_slot_mask is set, its last slot -- one slot of every page of
+ * a path laid out in whole pages (the committed prefix, and each retained
+ * route with its last slot).  At most ATLAS_PRUNE_MAX_PATHS paths and
+ * 524,288 pages (one workgroup's LDS bitmap); larger prunes return
+ * ATLAS_EUNSUPPORTED and go through atlas_prune_pages.  Same result as
+ * atlas_prune_pages over the concatenated samples; replaces the same
+ * release_unreferenced_node_slots (sglang_runtime.py:507-539), whose live set
+ * is the prefix plus every retained route's path. */
+int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                            const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
+                            int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev, void* stream);
+
 /* Set the owned bit of the pages of `n` slot ids (pages newly handed out). */
 int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev, int64_t n,
                      int64_t page_size, void* stream);

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 7
+    assert lib.atlas_abi_version() == 8
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -163,3 +163,30 @@ def test_verify_entry_points_refuse_too_few_partial_rows():
         assert b"merge items reference 65 partial rows" in lib.atlas_last_error(), name
         rc = getattr(lib, name)(*_verify_args(name, merge_rows=0))
         assert rc == lib_mod.ATLAS_EINVAL and b"merge items reference 0" in lib.atlas_last_error(), name
+
+
+def test_prune_by_paths_limits_without_device_work():
+    """atlas_prune_pages_paths refuses more than ATLAS_PRUNE_MAX_PATHS paths
+    or pools beyond one workgroup's bitmap (ATLAS_EUNSUPPORTED: the caller
+    prunes through atlas_prune_pages) and a path with NULL slots or a negative
+    length (ATLAS_EINVAL), before any launch."""
+    import ctypes
+
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    fake = ctypes.c_void_p(1 << 20)
+    paths = (lib_mod.SlotPath * 65)()
+    for p in paths:
+        p.slots, p.len = 1 << 20, 4
+
+    def call(n, num_pages=4096, arr=paths):
+        return lib.atlas_prune_pages_paths(fake, fake, num_pages, arr, n, 0, 16, fake, fake, None)
+
+    assert call(65) == lib_mod.ATLAS_EUNSUPPORTED and b"64 paths" in lib.atlas_last_error()
+    assert call(1, num_pages=lib_mod.PRUNE_PATHS_MAX_PAGES + 1) == lib_mod.ATLAS_EUNSUPPORTED
+    bad = (lib_mod.SlotPath * 2)()
+    bad[0].slots, bad[0].len = 1 << 20, 3
+    bad[1].slots, bad[1].len = None, 2
+    assert call(2, arr=bad) == lib_mod.ATLAS_EINVAL and b"path 1" in lib.atlas_last_error()
+    bad[1].slots, bad[1].len = 1 << 20, -1
+    assert call(2, arr=bad) == lib_mod.ATLAS_EINVAL

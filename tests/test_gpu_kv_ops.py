@@ -354,3 +354,33 @@ def test_random_commits_match_gather_then_scatter(dev, seed):
     case = f"seed {seed}: layers {layers} ps {ps} h {h} d {d} requests {nreq} items {len(req)} tensors {as_tensors}"
     for a, e in zip(devs, expect):
         np.testing.assert_array_equal(bits16(a), e, err_msg=case)
+
+
+def test_host_staging_ring_keeps_every_pending_upload(dev):
+    """Uploads through a small pinned ring (four 1 KiB quarters) that wraps
+    many times while its copies are still queued behind device work: every
+    upload arrives intact (a quarter is rewritten only after the copies out
+    of it ran), also when the stream changes between uploads."""
+    lib = pkg("_lib")
+    ring = lib.HostStaging(4096)
+    rng = np.random.default_rng(5)
+    side = torch.cuda.Stream()
+    sent, got = [], []
+    for i in range(300):
+        if i % 50 == 0:
+            # keep the device busy so copies stay queued while the host runs ahead
+            big = torch.randn((2048, 2048), device=dev)
+            big @ big
+        n = int(rng.integers(1, 1000))
+        host = rng.integers(0, 256, size=n, dtype=np.uint8)
+        sent.append(host)
+        if i % 7 == 3:
+            with torch.cuda.stream(side):
+                got.append(ring.upload(host, dev))
+        else:
+            got.append(ring.upload(host, dev))
+    torch.cuda.synchronize()
+    for h, d in zip(sent, got):
+        assert np.array_equal(d.cpu().numpy(), h)
+    vals = [int(x) for x in rng.integers(-2**62, 2**62, size=33)]
+    assert lib.upload_i64(vals, dev).cpu().tolist() == vals

@@ -102,6 +102,49 @@ def test_prune_fused_and_multi_launch_paths(dev, num_pages, n_slots, ps):
     assert _set_from_bitmap(live_bm) == live
 
 
+@pytest.mark.parametrize("num_pages,num_paths,ps", [(4096, 10, 16), (95367, 64, 64), (524288, 3, 16),
+                                                      (3000, 7, 24), (64, 1, 4)])
+def test_prune_by_paths_matches_oracle_and_sample_list(dev, num_pages, num_paths, ps):
+    """atlas_prune_pages_paths samples each path's page-start slots (and, for
+    paths with their bit in the mask, the last slot) inside the launch: the
+    released pages, the owned bitmap and the live bitmap equal the oracle's
+    prune of the same paths and atlas_prune_pages over the sample list
+    (sglang_runtime.py:507-539).  Empty paths and a prefix without its last
+    slot are included."""
+    lib = _lib()
+    rng = np.random.default_rng(num_pages * 7 + num_paths)
+    owned = set(rng.choice(num_pages, size=min(num_pages, 5000), replace=False).tolist())
+    paths, last = [], []
+    for i in range(num_paths):
+        pages = rng.choice(num_pages, size=min(num_pages, 40), replace=False)
+        length = 0 if i == 1 else int(rng.integers(1, len(pages) * ps + 1))
+        paths.append([int(pages[j // ps]) * ps + j % ps for j in range(length)])
+        last.append(i != 0)  # path 0 plays the prefix: page starts only
+    sampled = [s for p, l in zip(paths, last) for s in (p[::ps] + (p[-1:] if l else []))]
+    exp_freed, exp_left = _prune(dev, owned, sampled, num_pages, ps)
+    ref_freed, ref_left = ref.prune(owned, paths[0] or None, [p for p in paths[1:] if p], ps)
+    assert (exp_freed, exp_left) == (ref_freed, ref_left)
+
+    owned_bm = _bitmap(owned, num_pages, dev)
+    live_bm = torch.full_like(owned_bm, -1)
+    free = torch.full((num_pages,), -1, dtype=torch.int64, device=dev)
+    cnt = torch.zeros(1, dtype=torch.int64, device=dev)
+    tensors = [torch.tensor(p, dtype=torch.int64, device=dev) for p in paths]
+    arr = (lib.SlotPath * num_paths)()
+    mask = 0
+    for i, t in enumerate(tensors):
+        arr[i].slots, arr[i].len = (t.data_ptr() if t.numel() else None), t.numel()
+        mask |= (1 << i) if last[i] else 0
+    rc = lib.load().atlas_prune_pages_paths(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, arr, num_paths, mask,
+                                            ps, lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev))
+    lib.check(rc, "prune by paths")
+    torch.cuda.synchronize()
+    n = int(cnt.item())
+    assert free[:n].cpu().tolist() == exp_freed
+    assert _set_from_bitmap(owned_bm) == exp_left
+    assert _set_from_bitmap(live_bm) == {s // ps for s in sampled}
+
+
 def test_prune_empty_live_frees_everything_ascending(dev):
     owned = {5, 3, 900, 64, 31, 32}
     freed, left = _prune(dev, owned, [], 1000, 16)
