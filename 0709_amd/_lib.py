@@ -114,6 +114,7 @@ _SIGNATURES: dict[str, list] = {
         ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp,
     ],
     "atlas_attn_page_windows": [_vp, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp],
+    "atlas_attn_plan_install": [_vp, ctypes.c_int, _vp, _c_i64, _vp, _vp, _c_i64, _vp, ctypes.c_int, _vp, _vp],
     "atlas_prune_pages": [_vp, _vp, _c_i64, _vp, _c_i64, _c_i64, _vp, _vp, _vp],
     "atlas_prune_pages_paths": [_vp, _vp, _c_i64, _vp, ctypes.c_int, ctypes.c_uint64, _c_i64, _vp, _vp, _vp],
     "atlas_mark_pages": [_vp, _c_i64, _vp, _c_i64, _c_i64, _vp],
@@ -302,15 +303,25 @@ class HostStaging:
                 return
         self.events[q] = sorted({dev for dev, _ in users})
 
-    def upload(self, host: "np.ndarray", device: torch.device) -> torch.Tensor:
-        """A device copy (uint8, ``host.nbytes`` long) of a contiguous numpy
-        array, queued on the device's current stream."""
+    def upload(self, host: "np.ndarray", device: torch.device, out: torch.Tensor | None = None) -> torch.Tensor:
+        """A device copy (uint8, ``host.nbytes`` long) of a numpy array,
+        queued on the device's current stream; with ``out`` (a contiguous
+        device tensor of ``host.nbytes`` bytes) the bytes land there and
+        ``out`` is returned."""
         import numpy as np
 
         nbytes = int(host.nbytes)
         src = np.ascontiguousarray(host).reshape(-1).view(np.uint8)
+        if out is not None:
+            if not out.is_contiguous() or out.numel() * out.element_size() != nbytes:
+                raise ValueError("out must be a contiguous tensor of the array's size")
+            dst = out.view(-1).view(torch.uint8)
         if nbytes > self.quarter or nbytes == 0:
-            return torch.from_numpy(src.copy()).to(device, non_blocking=False)
+            staged = torch.from_numpy(src.copy())
+            if out is None:
+                return staged.to(device, non_blocking=False)
+            dst.copy_(staged)
+            return out
         idx = torch.cuda.current_device() if device.index is None else device.index
         with self.lock:
             q = self.cur
@@ -321,8 +332,9 @@ class HostStaging:
                 self._enter(q)
                 start = q * self.quarter
             self.host_np[start : start + nbytes] = src
-            out = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            out.copy_(self.host[start : start + nbytes], non_blocking=True)
+            if out is None:
+                out = dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
+            dst.copy_(self.host[start : start + nbytes], non_blocking=True)
             self.users[q].add((idx, _RAW_STREAM(idx) if _RAW_STREAM is not None else
                                torch.cuda.current_stream(idx).cuda_stream))
             self.pos = (start + nbytes + 63) & ~63
@@ -367,3 +379,4 @@ def upload_i64(values: Sequence[int], device: torch.device) -> torch.Tensor:
     if device.type != "cuda":
         return torch.tensor(values, dtype=torch.int64, device=device)
     return staging().upload_i64(values, device)
+

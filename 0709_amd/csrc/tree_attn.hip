@@ -1806,10 +1806,62 @@ __global__ __launch_bounds__(64) void attn_page_windows_kernel(const atlas_attn_
   window[int64_t(blockIdx.x) * 64 + l] = id;
 }
 
+// A plan's device set-up in one launch: blocks [0, num_work) write the page
+// windows (as attn_page_windows_kernel, reading the caller's page table), the
+// blocks after them copy the page table and the tree mask words into the
+// plan's own buffers.
+__global__ __launch_bounds__(64) void attn_plan_install_kernel(const atlas_attn_work_t* work, int num_work,
+                                                               const int32_t* src_indices, int64_t n_indices,
+                                                               int32_t* dst_indices, const int64_t* src_words,
+                                                               int64_t n_words, int64_t* dst_words, int page_shift,
+                                                               int32_t* window) {
+  if (int(blockIdx.x) < num_work) {
+    const atlas_attn_work_t w = work[blockIdx.x];
+    const int l = threadIdx.x;
+    const int kv_end = min(w.kv_end, w.kv_len);
+    const int t_first = w.kv_start < kv_end ? w.kv_start : kv_end;
+    int id = 0;
+    if (t_first < kv_end) {
+      const int page0 = t_first >> page_shift;
+      const int last_page = (kv_end - 1) >> page_shift;
+      id = src_indices[int64_t(w.page_offset) + min(page0 + l, last_page)];
+    }
+    window[int64_t(blockIdx.x) * 64 + l] = id;
+    return;
+  }
+  const int64_t stride = int64_t(gridDim.x - num_work) * 64;
+  const int64_t t = int64_t(blockIdx.x - num_work) * 64 + threadIdx.x;
+  for (int64_t i = t; i < n_indices; i += stride) dst_indices[i] = src_indices[i];
+  for (int64_t i = t; i < n_words; i += stride) dst_words[i] = src_words[i];
+}
+
 }  // namespace
 }  // namespace atlas
 
 using namespace atlas;
+
+extern "C" int atlas_attn_plan_install(const atlas_attn_work_t* work_dev, int num_work,
+                                       const int32_t* src_indices_dev, int64_t n_indices, int32_t* dst_indices_dev,
+                                       const int64_t* src_words_dev, int64_t n_words, int64_t* dst_words_dev,
+                                       int page_size, int32_t* window_dev, void* stream) {
+  ATLAS_REQUIRE(num_work >= 0 && n_indices >= 0 && n_words >= 0, "negative count");
+  ATLAS_REQUIRE(n_indices == 0 || (src_indices_dev && dst_indices_dev), "page table buffers must not be NULL");
+  ATLAS_REQUIRE(n_words == 0 || (src_words_dev && dst_words_dev), "mask word buffers must not be NULL");
+  const int windows = window_dev != nullptr ? num_work : 0;
+  if (windows) {
+    ATLAS_REQUIRE(work_dev && src_indices_dev, "windows need the work list and the page table");
+    ATLAS_REQUIRE(page_size > 0 && (page_size & (page_size - 1)) == 0, "page_size must be a power of two, got %d",
+                  page_size);
+  }
+  const int64_t most = n_indices > n_words ? n_indices : n_words;
+  const int copy_blocks = most > 0 ? static_cast<int>(std::min<int64_t>((most + 255) / 256, 256)) : 0;
+  if (windows + copy_blocks == 0) return ATLAS_OK;
+  const int shift = page_size > 0 ? __builtin_ctz(static_cast<unsigned>(page_size)) : 0;
+  hipLaunchKernelGGL(attn_plan_install_kernel, dim3(windows + copy_blocks), dim3(64), 0,
+                     static_cast<hipStream_t>(stream), work_dev, windows, src_indices_dev, n_indices, dst_indices_dev,
+                     src_words_dev, n_words, dst_words_dev, shift, window_dev);
+  return launch_status("attn_plan_install_kernel");
+}
 
 extern "C" int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
                                        const int32_t* kv_indices_dev, int page_size, int32_t* window_dev,

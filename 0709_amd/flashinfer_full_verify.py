@@ -244,19 +244,22 @@ def _tree_spec(
     compact = node_count <= 64
     # wide trees: one visibility word per 64-key tile of the tree region
     tiles = _tile_words(bits, prefix_len, kv_len) if 64 < node_count <= _MAX_TILE_NODES else None
-    i64 = np.concatenate((
-        np.asarray(token_ids, dtype=np.int64), np.asarray(depths, dtype=np.int64),
-        np.asarray([_signed64(b) for b in bits] if compact else [], dtype=np.int64),
-        tiles.reshape(-1).view(np.int64) if tiles is not None else np.zeros(0, dtype=np.int64)))
-    i32 = np.concatenate((np.asarray([0, node_count, 0, total_pages, last], dtype=np.int32),
-                          np.arange(total_pages, dtype=np.int32)))
-    i32 = np.concatenate((i32, np.zeros(len(i32) % 2, dtype=np.int32)))  # keep the bool block 8-byte aligned
+    tok_dep = (np.asarray(token_ids, dtype=np.int64), np.asarray(depths, dtype=np.int64))
     if compact:
-        words = np.asarray([b & ((1 << 64) - 1) for b in bits], dtype=np.uint64)
-        block = ((words[:, None] >> np.arange(node_count, dtype=np.uint64)[None, :]) & 1).astype(np.bool_)
+        words = np.asarray(bits, dtype=np.uint64)  # below 2**64 for up to 64 nodes
+        i64 = np.concatenate((*tok_dep, words.view(np.int64)))
+        # row i, column j: bit j of word i
+        block = np.unpackbits(words.view(np.uint8).reshape(node_count, 8), axis=1,
+                              bitorder="little")[:, :node_count]
     else:
-        block = np.asarray([[(b >> j) & 1 for j in range(node_count)] for b in bits], dtype=np.bool_)
-    host = np.concatenate((i64.view(np.uint8), i32.view(np.uint8), block.reshape(-1).view(np.uint8)))
+        i64 = np.concatenate((*tok_dep, tiles.reshape(-1).view(np.int64) if tiles is not None
+                              else np.zeros(0, dtype=np.int64)))
+        block = np.asarray([[(b >> j) & 1 for j in range(node_count)] for b in bits], dtype=np.uint8)
+    # [qo_indptr 0 n | kv_indptr 0 pages | last | identity page table | pad to 8 bytes]
+    i32 = np.zeros(5 + total_pages + (1 + total_pages) % 2, dtype=np.int32)
+    i32[:5] = (0, node_count, 0, total_pages, last)
+    i32[5 : 5 + total_pages] = np.arange(total_pages, dtype=np.int32)
+    host = np.concatenate((i64.view(np.uint8), i32.view(np.uint8), block.reshape(-1)))
     # Normal tensors even under torch.inference_mode (the Target verify runs
     # in it): their version counters let a plan trust the attached host
     # values only while the tensors are unchanged.
@@ -265,6 +268,17 @@ def _tree_spec(
                                   last=last, prefix_len=prefix_len, compact=compact, device=device,
                                   parent_indices=parent_indices,
                                   tile_shape=None if tiles is None else tiles.shape)
+
+
+_TRUE: dict = {}
+
+
+def _true(device: torch.device) -> torch.Tensor:
+    """A [1, 1] bool True on ``device`` (kept per device) to expand."""
+    t = _TRUE.get(device)
+    if t is None:
+        t = _TRUE[device] = torch.ones((1, 1), dtype=torch.bool, device=device)
+    return t
 
 
 # Largest tree whose per-tile mask words the builder prepares on the host
@@ -296,23 +310,26 @@ def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last,
         buf = _lib.staging().upload(host, device)
     else:
         buf = torch.from_numpy(host).to(device)
-    o64 = 0
     n64 = len(i64)
-    flat_token_ids = buf[o64 * 8:(o64 + node_count) * 8].view(torch.int64)
-    depths_t = buf[(o64 + node_count) * 8:(o64 + 2 * node_count) * 8].view(torch.int64)
-    tree_mask = buf[2 * node_count * 8:n64 * 8].view(torch.int64) if compact else None
-    tile_words = buf[2 * node_count * 8:n64 * 8].view(torch.int64).view(tile_shape) if tile_shape else None
-    b32 = n64 * 8
-    qo_indptr = with_host_values(buf[b32:b32 + 8].view(torch.int32), [0, node_count])
-    kv_indptr = with_host_values(buf[b32 + 8:b32 + 16].view(torch.int32), [0, total_pages])
-    kv_last = with_host_values(buf[b32 + 16:b32 + 20].view(torch.int32), [last])
-    kv_indices = buf[b32 + 20:b32 + 20 + 4 * total_pages].view(torch.int32)
-    b_block = b32 + 4 * len(i32)
+    nb = 8 * node_count
+    (tok_b, dep_b, words_b, qo_b, kvp_b, last_b, idx_b, _, block_b) = buf.split(
+        [nb, nb, 8 * n64 - 2 * nb, 8, 8, 4, 4 * total_pages, 4 * len(i32) - 20 - 4 * total_pages,
+         node_count * node_count])
+    flat_token_ids = tok_b.view(torch.int64)
+    depths_t = dep_b.view(torch.int64)
+    tree_mask = words_b.view(torch.int64) if compact else None
+    tile_words = words_b.view(torch.int64).view(tile_shape) if tile_shape else None
+    qo_indptr = with_host_values(qo_b.view(torch.int32), [0, node_count])
+    kv_indptr = with_host_values(kvp_b.view(torch.int32), [0, total_pages])
+    kv_last = with_host_values(last_b.view(torch.int32), [last])
+    kv_indices = idx_b.view(torch.int32)
     # Dense mask [node, prefix + node]: prefix columns all visible, tree column
-    # j visible iff bit j of the row's ancestor bitmask.
-    mask = torch.ones((node_count, kv_len), dtype=torch.bool, device=device)
-    if node_count:
-        mask[:, prefix_len:] = buf[b_block:].view(torch.bool).view(node_count, node_count)
+    # j visible iff bit j of the row's ancestor bitmask (one launch).
+    block_t = block_b.view(torch.bool).view(node_count, node_count)
+    if prefix_len:
+        mask = torch.cat((_true(device).expand(node_count, prefix_len), block_t), dim=1)
+    else:
+        mask = block_t.clone()
     flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.

@@ -236,7 +236,7 @@ def _paged_layer_tables(layers: Sequence[torch.Tensor]):
     and the first layer's shape, strides and dtype, so a changed list never
     reuses a stale table."""
     l0 = layers[0]
-    key = (tuple(int(t.data_ptr()) for t in layers), tuple(l0.shape), l0.stride(), l0.dtype)
+    key = (tuple(map(torch.Tensor.data_ptr, layers)), tuple(l0.shape), l0.stride(), l0.dtype)
     hit = _LAYER_TABLES.get(key)
     if hit is None:
         for t in layers[1:]:

@@ -768,22 +768,22 @@ class DirectFlashInferMaskedTreeVerifyBackend:
             values = values.astype(np.float16).astype(np.float32)
         elif self.match_logits_dtype_rounding and verify_logits.dtype == torch.bfloat16:
             values = torch.from_numpy(values).to(torch.bfloat16).float().numpy()
-        first_vals = values[: len(paths)]
-        rest = values[len(paths):]
-        scores, k = [], 0
+        vals = values.tolist()
+        n_routes = len(paths)
+        scores, k = [], n_routes
         for i, (route, path) in enumerate(zip(routes, paths)):
-            lps = [float(first_vals[i])]
-            for _ in range(1, len(path)):
-                lps.append(float(rest[k]))
-                k += 1
+            d = len(path)
+            rest = max(d - 1, 0)
+            lps = [vals[i], *vals[k : k + rest]]
+            k += rest
             target = sum(lps)
-            weights = self._weights_for_depth(len(lps))
+            weights = self._weights_for_depth(d)
             sel = target if weights is None else sum(w * v for w, v in zip(weights, lps))
             scores.append(TargetRouteScore(
-                route_id=int(route.route_id), token_ids=tuple(int(t) for t in path), target_logprob=target,
+                route_id=int(route.route_id), token_ids=tuple(map(int, path)), target_logprob=target,
                 draft_logprob=float(route.draft_logprob), token_logprobs=tuple(lps), first_token_logprob=lps[0],
                 selection_score=sel, score_weights=() if weights is None else tuple(weights),
-                draft_token_logprobs=tuple(float(v) for v in route.draft_token_logprobs),
+                draft_token_logprobs=tuple(map(float, route.draft_token_logprobs)),
             ))
         return scores
 

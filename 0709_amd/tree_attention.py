@@ -556,29 +556,35 @@ class BatchPrefillWithPagedKVCacheWrapper:
         meta = self._persistent("_meta_buf", len(meta_np), torch.int32)
         if self._meta_uploaded is None or self._meta_uploaded[0] is not meta or \
                 not np.array_equal(self._meta_uploaded[1], meta_np):
-            meta[: len(meta_np)].copy_(torch.from_numpy(meta_np), non_blocking=non_blocking)
+            if device.type == "cuda":
+                _lib.staging().upload(meta_np, device, out=meta[: len(meta_np)])
+            else:
+                meta[: len(meta_np)].copy_(torch.from_numpy(meta_np))
             self._meta_uploaded = (meta, meta_np)
         work = dec["work"]
         n_idx = int(indices_src.numel())
         indices = self._persistent("_indices_buf", n_idx, torch.int32)
-        if n_idx:
-            indices[:n_idx].copy_(indices_src.to(device=device, dtype=torch.int32), non_blocking=non_blocking)
-        bits_buf = None
+        src_idx = indices_src
+        if src_idx.dtype != torch.int32 or src_idx.device != device or not src_idx.is_contiguous():
+            src_idx = src_idx.to(device=device, dtype=torch.int32).contiguous()
+        bits_buf = src_bits = None
+        nb = 0
         if tree_bits is not None:
             nb = int(tree_bits.numel())
             bits_buf = self._persistent("_bits_buf", nb, torch.int64)
-            if nb:
-                bits_buf[:nb].copy_(tree_bits, non_blocking=non_blocking)
-
-        # First page-id window of every work item, gathered on the device once
-        # per plan (the page table is fixed until the next plan), so the
-        # head_dim-128 kernel requests its first page ids with its work item.
+            src_bits = tree_bits.to(device=device, dtype=torch.int64).contiguous()
+        # The page table and mask words go into the plan's own buffers, and
+        # the first page-id window of every work item is gathered (the page
+        # table is fixed until the next plan, so the head_dim-128 kernel
+        # requests its first page ids with its work item): one launch.
         windows = None
         if dec["direct"] and work and self.use_page_windows:
             windows = self._persistent("_windows_buf", 64 * len(work), torch.int32)
-            rc = _lib.load().atlas_attn_page_windows(int(meta.data_ptr()), len(work), _lib.ptr(indices), ps,
-                                                     _lib.ptr(windows), _lib.stream_of(device))
-            _lib.check(rc, "atlas_attn_page_windows")
+        rc = _lib.load().atlas_attn_plan_install(
+            int(meta.data_ptr()), len(work) if windows is not None else 0, _lib.ptr(src_idx), n_idx,
+            _lib.ptr(indices), _lib.ptr(src_bits), nb, _lib.ptr(bits_buf), ps, _lib.ptr(windows),
+            _lib.stream_of(device))
+        _lib.check(rc, "atlas_attn_plan_install")
 
         self._plan = AttentionPlan(
             batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,

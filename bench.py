@@ -131,6 +131,8 @@ class HeadlineStep:
         self.free_count = torch.zeros(1, dtype=torch.int64, device=dev)
         all_pos = torch.arange(self.kv_len)
         self.all_slots = (idx[all_pos // page_size] * page_size + all_pos % page_size).to(dev)
+        self.live_path = (self.lib.SlotPath * 1)()
+        self.live_path[0].slots = self.all_slots.data_ptr()
         self.fwd_events = []
         self.commit_events = []
         self.prune_events = []
@@ -217,12 +219,13 @@ class HeadlineStep:
     def step(self):
         lib = self.lib
         stream = lib.stream_of(self.dev)
+        route_nodes = self.plan()
+        self._timed(self.fwd_events, self.graph_fwd.replay)
         # pages of the whole request (prefix + tree) are owned at verify time
+        # (marked behind the forward: only the prune reads them)
         rc = lib.load().atlas_mark_pages(lib.ptr(self.owned), self.pool_pages, lib.ptr(self.all_slots),
                                          self.kv_len, self.ps, stream)
         lib.check(rc, "atlas_mark_pages")
-        route_nodes = self.plan()
-        self._timed(self.fwd_events, self.graph_fwd.replay)
         # scoring + best route
         backend = object.__new__(self.tr.DirectFlashInferMaskedTreeVerifyBackend)
         backend.score_weights = None
@@ -238,14 +241,15 @@ class HeadlineStep:
         dst = list(range(self.prefix_len, self.prefix_len + len(nodes)))
         self._timed(self.commit_events, lambda: self.kv_ops.commit_paged(
             self.layers, src, dst, kv_indptr=self.kv_indptr, kv_indices=self.kv.kv_indices))
-        live = self.all_slots[: self.prefix_len + len(nodes)]
-        sampled = torch.cat((live[:: self.ps], live[-1:]))
+        # the live set: the committed path's page starts and its last slot,
+        # sampled inside the prune launch
+        self.live_path[0].len = self.prefix_len + len(nodes)
 
         def prune():
-            rc = lib.load().atlas_prune_pages(lib.ptr(self.owned), lib.ptr(self.live), self.pool_pages,
-                                              lib.ptr(sampled), int(sampled.numel()), self.ps,
-                                              lib.ptr(self.free_pages), lib.ptr(self.free_count), stream)
-            lib.check(rc, "atlas_prune_pages")
+            rc = lib.load().atlas_prune_pages_paths(lib.ptr(self.owned), lib.ptr(self.live), self.pool_pages,
+                                                    self.live_path, 1, 1, self.ps, lib.ptr(self.free_pages),
+                                                    lib.ptr(self.free_count), stream)
+            lib.check(rc, "atlas_prune_pages_paths")
 
         self._timed(self.prune_events, prune)
         # the pruned-page count stays on the device: nothing in the step waits

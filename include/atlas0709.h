@@ -159,6 +159,20 @@ typedef struct {
  * of two.  No counterpart in the reference: it is part of this library's
  * plan, as FlashInfer's plan keeps scheduling metadata of its own
  * (src/atlas_0709/flashinfer_full_verify.py:953-985 calls that plan). */
+/* A plan's whole device set-up in one launch: the page windows of
+ * atlas_attn_page_windows (window_dev NULL: none), read from src_indices_dev,
+ * plus copies of the page table (n_indices int32 from src_indices_dev to
+ * dst_indices_dev) and of the tree mask words (n_words int64 from
+ * src_words_dev to dst_words_dev) into the plan's own buffers, which the
+ * attention launches then read.  Sources and destinations must not overlap.
+ * No counterpart in the reference, as atlas_attn_page_windows: part of this
+ * library's plan (src/atlas_0709/flashinfer_full_verify.py:953-985 calls that
+ * plan). */
+int atlas_attn_plan_install(const atlas_attn_work_t* work_dev, int num_work, const int32_t* src_indices_dev,
+                            int64_t n_indices, int32_t* dst_indices_dev, const int64_t* src_words_dev,
+                            int64_t n_words, int64_t* dst_words_dev, int page_size, int32_t* window_dev,
+                            void* stream);
+
 int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
                             const int32_t* kv_indices_dev, int page_size, int32_t* window_dev,
                             void* stream);

@@ -307,7 +307,8 @@ def test_reference_plan_helper_and_kv_tuple(dev):
 @pytest.mark.parametrize("split_target", [None, 1, 64])
 def test_page_windows_match_page_table_path(dev, split_target):
     """Plan-time page-id windows: each item's window holds the ids of its first
-    64 pages (clamped to its last page), and attention with them is bit-equal
+    64 pages (clamped to its last page), the plan's page table and mask words
+    equal the caller's, and attention with the windows is bit-equal
     to attention reading the page table after the work item.  Split target 1
     gives one split of ~330 pages per KV head, so the kernel still loads later
     windows from the page table."""
@@ -338,9 +339,14 @@ def test_page_windows_match_page_table_path(dev, split_target):
     (plan, out_a, lse_a), (plan_b, out_b, lse_b) = results
     assert plan.page_windows is not None and plan_b.page_windows is None
     assert torch.equal(out_a, out_b) and torch.equal(lse_a, lse_b)
+    order = c["order"].tolist()
+    words = c["spec"].tree_mask.cpu().tolist()
+    for p in (plan, plan_b):
+        # the one-launch plan install copied the page table and the mask words
+        assert p.kv_indices[: len(order)].cpu().tolist() == order
+        assert p.tree_mask[: len(words)].cpu().tolist() == words
     win = plan.page_windows.cpu().view(-1, 64)
     meta = plan.meta.cpu()
-    order = c["order"].tolist()
     ps = c["ps"]
     for i in range(plan.num_work):
         item = meta[16 * i : 16 * i + 16].tolist()
