@@ -87,29 +87,33 @@ _SIGNATURES: dict[str, list] = {
     "atlas_abi_version": [],
     "atlas_kv_move_slots": [_VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp],
     "atlas_kv_append": [
-        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _VPP, _VPP, _c_i64, _vp, _c_i64, _c_i64, _vp,
+        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _VPP, _VPP, _c_i64, _vp, _c_i64,
+        _c_i64, _vp,
     ],
     "atlas_kv_commit_paged": [
-        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_i64,
+        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, _vp, _c_i64,
         ctypes.c_int, _vp, ctypes.c_size_t, _vp,
     ],
     "atlas_kv_commit_paged_host": [
-        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp,
+        _VPP, _VPP, ctypes.c_int, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp,
         ctypes.POINTER(_c_i32), ctypes.POINTER(_c_i64), ctypes.POINTER(_c_i64), _c_i64, _vp,
     ],
     "atlas_tree_verify_attn": [
-        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int,
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
+        ctypes.c_int,
         _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _c_i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_size_t, _vp,
     ],
     "atlas_tree_verify_attn_append": [
-        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int,
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
+        ctypes.c_int,
         _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _c_i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _vp, ctypes.c_size_t,
         _vp, _vp, _c_i64, _c_i64, _vp, _vp, _c_i64, _vp,
     ],
     "atlas_tree_verify_attn_noalloc": [
-        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp, ctypes.c_int,
+        _vp, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _c_i64, _c_i64, _vp, _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
+        ctypes.c_int,
         _vp, ctypes.c_int, _vp, _vp, ctypes.c_int, _c_i64, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
         ctypes.c_int, ctypes.c_float, ctypes.c_int, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp,
     ],

@@ -53,7 +53,8 @@ struct SlotGeom {
   int32_t page_shift;  // log2(page_size) when a power of two, else -1
   int32_t row_vecs;    // 16-byte vectors per token row
   int32_t row_shift;   // log2(row_vecs) when a power of two, else -1
-  int32_t pad;
+  int32_t head_shift;  // rows split by KV head (HND pages): log2(16-byte vectors per head), else -1
+  int64_t head_stride; // bytes between a token's KV heads when head_shift >= 0
 };
 
 __device__ __forceinline__ int64_t slot_offset(int64_t slot, const SlotGeom& g) {
@@ -66,6 +67,14 @@ __device__ __forceinline__ int64_t slot_offset(int64_t slot, const SlotGeom& g) 
     off = slot - page * g.page_size;
   }
   return page * g.page_stride + off * g.token_stride;
+}
+
+// Byte offset of 16-byte vector `vec` of a token row from the row's first
+// byte: contiguous rows (NHD pages, flat pools), or one run of vectors per KV
+// head, head_stride apart (HND pages).
+__device__ __forceinline__ int64_t vec_offset(int vec, const SlotGeom& g) {
+  if (g.head_shift < 0) return int64_t(vec) * 16;
+  return int64_t(vec >> g.head_shift) * g.head_stride + int64_t(vec & ((1 << g.head_shift) - 1)) * 16;
 }
 
 __device__ __forceinline__ void split_row(int64_t idx, const SlotGeom& g, int64_t& item, int& vec) {

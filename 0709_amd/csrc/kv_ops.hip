@@ -40,8 +40,8 @@ __global__ __launch_bounds__(kThreads) void kv_move_kernel(LayerTable lt, SlotGe
       int64_t item;
       int vec;
       split_row(idx, g, item, vec);
-      const int64_t so = slot_offset(src[item], g) + int64_t(vec) * 16;
-      dofs[u] = slot_offset(dst[item], g) + int64_t(vec) * 16;
+      const int64_t so = slot_offset(src[item], g) + vec_offset(vec, g);
+      dofs[u] = slot_offset(dst[item], g) + vec_offset(vec, g);
       buf[u] = *reinterpret_cast<const uint4*>(base + so);
     }
   }
@@ -125,7 +125,7 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(LayerTable lt, SrcT
       int vec;
       split_row(idx, g, item, vec);
       const int64_t slot = dst ? dst[item] : dst_start + item;
-      dofs[u] = slot_offset(slot, g) + int64_t(vec) * 16;
+      dofs[u] = slot_offset(slot, g) + vec_offset(vec, g);
       buf[u] = *reinterpret_cast<const uint4*>(sbase + item * src_token_stride + int64_t(vec) * 16);
     }
   }
@@ -208,31 +208,36 @@ __global__ __launch_bounds__(kThreads) void kv_commit_rows_kernel(
     dst_k = (MODE == kGather) ? wk : kb + dst_off;
     dst_v = (MODE == kGather) ? wv : vb + dst_off;
   }
+  // paged rows may be split by KV head; workspace rows are contiguous
+  auto src_off_of = [&](int v) { return MODE == kScatter ? int64_t(v) * 16 : vec_offset(v, g); };
+  auto dst_off_of = [&](int v) { return MODE == kGather ? int64_t(v) * 16 : vec_offset(v, g); };
   if constexpr (CPR > 0) {
     u32x4v a[CPR], b[CPR];
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
-      a[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_k + int64_t(c * 64 + lane) * 16));
-      b[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_v + int64_t(c * 64 + lane) * 16));
+      const int64_t so = src_off_of(c * 64 + lane);
+      a[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_k + so));
+      b[c] = __builtin_nontemporal_load(reinterpret_cast<const u32x4v*>(src_v + so));
     }
 #pragma unroll
     for (int c = 0; c < CPR; ++c) {
-      __builtin_nontemporal_store(a[c], reinterpret_cast<u32x4v*>(dst_k + int64_t(c * 64 + lane) * 16));
-      __builtin_nontemporal_store(b[c], reinterpret_cast<u32x4v*>(dst_v + int64_t(c * 64 + lane) * 16));
+      const int64_t d = dst_off_of(c * 64 + lane);
+      __builtin_nontemporal_store(a[c], reinterpret_cast<u32x4v*>(dst_k + d));
+      __builtin_nontemporal_store(b[c], reinterpret_cast<u32x4v*>(dst_v + d));
     }
   } else {
 #pragma unroll 2
     for (int v = lane; v < g.row_vecs; v += 64) {
-      const uint4 a = *reinterpret_cast<const uint4*>(src_k + int64_t(v) * 16);
-      const uint4 b = *reinterpret_cast<const uint4*>(src_v + int64_t(v) * 16);
-      *reinterpret_cast<uint4*>(dst_k + int64_t(v) * 16) = a;
-      *reinterpret_cast<uint4*>(dst_v + int64_t(v) * 16) = b;
+      const uint4 a = *reinterpret_cast<const uint4*>(src_k + src_off_of(v));
+      const uint4 b = *reinterpret_cast<const uint4*>(src_v + src_off_of(v));
+      *reinterpret_cast<uint4*>(dst_k + dst_off_of(v)) = a;
+      *reinterpret_cast<uint4*>(dst_v + dst_off_of(v)) = b;
     }
   }
 }
 
 int make_geom(int64_t page_size, int64_t page_stride, int64_t token_stride, int64_t row_bytes,
-              SlotGeom& g) {
+              SlotGeom& g, int64_t head_bytes = 0, int64_t head_stride = 0) {
   ATLAS_REQUIRE(page_size > 0, "page_size must be positive");
   ATLAS_REQUIRE(row_bytes > 0 && row_bytes % 16 == 0, "row_bytes must be a positive multiple of 16");
   ATLAS_REQUIRE(page_stride % 16 == 0 && token_stride % 16 == 0,
@@ -244,7 +249,18 @@ int make_geom(int64_t page_size, int64_t page_stride, int64_t token_stride, int6
   g.page_shift = ilog2_exact(page_size);
   g.row_vecs = static_cast<int32_t>(row_bytes / 16);
   g.row_shift = ilog2_exact(g.row_vecs);
-  g.pad = 0;
+  g.head_shift = -1;
+  g.head_stride = 0;
+  if (head_stride != 0 && head_stride != head_bytes) {
+    // rows split by KV head: head_bytes contiguous per head, head_stride apart
+    ATLAS_REQUIRE(head_bytes > 0 && head_bytes % 16 == 0 && row_bytes % head_bytes == 0,
+                  "head_bytes must be a positive multiple of 16 dividing row_bytes");
+    ATLAS_REQUIRE(ilog2_exact(head_bytes / 16) >= 0, "head_bytes / 16 must be a power of two");
+    ATLAS_REQUIRE(head_stride % 16 == 0 && head_stride >= head_bytes,
+                  "head_stride must be a multiple of 16 bytes covering a head's row");
+    g.head_shift = ilog2_exact(head_bytes / 16);
+    g.head_stride = head_stride;
+  }
   return ATLAS_OK;
 }
 
@@ -316,7 +332,8 @@ extern "C" int atlas_kv_move_slots(const void* const* k_layers, const void* cons
 
 extern "C" int atlas_kv_append(const void* const* k_layers, const void* const* v_layers,
                                int num_layers, int64_t page_size, int64_t page_stride,
-                               int64_t token_stride, int64_t row_bytes, const void* const* k_src,
+                               int64_t token_stride, int64_t row_bytes, int64_t head_bytes,
+                               int64_t head_stride, const void* const* k_src,
                                const void* const* v_src, int64_t src_token_stride,
                                const int64_t* dst_slots_dev, int64_t dst_start, int64_t n,
                                void* stream) {
@@ -329,7 +346,7 @@ extern "C" int atlas_kv_append(const void* const* k_layers, const void* const* v
                 "source token stride must be a multiple of 16 bytes and cover a row");
   ATLAS_REQUIRE(dst_slots_dev != nullptr || dst_start >= 0, "dst_start must be non-negative");
   SlotGeom g;
-  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g))) return rc;
+  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g, head_bytes, head_stride))) return rc;
   for (int l0 = 0; l0 < num_layers; l0 += ATLAS_MAX_LAYERS_PER_LAUNCH) {
     const int nl = std::min(ATLAS_MAX_LAYERS_PER_LAUNCH, num_layers - l0);
     LayerTable lt;
@@ -412,7 +429,8 @@ int commit_impl(const void* const* k_layers, const void* const* v_layers, int nu
 
 extern "C" int atlas_kv_commit_paged(const void* const* k_layers, const void* const* v_layers,
                                      int num_layers, int64_t page_size, int64_t page_stride,
-                                     int64_t token_stride, int64_t row_bytes,
+                                     int64_t token_stride, int64_t row_bytes, int64_t head_bytes,
+                                     int64_t head_stride,
                                      const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                      const int32_t* item_req_dev, const int64_t* src_pos_dev,
                                      const int64_t* dst_pos_dev, int64_t n, int needs_staging,
@@ -423,7 +441,7 @@ extern "C" int atlas_kv_commit_paged(const void* const* k_layers, const void* co
   int rc = check_layers(k_layers, v_layers, num_layers);
   if (rc) return rc;
   SlotGeom g;
-  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g))) return rc;
+  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g, head_bytes, head_stride))) return rc;
   if (needs_staging) {
     const size_t need = size_t(n) * 2 * size_t(num_layers) * size_t(row_bytes);
     ATLAS_REQUIRE(workspace_dev != nullptr && workspace_bytes >= need,
@@ -437,7 +455,8 @@ extern "C" int atlas_kv_commit_paged(const void* const* k_layers, const void* co
 
 extern "C" int atlas_kv_commit_paged_host(const void* const* k_layers, const void* const* v_layers,
                                           int num_layers, int64_t page_size, int64_t page_stride,
-                                          int64_t token_stride, int64_t row_bytes,
+                                          int64_t token_stride, int64_t row_bytes, int64_t head_bytes,
+                                          int64_t head_stride,
                                           const int32_t* kv_indptr_dev,
                                           const int32_t* kv_indices_dev,
                                           const int32_t* item_req_host, const int64_t* src_pos_host,
@@ -449,7 +468,7 @@ extern "C" int atlas_kv_commit_paged_host(const void* const* k_layers, const voi
   int rc = check_layers(k_layers, v_layers, num_layers);
   if (rc) return rc;
   SlotGeom g;
-  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g))) return rc;
+  if ((rc = make_geom(page_size, page_stride, token_stride, row_bytes, g, head_bytes, head_stride))) return rc;
   InlineItems items{};
   for (int64_t i = 0; i < n; ++i) {
     ATLAS_REQUIRE(src_pos_host[i] >= 0 && dst_pos_host[i] >= 0, "positions must be non-negative");

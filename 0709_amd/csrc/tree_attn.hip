@@ -51,6 +51,7 @@ struct AttnArgs {
   int64_t page_stride;  // bytes
   int64_t v_offset;     // bytes
   int64_t token_stride; // bytes
+  int64_t head_stride;  // bytes between a token's KV heads (head_dim * 2 for NHD pages, page_size * that for HND)
   const int32_t* qo_indptr;
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
@@ -355,7 +356,7 @@ __global__ __launch_bounds__(kThreads, (RT <= 2 ? 2 : 1)) void tree_attn_kernel(
   const int pt_base = w.page_offset;
   const int kv_end = min(w.kv_end, kv_len);
   const int G = a.group;
-  const int64_t head_off = int64_t(kvh) * D * 2;
+  const int64_t head_off = int64_t(kvh) * a.head_stride;
 
   // Keys < vis_all are visible to every row.
   int vis_all = kv_end;
@@ -1632,7 +1633,7 @@ __device__ __forceinline__ void d128_append_rows(const AttnArgs& a, const atlas_
                       (int64_t(c.qo_start + node) * a.app_stride_token + int64_t(w.kv_head) * a.app_stride_head) * 2;
     const int32_t pid = a.kv_indices[int64_t(w.page_offset) + (p >> a.page_shift)];
     char* dst = const_cast<char*>(a.kv) + int64_t(pid) * a.page_stride + int64_t(p & (a.page_size - 1)) * a.token_stride +
-                (is_v ? a.v_offset : 0) + int64_t(w.kv_head) * 256;
+                (is_v ? a.v_offset : 0) + int64_t(w.kv_head) * a.head_stride;
     u32x4v v = *reinterpret_cast<const u32x4v*>(src + g * 16);
     if (a.rope_cos != nullptr && !is_v) {
       const int64_t off = int64_t(c.qo_start + node) * a.rope_stride_token * 2 + g * 16;
@@ -1679,7 +1680,7 @@ __global__ __launch_bounds__(512, 1) void tree_attn_d128_kernel(AttnArgs a) {
   c.nt_plain = __builtin_amdgcn_readfirstlane(
       min(c.nt, vis_all >= c.t_first + kTileKeys ? (vis_all - c.t_first) / kTileKeys : 0));
   const int last_key = __builtin_amdgcn_readfirstlane(c.kv_end - 1);
-  const char* head_base = a.kv + int64_t(w.kv_head) * D * 2;
+  const char* head_base = a.kv + int64_t(w.kv_head) * a.head_stride;
   const int32_t* pages = a.kv_indices + w.page_offset;
   const uint32_t lds0 = lds_offset(lds);
   if (a.app_k != nullptr && max(c.t_first, c.kv_len - c.qo_len) < c.kv_end) {
@@ -1886,7 +1887,8 @@ int current_device_scratch(void** out);
 // its address is looked up only after every argument has been checked.
 static int verify_attn_impl(bool use_scratch,
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
-    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, int64_t kv_head_stride,
+    const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
@@ -1925,6 +1927,8 @@ static int verify_attn_impl(bool use_scratch,
   // token rows plus 256 bytes, in 32 bits)
   ATLAS_REQUIRE(token_stride > 0 && token_stride <= (int64_t(1) << 25), "token_stride %lld out of range",
                 (long long)token_stride);
+  ATLAS_REQUIRE(kv_head_stride >= int64_t(head_dim) * 2 && kv_head_stride % 16 == 0,
+                "kv_head_stride %lld must be a multiple of 16 bytes covering a head's row", (long long)kv_head_stride);
   if (num_work == 0) return ATLAS_OK;
   ATLAS_REQUIRE(work_dev != nullptr, "work list must not be NULL");
   const int row_tiles = (max_rows_per_item + 15) / 16;
@@ -1937,6 +1941,7 @@ static int verify_attn_impl(bool use_scratch,
   args.page_stride = page_stride;
   args.v_offset = kv_v_offset;
   args.token_stride = token_stride;
+  args.head_stride = kv_head_stride;
   args.qo_indptr = qo_indptr_dev;
   args.kv_indptr = kv_indptr_dev;
   args.kv_indices = kv_indices_dev;
@@ -2007,7 +2012,8 @@ static int verify_attn_impl(bool use_scratch,
 
 extern "C" int atlas_tree_verify_attn(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
-    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, int64_t kv_head_stride,
+    const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
@@ -2017,6 +2023,7 @@ extern "C" int atlas_tree_verify_attn(
     int64_t out_stride_head, float* lse, void* workspace_dev, size_t workspace_bytes,
     void* stream) {
   return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          kv_head_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
@@ -2026,7 +2033,8 @@ extern "C" int atlas_tree_verify_attn(
 
 extern "C" int atlas_tree_verify_attn_append(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
-    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, int64_t kv_head_stride,
+    const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
@@ -2050,6 +2058,7 @@ extern "C" int atlas_tree_verify_attn_append(
   ATLAS_REQUIRE(append_stride_token % 8 == 0 && append_stride_head % 8 == 0,
                 "append strides must be multiples of 8 elements");
   return verify_attn_impl(false, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          kv_head_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,
@@ -2096,7 +2105,8 @@ int current_device_scratch(void** out) {
 
 extern "C" int atlas_tree_verify_attn_noalloc(
     const void* q, int64_t q_stride_token, int64_t q_stride_head, const void* kv_cache,
-    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, const int32_t* qo_indptr_dev,
+    int64_t page_stride, int64_t kv_v_offset, int64_t token_stride, int64_t kv_head_stride,
+    const int32_t* qo_indptr_dev,
     const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev, const int32_t* kv_len_dev,
     int mask_mode, const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev, int tree_mask_words,
     const atlas_attn_work_t* work_dev, int num_work, const int32_t* page_window_dev,
@@ -2121,6 +2131,7 @@ extern "C" int atlas_tree_verify_attn_noalloc(
                 "the merge items reference %lld partial rows but partial_rows is %lld",
                 (long long)merge_partial_rows, (long long)partial_rows);
   return verify_attn_impl(true, q, q_stride_token, q_stride_head, kv_cache, page_stride, kv_v_offset, token_stride,
+                          kv_head_stride,
                           qo_indptr_dev, kv_indptr_dev, kv_indices_dev, kv_len_dev, mask_mode, tree_mask_dev,
                           mask_col_start_dev, tree_mask_words, work_dev, num_work, page_window_dev, merge_dev, num_merge,
                           merge_partial_rows, max_rows_per_item, num_qo_heads, num_kv_heads, head_dim, page_size, sm_scale, dtype, out,

@@ -71,7 +71,7 @@ def _unit_scale(value, name: str) -> None:
 
 class BatchDecodeWithPagedKVCacheWrapper:
     """FlashInfer ``BatchDecodeWithPagedKVCacheWrapper`` over the gfx950 paged
-    attention kernels (NHD layout, head_dim 64 or 128, fp16 / bf16)."""
+    attention kernels (NHD or HND pages, head_dim 64 or 128, fp16 / bf16)."""
 
     def __init__(
         self,
@@ -96,6 +96,11 @@ class BatchDecodeWithPagedKVCacheWrapper:
     @property
     def is_cuda_graph_enabled(self) -> bool:
         return self._use_cuda_graph
+
+    @property
+    def kv_layout(self) -> str:
+        """The paged layout run() reads: "NHD" or "HND"."""
+        return self._prefill.kv_layout
 
     @property
     def current_plan(self):
@@ -341,10 +346,12 @@ class BatchDecodeWithPagedKVCacheWrapper:
         """FlashInfer keeps this as a no-op."""
 
 
-def make_decode_wrapper(*, args, flashinfer=None) -> BatchDecodeWithPagedKVCacheWrapper:
-    """Workspace-backed decode wrapper (``flashinfer_full_verify.py:882-888``)."""
+def make_decode_wrapper(*, args, flashinfer=None, kv_layout: str | None = None) -> BatchDecodeWithPagedKVCacheWrapper:
+    """Workspace-backed decode wrapper (``flashinfer_full_verify.py:882-888``)
+    for ``kv_layout`` pages (default: ``args.kv_layout`` when set, else NHD)."""
     workspace = torch.empty(int(args.workspace_mb) * 1024 * 1024, dtype=torch.uint8, device=args.device)
-    return BatchDecodeWithPagedKVCacheWrapper(workspace, "NHD", backend=getattr(args, "flashinfer_backend", "auto"))
+    layout = kv_layout or getattr(args, "kv_layout", None) or "NHD"
+    return BatchDecodeWithPagedKVCacheWrapper(workspace, layout, backend=getattr(args, "flashinfer_backend", "auto"))
 
 
 def plan_decode_wrapper(wrapper, *, seq_len: int, args, config, dtype: torch.dtype) -> None:

@@ -390,10 +390,13 @@ def prefix_layer_to_paged_kv(
     node_count: int,
     page_size: int,
     total_pages: int | None = None,
+    kv_layout: str = "NHD",
 ) -> torch.Tensor:
     """HF ``[1, Hkv, T, D]`` prefix K/V -> zero-initialised paged layer
     ``[pages, 2, page_size, Hkv, D]`` with token t at page t // page_size,
-    offset t % page_size (``flashinfer_full_verify.py:814-849``)."""
+    offset t % page_size (``flashinfer_full_verify.py:814-849``);
+    ``kv_layout="HND"`` lays the pages out ``[pages, 2, Hkv, page_size, D]``."""
+    kv_ops.check_kv_layout(kv_layout)
     if key.shape[0] != 1 or value.shape[0] != 1:
         raise ValueError("full masked verify expects batch-1 prefix KV")
     if key.ndim != 4 or value.ndim != 4:
@@ -403,13 +406,12 @@ def prefix_layer_to_paged_kv(
         raise ValueError(f"prefix cache length mismatch: expected {prefix_len}, got {key_len}")
     if total_pages is None:
         total_pages = ceil_div(int(prefix_len) + int(node_count), int(page_size))
-    kv_cache = torch.zeros(
-        int(total_pages), 2, int(page_size), int(kv_heads), int(head_dim), dtype=key.dtype, device=key.device
-    )
+    page = (int(page_size), int(kv_heads)) if kv_layout == "NHD" else (int(kv_heads), int(page_size))
+    kv_cache = torch.zeros(int(total_pages), 2, *page, int(head_dim), dtype=key.dtype, device=key.device)
     if int(prefix_len) > 0:
         key_tokens = key[0].permute(1, 0, 2).contiguous()
         value_tokens = value[0].permute(1, 0, 2).contiguous()
-        kv_ops.append_paged([kv_cache], [key_tokens], [value_tokens], start_pos=0)
+        kv_ops.append_paged([kv_cache], [key_tokens], [value_tokens], start_pos=0, kv_layout=kv_layout)
     return kv_cache
 
 
@@ -421,11 +423,13 @@ def write_suffix_kv(
     prefix_len: int,
     page_size: int,
     start_pos: int | None = None,
+    kv_layout: str = "NHD",
 ) -> None:
     """Write node K/V ``[n, Hkv, D]`` at positions ``start + i`` of one paged
-    layer (``flashinfer_full_verify.py:1027-1042``)."""
-    if int(kv_cache.shape[2]) != int(page_size):
-        raise ValueError(f"page_size {page_size} does not match the cache's {int(kv_cache.shape[2])}")
+    layer (``flashinfer_full_verify.py:1027-1042``) of ``kv_layout`` pages."""
+    cache_ps = int(kv_cache.shape[2 if kv_ops.check_kv_layout(kv_layout) == "NHD" else 3])
+    if cache_ps != int(page_size):
+        raise ValueError(f"page_size {page_size} does not match the cache's {cache_ps}")
     start = int(prefix_len) if start_pos is None else int(start_pos)
     node_count = int(key_states.shape[0])
     if start < 0 or start + node_count > int(kv_cache.shape[0]) * int(page_size):
@@ -433,7 +437,7 @@ def write_suffix_kv(
             f"positions [{start}, {start + node_count}) exceed the cache's "
             f"{int(kv_cache.shape[0]) * int(page_size)} slots"
         )
-    kv_ops.append_paged([kv_cache], [key_states], [value_states], start_pos=start)
+    kv_ops.append_paged([kv_cache], [key_states], [value_states], start_pos=start, kv_layout=kv_layout)
 
 
 def first_tensor(value) -> torch.Tensor:
@@ -449,10 +453,13 @@ def first_tensor(value) -> torch.Tensor:
 from .decode_attention import make_decode_wrapper, plan_decode_wrapper  # noqa: E402  (decode wrapper helpers)
 
 
-def make_prefill_wrapper(*, args, flashinfer=None) -> BatchPrefillWithPagedKVCacheWrapper:
-    """Workspace-backed wrapper (``flashinfer_full_verify.py:877-879``)."""
+def make_prefill_wrapper(*, args, flashinfer=None, kv_layout: str | None = None) -> BatchPrefillWithPagedKVCacheWrapper:
+    """Workspace-backed wrapper (``flashinfer_full_verify.py:877-879``) for
+    ``kv_layout`` pages (default: ``args.kv_layout`` when set, else NHD, the
+    reference's)."""
     workspace = torch.empty(int(args.workspace_mb) * 1024 * 1024, dtype=torch.uint8, device=args.device)
-    return BatchPrefillWithPagedKVCacheWrapper(workspace, "NHD", backend=getattr(args, "flashinfer_backend", "auto"))
+    layout = kv_layout or getattr(args, "kv_layout", None) or "NHD"
+    return BatchPrefillWithPagedKVCacheWrapper(workspace, layout, backend=getattr(args, "flashinfer_backend", "auto"))
 
 
 def plan_prefill_wrapper(wrapper, tree: TreeSpec, *, args, config, dtype: torch.dtype) -> None:

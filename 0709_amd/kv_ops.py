@@ -1,11 +1,14 @@
 """All-layer KV movement on the HIP kernels: append, slot-to-slot move and
 page-table commit compaction.
 
-Two physical layouts are addressed through one slot formula (see
+Three physical layouts are addressed through one slot formula (see
 include/atlas0709.h):
 
-* FlashInfer NHD paged layers ``[pages, 2, page_size, Hkv, D]`` (the Target's
-  per-layer caches, ``flashinfer_full_verify.py:833-841`` of the reference);
+* FlashInfer NHD paged layers ``[pages, 2, page_size, Hkv, D]`` (the
+  reference's per-layer caches, ``flashinfer_full_verify.py:833-841``);
+* FlashInfer HND paged layers ``[pages, 2, Hkv, page_size, D]`` (a token's row
+  split by KV head, ``page_size * D`` elements apart: each head's keys of a
+  page are one contiguous run);
 * SGLang-style flat token pools ``[slots, Hkv, D]`` with separate K and V
   tensors per layer (the Drafter pool, addressed with ``page_size = 1``).
 """
@@ -22,30 +25,58 @@ from . import _lib
 
 @dataclass(frozen=True)
 class SlotGeometry:
-    """Byte geometry of one layer's K (or V) region."""
+    """Byte geometry of one layer's K (or V) region.  ``head_stride`` is the
+    distance between a token's KV heads, 0 when its row is contiguous."""
 
     page_size: int
     page_stride: int
     token_stride: int
     row_bytes: int
+    head_bytes: int = 0
+    head_stride: int = 0
 
     def as_args(self) -> tuple[int, int, int, int]:
+        """(page_size, page_stride, token_stride, row_bytes): contiguous rows."""
+        if self.head_stride and self.head_stride != self.head_bytes:
+            raise ValueError("this call takes contiguous token rows only")
         return self.page_size, self.page_stride, self.token_stride, self.row_bytes
 
+    def as_head_args(self) -> tuple[int, int, int, int, int, int]:
+        """as_args() followed by (head_bytes, head_stride)."""
+        return (self.page_size, self.page_stride, self.token_stride, self.row_bytes, self.head_bytes,
+                self.head_stride)
 
-def paged_layer_geometry(layer_kv: torch.Tensor) -> tuple[SlotGeometry, int]:
-    """Geometry of a FlashInfer NHD layer ``[pages, 2, page_size, Hkv, D]``.
+
+KV_LAYOUTS = ("NHD", "HND")
+
+
+def check_kv_layout(kv_layout: str) -> str:
+    if kv_layout not in KV_LAYOUTS:
+        raise ValueError(f"kv_layout must be one of {KV_LAYOUTS}, got {kv_layout!r}")
+    return kv_layout
+
+
+def paged_layer_geometry(layer_kv: torch.Tensor, kv_layout: str = "NHD") -> tuple[SlotGeometry, int]:
+    """Geometry of a FlashInfer paged layer, NHD ``[pages, 2, page_size, Hkv,
+    D]`` or HND ``[pages, 2, Hkv, page_size, D]``.
 
     Returns the slot geometry and the byte offset of the V half.
     """
+    check_kv_layout(kv_layout)
     if layer_kv.ndim != 5 or int(layer_kv.shape[1]) != 2:
-        raise ValueError(f"expected a paged layer [pages, 2, page_size, Hkv, D], got {tuple(layer_kv.shape)}")
-    _, _, page_size, heads, dim = (int(x) for x in layer_kv.shape)
+        raise ValueError(f"expected a paged layer [pages, 2, ...] of {kv_layout} pages, got {tuple(layer_kv.shape)}")
     es = layer_kv.element_size()
     s = layer_kv.stride()
-    if not rows_contiguous(layer_kv):
-        raise ValueError("paged layer rows (Hkv, D) must be contiguous")
-    geom = SlotGeometry(page_size, s[0] * es, s[2] * es, heads * dim * es)
+    if kv_layout == "NHD":
+        _, _, page_size, heads, dim = (int(x) for x in layer_kv.shape)
+        if not rows_contiguous(layer_kv):
+            raise ValueError("paged layer rows (Hkv, D) must be contiguous")
+        geom = SlotGeometry(page_size, s[0] * es, s[2] * es, heads * dim * es, dim * es, s[3] * es)
+    else:
+        _, _, heads, page_size, dim = (int(x) for x in layer_kv.shape)
+        if s[4] != 1 and dim != 1:
+            raise ValueError("paged layer head rows (D) must be contiguous")
+        geom = SlotGeometry(page_size, s[0] * es, s[3] * es, heads * dim * es, dim * es, s[2] * es)
     return geom, s[1] * es
 
 
@@ -161,7 +192,7 @@ def append_token_pool(
     dst = _as_long(dst_slots.reshape(-1), device)
     lib = _lib.load()
     rc = lib.atlas_kv_append(
-        k_tab, v_tab, len(k_layers), *geom.as_args(),
+        k_tab, v_tab, len(k_layers), *geom.as_head_args(),
         _lib.ptr_array([int(t.data_ptr()) for t in k_src]),
         _lib.ptr_array([int(t.data_ptr()) for t in v_src]),
         src_stride, _lib.ptr(dst), 0, n, _lib.stream_of(device),
@@ -176,13 +207,15 @@ def append_paged(
     *,
     start_pos: int | None = None,
     dst_slots: torch.Tensor | None = None,
+    kv_layout: str = "NHD",
 ) -> None:
-    """Write dense rows ``[n, Hkv, D]`` into paged layers at contiguous
-    positions ``start_pos + i`` (identity page table) or at physical slots."""
+    """Write dense rows ``[n, Hkv, D]`` into paged layers (``kv_layout``
+    pages) at contiguous positions ``start_pos + i`` (identity page table) or
+    at physical slots."""
     if not layers or len(k_src) != len(layers) or len(v_src) != len(layers):
         raise ValueError("one K and one V source per layer are required")
     device = _lib.require_device(layers[0], k_src[0], v_src[0], dst_slots, what="write_suffix_kv")
-    geom, v_off = paged_layer_geometry(layers[0])
+    geom, v_off = paged_layer_geometry(layers[0], kv_layout)
     n = int(k_src[0].shape[0])
     for t in (*k_src, *v_src):
         if t.dtype != layers[0].dtype:
@@ -202,7 +235,7 @@ def append_paged(
         raise ValueError("start_pos must be a non-negative position")
     lib = _lib.load()
     rc = lib.atlas_kv_append(
-        _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs), len(layers), *geom.as_args(),
+        _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs), len(layers), *geom.as_head_args(),
         _lib.ptr_array([int(t.data_ptr()) for t in k_src]),
         _lib.ptr_array([int(t.data_ptr()) for t in v_src]),
         src_stride, _lib.ptr(dst), 0 if start_pos is None else int(start_pos), n, _lib.stream_of(device),
@@ -229,20 +262,20 @@ def commit_positions_need_staging(
 _LAYER_TABLES: dict = {}
 
 
-def _paged_layer_tables(layers: Sequence[torch.Tensor]):
+def _paged_layer_tables(layers: Sequence[torch.Tensor], kv_layout: str = "NHD"):
     """(slot geometry, K pointer table, V pointer table) of a list of paged
     layers, kept for the most recent few layer sets: a Target commits into
     the same layer tensors every verify.  The key holds every layer's address
     and the first layer's shape, strides and dtype, so a changed list never
     reuses a stale table."""
     l0 = layers[0]
-    key = (tuple(map(torch.Tensor.data_ptr, layers)), tuple(l0.shape), l0.stride(), l0.dtype)
+    key = (tuple(map(torch.Tensor.data_ptr, layers)), tuple(l0.shape), l0.stride(), l0.dtype, kv_layout)
     hit = _LAYER_TABLES.get(key)
     if hit is None:
         for t in layers[1:]:
             if t.shape != l0.shape or t.stride() != l0.stride() or t.dtype != l0.dtype:
                 raise ValueError("every layer must have the first layer's shape, strides and dtype")
-        geom, v_off = paged_layer_geometry(l0)
+        geom, v_off = paged_layer_geometry(l0, kv_layout)
         k_ptrs, v_ptrs = _layer_ptrs(layers, v_off)
         hit = (geom, _lib.ptr_array(k_ptrs), _lib.ptr_array(v_ptrs))
         if len(_LAYER_TABLES) >= 8:
@@ -269,8 +302,10 @@ def commit_paged(
     item_req: Sequence[int] | torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     needs_staging: bool | None = None,
+    kv_layout: str = "NHD",
 ) -> None:
-    """Route-commit compaction over paged layers, every layer in one launch.
+    """Route-commit compaction over paged layers (``kv_layout`` pages), every
+    layer in one launch.
 
     Row at logical position ``src_pos[i]`` of request ``item_req[i]`` is copied
     to ``dst_pos[i]`` (positions are mapped through ``kv_indices`` starting at
@@ -282,7 +317,7 @@ def commit_paged(
     if not layers:
         raise ValueError("no layers given")
     device = _lib.require_device(layers[0], kv_indptr, kv_indices, what="target_kv_commit")
-    geom, k_tab, v_tab = _paged_layer_tables(layers)
+    geom, k_tab, v_tab = _paged_layer_tables(layers, kv_layout)
     lib = _lib.load()
     stream = _lib.stream_of(device)
     i32_indptr = _as_i32(kv_indptr, device)
@@ -302,7 +337,7 @@ def commit_paged(
         staging = commit_positions_need_staging(src, dst, reqs) if needs_staging is None else needs_staging
         if n <= _lib.MAX_INLINE_ITEMS and not staging:
             rc = lib.atlas_kv_commit_paged_host(
-                k_tab, v_tab, len(layers), *geom.as_args(),
+                k_tab, v_tab, len(layers), *geom.as_head_args(),
                 _lib.ptr(i32_indptr), _lib.ptr(i32_indices),
                 (ctypes_i32 * n)(*reqs), (ctypes_i64 * n)(*src), (ctypes_i64 * n)(*dst), n, stream,
             )
@@ -328,7 +363,7 @@ def commit_paged(
             workspace = torch.empty(need, dtype=torch.uint8, device=device)
         ws_bytes = workspace.numel() * workspace.element_size()
     rc = lib.atlas_kv_commit_paged(
-        k_tab, v_tab, len(layers), *geom.as_args(),
+        k_tab, v_tab, len(layers), *geom.as_head_args(),
         _lib.ptr(i32_indptr), _lib.ptr(i32_indices), _lib.ptr(req_t), _lib.ptr(src_t), _lib.ptr(dst_t), n,
         1 if staging else 0, _lib.ptr(workspace if staging else None), ws_bytes, stream,
     )

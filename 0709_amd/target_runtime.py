@@ -198,7 +198,8 @@ def run_full_verify(*, model, wrapper, state: FullVerifyState, prefix_len: int, 
         else:
             q = (q * cos3 + rotate_half(q) * sin3).contiguous()
             k = (k * cos3 + rotate_half(k) * sin3).contiguous()
-            write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size)
+            write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size,
+                            kv_layout=getattr(wrapper, "kv_layout", "NHD"))
             out = wrapper.run(q, kv_cache)
         attn = first_tensor(out).reshape(n, hq * head_dim)
         hidden = residual + layer.self_attn.o_proj(attn)
@@ -247,7 +248,7 @@ def run_full_ar_decode(*, model, wrappers, state: FullDecodeState, prefix_len: i
             k = (k * cos + rotate_half(k) * sin).contiguous()
             kv_cache = state.paged_prefix_kv[layer_idx]
             write_suffix_kv(kv_cache, key_states=k, value_states=v, prefix_len=prefix_len, page_size=page_size,
-                            start_pos=pos)
+                            start_pos=pos, kv_layout=getattr(wrapper, "kv_layout", "NHD"))
             attn = first_tensor(wrapper.run(q, kv_cache)).reshape(1, hq * head_dim)
             hidden = residual + layer.self_attn.o_proj(attn)
             residual = hidden
@@ -307,7 +308,12 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         self.model = model
         self.tokenizer = tokenizer
         self.dtype = next(model.parameters()).dtype if model is not None else torch.float16
-        self._wrapper = make_prefill_wrapper(args=config) if model is not None else None
+        # The committed prefix lives in HND pages ([pages, 2, Hkv, page_size, D]):
+        # each KV head's keys of a page are one contiguous run, which the
+        # attention streams faster than the NHD pages of the reference
+        # (``args.kv_layout = "NHD"`` keeps those).
+        self.kv_layout = kv_ops.check_kv_layout(getattr(config, "kv_layout", None) or "HND")
+        self._wrapper = make_prefill_wrapper(args=config, kv_layout=self.kv_layout) if model is not None else None
         self.prefix_token_ids: tuple[int, ...] = ()
         self._paged_prefix_kv: list[torch.Tensor] | None = None
         self._prefix_logits: torch.Tensor | None = None
@@ -336,7 +342,7 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         for layer_idx in range(len(self.model.model.layers)):
             key, value = _legacy_layer_kv(past, layer_idx)
             layers.append(prefix_layer_to_paged_kv(key=key, value=value, prefix_len=len(token_ids), node_count=0,
-                                                   page_size=self.config.page_size))
+                                                   page_size=self.config.page_size, kv_layout=self.kv_layout))
         self.prefix_token_ids = token_ids
         self._paged_prefix_kv = layers
         self._prefix_logits = out.logits[:, -1, :].detach()
@@ -809,7 +815,7 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         setup_s = plan_s = model_s = 0.0
         t0 = self._profile_clock() if profile else 0.0
         if self._fallback_decode_wrapper is None:
-            self._fallback_decode_wrapper = make_decode_wrapper(args=self.config)
+            self._fallback_decode_wrapper = make_decode_wrapper(args=self.config, kv_layout=self.kv_layout)
         if profile:
             setup_s = self._profile_clock() - t0
         wrapper = self._fallback_decode_wrapper
@@ -875,7 +881,7 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         prefix_len = len(self.prefix_token_ids)
         src = [prefix_len + int(n) for n in node_ids]
         dst = list(range(prefix_len, prefix_len + len(node_ids)))
-        kv_ops.commit_paged(self._paged_prefix_kv, src, dst)
+        kv_ops.commit_paged(self._paged_prefix_kv, src, dst, kv_layout=self.kv_layout)
         self.prefix_token_ids = (*self.prefix_token_ids, *(int(t) for t in token_ids))
         self._prefix_logits = verify_logits[int(node_ids[-1])].detach().unsqueeze(0)
         self._committed_verify_rounds += 1

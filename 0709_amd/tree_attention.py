@@ -282,8 +282,8 @@ class BatchPrefillWithPagedKVCacheWrapper:
         backend: str = "auto",
         **_unused,
     ) -> None:
-        if kv_layout != "NHD":
-            raise NotImplementedError("only the NHD paged layout is supported")
+        if kv_layout not in ("NHD", "HND"):
+            raise NotImplementedError(f"paged layout {kv_layout!r}: NHD and HND are supported")
         self._workspace = float_workspace_buffer
         self._kv_layout = kv_layout
         self._backend = backend
@@ -599,6 +599,11 @@ class BatchPrefillWithPagedKVCacheWrapper:
             fused_append=dec["fused_append"],
         )
 
+    @property
+    def kv_layout(self) -> str:
+        """The paged layout run() reads: "NHD" or "HND"."""
+        return self._kv_layout
+
     def _persistent(self, name: str, count: int, dtype: torch.dtype) -> torch.Tensor:
         buf = getattr(self, name, None)
         if buf is None or int(buf.numel()) < count or buf.dtype != dtype:
@@ -651,36 +656,38 @@ class BatchPrefillWithPagedKVCacheWrapper:
         plan = self._plan
         if plan is None:
             raise RuntimeError("plan() must be called before run()")
+        hnd = self._kv_layout == "HND"
+        # (token, head) dims of a page: NHD pages [.., page_size, Hkv, D],
+        # HND pages [.., Hkv, page_size, D]
+        td, hd = (-2, -3) if hnd else (-3, -2)
         if isinstance(paged_kv_cache, (tuple, list)):
             k_cache, v_cache = paged_kv_cache
             if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
                 raise ValueError("K and V caches must have the same shape and strides")
             if k_cache.ndim != 4:
-                raise ValueError("tuple KV caches must be [pages, page_size, Hkv, D]")
+                raise ValueError(f"tuple KV caches must be [pages, {'Hkv, page_size' if hnd else 'page_size, Hkv'}, D]")
             base = k_cache
-            es = k_cache.element_size()
-            page_stride = k_cache.stride(0) * es
-            token_stride = k_cache.stride(1) * es
             v_offset = int(v_cache.data_ptr()) - int(k_cache.data_ptr())
-            shape_tail = tuple(k_cache.shape[1:])
         else:
             kv = paged_kv_cache
             if kv.ndim != 5 or int(kv.shape[1]) != 2:
-                raise ValueError(f"kv cache must be [pages, 2, page_size, Hkv, D], got {tuple(kv.shape)}")
+                raise ValueError(f"kv cache must be [pages, 2, {'Hkv, page_size' if hnd else 'page_size, Hkv'}, D], "
+                                 f"got {tuple(kv.shape)}")
             base = kv
-            es = kv.element_size()
-            page_stride = kv.stride(0) * es
-            token_stride = kv.stride(2) * es
-            v_offset = kv.stride(1) * es
-            shape_tail = (int(kv.shape[2]), int(kv.shape[3]), int(kv.shape[4]))
+            v_offset = kv.stride(1) * kv.element_size()
+        es = base.element_size()
+        page_stride = base.stride(0) * es
+        token_stride = base.stride(td) * es
+        head_stride = base.stride(hd) * es
+        shape_tail = (int(base.shape[td]), int(base.shape[hd]), int(base.shape[-1]))
         device = _lib.require_device(q, base, what="tree verify attention")
         if shape_tail != (plan.page_size, plan.num_kv_heads, plan.head_dim):
             raise ValueError(
-                f"kv cache page shape {shape_tail} does not match the plan "
+                f"kv cache (page_size, Hkv, D) {shape_tail} does not match the plan "
                 f"({plan.page_size}, {plan.num_kv_heads}, {plan.head_dim})"
             )
-        if base.stride(-1) != 1 or (plan.num_kv_heads > 1 and base.stride(-2) != plan.head_dim):
-            raise ValueError("kv cache rows (Hkv, D) must be contiguous")
+        if base.stride(-1) != 1 or (not hnd and plan.num_kv_heads > 1 and base.stride(-2) != plan.head_dim):
+            raise ValueError("kv cache rows must be contiguous: (Hkv, D) for NHD pages, D for HND pages")
         if q.dtype != plan.q_dtype or base.dtype != plan.kv_dtype:
             raise TypeError(f"dtype mismatch: q {q.dtype}, kv {base.dtype}, planned {plan.q_dtype}")
         if q.ndim != 3 or tuple(q.shape[1:]) != (plan.num_qo_heads, plan.head_dim) or int(q.shape[0]) < plan.nnz:
@@ -699,7 +706,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         ws_bytes = plan.partial_rows * _partial_row_bytes(plan.head_dim)
         lib = _lib.load()
         common = (
-            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride,
+            _lib.ptr(q), q.stride(0), q.stride(1), _lib.ptr(base), page_stride, v_offset, token_stride, head_stride,
             _lib.ptr(plan.qo_indptr), _lib.ptr(plan.kv_indptr), _lib.ptr(plan.kv_indices),
             plan.device_view(plan.kv_len_offset), plan.mask_mode, _lib.ptr(plan.tree_mask),
             plan.device_view(plan.col_offset), plan.mask_words, plan.device_view(plan.work_offset), plan.num_work,

@@ -63,17 +63,24 @@ def forest_routes(seed: int, k: int = 3, depth: int = 4) -> list[tuple[int, ...]
 class PagedTargetKV:
     """One request's Target KV in a paged pool, all layers in one allocation.
 
-    ``pool[l]`` is layer l's ``[pool_pages, 2, page_size, Hkv, D]`` view; the
-    request's pages are ``kv_indices`` (a random permutation of pool pages).
+    ``pool[l]`` is layer l's page view: ``[pool_pages, 2, page_size, Hkv, D]``
+    ("NHD") or ``[pool_pages, 2, Hkv, page_size, D]`` ("HND", each KV head's
+    keys of a page contiguous); the request's pages are ``kv_indices`` (a
+    random permutation of pool pages).
     """
 
-    pool: torch.Tensor  # [L, pool_pages, 2, ps, Hkv, D]
+    pool: torch.Tensor  # [L, pool_pages, 2, ps, Hkv, D] or [L, pool_pages, 2, Hkv, ps, D]
     kv_indices: torch.Tensor  # int32 [pages]
     page_size: int
+    kv_layout: str = "NHD"
 
     @property
     def layers(self) -> list[torch.Tensor]:
         return list(self.pool.unbind(0))
+
+    def nhd_layer(self, l: int) -> torch.Tensor:
+        """Layer l as an ``[pool_pages, 2, page_size, Hkv, D]`` view."""
+        return self.pool[l] if self.kv_layout == "NHD" else self.pool[l].permute(0, 1, 3, 2, 4)
 
 
 def make_paged_target_kv(
@@ -86,17 +93,24 @@ def make_paged_target_kv(
     seed: int = 0,
     spare_pages: int = 0,
     scale: float = 0.1,
+    kv_layout: str = "NHD",
 ) -> PagedTargetKV:
+    """The values depend on the seed only: an "HND" pool holds the same keys
+    and values as the "NHD" pool of the same seed."""
+    if kv_layout not in ("NHD", "HND"):
+        raise ValueError(f"kv_layout must be 'NHD' or 'HND', got {kv_layout!r}")
     pages = math.ceil(kv_len / page_size)
     pool_pages = pages + spare_pages
     gen = torch.Generator(device=device).manual_seed(seed)
-    pool = torch.empty((geom.layers, pool_pages, 2, page_size, geom.kv_heads, geom.head_dim), dtype=dtype,
-                       device=device)
+    nhd = (pool_pages, 2, page_size, geom.kv_heads, geom.head_dim)
+    page = nhd if kv_layout == "NHD" else (pool_pages, 2, geom.kv_heads, page_size, geom.head_dim)
+    kv = PagedTargetKV(pool=torch.empty((geom.layers,) + page, dtype=dtype, device=device), kv_indices=None,
+                       page_size=page_size, kv_layout=kv_layout)
     for l in range(geom.layers):
-        pool[l].copy_(torch.randn(pool[l].shape, generator=gen, device=device, dtype=torch.float32) * scale)
+        kv.nhd_layer(l).copy_(torch.randn(nhd, generator=gen, device=device, dtype=torch.float32) * scale)
     perm_gen = torch.Generator().manual_seed(seed + 1)
-    kv_indices = torch.randperm(pool_pages, generator=perm_gen)[:pages].to(torch.int32).to(device)
-    return PagedTargetKV(pool=pool, kv_indices=kv_indices, page_size=page_size)
+    kv.kv_indices = torch.randperm(pool_pages, generator=perm_gen)[:pages].to(torch.int32).to(device)
+    return kv
 
 
 def random_queries(geom: Geometry, n: int, *, dtype: torch.dtype, device: torch.device, seed: int,

@@ -66,6 +66,12 @@ def _ev():
 # attention wrapper the bench builds (headline and attention legs).
 PLAN_TUNING: dict = {}
 
+# Page layout of the Target KV pools the bench builds: "HND" pages
+# [pages, 2, Hkv, page_size, D] (each KV head's keys of a page contiguous,
+# the layout the verify attention reads fastest) or the reference's "NHD"
+# [pages, 2, page_size, Hkv, D].
+KV_LAYOUT = "HND"
+
 
 class HeadlineStep:
     def __init__(self, dev, *, prefix_len=16384, page_size=16, seed=0, split_target=None, max_rows=None,
@@ -86,8 +92,9 @@ class HeadlineStep:
         self.n = spec.node_count
         self.kv_len = prefix_len + self.n
         self.pages = math.ceil(self.kv_len / page_size)
+        self.kv_layout = KV_LAYOUT
         self.kv = wl.make_paged_target_kv(self.geom, kv_len=self.kv_len, page_size=page_size, dtype=torch.float16,
-                                          device=dev, seed=seed, spare_pages=64)
+                                          device=dev, seed=seed, spare_pages=64, kv_layout=self.kv_layout)
         self.layers = self.kv.layers
         self.q = wl.random_queries(self.geom, self.n, dtype=torch.float16, device=dev, seed=seed + 7)
         g = torch.Generator(device=dev).manual_seed(seed + 11)
@@ -103,7 +110,7 @@ class HeadlineStep:
         self.verify_logits = (torch.randn((self.n, 128256), generator=g, device=dev) * 2.0).half()
         self.prefix_logits = (torch.randn((128256,), generator=g, device=dev) * 2.0).half()
         ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
-        self.wrapper = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+        self.wrapper = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, self.kv_layout)
         for key, value in PLAN_TUNING.items():
             setattr(self.wrapper, key, value)
         if split_target is not None:
@@ -183,7 +190,8 @@ class HeadlineStep:
                                  append_value_states=self.v_new[l])
                 continue
             if with_append:
-                self.kv_ops.append_paged([layer], [self.k_new[l]], [self.v_new[l]], dst_slots=self.tree_slots)
+                self.kv_ops.append_paged([layer], [self.k_new[l]], [self.v_new[l]], dst_slots=self.tree_slots,
+                                         kv_layout=self.kv_layout)
             self.wrapper.run(self.q[l], layer, out=self.outs[l], lse=self.lses[l] if with_lse else None)
 
     def capture(self):
@@ -240,7 +248,8 @@ class HeadlineStep:
         src = [self.prefix_len + x for x in nodes]
         dst = list(range(self.prefix_len, self.prefix_len + len(nodes)))
         self._timed(self.commit_events, lambda: self.kv_ops.commit_paged(
-            self.layers, src, dst, kv_indptr=self.kv_indptr, kv_indices=self.kv.kv_indices))
+            self.layers, src, dst, kv_indptr=self.kv_indptr, kv_indices=self.kv.kv_indices,
+            kv_layout=self.kv_layout))
         # the live set: the committed path's page starts and its last slot,
         # sampled inside the prune launch
         self.live_path[0].len = self.prefix_len + len(nodes)
@@ -327,8 +336,9 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, pr
     while pool is None:
         pool_pages = max(need_pages + 64, int(pool_gb * 1e9 / (geom.layers * page_bytes)))
         try:
-            pool = torch.empty((geom.layers, pool_pages, 2, ps, geom.kv_heads, geom.head_dim), dtype=torch.bfloat16,
-                               device=dev)
+            page = (2, ps, geom.kv_heads, geom.head_dim) if KV_LAYOUT == "NHD" else (2, geom.kv_heads, ps,
+                                                                                          geom.head_dim)
+            pool = torch.empty((geom.layers, pool_pages) + page, dtype=torch.bfloat16, device=dev)
         except torch.cuda.OutOfMemoryError:
             pool_gb /= 2
             if pool_gb < 1:
@@ -343,8 +353,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, pr
     used = perm.to(dev)
     g = torch.Generator(device=dev).manual_seed(5)
     for l in range(geom.layers):
-        pool[l, used] = (torch.randn((need_pages, 2, ps, geom.kv_heads, geom.head_dim), generator=g, device=dev)
-                         * 0.1).to(torch.bfloat16)
+        pool[l, used] = (torch.randn((need_pages,) + page, generator=g, device=dev) * 0.1).to(torch.bfloat16)
     layers = list(pool.unbind(0))
     kv_indptr_h = case.kv_indptr
     qo_h = case.qo_indptr
@@ -358,7 +367,7 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, pr
          for _ in range(layers_timed)]
     outs = [torch.empty_like(x) for x in q]
     ws = torch.empty(512 * 1024 * 1024, dtype=torch.uint8, device=dev)
-    w = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w = ffv.BatchPrefillWithPagedKVCacheWrapper(ws, KV_LAYOUT)
     w.plan(qo, kv_indptr, kv_indices, last, geom.q_heads, geom.kv_heads, geom.head_dim, ps, custom_mask=flat_mask,
            causal=False, q_data_type=torch.bfloat16)
 
@@ -406,18 +415,18 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, pr
         # (the same positions on other physical pages), so every copy is cold
         for k in range(profile_launches):
             kv_idx = torch.randperm(pool_pages, generator=gen)[:need_pages].to(torch.int32).to(dev)
-            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **dict(args, kv_indices=kv_idx))
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **dict(args, kv_indices=kv_idx))
             torch.cuda.synchronize()
             print(f"batched leg: commit launch {k} done", file=sys.stderr, flush=True)
         return {"profile_launches": profile_launches, "items": len(src), "moved_bytes":
                 len(src) * geom.layers * geom.token_bytes()}
     for _ in range(5):
-        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **args)
     torch.cuda.synchronize()
     print("batched leg: attention timed", file=sys.stderr, flush=True)
     a.record()
     for _ in range(50):
-        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **args)
     b.record()
     torch.cuda.synchronize()
     commit_call_us = a.elapsed_time(b) * 1000.0 / 50
@@ -431,16 +440,16 @@ def batched_leg(dev, *, pool_gb=200.0, requests=32, layers_timed=32, iters=5, pr
     inst_args = [args] + [dict(args, kv_indices=torch.randperm(pool_pages, generator=gen)[:need_pages]
                                .to(torch.int32).to(dev)) for _ in range(n_inst - 1)]
     with torch.cuda.stream(side):
-        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+        kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **args)
     torch.cuda.current_stream().wait_stream(side)
     cgraph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(cgraph):
         for k in range(n_inst):
-            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **inst_args[k])
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **inst_args[k])
     hgraph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(hgraph):
         for _ in range(20):
-            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, **args)
+            kv_ops.commit_paged(layers, src_t, dst_t, needs_staging=staging, kv_layout=KV_LAYOUT, **args)
     cgraph.replay()
     hgraph.replay()
     torch.cuda.synchronize()
@@ -537,7 +546,7 @@ def commit_floors(dev, layers, inst_args, item_req, src, dst, moved, ps, side, l
 
     def rows(k):
         s_t, d_t = slot_sets[k]
-        kv_ops.commit_paged(layers, s_t, d_t, needs_staging=False)
+        kv_ops.commit_paged(layers, s_t, d_t, needs_staging=False, kv_layout=KV_LAYOUT)
 
     bufs = torch.empty((2 * n_inst, moved), dtype=torch.uint8, device=dev)
     bufs.fill_(1)
@@ -707,13 +716,13 @@ def decode_leg(dev, *, requests=8, routes=9, prefix_len=None, steps=8, iters=5, 
     perm = torch.randperm(pool_pages, generator=gen)
     phys = [int(perm[i]) for i in indices]
     batch = requests * routes
-    layers = [(torch.randn((pool_pages, 2, ps, geom.kv_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
-              for _ in range(geom.layers)]
+    page = (2, ps, geom.kv_heads, geom.head_dim) if KV_LAYOUT == "NHD" else (2, geom.kv_heads, ps, geom.head_dim)
+    layers = [(torch.randn((pool_pages,) + page, device=dev) * 0.1).to(torch.bfloat16) for _ in range(geom.layers)]
     q = [(torch.randn((batch, geom.q_heads, geom.head_dim), device=dev) * 0.1).to(torch.bfloat16)
          for _ in range(geom.layers)]
     outs = [torch.empty_like(x) for x in q]
     ws = torch.empty(256 * 1024 * 1024, dtype=torch.uint8, device=dev)
-    w = da.BatchDecodeWithPagedKVCacheWrapper(ws, "NHD")
+    w = da.BatchDecodeWithPagedKVCacheWrapper(ws, KV_LAYOUT)
     w.use_cascade = cascade
     w.split_target_items = split_target
     w.plan(torch.tensor(indptr, dtype=torch.int32, device=dev), torch.tensor(phys, dtype=torch.int32, device=dev),
@@ -944,7 +953,7 @@ def cpu_baseline(step: HeadlineStep, budget_s: float):
     times = []
     t_start = time.perf_counter()
     for l in range(step.geom.layers):
-        layer = step.layers[l].cpu().numpy()
+        layer = step.kv.nhd_layer(l).cpu().numpy()
         q = step.q[l].cpu().numpy()
         t0 = time.perf_counter()
         oatt.masked_attention(q, layer, [0, step.n], [0, step.pages], idx, [last], masks=[mask], dtype=np.float32)
@@ -987,7 +996,7 @@ def cpu_kv_legs(step: HeadlineStep):
     layers = [torch.empty((step.pages, 2, ps, step.geom.kv_heads, step.geom.head_dim), dtype=torch.float16)
               for _ in range(step.geom.layers)]
     for l, layer in enumerate(layers):
-        layer.copy_(step.layers[l][torch.tensor(step.kv_indices_host, device=step.dev).long()].cpu())
+        layer.copy_(step.kv.nhd_layer(l)[torch.tensor(step.kv_indices_host, device=step.dev).long()].cpu())
     k_new = [k.cpu() for k in step.k_new]
     v_new = [v.cpu() for v in step.v_new]
     _, parents, _, route_nodes = _oracle_dedup(step.routes)
@@ -1061,6 +1070,8 @@ def main():
     ap.add_argument("--split-granule", type=int, default=None, metavar="KEYS",
                     help="key granule of the attention splits (default: the planner's)")
     ap.add_argument("--max-rows", type=int, default=None)
+    ap.add_argument("--kv-layout", choices=("HND", "NHD"), default=KV_LAYOUT,
+                    help="page layout of the Target KV pools (default %(default)s)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="also run device-to-device copies of MIB MiB (calibrates HBM byte counters)")
     ap.add_argument("--commit-pool-gb", type=float, default=200.0)
@@ -1075,6 +1086,7 @@ def main():
                                    "and has no multi-GPU leg", "n_gpus": args.gpus}))
         sys.exit(2)
     dev = torch.device("cuda:0")
+    globals()["KV_LAYOUT"] = args.kv_layout
     if args.split_target is not None:
         PLAN_TUNING["split_target_items"] = args.split_target
     if args.split_granule is not None:
@@ -1147,7 +1159,8 @@ def main():
         "config": {
             "workload": "forest dedup + 32-layer masked verify attention + commit + prune",
             "geometry": "Llama-3.1-8B KV (32 layers, 32 q heads, 8 kv heads, head_dim 128)",
-            "prefix_len": step.prefix_len, "page_size": step.ps, "routes": len(step.routes), "depth": 4,
+            "prefix_len": step.prefix_len, "page_size": step.ps, "kv_layout": step.kv_layout,
+            "routes": len(step.routes), "depth": 4,
             "nodes": step.n, "kv_len": step.kv_len, "work_items": plan.num_work, "merge_items": plan.num_merge,
             "tiles_per_split": plan.tiles_per_split,
         },

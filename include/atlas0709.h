@@ -13,14 +13,22 @@
  *     ATLAS_EHIP_BASE - hipError_t for a HIP runtime error.  atlas_last_error()
  *     returns a message for the last failing call on the calling thread.
  *
- * KV layouts.  A layer's K (or V) row for one token is `row_bytes` contiguous
- * bytes (num_kv_heads * head_dim * element size).  A physical slot id s lives at
+ * KV layouts.  A layer's K (or V) row for one token is `row_bytes` bytes
+ * (num_kv_heads * head_dim * element size).  A physical slot id s starts at
  *     base + (s / page_size) * page_stride + (s % page_size) * token_stride
- * where base is the layer's K or V base address.  This covers
+ * where base is the layer's K or V base address, and KV head h of the row at
+ * h * head_stride from there (head_stride = head_dim * element size when the
+ * row is contiguous).  This covers
  *   - FlashInfer NHD pages [pages, 2, page_size, Hkv, D] (V base = K base +
- *     page_size*token_stride, page_stride = 2*page_size*token_stride), and
+ *     page_size*token_stride, page_stride = 2*page_size*token_stride,
+ *     contiguous rows),
+ *   - FlashInfer HND pages [pages, 2, Hkv, page_size, D] (token_stride =
+ *     head_dim * element size, head_stride = page_size * token_stride), and
  *   - SGLang's flat token pool [slots, Hkv, D] per layer (page_size = 1,
  *     separate K and V bases, page_stride = token_stride = row_bytes).
+ * Entry points with head_bytes / head_stride arguments take rows split by KV
+ * head: head_bytes (head_dim * element size) contiguous per head, head_stride
+ * apart; head_stride = 0 or head_stride = head_bytes means contiguous rows.
  */
 #ifndef ATLAS0709_H
 #define ATLAS0709_H
@@ -78,7 +86,8 @@ int atlas_kv_move_slots(const void* const* k_layers, const void* const* v_layers
  * (src/atlas_0709/flashinfer_paged/sglang_page_attention.py:187-194). */
 int atlas_kv_append(const void* const* k_layers, const void* const* v_layers, int num_layers,
                     int64_t page_size, int64_t page_stride, int64_t token_stride,
-                    int64_t row_bytes, const void* const* k_src, const void* const* v_src,
+                    int64_t row_bytes, int64_t head_bytes, int64_t head_stride,
+                    const void* const* k_src, const void* const* v_src,
                     int64_t src_token_stride, const int64_t* dst_slots_dev, int64_t dst_start,
                     int64_t n, void* stream);
 
@@ -94,7 +103,8 @@ int atlas_kv_append(const void* const* k_layers, const void* const* v_layers, in
  * (src/atlas_0709/target_runtime.py:873-920). */
 int atlas_kv_commit_paged(const void* const* k_layers, const void* const* v_layers, int num_layers,
                           int64_t page_size, int64_t page_stride, int64_t token_stride,
-                          int64_t row_bytes, const int32_t* kv_indptr_dev,
+                          int64_t row_bytes, int64_t head_bytes, int64_t head_stride,
+                          const int32_t* kv_indptr_dev,
                           const int32_t* kv_indices_dev, const int32_t* item_req_dev,
                           const int64_t* src_pos_dev, const int64_t* dst_pos_dev, int64_t n,
                           int needs_staging, void* workspace_dev, size_t workspace_bytes,
@@ -105,7 +115,8 @@ int atlas_kv_commit_paged(const void* const* k_layers, const void* const* v_laye
  * argument block, so the commit costs no host-to-device copy. */
 int atlas_kv_commit_paged_host(const void* const* k_layers, const void* const* v_layers,
                                int num_layers, int64_t page_size, int64_t page_stride,
-                               int64_t token_stride, int64_t row_bytes,
+                               int64_t token_stride, int64_t row_bytes, int64_t head_bytes,
+                               int64_t head_stride,
                                const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                const int32_t* item_req_host, const int64_t* src_pos_host,
                                const int64_t* dst_pos_host, int64_t n, void* stream);
@@ -193,8 +204,10 @@ int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
 /* O = softmax(Q K^T * sm_scale + M) V over paged KV, GQA (num_qo_heads a
  * multiple of num_kv_heads), one launch for all requests plus a merge launch
  * when a row block is split along the keys.  q: [nnz, Hq, D]; kv_cache:
- * FlashInfer NHD pages [pages, 2, page_size, Hkv, D] addressed with the
- * strides above; out: [nnz, Hq, D] in the input dtype; lse (optional, may be
+ * FlashInfer NHD pages [pages, 2, page_size, Hkv, D] or HND pages
+ * [pages, 2, Hkv, page_size, D] addressed with the strides above (KV head h
+ * of a token row at h * kv_head_stride); out: [nnz, Hq, D] in the input
+ * dtype; lse (optional, may be
  * NULL): [nnz, Hq] fp32, natural-log log-sum-exp of the scaled scores.
  * workspace_dev holds the split partial states: partial_rows rows of D
  * 16-bit values in the output dtype (the normalised partial O, as FlashInfer
@@ -209,7 +222,7 @@ int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
  * (src/atlas_0709/flashinfer_full_verify.py:953-985, :1223). */
 int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                            const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
-                           int64_t token_stride, const int32_t* qo_indptr_dev,
+                           int64_t token_stride, int64_t kv_head_stride, const int32_t* qo_indptr_dev,
                            const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                            const int32_t* kv_len_dev, int mask_mode,
                            const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
@@ -242,7 +255,7 @@ int atlas_tree_verify_attn(const void* q, int64_t q_stride_token, int64_t q_stri
  * called at :1213): the cache receives the rotated K rows bit for bit. */
 int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                                   const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
-                                  int64_t token_stride, const int32_t* qo_indptr_dev,
+                                  int64_t token_stride, int64_t kv_head_stride, const int32_t* qo_indptr_dev,
                                   const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                   const int32_t* kv_len_dev, int mask_mode,
                                   const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,
@@ -282,7 +295,7 @@ int atlas_tree_verify_attn_append(const void* q, int64_t q_stride_token, int64_t
  * forbid allocation). */
 int atlas_tree_verify_attn_noalloc(const void* q, int64_t q_stride_token, int64_t q_stride_head,
                                    const void* kv_cache, int64_t page_stride, int64_t kv_v_offset,
-                                   int64_t token_stride, const int32_t* qo_indptr_dev,
+                                   int64_t token_stride, int64_t kv_head_stride, const int32_t* qo_indptr_dev,
                                    const int32_t* kv_indptr_dev, const int32_t* kv_indices_dev,
                                    const int32_t* kv_len_dev, int mask_mode,
                                    const uint64_t* tree_mask_dev, const int32_t* mask_col_start_dev,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 9
+    assert lib.atlas_abi_version() == 10
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -45,7 +45,7 @@ def test_argument_errors_are_reported_without_device_work():
     assert b"" != lib.atlas_last_error()
     rc = lib.atlas_tree_verify_attn(
         None, 0, 0,            # q, strides
-        None, 0, 0, 0,         # kv cache, page stride, V offset, token stride
+        None, 0, 0, 0, 0,      # kv cache, page stride, V offset, token stride, head stride
         None, None, None, None,  # qo_indptr, kv_indptr, kv_indices, kv_len
         0, None, None, 1,      # mask mode, tree mask, mask column start, mask words
         None, 0, None,         # work list, page windows
@@ -110,11 +110,12 @@ def _verify_args(name, **over):
     fake = ctypes.c_void_p(1 << 20)
     row = 2 * 128 + 4
     a = dict(q=fake, q_st=32 * 128, q_sh=128, kv=fake, page_stride=2 * 16 * 8 * 256, v_off=16 * 8 * 256,
-             token_stride=8 * 256, qo=fake, kvp=fake, kvi=fake, kvl=fake, mask_mode=1, tree=fake, col=fake, words=1,
+             token_stride=8 * 256, head_stride=256, qo=fake, kvp=fake, kvi=fake, kvl=fake, mask_mode=1, tree=fake, col=fake, words=1,
              work=fake, nwork=1, win=None, merge=fake, nmerge=1, merge_rows=64, rows=64, hq=32, hkv=8, d=128,
              ps=16, scale=ctypes.c_float(0.088), dtype=0, out=fake, o_st=32 * 128, o_sh=128, lse=None)
     a.update(over)
-    head = [a[k] for k in ("q", "q_st", "q_sh", "kv", "page_stride", "v_off", "token_stride", "qo", "kvp", "kvi",
+    head = [a[k] for k in ("q", "q_st", "q_sh", "kv", "page_stride", "v_off", "token_stride", "head_stride", "qo",
+                           "kvp", "kvi",
                            "kvl", "mask_mode", "tree", "col", "words", "work", "nwork", "win", "merge", "nmerge",
                            "merge_rows", "rows", "hq", "hkv", "d", "ps", "scale", "dtype", "out", "o_st", "o_sh",
                            "lse")]

@@ -93,7 +93,8 @@ def cpu_target(monkeypatch):
         lp = torch.log_softmax(lg.float(), dim=-1)
         return lp[torch.tensor(rows), torch.tensor(tokens)]
 
-    def layout(*, key, value, prefix_len, node_count, page_size):
+    def layout(*, key, value, prefix_len, node_count, page_size, kv_layout="NHD"):
+        assert kv_layout == "NHD"  # the configuration below asks for the reference's pages
         pages = math.ceil((prefix_len + node_count) / page_size)
         out = torch.zeros((pages, 2, page_size, key.shape[1], key.shape[3]), dtype=key.dtype)
         for pos in range(prefix_len):
@@ -101,7 +102,8 @@ def cpu_target(monkeypatch):
             out[pos // page_size, 1, pos % page_size] = value[0, :, pos]
         return out
 
-    def commit(layers, src, dst):
+    def commit(layers, src, dst, kv_layout="NHD"):
+        assert kv_layout == "NHD"
         for kv in layers:
             ps = kv.shape[2]
             rows = [kv[s // ps, :, s % ps].clone() for s in src]
@@ -115,7 +117,7 @@ def cpu_target(monkeypatch):
     monkeypatch.setattr(tr, "gather_token_logprobs", gather)
     monkeypatch.setattr(tr.kv_ops, "commit_paged", commit)
     cfg = SimpleNamespace(k=3, d=3, page_size=4, device="cpu", dtype="float32", workspace_mb=1,
-                          flashinfer_backend="auto", use_packed_custom_mask=False)
+                          flashinfer_backend="auto", use_packed_custom_mask=False, kv_layout="NHD")
 
     def make(**kw):
         nonlocal backend

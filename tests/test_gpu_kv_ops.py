@@ -384,3 +384,58 @@ def test_host_staging_ring_keeps_every_pending_upload(dev):
         assert np.array_equal(d.cpu().numpy(), h)
     vals = [int(x) for x in rng.integers(-2**62, 2**62, size=33)]
     assert lib.upload_i64(vals, dev).cpu().tolist() == vals
+
+
+@pytest.mark.parametrize("heads,dim,staged,as_tensors", [(8, 128, False, False), (8, 64, False, True),
+                                                        (2, 128, True, False), (8, 128, True, True),
+                                                        (1, 64, False, False)])
+def test_hnd_append_and_commit_match_nhd(dev, heads, dim, staged, as_tensors):
+    """HND pages [pages, 2, Hkv, ps, D] (a token's row split by KV head):
+    append_paged at positions and at slots, and commit_paged (in place,
+    staged through the workspace, host-list and device-tensor positions)
+    leave the same values, read back as NHD, as the same calls on NHD pages,
+    which match the oracle elsewhere in this file (2 KiB, 1 KiB and 256-byte
+    rows: both one-wave row paths and the vector loop)."""
+    kv = pkg("kv_ops")
+    gen = torch.Generator().manual_seed(heads * dim + staged)
+    layers, pages, ps = 3, 10, 16
+    nhd = [_rand(gen, (pages, 2, ps, heads, dim), torch.float16) for _ in range(layers)]
+    k_new = [_rand(gen, (5, heads, dim), torch.float16) for _ in range(layers)]
+    v_new = [_rand(gen, (5, heads, dim), torch.float16) for _ in range(layers)]
+    indices = torch.randperm(pages, generator=gen).to(torch.int32)
+    slots = torch.tensor([int(indices[p // ps]) * ps + p % ps for p in (40, 41, 57, 58, 100)], dtype=torch.int64)
+    if staged:
+        src, dst = [100, 90, 120, 95], [90, 95, 101, 102]  # dst 90 and 95 are sources of other items
+    else:
+        src, dst = [100, 103, 120, 95], [90, 91, 92, 93]
+    results = []
+    for layout in ("NHD", "HND"):
+        caches = [(t if layout == "NHD" else t.permute(0, 1, 3, 2, 4)).contiguous().to(dev) for t in nhd]
+        kv.append_paged(caches, [x.to(dev) for x in k_new], [x.to(dev) for x in v_new], start_pos=3,
+                        kv_layout=layout)
+        kv.append_paged(caches, [x.to(dev) for x in k_new], [x.to(dev) for x in v_new], dst_slots=slots.to(dev),
+                        kv_layout=layout)
+        pos = (torch.tensor(src, device=dev), torch.tensor(dst, device=dev)) if as_tensors else (src, dst)
+        kv.commit_paged(caches, *pos, kv_indptr=torch.tensor([0, pages], dtype=torch.int32, device=dev),
+                        kv_indices=indices.to(dev), kv_layout=layout)
+        torch.cuda.synchronize()
+        results.append([(c if layout == "NHD" else c.permute(0, 1, 3, 2, 4)).cpu().contiguous() for c in caches])
+    for a, b in zip(*results):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+    # the calls changed the cache (the comparison is not vacuous)
+    assert not torch.equal(results[0][0].view(torch.int16), nhd[0].view(torch.int16))
+
+
+def test_hnd_layout_geometry_and_refusals(dev):
+    """HND geometry: token stride D, head stride page_size * D; a layout name
+    outside NHD / HND is refused."""
+    kv = pkg("kv_ops")
+    hnd = torch.zeros((4, 2, 8, 16, 128), dtype=torch.float16, device=dev)
+    geom, v_off = kv.paged_layer_geometry(hnd, "HND")
+    assert (geom.page_size, geom.token_stride, geom.head_stride, geom.head_bytes, geom.row_bytes) == \
+        (16, 256, 16 * 256, 256, 8 * 256)
+    assert v_off == 8 * 16 * 256 and geom.page_stride == 2 * v_off
+    nhd_geom, _ = kv.paged_layer_geometry(torch.zeros((4, 2, 16, 8, 128), dtype=torch.float16, device=dev))
+    assert nhd_geom.token_stride == 8 * 256 and nhd_geom.head_stride == 256
+    with pytest.raises(ValueError, match="kv_layout"):
+        kv.paged_layer_geometry(hnd, "NDH")

@@ -118,30 +118,34 @@ def test_score_routes_forest_matches_oracle_and_selection(dev):
     assert b._select_route(scores).route_id == best["route_id"]
 
 
-def test_commit_selected_path_reference_literal(dev):
-    # tests/test_target_kv_commit.py:13-45 on fp16 rows (D = 8 for 16-byte rows)
+@pytest.mark.parametrize("layout", ["NHD", "HND"])
+def test_commit_selected_path_reference_literal(dev, layout):
+    # tests/test_target_kv_commit.py:13-45 on fp16 rows (D = 8 for 16-byte
+    # rows, two KV heads), in the reference's NHD pages and in HND pages
     tr = pkg("target_runtime")
-    b = _backend(tr)
+    b = _backend(tr, kv_layout=layout)
     b.config = SimpleNamespace(page_size=4)
     b.prefix_token_ids = (1, 2, 3)
     b._prefix_logits = torch.zeros((1, 8), device=dev)
     b._committed_verify_rounds = 0
-    cache = torch.zeros((2, 2, 4, 1, 8), dtype=torch.float16)
+    cache = torch.zeros((2, 2, 4, 2, 8), dtype=torch.float16)
     for pos in range(8):
         page, off = divmod(pos, 4)
-        cache[page, 0, off] = 100 + pos
-        cache[page, 1, off] = 200 + pos
-    b._paged_prefix_kv = [cache.to(dev)]
+        cache[page, 0, off] = 100 + pos + torch.tensor([[0.0], [0.5]])
+        cache[page, 1, off] = 200 + pos + torch.tensor([[0.0], [0.5]])
+    as_layout = (lambda t: t) if layout == "NHD" else (lambda t: t.permute(0, 1, 3, 2, 4))
+    b._paged_prefix_kv = [as_layout(cache).contiguous().to(dev)]
     logits = torch.arange(32, dtype=torch.float32, device=dev).reshape(4, 8)
     b._commit_selected_path(token_ids=(9, 10), node_ids=(0, 2), verify_logits=logits)
-    c = b._paged_prefix_kv[0].cpu()
-    assert c[0, 0, 3, 0, 0].item() == 103 and c[1, 0, 0, 0, 0].item() == 105
-    assert c[0, 1, 3, 0, 0].item() == 203 and c[1, 1, 0, 0, 0].item() == 205
+    c = as_layout(b._paged_prefix_kv[0].cpu())  # back to NHD indexing
+    for h, add in ((0, 0.0), (1, 0.5)):
+        assert c[0, 0, 3, h, 0].item() == 103 + add and c[1, 0, 0, h, 0].item() == 105 + add
+        assert c[0, 1, 3, h, 0].item() == 203 + add and c[1, 1, 0, h, 0].item() == 205 + add
     assert b.prefix_token_ids == (1, 2, 3, 9, 10)
     assert torch.equal(b._prefix_logits, logits[2].unsqueeze(0))
     assert b._committed_verify_rounds == 1
     b._ensure_page_capacity(4)
-    assert b._paged_prefix_kv[0].shape[0] == 4 and torch.equal(b._paged_prefix_kv[0][:2].cpu(), c)
+    assert b._paged_prefix_kv[0].shape[0] == 4 and torch.equal(as_layout(b._paged_prefix_kv[0][:2].cpu()), c)
     with pytest.raises(ValueError):
         b._commit_selected_path(token_ids=(1,), node_ids=(), verify_logits=logits)
 

@@ -84,15 +84,22 @@ def _model(dev, seed):
     return m.half().to(dev).eval()
 
 
-def _backend(dev, model, *, prefix_len, seed, **kw):
+def _nhd(cache, layout):
+    """A paged layer as NHD pages [pages, 2, PS, HKV, D]."""
+    return cache if layout == "NHD" else cache.permute(0, 1, 3, 2, 4)
+
+
+def _backend(dev, model, *, prefix_len, seed, kv_layout=None, **kw):
+    """The runtime over a random prefix cache; ``kv_layout`` None takes the
+    runtime's default (HND pages), the same values either way."""
     tr = pkg("target_runtime")
     cfg = SimpleNamespace(k=3, d=4, page_size=PS, device=str(dev), workspace_mb=64, flashinfer_backend="auto",
-                          use_packed_custom_mask=False)
+                          use_packed_custom_mask=False, kv_layout=kv_layout)
     b = tr.DirectFlashInferMaskedTreeVerifyBackend(config=cfg, model=model, **kw)
     g = torch.Generator(device=dev).manual_seed(seed)
     pages = math.ceil(prefix_len / PS)
-    b._paged_prefix_kv = [(torch.randn((pages, 2, PS, HKV, D), generator=g, device=dev) * 0.5).half()
-                          for _ in range(LAYERS)]
+    nhd = [(torch.randn((pages, 2, PS, HKV, D), generator=g, device=dev) * 0.5).half() for _ in range(LAYERS)]
+    b._paged_prefix_kv = nhd if b.kv_layout == "NHD" else [x.permute(0, 1, 3, 2, 4).contiguous() for x in nhd]
     b.prefix_token_ids = tuple(int(x) for x in torch.randint(0, VOCAB, (prefix_len,), generator=g, device=dev))
     b._prefix_logits = (torch.randn((1, VOCAB), generator=g, device=dev) * 3).half()
     return b
@@ -151,6 +158,36 @@ def test_three_verify_rounds_fused_equals_separate(dev):
         assert x.shape == y.shape and torch.equal(x.view(torch.int16), y.view(torch.int16))
 
 
+def test_hnd_and_nhd_prefix_pages_give_the_same_rounds(dev):
+    """The runtime's HND prefix pages and the reference's NHD pages holding
+    the same values: three verify rounds (fused forward, commits growing the
+    prefix past a page boundary) and a fallback AR give the same selections,
+    per-token log-probs, prefix logits and, read as NHD, the same KV bits."""
+    model = _model(dev, 9)
+    runs = []
+    for layout in ("NHD", "HND"):
+        b = _backend(dev, model, prefix_len=300, seed=10, kv_layout=layout, fallback_ar_tokens=3)
+        assert b.kv_layout == layout and b._wrapper.kv_layout == layout
+        rounds = []
+        for r in range(3):
+            res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=_routes(30 + r))
+            torch.cuda.synchronize()
+            rounds.append((res.selected_route_id, b.prefix_token_ids, [sc.token_logprobs for sc in res.scores],
+                           b._prefix_logits.clone().view(torch.int16)))
+        b.fallback_threshold = 1e9
+        res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=_routes(40))
+        torch.cuda.synchronize()
+        rounds.append((tuple(res.fallback_token_ids), b.prefix_token_ids, None,
+                       b._prefix_logits.clone().view(torch.int16)))
+        runs.append((rounds, [_nhd(x, layout).contiguous() for x in b._paged_prefix_kv]))
+    (ra, kva), (rb, kvb) = runs
+    assert len(ra[2][1]) > 304
+    for (sa, pa, la, xa), (sb, pb, lb, xb) in zip(ra, rb):
+        assert sa == sb and pa == pb and la == lb and torch.equal(xa, xb)
+    for x, y in zip(kva, kvb):
+        assert x.shape == y.shape and torch.equal(x.view(torch.int16), y.view(torch.int16))
+
+
 def _dense_step_logits(model, cache, seq_len, token, pos):
     """One decode step of the tiny model in float32 over the first seq_len
     rows of the paged cache (whose row pos already holds this token's K/V,
@@ -166,7 +203,7 @@ def _dense_step_logits(model, cache, seq_len, token, pos):
         k = layer.self_attn.k_proj(x).reshape(1, HKV, D)
         q = q * cos + tr.rotate_half(q) * sin
         k = k * cos + tr.rotate_half(k) * sin
-        kv = cache[li].reshape(-1, 2, PS, HKV, D)
+        kv = cache[li]
         keys = kv[:, 0].reshape(-1, HKV, D)[:seq_len].float()
         vals = kv[:, 1].reshape(-1, HKV, D)[:seq_len].float()
         if li == 0:  # the first layer's K row depends on the token alone: written bit for bit
@@ -197,7 +234,8 @@ def test_fallback_ar_decodes_on_the_prefix_pages(dev):
     # replay the steps densely: step i consumed token i at position prefix_len + i
     for i, tok in enumerate(toks):
         with torch.no_grad():
-            dense = _dense_step_logits(model, b._paged_prefix_kv, prefix_len + i + 1, tok, prefix_len + i)
+            dense = _dense_step_logits(model, [_nhd(x, b.kv_layout) for x in b._paged_prefix_kv],
+                                       prefix_len + i + 1, tok, prefix_len + i)
         if i + 1 < len(toks):
             top2 = torch.topk(dense[0], 2).values
             if float(top2[0] - top2[1]) > 2e-2:
@@ -242,7 +280,8 @@ def test_rpc_sequence_from_prefill_on_a_transformers_llama(dev):
     prompt = [int(x) for x in torch.randint(0, VOCAB, (300,), generator=g)]
     pre = app.prefill({"prompt_token_ids": prompt})
     assert pre["prompt_len"] == 300 and pre["metadata"]["committed_prefix_length"] == 300
-    assert len(backend._paged_prefix_kv) == LAYERS and backend._paged_prefix_kv[0].shape[1:] == (2, PS, HKV, D)
+    assert backend.kv_layout == "HND"  # the runtime's default pages: [pages, 2, Hkv, page_size, D]
+    assert len(backend._paged_prefix_kv) == LAYERS and backend._paged_prefix_kv[0].shape[1:] == (2, HKV, PS, D)
     prefix = list(prompt)
     for rnd in range(2):
         routes = [{"route_id": 10 * rnd + i, "token_ids": [int(x) for x in torch.randint(0, VOCAB, (4,), generator=g)],

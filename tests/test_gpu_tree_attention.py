@@ -73,11 +73,16 @@ def _build(dev, *, seed, prefix_len, routes, hq=32, hkv=8, d=128, ps=16, dtype=t
                 hq=hq, hkv=hkv, d=d, ps=ps, dtype=dtype, route_nodes=route_nodes)
 
 
-def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL, max_rows=None):
+def _hnd(kv):
+    """NHD pages [pool, 2, ps, Hkv, D] as HND pages [pool, 2, Hkv, ps, D]."""
+    return kv.permute(0, 1, 3, 2, 4).contiguous()
+
+
+def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL, max_rows=None, layout="NHD"):
     ta = pkg("tree_attention")
     ffv = pkg("flashinfer_full_verify")
     ws = torch.empty(128 * 1024 * 1024, dtype=torch.uint8, device=dev)
-    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, "NHD")
+    w = ta.BatchPrefillWithPagedKVCacheWrapper(ws, layout)
     if split_target is not None:
         w.split_target_items = split_target
     if max_rows is not None:
@@ -95,7 +100,8 @@ def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL, ma
         c["hq"], c["hkv"], c["d"], c["ps"], causal=False, pos_encoding_mode="NONE",
         q_data_type=c["dtype"], kv_data_type=c["dtype"], **mask_kw,
     )
-    out, lse = w.run(c["q"].to(dev), c["kv"].to(dev), return_lse=True)
+    kv = c["kv"] if layout == "NHD" else _hnd(c["kv"])
+    out, lse = w.run(c["q"].to(dev), kv.to(dev), return_lse=True)
     torch.cuda.synchronize()
     ro, rl = oatt.masked_attention(
         c["q"].float().numpy().astype(np.float64), c["kv"].float().numpy().astype(np.float64),
@@ -107,6 +113,7 @@ def _run_and_check(dev, c, *, split_target=None, use_packed=False, atol=ATOL, ma
     err_l = float(np.abs(l - rl).max())
     assert err_o <= atol, f"max |O - ref| = {err_o}"
     assert err_l <= atol, f"max |lse - ref| = {err_l}"
+    c.setdefault("outs", {})[(layout, split_target)] = (out.cpu(), lse.cpu())
     return w, o, ro
 
 
@@ -828,3 +835,65 @@ def test_wide_tree_mask_refused_beyond_its_width(dev):
                device=dev), torch.arange(pages, dtype=torch.int32, device=dev),
                torch.tensor([kv - (pages - 1) * 16], dtype=torch.int32, device=dev), 32, 8, 128, 16,
                custom_mask=mask.reshape(-1).to(dev), q_data_type=torch.float16)
+
+
+@pytest.mark.parametrize("case", ["forest16k", "forest16k_split1", "short61_bf16", "d64_ps32", "wide130_bf16",
+                                  "causal_free_4k"])
+def test_hnd_pages_match_oracle_and_nhd_bit_for_bit(dev, case):
+    """HND pages [pool, 2, Hkv, ps, D] (each KV head's keys of a page one
+    contiguous run) holding the NHD case's values: within 2e-3 of the fp64
+    oracle and bit-equal to the NHD run, on the head_dim-128 kernel (one
+    split and many), the generic kernel (head_dim 64, page 32), a wide tree
+    and a short prefix."""
+    gen = torch.Generator().manual_seed(91)
+    kw, split = {}, None
+    if case.startswith("forest16k"):
+        routes, prefix = _routes(gen, 9, 4, share=True), 16384
+        split = 1 if case.endswith("split1") else None
+    elif case == "short61_bf16":
+        routes, prefix, kw = _routes(gen, 4, 3, share=True), 61, dict(dtype=torch.bfloat16)
+    elif case == "d64_ps32":
+        routes, prefix, kw = _routes(gen, 6, 4, share=True), 3000, dict(hq=16, hkv=2, d=64, ps=32)
+    elif case == "wide130_bf16":
+        routes, prefix, kw = _routes(gen, 26, 5, share=False), 5000, dict(dtype=torch.bfloat16)
+    else:
+        routes, prefix = _routes(gen, 3, 4, share=False), 4096
+    c = _build(dev, seed=92, prefix_len=prefix, routes=routes, **kw)
+    _run_and_check(dev, c, split_target=split, layout="NHD")
+    _run_and_check(dev, c, split_target=split, layout="HND")
+    (o_n, l_n), (o_h, l_h) = c["outs"][("NHD", split)], c["outs"][("HND", split)]
+    assert torch.equal(o_n.view(torch.int16), o_h.view(torch.int16)) and torch.equal(l_n, l_h)
+
+
+@pytest.mark.parametrize("prefix_len", [16384, 300])
+def test_hnd_fused_rope_append_matches_nhd(dev, prefix_len):
+    """The fused RoPE + append + attention launch on HND pages writes the
+    same rows (read back as NHD) and returns the same output, bit for bit,
+    as on NHD pages."""
+    ta = pkg("tree_attention")
+    ffv = pkg("flashinfer_full_verify")
+    dtype = torch.float16
+    gen = torch.Generator().manual_seed(prefix_len + 5)
+    routes = _routes(gen, 9, 4, share=True)
+    c = _build(dev, seed=prefix_len + 6, prefix_len=prefix_len, routes=routes, dtype=dtype, spare_pages=9)
+    n, ps, hkv, d, hq = c["n"], c["ps"], c["hkv"], c["d"], c["hq"]
+    q_raw = (torch.randn((n, hq, d), generator=gen) * 2.0).to(dtype).to(dev)
+    k_raw = (torch.randn((n, hkv, d), generator=gen) * 2.0).to(dtype).to(dev)
+    v_new = (torch.randn((n, hkv, d), generator=gen) * 0.1).to(dtype).to(dev)
+    cos, sin = _rope_tables(prefix_len + c["spec"].depths.cpu(), d, dtype)
+    last = ffv.last_page_len(c["kv_len"], ps)
+    results = []
+    for layout in ("NHD", "HND"):
+        kv = (c["kv"] if layout == "NHD" else _hnd(c["kv"])).to(dev)
+        w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(64 << 20, dtype=torch.uint8, device=dev), layout)
+        w.plan(torch.tensor([0, n], dtype=torch.int32, device=dev),
+               torch.tensor([0, c["pages"]], dtype=torch.int32, device=dev), c["order"].to(dev),
+               torch.tensor([last], dtype=torch.int32, device=dev), hq, hkv, d, ps,
+               custom_mask=c["spec"].bool_mask, q_data_type=dtype)
+        out, lse = w.run(q_raw, kv, return_lse=True, append_key_states=k_raw, append_value_states=v_new,
+                         rope_cos_sin=(cos.to(dev), sin.to(dev)))
+        torch.cuda.synchronize()
+        results.append(((kv if layout == "NHD" else kv.permute(0, 1, 3, 2, 4)).cpu(), out.cpu(), lse.cpu()))
+    (kv_a, out_a, lse_a), (kv_b, out_b, lse_b) = results
+    assert torch.equal(kv_a.view(torch.int16), kv_b.contiguous().view(torch.int16))
+    assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)) and torch.equal(lse_a, lse_b)

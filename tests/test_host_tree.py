@@ -103,8 +103,9 @@ def test_plan_argument_validation_without_gpu():
     w = ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "NHD")
     with pytest.raises(RuntimeError, match="HIP device"):
         w.plan(torch.tensor([0, 1]), torch.tensor([0, 1]), torch.tensor([0]), torch.tensor([1]), 4, 2, 64, 16)
+    assert ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "HND").kv_layout == "HND"
     with pytest.raises(NotImplementedError):
-        ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "HND")
+        ta.BatchPrefillWithPagedKVCacheWrapper(torch.empty(16, dtype=torch.uint8), "NDH")
 
 
 def test_cached_tree_window_validated_against_plan():

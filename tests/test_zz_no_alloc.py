@@ -43,7 +43,7 @@ def _noalloc(w, q, kv, out, lse, partial_rows=None):
     es = kv.element_size()
     rc = lib_mod.load().atlas_tree_verify_attn_noalloc(
         lib_mod.ptr(q), q.stride(0), q.stride(1), lib_mod.ptr(kv), kv.stride(0) * es, kv.stride(1) * es,
-        kv.stride(2) * es, lib_mod.ptr(plan.qo_indptr), lib_mod.ptr(plan.kv_indptr), lib_mod.ptr(plan.kv_indices),
+        kv.stride(2) * es, kv.stride(3) * es, lib_mod.ptr(plan.qo_indptr), lib_mod.ptr(plan.kv_indptr), lib_mod.ptr(plan.kv_indices),
         plan.device_view(plan.kv_len_offset), plan.mask_mode, lib_mod.ptr(plan.tree_mask),
         plan.device_view(plan.col_offset), plan.mask_words, plan.device_view(plan.work_offset), plan.num_work,
         lib_mod.ptr(plan.page_windows) if plan.page_windows is not None else None,
