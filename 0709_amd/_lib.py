@@ -142,12 +142,30 @@ _SIGNATURES: dict[str, list] = {
     "atlas_candidate_select": [
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp,
     ],
+    "atlas_tree_spec_bytes": [ctypes.c_int32, ctypes.c_int32, _c_i64, ctypes.c_int32],
+    "atlas_route_select": [
+        _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp,
+        ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_double, _c_i64, _vp, _vp, _vp, _vp,
+    ],
+    "atlas_tree_spec_build": [
+        _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _c_i64, ctypes.c_int32, _vp, _c_i64, _vp, _vp, _vp,
+    ],
 }
 # entry points whose return value is not an int status
 _RESTYPES: dict[str, type] = {
     "atlas_frontier_workspace_bytes": ctypes.c_int64,
     "atlas_gather_logprobs_workspace_bytes": ctypes.c_int64,
+    "atlas_tree_spec_bytes": ctypes.c_int64,
 }
+
+SELECT_MAX_ROUTES = 64
+SELECT_MAX_DEPTH = 16
+SELECT_MAX_ENTRIES = 512
+SELECT_TARGET_BEST = 0
+SELECT_FIRST_ROUTE = 1
+ROUND_NONE = 0
+ROUND_F16 = 1
+ROUND_BF16 = 2
 
 FRONTIER_NONE = -1
 FRONTIER_ORDER = 0
@@ -274,6 +292,8 @@ class HostStaging:
         rc = _hip_runtime().hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(self.nbytes), ctypes.c_uint(1))
         if rc != 0 or not p.value:
             raise RuntimeError(f"hipHostMalloc of {self.nbytes} staging bytes failed ({rc})")
+        self.base = p.value
+        self.memcpy = _hip_runtime().hipMemcpyAsync
         buf = (ctypes.c_uint8 * self.nbytes).from_address(p.value)
         self.host = torch.frombuffer(buf, dtype=torch.uint8)
         self.host_np = self.host.numpy()
@@ -338,9 +358,12 @@ class HostStaging:
             self.host_np[start : start + nbytes] = src
             if out is None:
                 out = dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            dst.copy_(self.host[start : start + nbytes], non_blocking=True)
-            self.users[q].add((idx, _RAW_STREAM(idx) if _RAW_STREAM is not None else
-                               torch.cuda.current_stream(idx).cuda_stream))
+            raw = _RAW_STREAM(idx) if _RAW_STREAM is not None else torch.cuda.current_stream(idx).cuda_stream
+            # queued on the current stream straight from the pinned bytes
+            rc = self.memcpy(dst.data_ptr(), self.base + start, nbytes, _HIP_MEMCPY_H2D, raw)
+            if rc != 0:
+                raise RuntimeError(f"hipMemcpyAsync of {nbytes} staged bytes failed ({rc})")
+            self.users[q].add((idx, raw))
             self.pos = (start + nbytes + 63) & ~63
         return out
 
@@ -352,6 +375,7 @@ class HostStaging:
 
 
 _HIP = None
+_HIP_MEMCPY_H2D = 1  # hipMemcpyHostToDevice
 _STAGING: HostStaging | None = None
 
 
@@ -363,6 +387,9 @@ def _hip_runtime() -> ctypes.CDLL:
         hip = ctypes.CDLL("libamdhip64.so.7")
         hip.hipHostMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t, ctypes.c_uint]
         hip.hipHostMalloc.restype = ctypes.c_int
+        hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
+                                       ctypes.c_void_p]
+        hip.hipMemcpyAsync.restype = ctypes.c_int
         _HIP = hip
     return _HIP
 

@@ -34,6 +34,7 @@ windows, logit soft-capping, and k_scale / v_scale other than 1.
 
 from __future__ import annotations
 
+import dataclasses
 import math
 
 import torch
@@ -339,7 +340,9 @@ class BatchDecodeWithPagedKVCacheWrapper:
         if plan is None:
             raise RuntimeError("plan() must be called before forward()")
         if sm_scale is not None:
-            plan.sm_scale = float(sm_scale)
+            # a copy: a later plan() of the same shape may hand back the
+            # cached plan object, which keeps the plan's own scale
+            self._prefill._plan = dataclasses.replace(plan, sm_scale=float(sm_scale))
         return self.run(q, paged_kv_cache, q_scale=q_scale, k_scale=k_scale, v_scale=v_scale)
 
     def end_forward(self) -> None:

@@ -15,6 +15,7 @@ reference's tree / paged-KV functions.  Differences are in where the work runs:
 
 from __future__ import annotations
 
+import threading
 from dataclasses import dataclass, field
 from typing import Sequence
 
@@ -221,53 +222,64 @@ def with_host_values(t: torch.Tensor, values: Sequence[int]) -> torch.Tensor:
     return t
 
 
-def _tree_spec(
-    *,
-    token_ids: list[int],
-    parent_indices: list[int],
-    depths: list[int],
-    prefix_len: int,
-    page_size: int,
-    device: torch.device | str,
-) -> TreeSpec:
-    node_count = len(token_ids)
-    prefix_len = int(prefix_len)
-    kv_len = prefix_len + node_count
-    total_pages = ceil_div(kv_len, page_size)
-    bits = ancestor_bitmasks(parent_indices)
-    device = torch.device(device)
-    last = last_page_len(kv_len, page_size)
-    # Everything small goes to the device in one copy of one host buffer:
-    # token ids and depths (int64), the ancestor bitmasks (int64, up to 64
-    # nodes), qo/kv indptr, last page length and the identity page table
-    # (int32), then the tree block of the mask (bool).
-    compact = node_count <= 64
-    # wide trees: one visibility word per 64-key tile of the tree region
-    tiles = _tile_words(bits, prefix_len, kv_len) if 64 < node_count <= _MAX_TILE_NODES else None
-    tok_dep = (np.asarray(token_ids, dtype=np.int64), np.asarray(depths, dtype=np.int64))
-    if compact:
-        words = np.asarray(bits, dtype=np.uint64)  # below 2**64 for up to 64 nodes
-        i64 = np.concatenate((*tok_dep, words.view(np.int64)))
-        # row i, column j: bit j of word i
-        block = np.unpackbits(words.view(np.uint8).reshape(node_count, 8), axis=1,
-                              bitorder="little")[:, :node_count]
-    else:
-        i64 = np.concatenate((*tok_dep, tiles.reshape(-1).view(np.int64) if tiles is not None
-                              else np.zeros(0, dtype=np.int64)))
-        block = np.asarray([[(b >> j) & 1 for j in range(node_count)] for b in bits], dtype=np.uint8)
-    # [qo_indptr 0 n | kv_indptr 0 pages | last | identity page table | pad to 8 bytes]
-    i32 = np.zeros(5 + total_pages + (1 + total_pages) % 2, dtype=np.int32)
-    i32[:5] = (0, node_count, 0, total_pages, last)
-    i32[5 : 5 + total_pages] = np.arange(total_pages, dtype=np.int32)
-    host = np.concatenate((i64.view(np.uint8), i32.view(np.uint8), block.reshape(-1)))
+class _SpecScratch(threading.local):
+    """Per-thread host buffers of the native tree builder, grown on demand
+    (their contents are copied out before a build returns)."""
+
+    def __init__(self):
+        self.out = np.empty(0, dtype=np.uint8)
+        self.parents = np.empty(0, dtype=np.int32)
+        self.routes = np.empty(0, dtype=np.int32)
+        self.info = np.zeros(8, dtype=np.int64)
+        self.ptrs = (0, 0, 0, self.info.ctypes.data)
+
+    def reserve(self, nbytes: int, nodes: int) -> None:
+        if self.out.nbytes >= nbytes and self.parents.size >= nodes:
+            return
+        if self.out.nbytes < nbytes:
+            self.out = np.empty(max(nbytes, 2 * self.out.nbytes), dtype=np.uint8)
+        if self.parents.size < nodes:
+            self.parents = np.empty(max(nodes, 2 * self.parents.size), dtype=np.int32)
+            self.routes = np.empty_like(self.parents)
+        self.ptrs = (self.out.ctypes.data, self.parents.ctypes.data, self.routes.ctypes.data, self.ptrs[3])
+
+
+_SCRATCH = _SpecScratch()
+
+
+def _native_tree_spec(paths, *, prefix_len: int, page_size: int, device, dedup: bool):
+    """The spec of ``paths`` from the library's host builder
+    (``atlas_tree_spec_build``: trie, ancestor sets, packed upload buffer in
+    one call) and, for ``dedup``, the route -> node paths."""
+    if isinstance(paths, (torch.Tensor, np.ndarray)):
+        paths = paths.tolist()
+    depth = _validate_paths(paths)
+    arr = np.asarray(paths, dtype=np.int64)
+    k = int(arr.shape[0])
+    prefix_len, page_size = int(prefix_len), int(page_size)
+    lib = _lib.load()
+    need = lib.atlas_tree_spec_bytes(k, depth, prefix_len, page_size)
+    if need < 0:
+        raise ValueError(f"invalid tree shape: {k} paths of depth {depth}, prefix_len {prefix_len}, "
+                         f"page_size {page_size}")
+    sc = _SCRATCH
+    sc.reserve(need, k * depth)
+    out_p, par_p, rt_p, info_p = sc.ptrs
+    rc = lib.atlas_tree_spec_build(arr.ctypes.data, k, depth, 1 if dedup else 0, prefix_len, page_size, out_p,
+                                   sc.out.nbytes, par_p, rt_p, info_p)
+    _lib.check(rc, "atlas_tree_spec_build")
+    n, kv_len, total_pages, last, n_words, tiles, n32, nbytes = sc.info.tolist()
+    parents = sc.parents[:n].tolist()
+    route_nodes = sc.routes[: k * depth].reshape(k, depth).tolist() if dedup else None
     # Normal tensors even under torch.inference_mode (the Target verify runs
     # in it): their version counters let a plan trust the attached host
     # values only while the tensors are unchanged.
     with torch.inference_mode(False):
-        return _tree_spec_tensors(host, i64, i32, node_count=node_count, kv_len=kv_len, total_pages=total_pages,
-                                  last=last, prefix_len=prefix_len, compact=compact, device=device,
-                                  parent_indices=parent_indices,
-                                  tile_shape=None if tiles is None else tiles.shape)
+        spec = _tree_spec_tensors(sc.out[:nbytes], 2 * n + n_words, n32, node_count=n, kv_len=kv_len,
+                                  total_pages=total_pages, last=last, prefix_len=prefix_len, compact=n <= 64,
+                                  device=torch.device(device), parent_indices=parents,
+                                  tile_shape=(n, tiles) if tiles else None)
+    return spec, route_nodes
 
 
 _TRUE: dict = {}
@@ -281,39 +293,19 @@ def _true(device: torch.device) -> torch.Tensor:
     return t
 
 
-# Largest tree whose per-tile mask words the builder prepares on the host
-# (larger trees: the plan derives them from the dense mask).
-_MAX_TILE_NODES = 1024
-
-
-def _tile_words(bits: Sequence[int], prefix_len: int, kv_len: int) -> np.ndarray:
-    """[nodes, tiles] uint64: for tiles prefix_len // 64 .. (kv_len - 1) // 64,
-    bit b of word j is the visibility of key 64 (prefix_len // 64 + j) + b to
-    the node: prefix keys visible, tree key prefix_len + c iff bit c of the
-    node's ancestor bitmask."""
-    t0 = prefix_len // 64
-    ntiles = (kv_len - 1) // 64 - t0 + 1
-    low = prefix_len - 64 * t0
-    out = np.zeros((len(bits), ntiles), dtype=np.uint64)
-    full = (1 << 64) - 1
-    for i, b in enumerate(bits):
-        vis = (int(b) << low) | ((1 << low) - 1)
-        for j in range(ntiles):
-            out[i, j] = (vis >> (64 * j)) & full
-    return out
-
-
-def _tree_spec_tensors(host, i64, i32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
+def _tree_spec_tensors(host, n64, n32, *, node_count, kv_len, total_pages, last, prefix_len, compact, device,
                        parent_indices, tile_shape=None) -> TreeSpec:
+    """The spec's tensors as views of one device copy of ``host``: ``n64``
+    int64 (token ids, depths, mask words), ``n32`` int32 (indptrs, last page
+    length, page table, pad), then the n x n tree block of the mask."""
     if device.type == "cuda":
         # through pinned staging, so the copy is queued without waiting for the device
         buf = _lib.staging().upload(host, device)
     else:
-        buf = torch.from_numpy(host).to(device)
-    n64 = len(i64)
+        buf = torch.from_numpy(host.copy()).to(device)
     nb = 8 * node_count
     (tok_b, dep_b, words_b, qo_b, kvp_b, last_b, idx_b, _, block_b) = buf.split(
-        [nb, nb, 8 * n64 - 2 * nb, 8, 8, 4, 4 * total_pages, 4 * len(i32) - 20 - 4 * total_pages,
+        [nb, nb, 8 * n64 - 2 * nb, 8, 8, 4, 4 * total_pages, 4 * n32 - 20 - 4 * total_pages,
          node_count * node_count])
     flat_token_ids = tok_b.view(torch.int64)
     depths_t = dep_b.view(torch.int64)
@@ -362,9 +354,7 @@ def build_tree_spec_from_paths(
     device: torch.device | str,
 ) -> TreeSpec:
     """Undeduplicated tree (``flashinfer_full_verify.py:655-701``)."""
-    tokens, parents, depths = _path_tree_lists(paths)
-    return _tree_spec(token_ids=tokens, parent_indices=parents, depths=depths, prefix_len=prefix_len,
-                      page_size=page_size, device=device)
+    return _native_tree_spec(paths, prefix_len=prefix_len, page_size=page_size, device=device, dedup=False)[0]
 
 
 def build_deduplicated_tree_spec_from_paths(
@@ -376,10 +366,7 @@ def build_deduplicated_tree_spec_from_paths(
 ) -> tuple[TreeSpec, list[list[int]]]:
     """Deduplicated tree and its route -> node paths
     (``flashinfer_full_verify.py:704-739``)."""
-    tokens, parents, depths, route_nodes = _dedup_tree_lists(paths)
-    spec = _tree_spec(token_ids=tokens, parent_indices=parents, depths=depths, prefix_len=prefix_len,
-                      page_size=page_size, device=device)
-    return spec, route_nodes
+    return _native_tree_spec(paths, prefix_len=prefix_len, page_size=page_size, device=device, dedup=True)
 
 
 def prefix_layer_to_paged_kv(

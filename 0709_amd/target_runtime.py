@@ -21,6 +21,7 @@ way ``flashinfer_full_verify.run_flashinfer_full_verify`` does (``:1182-1231``).
 
 from __future__ import annotations
 
+import ctypes
 import hashlib
 import json
 import math
@@ -77,11 +78,12 @@ def verify_payload_from_mapping(item: dict) -> VerifyRoutePayload:
 
 
 def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Sequence[int],
-                          extra_logits: torch.Tensor | None = None) -> torch.Tensor:
+                          extra_logits: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """fp32 ``log_softmax(logits[row])[token]`` for each (row, token) pair,
     computed on the device in one launch.  ``logits``: [rows, vocab] or [vocab].
     With ``extra_logits`` ([rows2, vocab] or [vocab], same dtype and vocab),
-    row indices ``rows .. rows + rows2 - 1`` name its rows, in the same launch."""
+    row indices ``rows .. rows + rows2 - 1`` name its rows, in the same launch.
+    ``out``: a contiguous fp32 device tensor of len(rows) values to write."""
     device = _lib.require_device(logits, what="route scoring")
     lg = logits.reshape(1, -1) if logits.ndim == 1 else logits
     if lg.ndim != 2 or lg.stride(-1) != 1:
@@ -93,7 +95,10 @@ def gather_token_logprobs(logits: torch.Tensor, rows: Sequence[int], tokens: Seq
         if lg2.ndim != 2 or lg2.stride(-1) != 1 or int(lg2.shape[1]) != int(lg.shape[1]) or lg2.dtype != lg.dtype:
             raise ValueError("extra_logits must be [rows, vocab] rows of the same vocabulary and dtype")
     n = len(rows)
-    out = torch.empty(n, dtype=torch.float32, device=device)
+    if out is None:
+        out = torch.empty(n, dtype=torch.float32, device=device)
+    elif out.dtype != torch.float32 or out.device != device or not out.is_contiguous() or int(out.numel()) != n:
+        raise ValueError(f"out must be a contiguous float32 tensor of {n} values on {device}")
     if n == 0:
         return out
     if len(tokens) != n:
@@ -260,9 +265,39 @@ def run_full_ar_decode(*, model, wrappers, state: FullDecodeState, prefix_len: i
     return logits
 
 
+def _scoring_pairs(paths, route_to_node_paths, n_verify: int) -> tuple[list[int], list[int]]:
+    """(row, token) pairs of the route scoring, in the order the selection
+    launch reads them: every route's first token (the prefix logits, row
+    ``n_verify``), then each route's tokens t > 0 (the verify row of its node
+    t - 1)."""
+    rows = [n_verify] * len(paths)
+    toks = [int(path[0]) for path in paths]
+    for path, nodes in zip(paths, route_to_node_paths):
+        for off in range(1, len(path)):
+            rows.append(int(nodes[off - 1]))
+            toks.append(int(path[off]))
+    return rows, toks
+
+
+def _route_score(**fields) -> TargetRouteScore:
+    """``TargetRouteScore(**fields)`` for a keyword set naming every field,
+    with the fields set through the instance dict instead of the frozen
+    dataclass's per-field ``object.__setattr__`` (a verify step waits on the
+    loop that builds one per route)."""
+    score = object.__new__(TargetRouteScore)
+    score.__dict__.update(fields)
+    return score
+
+
 class DirectFlashInferMaskedTreeVerifyBackend:
     """Persistent Target: committed prefix KV, masked tree verify, route
     scoring / selection and in-place commit of the selected path."""
+
+    # Select target_best / first_route routes on the device and queue the
+    # commit behind the scoring (the host still selects from the read-back
+    # scores and refuses a disagreement); False keeps selection and commit
+    # launch on the host.
+    device_route_selection: bool = True
 
     def __init__(
         self,
@@ -449,13 +484,34 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         plan_prefill_wrapper(self._wrapper, tree, args=self.config, config=self.model.config, dtype=self.dtype)
         logits = run_full_verify(model=self.model, wrapper=self._wrapper, state=state, prefix_len=len(prefix),
                                  page_size=self.config.page_size, fused=self.fused_verify_step)
-        scores = self._score_routes(routes=routes, paths=paths, prefix_logits=self._prefix_logits[0],
-                                    verify_logits=logits, route_to_node_paths=route_nodes)
+        device_inputs = self._device_selection_inputs(routes, paths, route_nodes) if logits.is_cuda else None
+        if selected_path_max_tokens is not None and int(selected_path_max_tokens) <= 0:
+            device_inputs = None  # the host path raises after the fallback decision, as the reference does
+        if device_inputs is not None:
+            # every route's committed length (truncation), so the device
+            # commits the selected one without a host round trip
+            commit_lens = [len(self._truncate_selected_path(token_ids=p, node_ids=nd, max_tokens=selected_path_max_tokens,
+                                                            eos_token_id=eos_token_id)[0])
+                           for p, nd in zip(paths, route_nodes)]
+            scores, device_idx, device_count = self._score_select_commit(
+                routes=routes, paths=paths, prefix_logits=self._prefix_logits[0], verify_logits=logits,
+                route_to_node_paths=route_nodes, inputs=device_inputs, commit_lens=commit_lens,
+                prefix_len=len(prefix), layers=self._paged_prefix_kv, kv_layout=self.kv_layout)
+        else:
+            scores = self._score_routes(routes=routes, paths=paths, prefix_logits=self._prefix_logits[0],
+                                        verify_logits=logits, route_to_node_paths=route_nodes)
         best = max(scores, key=lambda s: (self._selection_score(s), s.draft_path_logprob, -s.route_id))
         selected, sampling_meta = self._select_route_with_metadata(
             scores, route_sampling_seed=route_sampling_seed, route_sampling_round=route_sampling_round
         )
         reason = self._fallback_reason(selected)
+        if device_inputs is not None:
+            host_idx = next(i for i, r in enumerate(routes) if int(r.route_id) == int(selected.route_id))
+            host_count = 0 if reason is not None else commit_lens[host_idx]
+            if (host_idx, host_count) != (device_idx, device_count):
+                raise RuntimeError(
+                    "device route selection disagrees with the host selection: device route index "
+                    f"{device_idx} ({device_count} tokens), host {host_idx} ({host_count} tokens)")
         # the key order of target_runtime.py:235-252 (later keys override the
         # runtime metadata's)
         common = {
@@ -506,7 +562,8 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         idx = next(i for i, r in enumerate(routes) if int(r.route_id) == int(selected.route_id))
         path, nodes = self._truncate_selected_path(token_ids=paths[idx], node_ids=route_nodes[idx],
                                                    max_tokens=selected_path_max_tokens, eos_token_id=eos_token_id)
-        self._commit_selected_path(token_ids=path, node_ids=nodes, verify_logits=logits)
+        self._commit_selected_path(token_ids=path, node_ids=nodes, verify_logits=logits,
+                                   launch=device_inputs is None)
         return TargetVerifyResult(
             selected_route_id=selected.route_id,
             scores=scores,
@@ -759,20 +816,25 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         # One launch for both logits tensors: the verify rows, then the
         # prefix logits as row n_verify.
         vl = verify_logits.reshape(1, -1) if verify_logits.ndim == 1 else verify_logits
-        n_verify = int(vl.shape[0])
-        rows, toks = [], []
-        for path in paths:
-            rows.append(n_verify)
-            toks.append(int(path[0]))
-        for path, nodes in zip(paths, route_to_node_paths):
-            for off in range(1, len(path)):
-                rows.append(int(nodes[off - 1]))
-                toks.append(int(path[off]))
+        rows, toks = _scoring_pairs(paths, route_to_node_paths, int(vl.shape[0]))
         values = gather_token_logprobs(vl, rows, toks, extra_logits=prefix_logits).cpu().numpy()
-        if self.match_logits_dtype_rounding and verify_logits.dtype == torch.float16:
+        return self._route_scores_from_values(routes, paths, values, verify_logits.dtype)
+
+    def _rounding_code(self, dtype: torch.dtype) -> int:
+        if self.match_logits_dtype_rounding and dtype == torch.float16:
+            return _lib.ROUND_F16
+        if self.match_logits_dtype_rounding and dtype == torch.bfloat16:
+            return _lib.ROUND_BF16
+        return _lib.ROUND_NONE
+
+    def _route_scores_from_values(self, routes, paths, values: np.ndarray, dtype: torch.dtype):
+        """The routes' TargetRouteScores from the scoring launch's fp32 values
+        (every route's first token, then each route's other tokens)."""
+        rounding = self._rounding_code(dtype)
+        if rounding == _lib.ROUND_F16:
             # The reference reads log_softmax outputs in the logits dtype.
             values = values.astype(np.float16).astype(np.float32)
-        elif self.match_logits_dtype_rounding and verify_logits.dtype == torch.bfloat16:
+        elif rounding == _lib.ROUND_BF16:
             values = torch.from_numpy(values).to(torch.bfloat16).float().numpy()
         vals = values.tolist()
         n_routes = len(paths)
@@ -780,18 +842,110 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         for i, (route, path) in enumerate(zip(routes, paths)):
             d = len(path)
             rest = max(d - 1, 0)
-            lps = [vals[i], *vals[k : k + rest]]
+            lps = (vals[i], *vals[k : k + rest])
             k += rest
             target = sum(lps)
             weights = self._weights_for_depth(d)
             sel = target if weights is None else sum(w * v for w, v in zip(weights, lps))
-            scores.append(TargetRouteScore(
+            scores.append(_route_score(
                 route_id=int(route.route_id), token_ids=tuple(map(int, path)), target_logprob=target,
-                draft_logprob=float(route.draft_logprob), token_logprobs=tuple(lps), first_token_logprob=lps[0],
+                draft_logprob=float(route.draft_logprob), token_logprobs=lps, first_token_logprob=lps[0],
                 selection_score=sel, score_weights=() if weights is None else tuple(weights),
                 draft_token_logprobs=tuple(map(float, route.draft_token_logprobs)),
             ))
         return scores
+
+    # ------------------------------------------------------------ device selection
+    def _device_selection_inputs(self, routes, paths, route_to_node_paths):
+        """The host inputs of the device selection (policy, weights, draft
+        path log-probs, route ids, node table), or None when this verify's
+        selection stays on the host: target_sample, routes or depth beyond
+        the selection launch's limits, or a NaN draft log-prob (Python's
+        tuple comparison treats one NaN object as equal to itself)."""
+        if not self.device_route_selection:
+            return None
+        policy = {"target_best": _lib.SELECT_TARGET_BEST, "first_route": _lib.SELECT_FIRST_ROUTE}.get(
+            self.route_selection_policy)
+        k, d = len(paths), len(paths[0])
+        if policy is None or k > _lib.SELECT_MAX_ROUTES or d > _lib.SELECT_MAX_DEPTH or \
+                k * d > _lib.SELECT_MAX_ENTRIES:
+            return None
+        weights = self._weights_for_depth(d)
+        if weights is not None and len(weights) != d:
+            return None
+        nodes = [int(x) for path_nodes in route_to_node_paths for x in path_nodes]
+        if len(nodes) != k * d or max(nodes) > 32767:
+            return None
+        draft = [float(sum(map(float, r.draft_token_logprobs))) if r.draft_token_logprobs else float(r.draft_logprob)
+                 for r in routes]
+        if any(math.isnan(x) for x in draft):
+            return None
+        return policy, weights, draft, [int(r.route_id) for r in routes], nodes
+
+    def _score_select_commit(self, *, routes, paths, prefix_logits, verify_logits, route_to_node_paths, inputs,
+                             commit_lens, prefix_len, layers, kv_indptr=None, kv_indices=None, kv_layout="NHD",
+                             before_commit=None, then=None):
+        """Scoring, route selection and the commit, queued in stream order
+        with one device-to-host copy: the scoring launch, the selection launch
+        (``atlas_route_select``: the selected route and its commit positions,
+        or none on a fallback), the copy of the values and of the selection to
+        pinned memory, the commit of the selected route (``commit_lens[r]``
+        tokens of route r; rows past the count copy onto themselves) and
+        ``then()``; then the host waits for the copy alone.  ``before_commit``
+        and ``then`` (optional) queue the caller's own work around the commit
+        launch.  Returns the routes' scores and the device's (route index,
+        committed count)."""
+        policy, weights, draft, route_ids, nodes = inputs
+        vl = verify_logits.reshape(1, -1) if verify_logits.ndim == 1 else verify_logits
+        device = vl.device
+        k, d = len(paths), len(paths[0])
+        rows, toks = _scoring_pairs(paths, route_to_node_paths, int(vl.shape[0]))
+        n = len(rows)
+        # values, then the selection result (two int32) in one buffer, so one copy brings both back
+        buf = torch.empty(n + 2, dtype=torch.float32, device=device)
+        gather_token_logprobs(vl, rows, toks, extra_logits=prefix_logits, out=buf[:n])
+        pos = torch.empty(2 * d, dtype=torch.int64, device=device)
+        c_double, c_i64, c_i32 = ctypes.c_double, ctypes.c_int64, ctypes.c_int32
+        thr_p, thr_f = self.fallback_threshold, self.first_token_threshold
+        rc = _lib.load().atlas_route_select(
+            _lib.ptr(buf), k, d, policy, self._rounding_code(verify_logits.dtype),
+            (c_double * d)(*weights) if weights is not None else None, 0 if weights is None else d,
+            (c_double * k)(*draft), (c_i64 * k)(*route_ids), (c_i32 * k)(*commit_lens), (c_i32 * (k * d))(*nodes),
+            int(thr_p is not None), float(thr_p or 0.0), int(thr_f is not None), float(thr_f or 0.0), int(prefix_len),
+            _lib.ptr(pos), _lib.ptr(pos[d:]), _lib.ptr(buf[n:]), _lib.stream_of(device))
+        _lib.check(rc, "atlas_route_select")
+        host = self._readback_buffer(n + 2)
+        host.copy_(buf, non_blocking=True)
+        done = self._readback_event()
+        done.record()
+        # the commit hazards of every route's committed rows, decided on the host
+        staging = any(
+            kv_ops.commit_positions_need_staging([prefix_len + x for x in route_to_node_paths[r][:commit_lens[r]]],
+                                                 range(prefix_len, prefix_len + commit_lens[r]))
+            for r in range(k))
+        if before_commit is not None:
+            before_commit()
+        kv_ops.commit_paged(layers, pos[:d], pos[d:], kv_indptr=kv_indptr, kv_indices=kv_indices,
+                            needs_staging=staging, kv_layout=kv_layout)
+        if then is not None:
+            then()
+        done.synchronize()
+        values = host[:n].numpy()
+        chosen, count = host[n:].view(torch.int32).tolist()
+        return self._route_scores_from_values(routes, paths, values, verify_logits.dtype), chosen, count
+
+    def _readback_buffer(self, n: int) -> torch.Tensor:
+        buf = getattr(self, "_readback", None)
+        if buf is None or int(buf.numel()) < n:
+            buf = torch.empty(max(n, 256), dtype=torch.float32, pin_memory=True)
+            self._readback = buf
+        return buf[:n]
+
+    def _readback_event(self) -> torch.cuda.Event:
+        ev = getattr(self, "_readback_done", None)
+        if ev is None:
+            ev = self._readback_done = torch.cuda.Event()
+        return ev
 
     # ------------------------------------------------------------ fallback AR
     def _generate_fallback_ar(self, *, max_tokens: int, eos_token_id: int | None) -> list[int]:
@@ -870,18 +1024,20 @@ class DirectFlashInferMaskedTreeVerifyBackend:
             grown.append(expanded)
         self._paged_prefix_kv = grown
 
-    def _commit_selected_path(self, *, token_ids, node_ids, verify_logits) -> None:
+    def _commit_selected_path(self, *, token_ids, node_ids, verify_logits, launch: bool = True) -> None:
         """Compact the selected nodes' KV into the committed prefix (every
         layer, one launch), extend the prefix and keep the last node's logits
-        as the next prefix logits (``target_runtime.py:873-920``)."""
+        as the next prefix logits (``target_runtime.py:873-920``).
+        ``launch=False``: the device selection already queued the copy."""
         if self._paged_prefix_kv is None:
             raise RuntimeError("target paged prefix KV is not initialized")
         if len(token_ids) != len(node_ids) or not node_ids:
             raise ValueError("selected path tokens and node ids must have equal non-zero length")
-        prefix_len = len(self.prefix_token_ids)
-        src = [prefix_len + int(n) for n in node_ids]
-        dst = list(range(prefix_len, prefix_len + len(node_ids)))
-        kv_ops.commit_paged(self._paged_prefix_kv, src, dst, kv_layout=self.kv_layout)
+        if launch:
+            prefix_len = len(self.prefix_token_ids)
+            src = [prefix_len + int(n) for n in node_ids]
+            dst = list(range(prefix_len, prefix_len + len(node_ids)))
+            kv_ops.commit_paged(self._paged_prefix_kv, src, dst, kv_layout=self.kv_layout)
         self.prefix_token_ids = (*self.prefix_token_ids, *(int(t) for t in token_ids))
         self._prefix_logits = verify_logits[int(node_ids[-1])].detach().unsqueeze(0)
         self._committed_verify_rounds += 1

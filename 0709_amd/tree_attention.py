@@ -301,6 +301,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         self.split_granule_keys: int | None = None
         self._decomp_cache: tuple | None = None
         self._meta_uploaded: tuple | None = None
+        self._plan_cache: tuple | None = None
         self._meta_buf: torch.Tensor | None = None
         self._indices_buf: torch.Tensor | None = None
         self._bits_buf: torch.Tensor | None = None
@@ -555,7 +556,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
         # holds is not uploaded again.
         meta = self._persistent("_meta_buf", len(meta_np), torch.int32)
         if self._meta_uploaded is None or self._meta_uploaded[0] is not meta or \
-                not np.array_equal(self._meta_uploaded[1], meta_np):
+                (self._meta_uploaded[1] is not meta_np and not np.array_equal(self._meta_uploaded[1], meta_np)):
             if device.type == "cuda":
                 _lib.staging().upload(meta_np, device, out=meta[: len(meta_np)])
             else:
@@ -586,6 +587,15 @@ class BatchPrefillWithPagedKVCacheWrapper:
             _lib.stream_of(device))
         _lib.check(rc, "atlas_attn_plan_install")
 
+        # The same work list over the same buffers and arguments is the same
+        # plan object (kv_lens and qo_lens are part of the work list's key).
+        plan_key = (dec, meta, indices, bits_buf, windows, sm_scale, q_dtype, kv_dtype, mask_mode, mask_words,
+                    batch, hq, hkv, d, ps)
+        cached = self._plan_cache
+        if cached is not None and len(cached[0]) == len(plan_key) and \
+                all(a is b or (type(a) in (int, float, str) and a == b) for a, b in zip(cached[0], plan_key)):
+            self._plan = cached[1]
+            return
         self._plan = AttentionPlan(
             batch=batch, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=ps,
             sm_scale=float(sm_scale) if sm_scale is not None else 1.0 / math.sqrt(d),
@@ -598,6 +608,7 @@ class BatchPrefillWithPagedKVCacheWrapper:
             kv_lens=kv_lens, qo_lens=qo_lens, tiles_per_split=dec["tiles_per_split"], page_windows=windows,
             fused_append=dec["fused_append"],
         )
+        self._plan_cache = (plan_key, self._plan)
 
     @property
     def kv_layout(self) -> str:

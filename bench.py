@@ -139,6 +139,14 @@ class HeadlineStep:
         all_pos = torch.arange(self.kv_len)
         self.all_slots = (idx[all_pos // page_size] * page_size + all_pos % page_size).to(dev)
         self.live_path = (self.lib.SlotPath * 1)()
+        # the Target runtime's scoring and selection (target_best, logits-dtype
+        # rounding, no thresholds), without a model
+        self.backend = object.__new__(self.tr.DirectFlashInferMaskedTreeVerifyBackend)
+        self.backend.score_weights = None
+        self.backend.route_selection_policy = "target_best"
+        self.backend.match_logits_dtype_rounding = True
+        self.backend.fallback_threshold = None
+        self.backend.first_token_threshold = None
         self.live_path[0].slots = self.all_slots.data_ptr()
         self.fwd_events = []
         self.commit_events = []
@@ -234,25 +242,18 @@ class HeadlineStep:
         rc = lib.load().atlas_mark_pages(lib.ptr(self.owned), self.pool_pages, lib.ptr(self.all_slots),
                                          self.kv_len, self.ps, stream)
         lib.check(rc, "atlas_mark_pages")
-        # scoring + best route
-        backend = object.__new__(self.tr.DirectFlashInferMaskedTreeVerifyBackend)
-        backend.score_weights = None
-        backend.route_selection_policy = "target_best"
-        backend.match_logits_dtype_rounding = True
+        # scoring, the route selection and the commit of the selected route
+        # queued on the device behind the forward, then the prune; the host
+        # waits only for the scores (and the device's choice, checked against
+        # the runtime's host selection)
+        backend = self.backend
         payloads = [self.tr.VerifyRoutePayload(route_id=i, token_ids=r, draft_logprob=0.0)
                     for i, r in enumerate(self.routes)]
-        scores = backend._score_routes(routes=payloads, paths=self.routes, prefix_logits=self.prefix_logits,
-                                       verify_logits=self.verify_logits, route_to_node_paths=route_nodes)
-        best = backend._select_route(scores)
-        nodes = route_nodes[int(best.route_id)]
-        src = [self.prefix_len + x for x in nodes]
-        dst = list(range(self.prefix_len, self.prefix_len + len(nodes)))
-        self._timed(self.commit_events, lambda: self.kv_ops.commit_paged(
-            self.layers, src, dst, kv_indptr=self.kv_indptr, kv_indices=self.kv.kv_indices,
-            kv_layout=self.kv_layout))
+        inputs = backend._device_selection_inputs(payloads, self.routes, route_nodes)
+        depth = len(self.routes[0])
         # the live set: the committed path's page starts and its last slot,
         # sampled inside the prune launch
-        self.live_path[0].len = self.prefix_len + len(nodes)
+        self.live_path[0].len = self.prefix_len + depth
 
         def prune():
             rc = lib.load().atlas_prune_pages_paths(lib.ptr(self.owned), lib.ptr(self.live), self.pool_pages,
@@ -260,10 +261,31 @@ class HeadlineStep:
                                                     lib.ptr(self.free_count), stream)
             lib.check(rc, "atlas_prune_pages_paths")
 
-        self._timed(self.prune_events, prune)
+        commit_mark = [None]
+
+        def before_commit():
+            if self.record:
+                commit_mark[0] = _ev()
+                commit_mark[0].record()
+
+        def then():
+            if self.record:
+                end = _ev()
+                end.record()
+                self.commit_events.append((commit_mark[0], end))
+            self._timed(self.prune_events, prune)
+
+        scores, chosen, count = backend._score_select_commit(
+            routes=payloads, paths=self.routes, prefix_logits=self.prefix_logits, verify_logits=self.verify_logits,
+            route_to_node_paths=route_nodes, inputs=inputs, commit_lens=[depth] * len(self.routes),
+            prefix_len=self.prefix_len, layers=self.layers, kv_indptr=self.kv_indptr, kv_indices=self.kv.kv_indices,
+            kv_layout=self.kv_layout, before_commit=before_commit, then=then)
+        best = backend._select_route(scores)
+        if int(best.route_id) != chosen or count != depth:
+            raise RuntimeError(f"device selection {chosen} ({count} tokens) differs from the host's {best.route_id}")
         # the pruned-page count stays on the device: nothing in the step waits
         # for it (the caller reads it once, after the timed steps)
-        return int(best.route_id), len(nodes), self.free_count
+        return int(best.route_id), count, self.free_count
 
     def attention_only(self, replays, graph=None):
         """ms per layer of back-to-back replays of the attention graph (or of

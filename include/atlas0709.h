@@ -188,6 +188,36 @@ int atlas_attn_page_windows(const atlas_attn_work_t* work_dev, int num_work,
                             const int32_t* kv_indices_dev, int page_size, int32_t* window_dev,
                             void* stream);
 
+/* Host-side tree specification (no device work).  paths_host holds
+ * num_paths routes of `depth` token ids each, row-major.  dedup != 0 builds
+ * the prefix trie (one node per unique token prefix, numbered in creation
+ * order, route by route, depth by depth), dedup == 0 one node per path
+ * position.  Writes parents_host[node] (-1 for a root; capacity num_paths *
+ * depth), route_nodes_host[route * depth + d] (may be NULL when dedup == 0)
+ * and one packed buffer at out_host, in this order:
+ *   token ids (int64, n), depths (int64, n),
+ *   mask words (int64): n <= 64: word i = node i's ancestor-or-self bits;
+ *     64 < n <= ATLAS_TREE_TILE_MAX_NODES: per node, one word per 64-key tile
+ *     from prefix_len / 64 to (kv_len - 1) / 64 (ATLAS_MASK_TREE's wide
+ *     layout); larger trees: none,
+ *   int32: qo indptr {0, n}, kv indptr {0, pages}, last page length, the
+ *     identity page table 0 .. pages - 1, a zero pad to an even count,
+ *   the tree block of the dense mask: n x n bytes, [i][j] = 1 iff node j is
+ *     an ancestor-or-self of node i.
+ * info_host[0..7] = n, kv_len (prefix_len + n), pages, last page length,
+ * mask words, words per node (tiles; 0 when n <= 64 or none), int32 count,
+ * bytes written.  atlas_tree_spec_bytes() bounds the buffer for any paths of
+ * that shape (-1 for an invalid shape); a smaller out_bytes than the tree
+ * needs is refused with ATLAS_EINVAL.  Replaces the host work of
+ * build_path_tree_tokens_from_paths, build_deduplicated_path_tree_tokens and
+ * build_(deduplicated_)tree_spec_from_paths
+ * (src/atlas_0709/flashinfer_full_verify.py:541-616, :655-739). */
+#define ATLAS_TREE_TILE_MAX_NODES 1024
+int64_t atlas_tree_spec_bytes(int32_t num_paths, int32_t depth, int64_t prefix_len, int32_t page_size);
+int atlas_tree_spec_build(const int64_t* paths_host, int32_t num_paths, int32_t depth, int32_t dedup,
+                          int64_t prefix_len, int32_t page_size, uint8_t* out_host, int64_t out_bytes,
+                          int32_t* parents_host, int32_t* route_nodes_host, int64_t* info_host);
+
 /* Mask modes. */
 #define ATLAS_MASK_NONE 0   /* every key < kv_len visible */
 #define ATLAS_MASK_TREE 1   /* keys < mask_col_start[req] visible; key p >= that
@@ -478,6 +508,46 @@ int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t nu
                           const int64_t* token_dev, int64_t n, float* row_lse_dev,
                           float* out_dev, void* workspace_dev, size_t workspace_bytes,
                           void* stream);
+
+/* Route selection and commit positions of a Target verify, on the device (one
+ * launch of one wave), so the commit can be queued behind the scoring without
+ * a host round trip.  logprobs_dev holds the scoring launch's values in this
+ * order: the first token of routes 0 .. num_routes - 1, then the remaining
+ * depth - 1 tokens of route 0, of route 1, ...  Each value is rounded to the
+ * logits dtype (rounding: ATLAS_ROUND_*), a route's score is the float64 sum
+ * of its values from the left (with num_weights == depth, the float64 sum of
+ * weights_host[t] * value_t instead); no operation is fused.  Policy
+ * ATLAS_SELECT_TARGET_BEST selects the first route whose key (score,
+ * draft_path_host[r], -route_ids_host[r]) is not exceeded by a later one
+ * under tuple comparison (NaN equals nothing); ATLAS_SELECT_FIRST_ROUTE
+ * selects route 0.  The selection falls back (commits nothing) when
+ * has_first_threshold and its first value < first_threshold, or
+ * has_path_threshold and its score < path_threshold.  Otherwise
+ * commit_len_host[best] tokens are committed: for i < depth, src_dev[i] =
+ * prefix_len + node_ids_host[best * depth + i] and dst_dev[i] = prefix_len + i
+ * for i below the count, src_dev[i] = dst_dev[i] = prefix_len + i (a row
+ * copied onto itself) past it.  result_dev[0] = the selected route's index,
+ * result_dev[1] = the committed count (0 on fallback).  Limits: num_routes <=
+ * ATLAS_SELECT_MAX_ROUTES, depth <= ATLAS_SELECT_MAX_DEPTH, num_routes *
+ * depth <= ATLAS_SELECT_MAX_ENTRIES, node ids <= 32767.  Replaces the
+ * selection of DirectFlashInferMaskedTreeVerifyBackend.verify_payloads
+ * (src/atlas_0709/target_runtime.py:567-573 target_best and first_route,
+ * :722-765 the scores, :754-760 the fallback thresholds, :873-920 the commit
+ * positions); target_sample stays on the host. */
+#define ATLAS_SELECT_MAX_ROUTES 64
+#define ATLAS_SELECT_MAX_DEPTH 16
+#define ATLAS_SELECT_MAX_ENTRIES 512
+#define ATLAS_SELECT_TARGET_BEST 0
+#define ATLAS_SELECT_FIRST_ROUTE 1
+#define ATLAS_ROUND_NONE 0
+#define ATLAS_ROUND_F16 1
+#define ATLAS_ROUND_BF16 2
+int atlas_route_select(const float* logprobs_dev, int num_routes, int depth, int policy, int rounding,
+                       const double* weights_host, int num_weights, const double* draft_path_host,
+                       const int64_t* route_ids_host, const int32_t* commit_len_host, const int32_t* node_ids_host,
+                       int has_path_threshold, double path_threshold, int has_first_threshold,
+                       double first_threshold, int64_t prefix_len, int64_t* src_dev, int64_t* dst_dev,
+                       int32_t* result_dev, void* stream);
 
 /* ------------------------------------------------------------------------
  * Drafter frontier: per-parent top-k, candidate order / selection, records.

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 10
+    assert lib.atlas_abi_version() == 12
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -86,7 +86,7 @@ def test_every_entry_point_refuses_null_buffers_before_device_work():
     lib_mod = pkg("_lib")
     lib = lib_mod.load()
     queries = {"atlas_last_error", "atlas_abi_version", "atlas_gather_logprobs_workspace_bytes",
-               "atlas_frontier_workspace_bytes"}
+               "atlas_frontier_workspace_bytes", "atlas_tree_spec_bytes"}
     ints = (ctypes.c_int, ctypes.c_int64, ctypes.c_int32, ctypes.c_size_t, ctypes.c_uint32, ctypes.c_uint64)
     checked = []
     for name, argtypes in lib_mod._SIGNATURES.items():

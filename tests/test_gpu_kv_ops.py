@@ -377,6 +377,11 @@ def test_host_staging_ring_keeps_every_pending_upload(dev):
         if i % 7 == 3:
             with torch.cuda.stream(side):
                 got.append(ring.upload(host, dev))
+        elif i % 5 == 1:
+            # into a caller's buffer (a slice of a larger tensor)
+            out = torch.empty(n + 16, dtype=torch.uint8, device=dev)[8 : 8 + n]
+            got.append(ring.upload(host, dev, out=out))
+            assert got[-1] is out
         else:
             got.append(ring.upload(host, dev))
     torch.cuda.synchronize()

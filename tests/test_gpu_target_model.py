@@ -307,3 +307,45 @@ def test_rpc_sequence_from_prefill_on_a_transformers_llama(dev):
     with torch.no_grad():
         dense = model(input_ids=torch.tensor([prefix], device=dev)).logits[0, -1].float()
     assert float((backend._prefix_logits[0].float() - dense).abs().max()) <= 5e-2
+
+
+@pytest.mark.parametrize("variant", ["best", "truncate_eos", "thresholds", "weights", "first_route"])
+def test_device_route_selection_equals_host_path(dev, variant):
+    """verify_payloads with the selection and commit queued on the device
+    and with both on the host: the same result records (selection, scores,
+    metadata, fallback tokens), prefix tokens, prefix logits and KV bits over
+    four rounds (the variants truncate at an EOS token and a token limit,
+    fall back on thresholds, weight the scores, or take the first route)."""
+    model = _model(dev, 11)
+    runs = []
+    for on_device in (True, False):
+        kw = {}
+        if variant == "thresholds":
+            kw = dict(first_token_threshold=-7.6, fallback_threshold=-40.0, fallback_ar_tokens=2)
+        elif variant == "weights":
+            kw = dict(score_weights=(1.0, 0.5, 0.25, 0.125))
+        elif variant == "first_route":
+            kw = dict(route_selection_policy="first_route")
+        b = _backend(dev, model, prefix_len=290, seed=12, **kw)
+        b.device_route_selection = on_device
+        rounds = []
+        for r in range(4):
+            routes = _routes(50 + r)
+            call = {}
+            if variant == "truncate_eos":
+                call = dict(selected_path_max_tokens=3 if r % 2 else None,
+                            eos_token_id=routes[r % 3].token_ids[1 + r % 2])
+            res = b.verify_payloads(prefix_token_ids=b.prefix_token_ids, routes=routes, **call)
+            torch.cuda.synchronize()
+            meta = {key: v for key, v in res.metadata.items() if key != "fallback_ar_profile"}
+            rounds.append((res.selected_route_id, res.decision, res.fallback_token_ids, res.scores, meta,
+                           b.prefix_token_ids, b._prefix_logits.clone().view(torch.int16)))
+        runs.append((rounds, [x.clone() for x in b._paged_prefix_kv]))
+    (ra, kva), (rb, kvb) = runs
+    for a, bb in zip(ra, rb):
+        assert a[:3] == bb[:3] and a[3] == bb[3] and a[4] == bb[4] and a[5] == bb[5] and torch.equal(a[6], bb[6])
+    decisions = {x[1] for x in ra}
+    if variant == "thresholds":
+        assert decisions == {"select", "fallback_ar"}
+    for x, y in zip(kva, kvb):
+        assert x.shape == y.shape and torch.equal(x.view(torch.int16), y.view(torch.int16))

@@ -201,3 +201,98 @@ def test_wide_tree_tile_words_match_brute_force():
     wide = torch.ones((2, ta.MAX_WIDE_TREE_WIDTH + 10), dtype=torch.bool)
     wide[0, 3] = False
     assert ta.tree_tile_words_from_dense(wide) is None
+
+
+def _lib_build(paths, prefix_len, page_size, dedup, out_bytes=None):
+    """Call atlas_tree_spec_build directly with a buffer of exactly
+    atlas_tree_spec_bytes (or ``out_bytes``) bytes."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    arr = np.asarray(paths, dtype=np.int64)
+    k, depth = arr.shape
+    need = lib.atlas_tree_spec_bytes(k, depth, prefix_len, page_size)
+    out = np.zeros(need if out_bytes is None else out_bytes, dtype=np.uint8)
+    parents = np.full(k * depth, -7, dtype=np.int32)
+    routes = np.full(k * depth, -7, dtype=np.int32)
+    info = np.zeros(8, dtype=np.int64)
+    rc = lib.atlas_tree_spec_build(arr.ctypes.data, k, depth, int(dedup), prefix_len, page_size, out.ctypes.data,
+                                   out.nbytes, parents.ctypes.data, routes.ctypes.data, info.ctypes.data)
+    return rc, need, out, parents, routes, info
+
+
+def test_native_tree_builder_matches_oracle_across_mask_regimes():
+    """The library's host builder against the oracle's trie and ancestor mask:
+    route -> node paths, parents, token ids, depths, the packed int32 block
+    and the tree block of the dense mask, for trees of up to 64 nodes (one
+    word per node), up to 1024 (tile words) and beyond (block only), with and
+    without deduplication; the buffer bound holds in every case."""
+    import random
+
+    rng = random.Random(11)
+    cases = [(9, 4, 3, 0), (3, 4, 2, 37), (40, 4, 6, 64), (300, 4, 40, 1000), (300, 5, 400, 17), (1, 1, 5, 0)]
+    for k, depth, vocab, prefix in cases:
+        paths = [tuple(rng.randrange(vocab) for _ in range(depth)) for _ in range(k)]
+        for dedup in (True, False):
+            rc, need, out, parents, routes, info = _lib_build(paths, prefix, 16, dedup)
+            assert rc == 0
+            n, kv_len, pages, last, n_words, tiles, n32, nbytes = info.tolist()
+            assert nbytes <= need
+            if dedup:
+                tokens, oparents, odepths, oroutes = ref.dedup_tree(paths)
+                assert routes.reshape(k, depth).tolist() == oroutes
+            else:
+                tokens = [t for p in paths for t in p]
+                odepths = [d for _ in paths for d in range(depth)]
+                oparents = [-1 if d == 0 else i - 1 for i, d in enumerate(odepths)]
+            assert n == len(tokens) and parents[:n].tolist() == list(oparents)
+            assert out[: 8 * n].view(np.int64).tolist() == list(tokens)
+            assert out[8 * n : 16 * n].view(np.int64).tolist() == list(odepths)
+            assert kv_len == prefix + n and pages == (kv_len + 15) // 16 and last == kv_len - 16 * (pages - 1)
+            assert n_words == (n if n <= 64 else n * tiles if n <= 1024 else 0) and (tiles > 0) == (64 < n <= 1024)
+            i32 = out[16 * n + 8 * n_words : 16 * n + 8 * n_words + 4 * n32].view(np.int32)
+            assert n32 % 2 == 0 and i32[:5].tolist() == [0, n, 0, pages, last]
+            assert i32[5 : 5 + pages].tolist() == list(range(pages)) and not i32[5 + pages :].any()
+            mask = ref.ancestor_mask(list(oparents), prefix)
+            block = out[16 * n + 8 * n_words + 4 * n32 : nbytes].reshape(n, n)
+            assert np.array_equal(block.astype(bool), mask[:, prefix:])
+            if n <= 64:
+                assert out[16 * n : 16 * n + 8 * n].view(np.uint64).tolist() == [
+                    int(sum(1 << j for j in range(n) if mask[i, prefix + j])) for i in range(n)]
+
+
+def test_native_tree_builder_bound_and_refusals():
+    """atlas_tree_spec_bytes bounds every tree of the shape, also when
+    deduplication brings a tree of more than 1024 path positions into the
+    tile-word range; a buffer one byte short, an empty path list, a zero
+    depth and NULL outputs are refused with ATLAS_EINVAL."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    # 1100 path positions, 1024 nodes after deduplication (all share token 0 at depth 0)
+    paths = [(0, 1 + i // 3, 1 + i % 3) for i in range(341)] + [(0, 1000, 1001)] * 26
+    paths = paths[:366] + [(0, 2000, 2001)]
+    rc, need, _, _, _, info = _lib_build(paths, 5000, 16, True)
+    assert rc == 0 and info[7] <= need and 64 < info[0] <= 1024
+    rc, *_ = _lib_build(paths, 5000, 16, True, out_bytes=int(info[7]) - 1)
+    assert rc == lib_mod.ATLAS_EINVAL and b"out buffer holds" in lib.atlas_last_error()
+    assert lib.atlas_tree_spec_bytes(0, 4, 0, 16) == -1 and lib.atlas_tree_spec_bytes(3, 0, 0, 16) == -1
+    assert lib.atlas_tree_spec_bytes(3, 4, -1, 16) == -1 and lib.atlas_tree_spec_bytes(3, 4, 0, 0) == -1
+    arr = np.zeros((2, 3), dtype=np.int64)
+    info = np.zeros(8, dtype=np.int64)
+    rc = lib.atlas_tree_spec_build(arr.ctypes.data, 2, 3, 1, 0, 16, None, 1 << 20, None, None, info.ctypes.data)
+    assert rc == lib_mod.ATLAS_EINVAL and b"NULL" in lib.atlas_last_error()
+    rc = lib.atlas_tree_spec_build(arr.ctypes.data, 0, 3, 1, 0, 16, None, 0, None, None, None)
+    assert rc == lib_mod.ATLAS_EINVAL and b"empty" in lib.atlas_last_error()
+
+
+def test_tree_spec_builders_accept_tensor_and_numpy_paths():
+    ffv = pkg("flashinfer_full_verify")
+    paths = [(10, 20, 30), (10, 20, 31), (11, 21, 32)]
+    want, routes = ffv.build_deduplicated_tree_spec_from_paths(paths=paths, prefix_len=5, page_size=4, device="cpu")
+    for alt in (torch.tensor(paths), np.asarray(paths), [list(p) for p in paths]):
+        got, r2 = ffv.build_deduplicated_tree_spec_from_paths(paths=alt, prefix_len=5, page_size=4, device="cpu")
+        assert r2 == routes and torch.equal(got.bool_mask, want.bool_mask)
+        assert got.flat_token_ids.tolist() == [10, 20, 30, 31, 11, 21, 32]
+    # a later build does not change an earlier spec (the builder reuses host buffers)
+    before = want.bool_mask.clone(), want.flat_token_ids.clone()
+    ffv.build_deduplicated_tree_spec_from_paths(paths=[(1, 2, 3)] * 4, prefix_len=9, page_size=4, device="cpu")
+    assert torch.equal(before[0], want.bool_mask) and torch.equal(before[1], want.flat_token_ids)

@@ -144,3 +144,20 @@ def test_weights_and_fallback_reasons():
     assert b._fallback_reason(s) == "first_token_below_threshold"
     b.first_token_threshold, b.fallback_threshold = -2.0, -3.0
     assert b._fallback_reason(s) is None  # equal to a threshold is not below it
+
+
+def test_route_score_fast_constructor_equals_dataclass():
+    """The scoring loop's constructor gives the same frozen object as the
+    dataclass's own __init__ for a keyword set naming every field."""
+    import dataclasses
+
+    tr = pkg("target_runtime")
+    ty = pkg("types")
+    fields = dict(route_id=3, token_ids=(5, 6), target_logprob=-1.5, draft_logprob=-0.25, token_logprobs=(-1.0, -0.5),
+                  first_token_logprob=-1.0, selection_score=-1.5, score_weights=(), draft_token_logprobs=(-0.1, -0.15))
+    assert set(fields) == {f.name for f in dataclasses.fields(ty.TargetRouteScore)}
+    fast, slow = tr._route_score(**fields), ty.TargetRouteScore(**fields)
+    assert fast == slow and hash(fast) == hash(slow) and repr(fast) == repr(slow)
+    assert fast.draft_path_logprob == slow.draft_path_logprob
+    with pytest.raises(dataclasses.FrozenInstanceError):
+        fast.route_id = 4
