@@ -291,3 +291,42 @@ def test_random_forked_tables_match_oracle(dev, seed):
     case = f"seed {seed}: hq {hq} hkv {hkv} d {d} ps {ps} {dtype} routes {batch} cascade groups {w.cascade_groups}"
     assert float(np.abs(out.float().cpu().numpy() - ro).max()) <= ATOL, case
     assert float(np.abs(lse.cpu().numpy() - rl).max()) <= ATOL, case
+
+
+@pytest.mark.parametrize("d,ps,cascade,as_tuple", [(64, 64, True, True), (64, 16, False, False), (128, 64, True, False),
+                                                   (128, 16, True, True), (64, 64, False, True)])
+def test_hnd_pages_equal_nhd_pages(dev, d, ps, cascade, as_tuple):
+    """Decode attention over HND pages ([pages, 2, Hkv, page_size, D], or the
+    (K, V) views [pages, Hkv, page_size, D] the Drafter passes) gives the
+    bits of the same batch over NHD pages holding the same values: the
+    head_dim-64 kernel (page 64 and 16) and the head_dim-128 kernel, cascade
+    plans and one item per route, O and LSE; the NHD result is checked
+    against the oracle in this file's other tests, and here once more."""
+    da = pkg("decode_attention")
+    gen = torch.Generator().manual_seed(d * 7 + ps)
+    requests, routes, hq, hkv = 3, 4, 8, 2
+    pool_pages = requests * (700 // ps + 1) + requests * routes * (90 // ps + 2) + 4
+    indptr, indices, last, kv_lens = _routes_batch(gen, requests=requests, routes=routes, prefix_range=(100, 700),
+                                                   extra_range=(0, 90), ps=ps, pool_pages=pool_pages)
+    batch = requests * routes
+    kv = (torch.randn((pool_pages, 2, ps, hkv, d), generator=gen) * 0.5).to(torch.bfloat16)
+    q = torch.randn((batch, hq, d), generator=gen).to(torch.bfloat16)
+    results = {}
+    for layout in ("NHD", "HND"):
+        cache = (kv if layout == "NHD" else kv.permute(0, 1, 3, 2, 4)).contiguous().to(dev)
+        paged = (cache[:, 0], cache[:, 1]) if as_tuple else cache
+        ws = torch.empty(32 * 1024 * 1024, dtype=torch.uint8, device=dev)
+        w = da.BatchDecodeWithPagedKVCacheWrapper(ws, layout)
+        w.use_cascade = cascade
+        w.plan(torch.tensor(indptr, dtype=torch.int32, device=dev), torch.tensor(indices, dtype=torch.int32, device=dev),
+               torch.tensor(last, dtype=torch.int32, device=dev), hq, hkv, d, ps, data_type=torch.bfloat16,
+               q_data_type=torch.bfloat16)
+        out, lse = w.run(q.to(dev), paged, return_lse=True)
+        torch.cuda.synchronize()
+        results[layout] = (out.cpu(), lse.cpu())
+    (on, ln), (oh, lh) = results["NHD"], results["HND"]
+    assert torch.equal(on.view(torch.int16), oh.view(torch.int16)) and torch.equal(ln, lh)
+    ro, rl = oatt.masked_attention(q.double().numpy(), kv.double().numpy(), list(range(batch + 1)), indptr, indices,
+                                   last)
+    assert float(np.abs(on.float().numpy() - ro).max()) <= ATOL
+    assert float(np.abs(ln.numpy() - rl).max()) <= ATOL
