@@ -237,11 +237,6 @@ class HeadlineStep:
         stream = lib.stream_of(self.dev)
         route_nodes = self.plan()
         self._timed(self.fwd_events, self.graph_fwd.replay)
-        # pages of the whole request (prefix + tree) are owned at verify time
-        # (marked behind the forward: only the prune reads them)
-        rc = lib.load().atlas_mark_pages(lib.ptr(self.owned), self.pool_pages, lib.ptr(self.all_slots),
-                                         self.kv_len, self.ps, stream)
-        lib.check(rc, "atlas_mark_pages")
         # scoring, the route selection and the commit of the selected route
         # queued on the device behind the forward, then the prune; the host
         # waits only for the scores (and the device's choice, checked against
@@ -256,6 +251,12 @@ class HeadlineStep:
         self.live_path[0].len = self.prefix_len + depth
 
         def prune():
+            # pages of the whole request (prefix + tree) are owned at verify
+            # time; marked here, behind the score copy, since only the prune
+            # reads them
+            rc = lib.load().atlas_mark_pages(lib.ptr(self.owned), self.pool_pages, lib.ptr(self.all_slots),
+                                             self.kv_len, self.ps, stream)
+            lib.check(rc, "atlas_mark_pages")
             rc = lib.load().atlas_prune_pages_paths(lib.ptr(self.owned), lib.ptr(self.live), self.pool_pages,
                                                     self.live_path, 1, 1, self.ps, lib.ptr(self.free_pages),
                                                     lib.ptr(self.free_count), stream)
