@@ -1,9 +1,10 @@
 """Route selection on the device (atlas_route_select) against the host
 selection of the Target runtime, which follows the reference's
 verify_payloads (src/atlas_0709/target_runtime.py:567-573, :722-765,
-:754-760): the same selected route, committed count and commit positions on
-seeded cases with ties, NaN and infinite log-probs, weights, thresholds,
-truncated routes, both policies and the three roundings."""
+:754-760), and against the oracle's select_best: the same selected route,
+committed count and commit positions on seeded cases with ties, NaN and
+infinite log-probs, weights, thresholds, truncated routes, both policies and
+the three roundings."""
 
 import math
 import random
@@ -15,6 +16,30 @@ import torch
 from helpers import pkg
 
 pytestmark = pytest.mark.gpu
+
+
+def _oracle_index(routes, values, dtype, d, policy, weights):
+    """Index of the route the oracle selects: per-token values rounded to
+    the logits dtype, the score a left-to-right float sum (or the weighted
+    sum), then oracle.scoring.select_best (target_best) or route 0."""
+    from oracle import scoring as osc
+
+    if policy == "first_route":
+        return 0
+    if dtype == torch.float16:
+        vals = values.astype(np.float16).astype(np.float32).tolist()
+    elif dtype == torch.bfloat16:
+        vals = torch.from_numpy(values.copy()).to(torch.bfloat16).float().tolist()
+    else:
+        vals = values.tolist()
+    k = len(routes)
+    dicts = []
+    for i, r in enumerate(routes):
+        lps = [vals[i]] + vals[k + i * (d - 1): k + (i + 1) * (d - 1)]
+        sel = sum(lps) if weights is None else sum(w * v for w, v in zip(weights, lps))
+        draft = float(sum(r.draft_token_logprobs)) if r.draft_token_logprobs else float(r.draft_logprob)
+        dicts.append(dict(index=i, route_id=r.route_id, selection_score=sel, draft_path_logprob=draft))
+    return osc.select_best(dicts)["index"]
 
 
 def _backend(policy, weights, thr_path, thr_first):
@@ -89,6 +114,8 @@ def test_device_selection_matches_host_selection(dev, dtype):
         host_idx = next(i for i, r in enumerate(routes) if r.route_id == selected.route_id)
         reason = b._fallback_reason(selected)
         host_count = 0 if reason is not None else commit_lens[host_idx]
+        # the oracle's selection (oracle/scoring.py) from the values read in the logits dtype
+        assert host_idx == _oracle_index(routes, values, dtype, d, policy, weights)
         # device
         buf = torch.empty(len(values) + 2, dtype=torch.float32, device=dev)
         buf[: len(values)] = torch.from_numpy(values).to(dev)
