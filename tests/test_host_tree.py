@@ -296,3 +296,49 @@ def test_tree_spec_builders_accept_tensor_and_numpy_paths():
     before = want.bool_mask.clone(), want.flat_token_ids.clone()
     ffv.build_deduplicated_tree_spec_from_paths(paths=[(1, 2, 3)] * 4, prefix_len=9, page_size=4, device="cpu")
     assert torch.equal(before[0], want.bool_mask) and torch.equal(before[1], want.flat_token_ids)
+
+
+def _paths_strategy():
+    from hypothesis import strategies as st
+
+    return st.integers(1, 6).flatmap(lambda depth: st.lists(
+        st.lists(st.integers(0, 3), min_size=depth, max_size=depth).map(tuple), min_size=1, max_size=14))
+
+
+def test_tree_spec_builders_match_oracle_on_random_shapes():
+    """Property test of the spec builders (the library's host builder behind
+    them) against the oracle's trie and ancestor mask: small token alphabets
+    (so routes share prefixes and repeat), depth 1 to 6, prefixes on and off
+    64-key tiles, page sizes 1 to 64."""
+    from hypothesis import HealthCheck, given, settings
+    from hypothesis import strategies as st
+
+    ffv = pkg("flashinfer_full_verify")
+
+    @settings(max_examples=150, deadline=None, suppress_health_check=[HealthCheck.too_slow])
+    @given(paths=_paths_strategy(), prefix=st.integers(0, 200), ps=st.sampled_from([1, 4, 16, 64]),
+           dedup=st.booleans())
+    def check(paths, prefix, ps, dedup):
+        if dedup:
+            spec, routes = ffv.build_deduplicated_tree_spec_from_paths(paths=paths, prefix_len=prefix, page_size=ps,
+                                                                      device="cpu")
+            tokens, parents, depths, oroutes = ref.dedup_tree(paths)
+            assert routes == oroutes
+        else:
+            spec = ffv.build_tree_spec_from_paths(paths=paths, prefix_len=prefix, page_size=ps, device="cpu")
+            tokens = [t for p in paths for t in p]
+            depths = [d for p in paths for d in range(len(p))]
+            parents = [-1 if d == 0 else i - 1 for i, d in enumerate(depths)]
+        n = len(tokens)
+        assert spec.flat_token_ids.tolist() == list(tokens) and spec.parent_indices == list(parents)
+        assert spec.depths.tolist() == list(depths)
+        mask = ref.ancestor_mask(list(parents), prefix)
+        assert spec.bool_mask.numpy().tolist() == mask.reshape(-1).tolist()
+        kv_len = prefix + n
+        pages = -(-kv_len // ps)
+        assert (spec.node_count, spec.kv_len, spec.total_pages) == (n, kv_len, pages)
+        assert spec.kv_last_page_len.tolist() == [kv_len - (pages - 1) * ps]
+        assert spec.qo_indptr.tolist() == [0, n] and spec.kv_indptr.tolist() == [0, pages]
+        assert spec.kv_indices.tolist() == list(range(pages))
+
+    check()
