@@ -143,6 +143,7 @@ _SIGNATURES: dict[str, list] = {
         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _c_i64, ctypes.c_int, _c_i64, _vp, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _vp,
     ],
     "atlas_tree_spec_bytes": [ctypes.c_int32, ctypes.c_int32, _c_i64, ctypes.c_int32],
+    "atlas_tree_mask_fill": [_vp, ctypes.c_int32, _c_i64, _vp, _vp],
     "atlas_route_select": [
         _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp,
         ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_double, _c_i64, _vp, _vp, _vp, _vp,

@@ -210,3 +210,38 @@ extern "C" int atlas_tree_spec_build(const int64_t* paths_host, int32_t num_path
   info_host[7] = sz.bytes;
   return ATLAS_OK;
 }
+
+namespace atlas {
+namespace {
+
+// Dense mask row i: keys below prefix_len visible, tree key prefix_len + j
+// visible iff block[i][j]; four mask bytes per thread.
+__global__ __launch_bounds__(256) void tree_mask_fill_kernel(const uint8_t* __restrict__ block, int32_t n,
+                                                             int64_t prefix_len, uint8_t* __restrict__ mask,
+                                                             int64_t total) {
+  const int64_t kv_len = prefix_len + n;
+  const int64_t f0 = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t f = f0 + b;
+    if (f >= total) return;
+    const int64_t row = f / kv_len;
+    const int64_t col = f - row * kv_len;
+    mask[f] = col < prefix_len ? uint8_t(1) : block[row * n + (col - prefix_len)];
+  }
+}
+
+}  // namespace
+}  // namespace atlas
+
+extern "C" int atlas_tree_mask_fill(const uint8_t* block_dev, int32_t n, int64_t prefix_len, uint8_t* mask_dev,
+                                    void* stream) {
+  ATLAS_REQUIRE(n > 0 && prefix_len >= 0, "n must be positive and prefix_len >= 0");
+  ATLAS_REQUIRE(block_dev && mask_dev, "block and mask must not be NULL");
+  const int64_t total = int64_t(n) * (prefix_len + n);
+  const int64_t threads = (total + 3) / 4;
+  ATLAS_REQUIRE(threads / 256 < (int64_t(1) << 31), "mask too large");
+  hipLaunchKernelGGL(atlas::tree_mask_fill_kernel, dim3(unsigned((threads + 255) / 256)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), block_dev, n, prefix_len, mask_dev, total);
+  return atlas::launch_status("tree_mask_fill_kernel");
+}

@@ -271,15 +271,17 @@ def _native_tree_spec(paths, *, prefix_len: int, page_size: int, device, dedup: 
     n, kv_len, total_pages, last, n_words, tiles, n32, nbytes = sc.info.tolist()
     parents = sc.parents[:n].tolist()
     route_nodes = sc.routes[: k * depth].reshape(k, depth).tolist() if dedup else None
+    args = (sc.out[:nbytes], 2 * n + n_words, n32)
+    kw = dict(node_count=n, kv_len=kv_len, total_pages=total_pages, last=last, prefix_len=prefix_len,
+              compact=n <= 64, device=torch.device(device), parent_indices=parents,
+              tile_shape=(n, tiles) if tiles else None)
+    if not torch.is_inference_mode_enabled():
+        return _tree_spec_tensors(*args, **kw), route_nodes
     # Normal tensors even under torch.inference_mode (the Target verify runs
     # in it): their version counters let a plan trust the attached host
     # values only while the tensors are unchanged.
     with torch.inference_mode(False):
-        spec = _tree_spec_tensors(sc.out[:nbytes], 2 * n + n_words, n32, node_count=n, kv_len=kv_len,
-                                  total_pages=total_pages, last=last, prefix_len=prefix_len, compact=n <= 64,
-                                  device=torch.device(device), parent_indices=parents,
-                                  tile_shape=(n, tiles) if tiles else None)
-    return spec, route_nodes
+        return _tree_spec_tensors(*args, **kw), route_nodes
 
 
 _TRUE: dict = {}
@@ -298,9 +300,15 @@ def _tree_spec_tensors(host, n64, n32, *, node_count, kv_len, total_pages, last,
     """The spec's tensors as views of one device copy of ``host``: ``n64``
     int64 (token ids, depths, mask words), ``n32`` int32 (indptrs, last page
     length, page table, pad), then the n x n tree block of the mask."""
+    dense = None
     if device.type == "cuda":
-        # through pinned staging, so the copy is queued without waiting for the device
-        buf = _lib.staging().upload(host, device)
+        # one allocation: the uploaded buffer (through pinned staging, so the
+        # copy is queued without waiting for the device), then the dense mask
+        nbytes = int(host.nbytes)
+        head = (nbytes + 15) & ~15
+        alloc = torch.empty(head + node_count * kv_len, dtype=torch.uint8, device=device)
+        buf = _lib.staging().upload(host, device, out=alloc[:nbytes])
+        dense = alloc[head:]
     else:
         buf = torch.from_numpy(host.copy()).to(device)
     nb = 8 * node_count
@@ -317,12 +325,16 @@ def _tree_spec_tensors(host, n64, n32, *, node_count, kv_len, total_pages, last,
     kv_indices = idx_b.view(torch.int32)
     # Dense mask [node, prefix + node]: prefix columns all visible, tree column
     # j visible iff bit j of the row's ancestor bitmask (one launch).
-    block_t = block_b.view(torch.bool).view(node_count, node_count)
-    if prefix_len:
-        mask = torch.cat((_true(device).expand(node_count, prefix_len), block_t), dim=1)
+    if dense is not None:
+        rc = _lib.load().atlas_tree_mask_fill(_lib.ptr(block_b), node_count, prefix_len, _lib.ptr(dense),
+                                              _lib.stream_of(device))
+        _lib.check(rc, "atlas_tree_mask_fill")
+        flat_mask = dense.view(torch.bool)
     else:
-        mask = block_t.clone()
-    flat_mask = mask.flatten()
+        block_t = block_b.view(torch.bool).view(node_count, node_count)
+        mask = torch.cat((_true(device).expand(node_count, prefix_len), block_t), dim=1) if prefix_len \
+            else block_t.clone()
+        flat_mask = mask.flatten()
     if tree_mask is not None:
         # Lets the attention plan skip re-deriving the bitmask from the mask.
         # The version counter lets plan() notice an in-place change of the mask.

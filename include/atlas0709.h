@@ -217,6 +217,12 @@ int64_t atlas_tree_spec_bytes(int32_t num_paths, int32_t depth, int64_t prefix_l
 int atlas_tree_spec_build(const int64_t* paths_host, int32_t num_paths, int32_t depth, int32_t dedup,
                           int64_t prefix_len, int32_t page_size, uint8_t* out_host, int64_t out_bytes,
                           int32_t* parents_host, int32_t* route_nodes_host, int64_t* info_host);
+/* The spec's dense mask on the device from its tree block: mask_dev[i *
+ * (prefix_len + n) + c] = 1 for c < prefix_len, block_dev[i * n + c -
+ * prefix_len] otherwise (bytes, 0 or 1), one launch.  Replaces the dense
+ * mask build of build_(deduplicated_)tree_spec_from_paths
+ * (src/atlas_0709/flashinfer_full_verify.py:682-687, :719-724). */
+int atlas_tree_mask_fill(const uint8_t* block_dev, int32_t n, int64_t prefix_len, uint8_t* mask_dev, void* stream);
 
 /* Mask modes. */
 #define ATLAS_MASK_NONE 0   /* every key < kv_len visible */

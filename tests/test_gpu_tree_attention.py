@@ -897,3 +897,38 @@ def test_hnd_fused_rope_append_matches_nhd(dev, prefix_len):
     (kv_a, out_a, lse_a), (kv_b, out_b, lse_b) = results
     assert torch.equal(kv_a.view(torch.int16), kv_b.contiguous().view(torch.int16))
     assert torch.equal(out_a.view(torch.int16), out_b.view(torch.int16)) and torch.equal(lse_a, lse_b)
+
+
+@pytest.mark.parametrize("n_routes,depth,prefix,dedup", [(9, 4, 16384, True), (3, 4, 0, True), (1, 1, 7, False),
+                                                         (40, 4, 100, True), (300, 5, 64, True), (6, 3, 61, False)])
+def test_device_tree_spec_equals_host_spec(dev, n_routes, depth, prefix, dedup):
+    """A tree spec built for the device (its dense mask filled by
+    atlas_tree_mask_fill in the same allocation as the uploaded buffer)
+    equals the one built for the host, tensor for tensor, and the oracle's
+    ancestor mask; the plan's cached window and tile words ride along, and an
+    in-place change of the device mask is seen by the plan (version counter)."""
+    import random
+
+    ffv = pkg("flashinfer_full_verify")
+    ta = pkg("tree_attention")
+    rng = random.Random(n_routes * 31 + depth)
+    paths = [tuple(rng.randrange(6) for _ in range(depth)) for _ in range(n_routes)]
+    build = ffv.build_deduplicated_tree_spec_from_paths if dedup else ffv.build_tree_spec_from_paths
+    outs = [build(paths=paths, prefix_len=prefix, page_size=16, device=d) for d in (dev, "cpu")]
+    (gpu, cpu) = [o[0] if dedup else o for o in outs]
+    torch.cuda.synchronize()
+    for name in ("flat_token_ids", "depths", "bool_mask", "qo_indptr", "kv_indptr", "kv_indices", "kv_last_page_len"):
+        assert torch.equal(getattr(gpu, name).cpu(), getattr(cpu, name)), name
+    assert (gpu.node_count, gpu.kv_len, gpu.total_pages, gpu.parent_indices) == \
+        (cpu.node_count, cpu.kv_len, cpu.total_pages, cpu.parent_indices)
+    _, parents, _, _ = ref.dedup_tree(paths) if dedup else (None, cpu.parent_indices, None, None)
+    mask = ref.ancestor_mask(list(parents), prefix)
+    assert gpu.bool_mask.cpu().numpy().tolist() == mask.reshape(-1).tolist()
+    n, kv = gpu.node_count, gpu.kv_len
+    if n <= 64:
+        assert torch.equal(gpu.tree_mask.cpu(), cpu.tree_mask)
+        assert ta._cached_tree_window(gpu.bool_mask, [n], [kv]) is not None
+        gpu.bool_mask[kv * (n - 1) + prefix] = not bool(gpu.bool_mask[kv * (n - 1) + prefix])
+        assert ta._cached_tree_window(gpu.bool_mask, [n], [kv]) is None
+    elif n <= 1024:
+        assert ta._cached_tree_tiles(gpu.bool_mask, [n], [kv]) is not None
