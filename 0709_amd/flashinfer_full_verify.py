@@ -23,7 +23,7 @@ import numpy as np
 import torch
 
 from . import _lib, kv_ops
-from .tree_attention import BatchPrefillWithPagedKVCacheWrapper
+from .tree_attention import BatchPrefillWithPagedKVCacheWrapper, tensor_version
 
 
 @dataclass(frozen=True)
@@ -62,15 +62,6 @@ class TreeSpec:
 class FullVerifyState:
     tree: TreeSpec
     paged_prefix_kv: list[torch.Tensor]
-
-
-def tensor_version(t: torch.Tensor) -> int | None:
-    """The tensor's in-place version counter, or None for an inference tensor
-    (created under torch.inference_mode, which keeps no counter)."""
-    try:
-        return int(t._version)
-    except RuntimeError:
-        return None
 
 
 def ceil_div(value: int, divisor: int) -> int:

@@ -839,13 +839,16 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         vals = values.tolist()
         n_routes = len(paths)
         scores, k = [], n_routes
+        weights_of: dict[int, tuple[float, ...] | None] = {}
         for i, (route, path) in enumerate(zip(routes, paths)):
             d = len(path)
             rest = max(d - 1, 0)
             lps = (vals[i], *vals[k : k + rest])
             k += rest
             target = sum(lps)
-            weights = self._weights_for_depth(d)
+            if d not in weights_of:
+                weights_of[d] = self._weights_for_depth(d)
+            weights = weights_of[d]
             sel = target if weights is None else sum(w * v for w, v in zip(weights, lps))
             scores.append(_route_score(
                 route_id=int(route.route_id), token_ids=tuple(map(int, path)), target_logprob=target,
@@ -930,15 +933,18 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         if then is not None:
             then()
         done.synchronize()
-        values = host[:n].numpy()
-        chosen, count = host[n:].view(torch.int32).tolist()
-        return self._route_scores_from_values(routes, paths, values, verify_logits.dtype), chosen, count
+        host_np = self._readback_np
+        chosen, count = host_np[n:n + 2].view(np.int32).tolist()
+        return self._route_scores_from_values(routes, paths, host_np[:n], verify_logits.dtype), chosen, count
 
     def _readback_buffer(self, n: int) -> torch.Tensor:
+        """The first n floats of the pinned read-back buffer (grown on demand;
+        ``_readback_np`` is its numpy view)."""
         buf = getattr(self, "_readback", None)
         if buf is None or int(buf.numel()) < n:
             buf = torch.empty(max(n, 256), dtype=torch.float32, pin_memory=True)
             self._readback = buf
+            self._readback_np = buf.numpy()
         return buf[:n]
 
     def _readback_event(self) -> torch.cuda.Event:

@@ -78,6 +78,15 @@ class AttentionPlan:
         return int(self.meta.data_ptr()) + 4 * offset
 
 
+def tensor_version(t: torch.Tensor) -> int | None:
+    """The tensor's in-place version counter, or None for an inference tensor
+    (created under torch.inference_mode, which keeps no counter)."""
+    try:
+        return t._version
+    except RuntimeError:
+        return None
+
+
 def _cached_host_values(t: torch.Tensor) -> list[int] | None:
     """The host copy a tree builder attached to a small index tensor, if the
     tensor has not been modified in place since (version counter unchanged).
@@ -86,8 +95,6 @@ def _cached_host_values(t: torch.Tensor) -> list[int] | None:
     cached = getattr(t, "_atlas_host_values", None)
     if cached is None:
         return None
-    from .flashinfer_full_verify import tensor_version
-
     values, version = cached
     if version is None or version != tensor_version(t) or len(values) != int(t.numel()):
         return None
@@ -185,8 +192,6 @@ def _cached_tree_window(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     if cached is None or len(qo_lens) != 1 or len(cached) != 3:
         return None
     col0, bits, version = cached
-    from .flashinfer_full_verify import tensor_version
-
     if version is None or version != tensor_version(custom_mask) or \
             int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
         return None
@@ -206,8 +211,6 @@ def _cached_tree_tiles(custom_mask, qo_lens: list[int], kv_lens: list[int]):
     if cached is None or len(qo_lens) != 1 or len(cached) != 3:
         return None
     col0, words, version = cached
-    from .flashinfer_full_verify import tensor_version
-
     if version is None or version != tensor_version(custom_mask) or \
             int(custom_mask.numel()) != qo_lens[0] * kv_lens[0]:
         return None
