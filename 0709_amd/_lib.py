@@ -146,7 +146,7 @@ _SIGNATURES: dict[str, list] = {
     "atlas_tree_mask_fill": [_vp, ctypes.c_int32, _c_i64, _vp, _vp],
     "atlas_route_select": [
         _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp,
-        ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_double, _c_i64, _vp, _vp, _vp, _vp,
+        ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_double, _c_i64, _vp, _vp, _vp, _vp, _vp,
     ],
     "atlas_tree_spec_build": [
         _vp, ctypes.c_int32, ctypes.c_int32, ctypes.c_int32, _c_i64, ctypes.c_int32, _vp, _c_i64, _vp, _vp, _vp,
@@ -375,6 +375,32 @@ class HostStaging:
         return self.upload(np.asarray(values, dtype=np.int64), device).view(torch.int64)
 
 
+class MappedReadback:
+    """Pinned host memory the device writes into directly (``hipHostMalloc``
+    with the portable, mapped and coherent flags): ``np`` is the host's
+    float32 view and ``device_ptr`` the address a kernel stores through.  A
+    launch's stores are visible to the host once an event recorded behind the
+    launch has completed.  Held until the process ends."""
+
+    _FLAGS = 0x1 | 0x2 | 0x40000000  # hipHostMallocPortable | Mapped | Coherent
+
+    def __init__(self, count: int) -> None:
+        import numpy as np
+
+        hip = _hip_runtime()
+        self.count = int(count)
+        p = ctypes.c_void_p()
+        rc = hip.hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(4 * self.count), ctypes.c_uint(self._FLAGS))
+        if rc != 0 or not p.value:
+            raise RuntimeError(f"hipHostMalloc of {4 * self.count} mapped bytes failed ({rc})")
+        d = ctypes.c_void_p()
+        rc = hip.hipHostGetDevicePointer(ctypes.byref(d), ctypes.c_void_p(p.value), ctypes.c_uint(0))
+        if rc != 0 or not d.value:
+            raise RuntimeError(f"hipHostGetDevicePointer failed ({rc})")
+        self.device_ptr = ctypes.c_void_p(d.value)
+        self.np = np.frombuffer((ctypes.c_float * self.count).from_address(p.value), dtype=np.float32)
+
+
 _HIP = None
 _HIP_MEMCPY_H2D = 1  # hipMemcpyHostToDevice
 _STAGING: HostStaging | None = None
@@ -391,6 +417,8 @@ def _hip_runtime() -> ctypes.CDLL:
         hip.hipMemcpyAsync.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int,
                                        ctypes.c_void_p]
         hip.hipMemcpyAsync.restype = ctypes.c_int
+        hip.hipHostGetDevicePointer.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_void_p, ctypes.c_uint]
+        hip.hipHostGetDevicePointer.restype = ctypes.c_int
         _HIP = hip
     return _HIP
 

@@ -19,6 +19,7 @@ struct SelectArgs {
   int64_t* src;
   int64_t* dst;
   int32_t* result;
+  float* host_out;  // mapped host memory for the values and the result, or NULL
   int64_t prefix_len;
   double path_threshold, first_threshold;
   int32_t num_routes, depth, policy, rounding, num_weights, has_path_threshold, has_first_threshold;
@@ -69,6 +70,11 @@ __global__ __launch_bounds__(64) void route_select_kernel(SelectArgs a) {
     first[r] = f;
   }
   __syncthreads();
+  if (a.host_out != nullptr) {
+    // the values, read back by the host with the selection (no separate copy)
+    const int n = a.num_routes * a.depth;
+    for (int i = r; i < n; i += 64) a.host_out[i] = a.logprobs[i];
+  }
   if (r != 0) return;
   int best = 0;
   if (a.policy == ATLAS_SELECT_TARGET_BEST) {
@@ -87,6 +93,11 @@ __global__ __launch_bounds__(64) void route_select_kernel(SelectArgs a) {
   }
   a.result[0] = best;
   a.result[1] = count;
+  if (a.host_out != nullptr) {
+    int32_t* res = reinterpret_cast<int32_t*>(a.host_out + a.num_routes * a.depth);
+    res[0] = best;
+    res[1] = count;
+  }
 }
 
 }  // namespace
@@ -97,7 +108,8 @@ extern "C" int atlas_route_select(const float* logprobs_dev, int num_routes, int
                                   const int64_t* route_ids_host, const int32_t* commit_len_host,
                                   const int32_t* node_ids_host, int has_path_threshold, double path_threshold,
                                   int has_first_threshold, double first_threshold, int64_t prefix_len,
-                                  int64_t* src_dev, int64_t* dst_dev, int32_t* result_dev, void* stream) {
+                                  int64_t* src_dev, int64_t* dst_dev, int32_t* result_dev, float* host_out,
+                                  void* stream) {
   ATLAS_REQUIRE(num_routes >= 1 && num_routes <= ATLAS_SELECT_MAX_ROUTES, "num_routes must be in [1, %d]",
                 ATLAS_SELECT_MAX_ROUTES);
   ATLAS_REQUIRE(depth >= 1 && depth <= ATLAS_SELECT_MAX_DEPTH && num_routes * depth <= ATLAS_SELECT_MAX_ENTRIES,
@@ -117,6 +129,7 @@ extern "C" int atlas_route_select(const float* logprobs_dev, int num_routes, int
   a.src = src_dev;
   a.dst = dst_dev;
   a.result = result_dev;
+  a.host_out = host_out;
   a.prefix_len = prefix_len;
   a.path_threshold = path_threshold;
   a.first_threshold = first_threshold;

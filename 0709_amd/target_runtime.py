@@ -888,14 +888,14 @@ class DirectFlashInferMaskedTreeVerifyBackend:
     def _score_select_commit(self, *, routes, paths, prefix_logits, verify_logits, route_to_node_paths, inputs,
                              commit_lens, prefix_len, layers, kv_indptr=None, kv_indices=None, kv_layout="NHD",
                              before_commit=None, then=None):
-        """Scoring, route selection and the commit, queued in stream order
-        with one device-to-host copy: the scoring launch, the selection launch
-        (``atlas_route_select``: the selected route and its commit positions,
-        or none on a fallback), the copy of the values and of the selection to
-        pinned memory, the commit of the selected route (``commit_lens[r]``
-        tokens of route r; rows past the count copy onto themselves) and
-        ``then()``; then the host waits for the copy alone.  ``before_commit``
-        and ``then`` (optional) queue the caller's own work around the commit
+        """Scoring, route selection and the commit, queued in stream order:
+        the scoring launch, the selection launch (``atlas_route_select``: the
+        selected route and its commit positions, or none on a fallback; it
+        also writes the values and the selection to mapped host memory), the
+        commit of the selected route (``commit_lens[r]`` tokens of route r;
+        rows past the count copy onto themselves) and ``then()``; then the
+        host waits for the selection launch alone.  ``before_commit`` and
+        ``then`` (optional) queue the caller's own work around the commit
         launch.  Returns the routes' scores and the device's (route index,
         committed count)."""
         policy, weights, draft, route_ids, nodes = inputs
@@ -904,21 +904,20 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         k, d = len(paths), len(paths[0])
         rows, toks = _scoring_pairs(paths, route_to_node_paths, int(vl.shape[0]))
         n = len(rows)
-        # values, then the selection result (two int32) in one buffer, so one copy brings both back
+        # values, then the selection result (two int32)
         buf = torch.empty(n + 2, dtype=torch.float32, device=device)
         gather_token_logprobs(vl, rows, toks, extra_logits=prefix_logits, out=buf[:n])
         pos = torch.empty(2 * d, dtype=torch.int64, device=device)
         c_double, c_i64, c_i32 = ctypes.c_double, ctypes.c_int64, ctypes.c_int32
         thr_p, thr_f = self.fallback_threshold, self.first_token_threshold
+        readback = self._readback_buffer()
         rc = _lib.load().atlas_route_select(
             _lib.ptr(buf), k, d, policy, self._rounding_code(verify_logits.dtype),
             (c_double * d)(*weights) if weights is not None else None, 0 if weights is None else d,
             (c_double * k)(*draft), (c_i64 * k)(*route_ids), (c_i32 * k)(*commit_lens), (c_i32 * (k * d))(*nodes),
             int(thr_p is not None), float(thr_p or 0.0), int(thr_f is not None), float(thr_f or 0.0), int(prefix_len),
-            _lib.ptr(pos), _lib.ptr(pos[d:]), _lib.ptr(buf[n:]), _lib.stream_of(device))
+            _lib.ptr(pos), _lib.ptr(pos[d:]), _lib.ptr(buf[n:]), readback.device_ptr, _lib.stream_of(device))
         _lib.check(rc, "atlas_route_select")
-        host = self._readback_buffer(n + 2)
-        host.copy_(buf, non_blocking=True)
         done = self._readback_event()
         done.record()
         # the commit hazards of every route's committed rows, decided on the host
@@ -933,19 +932,17 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         if then is not None:
             then()
         done.synchronize()
-        host_np = self._readback_np
+        host_np = readback.np
         chosen, count = host_np[n:n + 2].view(np.int32).tolist()
         return self._route_scores_from_values(routes, paths, host_np[:n], verify_logits.dtype), chosen, count
 
-    def _readback_buffer(self, n: int) -> torch.Tensor:
-        """The first n floats of the pinned read-back buffer (grown on demand;
-        ``_readback_np`` is its numpy view)."""
+    def _readback_buffer(self) -> "_lib.MappedReadback":
+        """The mapped read-back buffer: room for the largest selection the
+        launch accepts (its values and the two result words)."""
         buf = getattr(self, "_readback", None)
-        if buf is None or int(buf.numel()) < n:
-            buf = torch.empty(max(n, 256), dtype=torch.float32, pin_memory=True)
-            self._readback = buf
-            self._readback_np = buf.numpy()
-        return buf[:n]
+        if buf is None:
+            buf = self._readback = _lib.MappedReadback(_lib.SELECT_MAX_ENTRIES + 2)
+        return buf
 
     def _readback_event(self) -> torch.cuda.Event:
         ev = getattr(self, "_readback_done", None)

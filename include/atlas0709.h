@@ -533,7 +533,13 @@ int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t nu
  * prefix_len + node_ids_host[best * depth + i] and dst_dev[i] = prefix_len + i
  * for i below the count, src_dev[i] = dst_dev[i] = prefix_len + i (a row
  * copied onto itself) past it.  result_dev[0] = the selected route's index,
- * result_dev[1] = the committed count (0 on fallback).  Limits: num_routes <=
+ * result_dev[1] = the committed count (0 on fallback).  host_out (may be
+ * NULL): device-accessible mapped host memory (hipHostMalloc with
+ * hipHostMallocMapped, through hipHostGetDevicePointer) of num_routes * depth
+ * floats plus two int32: the launch also writes the values there and the two
+ * result words after them, visible to the host once the launch has completed
+ * (an event recorded behind it), so no device-to-host copy is needed.
+ * Limits: num_routes <=
  * ATLAS_SELECT_MAX_ROUTES, depth <= ATLAS_SELECT_MAX_DEPTH, num_routes *
  * depth <= ATLAS_SELECT_MAX_ENTRIES, node ids <= 32767.  Replaces the
  * selection of DirectFlashInferMaskedTreeVerifyBackend.verify_payloads
@@ -553,7 +559,7 @@ int atlas_route_select(const float* logprobs_dev, int num_routes, int depth, int
                        const int64_t* route_ids_host, const int32_t* commit_len_host, const int32_t* node_ids_host,
                        int has_path_threshold, double path_threshold, int has_first_threshold,
                        double first_threshold, int64_t prefix_len, int64_t* src_dev, int64_t* dst_dev,
-                       int32_t* result_dev, void* stream);
+                       int32_t* result_dev, float* host_out, void* stream);
 
 /* ------------------------------------------------------------------------
  * Drafter frontier: per-parent top-k, candidate order / selection, records.

@@ -88,6 +88,8 @@ def test_device_selection_matches_host_selection(dev, dtype):
     lib_mod = pkg("_lib")
     lib = lib_mod.load()
     rng = random.Random({torch.float16: 1, torch.bfloat16: 2, torch.float32: 3}[dtype])
+    mapped = lib_mod.MappedReadback(lib_mod.SELECT_MAX_ENTRIES + 2)
+    mapped.np[:] = np.nan
     checked = fallbacks = 0
     for case in range(400):
         k, d = rng.randint(1, 12), rng.randint(1, 6)
@@ -129,11 +131,17 @@ def test_device_selection_matches_host_selection(dev, dtype):
             (ctypes.c_double * k)(*draft), (ctypes.c_int64 * k)(*route_ids), (ctypes.c_int32 * k)(*commit_lens),
             (ctypes.c_int32 * (k * d))(*flat_nodes), int(thr_path is not None), float(thr_path or 0.0),
             int(thr_first is not None), float(thr_first or 0.0), prefix, lib_mod.ptr(pos), lib_mod.ptr(pos[d:]),
-            lib_mod.ptr(buf[len(values):]), lib_mod.stream_of(dev))
+            lib_mod.ptr(buf[len(values):]), mapped.device_ptr if case % 2 else None, lib_mod.stream_of(dev))
         lib_mod.check(rc, "atlas_route_select")
         torch.cuda.synchronize()
         dev_idx, dev_count = buf[len(values):].view(torch.int32).tolist()
         assert (dev_idx, dev_count) == (host_idx, host_count), (case, k, d, policy, weights, thr_path, thr_first)
+        if case % 2:
+            # the same values and result, written by the launch to mapped host memory
+            nv = len(values)
+            assert mapped.np[:nv].tobytes() == values.tobytes()
+            assert mapped.np[nv:nv + 2].view(np.int32).tolist() == [host_idx, host_count]
+            mapped.np[:] = np.nan
         src, dst = pos[:d].tolist(), pos[d:].tolist()
         assert dst == [prefix + i for i in range(d)]
         assert src == [prefix + nodes[host_idx][i] if i < host_count else prefix + i for i in range(d)]
@@ -158,7 +166,8 @@ def test_device_selection_refusals(dev):
         return lib.atlas_route_select(
             lib_mod.ptr(buf), k, d, policy, rounding, None, 0, (ctypes.c_double * max(k, 1))(),
             (ctypes.c_int64 * max(k, 1))(), (ctypes.c_int32 * max(k, 1))(*lens), (ctypes.c_int32 * max(k * d, 1))(*nodes),
-            0, 0.0, 0, 0.0, 0, lib_mod.ptr(pos), lib_mod.ptr(pos[32:]), lib_mod.ptr(buf[60:]), lib_mod.stream_of(dev))
+            0, 0.0, 0, 0.0, 0, lib_mod.ptr(pos), lib_mod.ptr(pos[32:]), lib_mod.ptr(buf[60:]), None,
+            lib_mod.stream_of(dev))
 
     einval = lib_mod.ATLAS_EINVAL
     assert call(65, 1) == einval and call(0, 1) == einval and call(4, 17) == einval
