@@ -127,7 +127,11 @@ _SIGNATURES: dict[str, list] = {
     "atlas_paged_metadata": [_vp, _vp, _vp, ctypes.c_int, _c_i64, _c_i64, ctypes.c_int, _vp, _vp, _vp],
     "atlas_pool_prepare_frontier": [
         _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _c_i64,
-        _vp, _vp, _vp, _vp, _c_i64, _vp, _c_i64, _vp,
+        _vp, _vp, _vp, _vp, _c_i64, _vp, _vp,
+    ],
+    "atlas_pool_prepare_frontier_host": [
+        _vp, _vp, _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp,
+        _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp,
     ],
     "atlas_gather_logprobs_workspace_bytes": [_c_i64, _c_i64],
     "atlas_gather_logprobs": [
@@ -159,6 +163,11 @@ _RESTYPES: dict[str, type] = {
     "atlas_tree_spec_bytes": ctypes.c_int64,
 }
 
+FRONTIER_BAD_DESCRIPTOR = 1
+FRONTIER_BAD_LAYOUT = 2
+FRONTIER_DUPLICATE_SLOT = 4
+FRONTIER_COW_OVERLAP = 8
+FRONTIER_MAX_HOST_ROUTES = 24
 SELECT_MAX_ROUTES = 64
 SELECT_MAX_DEPTH = 16
 SELECT_MAX_ENTRIES = 512

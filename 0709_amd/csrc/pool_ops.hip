@@ -306,14 +306,13 @@ struct FrontierLimits {
   int64_t flat_total;
   int64_t cow_total;
   int64_t page_total;
-  int64_t num_flag_groups;
   int64_t num_routes;
 };
 
 __device__ __forceinline__ int64_t floor_div(int64_t a, int64_t b) { return a >= 0 ? a / b : -((-a + b - 1) / b); }
 
 // Every index a descriptor carries stays inside the buffers the launch was
-// given; a route that fails is skipped (and reported through flags[0]).
+// given; a route that fails is skipped (and reported in its check word).
 __device__ bool frontier_route_ok(const atlas_pool_frontier_route_t& d, const FrontierLimits& L) {
   const int64_t ps = L.page_size;
   if (d.prev_len < 0 || d.prev_len + 1 > L.row_stride) return false;
@@ -327,8 +326,7 @@ __device__ bool frontier_route_ok(const atlas_pool_frontier_route_t& d, const Fr
     return false;
   if ((d.prev_len % ps == 0) != (d.new_free_index >= 0) || d.new_free_index >= L.num_free) return false;
   if (d.req_row < 0 || d.req_row >= L.req_rows || d.write_start < 0 || d.write_start > d.prev_len) return false;
-  if (d.group_first < 0 || d.group_count < 1 || d.group_first + d.group_count > L.num_routes) return false;
-  return d.flag_index >= 0 && d.flag_index < L.num_flag_groups;
+  return d.group_first >= 0 && d.group_count >= 1 && d.group_first + d.group_count <= L.num_routes;
 }
 
 // Decode slot of a route (the allocator's decode rule applied to its new
@@ -351,25 +349,40 @@ __device__ __forceinline__ int64_t frontier_slot(const atlas_pool_frontier_route
   return d.path[p];
 }
 
-__global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
-    const atlas_pool_frontier_route_t* __restrict__ routes, FrontierLimits L, const int64_t* __restrict__ free_pages,
-    int64_t* __restrict__ req_to_token, int64_t* __restrict__ flat, int64_t* __restrict__ out_slots,
-    int64_t* __restrict__ cow_dst, int64_t* __restrict__ cow_src, int32_t* __restrict__ kv_indptr,
-    int32_t* __restrict__ kv_last, int32_t* __restrict__ seq_lens, int32_t* __restrict__ page_ids,
-    int64_t* __restrict__ flags) {
+// The route of this workgroup.  Writes its outputs and its check word
+// (ATLAS_FRONTIER_* bits, 0 when every check passed), so nothing has to be
+// cleared before the launch.  With batch != NULL it also writes the route's
+// model inputs: token, sequence length, position, request row and route id,
+// each a run of num_routes int64.
+__device__ __forceinline__ void frontier_prepare_route(
+    const atlas_pool_frontier_route_t* routes, const int64_t* tokens, const int64_t* route_ids,
+    const FrontierLimits& L, const int64_t* __restrict__ free_pages, int64_t* __restrict__ req_to_token,
+    int64_t* __restrict__ flat, int64_t* __restrict__ out_slots, int64_t* __restrict__ cow_dst,
+    int64_t* __restrict__ cow_src, int32_t* __restrict__ kv_indptr, int32_t* __restrict__ kv_last,
+    int32_t* __restrict__ seq_lens, int32_t* __restrict__ page_ids, int64_t* __restrict__ route_flags,
+    int64_t* __restrict__ batch) {
+  __shared__ int bits;
   const int64_t r = blockIdx.x;
   const int tid = threadIdx.x;
   const atlas_pool_frontier_route_t d = routes[r];
   const int64_t ps = L.page_size;
+  if (batch != nullptr && tid == 0) {
+    const int64_t R = L.num_routes;
+    batch[r] = tokens[r];
+    batch[R + r] = d.prev_len + 1;
+    batch[2 * R + r] = d.prev_len;
+    batch[3 * R + r] = d.req_row;
+    batch[4 * R + r] = route_ids[r];
+  }
   if (!frontier_route_ok(d, L)) {
-    if (tid == 0) flags[0] = 0;
+    if (tid == 0) route_flags[r] = ATLAS_FRONTIER_BAD_DESCRIPTOR;
     return;
   }
+  if (tid == 0) bits = 0;
   int64_t cow_page;
   const int64_t out = frontier_decode_slot(d, free_pages, ps, cow_page);
   const int64_t n = d.prev_len + 1;
   const int64_t npages = (n + ps - 1) / ps;
-  int64_t* fl = flags + 1 + 3 * d.flag_index;
   if (tid == 0) {
     out_slots[r] = out;
     seq_lens[r] = static_cast<int32_t>(n);
@@ -382,8 +395,8 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
       if (cow_page >= 0 && cow_page < L.num_pages) atomicOr(&d.owned_bitmap[cow_page >> 5], 1u << (cow_page & 31));
     }
   }
+  int mine = 0;
   // New path, request-row slice, page table and layout check.
-  bool layout_ok = true;
   for (int64_t p = tid; p < n; p += kFrontierThreads) {
     const int64_t v = frontier_slot(d, p, cow_page, out, ps);
     flat[d.flat_offset + p] = v;
@@ -391,12 +404,11 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
     const int64_t in_page = p % ps;
     if (in_page == 0) {
       page_ids[d.page_offset + p / ps] = static_cast<int32_t>(floor_div(v, ps));
-      if (((v % ps) + ps) % ps != 0) layout_ok = false;
+      if (((v % ps) + ps) % ps != 0) mine |= ATLAS_FRONTIER_BAD_LAYOUT;
     } else if (v != frontier_slot(d, p - in_page, cow_page, out, ps) + in_page) {
-      layout_ok = false;
+      mine |= ATLAS_FRONTIER_BAD_LAYOUT;
     }
   }
-  if (!layout_ok) fl[0] = 0;
   // Copy-on-write slot pairs; the fresh page must not be a copy source of
   // the same request.
   if (d.cow_tail > 0) {
@@ -407,16 +419,14 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
     }
     // One thread per (route of the request, tail slot), so every descriptor
     // and tail load is in flight at once.
-    bool disjoint = true;
     const int64_t slots_per_route = ps;  // a tail holds fewer than page_size slots
     for (int64_t i = tid; i < d.group_count * slots_per_route; i += kFrontierThreads) {
       const int64_t s = d.group_first + i / slots_per_route;
       const int64_t t = i % slots_per_route;
       const atlas_pool_frontier_route_t e = routes[s];
       if (t >= e.cow_tail || !frontier_route_ok(e, L)) continue;
-      if (floor_div(e.path[e.prev_len - e.cow_tail + t], ps) == cow_page) disjoint = false;
+      if (floor_div(e.path[e.prev_len - e.cow_tail + t], ps) == cow_page) mine |= ATLAS_FRONTIER_COW_OVERLAP;
     }
-    if (!disjoint) fl[2] = 0;
   }
   // Distinct decode slots among the request's routes.
   for (int64_t s = d.group_first + tid; s < d.group_first + d.group_count; s += kFrontierThreads) {
@@ -424,8 +434,40 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
     const atlas_pool_frontier_route_t e = routes[s];
     if (!frontier_route_ok(e, L)) continue;
     int64_t ecow;
-    if (frontier_decode_slot(e, free_pages, ps, ecow) == out) fl[1] = 0;
+    if (frontier_decode_slot(e, free_pages, ps, ecow) == out) mine |= ATLAS_FRONTIER_DUPLICATE_SLOT;
   }
+  __syncthreads();  // bits is cleared
+  if (mine) atomicOr(&bits, mine);
+  __syncthreads();
+  if (tid == 0) route_flags[r] = bits;
+}
+
+__global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_kernel(
+    const atlas_pool_frontier_route_t* __restrict__ routes, FrontierLimits L, const int64_t* __restrict__ free_pages,
+    int64_t* __restrict__ req_to_token, int64_t* __restrict__ flat, int64_t* __restrict__ out_slots,
+    int64_t* __restrict__ cow_dst, int64_t* __restrict__ cow_src, int32_t* __restrict__ kv_indptr,
+    int32_t* __restrict__ kv_last, int32_t* __restrict__ seq_lens, int32_t* __restrict__ page_ids,
+    int64_t* __restrict__ route_flags) {
+  frontier_prepare_route(routes, nullptr, nullptr, L, free_pages, req_to_token, flat, out_slots, cow_dst, cow_src,
+                         kv_indptr, kv_last, seq_lens, page_ids, route_flags, nullptr);
+}
+
+// The descriptors, tokens and route ids of up to ATLAS_FRONTIER_MAX_HOST_ROUTES
+// routes, passed by value in the launch's argument block.
+struct FrontierHostRoutes {
+  atlas_pool_frontier_route_t d[ATLAS_FRONTIER_MAX_HOST_ROUTES];
+  int64_t token[ATLAS_FRONTIER_MAX_HOST_ROUTES];
+  int64_t route_id[ATLAS_FRONTIER_MAX_HOST_ROUTES];
+};
+
+__global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_host_kernel(
+    const FrontierHostRoutes a, FrontierLimits L, const int64_t* __restrict__ free_pages,
+    int64_t* __restrict__ req_to_token, int64_t* __restrict__ flat, int64_t* __restrict__ out_slots,
+    int64_t* __restrict__ cow_dst, int64_t* __restrict__ cow_src, int32_t* __restrict__ kv_indptr,
+    int32_t* __restrict__ kv_last, int32_t* __restrict__ seq_lens, int32_t* __restrict__ page_ids,
+    int64_t* __restrict__ route_flags, int64_t* __restrict__ batch) {
+  frontier_prepare_route(a.d, a.token, a.route_id, L, free_pages, req_to_token, flat, out_slots, cow_dst, cow_src,
+                         kv_indptr, kv_last, seq_lens, page_ids, route_flags, batch);
 }
 
 }  // namespace
@@ -538,6 +580,29 @@ extern "C" int atlas_alloc_extend_slots(const int64_t* prefix_lens_dev, const in
   return launch_status("alloc_extend_kernel");
 }
 
+namespace {
+
+int frontier_limits(int num_routes, const int64_t* free_pages_dev, int64_t num_free, int64_t page_size,
+                    int64_t num_pages, int64_t* req_to_token_dev, int64_t req_rows, int64_t req_row_stride,
+                    int64_t* flat_dev, int64_t flat_total, int64_t* out_slots_dev, int64_t* cow_dst_dev,
+                    int64_t* cow_src_dev, int64_t cow_total, int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev,
+                    int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
+                    int64_t* route_flags_dev, FrontierLimits* L) {
+  ATLAS_REQUIRE(req_to_token_dev && flat_dev && out_slots_dev && kv_indptr_dev && kv_last_page_len_dev &&
+                    seq_lens_dev && kv_page_indices_dev && route_flags_dev,
+                "frontier buffers must not be NULL");
+  ATLAS_REQUIRE(num_free >= 0 && (num_free == 0 || free_pages_dev), "free list must not be NULL");
+  ATLAS_REQUIRE(cow_total >= 0 && (cow_total == 0 || (cow_dst_dev && cow_src_dev)), "copy-on-write lists missing");
+  ATLAS_REQUIRE(req_rows > 0 && req_row_stride > 0, "request-row pool must not be empty");
+  ATLAS_REQUIRE(flat_total >= num_routes && page_total >= num_routes, "output sizes too small for %d routes",
+                num_routes);
+  *L = FrontierLimits{num_free, page_size, num_pages, req_rows, req_row_stride, flat_total, cow_total, page_total,
+                      num_routes};
+  return ATLAS_OK;
+}
+
+}  // namespace
+
 extern "C" int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, int num_routes,
                                       const int64_t* free_pages_dev, int64_t num_free, int64_t page_size,
                                       int64_t num_pages, int64_t* req_to_token_dev, int64_t req_rows,
@@ -545,22 +610,51 @@ extern "C" int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* ro
                                       int64_t* out_slots_dev, int64_t* cow_dst_dev, int64_t* cow_src_dev,
                                       int64_t cow_total, int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev,
                                       int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
-                                      int64_t* flags_dev, int64_t num_flag_groups, void* stream) {
+                                      int64_t* route_flags_dev, void* stream) {
   ATLAS_REQUIRE(num_routes >= 0 && page_size > 0 && num_pages > 0, "bad route count / page arguments");
   if (num_routes == 0) return ATLAS_OK;
-  ATLAS_REQUIRE(routes_dev && req_to_token_dev && flat_dev && out_slots_dev && kv_indptr_dev && kv_last_page_len_dev &&
-                    seq_lens_dev && kv_page_indices_dev && flags_dev,
-                "frontier buffers must not be NULL");
-  ATLAS_REQUIRE(num_free >= 0 && (num_free == 0 || free_pages_dev), "free list must not be NULL");
-  ATLAS_REQUIRE(cow_total >= 0 && (cow_total == 0 || (cow_dst_dev && cow_src_dev)), "copy-on-write lists missing");
-  ATLAS_REQUIRE(req_rows > 0 && req_row_stride > 0, "request-row pool must not be empty");
-  ATLAS_REQUIRE(flat_total >= num_routes && page_total >= num_routes && num_flag_groups > 0,
-                "output sizes too small for %d routes", num_routes);
-  FrontierLimits L{num_free, page_size, num_pages, req_rows, req_row_stride, flat_total, cow_total, page_total,
-                   num_flag_groups, num_routes};
+  ATLAS_REQUIRE(routes_dev, "frontier buffers must not be NULL");
+  FrontierLimits L;
+  if (int rc = frontier_limits(num_routes, free_pages_dev, num_free, page_size, num_pages, req_to_token_dev, req_rows,
+                               req_row_stride, flat_dev, flat_total, out_slots_dev, cow_dst_dev, cow_src_dev,
+                               cow_total, kv_indptr_dev, kv_last_page_len_dev, seq_lens_dev, kv_page_indices_dev,
+                               page_total, route_flags_dev, &L))
+    return rc;
   hipLaunchKernelGGL(frontier_prepare_kernel, dim3(num_routes), dim3(kFrontierThreads), 0,
                      static_cast<hipStream_t>(stream), routes_dev, L, free_pages_dev, req_to_token_dev, flat_dev,
                      out_slots_dev, cow_dst_dev, cow_src_dev, kv_indptr_dev, kv_last_page_len_dev, seq_lens_dev,
-                     kv_page_indices_dev, flags_dev);
+                     kv_page_indices_dev, route_flags_dev);
   return launch_status("frontier_prepare_kernel");
+}
+
+extern "C" int atlas_pool_prepare_frontier_host(
+    const atlas_pool_frontier_route_t* routes_host, const int64_t* tokens_host, const int64_t* route_ids_host,
+    int num_routes, const int64_t* free_pages_dev, int64_t num_free, int64_t page_size, int64_t num_pages,
+    int64_t* req_to_token_dev, int64_t req_rows, int64_t req_row_stride, int64_t* flat_dev, int64_t flat_total,
+    int64_t* out_slots_dev, int64_t* cow_dst_dev, int64_t* cow_src_dev, int64_t cow_total, int32_t* kv_indptr_dev,
+    int32_t* kv_last_page_len_dev, int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
+    int64_t* route_flags_dev, int64_t* batch_dev, void* stream) {
+  ATLAS_REQUIRE(num_routes >= 0 && page_size > 0 && num_pages > 0, "bad route count / page arguments");
+  if (num_routes == 0) return ATLAS_OK;
+  if (num_routes > ATLAS_FRONTIER_MAX_HOST_ROUTES) {
+    set_error("a frontier step with descriptors from host memory takes at most %d routes (got %d)",
+              ATLAS_FRONTIER_MAX_HOST_ROUTES, num_routes);
+    return ATLAS_EUNSUPPORTED;
+  }
+  ATLAS_REQUIRE(routes_host && tokens_host && route_ids_host && batch_dev, "frontier buffers must not be NULL");
+  FrontierLimits L;
+  if (int rc = frontier_limits(num_routes, free_pages_dev, num_free, page_size, num_pages, req_to_token_dev, req_rows,
+                               req_row_stride, flat_dev, flat_total, out_slots_dev, cow_dst_dev, cow_src_dev,
+                               cow_total, kv_indptr_dev, kv_last_page_len_dev, seq_lens_dev, kv_page_indices_dev,
+                               page_total, route_flags_dev, &L))
+    return rc;
+  FrontierHostRoutes a{};
+  std::memcpy(a.d, routes_host, sizeof(atlas_pool_frontier_route_t) * num_routes);
+  std::memcpy(a.token, tokens_host, sizeof(int64_t) * num_routes);
+  std::memcpy(a.route_id, route_ids_host, sizeof(int64_t) * num_routes);
+  hipLaunchKernelGGL(frontier_prepare_host_kernel, dim3(num_routes), dim3(kFrontierThreads), 0,
+                     static_cast<hipStream_t>(stream), a, L, free_pages_dev, req_to_token_dev, flat_dev,
+                     out_slots_dev, cow_dst_dev, cow_src_dev, kv_indptr_dev, kv_last_page_len_dev, seq_lens_dev,
+                     kv_page_indices_dev, route_flags_dev, batch_dev);
+  return launch_status("frontier_prepare_host_kernel");
 }

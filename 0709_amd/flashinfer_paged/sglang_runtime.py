@@ -1243,14 +1243,16 @@ def _prefetch_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> None:
 
 
 class _StepFlags:
-    """Check flags of one fused frontier step (device int64s the kernel
-    clears on a failed check).  They stay on the device until a check needs
-    them: the prune reads the flags of every pending step back in the copy
-    that brings its released-page counts, so a decode step queues no copy of
-    its own."""
+    """Check words of one fused frontier step: one device int64 per route,
+    the launch's ``FRONTIER_*`` bits (0 when every check passed), and each
+    request's route range ``spans[group]``.  They stay on the device until a
+    check needs them: the prune reads the words of every pending step back
+    in the copy that brings its released-page counts, so a decode step
+    queues no copy of its own."""
 
-    def __init__(self, flags: torch.Tensor) -> None:
+    def __init__(self, flags: torch.Tensor, spans: Sequence[tuple[int, int]]) -> None:
         self.flags = flags
+        self.spans = spans
         self._host: list[int] | None = None
 
     def host(self) -> list[int]:
@@ -1260,16 +1262,19 @@ class _StepFlags:
 
     def check(self, group: int, validate_layout: bool) -> None:
         h = self.host()
-        if not h[0]:
+        if any(w & _lib.FRONTIER_BAD_DESCRIPTOR for w in h):
             raise RuntimeError("frontier step: a route descriptor was out of range and the route was skipped")
-        base = 1 + 3 * int(group)
+        lo, hi = self.spans[int(group)]
+        bits = 0
+        for w in h[lo:hi]:
+            bits |= w
         # the order prepare_frontier records these checks in
-        if not h[base + 2]:
+        if bits & _lib.FRONTIER_COW_OVERLAP:
             raise RuntimeError("copy-on-write destination pages overlap its source pages")
-        if not h[base + 1]:
+        if bits & _lib.FRONTIER_DUPLICATE_SLOT:
             raise RuntimeError("SGLang allocated duplicate output KV slots across forked routes; "
                                "tail-page copy-on-write is not active")
-        if validate_layout and not h[base]:
+        if validate_layout and bits & _lib.FRONTIER_BAD_LAYOUT:
             from .paged_metadata import LAYOUT_MESSAGE
             raise RuntimeError(LAYOUT_MESSAGE)
 
@@ -1287,7 +1292,7 @@ class FusedFrontierStep:
     prevs: tuple[int, ...] = ()  # every route's path length before the step
 
 
-_ROUTE_FIELDS = 14  # int64 fields of one frontier route descriptor
+_ROUTE_FIELDS = 13  # int64 fields of one frontier route descriptor
 
 
 # (allocator, request pool, request table, result) of the last pools checked
@@ -1443,7 +1448,7 @@ def _prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
             else:
                 new_free = -1
             desc += (int(plan.paths[i].data_ptr()) if prev else 0, prev, tail, cow_free, cow_at, new_free,
-                     flat_off, page_off, plan.rows[i], plan.starts[i], bitmap, first, n, g)
+                     flat_off, page_off, plan.rows[i], plan.starts[i], bitmap, first, n)
             flat_off += prev + 1
             page_off += (prev + ps) // ps
             seq_lens.append(prev + 1)
@@ -1455,36 +1460,52 @@ def _prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
         raise RuntimeError(f"SGLang KV pool cannot allocate {free_idx} pages for the frontier step "
                            f"({num_free} free)")
     R = len(seq_lens)
-    nb = len(bridges)
-    positions = [n - 1 for n in seq_lens]
-    rows = [r for plan in plans for r in plan.rows]
-    host = desc + [1] * (1 + 3 * nb) + tokens + seq_lens + positions + rows + route_ids
-    packed = _lib.upload_i64(host, device)
-    _, flags, input_ids, seq_dev, pos_dev, req_dev, rid_dev = packed.split(
-        [_ROUTE_FIELDS * R, 1 + 3 * nb, R, R, R, R, R])
-
     F, C, P = flat_off, cow_off, page_off
-    # one allocation: the int64 outputs, then the int32 ones
-    n64 = F + R + 2 * C
+    # launch arguments carry one request's descriptors; larger steps upload them
+    by_value = R <= _lib.FRONTIER_MAX_HOST_ROUTES
+    # one allocation: the int64 outputs (a check word per route; the model
+    # inputs when the launch writes them), then the int32 ones
     n32 = 3 * R + 1 + P
-    out = torch.empty(n64 + (n32 + 1) // 2, dtype=torch.int64, device=device)
-    flat, out_slots, cow_dst, cow_src, rest = out.split([F, R, C, C, (n32 + 1) // 2])
-    kv_indptr, kv_last, seq32, page_ids, _ = rest.view(torch.int32).split([R + 1, R, R, P, n32 % 2])
+    sizes = [F, R, R] + ([C, C] if C else []) + ([5 * R] if by_value else []) + [(n32 + 1) // 2]
+    out = torch.empty(sum(sizes), dtype=torch.int64, device=device)
+    parts = out.split(sizes)
+    flat, out_slots, flags = parts[:3]
+    cow_dst, cow_src = parts[3:5] if C else (None, None)
+    kv_indptr, kv_last, seq32, page_ids, _ = parts[-1].view(torch.int32).split([R + 1, R, R, P, n32 % 2])
     lib = _lib.load()
-    rc = lib.atlas_pool_prepare_frontier(
-        _lib.ptr(packed), R, ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps,
-        int(b0.owned_page_ids.num_pages), _lib.ptr(table), int(table.shape[0]), int(table.stride(0)),
-        _lib.ptr(flat), F, _lib.ptr(out_slots), _lib.ptr(cow_dst), _lib.ptr(cow_src), C,
-        _lib.ptr(kv_indptr), _lib.ptr(kv_last), _lib.ptr(seq32), _lib.ptr(page_ids), P,
-        _lib.ptr(flags), nb, _lib.stream_of(device),
-    )
-    _lib.check(rc, "atlas_pool_prepare_frontier")
+    if by_value:
+        batch = parts[-2]
+        host = np.asarray(desc + tokens + route_ids, dtype=np.int64)
+        base = host.ctypes.data
+        rc = lib.atlas_pool_prepare_frontier_host(
+            base, base + 8 * _ROUTE_FIELDS * R, base + 8 * (_ROUTE_FIELDS + 1) * R, R,
+            ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps, int(b0.owned_page_ids.num_pages),
+            _lib.ptr(table), int(table.shape[0]), int(table.stride(0)), _lib.ptr(flat), F, _lib.ptr(out_slots),
+            _lib.ptr(cow_dst) if C else None, _lib.ptr(cow_src) if C else None, C, _lib.ptr(kv_indptr),
+            _lib.ptr(kv_last), _lib.ptr(seq32), _lib.ptr(page_ids), P, _lib.ptr(flags), _lib.ptr(batch),
+            _lib.stream_of(device),
+        )
+        _lib.check(rc, "atlas_pool_prepare_frontier_host")
+    else:
+        positions = [n - 1 for n in seq_lens]
+        rows = [r for plan in plans for r in plan.rows]
+        packed = _lib.upload_i64(desc + tokens + seq_lens + positions + rows + route_ids, device)
+        batch = packed[_ROUTE_FIELDS * R:]
+        rc = lib.atlas_pool_prepare_frontier(
+            _lib.ptr(packed), R, ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps,
+            int(b0.owned_page_ids.num_pages), _lib.ptr(table), int(table.shape[0]), int(table.stride(0)),
+            _lib.ptr(flat), F, _lib.ptr(out_slots), _lib.ptr(cow_dst) if C else None,
+            _lib.ptr(cow_src) if C else None, C, _lib.ptr(kv_indptr), _lib.ptr(kv_last), _lib.ptr(seq32),
+            _lib.ptr(page_ids), P, _lib.ptr(flags), _lib.stream_of(device),
+        )
+        _lib.check(rc, "atlas_pool_prepare_frontier")
+    input_ids, seq_dev, pos_dev, req_dev, rid_dev = batch.split(R)
     if C:
         alloc.get_kvcache().move_kv_cache(cow_dst, cow_src)
     alloc.consume_pages(free_idx)
 
     full = flat.split(seq_lens)
-    step_flags = _StepFlags(flags)
+    step_flags = _StepFlags(flags, spans)
     for g, (b, plan) in enumerate(zip(bridges, plans)):
         lo, hi = spans[g]
         b._finish_fused_frontier(plan, full[lo:hi], step_flags, g)

@@ -433,7 +433,7 @@ int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_d
  * Frontier step of many requests in one launch.
  * ---------------------------------------------------------------------- */
 
-/* One active route of a frontier step (every field is 8 bytes).  The route's
+/* One active route of a frontier step (13 fields of 8 bytes).  The route's
  * new slot path is its current path with, when cow_tail > 0, the last
  * cow_tail slots replaced by the first slots of a fresh page (copy-on-write),
  * followed by its decode slot. */
@@ -454,8 +454,14 @@ typedef struct {
   uint32_t* owned_bitmap; /* owned-page bitmap of the route's request (NULL: none) */
   int64_t group_first;    /* routes of the same request: group_first .. +group_count-1 */
   int64_t group_count;
-  int64_t flag_index;     /* that request's check flags: flags[1 + 3*flag_index + k] */
 } atlas_pool_frontier_route_t;
+
+/* Bits of a route's check word (0: every check passed). */
+#define ATLAS_FRONTIER_BAD_DESCRIPTOR 1  /* an index is out of range; the route was skipped */
+#define ATLAS_FRONTIER_BAD_LAYOUT 2      /* a page of the new path is not page-aligned and contiguous */
+#define ATLAS_FRONTIER_DUPLICATE_SLOT 4  /* another route of the request got the same decode slot */
+#define ATLAS_FRONTIER_COW_OVERLAP 8     /* the copy-on-write page is a copy source of the request */
+#define ATLAS_FRONTIER_MAX_HOST_ROUTES 24
 
 /* The device half of SGLangRoutePoolBridge.prepare_frontier for the routes of
  * many requests that share one paged allocator, request-row pool and KV pool
@@ -471,13 +477,10 @@ typedef struct {
  *   kv_indptr[r + 1], kv_last_page_len[r], seq_lens[r] (kv_indptr[0] = 0),
  *   kv_page_indices[page_offset ..]  page id of each page of the new path,
  *   cow_dst/cow_src[cow_offset ..]   the slot pairs of its copy-on-write,
- * and sets the owned bits of its decode page and copy-on-write page.
- * Checks clear flags (which the caller sets to 1 before the call):
- * flags[0] when a descriptor is out of range (the route is then skipped);
- * per request, flags[1 + 3f] when a page of a new path is not page-aligned
- * and contiguous, flags[2 + 3f] when two of its routes get one decode slot,
- * flags[3 + 3f] when a copy-on-write page is one of its copy sources.  The
- * KV bytes of the copied slots are not moved here (atlas_kv_move_slots). */
+ * and sets the owned bits of its decode page and copy-on-write page, and
+ * route_flags[r], its check word (ATLAS_FRONTIER_* bits; written for every
+ * route, so nothing is cleared before the call).  The KV bytes of the copied
+ * slots are not moved here (atlas_kv_move_slots). */
 int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, int num_routes,
                            const int64_t* free_pages_dev, int64_t num_free, int64_t page_size,
                            int64_t num_pages, int64_t* req_to_token_dev, int64_t req_rows,
@@ -485,7 +488,25 @@ int atlas_pool_prepare_frontier(const atlas_pool_frontier_route_t* routes_dev, i
                            int64_t* out_slots_dev, int64_t* cow_dst_dev, int64_t* cow_src_dev,
                            int64_t cow_total, int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev,
                            int32_t* seq_lens_dev, int32_t* kv_page_indices_dev, int64_t page_total,
-                           int64_t* flags_dev, int64_t num_flag_groups, void* stream);
+                           int64_t* route_flags_dev, void* stream);
+
+/* atlas_pool_prepare_frontier for up to ATLAS_FRONTIER_MAX_HOST_ROUTES routes
+ * (one request's decode step) with the descriptors, tokens and route ids in
+ * host memory: they travel in the launch's argument block, so no upload
+ * precedes the launch.  It also writes the model inputs to batch_dev, five
+ * runs of num_routes int64: tokens, sequence lengths (prev_len + 1),
+ * positions (prev_len), request rows and route ids.  More routes return
+ * ATLAS_EUNSUPPORTED.  No counterpart in the reference: the batch of one
+ * that decode_frontier_one_token (sglang_runtime.py:1299-1346) runs. */
+int atlas_pool_prepare_frontier_host(const atlas_pool_frontier_route_t* routes_host, const int64_t* tokens_host,
+                                     const int64_t* route_ids_host, int num_routes, const int64_t* free_pages_dev,
+                                     int64_t num_free, int64_t page_size, int64_t num_pages,
+                                     int64_t* req_to_token_dev, int64_t req_rows, int64_t req_row_stride,
+                                     int64_t* flat_dev, int64_t flat_total, int64_t* out_slots_dev,
+                                     int64_t* cow_dst_dev, int64_t* cow_src_dev, int64_t cow_total,
+                                     int32_t* kv_indptr_dev, int32_t* kv_last_page_len_dev, int32_t* seq_lens_dev,
+                                     int32_t* kv_page_indices_dev, int64_t page_total, int64_t* route_flags_dev,
+                                     int64_t* batch_dev, void* stream);
 
 /* ------------------------------------------------------------------------
  * Route scoring.

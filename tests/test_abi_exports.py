@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 14
+    assert lib.atlas_abi_version() == 15
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -191,3 +191,17 @@ def test_prune_by_paths_limits_without_device_work():
     assert call(2, arr=bad) == lib_mod.ATLAS_EINVAL and b"path 1" in lib.atlas_last_error()
     bad[1].slots, bad[1].len = 1 << 20, -1
     assert call(2, arr=bad) == lib_mod.ATLAS_EINVAL
+
+
+def test_frontier_host_descriptors_limit_without_device_work():
+    """A frontier step whose descriptors travel in the launch's arguments
+    takes at most FRONTIER_MAX_HOST_ROUTES routes; more are refused as
+    unsupported before any buffer is read or any launch."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    fake = ctypes.c_void_p(1 << 20)  # never dereferenced: the call refuses first
+    n = lib_mod.FRONTIER_MAX_HOST_ROUTES + 1
+    rc = lib.atlas_pool_prepare_frontier_host(fake, fake, fake, n, fake, 4, 16, 64, fake, 4, 64, fake, 64, fake,
+                                              None, None, 0, fake, fake, fake, fake, 64, fake, fake, None)
+    assert rc == lib_mod.ATLAS_EUNSUPPORTED
+    assert b"at most" in lib.atlas_last_error()

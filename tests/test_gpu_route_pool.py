@@ -274,11 +274,16 @@ def test_fused_frontier_metadata_matches_oracle(dev):
         assert md.seq_lens_sum == sum(exp.seq_lens) and md.page_index_count == len(exp.kv_page_indices)
 
 
-def test_fused_frontier_rejects_out_of_range_descriptors(dev):
+@pytest.mark.parametrize("descriptors", ["device", "launch_arguments"])
+def test_fused_frontier_rejects_out_of_range_descriptors(dev, descriptors):
     """A route descriptor whose request row lies outside the row table is
-    skipped by the kernel's own range checks and reported in flag 0; the
-    in-range route of the same launch is written."""
+    skipped by the kernel's own range checks and reported in its check word;
+    the in-range route of the same launch is written and its word is 0.  The
+    same through both entry points: descriptors in device memory, and
+    descriptors passed in the launch's arguments (which also writes the
+    model inputs)."""
     import ctypes
+    import numpy as np
     lib_mod = pkg("_lib")
     lib = lib_mod.load()
     ps = 16
@@ -289,25 +294,37 @@ def test_fused_frontier_rejects_out_of_range_descriptors(dev):
     desc = []
     for row in (1, 9):  # 9 is outside the 4-row table
         desc += [path.data_ptr(), 5, 0, -1, 0, -1, 0 if row == 1 else 6, 0 if row == 1 else 1, row, 0,
-                 bitmap.data_ptr(), 0, 2, 0]
-    d = torch.tensor(desc, dtype=torch.int64, device=dev)
-    flags = torch.ones(4, dtype=torch.int64, device=dev)
+                 bitmap.data_ptr(), 0, 2]
+    words = torch.full((2,), -5, dtype=torch.int64, device=dev)
     flat = torch.full((12,), -5, dtype=torch.int64, device=dev)
     out = torch.full((2,), -5, dtype=torch.int64, device=dev)
     i32 = torch.full((3 * 2 + 1 + 2,), -5, dtype=torch.int32, device=dev)
-    print("fused frontier: out-of-range descriptor", flush=True)
-    rc = lib.atlas_pool_prepare_frontier(
-        lib_mod.ptr(d), 2, lib_mod.ptr(free), 2, ps, 32, lib_mod.ptr(table), 4, 64, lib_mod.ptr(flat), 12,
-        lib_mod.ptr(out), None, None, 0, lib_mod.ptr(i32[:3]), lib_mod.ptr(i32[3:5]), lib_mod.ptr(i32[5:7]),
-        lib_mod.ptr(i32[7:]), 2, lib_mod.ptr(flags), 1, lib_mod.stream_of(dev))
+    batch = torch.full((10,), -5, dtype=torch.int64, device=dev)
+    tail = (lib_mod.ptr(free), 2, ps, 32, lib_mod.ptr(table), 4, 64, lib_mod.ptr(flat), 12, lib_mod.ptr(out), None,
+            None, 0, lib_mod.ptr(i32[:3]), lib_mod.ptr(i32[3:5]), lib_mod.ptr(i32[5:7]), lib_mod.ptr(i32[7:]), 2,
+            lib_mod.ptr(words))
+    print(f"fused frontier: out-of-range descriptor, {descriptors}", flush=True)
+    if descriptors == "device":
+        d = torch.tensor(desc, dtype=torch.int64, device=dev)
+        rc = lib.atlas_pool_prepare_frontier(lib_mod.ptr(d), 2, *tail, lib_mod.stream_of(dev))
+    else:
+        host = np.asarray(desc + [11, 12] + [40, 41], dtype=np.int64)
+        base = host.ctypes.data
+        rc = lib.atlas_pool_prepare_frontier_host(base, base + 8 * 26, base + 8 * 28, 2, *tail, lib_mod.ptr(batch),
+                                                  lib_mod.stream_of(dev))
     lib_mod.check(rc, "atlas_pool_prepare_frontier")
     torch.cuda.synchronize()
-    assert flags.tolist() == [0, 1, 1, 1]
+    assert words.tolist() == [0, lib_mod.FRONTIER_BAD_DESCRIPTOR]
     assert flat[:6].tolist() == [32, 33, 34, 35, 36, 37] and flat[6:].tolist() == [-5] * 6
     assert out.tolist() == [37, -5]
     assert table[1, :6].tolist() == [32, 33, 34, 35, 36, 37] and int(table[2:].abs().sum()) == 0
     assert i32[:2].tolist() == [0, 1] and i32[3].item() == 6 and i32[5].item() == 6 and i32[7].item() == 2
     assert bitmap.item() == 1 << 2
+    if descriptors == "launch_arguments":
+        # tokens, sequence lengths, positions, request rows, route ids
+        assert batch.tolist() == [11, 12, 6, 6, 5, 5, 1, 9, 40, 41]
+    else:
+        assert batch.tolist() == [-5] * 10
 
 
 def test_batched_extend_equals_per_request_calls_and_refusals(dev):

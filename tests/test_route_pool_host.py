@@ -567,31 +567,40 @@ def test_fused_frontier_step_needs_native_pools():
 
 
 def test_fused_step_flags_raise_in_prepare_frontier_order():
-    """Check flags of a fused step: a skipped descriptor first, then per
-    request the copy-on-write overlap, duplicate decode slots and page layout
-    checks, in the order prepare_frontier records them."""
+    """Check words of a fused step (one per route): a skipped descriptor of
+    any route first, then per request the copy-on-write overlap, duplicate
+    decode slots and page layout checks, in the order prepare_frontier
+    records them; a request's checks read only its own routes' words."""
     sr, _ = _mods()
     pm = pkg("flashinfer_paged.paged_metadata")
+    lib = pkg("_lib")
+    bad_desc, layout, dup, cow = (lib.FRONTIER_BAD_DESCRIPTOR, lib.FRONTIER_BAD_LAYOUT, lib.FRONTIER_DUPLICATE_SLOT,
+                                  lib.FRONTIER_COW_OVERLAP)
+    spans = [(0, 2), (2, 3)]
     cases = [
-        ([0, 1, 1, 1], "out of range"),
-        ([1, 0, 0, 0], "overlap"),
-        ([1, 0, 0, 1], "duplicate output KV slots"),
-        ([1, 0, 1, 1], pm.LAYOUT_MESSAGE[:40]),
+        ([0, 0, bad_desc], "out of range", True),
+        ([layout, cow | dup], "overlap", False),
+        ([dup, layout], "duplicate output KV slots", False),
+        ([0, layout], pm.LAYOUT_MESSAGE[:40], False),
     ]
-    for host, message in cases:
-        flags = sr._StepFlags(torch.tensor(host + [1, 1, 1], dtype=torch.int64))
+    for words, message, everywhere in cases:
+        flags = sr._StepFlags(torch.tensor(words + [0], dtype=torch.int64), spans)
         with pytest.raises(RuntimeError, match=message):
             flags.check(0, True)
-        if host[0]:
-            flags.check(1, True)  # the other request's flags are clear
-    sr._StepFlags(torch.tensor([1, 0, 1, 1], dtype=torch.int64)).check(0, False)  # layout not validated
+        if everywhere:
+            with pytest.raises(RuntimeError, match=message):
+                flags.check(1, True)
+        else:
+            flags.check(1, True)  # the other request's words are clear
+    sr._StepFlags(torch.tensor([0, layout, 0], dtype=torch.int64), spans).check(0, False)  # layout not validated
 
 
 def test_pending_step_checks_read_once_and_raise_in_order():
-    """The flags of every fused step with a check pending on a set of bridges
-    are brought to the host once; the checks then raise in the order
+    """The words of every fused step with a check pending on a set of
+    bridges are brought to the host once; the checks then raise in the order
     recorded, and a bridge's pending list is empty after its checks ran."""
     sr, _ = _mods()
+    lib = pkg("_lib")
 
     class Bridge:
         check_pending_device_checks = sr.SGLangRoutePoolBridge.check_pending_device_checks
@@ -599,12 +608,13 @@ def test_pending_step_checks_read_once_and_raise_in_order():
         def __init__(self, checks):
             self.pending_device_checks = checks
 
-    good = sr._StepFlags(torch.tensor([1, 1, 1, 1, 1, 1, 1], dtype=torch.int64))
-    bad = sr._StepFlags(torch.tensor([1, 1, 1, 1, 1, 0, 1], dtype=torch.int64))  # group 1: duplicate slots
+    spans = [(0, 2), (2, 4)]
+    good = sr._StepFlags(torch.zeros(4, dtype=torch.int64), spans)
+    bad = sr._StepFlags(torch.tensor([0, 0, 0, lib.FRONTIER_DUPLICATE_SLOT], dtype=torch.int64), spans)
     a = Bridge([sr._StepCheck(good, 0, True), sr._StepCheck(bad, 0, True)])
     b = Bridge([sr._StepCheck(good, 1, True), sr._StepCheck(bad, 1, True)])
     sr._prefetch_step_flags([a, b])
-    assert good._host == [1] * 7 and bad._host == [1, 1, 1, 1, 1, 0, 1]
+    assert good._host == [0] * 4 and bad._host == [0, 0, 0, lib.FRONTIER_DUPLICATE_SLOT]
     a.check_pending_device_checks()
     assert a.pending_device_checks == []
     with pytest.raises(RuntimeError, match="duplicate output KV slots"):
