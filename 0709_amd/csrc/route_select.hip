@@ -71,9 +71,10 @@ __global__ __launch_bounds__(64) void route_select_kernel(SelectArgs a) {
   }
   __syncthreads();
   if (a.host_out != nullptr) {
-    // the values, read back by the host with the selection (no separate copy)
+    // the values as the host reads them (rounded to the logits dtype), with
+    // the selection, so no separate copy follows
     const int n = a.num_routes * a.depth;
-    for (int i = r; i < n; i += 64) a.host_out[i] = a.logprobs[i];
+    for (int i = r; i < n; i += 64) a.host_out[i] = round_logits_dtype(a.logprobs[i], a.rounding);
   }
   if (r != 0) return;
   int best = 0;

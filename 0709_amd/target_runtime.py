@@ -827,35 +827,47 @@ class DirectFlashInferMaskedTreeVerifyBackend:
             return _lib.ROUND_BF16
         return _lib.ROUND_NONE
 
-    def _route_scores_from_values(self, routes, paths, values: np.ndarray, dtype: torch.dtype):
-        """The routes' TargetRouteScores from the scoring launch's fp32 values
-        (every route's first token, then each route's other tokens)."""
-        rounding = self._rounding_code(dtype)
-        if rounding == _lib.ROUND_F16:
-            # The reference reads log_softmax outputs in the logits dtype.
-            values = values.astype(np.float16).astype(np.float32)
-        elif rounding == _lib.ROUND_BF16:
-            values = torch.from_numpy(values).to(torch.bfloat16).float().numpy()
-        vals = values.tolist()
-        n_routes = len(paths)
-        scores, k = [], n_routes
+    def _route_score_parts(self, routes, paths) -> list[tuple[int, tuple | None, dict]]:
+        """The parts of each route's TargetRouteScore that do not depend on the
+        scores: (depth, weights or None, the fixed fields)."""
+        parts = []
         weights_of: dict[int, tuple[float, ...] | None] = {}
-        for i, (route, path) in enumerate(zip(routes, paths)):
+        for route, path in zip(routes, paths):
             d = len(path)
+            if d not in weights_of:
+                weights_of[d] = self._weights_for_depth(d)
+            weights = weights_of[d]
+            parts.append((d, weights, dict(
+                route_id=int(route.route_id), token_ids=tuple(map(int, path)),
+                draft_logprob=float(route.draft_logprob), score_weights=() if weights is None else tuple(weights),
+                draft_token_logprobs=tuple(map(float, route.draft_token_logprobs)))))
+        return parts
+
+    def _route_scores_from_values(self, routes, paths, values: np.ndarray, dtype: torch.dtype, *,
+                                  parts=None, rounded: bool = False):
+        """The routes' TargetRouteScores from the scoring launch's fp32 values
+        (every route's first token, then each route's other tokens).
+        ``rounded``: the values are already rounded to the logits dtype;
+        ``parts``: ``_route_score_parts(routes, paths)``, when built ahead."""
+        if not rounded:
+            rounding = self._rounding_code(dtype)
+            if rounding == _lib.ROUND_F16:
+                # The reference reads log_softmax outputs in the logits dtype.
+                values = values.astype(np.float16).astype(np.float32)
+            elif rounding == _lib.ROUND_BF16:
+                values = torch.from_numpy(values).to(torch.bfloat16).float().numpy()
+        vals = values.tolist()
+        if parts is None:
+            parts = self._route_score_parts(routes, paths)
+        scores, k = [], len(paths)
+        for i, (d, weights, fixed) in enumerate(parts):
             rest = max(d - 1, 0)
             lps = (vals[i], *vals[k : k + rest])
             k += rest
             target = sum(lps)
-            if d not in weights_of:
-                weights_of[d] = self._weights_for_depth(d)
-            weights = weights_of[d]
             sel = target if weights is None else sum(w * v for w, v in zip(weights, lps))
-            scores.append(_route_score(
-                route_id=int(route.route_id), token_ids=tuple(map(int, path)), target_logprob=target,
-                draft_logprob=float(route.draft_logprob), token_logprobs=lps, first_token_logprob=lps[0],
-                selection_score=sel, score_weights=() if weights is None else tuple(weights),
-                draft_token_logprobs=tuple(map(float, route.draft_token_logprobs)),
-            ))
+            scores.append(_route_score(target_logprob=target, token_logprobs=lps, first_token_logprob=lps[0],
+                                       selection_score=sel, **fixed))
         return scores
 
     # ------------------------------------------------------------ device selection
@@ -891,7 +903,8 @@ class DirectFlashInferMaskedTreeVerifyBackend:
         """Scoring, route selection and the commit, queued in stream order:
         the scoring launch, the selection launch (``atlas_route_select``: the
         selected route and its commit positions, or none on a fallback; it
-        also writes the values and the selection to mapped host memory), the
+        also writes the values, rounded to the logits dtype, and the selection
+        to mapped host memory), the
         commit of the selected route (``commit_lens[r]`` tokens of route r;
         rows past the count copy onto themselves) and ``then()``; then the
         host waits for the selection launch alone.  ``before_commit`` and
@@ -931,10 +944,14 @@ class DirectFlashInferMaskedTreeVerifyBackend:
                             needs_staging=staging, kv_layout=kv_layout)
         if then is not None:
             then()
+        parts = self._route_score_parts(routes, paths)
         done.synchronize()
         host_np = readback.np
         chosen, count = host_np[n:n + 2].view(np.int32).tolist()
-        return self._route_scores_from_values(routes, paths, host_np[:n], verify_logits.dtype), chosen, count
+        # the launch wrote the values rounded to the logits dtype
+        scores = self._route_scores_from_values(routes, paths, host_np[:n], verify_logits.dtype, parts=parts,
+                                                rounded=True)
+        return scores, chosen, count
 
     def _readback_buffer(self) -> "_lib.MappedReadback":
         """The mapped read-back buffer: room for the largest selection the

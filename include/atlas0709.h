@@ -557,8 +557,9 @@ int atlas_gather_logprobs(const void* logits_dev, int64_t row_stride, int64_t nu
  * result_dev[1] = the committed count (0 on fallback).  host_out (may be
  * NULL): device-accessible mapped host memory (hipHostMalloc with
  * hipHostMallocMapped, through hipHostGetDevicePointer) of num_routes * depth
- * floats plus two int32: the launch also writes the values there and the two
- * result words after them, visible to the host once the launch has completed
+ * floats plus two int32: the launch also writes the values there, rounded
+ * to the logits dtype as the selection reads them, and the two result words
+ * after them, visible to the host once the launch has completed
  * (an event recorded behind it), so no device-to-host copy is needed.
  * Limits: num_routes <=
  * ATLAS_SELECT_MAX_ROUTES, depth <= ATLAS_SELECT_MAX_DEPTH, num_routes *

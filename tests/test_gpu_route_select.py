@@ -42,6 +42,26 @@ def _oracle_index(routes, values, dtype, d, policy, weights):
     return osc.select_best(dicts)["index"]
 
 
+def _rounded(values, dtype):
+    """The fp32 values rounded to the logits dtype (what the host reads)."""
+    if dtype == torch.float16:
+        return values.astype(np.float16).astype(np.float32)
+    if dtype == torch.bfloat16:
+        return torch.from_numpy(values.copy()).to(torch.bfloat16).float().numpy()
+    return values.copy()
+
+
+def _score_key(score):
+    """A TargetRouteScore's fields with NaN made comparable."""
+    def fix(v):
+        if isinstance(v, float) and math.isnan(v):
+            return "nan"
+        if isinstance(v, tuple):
+            return tuple(fix(x) for x in v)
+        return v
+    return tuple(sorted((k, fix(v)) for k, v in vars(score).items()))
+
+
 def _backend(policy, weights, thr_path, thr_first):
     tr = pkg("target_runtime")
     b = object.__new__(tr.DirectFlashInferMaskedTreeVerifyBackend)
@@ -137,10 +157,18 @@ def test_device_selection_matches_host_selection(dev, dtype):
         dev_idx, dev_count = buf[len(values):].view(torch.int32).tolist()
         assert (dev_idx, dev_count) == (host_idx, host_count), (case, k, d, policy, weights, thr_path, thr_first)
         if case % 2:
-            # the same values and result, written by the launch to mapped host memory
+            # the values rounded to the logits dtype, as the host rounds them, and the result,
+            # written by the launch to mapped host memory
             nv = len(values)
-            assert mapped.np[:nv].tobytes() == values.tobytes()
+            got = mapped.np[:nv].copy()
+            exp = _rounded(values, dtype)
+            nan = np.isnan(exp)
+            assert (np.isnan(got) == nan).all()
+            assert (got[~nan].view(np.uint32) == exp[~nan].view(np.uint32)).all()
             assert mapped.np[nv:nv + 2].view(np.int32).tolist() == [host_idx, host_count]
+            # and the scores built from them without rounding again equal the host's
+            again = b._route_scores_from_values(routes, paths, got, dtype, rounded=True)
+            assert [_score_key(x) for x in again] == [_score_key(x) for x in scores]
             mapped.np[:] = np.nan
         src, dst = pos[:d].tolist(), pos[d:].tolist()
         assert dst == [prefix + i for i in range(d)]
