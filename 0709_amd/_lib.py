@@ -148,6 +148,7 @@ _SIGNATURES: dict[str, list] = {
     ],
     "atlas_tree_spec_bytes": [ctypes.c_int32, ctypes.c_int32, _c_i64, ctypes.c_int32],
     "atlas_tree_mask_fill": [_vp, ctypes.c_int32, _c_i64, _vp, _vp],
+    "atlas_tree_spec_upload": [_vp, _c_i64, ctypes.c_int32, _c_i64, _vp, _vp, _vp],
     "atlas_route_select": [
         _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, ctypes.c_int, _vp, _vp, _vp, _vp,
         ctypes.c_int, ctypes.c_double, ctypes.c_int, ctypes.c_double, _c_i64, _vp, _vp, _vp, _vp, _vp,
@@ -284,8 +285,9 @@ def dtype_code(dtype: torch.dtype) -> int:
 
 
 class HostStaging:
-    """Pinned host memory (``hipHostMalloc``) for small host-to-device
-    uploads, handed out from a ring of four quarters.
+    """Pinned host memory (``hipHostMalloc``, mapped and coherent, so kernels
+    can also read it in place) for small host-to-device uploads, handed out
+    from a ring of four quarters.
 
     A quarter is written again only after the copies queued from it have run:
     when the ring leaves a quarter it records an event on the stream that
@@ -298,11 +300,17 @@ class HostStaging:
     def __init__(self, nbytes: int = 4 << 20) -> None:
         self.quarter = (nbytes // 4) & ~63
         self.nbytes = 4 * self.quarter
+        hip = _hip_runtime()
         p = ctypes.c_void_p()
-        rc = _hip_runtime().hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(self.nbytes), ctypes.c_uint(1))
+        rc = hip.hipHostMalloc(ctypes.byref(p), ctypes.c_size_t(self.nbytes), ctypes.c_uint(MappedReadback._FLAGS))
         if rc != 0 or not p.value:
             raise RuntimeError(f"hipHostMalloc of {self.nbytes} staging bytes failed ({rc})")
         self.base = p.value
+        d = ctypes.c_void_p()
+        rc = hip.hipHostGetDevicePointer(ctypes.byref(d), ctypes.c_void_p(p.value), ctypes.c_uint(0))
+        if rc != 0 or not d.value:
+            raise RuntimeError(f"hipHostGetDevicePointer of the staging ring failed ({rc})")
+        self.device_base = d.value
         self.memcpy = _hip_runtime().hipMemcpyAsync
         buf = (ctypes.c_uint8 * self.nbytes).from_address(p.value)
         self.host = torch.frombuffer(buf, dtype=torch.uint8)
@@ -356,26 +364,51 @@ class HostStaging:
                 return staged.to(device, non_blocking=False)
             dst.copy_(staged)
             return out
-        idx = torch.cuda.current_device() if device.index is None else device.index
         with self.lock:
-            q = self.cur
-            start = self.pos
-            if start + nbytes > (q + 1) * self.quarter:
-                self._leave(q)
-                q = self.cur = (q + 1) % 4
-                self._enter(q)
-                start = q * self.quarter
-            self.host_np[start : start + nbytes] = src
+            start, raw = self._place(src, nbytes, device)
             if out is None:
                 out = dst = torch.empty(nbytes, dtype=torch.uint8, device=device)
-            raw = _RAW_STREAM(idx) if _RAW_STREAM is not None else torch.cuda.current_stream(idx).cuda_stream
             # queued on the current stream straight from the pinned bytes
             rc = self.memcpy(dst.data_ptr(), self.base + start, nbytes, _HIP_MEMCPY_H2D, raw)
             if rc != 0:
                 raise RuntimeError(f"hipMemcpyAsync of {nbytes} staged bytes failed ({rc})")
-            self.users[q].add((idx, raw))
-            self.pos = (start + nbytes + 63) & ~63
         return out
+
+    def _place(self, src, nbytes: int, device: torch.device) -> tuple[int, int]:
+        """Write ``src`` (uint8, ``nbytes``) into the ring for work queued
+        next on the device's current stream; returns its ring offset (64-byte
+        aligned) and the raw stream.  Called with the lock held."""
+        idx = torch.cuda.current_device() if device.index is None else device.index
+        q = self.cur
+        start = self.pos
+        if start + nbytes > (q + 1) * self.quarter:
+            self._leave(q)
+            q = self.cur = (q + 1) % 4
+            self._enter(q)
+            start = q * self.quarter
+        self.host_np[start : start + nbytes] = src
+        raw = _RAW_STREAM(idx) if _RAW_STREAM is not None else torch.cuda.current_stream(idx).cuda_stream
+        self.users[q].add((idx, raw))
+        self.pos = (start + nbytes + 63) & ~63
+        return start, raw
+
+    def stage(self, host: "np.ndarray", device: torch.device, launch) -> bool:
+        """Copy a numpy array's bytes into the ring and call ``launch(addr)``
+        with their device address, under the ring's lock, so the kernel it
+        queues on the device's current stream reads them in place (the ring
+        is mapped host memory, and that part of it is not written again
+        before the work queued after it has run).  False, and no call, when
+        the array is empty or larger than a quarter of the ring."""
+        import numpy as np
+
+        nbytes = int(host.nbytes)
+        if nbytes > self.quarter or nbytes == 0:
+            return False
+        src = np.ascontiguousarray(host).reshape(-1).view(np.uint8)
+        with self.lock:
+            start, _ = self._place(src, nbytes, device)
+            launch(self.device_base + start)
+        return True
 
     def upload_i64(self, values: Sequence[int], device: torch.device) -> torch.Tensor:
         """``torch.tensor(values, dtype=torch.int64)`` on ``device``."""

@@ -231,8 +231,58 @@ __global__ __launch_bounds__(256) void tree_mask_fill_kernel(const uint8_t* __re
   }
 }
 
+// The spec's bytes copied from src to dst by the first copy_blocks
+// workgroups (16 bytes per thread), and the dense mask filled by the others
+// from the tree block, the spec's last n * n bytes, read at src.  src may be
+// mapped host memory: the launch then reads the spec once over the bus and
+// no copy precedes it.
+__global__ __launch_bounds__(256) void tree_spec_upload_kernel(const uint8_t* __restrict__ src, int64_t nbytes,
+                                                               int32_t n, int64_t prefix_len,
+                                                               uint8_t* __restrict__ dst,
+                                                               uint8_t* __restrict__ mask, int64_t total,
+                                                               int32_t copy_blocks) {
+  if (int32_t(blockIdx.x) < copy_blocks) {
+    const int64_t i = (int64_t(blockIdx.x) * blockDim.x + threadIdx.x) * 16;
+    if (i + 16 <= nbytes) {
+      *reinterpret_cast<uint4*>(dst + i) = *reinterpret_cast<const uint4*>(src + i);
+    } else {
+      for (int64_t b = i; b < nbytes; ++b) dst[b] = src[b];
+    }
+    return;
+  }
+  const uint8_t* block = src + (nbytes - int64_t(n) * n);
+  const int64_t kv_len = prefix_len + n;
+  const int64_t f0 = (int64_t(blockIdx.x - copy_blocks) * blockDim.x + threadIdx.x) * 4;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const int64_t f = f0 + b;
+    if (f >= total) return;
+    const int64_t row = f / kv_len;
+    const int64_t col = f - row * kv_len;
+    mask[f] = col < prefix_len ? uint8_t(1) : block[row * n + (col - prefix_len)];
+  }
+}
+
 }  // namespace
 }  // namespace atlas
+
+extern "C" int atlas_tree_spec_upload(const uint8_t* spec_src, int64_t nbytes, int32_t n, int64_t prefix_len,
+                                      uint8_t* spec_dev, uint8_t* mask_dev, void* stream) {
+  ATLAS_REQUIRE(n > 0 && prefix_len >= 0, "n must be positive and prefix_len >= 0");
+  ATLAS_REQUIRE(nbytes >= int64_t(n) * n, "the spec (%lld bytes) must end with its %d x %d tree block",
+                static_cast<long long>(nbytes), n, n);
+  ATLAS_REQUIRE(spec_src && spec_dev && mask_dev, "spec and mask buffers must not be NULL");
+  ATLAS_REQUIRE(reinterpret_cast<uintptr_t>(spec_src) % 16 == 0 && reinterpret_cast<uintptr_t>(spec_dev) % 16 == 0,
+                "spec buffers must be 16-byte aligned");
+  const int64_t total = int64_t(n) * (prefix_len + n);
+  const int64_t fill_blocks = ((total + 3) / 4 + 255) / 256;
+  const int64_t copy_blocks = spec_src == spec_dev ? 0 : ((nbytes + 15) / 16 + 255) / 256;
+  ATLAS_REQUIRE(fill_blocks + copy_blocks < (int64_t(1) << 31), "mask too large");
+  hipLaunchKernelGGL(atlas::tree_spec_upload_kernel, dim3(unsigned(fill_blocks + copy_blocks)), dim3(256), 0,
+                     static_cast<hipStream_t>(stream), spec_src, nbytes, n, prefix_len, spec_dev, mask_dev, total,
+                     int32_t(copy_blocks));
+  return atlas::launch_status("tree_spec_upload_kernel");
+}
 
 extern "C" int atlas_tree_mask_fill(const uint8_t* block_dev, int32_t n, int64_t prefix_len, uint8_t* mask_dev,
                                     void* stream) {

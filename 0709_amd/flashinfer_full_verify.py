@@ -293,13 +293,26 @@ def _tree_spec_tensors(host, n64, n32, *, node_count, kv_len, total_pages, last,
     length, page table, pad), then the n x n tree block of the mask."""
     dense = None
     if device.type == "cuda":
-        # one allocation: the uploaded buffer (through pinned staging, so the
-        # copy is queued without waiting for the device), then the dense mask
+        # One allocation: the spec buffer, then the dense mask.  One launch
+        # copies the spec from the pinned ring (mapped host memory) and fills
+        # the mask (prefix columns visible, tree column j visible iff bit j of
+        # the row's ancestor bitmask).
         nbytes = int(host.nbytes)
         head = (nbytes + 15) & ~15
         alloc = torch.empty(head + node_count * kv_len, dtype=torch.uint8, device=device)
-        buf = _lib.staging().upload(host, device, out=alloc[:nbytes])
+        buf = alloc[:nbytes]
         dense = alloc[head:]
+        lib, dst, mask, stream = _lib.load(), _lib.ptr(buf), _lib.ptr(dense), _lib.stream_of(device)
+
+        def launch(src):
+            _lib.check(lib.atlas_tree_spec_upload(src, nbytes, node_count, prefix_len, dst, mask, stream),
+                       "atlas_tree_spec_upload")
+
+        staging = _lib.staging()
+        if not staging.stage(host, device, launch):
+            # larger than the ring takes: a plain copy, then the mask from it
+            staging.upload(host, device, out=buf)
+            launch(dst)
     else:
         buf = torch.from_numpy(host.copy()).to(device)
     nb = 8 * node_count
@@ -314,12 +327,7 @@ def _tree_spec_tensors(host, n64, n32, *, node_count, kv_len, total_pages, last,
     kv_indptr = with_host_values(kvp_b.view(torch.int32), [0, total_pages])
     kv_last = with_host_values(last_b.view(torch.int32), [last])
     kv_indices = idx_b.view(torch.int32)
-    # Dense mask [node, prefix + node]: prefix columns all visible, tree column
-    # j visible iff bit j of the row's ancestor bitmask (one launch).
     if dense is not None:
-        rc = _lib.load().atlas_tree_mask_fill(_lib.ptr(block_b), node_count, prefix_len, _lib.ptr(dense),
-                                              _lib.stream_of(device))
-        _lib.check(rc, "atlas_tree_mask_fill")
         flat_mask = dense.view(torch.bool)
     else:
         block_t = block_b.view(torch.bool).view(node_count, node_count)

@@ -223,6 +223,19 @@ int atlas_tree_spec_build(const int64_t* paths_host, int32_t num_paths, int32_t 
  * mask build of build_(deduplicated_)tree_spec_from_paths
  * (src/atlas_0709/flashinfer_full_verify.py:682-687, :719-724). */
 int atlas_tree_mask_fill(const uint8_t* block_dev, int32_t n, int64_t prefix_len, uint8_t* mask_dev, void* stream);
+/* The spec buffer of atlas_tree_spec_build moved to the device and its dense
+ * mask filled, in one launch: the nbytes at spec_src (device memory, or
+ * mapped pinned host memory: hipHostMalloc with hipHostMallocMapped and
+ * hipHostMallocCoherent, through hipHostGetDevicePointer) are copied to
+ * spec_dev, and mask_dev is filled as by atlas_tree_mask_fill from the tree
+ * block, the spec's last n * n bytes, read at spec_src.  spec_src ==
+ * spec_dev fills the mask only.  Both spec pointers 16-byte aligned.  Host
+ * memory at spec_src must stay unchanged until the launch has completed.
+ * Replaces the upload and the dense mask build of
+ * build_(deduplicated_)tree_spec_from_paths
+ * (src/atlas_0709/flashinfer_full_verify.py:682-687, :719-724). */
+int atlas_tree_spec_upload(const uint8_t* spec_src, int64_t nbytes, int32_t n, int64_t prefix_len, uint8_t* spec_dev,
+                           uint8_t* mask_dev, void* stream);
 
 /* Mask modes. */
 #define ATLAS_MASK_NONE 0   /* every key < kv_len visible */

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 15
+    assert lib.atlas_abi_version() == 16
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -205,3 +205,15 @@ def test_frontier_host_descriptors_limit_without_device_work():
                                               None, None, 0, fake, fake, fake, fake, 64, fake, fake, None)
     assert rc == lib_mod.ATLAS_EUNSUPPORTED
     assert b"at most" in lib.atlas_last_error()
+
+
+def test_tree_spec_upload_refusals_without_device_work():
+    """The one-launch spec upload refuses a spec shorter than its tree block
+    and unaligned spec buffers before any launch."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    a, b = ctypes.c_void_p(1 << 20), ctypes.c_void_p(2 << 20)  # never dereferenced: the calls refuse first
+    assert lib.atlas_tree_spec_upload(a, 15, 4, 8, b, b, None) == lib_mod.ATLAS_EINVAL  # 15 < 4 * 4
+    assert b"tree block" in lib.atlas_last_error()
+    assert lib.atlas_tree_spec_upload(ctypes.c_void_p((1 << 20) + 8), 64, 4, 8, b, b, None) == lib_mod.ATLAS_EINVAL
+    assert b"aligned" in lib.atlas_last_error()

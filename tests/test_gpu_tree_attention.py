@@ -902,8 +902,9 @@ def test_hnd_fused_rope_append_matches_nhd(dev, prefix_len):
 @pytest.mark.parametrize("n_routes,depth,prefix,dedup", [(9, 4, 16384, True), (3, 4, 0, True), (1, 1, 7, False),
                                                          (40, 4, 100, True), (300, 5, 64, True), (6, 3, 61, False)])
 def test_device_tree_spec_equals_host_spec(dev, n_routes, depth, prefix, dedup):
-    """A tree spec built for the device (its dense mask filled by
-    atlas_tree_mask_fill in the same allocation as the uploaded buffer)
+    """A tree spec built for the device (one atlas_tree_spec_upload launch
+    copies the buffer from the pinned ring and fills the dense mask in the
+    same allocation; a spec larger than the ring's quarter is copied first)
     equals the one built for the host, tensor for tensor, and the oracle's
     ancestor mask; the plan's cached window and tile words ride along, and an
     in-place change of the device mask is seen by the plan (version counter)."""
@@ -932,3 +933,43 @@ def test_device_tree_spec_equals_host_spec(dev, n_routes, depth, prefix, dedup):
         assert ta._cached_tree_window(gpu.bool_mask, [n], [kv]) is None
     elif n <= 1024:
         assert ta._cached_tree_tiles(gpu.bool_mask, [n], [kv]) is not None
+
+
+@pytest.mark.parametrize("source", ["mapped", "device", "in_place"])
+def test_tree_spec_upload_copies_and_fills(dev, source):
+    """atlas_tree_spec_upload from mapped pinned memory, from another device
+    buffer, and in place (mask only): the spec bytes arrive unchanged (an odd
+    length, so the last 16-byte chunk is partial) and the dense mask has the
+    prefix columns set and the tree block after them."""
+    import numpy as np
+
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    rng = np.random.default_rng(7)
+    n, prefix = 13, 70
+    spec = rng.integers(0, 256, size=1000 + n * n, dtype=np.uint8)
+    spec[-n * n:] = rng.integers(0, 2, size=n * n)
+    nbytes = int(spec.nbytes)
+    dst = torch.full((nbytes + 15,), 0xEE, dtype=torch.uint8, device=dev)
+    mask = torch.full((n * (prefix + n) + 5,), 0xEE, dtype=torch.uint8, device=dev)
+    stream = lib_mod.stream_of(dev)
+    print(f"tree spec upload: {source}", flush=True)
+
+    def launch(src):
+        lib_mod.check(lib.atlas_tree_spec_upload(src, nbytes, n, prefix, lib_mod.ptr(dst), lib_mod.ptr(mask), stream),
+                      "atlas_tree_spec_upload")
+
+    if source == "mapped":
+        assert lib_mod.staging().stage(spec, dev, launch)
+    elif source == "device":
+        launch(lib_mod.ptr(torch.from_numpy(spec).to(dev)))
+    else:
+        dst[:nbytes].copy_(torch.from_numpy(spec))
+        launch(lib_mod.ptr(dst))
+    torch.cuda.synchronize()
+    assert dst[:nbytes].cpu().numpy().tobytes() == spec.tobytes()
+    assert dst[nbytes:].tolist() == [0xEE] * 15
+    block = spec[-n * n:].reshape(n, n)
+    want = np.concatenate([np.ones((n, prefix), dtype=np.uint8), block], axis=1).reshape(-1)
+    got = mask.cpu().numpy()
+    assert got[: want.size].tobytes() == want.tobytes() and got[want.size:].tolist() == [0xEE] * 5
