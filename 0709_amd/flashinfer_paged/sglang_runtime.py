@@ -1254,6 +1254,7 @@ class _StepFlags:
         self.flags = flags
         self.spans = spans
         self._host: list[int] | None = None
+        self._groups: list[int] | None = None  # each request's words ORed, once
 
     def host(self) -> list[int]:
         if self._host is None:
@@ -1261,13 +1262,19 @@ class _StepFlags:
         return self._host
 
     def check(self, group: int, validate_layout: bool) -> None:
-        h = self.host()
-        if any(w & _lib.FRONTIER_BAD_DESCRIPTOR for w in h):
+        groups = self._groups
+        if groups is None:
+            h = self.host()
+            groups = []
+            for lo, hi in self.spans:
+                bits = 0
+                for w in h[lo:hi]:
+                    bits |= w
+                groups.append(bits)
+            self._groups = groups
+        if any(b & _lib.FRONTIER_BAD_DESCRIPTOR for b in groups):
             raise RuntimeError("frontier step: a route descriptor was out of range and the route was skipped")
-        lo, hi = self.spans[int(group)]
-        bits = 0
-        for w in h[lo:hi]:
-            bits |= w
+        bits = groups[int(group)]
         # the order prepare_frontier records these checks in
         if bits & _lib.FRONTIER_COW_OVERLAP:
             raise RuntimeError("copy-on-write destination pages overlap its source pages")
@@ -1466,40 +1473,39 @@ def _prepare_frontiers(bridges: Sequence[SGLangRoutePoolBridge],
     # one allocation: the int64 outputs (a check word per route; the model
     # inputs when the launch writes them), then the int32 ones
     n32 = 3 * R + 1 + P
-    sizes = [F, R, R] + ([C, C] if C else []) + ([5 * R] if by_value else []) + [(n32 + 1) // 2]
+    # flat paths, decode slots, check words, [copy pairs], [model inputs], the int32 outputs
+    sizes = [F, R, R] + ([C, C] if C else []) + ([R] * 5 if by_value else []) + [(n32 + 1) // 2]
     out = torch.empty(sum(sizes), dtype=torch.int64, device=device)
     parts = out.split(sizes)
     flat, out_slots, flags = parts[:3]
     cow_dst, cow_src = parts[3:5] if C else (None, None)
     kv_indptr, kv_last, seq32, page_ids, _ = parts[-1].view(torch.int32).split([R + 1, R, R, P, n32 % 2])
     lib = _lib.load()
+    free_ptr, table_ptr = alloc.free_pages.data_ptr(), table.data_ptr()
+    cow = (cow_dst.data_ptr(), cow_src.data_ptr()) if C else (None, None)
     if by_value:
-        batch = parts[-2]
+        input_ids, seq_dev, pos_dev, req_dev, rid_dev = parts[-6:-1]
         host = np.asarray(desc + tokens + route_ids, dtype=np.int64)
         base = host.ctypes.data
         rc = lib.atlas_pool_prepare_frontier_host(
-            base, base + 8 * _ROUTE_FIELDS * R, base + 8 * (_ROUTE_FIELDS + 1) * R, R,
-            ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps, int(b0.owned_page_ids.num_pages),
-            _lib.ptr(table), int(table.shape[0]), int(table.stride(0)), _lib.ptr(flat), F, _lib.ptr(out_slots),
-            _lib.ptr(cow_dst) if C else None, _lib.ptr(cow_src) if C else None, C, _lib.ptr(kv_indptr),
-            _lib.ptr(kv_last), _lib.ptr(seq32), _lib.ptr(page_ids), P, _lib.ptr(flags), _lib.ptr(batch),
-            _lib.stream_of(device),
+            base, base + 8 * _ROUTE_FIELDS * R, base + 8 * (_ROUTE_FIELDS + 1) * R, R, free_ptr, num_free, ps,
+            int(b0.owned_page_ids.num_pages), table_ptr, int(table.shape[0]), int(table.stride(0)), flat.data_ptr(),
+            F, out_slots.data_ptr(), *cow, C, kv_indptr.data_ptr(), kv_last.data_ptr(), seq32.data_ptr(),
+            page_ids.data_ptr(), P, flags.data_ptr(), input_ids.data_ptr(), _lib.stream_of(device),
         )
         _lib.check(rc, "atlas_pool_prepare_frontier_host")
     else:
         positions = [n - 1 for n in seq_lens]
         rows = [r for plan in plans for r in plan.rows]
         packed = _lib.upload_i64(desc + tokens + seq_lens + positions + rows + route_ids, device)
-        batch = packed[_ROUTE_FIELDS * R:]
+        input_ids, seq_dev, pos_dev, req_dev, rid_dev = packed[_ROUTE_FIELDS * R:].split(R)
         rc = lib.atlas_pool_prepare_frontier(
-            _lib.ptr(packed), R, ctypes.c_void_p(int(alloc.free_pages.data_ptr())), num_free, ps,
-            int(b0.owned_page_ids.num_pages), _lib.ptr(table), int(table.shape[0]), int(table.stride(0)),
-            _lib.ptr(flat), F, _lib.ptr(out_slots), _lib.ptr(cow_dst) if C else None,
-            _lib.ptr(cow_src) if C else None, C, _lib.ptr(kv_indptr), _lib.ptr(kv_last), _lib.ptr(seq32),
-            _lib.ptr(page_ids), P, _lib.ptr(flags), _lib.stream_of(device),
+            packed.data_ptr(), R, free_ptr, num_free, ps, int(b0.owned_page_ids.num_pages), table_ptr,
+            int(table.shape[0]), int(table.stride(0)), flat.data_ptr(), F, out_slots.data_ptr(), *cow, C,
+            kv_indptr.data_ptr(), kv_last.data_ptr(), seq32.data_ptr(), page_ids.data_ptr(), P, flags.data_ptr(),
+            _lib.stream_of(device),
         )
         _lib.check(rc, "atlas_pool_prepare_frontier")
-    input_ids, seq_dev, pos_dev, req_dev, rid_dev = batch.split(R)
     if C:
         alloc.get_kvcache().move_kv_cache(cow_dst, cow_src)
     alloc.consume_pages(free_idx)
@@ -1787,14 +1793,17 @@ class SGLangFlashInferFrontierModelBackend:
         logits = ex.forward_frontier(input_ids=step.input_ids, route_kv_metadata=step.metadata)
         out_slots = step.metadata.out_cache_loc
         outputs = []
+        # one request whose rows are the whole batch: no slices
+        whole = len(backends) == 1 and int(logits.shape[0]) == step.spans[0][1]
         for i, b in enumerate(backends):
             lo, hi = step.spans[i]
-            b.route_pool.register_node_slots(new_nodes[i], out_slots[lo:hi])
+            b.route_pool.register_node_slots(new_nodes[i], out_slots if whole else out_slots[lo:hi])
             ps = int(b.route_pool.page_size)
             prevs = step.prevs[lo:hi]
             outputs.append(b._frontier_output(
-                step.route_ids[lo:hi], logits[lo:hi], new_nodes[i], start, before[i], ps,
-                sum(prevs) + len(prevs), sum((p + ps) // ps for p in prevs), attention_backend))
+                step.route_ids if whole else step.route_ids[lo:hi], logits if whole else logits[lo:hi],
+                new_nodes[i], start, before[i], ps, sum(prevs) + len(prevs), sum((p + ps) // ps for p in prevs),
+                attention_backend))
         return outputs
 
     @staticmethod

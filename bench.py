@@ -252,8 +252,8 @@ class HeadlineStep:
 
         def prune():
             # pages of the whole request (prefix + tree) are owned at verify
-            # time; marked here, behind the score copy, since only the prune
-            # reads them
+            # time; marked here, behind the selection and the commit, since
+            # only the prune reads them
             rc = lib.load().atlas_mark_pages(lib.ptr(self.owned), self.pool_pages, lib.ptr(self.all_slots),
                                              self.kv_len, self.ps, stream)
             lib.check(rc, "atlas_mark_pages")
