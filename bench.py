@@ -883,7 +883,7 @@ def frontier_leg(dev, *, rows=72, vocab=128256, k=3, iters=20):
             "depth_call_us": round(call_us, 1), "torch_sequence_us": round(torch_us, 1)}
 
 
-def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
+def drafter_leg(dev, *, requests=8, repeats=6, warmup=1, batched=True):
     """Drafter route-pool fork stress (Llama-3.2-1B KV geometry, bf16, page
     64): 8 requests, each forking to 9 routes at random fill levels of its
     partial tail page, 8 decode steps, commit + promote of 3 routes, prune,
@@ -893,13 +893,15 @@ def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
     replaced by one all-layer K/V append per forward.  ``batched``: each
     decode step of the 8 requests is one fused frontier step (one launch for
     all 72 routes, one forward); else one bridge call per request.  Wall time
-    per phase, GPU synchronised at each phase end."""
+    per phase, GPU synchronised at each phase end; ``warmup`` untimed
+    repetitions first (first calls, the allocator's first blocks), then the
+    median over ``repeats``, each on fresh pools."""
     dw = _pkg("drafter_workload")
     npool = _pkg("flashinfer_paged.native_pool")
     geom = _pkg("workloads").LLAMA_1B
     ps = 64
     runs = []
-    for rep in range(repeats):
+    for rep in range(warmup + repeats):
         req_pool, kv, alloc = npool.create_native_pools(
             num_pages=640, page_size=ps, dtype=torch.bfloat16, head_num=geom.kv_heads, head_dim=geom.head_dim,
             layer_num=geom.layers, max_running_requests=128, max_context_len=4096, device=dev)
@@ -913,7 +915,9 @@ def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
             kv.set_kv_buffer_all_layers(slots, [rows[:n]] * geom.layers, [rows[:n]] * geom.layers)
             model[0] += time.perf_counter() - t0
 
-        work = dw.DrafterForkWorkload(plans=dw.config5_plans(requests, ps, rep), req_pool=req_pool, allocator=alloc,
+        # seeds 0, 1, 2 in turn: the timed repetitions cover each workload twice
+        work = dw.DrafterForkWorkload(plans=dw.config5_plans(requests, ps, rep % 3), req_pool=req_pool,
+                                      allocator=alloc,
                                       page_size=ps, device=dev, writer=writer, batched=batched)
         marks = []
 
@@ -932,9 +936,10 @@ def drafter_leg(dev, *, requests=8, repeats=3, batched=True):
             spans[name + "/model"] = m * 1e6
         cow_pages = sum(r.bridge.cow_pages_copied for r in work.requests)
         cow_tokens = sum(r.bridge.cow_tokens_copied for r in work.requests)
-        runs.append((spans, cow_pages, cow_tokens))
+        if rep >= warmup:
+            runs.append((spans, cow_pages, cow_tokens))
         del work, req_pool, kv, alloc
-        torch.cuda.empty_cache()
+    torch.cuda.empty_cache()
     decode = [statistics.fmean(sp[f"decode{t}"] for t in range(8)) for sp, _, _ in runs]
     decode_model = [statistics.fmean(sp[f"decode{t}/model"] for t in range(8)) for sp, _, _ in runs]
     return {
