@@ -1,6 +1,6 @@
 """CPU restatement of the reference's paged-KV tree path -- TEST INFRASTRUCTURE.
 
-This package is the checker, never the product: only ``tests/``,
+This package checks the product and is never part of it: only ``tests/``,
 ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import
 it.  Every function cites the reference file:line it restates (paths relative
 to the reference's ``src/atlas_0709/``).  Integer and byte work is numpy;
