@@ -217,3 +217,23 @@ def test_tree_spec_upload_refusals_without_device_work():
     assert b"tree block" in lib.atlas_last_error()
     assert lib.atlas_tree_spec_upload(ctypes.c_void_p((1 << 20) + 8), 64, 4, 8, b, b, None) == lib_mod.ATLAS_EINVAL
     assert b"aligned" in lib.atlas_last_error()
+
+
+def test_header_constants_match_the_binding():
+    """Every ``#define ATLAS_X value`` of include/ that the Python binding
+    mirrors (as ``ATLAS_X`` or ``X``) has the same value there, and the
+    limits and codes the runtime passes to the library are among them."""
+    lib_mod = pkg("_lib")
+    defines = {}
+    for header in (ROOT / "include").glob("*.h"):
+        for name, value in re.findall(r"^#define (ATLAS_\w+) \(?(-?\d+)\)?", header.read_text(), flags=re.M):
+            defines[name] = int(value)
+    checked = set()
+    for name, value in defines.items():
+        for py in (name, name[len("ATLAS_"):]):
+            if hasattr(lib_mod, py):
+                assert getattr(lib_mod, py) == value, f"{py} = {getattr(lib_mod, py)} but the header says {value}"
+                checked.add(name)
+    assert {"ATLAS_FRONTIER_MAX_HOST_ROUTES", "ATLAS_FRONTIER_BAD_DESCRIPTOR", "ATLAS_FRONTIER_COW_OVERLAP",
+            "ATLAS_SELECT_MAX_ENTRIES", "ATLAS_ROUND_BF16", "ATLAS_PRUNE_MAX_PATHS", "ATLAS_ATTN_SCRATCH_BYTES",
+            "ATLAS_MAX_LAYERS_PER_LAUNCH", "ATLAS_EUNSUPPORTED", "ATLAS_MASK_TREE"} <= checked
