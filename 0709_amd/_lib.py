@@ -129,6 +129,7 @@ _SIGNATURES: dict[str, list] = {
         _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp, _c_i64,
         _vp, _vp, _vp, _vp, _c_i64, _vp, _vp,
     ],
+    "atlas_gather_i64": [_vp, ctypes.c_int, _vp, _vp],
     "atlas_pool_prepare_frontier_host": [
         _vp, _vp, _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp,
         _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp,
@@ -164,6 +165,7 @@ _RESTYPES: dict[str, type] = {
     "atlas_tree_spec_bytes": ctypes.c_int64,
 }
 
+GATHER_MAX_SEGMENTS = 32
 FRONTIER_BAD_DESCRIPTOR = 1
 FRONTIER_BAD_LAYOUT = 2
 FRONTIER_DUPLICATE_SLOT = 4
@@ -415,6 +417,12 @@ class HostStaging:
         import numpy as np
 
         return self.upload(np.asarray(values, dtype=np.int64), device).view(torch.int64)
+
+
+class I64Segment(ctypes.Structure):
+    """``atlas_i64_segment_t``: a strided run of int64 values on the device."""
+
+    _fields_ = [("src", ctypes.c_void_p), ("count", ctypes.c_int64), ("stride", ctypes.c_int64)]
 
 
 class MappedReadback:

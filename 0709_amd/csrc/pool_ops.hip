@@ -470,10 +470,51 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_host_kernel
                          kv_indptr, kv_last, seq_lens, page_ids, route_flags, batch);
 }
 
+// The int64 values of up to ATLAS_GATHER_MAX_SEGMENTS strided segments,
+// concatenated into out (device memory or mapped host memory): one launch
+// brings a pool's small results (released-page counts, page starts, check
+// words) to the host together.
+struct GatherSegments {
+  atlas_i64_segment_t s[ATLAS_GATHER_MAX_SEGMENTS];
+  int64_t start[ATLAS_GATHER_MAX_SEGMENTS + 1];
+  int32_t n;
+};
+
+__global__ __launch_bounds__(256) void gather_i64_kernel(const GatherSegments g, int64_t* __restrict__ out) {
+  const int64_t total = g.start[g.n];
+  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
+    int k = 0;
+    while (i >= g.start[k + 1]) ++k;
+    out[i] = g.s[k].src[(i - g.start[k]) * g.s[k].stride];
+  }
+}
+
 }  // namespace
 }  // namespace atlas
 
 using namespace atlas;
+
+extern "C" int atlas_gather_i64(const atlas_i64_segment_t* segments_host, int num_segments, int64_t* out,
+                                void* stream) {
+  ATLAS_REQUIRE(num_segments >= 0 && num_segments <= ATLAS_GATHER_MAX_SEGMENTS, "num_segments must be in [0, %d]",
+                ATLAS_GATHER_MAX_SEGMENTS);
+  ATLAS_REQUIRE(num_segments == 0 || segments_host, "segments must not be NULL");
+  GatherSegments g{};
+  g.n = num_segments;
+  for (int k = 0; k < num_segments; ++k) {
+    const atlas_i64_segment_t& sk = segments_host[k];
+    ATLAS_REQUIRE(sk.count >= 0 && (sk.count == 0 || sk.src), "segment %d: bad source or count", k);
+    g.s[k] = sk;
+    g.start[k + 1] = g.start[k] + sk.count;
+  }
+  const int64_t total = g.start[num_segments];
+  if (total == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(out, "out must not be NULL");
+  ATLAS_REQUIRE(total < (int64_t(1) << 31), "too many values");
+  const int blocks = static_cast<int>(std::min<int64_t>((total + 255) / 256, 64));
+  hipLaunchKernelGGL(gather_i64_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), g, out);
+  return launch_status("gather_i64_kernel");
+}
 
 extern "C" int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev,
                                 int64_t n, int64_t page_size, void* stream) {

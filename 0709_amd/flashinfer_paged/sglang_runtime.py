@@ -22,6 +22,7 @@ from __future__ import annotations
 import ctypes
 import operator
 import sys
+import threading
 import time
 from dataclasses import dataclass, field
 from typing import Any, Sequence
@@ -1218,15 +1219,68 @@ def _unread_step_flags(bridges: Sequence["SGLangRoutePoolBridge"]) -> list["_Ste
     return out
 
 
+class _HostGather:
+    """Mapped pinned host memory for ``atlas_gather_i64``: a read-back of up
+    to ``capacity`` int64 values is one launch and one event wait (no
+    concatenation on the device, no separate copy).  One per process,
+    serialised by its lock."""
+
+    capacity = 8192
+
+    def __init__(self) -> None:
+        self.lock = threading.Lock()
+        self.buf: _lib.MappedReadback | None = None
+        self.values: np.ndarray | None = None
+        self.events: dict[int, torch.cuda.Event] = {}
+
+    def read(self, tensors: Sequence[torch.Tensor]) -> list[int] | None:
+        """The values of the 1-D int64 device tensors, concatenated, or None
+        when this path does not take them (host tensors, other dtypes, more
+        segments or values than it holds)."""
+        dev = tensors[0].device
+        if dev.type != "cuda" or len(tensors) > _lib.GATHER_MAX_SEGMENTS:
+            return None
+        segs = (_lib.I64Segment * len(tensors))()
+        total = 0
+        for i, t in enumerate(tensors):
+            if t.device != dev or t.dtype != torch.int64 or t.dim() != 1:
+                return None
+            n = int(t.numel())
+            seg = segs[i]
+            seg.src, seg.count, seg.stride = t.data_ptr(), n, int(t.stride(0))
+            total += n
+        if total > self.capacity:
+            return None
+        with self.lock:
+            if self.buf is None:
+                self.buf = _lib.MappedReadback(2 * self.capacity)
+                self.values = self.buf.np.view(np.int64)
+            _lib.check(_lib.load().atlas_gather_i64(segs, len(tensors), self.buf.device_ptr, _lib.stream_of(dev)),
+                       "atlas_gather_i64")
+            idx = dev.index if dev.index is not None else torch.cuda.current_device()
+            ev = self.events.get(idx)
+            if ev is None:
+                ev = self.events[idx] = torch.cuda.Event()
+            ev.record(torch.cuda.current_stream(dev))
+            ev.synchronize()
+            return self.values[:total].tolist()
+
+
+_HOST_GATHER = _HostGather()
+
+
 def _read_back(parts: Sequence[torch.Tensor], bridges: Sequence["SGLangRoutePoolBridge"]) -> list[int]:
-    """ONE copy to the host of the int64 tensors ``parts`` together with the
-    flags of every fused frontier step with a check pending on ``bridges``;
+    """ONE read-back to the host of the int64 tensors ``parts`` together with
+    the check words of every fused frontier step with a check pending on
+    ``bridges`` (one gather launch into mapped host memory, else one copy);
     returns the values of ``parts``, concatenated."""
     flags = _unread_step_flags(bridges)
     tensors = [*parts, *(f.flags for f in flags)]
     if not tensors:
         return []
-    flat = _int_list(torch.cat(tensors) if len(tensors) > 1 else tensors[0])
+    flat = _HOST_GATHER.read(tensors)
+    if flat is None:
+        flat = _int_list(torch.cat(tensors) if len(tensors) > 1 else tensors[0])
     off = sum(int(t.numel()) for t in parts)
     head = flat[:off]
     for f in flags:

@@ -446,6 +446,26 @@ int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_d
  * Frontier step of many requests in one launch.
  * ---------------------------------------------------------------------- */
 
+/* A strided run of int64 values in device memory: src[0], src[stride], ...
+ * (count of them). */
+typedef struct {
+  const int64_t* src;
+  int64_t count;
+  int64_t stride;
+} atlas_i64_segment_t;
+#define ATLAS_GATHER_MAX_SEGMENTS 32
+
+/* The values of num_segments segments (at most ATLAS_GATHER_MAX_SEGMENTS, in
+ * host memory; they travel in the launch's arguments) concatenated into out,
+ * in one launch.  out may be mapped pinned host memory (hipHostMalloc with
+ * hipHostMallocMapped and hipHostMallocCoherent, through
+ * hipHostGetDevicePointer): the values are then on the host once an event
+ * recorded after the launch has completed.  No counterpart in the reference:
+ * it replaces the concatenation and device-to-host copy of a pool's small
+ * results (released-page counts, prefix page starts, check words) that the
+ * prune and commit read back. */
+int atlas_gather_i64(const atlas_i64_segment_t* segments_host, int num_segments, int64_t* out, void* stream);
+
 /* One active route of a frontier step (13 fields of 8 bytes).  The route's
  * new slot path is its current path with, when cow_tail > 0, the last
  * cow_tail slots replaced by the first slots of a fresh page (copy-on-write),

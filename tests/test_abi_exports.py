@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 16
+    assert lib.atlas_abi_version() == 17
     assert isinstance(lib.atlas_last_error(), bytes)
 
 
@@ -237,3 +237,18 @@ def test_header_constants_match_the_binding():
     assert {"ATLAS_FRONTIER_MAX_HOST_ROUTES", "ATLAS_FRONTIER_BAD_DESCRIPTOR", "ATLAS_FRONTIER_COW_OVERLAP",
             "ATLAS_SELECT_MAX_ENTRIES", "ATLAS_ROUND_BF16", "ATLAS_PRUNE_MAX_PATHS", "ATLAS_ATTN_SCRATCH_BYTES",
             "ATLAS_MAX_LAYERS_PER_LAUNCH", "ATLAS_EUNSUPPORTED", "ATLAS_MASK_TREE"} <= checked
+
+
+def test_gather_limits_without_device_work():
+    """The read-back gather refuses more than GATHER_MAX_SEGMENTS segments
+    and a segment with values but no source, before any launch; nothing to
+    gather is no launch at all."""
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    segs = (lib_mod.I64Segment * (lib_mod.GATHER_MAX_SEGMENTS + 1))()
+    assert lib.atlas_gather_i64(segs, lib_mod.GATHER_MAX_SEGMENTS + 1, None, None) == lib_mod.ATLAS_EINVAL
+    segs[0].count = 3  # NULL source
+    assert lib.atlas_gather_i64(segs, 1, None, None) == lib_mod.ATLAS_EINVAL
+    assert b"segment 0" in lib.atlas_last_error()
+    segs[0].count = 0
+    assert lib.atlas_gather_i64(segs, 2, None, None) == lib_mod.ATLAS_OK

@@ -321,3 +321,36 @@ def test_mark_and_prune_graph_replays(dev, num_pages, n_slots):
         assert float(scratch) == float(scratch)
         assert int(cnt.item()) == eager[2], f"replay {rep}: count differs"
         assert torch.equal(owned_bm, eager[0]) and torch.equal(free[: eager[2]], eager[1]), f"replay {rep} differs"
+
+
+@pytest.mark.parametrize("target", ["mapped", "device"])
+def test_gather_i64_segments(dev, target):
+    """atlas_gather_i64: contiguous, strided, single-value and empty
+    segments concatenated in order, into mapped host memory and into device
+    memory; nothing past the values is written."""
+    import numpy as np
+
+    lib_mod = pkg("_lib")
+    lib = lib_mod.load()
+    a = torch.arange(100, 140, dtype=torch.int64, device=dev)
+    b = torch.arange(-500, 0, dtype=torch.int64, device=dev)[::7]  # strided view
+    c = torch.tensor([1 << 40], dtype=torch.int64, device=dev)
+    e = a[:0]
+    parts = [a, e, b, c, a[5:9]]
+    want = np.concatenate([p.cpu().numpy() for p in parts]).tolist()
+    segs = (lib_mod.I64Segment * len(parts))()
+    for i, t in enumerate(parts):
+        segs[i].src, segs[i].count, segs[i].stride = t.data_ptr(), t.numel(), t.stride(0)
+    print(f"gather_i64 into {target}: {len(want)} values", flush=True)
+    if target == "mapped":
+        buf = lib_mod.MappedReadback(2 * (len(want) + 8))
+        vals = buf.np.view(np.int64)
+        vals[:] = -7
+        out = buf.device_ptr
+    else:
+        dst = torch.full((len(want) + 8,), -7, dtype=torch.int64, device=dev)
+        out = dst.data_ptr()
+    lib_mod.check(lib.atlas_gather_i64(segs, len(parts), out, lib_mod.stream_of(dev)), "atlas_gather_i64")
+    torch.cuda.synchronize()
+    got = vals.tolist() if target == "mapped" else dst.tolist()
+    assert got[: len(want)] == want and got[len(want):] == [-7] * 8
