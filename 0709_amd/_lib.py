@@ -130,6 +130,9 @@ _SIGNATURES: dict[str, list] = {
         _vp, _vp, _vp, _vp, _c_i64, _vp, _vp,
     ],
     "atlas_gather_i64": [_vp, ctypes.c_int, _vp, _vp],
+    "atlas_prune_pages_paths_gather": [
+        _vp, _vp, _c_i64, _vp, ctypes.c_int, ctypes.c_uint64, _c_i64, _vp, _vp, _vp, ctypes.c_int, _vp, _vp,
+    ],
     "atlas_pool_prepare_frontier_host": [
         _vp, _vp, _vp, ctypes.c_int, _vp, _c_i64, _c_i64, _c_i64, _vp, _c_i64, _c_i64, _vp, _c_i64, _vp, _vp, _vp,
         _c_i64, _vp, _vp, _vp, _vp, _c_i64, _vp, _vp, _vp,

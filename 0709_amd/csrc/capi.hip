@@ -18,4 +18,4 @@ void set_error(const char* fmt, ...) {
 
 extern "C" const char* atlas_last_error(void) { return atlas::g_last_error; }
 
-extern "C" int atlas_abi_version(void) { return 17; }
+extern "C" int atlas_abi_version(void) { return 18; }

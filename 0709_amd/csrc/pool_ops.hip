@@ -162,12 +162,34 @@ struct PrunePaths {
 // contributes slots[0], slots[ps], slots[2 ps], ... and, when bit p of
 // last_mask is set, slots[len - 1] -- one slot of every page of a path laid
 // out in whole pages.  Then the sweep of prune_fused_kernel.
-__global__ __launch_bounds__(kSweepThreads) void prune_paths_kernel(uint32_t* owned, uint32_t* live_out,
-                                                                    int64_t num_pages, int64_t num_words,
-                                                                    PrunePaths paths, int num_paths,
-                                                                    uint64_t last_mask, int64_t page_size,
-                                                                    int page_shift, int64_t* free_pages,
-                                                                    int64_t* free_count) {
+// The int64 values of up to ATLAS_GATHER_MAX_SEGMENTS strided segments,
+// concatenated into out (device memory or mapped host memory): one launch
+// brings a pool's small results (released-page counts, page starts, check
+// words) to the host together.
+struct GatherSegments {
+  atlas_i64_segment_t s[ATLAS_GATHER_MAX_SEGMENTS];
+  int64_t start[ATLAS_GATHER_MAX_SEGMENTS + 1];
+  int32_t n;
+};
+
+__device__ __forceinline__ void gather_values(const GatherSegments& g, int64_t* __restrict__ out, int64_t first,
+                                              int64_t step) {
+  const int64_t total = g.start[g.n];
+  for (int64_t i = first; i < total; i += step) {
+    int k = 0;
+    while (i >= g.start[k + 1]) ++k;
+    out[i] = g.s[k].src[(i - g.start[k]) * g.s[k].stride];
+  }
+}
+
+__global__ __launch_bounds__(256) void gather_i64_kernel(const GatherSegments g, int64_t* __restrict__ out) {
+  gather_values(g, out, int64_t(blockIdx.x) * blockDim.x + threadIdx.x, int64_t(gridDim.x) * blockDim.x);
+}
+
+__device__ __forceinline__ void prune_paths_body(uint32_t* owned, uint32_t* live_out,
+                                                 int64_t num_pages, int64_t num_words, const PrunePaths& paths,
+                                                 int num_paths, uint64_t last_mask, int64_t page_size,
+                                                 int page_shift, int64_t* free_pages, int64_t* free_count) {
   __shared__ uint32_t live[kFusedWords];
   __shared__ int64_t scan[kSweepThreads];
   const int tid = threadIdx.x;
@@ -188,6 +210,29 @@ __global__ __launch_bounds__(kSweepThreads) void prune_paths_kernel(uint32_t* ow
   }
   __syncthreads();
   fused_sweep(owned, live_out, live, num_words, scan, free_pages, free_count);
+}
+
+__global__ __launch_bounds__(kSweepThreads) void prune_paths_kernel(uint32_t* owned, uint32_t* live_out,
+                                                                    int64_t num_pages, int64_t num_words,
+                                                                    PrunePaths paths, int num_paths,
+                                                                    uint64_t last_mask, int64_t page_size,
+                                                                    int page_shift, int64_t* free_pages,
+                                                                    int64_t* free_count) {
+  prune_paths_body(owned, live_out, num_pages, num_words, paths, num_paths, last_mask, page_size, page_shift,
+                   free_pages, free_count);
+}
+
+// The same prune, then the workgroup copies the read-back segments to out:
+// its own released-page count among them, read after the barrier that ends
+// the sweep.
+__global__ __launch_bounds__(kSweepThreads) void prune_paths_gather_kernel(
+    uint32_t* owned, uint32_t* live_out, int64_t num_pages, int64_t num_words, PrunePaths paths, int num_paths,
+    uint64_t last_mask, int64_t page_size, int page_shift, int64_t* free_pages, int64_t* free_count,
+    const GatherSegments g, int64_t* __restrict__ out) {
+  prune_paths_body(owned, live_out, num_pages, num_words, paths, num_paths, last_mask, page_size, page_shift,
+                   free_pages, free_count);
+  __syncthreads();
+  gather_values(g, out, threadIdx.x, kSweepThreads);
 }
 
 // Page tables from concatenated slot paths.  Thread per page: the page id is
@@ -470,51 +515,10 @@ __global__ __launch_bounds__(kFrontierThreads) void frontier_prepare_host_kernel
                          kv_indptr, kv_last, seq_lens, page_ids, route_flags, batch);
 }
 
-// The int64 values of up to ATLAS_GATHER_MAX_SEGMENTS strided segments,
-// concatenated into out (device memory or mapped host memory): one launch
-// brings a pool's small results (released-page counts, page starts, check
-// words) to the host together.
-struct GatherSegments {
-  atlas_i64_segment_t s[ATLAS_GATHER_MAX_SEGMENTS];
-  int64_t start[ATLAS_GATHER_MAX_SEGMENTS + 1];
-  int32_t n;
-};
-
-__global__ __launch_bounds__(256) void gather_i64_kernel(const GatherSegments g, int64_t* __restrict__ out) {
-  const int64_t total = g.start[g.n];
-  for (int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x; i < total; i += int64_t(gridDim.x) * blockDim.x) {
-    int k = 0;
-    while (i >= g.start[k + 1]) ++k;
-    out[i] = g.s[k].src[(i - g.start[k]) * g.s[k].stride];
-  }
-}
-
 }  // namespace
 }  // namespace atlas
 
 using namespace atlas;
-
-extern "C" int atlas_gather_i64(const atlas_i64_segment_t* segments_host, int num_segments, int64_t* out,
-                                void* stream) {
-  ATLAS_REQUIRE(num_segments >= 0 && num_segments <= ATLAS_GATHER_MAX_SEGMENTS, "num_segments must be in [0, %d]",
-                ATLAS_GATHER_MAX_SEGMENTS);
-  ATLAS_REQUIRE(num_segments == 0 || segments_host, "segments must not be NULL");
-  GatherSegments g{};
-  g.n = num_segments;
-  for (int k = 0; k < num_segments; ++k) {
-    const atlas_i64_segment_t& sk = segments_host[k];
-    ATLAS_REQUIRE(sk.count >= 0 && (sk.count == 0 || sk.src), "segment %d: bad source or count", k);
-    g.s[k] = sk;
-    g.start[k + 1] = g.start[k] + sk.count;
-  }
-  const int64_t total = g.start[num_segments];
-  if (total == 0) return ATLAS_OK;
-  ATLAS_REQUIRE(out, "out must not be NULL");
-  ATLAS_REQUIRE(total < (int64_t(1) << 31), "too many values");
-  const int blocks = static_cast<int>(std::min<int64_t>((total + 255) / 256, 64));
-  hipLaunchKernelGGL(gather_i64_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), g, out);
-  return launch_status("gather_i64_kernel");
-}
 
 extern "C" int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev,
                                 int64_t n, int64_t page_size, void* stream) {
@@ -558,10 +562,12 @@ extern "C" int atlas_prune_pages(uint32_t* owned_bitmap_dev, uint32_t* live_bitm
   return launch_status("sweep_kernel");
 }
 
-extern "C" int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
-                                       const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
-                                       int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev,
-                                       void* stream) {
+namespace {
+
+// Arguments of the prune by paths, checked: ATLAS_OK, or the refusal.
+int prune_paths_args(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                     const atlas_slot_path_t* paths, int num_paths, int64_t page_size, int64_t* free_pages_dev,
+                     int64_t* free_count_dev, PrunePaths* pp) {
   ATLAS_REQUIRE(owned_bitmap_dev && live_bitmap_dev && free_pages_dev && free_count_dev,
                 "prune buffers must not be NULL");
   ATLAS_REQUIRE(num_pages > 0 && page_size > 0, "num_pages and page_size must be positive");
@@ -571,16 +577,76 @@ extern "C" int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* liv
               static_cast<long long>(kFusedWords * 32), num_paths, static_cast<long long>(num_pages));
     return ATLAS_EUNSUPPORTED;
   }
-  PrunePaths pp{};
   for (int p = 0; p < num_paths; ++p) {
     ATLAS_REQUIRE(paths[p].len >= 0 && (paths[p].len == 0 || paths[p].slots), "path %d: bad slots or length", p);
-    pp.p[p] = paths[p];
+    pp->p[p] = paths[p];
   }
+  return ATLAS_OK;
+}
+
+// The read-back segments, checked, into the launch's argument block.
+int gather_args(const atlas_i64_segment_t* segments_host, int num_segments, GatherSegments* g) {
+  ATLAS_REQUIRE(num_segments >= 0 && num_segments <= ATLAS_GATHER_MAX_SEGMENTS, "num_segments must be in [0, %d]",
+                ATLAS_GATHER_MAX_SEGMENTS);
+  ATLAS_REQUIRE(num_segments == 0 || segments_host, "segments must not be NULL");
+  g->n = num_segments;
+  g->start[0] = 0;
+  for (int k = 0; k < num_segments; ++k) {
+    const atlas_i64_segment_t& sk = segments_host[k];
+    ATLAS_REQUIRE(sk.count >= 0 && (sk.count == 0 || sk.src), "segment %d: bad source or count", k);
+    g->s[k] = sk;
+    g->start[k + 1] = g->start[k] + sk.count;
+  }
+  ATLAS_REQUIRE(g->start[num_segments] < (int64_t(1) << 31), "too many values");
+  return ATLAS_OK;
+}
+
+}  // namespace
+
+extern "C" int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                                       const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
+                                       int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev,
+                                       void* stream) {
+  PrunePaths pp{};
+  if (int rc = prune_paths_args(owned_bitmap_dev, live_bitmap_dev, num_pages, paths, num_paths, page_size,
+                                free_pages_dev, free_count_dev, &pp))
+    return rc;
   const int64_t words = (num_pages + 31) / 32;
   hipLaunchKernelGGL(prune_paths_kernel, dim3(1), dim3(kSweepThreads), 0, static_cast<hipStream_t>(stream),
                      owned_bitmap_dev, live_bitmap_dev, num_pages, words, pp, num_paths, last_slot_mask, page_size,
                      ilog2_exact(page_size), free_pages_dev, free_count_dev);
   return launch_status("prune_paths_kernel");
+}
+
+extern "C" int atlas_prune_pages_paths_gather(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev,
+                                              int64_t num_pages, const atlas_slot_path_t* paths, int num_paths,
+                                              uint64_t last_slot_mask, int64_t page_size, int64_t* free_pages_dev,
+                                              int64_t* free_count_dev, const atlas_i64_segment_t* segments_host,
+                                              int num_segments, int64_t* out, void* stream) {
+  PrunePaths pp{};
+  if (int rc = prune_paths_args(owned_bitmap_dev, live_bitmap_dev, num_pages, paths, num_paths, page_size,
+                                free_pages_dev, free_count_dev, &pp))
+    return rc;
+  GatherSegments g{};
+  if (int rc = gather_args(segments_host, num_segments, &g)) return rc;
+  ATLAS_REQUIRE(g.start[num_segments] == 0 || out, "out must not be NULL");
+  const int64_t words = (num_pages + 31) / 32;
+  hipLaunchKernelGGL(prune_paths_gather_kernel, dim3(1), dim3(kSweepThreads), 0, static_cast<hipStream_t>(stream),
+                     owned_bitmap_dev, live_bitmap_dev, num_pages, words, pp, num_paths, last_slot_mask, page_size,
+                     ilog2_exact(page_size), free_pages_dev, free_count_dev, g, out);
+  return launch_status("prune_paths_gather_kernel");
+}
+
+extern "C" int atlas_gather_i64(const atlas_i64_segment_t* segments_host, int num_segments, int64_t* out,
+                                void* stream) {
+  GatherSegments g{};
+  if (int rc = gather_args(segments_host, num_segments, &g)) return rc;
+  const int64_t total = g.start[num_segments];
+  if (total == 0) return ATLAS_OK;
+  ATLAS_REQUIRE(out, "out must not be NULL");
+  const int blocks = static_cast<int>(std::min<int64_t>((total + 255) / 256, 64));
+  hipLaunchKernelGGL(gather_i64_kernel, dim3(blocks), dim3(256), 0, static_cast<hipStream_t>(stream), g, out);
+  return launch_status("gather_i64_kernel");
 }
 
 extern "C" int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_dev,

@@ -121,12 +121,14 @@ class DeviceOwnedPages:
                                    _lib.ptr(self.free_count), _lib.stream_of(self.device))
         _lib.check(rc, "atlas_prune_pages")
 
-    def sweep_paths_launch(self, paths: Sequence[torch.Tensor], with_last: Sequence[bool]) -> bool:
+    def sweep_paths_launch(self, paths: Sequence[torch.Tensor], with_last: Sequence[bool], gather=None) -> bool:
         """``sweep_launch`` whose live slots are sampled from slot paths in
         the launch (path p: its page-start slots, plus its last slot when
-        ``with_last[p]``), with no sample list built first.  Returns False,
-        launching nothing, when the paths are not contiguous int64 device
-        tensors or exceed the launch's limits (then use ``sweep_launch``)."""
+        ``with_last[p]``), with no sample list built first.  ``gather``:
+        (segments, count, out) the same launch then copies to ``out`` (see
+        ``atlas_gather_i64``).  Returns False, launching nothing, when the
+        paths are not contiguous int64 device tensors or exceed the launch's
+        limits (then use ``sweep_launch``)."""
         n = len(paths)
         if n > _lib.PRUNE_MAX_PATHS or self.num_pages > _lib.PRUNE_PATHS_MAX_PAGES:
             return False
@@ -140,9 +142,14 @@ class DeviceOwnedPages:
             if last:
                 mask |= 1 << i
         lib = _lib.load()
-        rc = lib.atlas_prune_pages_paths(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, arr, n, mask,
-                                         self.page_size, _lib.ptr(self.free_pages), _lib.ptr(self.free_count),
-                                         _lib.stream_of(self.device))
+        if gather is None:
+            rc = lib.atlas_prune_pages_paths(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, arr, n,
+                                             mask, self.page_size, _lib.ptr(self.free_pages),
+                                             _lib.ptr(self.free_count), _lib.stream_of(self.device))
+        else:
+            rc = lib.atlas_prune_pages_paths_gather(_lib.ptr(self.bitmap), _lib.ptr(self.live), self.num_pages, arr,
+                                                    n, mask, self.page_size, _lib.ptr(self.free_pages),
+                                                    _lib.ptr(self.free_count), *gather, _lib.stream_of(self.device))
         _lib.check(rc, "atlas_prune_pages_paths")
         return True
 
@@ -1233,9 +1240,9 @@ class _HostGather:
         self.values: np.ndarray | None = None
         self.events: dict[int, torch.cuda.Event] = {}
 
-    def read(self, tensors: Sequence[torch.Tensor]) -> list[int] | None:
-        """The values of the 1-D int64 device tensors, concatenated, or None
-        when this path does not take them (host tensors, other dtypes, more
+    def segments(self, tensors: Sequence[torch.Tensor]):
+        """(segments, count, total) of 1-D int64 device tensors, or None when
+        this path does not take them (host tensors, other dtypes, more
         segments or values than it holds)."""
         dev = tensors[0].device
         if dev.type != "cuda" or len(tensors) > _lib.GATHER_MAX_SEGMENTS:
@@ -1251,12 +1258,16 @@ class _HostGather:
             total += n
         if total > self.capacity:
             return None
+        return segs, len(tensors), total
+
+    def run(self, launch, total: int, dev: torch.device) -> list[int]:
+        """``launch(out)`` queues work that writes ``total`` values to the
+        device address ``out``; the values once it has run."""
         with self.lock:
             if self.buf is None:
                 self.buf = _lib.MappedReadback(2 * self.capacity)
                 self.values = self.buf.np.view(np.int64)
-            _lib.check(_lib.load().atlas_gather_i64(segs, len(tensors), self.buf.device_ptr, _lib.stream_of(dev)),
-                       "atlas_gather_i64")
+            launch(self.buf.device_ptr)
             idx = dev.index if dev.index is not None else torch.cuda.current_device()
             ev = self.events.get(idx)
             if ev is None:
@@ -1264,6 +1275,20 @@ class _HostGather:
             ev.record(torch.cuda.current_stream(dev))
             ev.synchronize()
             return self.values[:total].tolist()
+
+    def read(self, tensors: Sequence[torch.Tensor]) -> list[int] | None:
+        """The values of the tensors, concatenated, through one gather
+        launch, or None (see ``segments``)."""
+        plan = self.segments(tensors)
+        if plan is None:
+            return None
+        segs, n, total = plan
+        dev = tensors[0].device
+
+        def launch(out):
+            _lib.check(_lib.load().atlas_gather_i64(segs, n, out, _lib.stream_of(dev)), "atlas_gather_i64")
+
+        return self.run(launch, total, dev)
 
 
 _HOST_GATHER = _HostGather()
@@ -1281,6 +1306,12 @@ def _read_back(parts: Sequence[torch.Tensor], bridges: Sequence["SGLangRoutePool
     flat = _HOST_GATHER.read(tensors)
     if flat is None:
         flat = _int_list(torch.cat(tensors) if len(tensors) > 1 else tensors[0])
+    return _read_back_split(parts, flags, flat)
+
+
+def _read_back_split(parts: Sequence[torch.Tensor], flags: Sequence["_StepFlags"], flat: list[int]) -> list[int]:
+    """Hands the step flags their values from a read-back of ``parts`` and
+    their words (in that order); returns the values of ``parts``."""
     off = sum(int(t.numel()) for t in parts)
     head = flat[:off]
     for f in flags:
@@ -1420,10 +1451,9 @@ def _sweep_bridges(bridges: Sequence[SGLangRoutePoolBridge], live_node_id_lists:
     before any page goes back to the free list; the released pages are
     prepended bridge by bridge, so the free list ends as one call per bridge
     in this order leaves it."""
-    for b in bridges:
-        paths, last = b._live_paths()
-        if not b.owned_page_ids.sweep_paths_launch(paths, last):
-            b.owned_page_ids.sweep_launch(b._live_slot_samples())
+    # what comes back: the released-page counts, the prefix page starts and
+    # the pending frontier steps' check words (all written by earlier launches
+    # or by the sweeps below)
     parts = [b.owned_page_ids.free_count for b in bridges]
     starts: list[int] = []
     if refresh_prefix:
@@ -1434,7 +1464,30 @@ def _sweep_bridges(bridges: Sequence[SGLangRoutePoolBridge], live_node_id_lists:
                 continue
             parts.append(slots[:: b.page_size])
             starts.append(int(parts[-1].numel()))
-    flat = _read_back(parts, bridges)
+    flags = _unread_step_flags(bridges)
+    tensors = [*parts, *(f.flags for f in flags)]
+    plan = _HOST_GATHER.segments(tensors)
+    fused = bridges[-1] if plan is not None else None  # its sweep also does the read-back
+    for b in bridges:
+        if b is fused:
+            continue
+        paths, last = b._live_paths()
+        if not b.owned_page_ids.sweep_paths_launch(paths, last):
+            b.owned_page_ids.sweep_launch(b._live_slot_samples())
+    if fused is not None:
+        segs, n, total = plan
+        pages = fused.owned_page_ids
+
+        def launch(out):
+            paths, last = fused._live_paths()
+            if not pages.sweep_paths_launch(paths, last, gather=(segs, n, out)):
+                pages.sweep_launch(fused._live_slot_samples())
+                _lib.check(_lib.load().atlas_gather_i64(segs, n, out, _lib.stream_of(pages.device)),
+                           "atlas_gather_i64")
+
+        flat = _read_back_split(parts, flags, _HOST_GATHER.run(launch, total, pages.device))
+    else:
+        flat = _read_back(parts, bridges)
     for b in bridges:
         b.check_pending_device_checks()
     counts = flat[: len(bridges)]

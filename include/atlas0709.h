@@ -398,6 +398,26 @@ typedef struct {
 int atlas_prune_pages_paths(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
                             const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
                             int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev, void* stream);
+/* A strided run of int64 values in device memory: src[0], src[stride], ...
+ * (count of them). */
+typedef struct {
+  const int64_t* src;
+  int64_t count;
+  int64_t stride;
+} atlas_i64_segment_t;
+#define ATLAS_GATHER_MAX_SEGMENTS 32
+
+/* atlas_prune_pages_paths, then the same launch copies the segments to out
+ * as atlas_gather_i64 does (after its own released-page count is written,
+ * so one of the segments may be free_count_dev): a prune and the read-back
+ * of its results in one launch.  No counterpart in the reference: it ends
+ * the prune of release_unreferenced_node_slots (sglang_runtime.py:507-539)
+ * with the values the host needs next. */
+int atlas_prune_pages_paths_gather(uint32_t* owned_bitmap_dev, uint32_t* live_bitmap_dev, int64_t num_pages,
+                                   const atlas_slot_path_t* paths, int num_paths, uint64_t last_slot_mask,
+                                   int64_t page_size, int64_t* free_pages_dev, int64_t* free_count_dev,
+                                   const atlas_i64_segment_t* segments_host, int num_segments, int64_t* out,
+                                   void* stream);
 
 /* Set the owned bit of the pages of `n` slot ids (pages newly handed out). */
 int atlas_mark_pages(uint32_t* bitmap_dev, int64_t num_pages, const int64_t* slots_dev, int64_t n,
@@ -445,15 +465,6 @@ int atlas_paged_metadata(const int64_t* slots_dev, const int64_t* path_offsets_d
 /* ------------------------------------------------------------------------
  * Frontier step of many requests in one launch.
  * ---------------------------------------------------------------------- */
-
-/* A strided run of int64 values in device memory: src[0], src[stride], ...
- * (count of them). */
-typedef struct {
-  const int64_t* src;
-  int64_t count;
-  int64_t stride;
-} atlas_i64_segment_t;
-#define ATLAS_GATHER_MAX_SEGMENTS 32
 
 /* The values of num_segments segments (at most ATLAS_GATHER_MAX_SEGMENTS, in
  * host memory; they travel in the launch's arguments) concatenated into out,

@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_abi_version_and_error_string():
     lib = pkg("_lib").load()
-    assert lib.atlas_abi_version() == 17
+    assert lib.atlas_abi_version() == 18
     assert isinstance(lib.atlas_last_error(), bytes)
 
 

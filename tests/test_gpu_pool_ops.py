@@ -102,15 +102,18 @@ def test_prune_fused_and_multi_launch_paths(dev, num_pages, n_slots, ps):
     assert _set_from_bitmap(live_bm) == live
 
 
+@pytest.mark.parametrize("read_back", [False, True])
 @pytest.mark.parametrize("num_pages,num_paths,ps", [(4096, 10, 16), (95367, 64, 64), (524288, 3, 16),
                                                       (3000, 7, 24), (64, 1, 4)])
-def test_prune_by_paths_matches_oracle_and_sample_list(dev, num_pages, num_paths, ps):
+def test_prune_by_paths_matches_oracle_and_sample_list(dev, num_pages, num_paths, ps, read_back):
     """atlas_prune_pages_paths samples each path's page-start slots (and, for
     paths with their bit in the mask, the last slot) inside the launch: the
     released pages, the owned bitmap and the live bitmap equal the oracle's
     prune of the same paths and atlas_prune_pages over the sample list
     (sglang_runtime.py:507-539).  Empty paths and a prefix without its last
-    slot are included."""
+    slot are included.  ``read_back``: atlas_prune_pages_paths_gather, the
+    same prune whose launch then copies its own released-page count and the
+    page starts of path 0 to mapped host memory."""
     lib = _lib()
     rng = np.random.default_rng(num_pages * 7 + num_paths)
     owned = set(rng.choice(num_pages, size=min(num_pages, 5000), replace=False).tolist())
@@ -135,11 +138,29 @@ def test_prune_by_paths_matches_oracle_and_sample_list(dev, num_pages, num_paths
     for i, t in enumerate(tensors):
         arr[i].slots, arr[i].len = (t.data_ptr() if t.numel() else None), t.numel()
         mask |= (1 << i) if last[i] else 0
-    rc = lib.load().atlas_prune_pages_paths(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, arr, num_paths, mask,
-                                            ps, lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev))
+    print(f"prune by paths: {num_pages} pages, {num_paths} paths, page {ps}, read_back={read_back}", flush=True)
+    if read_back:
+        starts = tensors[0][::ps]
+        segs = (lib.I64Segment * 2)()
+        for i, t in enumerate((cnt, starts)):
+            segs[i].src, segs[i].count, segs[i].stride = t.data_ptr(), t.numel(), t.stride(0)
+        mapped = lib.MappedReadback(2 * (1 + starts.numel() + 4))
+        vals = mapped.np.view(np.int64)
+        vals[:] = -9
+        rc = lib.load().atlas_prune_pages_paths_gather(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, arr,
+                                                       num_paths, mask, ps, lib.ptr(free), lib.ptr(cnt), segs, 2,
+                                                       mapped.device_ptr, lib.stream_of(dev))
+    else:
+        rc = lib.load().atlas_prune_pages_paths(lib.ptr(owned_bm), lib.ptr(live_bm), num_pages, arr, num_paths,
+                                                mask, ps, lib.ptr(free), lib.ptr(cnt), lib.stream_of(dev))
     lib.check(rc, "prune by paths")
     torch.cuda.synchronize()
     n = int(cnt.item())
+    if read_back:
+        # the launch's own count, then path 0's page starts, nothing after them
+        k = int(starts.numel())
+        assert vals[0] == n == len(exp_freed)
+        assert vals[1:1 + k].tolist() == paths[0][::ps] and vals[1 + k:].tolist() == [-9] * 4
     assert free[:n].cpu().tolist() == exp_freed
     assert _set_from_bitmap(owned_bm) == exp_left
     assert _set_from_bitmap(live_bm) == {s // ps for s in sampled}
