@@ -169,6 +169,24 @@ def test_route_pool_trace_matches_host_pools(dev, case):
         assert req.selected_route_id == select_best(scores)["route_id"]
 
 
+@pytest.mark.parametrize("batched", [False, True])
+def test_route_pool_trace_with_sweep_fallback_matches_host_pools(dev, monkeypatch, batched):
+    """With the prune by paths out of reach (its path limit patched to 0),
+    every prune takes the mark-and-sweep launches and its read-back a
+    separate gather launch; the trace still matches the host pools phase by
+    phase."""
+    dw = pkg("drafter_workload")
+    lib_mod = pkg("_lib")
+    monkeypatch.setattr(lib_mod, "PRUNE_MAX_PATHS", 0)
+    plans, ps, pages = dw.config5_plans(8, 64, 1), 64, 640
+    print(f"route-pool trace with the sweep fallback, batched={batched}", flush=True)
+    host = []
+    hw = _host_run(plans, page_size=ps, num_pages=pages, phases=host)
+    dw_run = _device_run(plans, page_size=ps, num_pages=pages, layers=4, heads=8, head_dim=64, dev=dev,
+                         host_phases=host, batched=batched)
+    assert [r.selected_route_id for r in dw_run.requests] == [r.selected_route_id for r in hw.requests]
+
+
 def test_device_ownership_set_operations(dev):
     sr = pkg("flashinfer_paged.sglang_runtime")
     own = sr.DeviceOwnedPages(100, 16, dev)
